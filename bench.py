@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""Benchmark of the BF16-weight inference hot path on one MI355X.
+
+Workload: the BF16-weight Linear GEMV microbench,
+y[M,N] = x[M,K] @ W[N,K]^T + b with x f32 N(0,1), W bf16 N(0,0.02), b = 0,
+f32 accumulate and output, for M in {1,4,16} x (K,N) in {(768,3072),
+(3072,768), (768,50257)}. One step = one launch of each of the 9 shapes.
+Each shape cycles through enough distinct weight copies that its working set
+exceeds 512 MB, so weights stream from HBM rather than the 256 MB MALL.
+Launches are replayed from HIP graphs (one graph per step) so the host does
+not pace the GPU.
+
+value = algorithmic bytes of one step (sum over shapes of 2KN + 4MK + 4MN)
+x steps / wall time of the timed steps. roofline = the shape with the
+largest kernel time, its algorithmic bytes / its average launch duration
+(HIP events on the stream the kernels run on). cpu_baseline = the CPU oracle
+(gorch's widen-per-call + f32 sgemm semantics) on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "BF16 GEMV GB/s (% HBM peak); GPT-2 decode tokens/sec at batch 1 and 16"
+HBM_PEAK_GBS = 8000.0
+MS = (1, 4, 16)
+KN = ((768, 3072), (3072, 768), (768, 50257))
+ROTATE_BYTES = 512 << 20
+
+
+def algo_bytes(M, K, N):
+    return 2 * K * N + 4 * M * K + 4 * M * N
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--shape", default=None,
+                    help="restrict to one shape 'M,K,N' (for profiling one kernel)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def gpu_leg(args, shapes):
+    import torch
+
+    from gorch_amd import hip
+    from gorch_amd import synthetic as syn
+
+    hip.init(0)
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream()  # default priority
+    torch.cuda.set_stream(stream)
+
+    bufs = []
+    for (M, K, N) in shapes:
+        x, W, b = syn.gemv_inputs(M, K, N, seed=M * 131 + K + N)
+        wbytes = 2 * K * N
+        copies = max(2, -(-ROTATE_BYTES // wbytes))
+        Wd = torch.from_numpy(W.view(np.int16)).cuda()
+        Ws = [Wd] + [Wd.clone() for _ in range(copies - 1)]
+        bufs.append(dict(M=M, K=K, N=N, x=torch.from_numpy(x).cuda(), W=Ws,
+                         b=torch.from_numpy(b).cuda(),
+                         y=torch.empty((M, N), dtype=torch.float32, device="cuda")))
+    torch.cuda.synchronize()
+
+    def launch(buf, i):
+        hip.linear_bf16(buf["x"], buf["W"][i % len(buf["W"])], buf["b"], buf["y"])
+
+    # eager warm-up reserves any split-K workspace before graph capture
+    for buf in bufs:
+        launch(buf, 0)
+    torch.cuda.synchronize()
+
+    # per-shape kernel timing: one graph of L launches cycling the copies
+    per_shape = []
+    for buf in bufs:
+        L = 4 * len(buf["W"]) if len(buf["W"]) < 64 else 2 * len(buf["W"])
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(L):
+                launch(buf, i)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 5
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * L)
+        nbytes = algo_bytes(buf["M"], buf["K"], buf["N"])
+        per_shape.append(dict(M=buf["M"], K=buf["K"], N=buf["N"], us=round(us, 3),
+                              GBs=round(nbytes / us / 1e3, 1), copies=len(buf["W"]),
+                              frac=round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)))
+        del g
+
+    # step graphs: step s launches every shape once, on copy s
+    n_graphs = max(len(buf["W"]) for buf in bufs)
+    graphs = []
+    for s in range(n_graphs):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for buf in bufs:
+                launch(buf, s)
+        graphs.append(g)
+
+    def run(nsteps, start):
+        for s in range(nsteps):
+            graphs[(start + s) % n_graphs].replay()
+
+    run(args.warmup, 0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run(args.steps, args.warmup)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_bytes = sum(algo_bytes(b_["M"], b_["K"], b_["N"]) for b_ in bufs)
+    value = step_bytes * args.steps / wall / 1e9
+    dom = max(per_shape, key=lambda r: r["us"])
+    return value, wall, per_shape, dom
+
+
+def cpu_leg(shapes, seconds):
+    """The oracle (gorch CPU semantics: widen the bf16 weight per call, f32
+    sgemm, bias add) over the same 9 shapes, repeated for ~`seconds`."""
+    import oracle as orc
+    from gorch_amd import synthetic as syn
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    inputs = [syn.gemv_inputs(M, K, N, seed=M * 131 + K + N) for (M, K, N) in shapes]
+    step_bytes = sum(algo_bytes(M, K, N) for (M, K, N) in shapes)
+    orc.set_widen_per_call(True)
+    for (x, W, b) in inputs:  # warm
+        orc.linear(x, W, b)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        for (x, W, b) in inputs:
+            orc.linear(x, W, b)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return dict(value=round(step_bytes * n / el / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                sample=f"{n} steps of the {len(shapes)}-shape sweep in {el:.1f} s; oracle widens the "
+                       f"bf16 weight on every call (bf16_matmul.go:166) then runs an f32 sgemm")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is described, not run)", file=sys.stderr)
+        sys.exit(2)
+    if args.shape:
+        M, K, N = (int(v) for v in args.shape.split(","))
+        shapes = [(M, K, N)]
+    else:
+        shapes = [(M, K, N) for (K, N) in KN for M in MS]
+
+    value, wall, per_shape, dom = gpu_leg(args, shapes)
+    cpu = None if args.no_cpu else cpu_leg(shapes, args.cpu_seconds)
+    dom_bytes = algo_bytes(dom["M"], dom["K"], dom["N"])
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "bf16-weight Linear GEMV microbench (BASELINE configs[1]): x f32 N(0,1) [M,K], "
+                        "W bf16 N(0,0.02) [N,K], f32 out; one step = one launch per shape",
+            "shapes": [f"M={s[0]},K={s[1]},N={s[2]}" for s in shapes],
+            "weights_rotated_over_bytes": ROTATE_BYTES,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"k_linear_bf16_mfma M={dom['M']} K={dom['K']} N={dom['N']}",
+            "achieved": round(dom_bytes / dom["us"] / 1e3, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dom_bytes / dom["us"] / 1e3 / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": dom_bytes,
+            "avg_launch_us": dom["us"],
+        },
+        "cpu_baseline": cpu,
+        "per_shape": per_shape,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,140 @@
+// common.h — shared device helpers and host error plumbing for libgorch_hip.
+//
+// gfx950 only: 64-lane wavefronts, bf16 MFMA, hardware f32->bf16 convert.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdio>
+#include <string>
+
+#include "../../include/gorch_hip.h"
+
+namespace gh {
+
+// ---------------------------------------------------------------- host side
+
+// Thread-local last error, returned by gorch_hip_last_error().
+void set_error(const std::string& msg);
+void clear_error();
+
+// Resolves a caller's stream argument (NULL -> the library's stream for the
+// current device).
+hipStream_t stream_of(void* s);
+
+// Device scratch owned by the library: split-K partials and their arrival
+// counters. Grown on demand, never shrunk; counters are zeroed once at
+// allocation and every kernel that uses them returns them to zero.
+struct Workspace {
+    float* partial = nullptr;
+    size_t partial_bytes = 0;
+    unsigned* counters = nullptr;
+    size_t counter_count = 0;
+};
+// Ensures the current device's workspace holds at least the requested
+// sizes. Returns false (with the error set) on allocation failure.
+bool workspace_reserve(size_t partial_bytes, size_t counters, Workspace** out);
+
+// Dispatch counters (the gorch ReadMetalDispatchCounts analogue).
+enum Counter {
+    CNT_GEMV = 0,
+    CNT_GEMM,
+    CNT_GENERIC_MATMUL,
+    CNT_ATTENTION,
+    CNT_NORM,
+    CNT_ELEMENTWISE,
+    CNT_MOE,
+    CNT_ARGMAX,
+    CNT_CODEC,
+    CNT_COUNT
+};
+void count(Counter c);
+
+// Returns 0 or sets the error from a HIP status and returns its code.
+int check(hipError_t e, const char* what);
+// Checks the last launch on the calling thread.
+int check_launch(const char* what);
+
+#define GH_TRY(expr)                 \
+    do {                             \
+        int _rc = (expr);            \
+        if (_rc != 0) return _rc;    \
+    } while (0)
+
+#define GH_REQUIRE(cond, msg)                 \
+    do {                                      \
+        if (!(cond)) {                        \
+            ::gh::set_error(msg);             \
+            return GORCH_HIP_EINVAL;          \
+        }                                     \
+    } while (0)
+
+// ---------------------------------------------------------------- device side
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// bf16 stored in the low half of a 16-bit word -> f32: an exact shift.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// gorch's f32 -> bf16 rounding: NaN keeps its top half with the quiet bit
+// set; everything else rounds to nearest even on the dropped 16 bits.
+__host__ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    uint32_t bits = __float_as_uint(v);
+#else
+    uint32_t bits;
+    __builtin_memcpy(&bits, &v, 4);
+#endif
+    if (((bits >> 23) & 0xffu) == 0xffu && (bits & 0x7fffffu) != 0)
+        return (uint16_t)((bits >> 16) | 0x40u);
+    return (uint16_t)((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+}
+
+// Splits eight f32 values into bf16 hi + bf16 lo with x ~= hi + lo to about
+// 2^-16 relative: hi is x truncated to bf16 (exact in f32), lo is the
+// remainder rounded to bf16. Two bf16 MFMAs over (hi, lo) against an exact
+// bf16 weight reproduce the f32-activation product to ~1e-5 relative.
+__device__ __forceinline__ void split_hi_lo(const float (&f)[8], bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint32_t u = __float_as_uint(f[i]) & 0xffff0000u;
+        float h = __uint_as_float(u);
+        hi[i] = __builtin_bit_cast(__bf16, (uint16_t)(u >> 16));
+        lo[i] = (__bf16)(f[i] - h);
+    }
+}
+
+__device__ __forceinline__ floatx4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const floatx4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// tanh-form GELU as gorch computes it (ops.go:417-443), f32 throughout.
+__device__ __forceinline__ float gelu_tanh(float x) {
+    float x3 = x * x * x;
+    float inner = 0.7978845608f * (x + 0.044715f * x3);
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+__device__ __forceinline__ float sigmoidf_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Wavefront (64-lane) reductions.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+}  // namespace gh
