@@ -49,7 +49,22 @@ def parse():
                     help="restrict to one shape 'M,K,N' (for profiling one kernel)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES (PMC byte-counter calibration)")
     return ap.parse_args()
+
+
+def copy_calibration(nbytes, reps=20):
+    """A plain device-to-device copy of known size, the reference point that
+    scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings."""
+    import torch
+
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "reps": reps}))
 
 
 def gpu_leg(args, shapes):
@@ -161,6 +176,9 @@ def cpu_leg(shapes, seconds):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
               "(multi-GPU sharding is described, not run)", file=sys.stderr)

@@ -13,36 +13,32 @@
 // keep ~2^-16 relative accuracy with f32 accumulation — the reference widens
 // the bf16 weight and runs an f32 sgemm (bf16_matmul.go:166-173).
 //
-// Grid: blockIdx.x = group of NT 16-row weight tiles, blockIdx.y = K split,
-// blockIdx.z = group of 16 activation rows (M > 16 re-reads W per group).
-// A block is 4 waves, each owning a contiguous K slice; the 4 partial
-// 16x16 tiles are summed in LDS in wave order. With more than one K split,
-// blocks write partials to the library workspace and the last block to
-// arrive (per output tile) sums them in split order — deterministic, one
-// launch, counters left at zero for the next call.
+// Grid: blockIdx.x = group of NT 16-row weight tiles,
+// blockIdx.y = group of 16 activation rows (M > 16 re-reads W per group).
+// A block is NW waves, each owning a contiguous K slice; the NW partial
+// 16x16 tiles are summed in LDS in wave order (deterministic). K is never
+// split across blocks: on gfx950 the agent-scope fence a cross-block
+// reduction needs writes back the L2 and costs tens of microseconds, while
+// a 16-wave block over a narrow N still keeps enough loads in flight.
 #include "common.h"
 
 namespace gh {
 
-constexpr int kWaves = 4;
-
-template <int NT>
-__global__ __launch_bounds__(256) void k_linear_bf16_mfma(
+// NW waves per block split K; NT 16-row weight tiles per block.
+template <int NT, int NW>
+__global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
     const float* __restrict__ x, const uint16_t* __restrict__ W, const float* __restrict__ bias,
-    const float* residual, float* y, int M, int N, int K, int kw, int ksplit, int epilogue,
-    float* __restrict__ partial, unsigned* __restrict__ counters) {
-    __shared__ floatx4 red[kWaves][NT][64];
-    __shared__ int s_last;
+    const float* residual, float* y, int M, int N, int K, int kw, int epilogue) {
+    __shared__ floatx4 red[NW][NT][64];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int r = lane & 15;  // A: activation row; B: weight row within tile
     const int g = lane >> 4;  // k-chunk group within a 32-wide k-step
     const int n0 = blockIdx.x * (16 * NT);
-    const int m0 = blockIdx.z * 16;
+    const int m0 = blockIdx.y * 16;
     const int mrow = m0 + r;
-    const int ks = blockIdx.y;
-    const int kb = ks * kWaves * kw + wave * kw;
+    const int kb = wave * kw;
     const int ke = min(kb + kw, K);
 
     const bool arow_ok = mrow < M;
@@ -105,126 +101,80 @@ __global__ __launch_bounds__(256) void k_linear_bf16_mfma(
     for (int t = 0; t < NT; t++) red[wave][t][lane] = acc[t];
     __syncthreads();
 
-    // Thread tid owns (tile t, lane e, slot v) for v = tid / 64: output row
-    // m = m0 + 4*(e/16) + v, column n = n0 + 16*t + e%16.
-    const int e = threadIdx.x & 63;
-    const int v = threadIdx.x >> 6;
-    const int om = m0 + 4 * (e >> 4) + v;
-    float val[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        float s = red[0][t][e][v];
-#pragma unroll
-        for (int w = 1; w < kWaves; w++) s += red[w][t][e][v];
-        val[t] = s;
-    }
-
-    if (ksplit > 1) {
-        // Publish this split's partial tile, then elect the last arrival.
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            int on = n0 + 16 * t + (e & 15);
-            if (om < M && on < N) partial[((size_t)ks * M + om) * N + on] = val[t];
-        }
-        __threadfence();
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            unsigned slot = blockIdx.z * gridDim.x + blockIdx.x;
-            unsigned prev = atomicAdd(&counters[slot], 1u);
-            s_last = (prev == (unsigned)(ksplit - 1));
-            if (s_last) __hip_atomic_store(&counters[slot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            int on = n0 + 16 * t + (e & 15);
-            float s = 0.f;
-            if (om < M && on < N) {
-                for (int q = 0; q < ksplit; q++)
-                    s += __hip_atomic_load(&partial[((size_t)q * M + om) * N + on], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-            }
-            val[t] = s;
-        }
-    }
-
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        int on = n0 + 16 * t + (e & 15);
+    // Output element o = (tile t, lane e, slot v): row m0 + 4*(e/16) + v,
+    // column n0 + 16*t + e%16. Partials are summed in wave order.
+    for (int o = threadIdx.x; o < NT * 256; o += NW * 64) {
+        const int t = o >> 8, e = o & 63, v = (o >> 6) & 3;
+        const int om = m0 + 4 * (e >> 4) + v;
+        const int on = n0 + 16 * t + (e & 15);
         if (om < M && on < N) {
-            float o = val[t];
-            if (bias) o = o + bias[on];
-            if (epilogue == GORCH_HIP_EPI_GELU) o = gelu_tanh(o);
+            float s = red[0][t][e][v];
+#pragma unroll
+            for (int w = 1; w < NW; w++) s += red[w][t][e][v];
+            if (bias) s = s + bias[on];
+            if (epilogue == GORCH_HIP_EPI_GELU) s = gelu_tanh(s);
             size_t idx = (size_t)om * N + on;
-            if (residual) o = residual[idx] + o;
-            y[idx] = o;
+            if (residual) s = residual[idx] + s;
+            y[idx] = s;
         }
     }
 }
-
-// Launch plan for one call. Tunable from the environment for sweeps:
-// GORCH_HIP_GEMV_NT (1|2|4), GORCH_HIP_GEMV_WAVES_TARGET.
-struct GemvPlan {
-    int nt, kw, ksplit, nblk, mblk;
-};
 
 static int env_int(const char* name, int dflt) {
     const char* s = getenv(name);
     return s ? atoi(s) : dflt;
 }
 
-static GemvPlan plan_gemv(int M, int N, int K) {
+// Launch plan: NT weight tiles and NW K-splitting waves per block, chosen
+// from a sweep of the decode shapes (GPT-2 small and XL, M = 1..16) on
+// MI355X. GORCH_HIP_GEMV_NT / GORCH_HIP_GEMV_NW override them.
+static void plan_gemv(int M, int N, int K, int* nt, int* nw) {
     static const int nt_env = env_int("GORCH_HIP_GEMV_NT", 0);
-    static const int target = env_int("GORCH_HIP_GEMV_WAVES_TARGET", 2048);
-    GemvPlan p;
-    int ntiles = (N + 15) / 16;
-    p.nt = nt_env ? nt_env : (ntiles >= 2048 ? 2 : 1);
-    p.mblk = (M + 15) / 16;
-    p.nblk = (ntiles + p.nt - 1) / p.nt;
-    int waves = p.nblk * kWaves * p.mblk;
-    int ksplit = 1;
-    if (waves < target) ksplit = (target + waves - 1) / waves;
-    // Each wave keeps at least two 32-wide k-steps.
-    int max_split = K / (kWaves * 64);
-    if (max_split < 1) max_split = 1;
-    if (ksplit > max_split) ksplit = max_split;
-    int per = (K + ksplit * kWaves - 1) / (ksplit * kWaves);
-    p.kw = (per + 31) / 32 * 32;
-    p.ksplit = (K + kWaves * p.kw - 1) / (kWaves * p.kw);
-    return p;
+    static const int nw_env = env_int("GORCH_HIP_GEMV_NW", 0);
+    const int ntiles = (N + 15) / 16;
+    int t, w;
+    if (ntiles >= 2048) {          // LM-head class: many tiles, short K
+        t = M > 4 ? 4 : 2;
+        w = M > 4 ? 8 : 4;
+    } else if (ntiles >= 256) {    // FFN-up / fused-QKV class
+        t = 2;
+        w = K >= 1536 ? 16 : 8;
+    } else {                       // narrow N: deep K split inside the block
+        t = 1;
+        w = 8;
+    }
+    // keep at least one 32-wide k-step per wave
+    while (w > 4 && (K + w - 1) / w < 32) w /= 2;
+    *nt = nt_env ? nt_env : t;
+    *nw = nw_env ? nw_env : w;
+}
+
+template <int NT, int NW>
+static void launch_t(hipStream_t s, dim3 grid, const float* x, const uint16_t* W, const float* bias,
+                     const float* residual, float* y, int M, int N, int K, int kw, int epilogue) {
+    hipLaunchKernelGGL((k_linear_bf16_mfma<NT, NW>), grid, dim3(NW * 64), 0, s, x, W, bias, residual, y, M,
+                       N, K, kw, epilogue);
 }
 
 int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                        const float* residual, float* y, int M, int N, int K, int epilogue) {
-    GemvPlan p = plan_gemv(M, N, K);
-    float* partial = nullptr;
-    unsigned* counters = nullptr;
-    if (p.ksplit > 1) {
-        Workspace* ws;
-        size_t need = (size_t)p.ksplit * M * N * sizeof(float);
-        if (!workspace_reserve(need, (size_t)p.nblk * p.mblk, &ws)) return GORCH_HIP_ENOMEM;
-        partial = ws->partial;
-        counters = ws->counters;
+    int nt, nw;
+    plan_gemv(M, N, K, &nt, &nw);
+    int per = (K + nw - 1) / nw;
+    int kw = (per + 31) / 32 * 32;
+    dim3 grid((N + 16 * nt - 1) / (16 * nt), (M + 15) / 16);
+#define GH_CASE(T, WV)                                                                 \
+    if (nt == T && nw == WV) {                                                         \
+        launch_t<T, WV>(s, grid, x, W, bias, residual, y, M, N, K, kw, epilogue);      \
+        count(M <= 16 ? CNT_GEMV : CNT_GEMM);                                          \
+        return check_launch("linear_bf16");                                            \
     }
-    dim3 grid(p.nblk, p.ksplit, p.mblk);
-    switch (p.nt) {
-        case 1:
-            hipLaunchKernelGGL(k_linear_bf16_mfma<1>, grid, dim3(256), 0, s, x, W, bias, residual, y, M,
-                               N, K, p.kw, p.ksplit, epilogue, partial, counters);
-            break;
-        case 2:
-            hipLaunchKernelGGL(k_linear_bf16_mfma<2>, grid, dim3(256), 0, s, x, W, bias, residual, y, M,
-                               N, K, p.kw, p.ksplit, epilogue, partial, counters);
-            break;
-        default:
-            hipLaunchKernelGGL(k_linear_bf16_mfma<4>, grid, dim3(256), 0, s, x, W, bias, residual, y, M,
-                               N, K, p.kw, p.ksplit, epilogue, partial, counters);
-            break;
-    }
-    count(M <= 16 ? CNT_GEMV : CNT_GEMM);
-    return check_launch("linear_bf16");
+    GH_CASE(1, 4) GH_CASE(1, 8) GH_CASE(1, 16)
+    GH_CASE(2, 4) GH_CASE(2, 8) GH_CASE(2, 16)
+    GH_CASE(4, 4) GH_CASE(4, 8) GH_CASE(4, 16)
+#undef GH_CASE
+    set_error("linear_bf16: unsupported tile plan");
+    return GORCH_HIP_EUNSUPPORTED;
 }
 
 }  // namespace gh
