@@ -1,0 +1,209 @@
+// attention.hip — attention over the KV cache for new query rows
+// (MHA.ForwardCached's per-head loops, nn/attention.go:355-397), the fused
+// staircase-causal softmax (causalSoftmaxForwardCPU, softmax_metal.go:111-141;
+// MSL softmax_causal_forward, metal/kernels.go:260-332) and the plain row
+// softmax (softmaxInPlace, nn/attention.go:274-296).
+//
+// Cache layout in HBM (f32, the reference's KVCache element type): per layer
+// K and V are [batch][max_seq][dim] with heads interleaved along dim, i.e.
+// one token's row is contiguous (nn/kvcache.go:14-19), so a head's 64-float
+// slice is a 256-byte segment.
+//
+// k_attn_cached: one 256-thread block per (head, query row). Scores for all
+// visible keys are staged in LDS: 16 lanes per key each take float4 slices
+// of the head (4 keys per wavefront instruction, 16-lane shuffle reduce);
+// block max / sum by LDS reduction; then P.V with lanes across the head's
+// dims (coalesced 256-byte rows) and waves across keys, summed in wave order.
+#include "common.h"
+
+namespace gh {
+
+__device__ float block_max(float v, float* sh) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) sh[wave] = v;
+    __syncthreads();
+    float t = sh[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) t = fmaxf(t, sh[w]);
+    __syncthreads();
+    return t;
+}
+
+__device__ float block_sum(float v, float* sh) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) sh[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++) t += sh[w];
+    __syncthreads();
+    return t;
+}
+
+
+constexpr int kAttnThreads = 256;
+
+__global__ __launch_bounds__(kAttnThreads) void k_attn_cached(AttnArgs a) {
+    extern __shared__ float sc[];  // [max visible keys]
+    __shared__ __align__(16) float qs[256];
+    __shared__ float red[8];
+    __shared__ float pv[4][256];
+
+    const int h = blockIdx.x;
+    const int row = blockIdx.y;
+    const int b = row / a.new_seq;
+    const int i = row - b * a.new_seq;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    const int T = a.causal ? pos + i + 1 : pos + a.new_seq;
+    const int hd = a.hd;
+    const size_t base = ((size_t)b * a.max_seq) * a.dim + (size_t)h * hd;
+    const float* K = a.kc + base;
+    const float* V = a.vc + base;
+
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = a.q[(size_t)row * a.q_stride + h * hd + d];
+    __syncthreads();
+
+    // scores: 16 lanes per key, float4 slices of the head dimension
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane & 15, kslot = lane >> 4;
+    const int hd4 = hd >> 2;
+    float lmax = -INFINITY;
+    for (int j0 = wave * 4; j0 < T; j0 += 16) {
+        const int j = j0 + kslot;
+        float acc = 0.f;
+        if (j < T) {
+            const float4* kr = reinterpret_cast<const float4*>(K + (size_t)j * a.dim);
+            for (int d4 = sub; d4 < hd4; d4 += 16) {
+                float4 kv = kr[d4];
+                float4 qv = reinterpret_cast<const float4*>(qs)[d4];
+                acc += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+            }
+        }
+        acc += __shfl_xor(acc, 8, 64);
+        acc += __shfl_xor(acc, 4, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        acc += __shfl_xor(acc, 1, 64);
+        if (j < T && sub == 0) {
+            float s = acc * a.scale;
+            sc[j] = s;
+            lmax = fmaxf(lmax, s);
+        }
+    }
+    const float mx = block_max(lmax, red);
+
+    float lsum = 0.f;
+    for (int j = threadIdx.x; j < T; j += blockDim.x) {
+        float e = expf(sc[j] - mx);
+        sc[j] = e;
+        lsum += e;
+    }
+    const float sum = block_sum(lsum, red);
+    for (int j = threadIdx.x; j < T; j += blockDim.x) sc[j] = sc[j] / sum;
+    __syncthreads();
+
+    // P.V: waves take keys j = wave, wave+4, ...; lanes take dims
+    for (int d0 = 0; d0 < hd; d0 += 64) {
+        const int d = d0 + lane;
+        float acc = 0.f;
+        if (d < hd) {
+            for (int j = wave; j < T; j += 4) acc += sc[j] * V[(size_t)j * a.dim + d];
+            pv[wave][d] = acc;
+        }
+    }
+    __syncthreads();
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+        float o = pv[0][d] + pv[1][d];
+        o = o + pv[2][d];
+        o = o + pv[3][d];
+        a.out[(size_t)row * a.dim + h * hd + d] = o;
+    }
+}
+
+int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
+    size_t lds = (size_t)a.max_seq * sizeof(float);
+    hipLaunchKernelGGL(k_attn_cached, dim3(heads, rows), dim3(kAttnThreads), lds, s, a);
+    count(CNT_ATTENTION);
+    return check_launch("attn_cached");
+}
+
+// softmax_metal.go:111-141
+__global__ __launch_bounds__(256) void k_causal_softmax(const float* __restrict__ x, float* __restrict__ y,
+                                                        int cols, int q_seq, float scale) {
+    __shared__ float red[8];
+    const int r = blockIdx.x;
+    const int limit = (r % q_seq) + (cols - q_seq);
+    const float* row = x + (size_t)r * cols;
+    float* orow = y + (size_t)r * cols;
+    float lmax = -INFINITY;
+    for (int j = threadIdx.x; j <= limit && j < cols; j += blockDim.x) lmax = fmaxf(lmax, row[j] * scale);
+    const float mx = block_max(lmax, red);
+    float lsum = 0.f;
+    for (int j = threadIdx.x; j < cols; j += blockDim.x) {
+        if (j <= limit) {
+            float e = expf(row[j] * scale - mx);
+            orow[j] = e;
+            lsum += e;
+        } else {
+            orow[j] = 0.f;
+        }
+    }
+    const float inv = 1.0f / block_sum(lsum, red);
+    for (int j = threadIdx.x; j <= limit && j < cols; j += blockDim.x) orow[j] = orow[j] * inv;
+}
+
+// nn/attention.go:274-296, in place
+__global__ __launch_bounds__(256) void k_softmax_rows(float* x, int cols) {
+    __shared__ float red[8];
+    float* row = x + (size_t)blockIdx.x * cols;
+    float lmax = -INFINITY;
+    for (int j = threadIdx.x; j < cols; j += blockDim.x) lmax = fmaxf(lmax, row[j]);
+    const float mx = block_max(lmax, red);
+    float lsum = 0.f;
+    for (int j = threadIdx.x; j < cols; j += blockDim.x) {
+        float e = expf(row[j] - mx);
+        row[j] = e;
+        lsum += e;
+    }
+    const float sum = block_sum(lsum, red);
+    for (int j = threadIdx.x; j < cols; j += blockDim.x) row[j] = row[j] / sum;
+}
+
+}  // namespace gh
+
+using namespace gh;
+
+extern "C" int gorch_hip_attention_cached(void* stream, const float* q, const float* k_cache, const float* v_cache,
+                                          float* out, int batch, int new_seq, int pos_offset, int heads,
+                                          int head_dim, int max_seq, int causal) {
+    GH_REQUIRE(batch > 0 && new_seq > 0 && heads > 0 && head_dim > 0 && max_seq > 0,
+               "gorch_hip_attention_cached: bad shape");
+    GH_REQUIRE(head_dim % 4 == 0 && head_dim <= 256, "gorch_hip_attention_cached: head_dim must be a multiple of 4, <= 256");
+    GH_REQUIRE(pos_offset >= 0 && pos_offset + new_seq <= max_seq,
+               "gorch_hip_attention_cached: cached sequence length exceeds max_seq");
+    GH_REQUIRE(max_seq <= 16384, "gorch_hip_attention_cached: max_seq above 16384 is not supported");
+    GH_REQUIRE(q && k_cache && v_cache && out, "gorch_hip_attention_cached: null pointer");
+    const int dim = heads * head_dim;
+    GH_REQUIRE(((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0, "gorch_hip_attention_cached: cache must be 16-byte aligned");
+    AttnArgs a{q, k_cache, v_cache, out, nullptr, pos_offset, new_seq, dim, head_dim, max_seq, dim, causal ? 1 : 0,
+               1.0f / sqrtf((float)head_dim)};
+    return launch_attn_cached(stream_of(stream), a, heads, batch * new_seq);
+}
+
+extern "C" int gorch_hip_causal_softmax(void* stream, const float* x, float* y, int rows, int cols, int q_seq,
+                                        float scale) {
+    GH_REQUIRE(rows >= 0 && cols > 0 && q_seq > 0 && q_seq <= cols, "gorch_hip_causal_softmax: bad shape");
+    if (rows == 0) return GORCH_HIP_OK;
+    GH_REQUIRE(x && y, "gorch_hip_causal_softmax: null pointer");
+    hipLaunchKernelGGL(k_causal_softmax, dim3(rows), dim3(256), 0, stream_of(stream), x, y, cols, q_seq, scale);
+    count(CNT_ATTENTION);
+    return check_launch("causal_softmax");
+}
+
+extern "C" int gorch_hip_softmax_rows(void* stream, float* x, int rows, int cols) {
+    GH_REQUIRE(rows >= 0 && cols > 0, "gorch_hip_softmax_rows: bad shape");
+    if (rows == 0) return GORCH_HIP_OK;
+    GH_REQUIRE(x, "gorch_hip_softmax_rows: null pointer");
+    hipLaunchKernelGGL(k_softmax_rows, dim3(rows), dim3(256), 0, stream_of(stream), x, cols);
+    count(CNT_ATTENTION);
+    return check_launch("softmax_rows");
+}

@@ -19,22 +19,14 @@ namespace gh {
 void set_error(const std::string& msg);
 void clear_error();
 
-// Resolves a caller's stream argument (NULL -> the library's stream for the
-// current device).
+// A caller's stream argument (NULL = the device's null stream).
 hipStream_t stream_of(void* s);
 
-// Device scratch owned by the library: split-K partials and their arrival
-// counters. Grown on demand, never shrunk; counters are zeroed once at
-// allocation and every kernel that uses them returns them to zero.
-struct Workspace {
-    float* partial = nullptr;
-    size_t partial_bytes = 0;
-    unsigned* counters = nullptr;
-    size_t counter_count = 0;
-};
-// Ensures the current device's workspace holds at least the requested
-// sizes. Returns false (with the error set) on allocation failure.
-bool workspace_reserve(size_t partial_bytes, size_t counters, Workspace** out);
+struct OutDesc;
+int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
+                       const float* residual, float* y, int M, int N, int K, int epilogue);
+int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
+                          const float* residual, const OutDesc& od, int M, int N, int K, int epilogue);
 
 // Dispatch counters (the gorch ReadMetalDispatchCounts analogue).
 enum Counter {
@@ -71,6 +63,61 @@ int check_launch(const char* what);
     } while (0)
 
 // ---------------------------------------------------------------- device side
+
+// Where a Linear's output element (m, n) goes. Columns split into up to
+// three segments (the fused QKV projection: Q to a buffer, K and V straight
+// into the KV cache). Row m of a segment lands at
+//   ptr + (m / rows_per_seq) * seq_stride + (m % rows_per_seq + pos) * row_stride + (n - n_begin)
+// where pos is *pos_dev for segments with use_pos set (the cache length
+// before this forward), else 0.
+struct OutDesc {
+    float* ptr[3];
+    int n_end[3];
+    long long seq_stride[3];
+    long long row_stride[3];
+    int use_pos[3];
+    int nseg;
+    int rows_per_seq;
+    const int* pos_dev;
+
+    static OutDesc plain(float* y, int N) {
+        OutDesc d{};
+        d.ptr[0] = y;
+        d.n_end[0] = N;
+        d.seq_stride[0] = 0;
+        d.row_stride[0] = N;
+        d.use_pos[0] = 0;
+        d.nseg = 1;
+        d.rows_per_seq = 1 << 30;
+        d.pos_dev = nullptr;
+        return d;
+    }
+
+    __device__ __forceinline__ float* at(int m, int n) const {
+        int s = 0, n0 = 0;
+        while (s + 1 < nseg && n >= n_end[s]) {
+            n0 = n_end[s];
+            s++;
+        }
+        const int seq = m / rows_per_seq;
+        int r = m - seq * rows_per_seq;
+        if (use_pos[s]) r += *pos_dev;
+        return ptr[s] + seq * seq_stride[s] + (long long)r * row_stride[s] + (n - n0);
+    }
+};
+
+// Arguments of the cached-attention kernel (attention.hip).
+struct AttnArgs {
+    const float* q;      // [rows, q_stride], head h at columns h*hd
+    const float* kc;     // [batch][max_seq][dim]
+    const float* vc;
+    float* out;          // [rows, dim]
+    const int* pos_dev;  // cache length before the new rows (device), or null
+    int pos_host;        // used when pos_dev is null
+    int new_seq, dim, hd, max_seq, q_stride, causal;
+    float scale;
+};
+int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows);
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));

@@ -24,11 +24,12 @@
 
 namespace gh {
 
-// NW waves per block split K; NT 16-row weight tiles per block.
-template <int NT, int NW>
+// NW waves per block split K; NT 16-row weight tiles per block; U k-steps
+// of loads issued per wave before their MFMAs.
+template <int NT, int NW, int U>
 __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
     const float* __restrict__ x, const uint16_t* __restrict__ W, const float* __restrict__ bias,
-    const float* residual, float* y, int M, int N, int K, int kw, int epilogue) {
+    const float* residual, OutDesc od, int M, int N, int K, int kw, int epilogue) {
     __shared__ floatx4 red[NW][NT][64];
 
     const int lane = threadIdx.x & 63;
@@ -59,7 +60,6 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
 
     // U k-steps per iteration: all weight loads of the group are issued
     // before any MFMA so several 16-byte loads per lane are in flight.
-    constexpr int U = (NT >= 4) ? 2 : 4;
     for (int k0 = kb; k0 < ke; k0 += 32 * U) {
         uint4 wv[U][NT];
         float f[U][8];
@@ -113,9 +113,8 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
             for (int w = 1; w < NW; w++) s += red[w][t][e][v];
             if (bias) s = s + bias[on];
             if (epilogue == GORCH_HIP_EPI_GELU) s = gelu_tanh(s);
-            size_t idx = (size_t)om * N + on;
-            if (residual) s = residual[idx] + s;
-            y[idx] = s;
+            if (residual) s = residual[(size_t)om * N + on] + s;
+            *od.at(om, on) = s;
         }
     }
 }
@@ -128,50 +127,71 @@ static int env_int(const char* name, int dflt) {
 // Launch plan: NT weight tiles and NW K-splitting waves per block, chosen
 // from a sweep of the decode shapes (GPT-2 small and XL, M = 1..16) on
 // MI355X. GORCH_HIP_GEMV_NT / GORCH_HIP_GEMV_NW override them.
-static void plan_gemv(int M, int N, int K, int* nt, int* nw) {
+struct GemvPlan {
+    int nt, nw, u;
+};
+
+static GemvPlan plan_gemv(int M, int N, int K) {
     static const int nt_env = env_int("GORCH_HIP_GEMV_NT", 0);
     static const int nw_env = env_int("GORCH_HIP_GEMV_NW", 0);
+    static const int u_env = env_int("GORCH_HIP_GEMV_U", 0);
     const int ntiles = (N + 15) / 16;
-    int t, w;
-    if (ntiles >= 2048) {          // LM-head class: many tiles, short K
-        t = M > 4 ? 4 : 2;
-        w = M > 4 ? 8 : 4;
+    GemvPlan p;
+    if (ntiles >= 2048) {          // LM-head class: many tiles
+        p.nt = 2;
+        if (M == 1 && K < 1024) {
+            p.nw = 4;
+            p.u = 8;
+        } else {
+            p.nw = 1;
+            p.u = 2;
+        }
     } else if (ntiles >= 256) {    // FFN-up / fused-QKV class
-        t = 2;
-        w = K >= 1536 ? 16 : 8;
+        p.nt = N >= 4096 ? 2 : 1;
+        p.nw = 8;
+        p.u = 2;
     } else {                       // narrow N: deep K split inside the block
-        t = 1;
-        w = 8;
+        p.nt = 1;
+        p.nw = 8;
+        p.u = M == 1 ? 4 : 2;
     }
     // keep at least one 32-wide k-step per wave
-    while (w > 4 && (K + w - 1) / w < 32) w /= 2;
-    *nt = nt_env ? nt_env : t;
-    *nw = nw_env ? nw_env : w;
+    while (p.nw > 1 && (K + p.nw - 1) / p.nw < 32) p.nw /= 2;
+    if (nt_env) p.nt = nt_env;
+    if (nw_env) p.nw = nw_env;
+    if (u_env) p.u = u_env;
+    return p;
 }
 
-template <int NT, int NW>
+template <int NT, int NW, int U>
 static void launch_t(hipStream_t s, dim3 grid, const float* x, const uint16_t* W, const float* bias,
-                     const float* residual, float* y, int M, int N, int K, int kw, int epilogue) {
-    hipLaunchKernelGGL((k_linear_bf16_mfma<NT, NW>), grid, dim3(NW * 64), 0, s, x, W, bias, residual, y, M,
-                       N, K, kw, epilogue);
+                     const float* residual, const OutDesc& od, int M, int N, int K, int kw, int epilogue) {
+    hipLaunchKernelGGL((k_linear_bf16_mfma<NT, NW, U>), grid, dim3(NW * 64), 0, s, x, W, bias, residual, od,
+                       M, N, K, kw, epilogue);
 }
 
 int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                        const float* residual, float* y, int M, int N, int K, int epilogue) {
-    int nt, nw;
-    plan_gemv(M, N, K, &nt, &nw);
-    int per = (K + nw - 1) / nw;
+    return launch_linear_bf16_od(s, x, W, bias, residual, OutDesc::plain(y, N), M, N, K, epilogue);
+}
+
+int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
+                          const float* residual, const OutDesc& od, int M, int N, int K, int epilogue) {
+    GemvPlan p = plan_gemv(M, N, K);
+    int per = (K + p.nw - 1) / p.nw;
     int kw = (per + 31) / 32 * 32;
-    dim3 grid((N + 16 * nt - 1) / (16 * nt), (M + 15) / 16);
-#define GH_CASE(T, WV)                                                                 \
-    if (nt == T && nw == WV) {                                                         \
-        launch_t<T, WV>(s, grid, x, W, bias, residual, y, M, N, K, kw, epilogue);      \
-        count(M <= 16 ? CNT_GEMV : CNT_GEMM);                                          \
-        return check_launch("linear_bf16");                                            \
+    dim3 grid((N + 16 * p.nt - 1) / (16 * p.nt), (M + 15) / 16);
+#define GH_CASE(T, WV, UV)                                                                   \
+    if (p.nt == T && p.nw == WV && p.u == UV) {                                              \
+        launch_t<T, WV, UV>(s, grid, x, W, bias, residual, od, M, N, K, kw, epilogue);       \
+        count(M <= 16 ? CNT_GEMV : CNT_GEMM);                                                \
+        return check_launch("linear_bf16");                                                  \
     }
-    GH_CASE(1, 4) GH_CASE(1, 8) GH_CASE(1, 16)
-    GH_CASE(2, 4) GH_CASE(2, 8) GH_CASE(2, 16)
-    GH_CASE(4, 4) GH_CASE(4, 8) GH_CASE(4, 16)
+#define GH_CASES_U(T, WV) GH_CASE(T, WV, 2) GH_CASE(T, WV, 4) GH_CASE(T, WV, 8)
+#define GH_CASES_W(T) GH_CASES_U(T, 1) GH_CASES_U(T, 2) GH_CASES_U(T, 4) GH_CASES_U(T, 8) GH_CASES_U(T, 16)
+    GH_CASES_W(1) GH_CASES_W(2) GH_CASES_W(4)
+#undef GH_CASES_W
+#undef GH_CASES_U
 #undef GH_CASE
     set_error("linear_bf16: unsupported tile plan");
     return GORCH_HIP_EUNSUPPORTED;

@@ -1,0 +1,503 @@
+// gpt.hip — host-side GPT decode engine over the HIP kernels: the C++
+// counterpart of gorch's nn.GPT / nn.KVCache / model.generateCached
+// (nn/gpt.go:12-121, nn/transformer.go:53-63, nn/attention.go:313-400,
+// nn/kvcache.go:14-60, model/generate.go:94-131), with weights resident in
+// HBM (gpt.ToMetal, nn/gpt.go:241-257).
+//
+// Layout in HBM:
+//   - one weight blob; per layer a fused QKV weight [3d, d] bf16 (the rows of
+//     Wq, Wk, Wv back to back — what gorch's Q/K/V Linears compute, in one
+//     weight stream), Wo [d, d], FFN1 [4d, d], FFN2 [d, 4d] bf16, f32 biases
+//     and LayerNorm parameters; f32 wte/wpe; LM head [V, d] bf16;
+//   - KV cache f32 [layer][batch][capacity][d] for K and for V;
+//   - the cache length (`pos`) and the generation step live in device memory,
+//     so a decode step is position-independent and is captured once as a HIP
+//     graph and replayed for every token without host synchronisation.
+//
+// Per layer and forward: LayerNorm -> fused QKV GEMV writing Q to a buffer
+// and K/V rows straight into the cache at pos -> cached attention -> Wo GEMV
+// with bias and residual fused -> LayerNorm -> FFN1 GEMV with bias+GELU ->
+// FFN2 GEMV with bias and residual fused. Then the final LayerNorm (on the
+// last row of each sequence when generating), LM head GEMV, and argmax.
+#include <cstring>
+#include <vector>
+
+#include "common.h"
+
+namespace gh {
+
+int launch_layernorm(hipStream_t s, const float* x, const float* g, const float* b, float* y, int M, int N,
+                     float eps, long long in_stride);
+int launch_embed_pos(hipStream_t s, const float* wte, const float* wpe, const int* ids, const int* pos_dev,
+                     float* out, int dim, int n_per_seq, int rows);
+int launch_argmax(hipStream_t s, const float* logits, int rows, int n, int* out, int* hist, const int* step_dev,
+                  int hist_stride, int* pos_dev, int pos_inc);
+int launch_advance_step(hipStream_t s, int* step_dev);
+
+__global__ void k_pos_add(int* pos_dev, int n) { *pos_dev += n; }
+
+struct LayerW {
+    uint16_t *wqkv, *wo, *w1, *w2;
+    float *bqkv, *bo, *b1, *b2, *ln1_g, *ln1_b, *ln2_g, *ln2_b;
+};
+
+}  // namespace gh
+
+using namespace gh;
+
+struct gorch_hip_gpt {
+    int vocab = 0, dim = 0, heads = 0, layers = 0, max_seq = 0;
+    char* blob = nullptr;
+    float *wte = nullptr, *wpe = nullptr, *lnf_g = nullptr, *lnf_b = nullptr, *blm = nullptr;
+    uint16_t* wlm = nullptr;
+    std::vector<LayerW> L;
+    // activations, grown on demand
+    size_t rows_cap = 0, logit_rows_cap = 0;
+    float *x = nullptr, *h = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr;
+    int* ids = nullptr;
+    size_t ids_cap = 0;
+    hipStream_t stream = nullptr;  // engine stream (default priority), used for graph capture
+};
+
+struct gorch_hip_kvcache {
+    gorch_hip_gpt* gpt = nullptr;
+    int batch = 0, capacity = 0, len = 0;
+    float *k = nullptr, *v = nullptr;
+    int* state = nullptr;  // [0] = pos (cache length), [1] = generation step
+    int* hist = nullptr;   // generated tokens [capacity][batch]
+};
+
+namespace gh {
+
+static float* kc_layer(gorch_hip_kvcache* c, int l) {
+    return c->k + (size_t)l * c->batch * c->capacity * c->gpt->dim;
+}
+static float* vc_layer(gorch_hip_kvcache* c, int l) {
+    return c->v + (size_t)l * c->batch * c->capacity * c->gpt->dim;
+}
+
+static int ensure_acts(gorch_hip_gpt* g, size_t rows, size_t logit_rows) {
+    if (rows > g->rows_cap) {
+        (void)hipFree(g->x);
+        (void)hipFree(g->h);
+        (void)hipFree(g->q);
+        (void)hipFree(g->att);
+        (void)hipFree(g->ff);
+        g->x = g->h = g->q = g->att = g->ff = nullptr;
+        g->rows_cap = 0;
+        const size_t d = g->dim;
+        GH_TRY(check(hipMalloc(&g->x, rows * d * 4), "hipMalloc x"));
+        GH_TRY(check(hipMalloc(&g->h, rows * d * 4), "hipMalloc h"));
+        GH_TRY(check(hipMalloc(&g->q, rows * d * 4), "hipMalloc q"));
+        GH_TRY(check(hipMalloc(&g->att, rows * d * 4), "hipMalloc att"));
+        GH_TRY(check(hipMalloc(&g->ff, rows * 4 * d * 4), "hipMalloc ff"));
+        g->rows_cap = rows;
+    }
+    if (logit_rows > g->logit_rows_cap) {
+        (void)hipFree(g->logits);
+        g->logits = nullptr;
+        g->logit_rows_cap = 0;
+        GH_TRY(check(hipMalloc(&g->logits, logit_rows * g->vocab * 4), "hipMalloc logits"));
+        g->logit_rows_cap = logit_rows;
+    }
+    if (rows > g->ids_cap) {
+        (void)hipFree(g->ids);
+        g->ids = nullptr;
+        g->ids_cap = 0;
+        GH_TRY(check(hipMalloc(&g->ids, rows * sizeof(int)), "hipMalloc ids"));
+        g->ids_cap = rows;
+    }
+    return GORCH_HIP_OK;
+}
+
+// One GPT forward over n new tokens per sequence (ids already in g->ids,
+// row-major [batch, n]). all_rows: LM head on every row (logits
+// [batch*n, V]); otherwise only on the last row of each sequence
+// (logits [batch, V]). Does not advance pos.
+static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows, hipStream_t s) {
+    const int d = g->dim, B = c->batch, rows = B * n, hd = d / g->heads;
+    const float eps = 1e-5f;
+    const int* pos = c->state;
+    GH_TRY(launch_embed_pos(s, g->wte, g->wpe, g->ids, pos, g->x, d, n, rows));
+    for (int l = 0; l < g->layers; l++) {
+        const LayerW& w = g->L[l];
+        GH_TRY(launch_layernorm(s, g->x, w.ln1_g, w.ln1_b, g->h, rows, d, eps, d));
+        OutDesc od{};
+        od.nseg = 3;
+        od.rows_per_seq = n;
+        od.pos_dev = pos;
+        od.ptr[0] = g->q;
+        od.n_end[0] = d;
+        od.seq_stride[0] = (long long)n * d;
+        od.row_stride[0] = d;
+        od.use_pos[0] = 0;
+        od.ptr[1] = kc_layer(c, l);
+        od.ptr[2] = vc_layer(c, l);
+        od.n_end[1] = 2 * d;
+        od.n_end[2] = 3 * d;
+        for (int sgi = 1; sgi < 3; sgi++) {
+            od.seq_stride[sgi] = (long long)c->capacity * d;
+            od.row_stride[sgi] = d;
+            od.use_pos[sgi] = 1;
+        }
+        GH_TRY(launch_linear_bf16_od(s, g->h, w.wqkv, w.bqkv, nullptr, od, rows, 3 * d, d, GORCH_HIP_EPI_NONE));
+        AttnArgs a{g->q, kc_layer(c, l), vc_layer(c, l), g->att, pos, 0, n, d, hd, c->capacity, d, 1,
+                   1.0f / sqrtf((float)hd)};
+        GH_TRY(launch_attn_cached(s, a, g->heads, rows));
+        GH_TRY(launch_linear_bf16(s, g->att, w.wo, w.bo, g->x, g->x, rows, d, d, GORCH_HIP_EPI_NONE));
+        GH_TRY(launch_layernorm(s, g->x, w.ln2_g, w.ln2_b, g->h, rows, d, eps, d));
+        GH_TRY(launch_linear_bf16(s, g->h, w.w1, w.b1, nullptr, g->ff, rows, 4 * d, d, GORCH_HIP_EPI_GELU));
+        GH_TRY(launch_linear_bf16(s, g->ff, w.w2, w.b2, g->x, g->x, rows, d, 4 * d, GORCH_HIP_EPI_NONE));
+    }
+    if (all_rows) {
+        GH_TRY(launch_layernorm(s, g->x, g->lnf_g, g->lnf_b, g->h, rows, d, eps, d));
+        GH_TRY(launch_linear_bf16(s, g->h, g->wlm, g->blm, nullptr, g->logits, rows, g->vocab, d,
+                                  GORCH_HIP_EPI_NONE));
+    } else {
+        GH_TRY(launch_layernorm(s, g->x + (size_t)(n - 1) * d, g->lnf_g, g->lnf_b, g->h, B, d, eps,
+                                (long long)n * d));
+        GH_TRY(launch_linear_bf16(s, g->h, g->wlm, g->blm, nullptr, g->logits, B, g->vocab, d,
+                                  GORCH_HIP_EPI_NONE));
+    }
+    return GORCH_HIP_OK;
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+}  // namespace gh
+
+extern "C" {
+
+gorch_hip_gpt* gorch_hip_gpt_create(const gorch_hip_gpt_weights* w) {
+    if (!w || w->vocab <= 0 || w->dim <= 0 || w->heads <= 0 || w->layers <= 0 || w->max_seq <= 0 ||
+        w->dim % w->heads != 0) {
+        set_error("gorch_hip_gpt_create: bad configuration");
+        return nullptr;
+    }
+    const int hd = w->dim / w->heads;
+    if (hd % 4 != 0 || hd > 256 || w->dim % 8 != 0) {
+        set_error("gorch_hip_gpt_create: needs dim % 8 == 0 and head_dim a multiple of 4, <= 256");
+        return nullptr;
+    }
+    if (w->max_seq > 16384) {
+        set_error("gorch_hip_gpt_create: max_seq above 16384 is not supported");
+        return nullptr;
+    }
+    auto* g = new gorch_hip_gpt();
+    g->vocab = w->vocab;
+    g->dim = w->dim;
+    g->heads = w->heads;
+    g->layers = w->layers;
+    g->max_seq = w->max_seq;
+    const size_t d = w->dim, V = w->vocab, S = w->max_seq;
+    // blob layout
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        size_t o = off;
+        off += align256(bytes);
+        return o;
+    };
+    const size_t o_wte = take(V * d * 4), o_wpe = take(S * d * 4), o_lnf_g = take(d * 4), o_lnf_b = take(d * 4);
+    const size_t o_wlm = take(V * d * 2), o_blm = take(V * 4);
+    struct LOff {
+        size_t wqkv, bqkv, wo, bo, w1, b1, w2, b2, ln1_g, ln1_b, ln2_g, ln2_b;
+    };
+    std::vector<LOff> lo(w->layers);
+    for (int l = 0; l < w->layers; l++) {
+        lo[l].wqkv = take(3 * d * d * 2);
+        lo[l].bqkv = take(3 * d * 4);
+        lo[l].wo = take(d * d * 2);
+        lo[l].bo = take(d * 4);
+        lo[l].w1 = take(4 * d * d * 2);
+        lo[l].b1 = take(4 * d * 4);
+        lo[l].w2 = take(4 * d * d * 2);
+        lo[l].b2 = take(d * 4);
+        lo[l].ln1_g = take(d * 4);
+        lo[l].ln1_b = take(d * 4);
+        lo[l].ln2_g = take(d * 4);
+        lo[l].ln2_b = take(d * 4);
+    }
+    if (check(hipMalloc(&g->blob, off), "hipMalloc weights")) {
+        delete g;
+        return nullptr;
+    }
+    bool ok = true;
+    auto put = [&](size_t o, const void* src, size_t bytes) {
+        if (!ok) return;
+        if (!src) {
+            set_error("gorch_hip_gpt_create: null weight pointer");
+            ok = false;
+            return;
+        }
+        ok = check(hipMemcpy(g->blob + o, src, bytes, hipMemcpyHostToDevice), "upload weights") == 0;
+    };
+    put(o_wte, w->wte, V * d * 4);
+    put(o_wpe, w->wpe, S * d * 4);
+    put(o_lnf_g, w->lnf_g, d * 4);
+    put(o_lnf_b, w->lnf_b, d * 4);
+    put(o_wlm, w->wlm, V * d * 2);
+    put(o_blm, w->blm, V * 4);
+    for (int l = 0; l < w->layers && ok; l++) {
+        put(lo[l].wqkv, w->wq[l], d * d * 2);
+        put(lo[l].wqkv + d * d * 2, w->wk[l], d * d * 2);
+        put(lo[l].wqkv + 2 * d * d * 2, w->wv[l], d * d * 2);
+        put(lo[l].bqkv, w->bq[l], d * 4);
+        put(lo[l].bqkv + d * 4, w->bk[l], d * 4);
+        put(lo[l].bqkv + 2 * d * 4, w->bv[l], d * 4);
+        put(lo[l].wo, w->wo[l], d * d * 2);
+        put(lo[l].bo, w->bo[l], d * 4);
+        put(lo[l].w1, w->w1[l], 4 * d * d * 2);
+        put(lo[l].b1, w->b1[l], 4 * d * 4);
+        put(lo[l].w2, w->w2[l], 4 * d * d * 2);
+        put(lo[l].b2, w->b2[l], d * 4);
+        put(lo[l].ln1_g, w->ln1_g[l], d * 4);
+        put(lo[l].ln1_b, w->ln1_b[l], d * 4);
+        put(lo[l].ln2_g, w->ln2_g[l], d * 4);
+        put(lo[l].ln2_b, w->ln2_b[l], d * 4);
+    }
+    if (!ok) {
+        gorch_hip_gpt_free(g);
+        return nullptr;
+    }
+    auto F = [&](size_t o) { return reinterpret_cast<float*>(g->blob + o); };
+    auto H = [&](size_t o) { return reinterpret_cast<uint16_t*>(g->blob + o); };
+    g->wte = F(o_wte);
+    g->wpe = F(o_wpe);
+    g->lnf_g = F(o_lnf_g);
+    g->lnf_b = F(o_lnf_b);
+    g->wlm = H(o_wlm);
+    g->blm = F(o_blm);
+    g->L.resize(w->layers);
+    for (int l = 0; l < w->layers; l++) {
+        LayerW& L = g->L[l];
+        L.wqkv = H(lo[l].wqkv);
+        L.bqkv = F(lo[l].bqkv);
+        L.wo = H(lo[l].wo);
+        L.bo = F(lo[l].bo);
+        L.w1 = H(lo[l].w1);
+        L.b1 = F(lo[l].b1);
+        L.w2 = H(lo[l].w2);
+        L.b2 = F(lo[l].b2);
+        L.ln1_g = F(lo[l].ln1_g);
+        L.ln1_b = F(lo[l].ln1_b);
+        L.ln2_g = F(lo[l].ln2_g);
+        L.ln2_b = F(lo[l].ln2_b);
+    }
+    if (check(hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking), "hipStreamCreate")) {
+        gorch_hip_gpt_free(g);
+        return nullptr;
+    }
+    return g;
+}
+
+void gorch_hip_gpt_free(gorch_hip_gpt* g) {
+    if (!g) return;
+    if (g->stream) {
+        (void)hipStreamSynchronize(g->stream);
+        (void)hipStreamDestroy(g->stream);
+    }
+    (void)hipFree(g->blob);
+    (void)hipFree(g->x);
+    (void)hipFree(g->h);
+    (void)hipFree(g->q);
+    (void)hipFree(g->att);
+    (void)hipFree(g->ff);
+    (void)hipFree(g->logits);
+    (void)hipFree(g->ids);
+    delete g;
+}
+
+gorch_hip_kvcache* gorch_hip_kvcache_create(gorch_hip_gpt* g, int batch, int capacity) {
+    if (!g || batch <= 0 || capacity <= 0 || capacity > g->max_seq) {
+        set_error("gorch_hip_kvcache_create: bad batch or capacity (1..max_seq)");
+        return nullptr;
+    }
+    auto* c = new gorch_hip_kvcache();
+    c->gpt = g;
+    c->batch = batch;
+    c->capacity = capacity;
+    const size_t elems = (size_t)g->layers * batch * capacity * g->dim;
+    if (check(hipMalloc(&c->k, elems * 4), "hipMalloc kv") || check(hipMalloc(&c->v, elems * 4), "hipMalloc kv") ||
+        check(hipMalloc(&c->state, 2 * sizeof(int)), "hipMalloc state") ||
+        check(hipMalloc(&c->hist, ((size_t)capacity + 1) * batch * sizeof(int)), "hipMalloc hist") ||
+        check(hipMemset(c->state, 0, 2 * sizeof(int)), "hipMemset state")) {
+        gorch_hip_kvcache_free(c);
+        return nullptr;
+    }
+    return c;
+}
+
+void gorch_hip_kvcache_free(gorch_hip_kvcache* c) {
+    if (!c) return;
+    (void)hipFree(c->k);
+    (void)hipFree(c->v);
+    (void)hipFree(c->state);
+    (void)hipFree(c->hist);
+    delete c;
+}
+
+int gorch_hip_kvcache_len(const gorch_hip_kvcache* c) { return c ? c->len : 0; }
+
+int gorch_hip_kvcache_reset(gorch_hip_kvcache* c) {
+    GH_REQUIRE(c, "gorch_hip_kvcache_reset: null cache");
+    c->len = 0;
+    return check(hipMemset(c->state, 0, 2 * sizeof(int)), "kvcache reset");
+}
+
+int gorch_hip_kvcache_read(const gorch_hip_kvcache* c, int layer, int seq, float* keys, float* values) {
+    GH_REQUIRE(c && layer >= 0 && layer < c->gpt->layers && seq >= 0 && seq < c->batch,
+               "gorch_hip_kvcache_read: bad layer or sequence");
+    const size_t d = c->gpt->dim, off = ((size_t)layer * c->batch + seq) * c->capacity * d;
+    if (keys) GH_TRY(check(hipMemcpy(keys, c->k + off, (size_t)c->len * d * 4, hipMemcpyDeviceToHost), "read k"));
+    if (values)
+        GH_TRY(check(hipMemcpy(values, c->v + off, (size_t)c->len * d * 4, hipMemcpyDeviceToHost), "read v"));
+    return GORCH_HIP_OK;
+}
+
+int gorch_hip_gpt_forward_cached(void* stream, gorch_hip_gpt* g, gorch_hip_kvcache* c, const int* ids, int n,
+                                 float* logits) {
+    GH_REQUIRE(g && c && c->gpt == g && ids && n > 0, "gorch_hip_gpt_forward_cached: bad arguments");
+    if (c->len + n > c->capacity) {
+        set_error("gorch_hip_gpt_forward_cached: cached sequence length exceeds MaxSeq");
+        return GORCH_HIP_EINVAL;
+    }
+    const int rows = c->batch * n;
+    for (int i = 0; i < rows; i++)
+        GH_REQUIRE(ids[i] >= 0 && ids[i] < g->vocab, "gorch_hip_gpt_forward_cached: token id out of range");
+    hipStream_t s = stream_of(stream);
+    GH_TRY(ensure_acts(g, rows, rows));
+    GH_TRY(check(hipMemcpyAsync(g->ids, ids, rows * sizeof(int), hipMemcpyHostToDevice, s), "upload ids"));
+    GH_TRY(forward(g, c, n, true, s));
+    hipLaunchKernelGGL(k_pos_add, dim3(1), dim3(1), 0, s, c->state, n);
+    GH_TRY(check_launch("pos_add"));
+    c->len += n;
+    if (logits)
+        GH_TRY(check(hipMemcpyAsync(logits, g->logits, (size_t)rows * g->vocab * 4, hipMemcpyDeviceToHost, s),
+                     "download logits"));
+    return check(hipStreamSynchronize(s), "forward sync");
+}
+
+int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* g, const int* prompts, int batch, int n_prompt,
+                              int max_new, int* out_ids, int* out_len, float* step_logits, float* timing_ms,
+                              int flags) {
+    GH_REQUIRE(g && prompts && out_ids && out_len && batch > 0 && n_prompt > 0 && max_new >= 0,
+               "gorch_hip_generate_cached: bad arguments");
+    // Prompt truncation to the last MaxSeq tokens (model/generate.go:101-103).
+    const int np = n_prompt > g->max_seq ? g->max_seq : n_prompt;
+    const int skip = n_prompt - np;
+    std::vector<int> ids((size_t)batch * np);
+    for (int b = 0; b < batch; b++)
+        for (int i = 0; i < np; i++) {
+            int t = prompts[(size_t)b * n_prompt + skip + i];
+            GH_REQUIRE(t >= 0 && t < g->vocab, "gorch_hip_generate_cached: token id out of range");
+            ids[(size_t)b * np + i] = t;
+        }
+    // The reference loop: token i comes from the latest logits; stop before
+    // a forward once the cache holds MaxSeq tokens (model/generate.go:107-129).
+    int tokens = 0, forwards = 0, len = np;
+    for (int i = 0; i < max_new; i++) {
+        tokens++;
+        if (len >= g->max_seq) break;
+        forwards++;
+        len++;
+    }
+    const int capacity = len;
+    GH_TRY(check(hipStreamSynchronize(stream_of(stream)), "caller stream sync"));
+    gorch_hip_kvcache* c = gorch_hip_kvcache_create(g, batch, capacity);
+    if (!c) return GORCH_HIP_ENOMEM;
+    hipStream_t s = g->stream;
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int rc = GORCH_HIP_OK;
+    const bool use_graph = (flags & 1) && !step_logits;
+    auto fail = [&](int r) {
+        rc = r;
+        return r;
+    };
+    do {
+        if (ensure_acts(g, (size_t)batch * np, batch)) { fail(GORCH_HIP_ENOMEM); break; }
+        for (auto& e : ev)
+            if (check(hipEventCreate(&e), "hipEventCreate")) { fail(GORCH_HIP_ERUNTIME); break; }
+        if (rc) break;
+        if (check(hipMemcpyAsync(g->ids, ids.data(), ids.size() * sizeof(int), hipMemcpyHostToDevice, s), "ids")) {
+            fail(GORCH_HIP_ERUNTIME);
+            break;
+        }
+        (void)hipEventRecord(ev[0], s);
+        // prefill: logits of the last prompt row per sequence -> token 0
+        if (forward(g, c, np, false, s) ||
+            launch_argmax(s, g->logits, batch, g->vocab, g->ids, c->hist, c->state + 1, batch, c->state, np) ||
+            launch_advance_step(s, c->state + 1)) {
+            fail(GORCH_HIP_ERUNTIME);
+            break;
+        }
+        (void)hipEventRecord(ev[1], s);
+        if (step_logits) {
+            if (check(hipMemcpyAsync(step_logits, g->logits, (size_t)batch * g->vocab * 4, hipMemcpyDeviceToHost, s),
+                      "logits")) { fail(GORCH_HIP_ERUNTIME); break; }
+        }
+        // one decode step: forward the latest token of each sequence, choose the next
+        auto step = [&]() -> int {
+            GH_TRY(forward(g, c, 1, false, s));
+            GH_TRY(launch_argmax(s, g->logits, batch, g->vocab, g->ids, c->hist, c->state + 1, batch, c->state, 1));
+            return launch_advance_step(s, c->state + 1);
+        };
+        if (use_graph && forwards > 0) {
+            if (check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture")) {
+                fail(GORCH_HIP_ERUNTIME);
+                break;
+            }
+            int r = step();
+            hipError_t e = hipStreamEndCapture(s, &graph);
+            if (r || check(e, "end capture") || check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate")) {
+                fail(GORCH_HIP_ERUNTIME);
+                break;
+            }
+            for (int i = 0; i < forwards; i++)
+                if (check(hipGraphLaunch(exec, s), "graph launch")) { fail(GORCH_HIP_ERUNTIME); break; }
+        } else {
+            for (int i = 0; i < forwards && !rc; i++) {
+                if (step()) { fail(GORCH_HIP_ERUNTIME); break; }
+                if (step_logits && i + 1 < tokens) {
+                    if (check(hipMemcpyAsync(step_logits + (size_t)(i + 1) * batch * g->vocab, g->logits,
+                                             (size_t)batch * g->vocab * 4, hipMemcpyDeviceToHost, s), "logits"))
+                        fail(GORCH_HIP_ERUNTIME);
+                }
+            }
+        }
+        if (rc) break;
+        (void)hipEventRecord(ev[2], s);
+        std::vector<int> hist((size_t)tokens * batch);
+        if (tokens > 0 &&
+            check(hipMemcpyAsync(hist.data(), c->hist, hist.size() * sizeof(int), hipMemcpyDeviceToHost, s), "hist")) {
+            fail(GORCH_HIP_ERUNTIME);
+            break;
+        }
+        if (check(hipStreamSynchronize(s), "generate sync")) { fail(GORCH_HIP_ERUNTIME); break; }
+        // result = (truncated) prompt followed by the generated tokens
+        const int total = np + tokens;
+        for (int b = 0; b < batch; b++) {
+            for (int i = 0; i < np; i++) out_ids[(size_t)b * total + i] = ids[(size_t)b * np + i];
+            for (int i = 0; i < tokens; i++) out_ids[(size_t)b * total + np + i] = hist[(size_t)i * batch + b];
+        }
+        *out_len = total;
+        if (timing_ms) {
+            float a = 0.f, bb = 0.f;
+            (void)hipEventElapsedTime(&a, ev[0], ev[1]);
+            (void)hipEventElapsedTime(&bb, ev[1], ev[2]);
+            timing_ms[0] = a;
+            timing_ms[1] = bb;
+            timing_ms[2] = (float)forwards;
+        }
+    } while (false);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    for (auto& e : ev)
+        if (e) (void)hipEventDestroy(e);
+    (void)hipStreamSynchronize(s);
+    gorch_hip_kvcache_free(c);
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,90 @@
+// norm.hip — LayerNorm (nn/layernorm.go:31-91) and RMSNorm
+// (nn/rmsnorm.go:39-81; MSL rmsnorm_forward, metal/kernels.go:152-190).
+//
+// One 256-thread block per row. Statistics accumulate in f64 exactly as the
+// reference's CPU loops do (mean and variance for LayerNorm, sum of squares
+// for RMSNorm); the row stays in L1/L2 between the two passes. The inverse
+// is rounded to f32 and the output computed in f32 in the reference's
+// operand order.
+#include "common.h"
+
+namespace gh {
+
+__device__ double block_sum_d(double v, double* sh) {
+    v = wave_sum_d(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) sh[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+    const int nw = blockDim.x >> 6;
+    for (int w = 0; w < nw; w++) t += sh[w];
+    __syncthreads();
+    return t;
+}
+
+__global__ __launch_bounds__(256) void k_layernorm(const float* __restrict__ x, const float* __restrict__ g,
+                                                   const float* __restrict__ b, float* __restrict__ y, int N,
+                                                   float eps, long long in_stride) {
+    __shared__ double sh[4];
+    const float* row = x + (size_t)blockIdx.x * in_stride;
+    float* out = y + (size_t)blockIdx.x * N;
+    double s = 0.0;
+    for (int j = threadIdx.x; j < N; j += blockDim.x) s += (double)row[j];
+    const double mean = block_sum_d(s, sh) / (double)N;
+    double v = 0.0;
+    for (int j = threadIdx.x; j < N; j += blockDim.x) {
+        double d = (double)row[j] - mean;
+        v += d * d;
+    }
+    const double var = block_sum_d(v, sh) / (double)N;
+    const float inv = (float)(1.0 / sqrt(var + (double)eps));
+    const float fm = (float)mean;
+    for (int j = threadIdx.x; j < N; j += blockDim.x) {
+        float normalized = (row[j] - fm) * inv;
+        out[j] = normalized * g[j] + b[j];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x, const float* __restrict__ g,
+                                                 float* __restrict__ y, int N, float eps) {
+    __shared__ double sh[4];
+    const float* row = x + (size_t)blockIdx.x * N;
+    float* out = y + (size_t)blockIdx.x * N;
+    double s = 0.0;
+    for (int j = threadIdx.x; j < N; j += blockDim.x) s += (double)row[j] * (double)row[j];
+    const double ss = block_sum_d(s, sh);
+    const float inv = (float)(1.0 / sqrt(ss / (double)N + (double)eps));
+    for (int j = threadIdx.x; j < N; j += blockDim.x) out[j] = row[j] * inv * g[j];
+}
+
+// Row i of the input starts at x + i * in_stride (in_stride = N for a dense
+// matrix); the output is dense [M, N].
+int launch_layernorm(hipStream_t s, const float* x, const float* g, const float* b, float* y, int M, int N,
+                     float eps, long long in_stride) {
+    if (M == 0) return GORCH_HIP_OK;
+    hipLaunchKernelGGL(k_layernorm, dim3(M), dim3(256), 0, s, x, g, b, y, N, eps, in_stride);
+    count(CNT_NORM);
+    return check_launch("layernorm");
+}
+
+}  // namespace gh
+
+using namespace gh;
+
+extern "C" int gorch_hip_layernorm(void* stream, const float* x, const float* gamma, const float* beta,
+                                   float* y, int M, int N, float eps) {
+    GH_REQUIRE(M >= 0 && N > 0, "gorch_hip_layernorm: bad shape");
+    if (M == 0) return GORCH_HIP_OK;
+    GH_REQUIRE(x && gamma && beta && y, "gorch_hip_layernorm: null pointer");
+    return launch_layernorm(stream_of(stream), x, gamma, beta, y, M, N, eps, N);
+}
+
+extern "C" int gorch_hip_rmsnorm(void* stream, const float* x, const float* gamma, float* y, int M, int N,
+                                 float eps) {
+    GH_REQUIRE(M >= 0 && N > 0, "gorch_hip_rmsnorm: bad shape");
+    if (M == 0) return GORCH_HIP_OK;
+    GH_REQUIRE(x && gamma && y, "gorch_hip_rmsnorm: null pointer");
+    hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(256), 0, stream_of(stream), x, gamma, y, N, eps);
+    count(CNT_NORM);
+    return check_launch("rmsnorm");
+}

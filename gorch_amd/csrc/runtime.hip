@@ -1,9 +1,7 @@
-// runtime.hip — device selection, errors, memory, copies, dispatch counters
-// and the library-owned split-K workspace. The Metal counterparts are
+// runtime.hip — device selection, errors, memory, copies and dispatch counters. The Metal counterparts are
 // metal/shim.m:120-437 (device, queue, buffers) and ops.go:15-78 (counters).
 #include <atomic>
 #include <cstring>
-#include <mutex>
 #include <string>
 
 #include "common.h"
@@ -28,45 +26,6 @@ hipStream_t stream_of(void* s) { return reinterpret_cast<hipStream_t>(s); }
 static std::atomic<uint64_t> g_counts[CNT_COUNT];
 
 void count(Counter c) { g_counts[c].fetch_add(1, std::memory_order_relaxed); }
-
-static constexpr int kMaxDevices = 64;
-static Workspace g_ws[kMaxDevices];
-static std::mutex g_ws_mu;
-
-bool workspace_reserve(size_t partial_bytes, size_t counters, Workspace** out) {
-    int dev = 0;
-    if (check(hipGetDevice(&dev), "hipGetDevice")) return false;
-    if (dev < 0 || dev >= kMaxDevices) {
-        set_error("device index out of range");
-        return false;
-    }
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    Workspace& w = g_ws[dev];
-    if (w.partial_bytes < partial_bytes) {
-        // Wait for in-flight users of the old buffer before replacing it.
-        if (w.partial && check(hipDeviceSynchronize(), "hipDeviceSynchronize")) return false;
-        if (w.partial) (void)hipFree(w.partial);
-        w.partial = nullptr;
-        w.partial_bytes = 0;
-        size_t want = partial_bytes < (1u << 20) ? (1u << 20) : partial_bytes;
-        if (check(hipMalloc(&w.partial, want), "workspace hipMalloc")) return false;
-        w.partial_bytes = want;
-    }
-    if (w.counter_count < counters) {
-        if (w.counters && check(hipDeviceSynchronize(), "hipDeviceSynchronize")) return false;
-        if (w.counters) (void)hipFree(w.counters);
-        w.counters = nullptr;
-        w.counter_count = 0;
-        size_t want = counters < 65536 ? 65536 : counters;
-        if (check(hipMalloc(&w.counters, want * sizeof(unsigned)), "counter hipMalloc")) return false;
-        // Zeroed once here; every split-K kernel leaves them at zero again.
-        if (check(hipMemset(w.counters, 0, want * sizeof(unsigned)), "counter hipMemset")) return false;
-        if (check(hipDeviceSynchronize(), "hipDeviceSynchronize")) return false;
-        w.counter_count = want;
-    }
-    *out = &w;
-    return true;
-}
 
 }  // namespace gh
 

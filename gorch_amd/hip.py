@@ -51,6 +51,27 @@ SIGNATURES = {
     "gorch_hip_matmul_dt": (i32, [vp, vp, vp, vp, u32, u32, u32, i32, i32, i32, i32]),
     "gorch_hip_batched_matmul_dt": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, i32, i32, i32, i32]),
     "gorch_hip_linear_bf16": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "gorch_hip_layernorm": (i32, [vp, vp, vp, vp, vp, i32, i32, f32]),
+    "gorch_hip_rmsnorm": (i32, [vp, vp, vp, vp, i32, i32, f32]),
+    "gorch_hip_add": (i32, [vp, vp, vp, vp, i64]),
+    "gorch_hip_bias_add": (i32, [vp, vp, vp, i32, i32]),
+    "gorch_hip_gelu": (i32, [vp, vp, vp, i64]),
+    "gorch_hip_silu": (i32, [vp, vp, vp, i64]),
+    "gorch_hip_swiglu": (i32, [vp, vp, vp, vp, i64]),
+    "gorch_hip_embedding": (i32, [vp, vp, i32, vp, i32, vp]),
+    "gorch_hip_attention_cached": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32]),
+    "gorch_hip_causal_softmax": (i32, [vp, vp, vp, i32, i32, i32, f32]),
+    "gorch_hip_softmax_rows": (i32, [vp, vp, i32, i32]),
+    "gorch_hip_argmax": (i32, [vp, vp, i32, i32, vp]),
+    "gorch_hip_gpt_create": (vp, [vp]),
+    "gorch_hip_gpt_free": (None, [vp]),
+    "gorch_hip_kvcache_create": (vp, [vp, i32, i32]),
+    "gorch_hip_kvcache_free": (None, [vp]),
+    "gorch_hip_kvcache_len": (i32, [vp]),
+    "gorch_hip_kvcache_reset": (i32, [vp]),
+    "gorch_hip_kvcache_read": (i32, [vp, i32, i32, vp, vp]),
+    "gorch_hip_gpt_forward_cached": (i32, [vp, vp, vp, vp, i32, vp]),
+    "gorch_hip_generate_cached": (i32, [vp, vp, vp, i32, i32, i32, vp, vp, vp, vp, i32]),
 }
 
 
@@ -138,9 +159,193 @@ def batched_matmul_dt(A, B, C_, M, N, K, batch, transA=False, transB=False, aBF1
                                           int(transB), int(aBF16), int(bBF16)))
 
 
+def _n(t):
+    return t.numel()
+
+
+def layernorm(x, gamma, beta, y, eps=1e-5) -> None:
+    M, N = x.shape
+    _ok(lib().gorch_hip_layernorm(_stream(), _p(x), _p(gamma), _p(beta), _p(y), M, N, eps))
+
+
+def rmsnorm(x, gamma, y, eps=1e-6) -> None:
+    M, N = x.shape
+    _ok(lib().gorch_hip_rmsnorm(_stream(), _p(x), _p(gamma), _p(y), M, N, eps))
+
+
+def add(a, b, c) -> None:
+    _ok(lib().gorch_hip_add(_stream(), _p(a), _p(b), _p(c), _n(a)))
+
+
+def bias_add(x, bias) -> None:
+    M, N = x.shape
+    _ok(lib().gorch_hip_bias_add(_stream(), _p(x), _p(bias), M, N))
+
+
+def gelu(x, y) -> None:
+    _ok(lib().gorch_hip_gelu(_stream(), _p(x), _p(y), _n(x)))
+
+
+def silu(x, y) -> None:
+    _ok(lib().gorch_hip_silu(_stream(), _p(x), _p(y), _n(x)))
+
+
+def swiglu(gate, value, y) -> None:
+    _ok(lib().gorch_hip_swiglu(_stream(), _p(gate), _p(value), _p(y), _n(gate)))
+
+
+def embedding(weight, ids, out) -> None:
+    """ids: int32 device tensor."""
+    _ok(lib().gorch_hip_embedding(_stream(), _p(weight), weight.shape[1], _p(ids), _n(ids), _p(out)))
+
+
+def attention_cached(q, k_cache, v_cache, out, batch, new_seq, pos_offset, heads, head_dim, max_seq,
+                     causal=True) -> None:
+    _ok(lib().gorch_hip_attention_cached(_stream(), _p(q), _p(k_cache), _p(v_cache), _p(out), batch, new_seq,
+                                         pos_offset, heads, head_dim, max_seq, int(causal)))
+
+
+def causal_softmax(x, y, q_seq, scale) -> None:
+    rows, cols = x.shape
+    _ok(lib().gorch_hip_causal_softmax(_stream(), _p(x), _p(y), rows, cols, q_seq, scale))
+
+
+def softmax_rows(x) -> None:
+    rows, cols = x.shape
+    _ok(lib().gorch_hip_softmax_rows(_stream(), _p(x), rows, cols))
+
+
+def argmax(logits, out) -> None:
+    """out: int32 device tensor [rows]."""
+    rows, n = logits.shape
+    _ok(lib().gorch_hip_argmax(_stream(), _p(logits), rows, n, _p(out)))
+
+
 def linear_bf16(x, W, bias, y, residual=None, epilogue=EPI_NONE) -> None:
     """y = residual + epi(x @ W^T + bias); x [M,K] f32, W [N,K] bf16 storage."""
     M, K = x.shape
     N = W.shape[0]
     _ok(lib().gorch_hip_linear_bf16(_stream(), _p(x), _p(W), _p(bias), _p(residual), _p(y), M, N, K,
                                     epilogue))
+
+
+# ------------------------------------------------------------------ GPT engine
+
+class _GPTWeights(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("vocab", "dim", "heads", "layers", "max_seq")] + [
+        ("wte", vp), ("wpe", vp),
+    ] + [(n, C.POINTER(vp)) for n in (
+        "ln1_g", "ln1_b", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo",
+        "ln2_g", "ln2_b", "w1", "b1", "w2", "b2")] + [
+        ("lnf_g", vp), ("lnf_b", vp), ("wlm", vp), ("blm", vp),
+    ]
+
+
+_LAYER_KEYS = ("ln1_g", "ln1_b", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo",
+               "ln2_g", "ln2_b", "w1", "b1", "w2", "b2")
+
+
+class GPT:
+    """gorch's nn.GPT on the GPU (nn/gpt.go:12-121). ``weights`` is a dict
+    of numpy arrays in the layout gorch_amd.synthetic produces (Linear
+    weights bf16 as uint16 [out, in])."""
+
+    def __init__(self, weights: dict):
+        import numpy as np
+
+        cfg = weights["cfg"]
+        self.cfg = dict(cfg)
+        keep = []
+        s = _GPTWeights()
+        s.vocab, s.dim, s.heads = cfg["vocab"], cfg["dim"], cfg["heads"]
+        s.layers, s.max_seq = cfg["layers"], cfg["max_seq"]
+        for key in ("wte", "wpe", "lnf_g", "lnf_b", "wlm", "blm"):
+            a = np.ascontiguousarray(weights[key])
+            keep.append(a)
+            setattr(s, key, a.ctypes.data)
+        for key in _LAYER_KEYS:
+            arrs = [np.ascontiguousarray(L[key]) for L in weights["layers"]]
+            if key.startswith("w") and any(a.dtype != np.uint16 for a in arrs):
+                raise ValueError(f"{key}: Linear weights must be bf16 (uint16 storage)")
+            keep.extend(arrs)
+            ptrs = (vp * len(arrs))(*[a.ctypes.data for a in arrs])
+            keep.append(ptrs)
+            setattr(s, key, C.cast(ptrs, C.POINTER(vp)))
+        h = lib().gorch_hip_gpt_create(C.byref(s))
+        if not h:
+            raise HipError(4, last_error())
+        self.h = h
+
+    def new_cache(self, batch: int = 1, capacity: int | None = None) -> "KVCache":
+        return KVCache(self, batch, capacity or self.cfg["max_seq"])
+
+    def forward_cached(self, ids, cache: "KVCache"):
+        """ids: [batch, n] (or [n] for batch 1) -> logits [batch*n, vocab]."""
+        import numpy as np
+
+        ids = np.ascontiguousarray(ids, np.int32)
+        n = ids.shape[-1]
+        out = np.empty((cache.batch * n, self.cfg["vocab"]), np.float32)
+        _ok(lib().gorch_hip_gpt_forward_cached(None, self.h, cache.h, ids.ctypes.data, n, out.ctypes.data))
+        return out
+
+    def generate_cached(self, prompts, max_new: int, want_logits=False, use_graph=True):
+        """Greedy generateCached for a [batch, n_prompt] array of prompts.
+        Returns (ids [batch, len], step_logits or None, timing dict)."""
+        import numpy as np
+
+        prompts = np.ascontiguousarray(np.atleast_2d(prompts), np.int32)
+        B, n = prompts.shape
+        out = np.empty((B, n + max_new), np.int32)
+        out_len = C.c_int(0)
+        V = self.cfg["vocab"]
+        logits = np.empty((max_new, B, V), np.float32) if want_logits else None
+        timing = (C.c_float * 3)()
+        _ok(lib().gorch_hip_generate_cached(None, self.h, prompts.ctypes.data, B, n, max_new, out.ctypes.data,
+                                            C.byref(out_len), None if logits is None else logits.ctypes.data,
+                                            timing, int(use_graph)))
+        L = out_len.value
+        ids = out.reshape(-1)[: B * L].reshape(B, L).copy()
+        return ids, logits, {"prefill_ms": timing[0], "decode_ms": timing[1], "decode_forwards": int(timing[2])}
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().gorch_hip_gpt_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+class KVCache:
+    """nn.KVCache (nn/kvcache.go:14-60) for ``batch`` independent sequences."""
+
+    def __init__(self, gpt: GPT, batch: int, capacity: int):
+        self.gpt = gpt
+        self.batch = batch
+        self.h = lib().gorch_hip_kvcache_create(gpt.h, batch, capacity)
+        if not self.h:
+            raise HipError(2, last_error())
+
+    def __len__(self):
+        return lib().gorch_hip_kvcache_len(self.h)
+
+    def reset(self):
+        _ok(lib().gorch_hip_kvcache_reset(self.h))
+
+    def read(self, layer: int, seq: int = 0):
+        import numpy as np
+
+        n, d = len(self), self.gpt.cfg["dim"]
+        k = np.empty((n, d), np.float32)
+        v = np.empty((n, d), np.float32)
+        _ok(lib().gorch_hip_kvcache_read(self.h, layer, seq, k.ctypes.data, v.ctypes.data))
+        return k, v
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().gorch_hip_kvcache_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()

@@ -6,8 +6,8 @@
  *   - Plain pointers and sizes only. Device pointers are HBM addresses from
  *     gorch_hip_alloc (or any allocator on the same device).
  *   - Every compute entry point takes `stream` (a hipStream_t passed as
- *     void*; NULL = the library's stream for the current device) and is
- *     asynchronous on it; gorch_hip_sync() waits for it (metal_finish /
+ *     void*; NULL = the current device's null stream) and is asynchronous
+ *     on it unless stated; gorch_hip_sync() waits for it (metal_finish /
  *     metal_sync_queue, metal/shim.m:216-242).
  *   - Return code 0 = success. Nonzero = the call did nothing useful and the
  *     caller should take its CPU path (the reference falls back to widen +
@@ -99,6 +99,103 @@ int gorch_hip_batched_matmul_dt(void* stream, const void* A, const void* B, floa
  * M <= 16 runs the HBM-streaming GEMV; larger M the MFMA GEMM. */
 int gorch_hip_linear_bf16(void* stream, const float* x, const uint16_t* W, const float* bias,
                           const float* residual, float* y, int M, int N, int K, int epilogue);
+
+/* ------------------------------------------------------------------------
+ * Decode-step ops (the forward halves of gorch's op layer on this path).
+ * ---------------------------------------------------------------------- */
+
+/* LayerNorm over the last dim of x [M,N] (nn/layernorm.go:31-91): mean and
+ * variance accumulated in f64, y = ((x - mean) * inv) * gamma + beta. */
+int gorch_hip_layernorm(void* stream, const float* x, const float* gamma, const float* beta, float* y,
+                        int M, int N, float eps);
+/* RMSNorm (nn/rmsnorm.go:39-81, RMSNormForwardMetal rmsnorm_metal.go:51):
+ * y = x * (1/sqrt(sum(x^2)/N + eps)) * gamma, sum in f64. */
+int gorch_hip_rmsnorm(void* stream, const float* x, const float* gamma, float* y, int M, int N, float eps);
+/* c = a + b (Add, ops.go:161-179; vec_add). */
+int gorch_hip_add(void* stream, const float* a, const float* b, float* c, int64_t n);
+/* x[m,n] += bias[n] in place (BiasAddInPlaceMetal, colreduce_metal.go:56-73). */
+int gorch_hip_bias_add(void* stream, float* x, const float* bias, int M, int N);
+/* tanh-form GELU (GELU, ops.go:417-443; vec_gelu). */
+int gorch_hip_gelu(void* stream, const float* x, float* y, int64_t n);
+/* SiLU and SwiGLU (silu.go:45-136; vec_silu / vec_swiglu). */
+int gorch_hip_silu(void* stream, const float* x, float* y, int64_t n);
+int gorch_hip_swiglu(void* stream, const float* gate, const float* value, float* y, int64_t n);
+/* Row gather out[i,:] = weight[ids[i],:] (EmbeddingLookup, attention_ops.go:64-77);
+ * ids is a device int32 array. */
+int gorch_hip_embedding(void* stream, const float* weight, int dim, const int* ids, int n, float* out);
+/* Attention of new query rows against a KV cache (MHA.ForwardCached's core,
+ * nn/attention.go:355-397). q/out [batch*new_seq, heads*head_dim]; caches
+ * [batch][max_seq][heads*head_dim] already holding the new rows at
+ * positions pos_offset..pos_offset+new_seq-1. causal: query i sees keys
+ * 0..pos_offset+i (else all pos_offset+new_seq keys). */
+int gorch_hip_attention_cached(void* stream, const float* q, const float* k_cache, const float* v_cache,
+                               float* out, int batch, int new_seq, int pos_offset, int heads, int head_dim,
+                               int max_seq, int causal);
+/* Staircase-causal scaled softmax (CausalSoftmax, softmax_metal.go:68-141):
+ * row r sees columns 0..(r mod q_seq)+(cols-q_seq); masked entries are 0. */
+int gorch_hip_causal_softmax(void* stream, const float* x, float* y, int rows, int cols, int q_seq, float scale);
+/* In-place row softmax (softmaxInPlace, nn/attention.go:274-296). */
+int gorch_hip_softmax_rows(void* stream, float* x, int rows, int cols);
+/* Row argmax, first maximum wins (argmax, model/generate.go:134-144);
+ * out: device int32 [rows]. */
+int gorch_hip_argmax(void* stream, const float* logits, int rows, int n, int* out);
+
+/* ------------------------------------------------------------------------
+ * GPT decode engine (nn.GPT / nn.KVCache / model.generateCached).
+ * ---------------------------------------------------------------------- */
+
+/* Host pointers to a GPT's parameters (NewGPT, nn/gpt.go:31-49): Linear
+ * weights bf16 [out, in], biases / LayerNorm / embeddings f32, per-layer
+ * arrays of `layers` pointers, an untied LM head. */
+typedef struct {
+    int vocab, dim, heads, layers, max_seq;
+    const float* wte;          /* [vocab, dim] */
+    const float* wpe;          /* [max_seq, dim] */
+    const float* const* ln1_g; const float* const* ln1_b;
+    const uint16_t* const* wq; const float* const* bq;
+    const uint16_t* const* wk; const float* const* bk;
+    const uint16_t* const* wv; const float* const* bv;
+    const uint16_t* const* wo; const float* const* bo;
+    const float* const* ln2_g; const float* const* ln2_b;
+    const uint16_t* const* w1; const float* const* b1;   /* FFN1 [4d, d] */
+    const uint16_t* const* w2; const float* const* b2;   /* FFN2 [d, 4d] */
+    const float* lnf_g; const float* lnf_b;
+    const uint16_t* wlm; const float* blm;               /* LM head [vocab, d] */
+} gorch_hip_gpt_weights;
+
+typedef struct gorch_hip_gpt gorch_hip_gpt;
+typedef struct gorch_hip_kvcache gorch_hip_kvcache;
+
+/* Uploads the weights to the current device (gpt.ToMetal, nn/gpt.go:241-257),
+ * fusing Wq/Wk/Wv into one [3d, d] weight. NULL on failure. */
+gorch_hip_gpt* gorch_hip_gpt_create(const gorch_hip_gpt_weights* w);
+void gorch_hip_gpt_free(gorch_hip_gpt* gpt);
+/* KV cache for `batch` independent sequences of up to `capacity` tokens
+ * (NewKVCache, nn/kvcache.go:23-36; one reference cache per sequence). */
+gorch_hip_kvcache* gorch_hip_kvcache_create(gorch_hip_gpt* gpt, int batch, int capacity);
+void gorch_hip_kvcache_free(gorch_hip_kvcache* cache);
+int gorch_hip_kvcache_len(const gorch_hip_kvcache* cache);   /* KVCache.Len, nn/kvcache.go:47-52 */
+int gorch_hip_kvcache_reset(gorch_hip_kvcache* cache);       /* KVCache.Reset, nn/kvcache.go:55-60 */
+/* Copies sequence `seq`'s cached keys/values of `layer` ([len, dim] each;
+ * either may be NULL) to host memory. */
+int gorch_hip_kvcache_read(const gorch_hip_kvcache* cache, int layer, int seq, float* keys, float* values);
+/* GPT.ForwardCached (nn/gpt.go:100-121) for every sequence of the cache:
+ * ids host int32 [batch, n]; logits (host, may be NULL) receives
+ * [batch*n, vocab]. Appends n tokens to the cache; rc EINVAL when the cache
+ * would exceed its capacity (the reference panics). Synchronous. */
+int gorch_hip_gpt_forward_cached(void* stream, gorch_hip_gpt* gpt, gorch_hip_kvcache* cache, const int* ids,
+                                 int n, float* logits);
+/* Greedy generateCached (model/generate.go:94-131, Temperature 0, no stop
+ * token) for `batch` prompts of n_prompt tokens (host int32 [batch, n_prompt]).
+ * out_ids (host int32, capacity batch*(n_prompt+max_new)) receives each
+ * sequence's (MaxSeq-truncated) prompt followed by its new tokens, row length
+ * *out_len. step_logits (host, may be NULL): [max_new, batch, vocab], row i
+ * = logits that chose token i (forces eager launches). timing_ms (may be
+ * NULL): {prefill ms, decode ms, decode forwards}. flags bit 0: replay the
+ * decode step from a HIP graph. Synchronous. */
+int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* gpt, const int* prompts, int batch, int n_prompt,
+                              int max_new, int* out_ids, int* out_len, float* step_logits, float* timing_ms,
+                              int flags);
 
 #ifdef __cplusplus
 }

@@ -59,6 +59,8 @@ def _load() -> C.CDLL:
                                   C.c_int, C.c_float]),
         "orc_topk": (None, [f32p, C.c_int, C.c_int, C.c_int, f32p, i32p]),
         "orc_argmax": (C.c_int, [f32p, C.c_int]),
+        "orc_attention_cached": (None, [f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                        C.c_int]),
         "orc_kvcache_new": (vp, [C.c_int, C.c_int, C.c_int]),
         "orc_kvcache_free": (None, [vp]),
         "orc_kvcache_len": (C.c_int, [vp]),
@@ -238,6 +240,17 @@ def rope_apply(x, cos_t, sin_t, start_pos=0, neox=False, sign=1.0):
                        np.ascontiguousarray(cos_t, np.float32).reshape(-1),
                        np.ascontiguousarray(sin_t, np.float32).reshape(-1), int(neox), sign)
     return y
+
+
+def attention_cached(q, K, V, pos_offset, heads, causal=True):
+    """q [new_seq, dim]; K, V [pos_offset + new_seq, dim] -> [new_seq, dim]."""
+    q = np.ascontiguousarray(q, np.float32)
+    K = np.ascontiguousarray(K, np.float32)
+    V = np.ascontiguousarray(V, np.float32)
+    new_seq, dim = q.shape
+    out = np.empty_like(q)
+    lib.orc_attention_cached(q, K, V, out, new_seq, pos_offset, heads, dim // heads, int(causal))
+    return out
 
 
 def topk(x, k):

@@ -447,15 +447,14 @@ static void kv_append(orc_kvcache* c, int layer, const float* k, const float* v,
 /* GPT                                                                 */
 /* ------------------------------------------------------------------ */
 
-/* nn/attention.go:313-400 without the final Wo projection: q/k/v are the
- * projected new rows [newSeq, dim]; writes the per-head attended sum into
- * out [newSeq, dim] (zero-initialised here as g.Zeros does). */
-static void mha_cached_core(const float* q, orc_kvcache* cache, int layer, int posOffset,
-                            int newSeq, int dim, int heads, float* out) {
-    int headDim = dim / heads;
-    int totalSeq = orc_kvcache_len(cache);
-    const float* K = cache->keys[layer];
-    const float* V = cache->values[layer];
+/* nn/attention.go:348-397 for one sequence: q [newSeq, dim] against keys /
+ * values [totalSeq, dim] (totalSeq = posOffset + newSeq); writes the
+ * per-head attended sum into out [newSeq, dim] (zero-initialised here as
+ * g.Zeros does). The causal mask uses absolute positions (:371-379). */
+void orc_attention_cached(const float* q, const float* K, const float* V, float* out, int newSeq,
+                          int posOffset, int heads, int headDim, int causal) {
+    int dim = heads * headDim;
+    int totalSeq = posOffset + newSeq;
     float invScale = (float)(1.0 / (double)(float)sqrt((double)(float)headDim));
     float* scores = (float*)malloc((size_t)newSeq * totalSeq * sizeof(float));
     memset(out, 0, (size_t)newSeq * dim * sizeof(float));
@@ -470,10 +469,11 @@ static void mha_cached_core(const float* q, orc_kvcache* cache, int layer, int p
                 scores[(int64_t)i * totalSeq + j] = sum * invScale;
             }
         }
-        /* causal mask in absolute coordinates (attention.go:371-379) */
-        for (int i = 0; i < newSeq; i++) {
-            int absPos = posOffset + i;
-            for (int j = absPos + 1; j < totalSeq; j++) scores[(int64_t)i * totalSeq + j] = -1e9f;
+        if (causal) {
+            for (int i = 0; i < newSeq; i++) {
+                int absPos = posOffset + i;
+                for (int j = absPos + 1; j < totalSeq; j++) scores[(int64_t)i * totalSeq + j] = -1e9f;
+            }
         }
         orc_softmax_inplace(scores, newSeq, totalSeq);
         for (int i = 0; i < newSeq; i++) {
@@ -488,6 +488,14 @@ static void mha_cached_core(const float* q, orc_kvcache* cache, int layer, int p
         }
     }
     free(scores);
+}
+
+/* nn/attention.go:313-400 without the Wo projection: the cache already holds
+ * the new rows (appended at :339). */
+static void mha_cached_core(const float* q, orc_kvcache* cache, int layer, int posOffset,
+                            int newSeq, int dim, int heads, float* out) {
+    orc_attention_cached(q, cache->keys[layer], cache->values[layer], out, newSeq, posOffset, heads,
+                         dim / heads, 1);
 }
 
 /* nn/attention.go:80-119 (batched path of MHA.Forward, before Wo):

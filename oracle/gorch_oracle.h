@@ -74,6 +74,11 @@ void orc_rope_apply(const float* x, float* y, int outer, int seqLen, int headDim
 void orc_topk(const float* x, int B, int V, int k, float* vals, int* idx); /* index_ops.go:153-186 */
 int orc_argmax(const float* logits, int n);                          /* model/generate.go:134-144 */
 
+/* MHA.ForwardCached's attention loops (nn/attention.go:348-397) for one
+ * sequence: q [newSeq, dim], K/V [posOffset + newSeq, dim]; out [newSeq, dim]. */
+void orc_attention_cached(const float* q, const float* K, const float* V, float* out, int newSeq,
+                          int posOffset, int heads, int headDim, int causal);
+
 /* ---- GPT with KV cache (nn/gpt.go, nn/transformer.go, nn/attention.go, nn/kvcache.go) ----
  * Weights: Linear weights are bf16 [out,in] (or f32 when the model is built
  * with linear_bf16 = 0), biases f32, LayerNorm gamma/beta f32, embeddings f32.

@@ -1,0 +1,139 @@
+"""GPU parity of the GPT decode engine (fused QKV GEMV -> KV cache ->
+attention -> fused residual GEMVs -> LM head -> argmax) against the CPU
+oracle's GPT.ForwardCached / generateCached, through the C-ABI.
+
+Bars: logits within 1e-3 of RMS for a forward;
+greedy tokens identical; full-run logits within 2e-2 of RMS. The reference
+invariants are re-checked on the GPU path: cached prefill + steps equals a
+one-shot forward over the whole sequence (nn/kvcache_test.go:53-114), the
+cache length advances (:116-141), and generation stops at MaxSeq
+(model/generate.go:119-124).
+"""
+import numpy as np
+import pytest
+
+import oracle as orc
+from gorch_amd import synthetic as syn
+from tests.conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(vocab=64, dim=32, heads=4, layers=2, max_seq=40)
+
+
+def tiny_weights(seed=31):
+    w = syn.gpt2_weights(TINY, seed=seed, random_affine=True)
+    from gorch_amd import bf16 as hb
+    for L in w["layers"]:   # sharper attention so mistakes in it show
+        for key in ("wq", "wk"):
+            L[key] = hb.f32_to_bf16(hb.bf16_to_f32(L[key]) * 20)
+    return w
+
+
+@pytest.fixture(scope="module")
+def tiny(gpu):
+    w = tiny_weights()
+    return w, gpu.GPT(w), orc.GPT(w)
+
+
+def test_forward_cached_prefill_and_steps(tiny):
+    w, g, o = tiny
+    ids = syn.prompt_ids(11, TINY["vocab"], seed=1)
+    gc, oc = g.new_cache(1, TINY["max_seq"]), o.new_cache()
+    for chunk in (ids[:8], ids[8:9], ids[9:11]):
+        got = g.forward_cached(chunk[None, :], gc)
+        ref = o.forward_cached(chunk, oc)
+        assert rel_err(got, ref) <= 1e-3
+        assert len(gc) == len(oc)
+    for layer in range(TINY["layers"]):
+        k, v = gc.read(layer)
+        assert rel_err(k, oc.keys(layer).reshape(k.shape)) <= 1e-4
+        assert rel_err(v, oc.values(layer).reshape(v.shape)) <= 1e-4
+
+
+def test_cached_steps_equal_one_shot(tiny):
+    w, g, o = tiny
+    ids = syn.prompt_ids(12, TINY["vocab"], seed=2)
+    c1 = g.new_cache(1, 20)
+    full = g.forward_cached(ids[None, :], c1)
+    c2 = g.new_cache(1, 20)
+    rows = [g.forward_cached(ids[None, :5], c2)]
+    for t in range(5, 12):
+        rows.append(g.forward_cached(ids[None, t:t + 1], c2))
+    assert np.max(np.abs(np.concatenate(rows) - full)) < 1e-3
+
+
+def test_forward_cached_capacity_error(tiny, gpu):
+    w, g, o = tiny
+    c = g.new_cache(1, 4)
+    g.forward_cached(np.zeros((1, 3), np.int32), c)
+    with pytest.raises(gpu.HipError):
+        g.forward_cached(np.zeros((1, 2), np.int32), c)
+    c.reset()
+    assert len(c) == 0
+    g.forward_cached(np.zeros((1, 4), np.int32), c)
+
+
+def test_generate_tokens_identical(tiny):
+    w, g, o = tiny
+    prompt = syn.prompt_ids(6, TINY["vocab"], seed=3)
+    ref_ids, ref_logits, gaps = o.generate_cached(prompt, 30, want_logits=True)
+    ids, logits, _ = g.generate_cached(prompt[None, :], 30, want_logits=True)
+    assert list(ids[0]) == list(ref_ids)
+    for i in range(30):
+        assert rel_err(logits[i, 0], ref_logits[i]) <= 1e-3
+    ids_graph, _, t = g.generate_cached(prompt[None, :], 30, use_graph=True)
+    assert np.array_equal(ids_graph, ids)
+    assert t["decode_forwards"] == 30
+
+
+def test_generate_batch_matches_per_sequence(tiny):
+    w, g, o = tiny
+    prompts = np.stack([syn.prompt_ids(7, TINY["vocab"], seed=10 + b) for b in range(3)])
+    ids, _, _ = g.generate_cached(prompts, 12)
+    for b in range(3):
+        ref, _, _ = o.generate_cached(prompts[b], 12)
+        assert list(ids[b]) == list(ref)
+
+
+def test_generate_stops_at_max_seq(tiny):
+    w, g, o = tiny
+    prompt = syn.prompt_ids(TINY["max_seq"] - 2, TINY["vocab"], seed=4)
+    ids, _, t = g.generate_cached(prompt[None, :], 10)
+    ref, _, _ = o.generate_cached(prompt, 10)
+    assert ids.shape[1] == TINY["max_seq"] + 1 == len(ref)
+    assert list(ids[0]) == list(ref)
+    assert t["decode_forwards"] == 2
+
+
+def test_generate_truncates_long_prompt(tiny):
+    w, g, o = tiny
+    prompt = syn.prompt_ids(TINY["max_seq"] + 5, TINY["vocab"], seed=5)
+    ids, _, _ = g.generate_cached(prompt[None, :], 3)
+    ref, _, _ = o.generate_cached(prompt, 3)
+    assert list(ids[0]) == list(ref)
+
+
+@pytest.fixture(scope="module")
+def gpt2_small(gpu):
+    w = syn.gpt2_weights(syn.GPT2_SMALL, seed=0)
+    return w, gpu.GPT(w), orc.GPT(w)
+
+
+def test_gpt2_small_greedy_decode(gpt2_small):
+    """GPT-2 small, bf16 weights N(0,0.02), 32-token
+    seeded prompt, 64 greedy tokens with the KV cache, batch 1."""
+    w, g, o = gpt2_small
+    prompt = syn.prompt_ids(32, syn.GPT2_SMALL["vocab"], seed=0)
+    orc.set_widen_per_call(False)     # same numerics, widened once
+    try:
+        ref_ids, ref_logits, gaps = o.generate_cached(prompt, 64, want_logits=True)
+    finally:
+        orc.set_widen_per_call(True)
+    ids, logits, _ = g.generate_cached(prompt[None, :], 64, want_logits=True)
+    print(f"min top-1/top-2 logit gap over 64 steps: {float(np.min(gaps)):.3e}")
+    assert list(ids[0]) == list(ref_ids)
+    assert rel_err(logits[0, 0], ref_logits[0]) <= 1e-3          # prefill logits
+    assert rel_err(logits[:, 0], ref_logits) <= 2e-2             # full run
+    ids_graph, _, _ = g.generate_cached(prompt[None, :], 64, use_graph=True)
+    assert np.array_equal(ids_graph, ids)

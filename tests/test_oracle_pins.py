@@ -381,3 +381,26 @@ def test_moe_rejects_bad_top_k():
     x, logits, w = syn.moe_inputs(M=4, dim=16, ffn=32, experts=2, top_k=3, seed=20)
     with pytest.raises(ValueError):
         orc.moe_forward(w, x, logits)
+
+
+def test_attention_cached_vs_f64():
+    rng = np.random.default_rng(25)
+    heads, hd, pos, n = 3, 16, 7, 4
+    d = heads * hd
+    q = rng.standard_normal((n, d)).astype(np.float32)
+    K = rng.standard_normal((pos + n, d)).astype(np.float32)
+    V = rng.standard_normal((pos + n, d)).astype(np.float32)
+    for causal in (True, False):
+        got = orc.attention_cached(q, K, V, pos, heads, causal)
+        ref = np.zeros((n, d))
+        for h in range(heads):
+            sl = slice(h * hd, (h + 1) * hd)
+            s = q[:, sl].astype(np.float64) @ K[:, sl].T.astype(np.float64) / math.sqrt(hd)
+            if causal:
+                for i in range(n):
+                    s[i, pos + i + 1:] = -np.inf
+            ref[:, sl] = scipy.special.softmax(s, axis=1) @ V[:, sl]
+        assert np.max(np.abs(got - ref)) < 1e-5
+    # one visible key: the output is that key's value row (closed form)
+    one = orc.attention_cached(q[:1], K[:1], V[:1], 0, heads, True)
+    assert np.allclose(one, V[:1], atol=1e-7)
