@@ -48,6 +48,7 @@ def parse():
     ap.add_argument("--shape", default=None,
                     help="restrict to one shape 'M,K,N' (for profiling one kernel)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-decode", action="store_true", help="skip the GPT decode legs")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (PMC byte-counter calibration)")
@@ -148,6 +149,77 @@ def gpu_leg(args, shapes):
     return value, wall, per_shape, dom
 
 
+MFMA_PEAK_TFLOPS = 2516.6  # dense bf16: 256 CU x 2.4 GHz x 4096 FLOP/clk
+
+
+def gemm_leg(M=512, K=768, Ns=(2304, 3072)):
+    """Prefill GEMM: operands resident (re-used across
+    launches), timed over a graph of back-to-back launches."""
+    import torch
+
+    from gorch_amd import hip
+    from gorch_amd import synthetic as syn
+
+    out = []
+    stream = torch.cuda.current_stream()
+    for N in Ns:
+        x, W, b = syn.gemv_inputs(M, K, N, seed=N)
+        xd, Wd = torch.from_numpy(x).cuda(), torch.from_numpy(W.view(np.int16)).cuda()
+        bd = torch.from_numpy(b).cuda()
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        for act_bf16 in (True, False):
+            hip.linear_bf16(xd, Wd, bd, y, act_bf16=act_bf16)
+            torch.cuda.synchronize()
+            L = 200
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for _ in range(L):
+                    hip.linear_bf16(xd, Wd, bd, y, act_bf16=act_bf16)
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(3):
+                g.replay()
+            e1.record(stream)
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (3 * L)
+            flops = 2.0 * M * K * N
+            # the f32-accurate mode issues two MFMAs per fragment: report the
+            # algorithmic rate (2MKN / time) for both
+            out.append({"M": M, "K": K, "N": N, "activations": "bf16" if act_bf16 else "f32 (hi+lo split)",
+                        "us": round(us, 3), "TFLOPs": round(flops / us / 1e6, 1),
+                        "frac_mfma_peak": round(flops / us / 1e6 / MFMA_PEAK_TFLOPS, 4)})
+            del g
+    return out
+
+
+def decode_leg(cfg_name, batch, n_prompt, max_new, reps=3):
+    """Greedy KV-cache decode through the engine (graph-replayed step).
+    tok/s = batch * decode forwards / decode wall time (prefill timed apart)."""
+    from gorch_amd import hip
+    from gorch_amd import synthetic as syn
+
+    cfg = dict(syn.GPT2_SMALL if cfg_name == "gpt2-small" else syn.GPT2_XL)
+    w = syn.gpt2_weights(cfg, seed=0)
+    g = hip.GPT(w)
+    del w
+    prompts = np.stack([syn.prompt_ids(n_prompt, cfg["vocab"], seed=b) for b in range(batch)])
+    g.generate_cached(prompts, max_new, use_graph=True)   # warm-up (graph build, caches)
+    runs = []
+    for _ in range(reps):
+        _, _, t = g.generate_cached(prompts, max_new, use_graph=True)
+        runs.append(t)
+    g.close()
+    runs.sort(key=lambda t: t["decode_ms"])
+    t = runs[len(runs) // 2]
+    fwd = t["decode_forwards"]
+    return {"model": cfg_name, "batch": batch, "prompt": n_prompt, "new_tokens": max_new,
+            "tok_s": round(batch * fwd / (t["decode_ms"] / 1e3), 1),
+            "ms_per_step": round(t["decode_ms"] / fwd, 4), "prefill_ms": round(t["prefill_ms"], 3),
+            "weights": "bf16 N(0,0.02) random init, synthetic prompts"}
+
+
 def cpu_leg(shapes, seconds):
     """The oracle (gorch CPU semantics: widen the bf16 weight per call, f32
     sgemm, bias add) over the same 9 shapes, repeated for ~`seconds`."""
@@ -190,6 +262,8 @@ def main():
         shapes = [(M, K, N) for (K, N) in KN for M in MS]
 
     value, wall, per_shape, dom = gpu_leg(args, shapes)
+    decode = [] if (args.shape or args.no_decode) else [decode_leg("gpt2-small", 1, 32, 64)]
+    gemm = [] if args.shape else gemm_leg()
     cpu = None if args.no_cpu else cpu_leg(shapes, args.cpu_seconds)
     dom_bytes = algo_bytes(dom["M"], dom["K"], dom["N"])
     out = {
@@ -224,6 +298,8 @@ def main():
         },
         "cpu_baseline": cpu,
         "per_shape": per_shape,
+        "decode": decode,
+        "prefill_gemm": gemm,
     }
     print(json.dumps(out))
 

@@ -1,0 +1,176 @@
+// gemm.hip — BF16-weight Linear for prefill- and MoE-sized M (M > 16):
+//   C[m,n] = residual[m,n] + epi( sum_k A[m,k] * W[n,k] + bias[n] )
+// with A f32 [M,K], W bf16 [N,K] (the nn.Linear layout, nn/module.go:61-88).
+//
+// Block tile BM x BN, K stepped by 64. 256 threads = 4 waves in a 2x2 grid,
+// each wave owning a (BM/2) x (BN/2) sub-tile of 16x16 MFMA accumulators
+// (v_mfma_f32_16x16x32_bf16). Each K step stages the A tile (converted from
+// f32 as it is written to LDS) and the W tile in LDS; the next step's global
+// loads are issued into registers before the current step's MFMAs so HBM
+// latency overlaps the math. LDS rows are padded by 16 bytes to spread the
+// 16-byte fragment reads across banks.
+//
+// Activation modes:
+//   split (default): A = hi + lo in bf16 (two MFMAs per fragment pair),
+//     ~2^-16 relative, i.e. f32-activation accuracy like the reference's
+//     widen + f32 sgemm (bf16_matmul.go:166-173);
+//   bf16 (GORCH_HIP_LINEAR_ACT_BF16): A rounded to bf16 (RNE), one MFMA —
+//     the bf16 x bf16 -> f32 MPSGraph path (metal/shim.m:808-857).
+#include "common.h"
+
+namespace gh {
+
+constexpr int kBK = 64;
+constexpr int kLDA = kBK + 8;  // bf16 elements per LDS row (16-byte pad)
+
+template <int BM, int BN, bool SPLIT>
+__global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A, const uint16_t* __restrict__ W,
+                                                    const float* __restrict__ bias, const float* residual,
+                                                    OutDesc od, int M, int N, int K, int epilogue) {
+    constexpr int NA = SPLIT ? 2 : 1;
+    constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
+    constexpr int A_F4 = BM * kBK / 4 / 256;  // float4 loads of A per thread
+    constexpr int W_U4 = BN * kBK / 8 / 256;  // uint4 loads of W per thread
+    __shared__ __align__(16) uint16_t As[NA][BM][kLDA];
+    __shared__ __align__(16) uint16_t Ws[BN][kLDA];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    float4 ra[A_F4];
+    uint4 rw[W_U4];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < A_F4; i++) {
+            const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
+            const int m = m0 + row, k = k0 + 4 * c4;
+            if (m < M && k < K)
+                ra[i] = *reinterpret_cast<const float4*>(A + (size_t)m * K + k);
+            else
+                ra[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < W_U4; i++) {
+            const int idx = tid + 256 * i, row = idx >> 3, c8 = idx & 7;
+            const int n = n0 + row, k = k0 + 8 * c8;
+            if (n < N && k < K)
+                rw[i] = *reinterpret_cast<const uint4*>(W + (size_t)n * K + k);
+            else
+                rw[i] = make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto sstore = [&]() {
+#pragma unroll
+        for (int i = 0; i < A_F4; i++) {
+            const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
+            const float f[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
+            uint16_t hi[4], lo[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (SPLIT) {
+                    uint32_t u = __float_as_uint(f[e]) & 0xffff0000u;
+                    hi[e] = (uint16_t)(u >> 16);
+                    lo[e] = __builtin_bit_cast(uint16_t, (__bf16)(f[e] - __uint_as_float(u)));
+                } else {
+                    hi[e] = __builtin_bit_cast(uint16_t, (__bf16)f[e]);
+                }
+            }
+            uint2 h2 = make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+            *reinterpret_cast<uint2*>(&As[0][row][4 * c4]) = h2;
+            if (SPLIT) {
+                uint2 l2 = make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
+                *reinterpret_cast<uint2*>(&As[NA - 1][row][4 * c4]) = l2;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < W_U4; i++) {
+            const int idx = tid + 256 * i, row = idx >> 3, c8 = idx & 7;
+            *reinterpret_cast<uint4*>(&Ws[row][8 * c8]) = rw[i];
+        }
+    };
+
+    floatx4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int r = lane & 15, g = lane >> 4;
+    gload(0);
+    for (int k0 = 0; k0 < K; k0 += kBK) {
+        __syncthreads();  // previous step's fragment reads are done
+        sstore();
+        __syncthreads();
+        if (k0 + kBK < K) gload(k0 + kBK);
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 32) {
+            bf16x8 bfr[TN];
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                bfr[j] = *reinterpret_cast<const bf16x8*>(&Ws[wn * WN + j * 16 + r][kk + 8 * g]);
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const bf16x8 ahi = *reinterpret_cast<const bf16x8*>(&As[0][wm * WM + i * 16 + r][kk + 8 * g]);
+#pragma unroll
+                for (int j = 0; j < TN; j++) acc[i][j] = mfma16x16x32(ahi, bfr[j], acc[i][j]);
+                if (SPLIT) {
+                    const bf16x8 alo =
+                        *reinterpret_cast<const bf16x8*>(&As[NA - 1][wm * WM + i * 16 + r][kk + 8 * g]);
+#pragma unroll
+                    for (int j = 0; j < TN; j++) acc[i][j] = mfma16x16x32(alo, bfr[j], acc[i][j]);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn * WN + j * 16 + r;
+            if (n >= N) continue;
+            const float bn = bias ? bias[n] : 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int m = m0 + wm * WM + i * 16 + 4 * g + v;
+                if (m < M) {
+                    float s = acc[i][j][v];
+                    if (bias) s = s + bn;
+                    if (epilogue == GORCH_HIP_EPI_GELU) s = gelu_tanh(s);
+                    if (residual) s = residual[(size_t)m * N + n] + s;
+                    *od.at(m, n) = s;
+                }
+            }
+        }
+}
+
+template <int BM, int BN, bool SPLIT>
+static void launch_gemm_t(hipStream_t s, const float* A, const uint16_t* W, const float* bias,
+                          const float* residual, const OutDesc& od, int M, int N, int K, int epilogue) {
+    dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+    hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT>), grid, dim3(256), 0, s, A, W, bias, residual, od, M, N, K,
+                       epilogue);
+}
+
+// Tile choice: the largest tile that still gives every CU a block.
+int launch_gemm_bf16w(hipStream_t s, const float* A, const uint16_t* W, const float* bias,
+                      const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
+                      bool act_bf16) {
+    const long long big = (long long)((M + 127) / 128) * ((N + 127) / 128);
+    const long long mid = (long long)((M + 63) / 64) * ((N + 127) / 128);
+    int tile = big >= 256 ? 2 : (mid >= 256 ? 1 : 0);
+    if (act_bf16) {
+        if (tile == 2) launch_gemm_t<128, 128, false>(s, A, W, bias, residual, od, M, N, K, epilogue);
+        else if (tile == 1) launch_gemm_t<64, 128, false>(s, A, W, bias, residual, od, M, N, K, epilogue);
+        else launch_gemm_t<64, 64, false>(s, A, W, bias, residual, od, M, N, K, epilogue);
+    } else {
+        if (tile == 2) launch_gemm_t<128, 128, true>(s, A, W, bias, residual, od, M, N, K, epilogue);
+        else if (tile == 1) launch_gemm_t<64, 128, true>(s, A, W, bias, residual, od, M, N, K, epilogue);
+        else launch_gemm_t<64, 64, true>(s, A, W, bias, residual, od, M, N, K, epilogue);
+    }
+    count(CNT_GEMM);
+    return check_launch("gemm_bf16w");
+}
+
+}  // namespace gh

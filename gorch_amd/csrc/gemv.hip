@@ -175,8 +175,15 @@ int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const f
     return launch_linear_bf16_od(s, x, W, bias, residual, OutDesc::plain(y, N), M, N, K, epilogue);
 }
 
+int launch_gemm_bf16w(hipStream_t s, const float* A, const uint16_t* W, const float* bias,
+                      const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
+                      bool act_bf16);
+
+// M <= 16: the weight-streaming GEMV below; larger M: the tiled MFMA GEMM
+// (gemm.hip), which re-reads each weight tile only once per BM rows.
 int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                           const float* residual, const OutDesc& od, int M, int N, int K, int epilogue) {
+    if (M > 16) return launch_gemm_bf16w(s, x, W, bias, residual, od, M, N, K, epilogue, false);
     GemvPlan p = plan_gemv(M, N, K);
     int per = (K + p.nw - 1) / p.nw;
     int kw = (per + 31) / 32 * 32;

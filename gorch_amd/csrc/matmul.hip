@@ -12,8 +12,9 @@
 
 namespace gh {
 
-int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
-                       const float* residual, float* y, int M, int N, int K, int epilogue);
+int launch_gemm_bf16w(hipStream_t s, const float* A, const uint16_t* W, const float* bias,
+                      const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
+                      bool act_bf16);
 
 __device__ __forceinline__ float load_op(const void* p, size_t i, int bf16) {
     return bf16 ? __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16)
@@ -63,8 +64,9 @@ static bool linear_fast_ok(const void* x, const void* W, int K) {
 
 using namespace gh;
 
-extern "C" int gorch_hip_linear_bf16(void* stream, const float* x, const uint16_t* W, const float* bias,
-                                     const float* residual, float* y, int M, int N, int K, int epilogue) {
+extern "C" int gorch_hip_linear_bf16_ex(void* stream, const float* x, const uint16_t* W, const float* bias,
+                                        const float* residual, float* y, int M, int N, int K, int epilogue,
+                                        int flags) {
     GH_REQUIRE(M >= 0 && N >= 0 && K >= 0, "gorch_hip_linear_bf16: negative dimension");
     GH_REQUIRE(epilogue == GORCH_HIP_EPI_NONE || epilogue == GORCH_HIP_EPI_GELU,
                "gorch_hip_linear_bf16: unknown epilogue");
@@ -75,7 +77,16 @@ extern "C" int gorch_hip_linear_bf16(void* stream, const float* x, const uint16_
         set_error("gorch_hip_linear_bf16: needs K % 8 == 0 and 16-byte aligned x and W");
         return GORCH_HIP_EUNSUPPORTED;
     }
+    GH_REQUIRE((flags & ~GORCH_HIP_LINEAR_ACT_BF16) == 0, "gorch_hip_linear_bf16_ex: unknown flag");
+    if (flags & GORCH_HIP_LINEAR_ACT_BF16)
+        return launch_gemm_bf16w(stream_of(stream), x, W, bias, residual, OutDesc::plain(y, N), M, N, K, epilogue,
+                                 true);
     return launch_linear_bf16(stream_of(stream), x, W, bias, residual, y, M, N, K, epilogue);
+}
+
+extern "C" int gorch_hip_linear_bf16(void* stream, const float* x, const uint16_t* W, const float* bias,
+                                     const float* residual, float* y, int M, int N, int K, int epilogue) {
+    return gorch_hip_linear_bf16_ex(stream, x, W, bias, residual, y, M, N, K, epilogue, 0);
 }
 
 static int matmul_dt_impl(void* stream, const void* A, const void* B, float* C, uint32_t M, uint32_t N,

@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(HERE, "libgorch_hip.so")
 
 EPI_NONE = 0
 EPI_GELU = 1
+LINEAR_ACT_BF16 = 1
 
 COUNTER_NAMES = ("gemv", "gemm", "generic_matmul", "attention", "norm", "elementwise", "moe",
                  "argmax", "codec")
@@ -51,6 +52,7 @@ SIGNATURES = {
     "gorch_hip_matmul_dt": (i32, [vp, vp, vp, vp, u32, u32, u32, i32, i32, i32, i32]),
     "gorch_hip_batched_matmul_dt": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, i32, i32, i32, i32]),
     "gorch_hip_linear_bf16": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "gorch_hip_linear_bf16_ex": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]),
     "gorch_hip_layernorm": (i32, [vp, vp, vp, vp, vp, i32, i32, f32]),
     "gorch_hip_rmsnorm": (i32, [vp, vp, vp, vp, i32, i32, f32]),
     "gorch_hip_add": (i32, [vp, vp, vp, vp, i64]),
@@ -221,12 +223,13 @@ def argmax(logits, out) -> None:
     _ok(lib().gorch_hip_argmax(_stream(), _p(logits), rows, n, _p(out)))
 
 
-def linear_bf16(x, W, bias, y, residual=None, epilogue=EPI_NONE) -> None:
-    """y = residual + epi(x @ W^T + bias); x [M,K] f32, W [N,K] bf16 storage."""
+def linear_bf16(x, W, bias, y, residual=None, epilogue=EPI_NONE, act_bf16=False) -> None:
+    """y = residual + epi(x @ W^T + bias); x [M,K] f32, W [N,K] bf16 storage.
+    act_bf16: round activations to bf16 on the MFMA GEMM (one MFMA per step)."""
     M, K = x.shape
     N = W.shape[0]
-    _ok(lib().gorch_hip_linear_bf16(_stream(), _p(x), _p(W), _p(bias), _p(residual), _p(y), M, N, K,
-                                    epilogue))
+    _ok(lib().gorch_hip_linear_bf16_ex(_stream(), _p(x), _p(W), _p(bias), _p(residual), _p(y), M, N, K,
+                                       epilogue, LINEAR_ACT_BF16 if act_bf16 else 0))
 
 
 # ------------------------------------------------------------------ GPT engine

@@ -95,10 +95,20 @@ int gorch_hip_batched_matmul_dt(void* stream, const void* A, const void* B, floa
 /* Fused bf16-weight Linear (nn/module.go:61-88 with the op that follows it):
  *   y[m,n] = residual[m,n] + epi( sum_k x[m,k] * W[n,k] + bias[n] )
  * x f32 [M,K]; W bf16 [N,K]; bias f32 [N] or NULL; residual f32 [M,N] or
- * NULL (it may alias y; x must not); epilogue GORCH_HIP_EPI_*.
- * M <= 16 runs the HBM-streaming GEMV; larger M the MFMA GEMM. */
+ * NULL (it may alias y; x must not); epilogue GORCH_HIP_EPI_*. Needs
+ * K % 8 == 0 and 16-byte aligned x and W (else GORCH_HIP_EUNSUPPORTED).
+ * M <= 16 runs the HBM-streaming GEMV; larger M the tiled MFMA GEMM. Both
+ * keep f32-activation accuracy (activations split into two bf16 terms). */
 int gorch_hip_linear_bf16(void* stream, const float* x, const uint16_t* W, const float* bias,
                           const float* residual, float* y, int M, int N, int K, int epilogue);
+
+/* Activations rounded to bf16 (RNE) before the matrix cores: the bf16 x bf16
+ * -> f32 product of the MPSGraph dtyped path (metal/shim.m:808-857). */
+#define GORCH_HIP_LINEAR_ACT_BF16 1
+/* gorch_hip_linear_bf16 with flags (GORCH_HIP_LINEAR_ACT_BF16: always the
+ * MFMA GEMM, one bf16 MFMA per fragment). */
+int gorch_hip_linear_bf16_ex(void* stream, const float* x, const uint16_t* W, const float* bias,
+                             const float* residual, float* y, int M, int N, int K, int epilogue, int flags);
 
 /* ------------------------------------------------------------------------
  * Decode-step ops (the forward halves of gorch's op layer on this path).

@@ -100,7 +100,7 @@ def test_linear_fused_epilogues(gpu):
 
 
 def test_linear_deterministic(gpu):
-    # split-K partials are summed in a fixed order: repeated calls agree bitwise
+    # the cross-wave reduction runs in a fixed order: repeated calls agree bitwise
     x, W, b = syn.gemv_inputs(16, 3072, 768, seed=22)
     a = run_linear(gpu, x, W, b)
     for _ in range(3):
@@ -164,3 +164,37 @@ def test_matmul_probe(gpu, known_answers):
         C = torch.empty((n, n), dtype=torch.float32, device="cuda")
         gpu.matmul_dt(dev(orc.f32_to_bf16(af)), dev(B), C, n, n, n, False, False, True, bb)
         assert np.max(np.abs(host(C) - ref)) <= known_answers["bf16_matmul_probe"]["tol_abs"]
+
+
+@pytest.mark.parametrize("N", [2304, 3072])
+def test_prefill_gemm_config(gpu, N):
+    """M=512 x K=768 x N (fused QKV 2304 / MLP-up 3072),
+    f32 N(0,1) activations, bf16 N(0,0.02) weights, f32 out."""
+    M, K = 512, 768
+    x, W, b = syn.gemv_inputs(M, K, N, seed=N)
+    gpu.reset_dispatch_counts()
+    got = run_linear(gpu, x, W, b)                         # f32-accurate activations
+    assert gpu.dispatch_counts()["gemm"] == 1
+    ref = orc.linear(x, W, b)
+    assert rel_err(got, ref) <= 1e-3
+    # bf16-rounded activations on the matrix cores (the dtyped MPSGraph path):
+    # 1e-3 against the oracle on bf16-rounded A, 5e-2 against f32 A
+    # (bf16_ops_test.go:22-26).
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    gpu.linear_bf16(dev(x), dev(W), dev(b), y, act_bf16=True)
+    got16 = host(y)
+    xr = orc.bf16_to_f32(orc.f32_to_bf16(x))
+    assert rel_err(got16, orc.linear(xr, W, b)) <= 1e-3
+    assert rel_err(got16, ref) <= 5e-2
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 50257, 768), (100, 1600, 6400), (256, 4800, 1600), (8192, 64, 64),
+                                   (33, 8, 8)])
+def test_gemm_shapes(gpu, M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    W = syn.bf16_normal(rng, (N, K))
+    b = rng.standard_normal(N).astype(np.float32) * 0.1
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    got = run_linear(gpu, x, W, b, residual=res, epilogue=gpu.EPI_GELU)
+    assert rel_err(got, orc.add(res, orc.gelu(orc.linear(x, W, b)))) <= 1e-3
