@@ -49,6 +49,8 @@ def parse():
                     help="restrict to one shape 'M,K,N' (for profiling one kernel)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the GPT decode legs")
+    ap.add_argument("--only", choices=("decode", "gemm", "decode-xl"), default=None,
+                    help="run only one secondary leg and print its JSON (for profiling)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (PMC byte-counter calibration)")
@@ -250,6 +252,19 @@ def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.only:
+        import torch
+
+        from gorch_amd import hip
+        hip.init(0)
+        torch.cuda.set_device(0)
+        if args.only == "decode":
+            print(json.dumps(decode_leg("gpt2-small", 1, 32, 64)))
+        elif args.only == "decode-xl":
+            print(json.dumps(decode_leg("gpt2-xl", 16, 512, 256, reps=1)))
+        else:
+            print(json.dumps(gemm_leg()))
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "

@@ -10,10 +10,10 @@
 // slice is a 256-byte segment.
 //
 // k_attn_cached: one 256-thread block per (head, query row). Scores for all
-// visible keys are staged in LDS: 16 lanes per key each take float4 slices
-// of the head (4 keys per wavefront instruction, 16-lane shuffle reduce);
-// block max / sum by LDS reduction; then P.V with lanes across the head's
-// dims (coalesced 256-byte rows) and waves across keys, summed in wave order.
+// visible keys are staged in LDS (4 lanes per key, 64 keys per block
+// iteration, 2-step shuffle reduce); block max / sum by LDS reduction; then
+// P.V with lanes across the head's dims (coalesced 256-byte rows) and waves
+// across keys, the 4 wave partials summed in wave order.
 #include "common.h"
 
 namespace gh {
@@ -63,24 +63,26 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_cached(AttnArgs a) {
     for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = a.q[(size_t)row * a.q_stride + h * hd + d];
     __syncthreads();
 
-    // scores: 16 lanes per key, float4 slices of the head dimension
+    // scores: 4 lanes per key, each taking every 4th float4 of the head (so
+    // the 4 lanes read 64 contiguous bytes per load); 16 keys per wavefront
+    // and 64 per block per iteration, all loads of a lane issued together.
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane & 15, kslot = lane >> 4;
+    const int sub = lane & 3, kslot = lane >> 2;
     const int hd4 = hd >> 2;
+    const float4* q4 = reinterpret_cast<const float4*>(qs);
     float lmax = -INFINITY;
-    for (int j0 = wave * 4; j0 < T; j0 += 16) {
+    for (int j0 = wave * 16; j0 < T; j0 += 64) {
         const int j = j0 + kslot;
         float acc = 0.f;
         if (j < T) {
             const float4* kr = reinterpret_cast<const float4*>(K + (size_t)j * a.dim);
-            for (int d4 = sub; d4 < hd4; d4 += 16) {
+#pragma unroll 4
+            for (int d4 = sub; d4 < hd4; d4 += 4) {
                 float4 kv = kr[d4];
-                float4 qv = reinterpret_cast<const float4*>(qs)[d4];
+                float4 qv = q4[d4];
                 acc += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
             }
         }
-        acc += __shfl_xor(acc, 8, 64);
-        acc += __shfl_xor(acc, 4, 64);
         acc += __shfl_xor(acc, 2, 64);
         acc += __shfl_xor(acc, 1, 64);
         if (j < T && sub == 0) {
@@ -101,13 +103,23 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_cached(AttnArgs a) {
     for (int j = threadIdx.x; j < T; j += blockDim.x) sc[j] = sc[j] / sum;
     __syncthreads();
 
-    // P.V: waves take keys j = wave, wave+4, ...; lanes take dims
+    // P.V: waves take keys j = wave, wave+4, ...; lanes take dims (one
+    // coalesced 256-byte row per key); four independent accumulators keep
+    // four rows in flight per lane.
     for (int d0 = 0; d0 < hd; d0 += 64) {
         const int d = d0 + lane;
-        float acc = 0.f;
         if (d < hd) {
-            for (int j = wave; j < T; j += 4) acc += sc[j] * V[(size_t)j * a.dim + d];
-            pv[wave][d] = acc;
+            const float* Vd = V + d;
+            float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+            int j = wave;
+            for (; j + 12 < T; j += 16) {
+                a0 += sc[j] * Vd[(size_t)j * a.dim];
+                a1 += sc[j + 4] * Vd[(size_t)(j + 4) * a.dim];
+                a2 += sc[j + 8] * Vd[(size_t)(j + 8) * a.dim];
+                a3 += sc[j + 12] * Vd[(size_t)(j + 12) * a.dim];
+            }
+            for (; j < T; j += 4) a0 += sc[j] * Vd[(size_t)j * a.dim];
+            pv[wave][d] = (a0 + a1) + (a2 + a3);
         }
     }
     __syncthreads();

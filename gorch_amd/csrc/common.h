@@ -23,10 +23,22 @@ void clear_error();
 hipStream_t stream_of(void* s);
 
 struct OutDesc;
+// Optional fusions of the weight-streaming GEMV (M <= 16):
+//   ln_g/ln_b: LayerNorm of each activation row applied as it is loaded;
+//   argmax_key: per-row packed (value, index) maximum of the outputs,
+//     combined with 64-bit atomicMax into argmax_key[m] (must start at 0).
+struct LinearExtras {
+    const float* ln_g = nullptr;
+    const float* ln_b = nullptr;
+    float ln_eps = 1e-5f;
+    unsigned long long* argmax_key = nullptr;
+    long long x_stride = 0;  // activation row stride in elements (0 = K)
+};
 int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                        const float* residual, float* y, int M, int N, int K, int epilogue);
 int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
-                          const float* residual, const OutDesc& od, int M, int N, int K, int epilogue);
+                          const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
+                          const LinearExtras& ex);
 
 // Dispatch counters (the gorch ReadMetalDispatchCounts analogue).
 enum Counter {
@@ -156,6 +168,21 @@ __device__ __forceinline__ void split_hi_lo(const float (&f)[8], bf16x8& hi, bf1
 
 __device__ __forceinline__ floatx4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const floatx4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Greedy-argmax key (model/generate.go:134-144 semantics under atomicMax):
+// the high word orders floats, the low word is ~index so ties keep the
+// first index. A NaN never wins, except at index 0, where it always wins
+// (the reference's loop keeps a leading NaN since no comparison beats it).
+__device__ __forceinline__ unsigned long long argmax_pack(float v, int idx) {
+    uint32_t b = __float_as_uint(v);
+    uint32_t ord;
+    if (v != v) ord = idx == 0 ? 0xffffffffu : 0u;
+    else ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
+}
+__device__ __forceinline__ int argmax_unpack(unsigned long long key) {
+    return (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
 }
 
 // tanh-form GELU as gorch computes it (ops.go:417-443), f32 throughout.

@@ -29,8 +29,10 @@ namespace gh {
 template <int NT, int NW, int U>
 __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
     const float* __restrict__ x, const uint16_t* __restrict__ W, const float* __restrict__ bias,
-    const float* residual, OutDesc od, int M, int N, int K, int kw, int epilogue) {
+    const float* residual, OutDesc od, int M, int N, int K, int kw, int epilogue, LinearExtras ex) {
     __shared__ floatx4 red[NW][NT][64];
+    __shared__ float s_mean[16], s_inv[16];
+    __shared__ unsigned long long s_key[16];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -42,8 +44,9 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
     const int kb = wave * kw;
     const int ke = min(kb + kw, K);
 
+    const long long xs = ex.x_stride ? ex.x_stride : K;
     const bool arow_ok = mrow < M;
-    const float* xrow = x + (size_t)(arow_ok ? mrow : 0) * K;
+    const float* xrow = x + (size_t)(arow_ok ? mrow : 0) * xs;
 
     const uint16_t* wrow[NT];
     bool wrow_ok[NT];
@@ -53,6 +56,38 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
         wrow_ok[t] = n < N;
         wrow[t] = W + (size_t)(wrow_ok[t] ? n : 0) * K;
     }
+
+    if (ex.ln_g) {
+        // LayerNorm prologue (nn/layernorm.go:61-91): per-row mean and
+        // variance in f64 over the whole K, computed by each block for its
+        // (at most 16) rows; the A operand is normalised as it is loaded.
+        for (int rr = wave; rr < 16; rr += NW) {
+            const int m = m0 + rr;
+            if (m >= M) break;
+            const float* row = x + (size_t)m * xs;
+            double s1 = 0.0;
+            for (int k = 4 * lane; k < K; k += 256) {
+                float4 v = *reinterpret_cast<const float4*>(row + k);
+                s1 += (double)v.x + (double)v.y + (double)v.z + (double)v.w;
+            }
+            const double mean = wave_sum_d(s1) / (double)K;
+            double s2 = 0.0;
+            for (int k = 4 * lane; k < K; k += 256) {
+                float4 v = *reinterpret_cast<const float4*>(row + k);
+                double d0 = (double)v.x - mean, d1 = (double)v.y - mean, d2 = (double)v.z - mean,
+                       d3 = (double)v.w - mean;
+                s2 += d0 * d0 + d1 * d1 + d2 * d2 + d3 * d3;
+            }
+            const double var = wave_sum_d(s2) / (double)K;
+            if (lane == 0) {
+                s_mean[rr] = (float)mean;
+                s_inv[rr] = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
+            }
+        }
+        __syncthreads();
+    }
+    const float ln_mean = ex.ln_g ? s_mean[r] : 0.f;
+    const float ln_inv = ex.ln_g ? s_inv[r] : 1.f;
 
     floatx4 acc[NT];
 #pragma unroll
@@ -79,6 +114,19 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
                 float4 a1 = *reinterpret_cast<const float4*>(xrow + kc + 4);
                 f[u][0] = a0.x; f[u][1] = a0.y; f[u][2] = a0.z; f[u][3] = a0.w;
                 f[u][4] = a1.x; f[u][5] = a1.y; f[u][6] = a1.z; f[u][7] = a1.w;
+                if (ex.ln_g) {
+                    float4 g0 = *reinterpret_cast<const float4*>(ex.ln_g + kc);
+                    float4 g1 = *reinterpret_cast<const float4*>(ex.ln_g + kc + 4);
+                    float4 b0 = *reinterpret_cast<const float4*>(ex.ln_b + kc);
+                    float4 b1 = *reinterpret_cast<const float4*>(ex.ln_b + kc + 4);
+                    const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+                    const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        float normalized = (f[u][i] - ln_mean) * ln_inv;
+                        f[u][i] = normalized * gg[i] + bb[i];
+                    }
+                }
             } else {
 #pragma unroll
                 for (int i = 0; i < 8; i++) f[u][i] = 0.f;
@@ -101,6 +149,9 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
     for (int t = 0; t < NT; t++) red[wave][t][lane] = acc[t];
     __syncthreads();
 
+    if (ex.argmax_key && threadIdx.x < 16) s_key[threadIdx.x] = 0ull;
+    if (ex.argmax_key) __syncthreads();
+
     // Output element o = (tile t, lane e, slot v): row m0 + 4*(e/16) + v,
     // column n0 + 16*t + e%16. Partials are summed in wave order.
     for (int o = threadIdx.x; o < NT * 256; o += NW * 64) {
@@ -115,7 +166,13 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
             if (epilogue == GORCH_HIP_EPI_GELU) s = gelu_tanh(s);
             if (residual) s = residual[(size_t)om * N + on] + s;
             *od.at(om, on) = s;
+            if (ex.argmax_key) atomicMax(&s_key[om - m0], argmax_pack(s, on));
         }
+    }
+    if (ex.argmax_key) {
+        __syncthreads();
+        if (threadIdx.x < 16 && m0 + (int)threadIdx.x < M)
+            atomicMax(&ex.argmax_key[m0 + threadIdx.x], s_key[threadIdx.x]);
     }
 }
 
@@ -165,14 +222,16 @@ static GemvPlan plan_gemv(int M, int N, int K) {
 
 template <int NT, int NW, int U>
 static void launch_t(hipStream_t s, dim3 grid, const float* x, const uint16_t* W, const float* bias,
-                     const float* residual, const OutDesc& od, int M, int N, int K, int kw, int epilogue) {
+                     const float* residual, const OutDesc& od, int M, int N, int K, int kw, int epilogue,
+                     const LinearExtras& ex) {
     hipLaunchKernelGGL((k_linear_bf16_mfma<NT, NW, U>), grid, dim3(NW * 64), 0, s, x, W, bias, residual, od,
-                       M, N, K, kw, epilogue);
+                       M, N, K, kw, epilogue, ex);
 }
 
 int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                        const float* residual, float* y, int M, int N, int K, int epilogue) {
-    return launch_linear_bf16_od(s, x, W, bias, residual, OutDesc::plain(y, N), M, N, K, epilogue);
+    return launch_linear_bf16_od(s, x, W, bias, residual, OutDesc::plain(y, N), M, N, K, epilogue,
+                                 LinearExtras{});
 }
 
 int launch_gemm_bf16w(hipStream_t s, const float* A, const uint16_t* W, const float* bias,
@@ -182,15 +241,22 @@ int launch_gemm_bf16w(hipStream_t s, const float* A, const uint16_t* W, const fl
 // M <= 16: the weight-streaming GEMV below; larger M: the tiled MFMA GEMM
 // (gemm.hip), which re-reads each weight tile only once per BM rows.
 int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
-                          const float* residual, const OutDesc& od, int M, int N, int K, int epilogue) {
-    if (M > 16) return launch_gemm_bf16w(s, x, W, bias, residual, od, M, N, K, epilogue, false);
+                          const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
+                          const LinearExtras& ex) {
+    if (M > 16) {
+        if (ex.ln_g || ex.argmax_key) {
+            set_error("linear_bf16: fused LayerNorm / argmax need M <= 16");
+            return GORCH_HIP_EUNSUPPORTED;
+        }
+        return launch_gemm_bf16w(s, x, W, bias, residual, od, M, N, K, epilogue, false);
+    }
     GemvPlan p = plan_gemv(M, N, K);
     int per = (K + p.nw - 1) / p.nw;
     int kw = (per + 31) / 32 * 32;
     dim3 grid((N + 16 * p.nt - 1) / (16 * p.nt), (M + 15) / 16);
 #define GH_CASE(T, WV, UV)                                                                   \
     if (p.nt == T && p.nw == WV && p.u == UV) {                                              \
-        launch_t<T, WV, UV>(s, grid, x, W, bias, residual, od, M, N, K, kw, epilogue);       \
+        launch_t<T, WV, UV>(s, grid, x, W, bias, residual, od, M, N, K, kw, epilogue, ex);   \
         count(M <= 16 ? CNT_GEMV : CNT_GEMM);                                                \
         return check_launch("linear_bf16");                                                  \
     }

@@ -65,6 +65,7 @@ struct gorch_hip_kvcache {
     float *k = nullptr, *v = nullptr;
     int* state = nullptr;  // [0] = pos (cache length), [1] = generation step
     int* hist = nullptr;   // generated tokens [capacity][batch]
+    unsigned long long* key = nullptr;  // fused-argmax keys [batch], zero between steps
 };
 
 namespace gh {
@@ -113,15 +114,18 @@ static int ensure_acts(gorch_hip_gpt* g, size_t rows, size_t logit_rows) {
 // One GPT forward over n new tokens per sequence (ids already in g->ids,
 // row-major [batch, n]). all_rows: LM head on every row (logits
 // [batch*n, V]); otherwise only on the last row of each sequence
-// (logits [batch, V]). Does not advance pos.
-static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows, hipStream_t s) {
+// (logits [batch, V]). With at most 16 rows the LayerNorms run inside the
+// following GEMV; argmax_key (last-row mode, batch <= 16) receives the
+// packed greedy choice per sequence. Does not advance pos.
+static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows, hipStream_t s,
+                   unsigned long long* argmax_key) {
     const int d = g->dim, B = c->batch, rows = B * n, hd = d / g->heads;
     const float eps = 1e-5f;
     const int* pos = c->state;
+    const bool fused = rows <= 16;
     GH_TRY(launch_embed_pos(s, g->wte, g->wpe, g->ids, pos, g->x, d, n, rows));
     for (int l = 0; l < g->layers; l++) {
         const LayerW& w = g->L[l];
-        GH_TRY(launch_layernorm(s, g->x, w.ln1_g, w.ln1_b, g->h, rows, d, eps, d));
         OutDesc od{};
         od.nseg = 3;
         od.rows_per_seq = n;
@@ -140,26 +144,82 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             od.row_stride[sgi] = d;
             od.use_pos[sgi] = 1;
         }
-        GH_TRY(launch_linear_bf16_od(s, g->h, w.wqkv, w.bqkv, nullptr, od, rows, 3 * d, d, GORCH_HIP_EPI_NONE));
+        LinearExtras ln1, ln2;
+        if (fused) {
+            ln1.ln_g = w.ln1_g;
+            ln1.ln_b = w.ln1_b;
+            ln2.ln_g = w.ln2_g;
+            ln2.ln_b = w.ln2_b;
+            ln1.ln_eps = ln2.ln_eps = eps;
+            GH_TRY(launch_linear_bf16_od(s, g->x, w.wqkv, w.bqkv, nullptr, od, rows, 3 * d, d, GORCH_HIP_EPI_NONE,
+                                         ln1));
+        } else {
+            GH_TRY(launch_layernorm(s, g->x, w.ln1_g, w.ln1_b, g->h, rows, d, eps, d));
+            GH_TRY(launch_linear_bf16_od(s, g->h, w.wqkv, w.bqkv, nullptr, od, rows, 3 * d, d, GORCH_HIP_EPI_NONE,
+                                         LinearExtras{}));
+        }
         AttnArgs a{g->q, kc_layer(c, l), vc_layer(c, l), g->att, pos, 0, n, d, hd, c->capacity, d, 1,
                    1.0f / sqrtf((float)hd)};
         GH_TRY(launch_attn_cached(s, a, g->heads, rows));
         GH_TRY(launch_linear_bf16(s, g->att, w.wo, w.bo, g->x, g->x, rows, d, d, GORCH_HIP_EPI_NONE));
-        GH_TRY(launch_layernorm(s, g->x, w.ln2_g, w.ln2_b, g->h, rows, d, eps, d));
-        GH_TRY(launch_linear_bf16(s, g->h, w.w1, w.b1, nullptr, g->ff, rows, 4 * d, d, GORCH_HIP_EPI_GELU));
+        if (fused) {
+            GH_TRY(launch_linear_bf16_od(s, g->x, w.w1, w.b1, nullptr, OutDesc::plain(g->ff, 4 * d), rows, 4 * d,
+                                         d, GORCH_HIP_EPI_GELU, ln2));
+        } else {
+            GH_TRY(launch_layernorm(s, g->x, w.ln2_g, w.ln2_b, g->h, rows, d, eps, d));
+            GH_TRY(launch_linear_bf16(s, g->h, w.w1, w.b1, nullptr, g->ff, rows, 4 * d, d, GORCH_HIP_EPI_GELU));
+        }
         GH_TRY(launch_linear_bf16(s, g->ff, w.w2, w.b2, g->x, g->x, rows, d, 4 * d, GORCH_HIP_EPI_NONE));
     }
-    if (all_rows) {
-        GH_TRY(launch_layernorm(s, g->x, g->lnf_g, g->lnf_b, g->h, rows, d, eps, d));
-        GH_TRY(launch_linear_bf16(s, g->h, g->wlm, g->blm, nullptr, g->logits, rows, g->vocab, d,
-                                  GORCH_HIP_EPI_NONE));
+    const int head_rows = all_rows ? rows : B;
+    const float* head_in = all_rows ? g->x : g->x + (size_t)(n - 1) * d;
+    const long long head_stride = all_rows ? d : (long long)n * d;
+    if (head_rows <= 16) {
+        LinearExtras lf;
+        lf.ln_g = g->lnf_g;
+        lf.ln_b = g->lnf_b;
+        lf.ln_eps = eps;
+        lf.x_stride = head_stride;
+        lf.argmax_key = all_rows ? nullptr : argmax_key;
+        GH_TRY(launch_linear_bf16_od(s, head_in, g->wlm, g->blm, nullptr, OutDesc::plain(g->logits, g->vocab),
+                                     head_rows, g->vocab, d, GORCH_HIP_EPI_NONE, lf));
     } else {
-        GH_TRY(launch_layernorm(s, g->x + (size_t)(n - 1) * d, g->lnf_g, g->lnf_b, g->h, B, d, eps,
-                                (long long)n * d));
-        GH_TRY(launch_linear_bf16(s, g->h, g->wlm, g->blm, nullptr, g->logits, B, g->vocab, d,
+        GH_TRY(launch_layernorm(s, head_in, g->lnf_g, g->lnf_b, g->h, head_rows, d, eps, head_stride));
+        GH_TRY(launch_linear_bf16(s, g->h, g->wlm, g->blm, nullptr, g->logits, head_rows, g->vocab, d,
                                   GORCH_HIP_EPI_NONE));
     }
     return GORCH_HIP_OK;
+}
+
+// Turns the last forward's logits into each sequence's next token: writes
+// it as the next input id and into the history, advances pos by `inc` and
+// the step by one. Batches of up to 16 use the argmax fused into the LM
+// head (one tiny kernel decodes and clears the keys); larger batches run
+// the standalone argmax kernel.
+__global__ void k_finalize_step(unsigned long long* key, int B, int* ids, int* hist, int* state, int inc) {
+    const int step = state[1];
+    for (int b = threadIdx.x; b < B; b += blockDim.x) {
+        const int tok = argmax_unpack(key[b]);
+        ids[b] = tok;
+        hist[(size_t)step * B + b] = tok;
+        key[b] = 0ull;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        state[0] += inc;
+        state[1] = step + 1;
+    }
+}
+
+static int choose_tokens(gorch_hip_gpt* g, gorch_hip_kvcache* c, int inc, hipStream_t s) {
+    if (c->batch <= 16) {
+        hipLaunchKernelGGL(k_finalize_step, dim3(1), dim3(64), 0, s, c->key, c->batch, g->ids, c->hist, c->state,
+                           inc);
+        count(CNT_ARGMAX);
+        return check_launch("finalize_step");
+    }
+    GH_TRY(launch_argmax(s, g->logits, c->batch, g->vocab, g->ids, c->hist, c->state + 1, c->batch, c->state, inc));
+    return launch_advance_step(s, c->state + 1);
 }
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -320,6 +380,8 @@ gorch_hip_kvcache* gorch_hip_kvcache_create(gorch_hip_gpt* g, int batch, int cap
     if (check(hipMalloc(&c->k, elems * 4), "hipMalloc kv") || check(hipMalloc(&c->v, elems * 4), "hipMalloc kv") ||
         check(hipMalloc(&c->state, 2 * sizeof(int)), "hipMalloc state") ||
         check(hipMalloc(&c->hist, ((size_t)capacity + 1) * batch * sizeof(int)), "hipMalloc hist") ||
+        check(hipMalloc(&c->key, (size_t)batch * sizeof(unsigned long long)), "hipMalloc key") ||
+        check(hipMemset(c->key, 0, (size_t)batch * sizeof(unsigned long long)), "hipMemset key") ||
         check(hipMemset(c->state, 0, 2 * sizeof(int)), "hipMemset state")) {
         gorch_hip_kvcache_free(c);
         return nullptr;
@@ -333,6 +395,7 @@ void gorch_hip_kvcache_free(gorch_hip_kvcache* c) {
     (void)hipFree(c->v);
     (void)hipFree(c->state);
     (void)hipFree(c->hist);
+    (void)hipFree(c->key);
     delete c;
 }
 
@@ -367,7 +430,7 @@ int gorch_hip_gpt_forward_cached(void* stream, gorch_hip_gpt* g, gorch_hip_kvcac
     hipStream_t s = stream_of(stream);
     GH_TRY(ensure_acts(g, rows, rows));
     GH_TRY(check(hipMemcpyAsync(g->ids, ids, rows * sizeof(int), hipMemcpyHostToDevice, s), "upload ids"));
-    GH_TRY(forward(g, c, n, true, s));
+    GH_TRY(forward(g, c, n, true, s, nullptr));
     hipLaunchKernelGGL(k_pos_add, dim3(1), dim3(1), 0, s, c->state, n);
     GH_TRY(check_launch("pos_add"));
     c->len += n;
@@ -426,9 +489,7 @@ int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* g, const int* prompts
         }
         (void)hipEventRecord(ev[0], s);
         // prefill: logits of the last prompt row per sequence -> token 0
-        if (forward(g, c, np, false, s) ||
-            launch_argmax(s, g->logits, batch, g->vocab, g->ids, c->hist, c->state + 1, batch, c->state, np) ||
-            launch_advance_step(s, c->state + 1)) {
+        if (forward(g, c, np, false, s, c->key) || choose_tokens(g, c, np, s)) {
             fail(GORCH_HIP_ERUNTIME);
             break;
         }
@@ -439,9 +500,8 @@ int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* g, const int* prompts
         }
         // one decode step: forward the latest token of each sequence, choose the next
         auto step = [&]() -> int {
-            GH_TRY(forward(g, c, 1, false, s));
-            GH_TRY(launch_argmax(s, g->logits, batch, g->vocab, g->ids, c->hist, c->state + 1, batch, c->state, 1));
-            return launch_advance_step(s, c->state + 1);
+            GH_TRY(forward(g, c, 1, false, s, c->key));
+            return choose_tokens(g, c, 1, s);
         };
         if (use_graph && forwards > 0) {
             if (check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture")) {

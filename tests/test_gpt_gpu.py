@@ -137,3 +137,13 @@ def test_gpt2_small_greedy_decode(gpt2_small):
     assert rel_err(logits[:, 0], ref_logits) <= 2e-2             # full run
     ids_graph, _, _ = g.generate_cached(prompt[None, :], 64, use_graph=True)
     assert np.array_equal(ids_graph, ids)
+
+
+def test_generate_batch_above_16(tiny):
+    # batches over 16 take the standalone argmax path instead of the fused one
+    w, g, o = tiny
+    prompts = np.stack([syn.prompt_ids(3, TINY["vocab"], seed=40 + b) for b in range(17)])
+    ids, _, _ = g.generate_cached(prompts, 5)
+    for b in (0, 9, 16):
+        ref, _, _ = o.generate_cached(prompts[b], 5)
+        assert list(ids[b]) == list(ref)
