@@ -49,7 +49,7 @@ def parse():
                     help="restrict to one shape 'M,K,N' (for profiling one kernel)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the GPT decode legs")
-    ap.add_argument("--only", choices=("decode", "gemm", "decode-xl"), default=None,
+    ap.add_argument("--only", choices=("decode", "gemm", "decode-xl", "moe"), default=None,
                     help="run only one secondary leg and print its JSON (for profiling)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -196,6 +196,40 @@ def gemm_leg(M=512, K=768, Ns=(2304, 3072)):
     return out
 
 
+def moe_leg():
+    """MoE layer: 2048 tokens, d 1024, 8 experts of ffn
+    4096, top-2, injected logits. Algorithmic FLOPs 6*d*ffn per assignment."""
+    import torch
+
+    from gorch_amd import hip
+    from gorch_amd import synthetic as syn
+
+    x, logits, w = syn.moe_inputs(seed=0)
+    m = hip.MoE(w)
+    xd, ld = torch.from_numpy(x).cuda(), torch.from_numpy(logits).cuda()
+    out = torch.empty_like(xd)
+    m.forward(xd, ld, out)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    L = 20
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(L):
+            m.forward(xd, ld, out)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(3):
+        g.replay()
+    e1.record(stream)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (3 * L)
+    flops = 2048 * 2 * 6.0 * 1024 * 4096
+    return {"tokens": 2048, "dim": 1024, "ffn": 4096, "experts": 8, "top_k": 2, "us": round(us, 2),
+            "TFLOPs": round(flops / us / 1e6, 1), "frac_mfma_peak": round(flops / us / 1e6 / MFMA_PEAK_TFLOPS, 4)}
+
+
 def decode_leg(cfg_name, batch, n_prompt, max_new, reps=3):
     """Greedy KV-cache decode through the engine (graph-replayed step).
     tok/s = batch * decode forwards / decode wall time (prefill timed apart)."""
@@ -263,6 +297,8 @@ def main():
             print(json.dumps(decode_leg("gpt2-small", 1, 32, 64)))
         elif args.only == "decode-xl":
             print(json.dumps(decode_leg("gpt2-xl", 16, 512, 256, reps=1)))
+        elif args.only == "moe":
+            print(json.dumps(moe_leg()))
         else:
             print(json.dumps(gemm_leg()))
         return
@@ -279,6 +315,7 @@ def main():
     value, wall, per_shape, dom = gpu_leg(args, shapes)
     decode = [] if (args.shape or args.no_decode) else [decode_leg("gpt2-small", 1, 32, 64)]
     gemm = [] if args.shape else gemm_leg()
+    moe = None if args.shape else moe_leg()
     cpu = None if args.no_cpu else cpu_leg(shapes, args.cpu_seconds)
     dom_bytes = algo_bytes(dom["M"], dom["K"], dom["N"])
     out = {
@@ -315,6 +352,7 @@ def main():
         "per_shape": per_shape,
         "decode": decode,
         "prefill_gemm": gemm,
+        "moe_layer": moe,
     }
     print(json.dumps(out))
 

@@ -1,0 +1,365 @@
+// moe.hip — the MoE FFN layer of nn.MoE.Forward (nn/moe.go:130-182):
+// router logits -> top-K (index_ops.go:153-186) -> softmax over the K
+// values with exp in f64 (softmaxRows, nn/moe.go:247-268) -> tokens grouped
+// per expert in token order (:143-149) -> per expert Gather -> Wgate, Wup
+// Linears -> SwiGLU -> Wdown Linear -> x routing weight -> ScatterAdd,
+// experts accumulated in ascending index (:155-180).
+//
+// On the GPU (one stream, no host round trip, no allocation):
+//   k_moe_route      one block: top-K, weights, stable counting sort of the
+//                    (token, slot) assignments by expert, the inverse map,
+//                    and the tile table of the grouped GEMMs;
+//   k_moe_gather     packs each expert's rows contiguously (Xg);
+//   grouped GEMM 1   H = SwiGLU(Xg We_gate^T + bg, Xg We_up^T + bu): gate and
+//                    up tiles accumulate side by side, SwiGLU in the epilogue;
+//   grouped GEMM 2   Yg = (H We_down^T + bd) * w(row), the routing weight
+//                    applied in the epilogue (the reference's Mul);
+//   k_moe_combine    out[t] = sum of the token's rows in ascending expert order.
+// Expert weights are stacked [E][out][in] bf16 in one device array each.
+#include <algorithm>
+
+#include "common.h"
+
+namespace gh {
+
+constexpr int kMoeBM = 64, kMoeBN = 64, kMoeBK = 64, kMoeLD = kMoeBK + 8;
+constexpr int kMaxExperts = 64;
+constexpr int kMaxTopK = 8;
+
+struct MoeWs {
+    float* logits;   // [M, E] (router output, or a copy of injected logits)
+    int* topi;       // [M, K]
+    float* topw;     // [M, K]
+    int* perm_tok;   // [M*K] token of packed row p
+    float* perm_w;   // [M*K] routing weight of packed row p
+    int* inv;        // [M, K] packed row of (token, slot)
+    int* tile_e;     // [max_tiles] expert of m-tile i
+    int* tile_r0;    // [max_tiles] first packed row
+    int* tile_n;     // [max_tiles] rows in the tile
+    int* ntiles;     // [1]
+    float* xg;       // [M*K, dim]
+    float* h;        // [M*K, ffn]
+    float* yg;       // [M*K, dim]
+};
+
+static size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
+
+static size_t moe_layout(int M, int dim, int ffn, int E, int K, char* base, MoeWs* ws) {
+    const size_t MK = (size_t)M * K;
+    const size_t max_tiles = MK / kMoeBM + E + 1;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        size_t o = off;
+        off += al(bytes);
+        return base ? base + o : nullptr;
+    };
+    MoeWs w;
+    w.logits = (float*)take((size_t)M * E * 4);
+    w.topi = (int*)take(MK * 4);
+    w.topw = (float*)take(MK * 4);
+    w.perm_tok = (int*)take(MK * 4);
+    w.perm_w = (float*)take(MK * 4);
+    w.inv = (int*)take(MK * 4);
+    w.tile_e = (int*)take(max_tiles * 4);
+    w.tile_r0 = (int*)take(max_tiles * 4);
+    w.tile_n = (int*)take(max_tiles * 4);
+    w.ntiles = (int*)take(4);
+    w.xg = (float*)take(MK * dim * 4);
+    w.h = (float*)take(MK * ffn * 4);
+    w.yg = (float*)take(MK * dim * 4);
+    if (ws) *ws = w;
+    return off;
+}
+
+// One 128-thread block. Thread t owns tokens [t*chunk, (t+1)*chunk).
+constexpr int kRouteThreads = 128;
+__global__ __launch_bounds__(kRouteThreads) void k_moe_route(const float* __restrict__ logits, int M, int E, int K,
+                                                             MoeWs ws) {
+    __shared__ int cnt[kRouteThreads][kMaxExperts + 1];
+    __shared__ int base[kMaxExperts + 1];
+    const int t = threadIdx.x;
+    const int chunk = (M + kRouteThreads - 1) / kRouteThreads;
+    const int t0 = min(M, t * chunk), t1 = min(M, t0 + chunk);
+    for (int e = 0; e < E; e++) cnt[t][e] = 0;
+    for (int tok = t0; tok < t1; tok++) {
+        const float* row = logits + (size_t)tok * E;
+        int idx[kMaxTopK];
+        float val[kMaxTopK];
+        // top-K, descending; ties keep the lower index first
+        for (int s = 0; s < K; s++) {
+            int best = -1;
+            float bv = 0.f;
+            for (int j = 0; j < E; j++) {
+                bool taken = false;
+                for (int u = 0; u < s; u++) taken |= (idx[u] == j);
+                if (taken) continue;
+                const float v = row[j];
+                if (best < 0 || v > bv) {
+                    best = j;
+                    bv = v;
+                }
+            }
+            idx[s] = best;
+            val[s] = bv;
+        }
+        // softmaxRows: max, exp in f64 rounded to f32, f32 sum, divide
+        float mx = val[0];
+        for (int s = 1; s < K; s++) mx = val[s] > mx ? val[s] : mx;
+        float e_[kMaxTopK];
+        float sum = 0.f;
+        for (int s = 0; s < K; s++) {
+            e_[s] = (float)exp((double)(val[s] - mx));
+            sum += e_[s];
+        }
+        for (int s = 0; s < K; s++) {
+            ws.topi[(size_t)tok * K + s] = idx[s];
+            ws.topw[(size_t)tok * K + s] = e_[s] / sum;
+            cnt[t][idx[s]]++;
+        }
+    }
+    __syncthreads();
+    // per-expert exclusive scan over threads (token order), expert bases
+    if (t < E) {
+        int run = 0;
+        for (int u = 0; u < kRouteThreads; u++) {
+            int c = cnt[u][t];
+            cnt[u][t] = run;
+            run += c;
+        }
+        base[t] = run;  // total for expert t, turned into a base below
+    }
+    __syncthreads();
+    if (t == 0) {
+        int run = 0, nt = 0;
+        for (int e = 0; e < E; e++) {
+            int n = base[e];
+            base[e] = run;
+            for (int r = 0; r < n; r += kMoeBM) {
+                ws.tile_e[nt] = e;
+                ws.tile_r0[nt] = run + r;
+                ws.tile_n[nt] = min(kMoeBM, n - r);
+                nt++;
+            }
+            run += n;
+        }
+        *ws.ntiles = nt;
+    }
+    __syncthreads();
+    for (int tok = t0; tok < t1; tok++)
+        for (int s = 0; s < K; s++) {
+            const int e = ws.topi[(size_t)tok * K + s];
+            const int p = base[e] + cnt[t][e]++;
+            ws.perm_tok[p] = tok;
+            ws.perm_w[p] = ws.topw[(size_t)tok * K + s];
+            ws.inv[(size_t)tok * K + s] = p;
+        }
+}
+
+__global__ void k_moe_gather(const float* __restrict__ x, const int* __restrict__ perm_tok, float* xg, int rows,
+                             int dim) {
+    const int d4 = dim / 4;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)rows * d4;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int p = (int)(i / d4), c = (int)(i - (int64_t)p * d4);
+        reinterpret_cast<float4*>(xg)[i] = reinterpret_cast<const float4*>(x + (size_t)perm_tok[p] * dim)[c];
+    }
+}
+
+// out[t] = sum over the token's K packed rows in ascending expert order
+// (the reference adds each expert's ScatterAdd contribution in order).
+__global__ void k_moe_combine(const float* __restrict__ yg, const int* __restrict__ inv,
+                              const int* __restrict__ topi, float* out, int M, int K, int dim) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)M * dim;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int t = (int)(i / dim), c = (int)(i - (int64_t)t * dim);
+        int order[kMaxTopK];
+        for (int s = 0; s < K; s++) order[s] = s;
+        for (int a = 1; a < K; a++)  // insertion sort of slots by expert index
+            for (int b = a; b > 0 && topi[(size_t)t * K + order[b]] < topi[(size_t)t * K + order[b - 1]]; b--) {
+                int tmp = order[b];
+                order[b] = order[b - 1];
+                order[b - 1] = tmp;
+            }
+        float acc = 0.f;
+        for (int s = 0; s < K; s++) acc = acc + yg[(size_t)inv[(size_t)t * K + order[s]] * dim + c];
+        out[i] = acc;
+    }
+}
+
+// Grouped GEMM over the tile table: blockIdx.y = m-tile (expert, packed rows),
+// blockIdx.x = 64-wide n tile. A rows are f32 (split into bf16 hi + lo), the
+// expert's weights bf16 [N, Kd]. DUAL: a second weight (up) accumulates
+// beside the first (gate) and the epilogue writes SwiGLU(gate, up). Else the
+// epilogue multiplies by the packed row's routing weight.
+template <bool DUAL>
+__global__ __launch_bounds__(256) void k_moe_gemm(const float* __restrict__ A, const uint16_t* __restrict__ W1,
+                                                  const uint16_t* __restrict__ W2, const float* __restrict__ b1,
+                                                  const float* __restrict__ b2, float* __restrict__ C, int N,
+                                                  int Kd, MoeWs ws) {
+    constexpr int NB = DUAL ? 2 : 1;
+    __shared__ __align__(16) uint16_t As[2][kMoeBM][kMoeLD];
+    __shared__ __align__(16) uint16_t Ws[NB][kMoeBN][kMoeLD];
+    if ((int)blockIdx.y >= *ws.ntiles) return;
+    const int e = ws.tile_e[blockIdx.y], r0 = ws.tile_r0[blockIdx.y], nrows = ws.tile_n[blockIdx.y];
+    const int n0 = blockIdx.x * kMoeBN;
+    const uint16_t* Wb[2] = {W1 + (size_t)e * N * Kd, DUAL ? W2 + (size_t)e * N * Kd : nullptr};
+    const float* bb[2] = {b1 ? b1 + (size_t)e * N : nullptr, (DUAL && b2) ? b2 + (size_t)e * N : nullptr};
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;  // 2x2 waves, 32x32 each
+    const int r = lane & 15, g = lane >> 4;
+    float4 ra[4];
+    uint4 rw[NB][2];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
+            const int k = k0 + 4 * c4;
+            ra[i] = (row < nrows && k < Kd) ? *reinterpret_cast<const float4*>(A + (size_t)(r0 + row) * Kd + k)
+                                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int idx = tid + 256 * i, row = idx >> 3, c8 = idx & 7;
+                const int n = n0 + row, k = k0 + 8 * c8;
+                rw[b][i] = (n < N && k < Kd) ? *reinterpret_cast<const uint4*>(Wb[b] + (size_t)n * Kd + k)
+                                             : make_uint4(0, 0, 0, 0);
+            }
+    };
+    auto sstore = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
+            const float f[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
+            uint16_t hi[4], lo[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                uint32_t u = __float_as_uint(f[q]) & 0xffff0000u;
+                hi[q] = (uint16_t)(u >> 16);
+                lo[q] = __builtin_bit_cast(uint16_t, (__bf16)(f[q] - __uint_as_float(u)));
+            }
+            *reinterpret_cast<uint2*>(&As[0][row][4 * c4]) =
+                make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+            *reinterpret_cast<uint2*>(&As[1][row][4 * c4]) =
+                make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int idx = tid + 256 * i, row = idx >> 3, c8 = idx & 7;
+                *reinterpret_cast<uint4*>(&Ws[b][row][8 * c8]) = rw[b][i];
+            }
+    };
+
+    floatx4 acc[NB][2][2];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc[b][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    gload(0);
+    for (int k0 = 0; k0 < Kd; k0 += kMoeBK) {
+        __syncthreads();
+        sstore();
+        __syncthreads();
+        if (k0 + kMoeBK < Kd) gload(k0 + kMoeBK);
+#pragma unroll
+        for (int kk = 0; kk < kMoeBK; kk += 32) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const bf16x8 ahi = *reinterpret_cast<const bf16x8*>(&As[0][wm * 32 + i * 16 + r][kk + 8 * g]);
+                const bf16x8 alo = *reinterpret_cast<const bf16x8*>(&As[1][wm * 32 + i * 16 + r][kk + 8 * g]);
+#pragma unroll
+                for (int b = 0; b < NB; b++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        const bf16x8 wf = *reinterpret_cast<const bf16x8*>(&Ws[b][wn * 32 + j * 16 + r][kk + 8 * g]);
+                        acc[b][i][j] = mfma16x16x32(ahi, wf, acc[b][i][j]);
+                        acc[b][i][j] = mfma16x16x32(alo, wf, acc[b][i][j]);
+                    }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn * 32 + j * 16 + r;
+            if (n >= N) continue;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int row = wm * 32 + i * 16 + 4 * g + v;
+                if (row >= nrows) continue;
+                const int p = r0 + row;
+                float s = acc[0][i][j][v];
+                if (bb[0]) s = s + bb[0][n];
+                if (DUAL) {
+                    float u = acc[NB - 1][i][j][v];
+                    if (bb[1]) u = u + bb[1][n];
+                    s = s * sigmoidf_ref(s) * u;  // SwiGLU: gate * sigma(gate) * up
+                } else {
+                    s = s * ws.perm_w[p];          // weighted = exOut * w
+                }
+                C[(size_t)p * N + n] = s;
+            }
+        }
+}
+
+}  // namespace gh
+
+using namespace gh;
+
+extern "C" size_t gorch_hip_moe_workspace_size(int M, int dim, int ffn, int experts, int top_k) {
+    if (M <= 0 || dim <= 0 || ffn <= 0 || experts <= 0 || top_k <= 0) return 0;
+    return moe_layout(M, dim, ffn, experts, top_k, nullptr, nullptr);
+}
+
+extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* w, const float* x, int M,
+                                     const float* logits, float* out, int* topk_idx, float* topk_w,
+                                     void* workspace, size_t workspace_bytes) {
+    GH_REQUIRE(w && x && out && M > 0, "gorch_hip_moe_forward: bad arguments");
+    const int E = w->experts, K = w->top_k, d = w->dim, F = w->ffn;
+    GH_REQUIRE(K >= 1 && K <= E, "gorch/nn: MoE numExpertsPerToken out of range");
+    GH_REQUIRE(E <= kMaxExperts && K <= kMaxTopK, "gorch_hip_moe_forward: at most 64 experts and top-8");
+    GH_REQUIRE(d % 8 == 0 && F % 8 == 0, "gorch_hip_moe_forward: dim and ffn must be multiples of 8");
+    GH_REQUIRE(w->wgate && w->wup && w->wdown, "gorch_hip_moe_forward: null expert weights");
+    GH_REQUIRE(logits || w->wr, "gorch_hip_moe_forward: need router weights or injected logits");
+    const size_t need = moe_layout(M, d, F, E, K, nullptr, nullptr);
+    GH_REQUIRE(workspace && workspace_bytes >= need, "gorch_hip_moe_forward: workspace too small");
+    MoeWs ws;
+    moe_layout(M, d, F, E, K, (char*)workspace, &ws);
+    hipStream_t s = stream_of(stream);
+    if (logits) {
+        GH_TRY(check(hipMemcpyAsync(ws.logits, logits, (size_t)M * E * 4, hipMemcpyDeviceToDevice, s), "logits"));
+    } else {
+        GH_TRY(launch_linear_bf16(s, x, w->wr, w->br, nullptr, ws.logits, M, E, d, GORCH_HIP_EPI_NONE));
+    }
+    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(kRouteThreads), 0, s, ws.logits, M, E, K, ws);
+    GH_TRY(check_launch("moe_route"));
+    const int MK = M * K;
+    const int gblocks = (int)std::min<int64_t>(8192, ((int64_t)MK * d / 4 + 255) / 256);
+    hipLaunchKernelGGL(k_moe_gather, dim3(gblocks), dim3(256), 0, s, x, ws.perm_tok, ws.xg, MK, d);
+    GH_TRY(check_launch("moe_gather"));
+    const int max_tiles = MK / kMoeBM + E + 1;
+    hipLaunchKernelGGL(k_moe_gemm<true>, dim3((F + kMoeBN - 1) / kMoeBN, max_tiles), dim3(256), 0, s, ws.xg,
+                       w->wgate, w->wup, w->bgate, w->bup, ws.h, F, d, ws);
+    GH_TRY(check_launch("moe_gemm_gate_up"));
+    hipLaunchKernelGGL(k_moe_gemm<false>, dim3((d + kMoeBN - 1) / kMoeBN, max_tiles), dim3(256), 0, s, ws.h,
+                       w->wdown, nullptr, w->bdown, nullptr, ws.yg, d, F, ws);
+    GH_TRY(check_launch("moe_gemm_down"));
+    const int cblocks = (int)std::min<int64_t>(8192, ((int64_t)M * d + 255) / 256);
+    hipLaunchKernelGGL(k_moe_combine, dim3(cblocks), dim3(256), 0, s, ws.yg, ws.inv, ws.topi, out, M, K, d);
+    GH_TRY(check_launch("moe_combine"));
+    if (topk_idx)
+        GH_TRY(check(hipMemcpyAsync(topk_idx, ws.topi, (size_t)M * K * 4, hipMemcpyDeviceToDevice, s), "topk idx"));
+    if (topk_w)
+        GH_TRY(check(hipMemcpyAsync(topk_w, ws.topw, (size_t)M * K * 4, hipMemcpyDeviceToDevice, s), "topk w"));
+    count(CNT_MOE);
+    return GORCH_HIP_OK;
+}

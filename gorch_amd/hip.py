@@ -65,6 +65,8 @@ SIGNATURES = {
     "gorch_hip_causal_softmax": (i32, [vp, vp, vp, i32, i32, i32, f32]),
     "gorch_hip_softmax_rows": (i32, [vp, vp, i32, i32]),
     "gorch_hip_argmax": (i32, [vp, vp, i32, i32, vp]),
+    "gorch_hip_moe_workspace_size": (C.c_size_t, [i32, i32, i32, i32, i32]),
+    "gorch_hip_moe_forward": (i32, [vp, vp, vp, i32, vp, vp, vp, vp, vp, C.c_size_t]),
     "gorch_hip_gpt_create": (vp, [vp]),
     "gorch_hip_gpt_free": (None, [vp]),
     "gorch_hip_kvcache_create": (vp, [vp, i32, i32]),
@@ -352,3 +354,62 @@ class KVCache:
 
     def __del__(self):
         self.close()
+
+
+# ------------------------------------------------------------------ MoE
+
+class _MoEWeights(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("dim", "ffn", "experts", "top_k")] + [
+        (n, vp) for n in ("wr", "br", "wgate", "bgate", "wup", "bup", "wdown", "bdown")]
+
+
+class MoE:
+    """gorch's nn.MoE (nn/moe.go:28-182) on the GPU. ``w`` holds numpy
+    arrays as gorch_amd.synthetic.moe_inputs builds them (per-expert lists);
+    they are stacked and uploaded once."""
+
+    def __init__(self, w: dict):
+        import numpy as np
+        import torch
+
+        def stack(key, dtype):
+            arrs = w.get(key)
+            if arrs is None:
+                return None
+            a = np.ascontiguousarray(np.stack(arrs))
+            t = torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).cuda()
+            return t
+
+        self.dim, self.ffn, self.experts, self.top_k = w["dim"], w["ffn"], w["experts"], w["top_k"]
+        self.t = {k: stack(k, None) for k in ("wgate", "bgate", "wup", "bup", "wdown", "bdown")}
+        self.t["wr"] = None if w.get("wr") is None else torch.from_numpy(
+            np.ascontiguousarray(w["wr"]).view(np.int16)).cuda()
+        self.t["br"] = None if w.get("br") is None else torch.from_numpy(np.ascontiguousarray(w["br"])).cuda()
+        s = _MoEWeights()
+        s.dim, s.ffn, s.experts, s.top_k = self.dim, self.ffn, self.experts, self.top_k
+        for k, v in self.t.items():
+            setattr(s, k, None if v is None else v.data_ptr())
+        self.s = s
+        self.ws = None
+
+    def workspace(self, M):
+        import torch
+
+        n = lib().gorch_hip_moe_workspace_size(M, self.dim, self.ffn, self.experts, self.top_k)
+        if self.ws is None or self.ws.numel() < n:
+            self.ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+        return self.ws
+
+    def forward(self, x, logits=None, out=None):
+        """x [M, dim] device f32; logits [M, experts] device f32 or None.
+        Returns (out, topk_idx, topk_w) device tensors."""
+        import torch
+
+        M = x.shape[0]
+        ws = self.workspace(M)
+        out = torch.empty((M, self.dim), dtype=torch.float32, device="cuda") if out is None else out
+        idx = torch.empty((M, self.top_k), dtype=torch.int32, device="cuda")
+        wts = torch.empty((M, self.top_k), dtype=torch.float32, device="cuda")
+        _ok(lib().gorch_hip_moe_forward(_stream(), C.byref(self.s), _p(x), M, _p(logits), _p(out), _p(idx),
+                                        _p(wts), ws.data_ptr(), ws.numel()))
+        return out, idx, wts

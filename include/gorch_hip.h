@@ -151,6 +151,34 @@ int gorch_hip_softmax_rows(void* stream, float* x, int rows, int cols);
 int gorch_hip_argmax(void* stream, const float* logits, int rows, int n, int* out);
 
 /* ------------------------------------------------------------------------
+ * MoE FFN layer (nn.MoE.Forward, nn/moe.go:130-182).
+ * ---------------------------------------------------------------------- */
+
+/* Device pointers. Expert weights are stacked per kind: wgate / wup
+ * [experts][ffn][dim], wdown [experts][dim][ffn] (bf16, Linear layout);
+ * biases [experts][out] f32 or NULL (= zero). wr / br: the router Linear
+ * [experts, dim] (bf16) / [experts], or NULL when logits are injected. */
+typedef struct {
+    int dim, ffn, experts, top_k;
+    const uint16_t* wr; const float* br;
+    const uint16_t* wgate; const float* bgate;
+    const uint16_t* wup; const float* bup;
+    const uint16_t* wdown; const float* bdown;
+} gorch_hip_moe_weights;
+
+/* Device workspace bytes gorch_hip_moe_forward needs for M tokens. */
+size_t gorch_hip_moe_workspace_size(int M, int dim, int ffn, int experts, int top_k);
+/* out [M, dim] = MoE(x [M, dim]). logits: injected router logits [M, experts]
+ * (device) or NULL to run the router Linear. topk_idx / topk_w (device,
+ * nullable) receive the chosen experts [M, top_k] (descending logit, ties
+ * to the lower index) and their softmax weights. The workspace is the
+ * caller's (no allocation inside; the call is graph-capturable). Top-k is
+ * limited to 8 and experts to 64. */
+int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* w, const float* x, int M,
+                          const float* logits, float* out, int* topk_idx, float* topk_w,
+                          void* workspace, size_t workspace_bytes);
+
+/* ------------------------------------------------------------------------
  * GPT decode engine (nn.GPT / nn.KVCache / model.generateCached).
  * ---------------------------------------------------------------------- */
 
