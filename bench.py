@@ -293,6 +293,7 @@ def main():
         from gorch_amd import hip
         hip.init(0)
         torch.cuda.set_device(0)
+        torch.cuda.set_stream(torch.cuda.Stream())  # graphs capture on a non-default stream
         if args.only == "decode":
             print(json.dumps(decode_leg("gpt2-small", 1, 32, 64)))
         elif args.only == "decode-xl":
