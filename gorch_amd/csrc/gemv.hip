@@ -181,6 +181,309 @@ static int env_int(const char* name, int dflt) {
     return s ? atoi(s) : dflt;
 }
 
+// ---------------------------------------------------------------------------
+// VALU GEMV for M <= 4 (decode batch 1..4): the weight stream uses the
+// access pattern that reaches the highest HBM bandwidth on MI355X — T lanes
+// (8..32) read one row's contiguous 16*T bytes per instruction, 64/T rows
+// per wavefront instruction — instead of the 16-row x 64-byte footprint an
+// MFMA B operand imposes. bf16 weights are widened in registers (a shift)
+// and multiplied in f32 against the activations, which the block first
+// stages in LDS (normalised there when a LayerNorm is fused). Each row's T
+// partial sums are combined with lane shuffles. Wavefronts walk row groups
+// with a grid stride, so the staging cost is shared by several row groups.
+template <int MT, int T>
+__global__ __launch_bounds__(256) void k_gemv_valu(const float* __restrict__ x, const uint16_t* __restrict__ W,
+                                                   const float* __restrict__ bias, const float* residual,
+                                                   OutDesc od, int M, int N, int K, int epilogue,
+                                                   LinearExtras ex) {
+    extern __shared__ __align__(16) float xs[];  // [MT][K]
+    __shared__ double red[8];
+    __shared__ unsigned long long s_key[MT];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const long long xstr = ex.x_stride ? ex.x_stride : K;
+
+    // stage the activation rows (LayerNorm applied here when fused)
+    for (int m = 0; m < MT; m++) {
+        float* dst = xs + (size_t)m * K;
+        if (m >= M) {
+            for (int k = tid; k < K; k += 256) dst[k] = 0.f;
+            continue;
+        }
+        const float* row = x + (size_t)m * xstr;
+        if (!ex.ln_g) {
+            for (int k = 4 * tid; k < K; k += 1024)
+                *reinterpret_cast<float4*>(dst + k) = *reinterpret_cast<const float4*>(row + k);
+            continue;
+        }
+        double s1 = 0.0;
+        for (int k = tid; k < K; k += 256) s1 += (double)row[k];
+        s1 = wave_sum_d(s1);
+        if (lane == 0) red[wave] = s1;
+        __syncthreads();
+        const double mean = (red[0] + red[1] + red[2] + red[3]) / (double)K;
+        __syncthreads();
+        double s2 = 0.0;
+        for (int k = tid; k < K; k += 256) {
+            double dd = (double)row[k] - mean;
+            s2 += dd * dd;
+        }
+        s2 = wave_sum_d(s2);
+        if (lane == 0) red[wave] = s2;
+        __syncthreads();
+        const double var = (red[0] + red[1] + red[2] + red[3]) / (double)K;
+        __syncthreads();
+        const float inv = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
+        const float fm = (float)mean;
+        for (int k = tid; k < K; k += 256) {
+            float normalized = (row[k] - fm) * inv;
+            dst[k] = normalized * ex.ln_g[k] + ex.ln_b[k];
+        }
+    }
+    if (ex.argmax_key && tid < MT) s_key[tid] = 0ull;
+    __syncthreads();
+
+    constexpr int RPI = 64 / T;         // rows per wavefront instruction
+    constexpr int CU = 8;               // 16-byte chunks per lane in flight
+    const int sub = lane % T, rloc = lane / T;
+    const int C = K / (8 * T);          // chunks per lane per row
+    const int ngroups = (N + RPI - 1) / RPI;
+    for (int rg = blockIdx.x * 4 + wave; rg < ngroups; rg += gridDim.x * 4) {
+        const int row = rg * RPI + rloc;
+        const bool row_ok = row < N;
+        const uint4* wr = reinterpret_cast<const uint4*>(W + (size_t)(row_ok ? row : 0) * K) + sub;
+        float acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; m++) acc[m] = 0.f;
+        for (int c0 = 0; c0 < C; c0 += CU) {
+            uint4 wv[CU];
+#pragma unroll
+            for (int u = 0; u < CU; u++)
+                wv[u] = (row_ok && c0 + u < C) ? wr[(size_t)T * (c0 + u)] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int u = 0; u < CU; u++) {
+                if (c0 + u >= C) break;
+                const int k = 8 * (sub + T * (c0 + u));
+                const float w8[8] = {bf16_lo(wv[u].x), bf16_hi(wv[u].x), bf16_lo(wv[u].y), bf16_hi(wv[u].y),
+                                     bf16_lo(wv[u].z), bf16_hi(wv[u].z), bf16_lo(wv[u].w), bf16_hi(wv[u].w)};
+#pragma unroll
+                for (int m = 0; m < MT; m++) {
+                    const float4 a0 = *reinterpret_cast<const float4*>(xs + (size_t)m * K + k);
+                    const float4 a1 = *reinterpret_cast<const float4*>(xs + (size_t)m * K + k + 4);
+                    acc[m] += a0.x * w8[0] + a0.y * w8[1] + a0.z * w8[2] + a0.w * w8[3] +
+                              a1.x * w8[4] + a1.y * w8[5] + a1.z * w8[6] + a1.w * w8[7];
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+            for (int o = T / 2; o > 0; o >>= 1) acc[m] += __shfl_xor(acc[m], o, 64);
+        if (sub == 0 && row_ok) {
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                if (m >= M) break;
+                float s = acc[m];
+                if (bias) s = s + bias[row];
+                if (epilogue == GORCH_HIP_EPI_GELU) s = gelu_tanh(s);
+                if (residual) s = residual[(size_t)m * N + row] + s;
+                *od.at(m, row) = s;
+                if (ex.argmax_key) atomicMax(&s_key[m], argmax_pack(s, row));
+            }
+        }
+    }
+    if (ex.argmax_key) {
+        __syncthreads();
+        if (tid < MT && tid < M) atomicMax(&ex.argmax_key[tid], s_key[tid]);
+    }
+}
+
+// M = 1 variant with the activation row held in registers: lane `sub`
+// always needs the same C chunks of x (k = 8*(sub + T*c)), so each wave
+// loads (and, with a fused LayerNorm, normalises) them once, computing the
+// row statistics itself with wave reductions — no LDS staging and no block
+// barrier before the weight stream starts. The next row group's weight
+// loads are issued before the current group is reduced.
+template <int T, int C, bool LN>
+__global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, const uint16_t* __restrict__ W,
+                                                 const float* __restrict__ bias, const float* residual, OutDesc od,
+                                                 int N, int K, int epilogue, LinearExtras ex) {
+    __shared__ unsigned long long s_key;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (ex.argmax_key) {
+        if (tid == 0) s_key = 0ull;
+        __syncthreads();
+    }
+    const int sub = lane % T, rloc = lane / T;
+    constexpr int RPI = 64 / T;
+    float xr[C][8];
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        const float4 a0 = *reinterpret_cast<const float4*>(x + 8 * (sub + T * c));
+        const float4 a1 = *reinterpret_cast<const float4*>(x + 8 * (sub + T * c) + 4);
+        xr[c][0] = a0.x; xr[c][1] = a0.y; xr[c][2] = a0.z; xr[c][3] = a0.w;
+        xr[c][4] = a1.x; xr[c][5] = a1.y; xr[c][6] = a1.z; xr[c][7] = a1.w;
+    }
+    if (LN) {
+        // the wave's lanes hold the row RPI times over (one copy per rloc):
+        // sum over the first T lanes only
+        double s1 = 0.0;
+        if (rloc == 0)
+#pragma unroll
+            for (int c = 0; c < C; c++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) s1 += (double)xr[c][i];
+        const double mean = wave_sum_d(s1) / (double)K;
+        double s2 = 0.0;
+        if (rloc == 0)
+#pragma unroll
+            for (int c = 0; c < C; c++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const double dd = (double)xr[c][i] - mean;
+                    s2 += dd * dd;
+                }
+        const double var = wave_sum_d(s2) / (double)K;
+        const float inv = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
+        const float fm = (float)mean;
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+            const int k = 8 * (sub + T * c);
+            const float4 g0 = *reinterpret_cast<const float4*>(ex.ln_g + k);
+            const float4 g1 = *reinterpret_cast<const float4*>(ex.ln_g + k + 4);
+            const float4 b0 = *reinterpret_cast<const float4*>(ex.ln_b + k);
+            const float4 b1 = *reinterpret_cast<const float4*>(ex.ln_b + k + 4);
+            const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+            const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float normalized = (xr[c][i] - fm) * inv;
+                xr[c][i] = normalized * gg[i] + bb[i];
+            }
+        }
+    }
+
+    const int ngroups = (N + RPI - 1) / RPI;
+    const int stride = gridDim.x * 4;
+    int rg = blockIdx.x * 4 + wave;
+    uint4 wv[C];
+    auto load = [&](int g) {
+        const int row = g * RPI + rloc;
+        const bool ok = g < ngroups && row < N;
+        const uint4* wr = reinterpret_cast<const uint4*>(W + (size_t)(ok ? row : 0) * K) + sub;
+#pragma unroll
+        for (int c = 0; c < C; c++) wv[c] = ok ? wr[(size_t)T * c] : make_uint4(0, 0, 0, 0);
+    };
+    load(rg);
+    unsigned long long best = 0ull;
+    for (; rg < ngroups; rg += stride) {
+        uint4 cur[C];
+#pragma unroll
+        for (int c = 0; c < C; c++) cur[c] = wv[c];
+        load(rg + stride);  // next group's stream starts before this one is reduced
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+            acc += xr[c][0] * bf16_lo(cur[c].x) + xr[c][1] * bf16_hi(cur[c].x) + xr[c][2] * bf16_lo(cur[c].y) +
+                   xr[c][3] * bf16_hi(cur[c].y) + xr[c][4] * bf16_lo(cur[c].z) + xr[c][5] * bf16_hi(cur[c].z) +
+                   xr[c][6] * bf16_lo(cur[c].w) + xr[c][7] * bf16_hi(cur[c].w);
+        }
+#pragma unroll
+        for (int o = T / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        const int row = rg * RPI + rloc;
+        if (sub == 0 && row < N) {
+            float v = acc;
+            if (bias) v = v + bias[row];
+            if (epilogue == GORCH_HIP_EPI_GELU) v = gelu_tanh(v);
+            if (residual) v = residual[row] + v;
+            *od.at(0, row) = v;
+            if (ex.argmax_key) {
+                const unsigned long long key = argmax_pack(v, row);
+                best = key > best ? key : best;
+            }
+        }
+    }
+    if (ex.argmax_key) {
+        atomicMax(&s_key, best);
+        __syncthreads();
+        if (tid == 0) atomicMax(ex.argmax_key, s_key);
+    }
+}
+
+// (T, C) for the register-x M = 1 kernel: T lanes per row, C 16-byte chunks
+// per lane, C <= 8; {0, 0} when K does not fit.
+static void m1_shape(int K, int* T, int* C) {
+    *T = *C = 0;
+    const int chunks = K / 8;
+    for (int t = 64; t >= 8; t >>= 1)
+        if (chunks % t == 0 && chunks / t <= 8) {
+            *T = t;
+            *C = chunks / t;
+            return;
+        }
+}
+
+static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const float* bias, const float* residual,
+                     const OutDesc& od, int N, int K, int epilogue, const LinearExtras& ex, int T, int C) {
+    const int rpi = 64 / T;
+    const int ngroups = (N + rpi - 1) / rpi;
+    static const int max_blocks = env_int("GORCH_HIP_GEMV_M1_BLOCKS", 2048);
+    int blocks = (ngroups + 3) / 4;
+    if (blocks > max_blocks) blocks = max_blocks;
+#define GH_M1(TT, CC)                                                                                        \
+    if (T == TT && C == CC) {                                                                                \
+        if (ex.ln_g)                                                                                         \
+            hipLaunchKernelGGL((k_gemv_m1<TT, CC, true>), dim3(blocks), dim3(256), 0, s, x, W, bias, residual, \
+                               od, N, K, epilogue, ex);                                                      \
+        else                                                                                                 \
+            hipLaunchKernelGGL((k_gemv_m1<TT, CC, false>), dim3(blocks), dim3(256), 0, s, x, W, bias,         \
+                               residual, od, N, K, epilogue, ex);                                            \
+        count(CNT_GEMV);                                                                                     \
+        return check_launch("gemv_m1");                                                                      \
+    }
+    GH_M1(64, 1) GH_M1(64, 2) GH_M1(64, 3) GH_M1(64, 4) GH_M1(64, 5) GH_M1(64, 6) GH_M1(64, 7) GH_M1(64, 8)
+    GH_M1(32, 1) GH_M1(32, 3) GH_M1(32, 5) GH_M1(32, 7)
+    GH_M1(16, 1) GH_M1(16, 3) GH_M1(16, 5) GH_M1(16, 7)
+    GH_M1(8, 1) GH_M1(8, 3) GH_M1(8, 5) GH_M1(8, 7)
+#undef GH_M1
+    return -1;  // not instantiated: caller falls through
+}
+
+template <int MT>
+static int launch_valu_mt(hipStream_t s, const float* x, const uint16_t* W, const float* bias, const float* residual,
+                          const OutDesc& od, int M, int N, int K, int epilogue, const LinearExtras& ex, int T) {
+    const int rpi = 64 / T;
+    const int ngroups = (N + rpi - 1) / rpi;
+    static const int max_blocks = env_int("GORCH_HIP_GEMV_VALU_BLOCKS", 2048);
+    int blocks = (ngroups + 3) / 4;
+    if (blocks > max_blocks) blocks = max_blocks;
+    const size_t lds = (size_t)MT * K * sizeof(float);
+    switch (T) {
+        case 32:
+            hipLaunchKernelGGL((k_gemv_valu<MT, 32>), dim3(blocks), dim3(256), lds, s, x, W, bias, residual, od, M,
+                               N, K, epilogue, ex);
+            break;
+        case 16:
+            hipLaunchKernelGGL((k_gemv_valu<MT, 16>), dim3(blocks), dim3(256), lds, s, x, W, bias, residual, od, M,
+                               N, K, epilogue, ex);
+            break;
+        default:
+            hipLaunchKernelGGL((k_gemv_valu<MT, 8>), dim3(blocks), dim3(256), lds, s, x, W, bias, residual, od, M,
+                               N, K, epilogue, ex);
+            break;
+    }
+    count(CNT_GEMV);
+    return check_launch("gemv_valu");
+}
+
+// Lanes per row for the VALU GEMV: the largest of 32/16/8 dividing K/8;
+// 0 when K fits none (then the MFMA kernel runs).
+static int valu_lanes_per_row(int K) {
+    const int chunks = K / 8;
+    for (int t = 32; t >= 8; t >>= 1)
+        if (chunks % t == 0) return t;
+    return 0;
+}
+
 // Launch plan: NT weight tiles and NW K-splitting waves per block, chosen
 // from a sweep of the decode shapes (GPT-2 small and XL, M = 1..16) on
 // MI355X. GORCH_HIP_GEMV_NT / GORCH_HIP_GEMV_NW override them.
@@ -249,6 +552,24 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
             return GORCH_HIP_EUNSUPPORTED;
         }
         return launch_gemm_bf16w(s, x, W, bias, residual, od, M, N, K, epilogue, false);
+    }
+    static const int valu_max_m = env_int("GORCH_HIP_GEMV_VALU_MAX_M", 1);
+    static const int m1_on = env_int("GORCH_HIP_GEMV_M1", 1);
+    // M = 1: the register-activation kernel for narrow/medium N (lowest
+    // latency), the LDS-staged one for LM-head-sized N (more waves in flight).
+    if (M == 1 && valu_max_m >= 1 && m1_on && N < 16384) {
+        int T1, C1;
+        m1_shape(K, &T1, &C1);
+        if (T1) {
+            int rc = launch_m1(s, x, W, bias, residual, od, N, K, epilogue, ex, T1, C1);
+            if (rc >= 0) return rc;
+        }
+    }
+    const int T = valu_lanes_per_row(K);
+    if (M <= valu_max_m && T && (size_t)4 * K * sizeof(float) <= 64 * 1024) {
+        if (M == 1) return launch_valu_mt<1>(s, x, W, bias, residual, od, M, N, K, epilogue, ex, T);
+        if (M == 2) return launch_valu_mt<2>(s, x, W, bias, residual, od, M, N, K, epilogue, ex, T);
+        return launch_valu_mt<4>(s, x, W, bias, residual, od, M, N, K, epilogue, ex, T);
     }
     GemvPlan p = plan_gemv(M, N, K);
     int per = (K + p.nw - 1) / p.nw;
