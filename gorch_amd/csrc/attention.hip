@@ -41,13 +41,12 @@ __device__ float block_sum(float v, float* sh) {
 }
 
 
-constexpr int kAttnThreads = 256;
-
-__global__ __launch_bounds__(kAttnThreads) void k_attn_cached(AttnArgs a) {
+template <int NWV>
+__global__ __launch_bounds__(NWV * 64) void k_attn_cached(AttnArgs a) {
     extern __shared__ float sc[];  // [max visible keys]
     __shared__ __align__(16) float qs[256];
-    __shared__ float red[8];
-    __shared__ float pv[4][256];
+    __shared__ float red[16];
+    __shared__ float pv[NWV][256];
 
     const int h = blockIdx.x;
     const int row = blockIdx.y;
@@ -56,7 +55,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_cached(AttnArgs a) {
     const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
     const int T = a.causal ? pos + i + 1 : pos + a.new_seq;
     const int hd = a.hd;
-    const size_t base = ((size_t)b * a.max_seq) * a.dim + (size_t)h * hd;
+    // grouped-query attention: query head h reads KV head h / (heads / kv_heads)
+    const int kvh = a.kv_heads ? h / ((int)gridDim.x / a.kv_heads) : h;
+    const int kvd = a.kv_dim ? a.kv_dim : a.dim;
+    const size_t base = ((size_t)b * a.max_seq) * kvd + (size_t)kvh * hd;
     const float* K = a.kc + base;
     const float* V = a.vc + base;
 
@@ -71,11 +73,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_cached(AttnArgs a) {
     const int hd4 = hd >> 2;
     const float4* q4 = reinterpret_cast<const float4*>(qs);
     float lmax = -INFINITY;
-    for (int j0 = wave * 16; j0 < T; j0 += 64) {
+    for (int j0 = wave * 16; j0 < T; j0 += 16 * NWV) {
         const int j = j0 + kslot;
         float acc = 0.f;
         if (j < T) {
-            const float4* kr = reinterpret_cast<const float4*>(K + (size_t)j * a.dim);
+            const float4* kr = reinterpret_cast<const float4*>(K + (size_t)j * kvd);
 #pragma unroll 4
             for (int d4 = sub; d4 < hd4; d4 += 4) {
                 float4 kv = kr[d4];
@@ -100,10 +102,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_cached(AttnArgs a) {
         lsum += e;
     }
     const float sum = block_sum(lsum, red);
-    for (int j = threadIdx.x; j < T; j += blockDim.x) sc[j] = sc[j] / sum;
+    const float rs = 1.0f / sum;
+    for (int j = threadIdx.x; j < T; j += blockDim.x) sc[j] = a.recip ? sc[j] * rs : sc[j] / sum;
     __syncthreads();
 
-    // P.V: waves take keys j = wave, wave+4, ...; lanes take dims (one
+    // P.V: waves take keys j = wave, wave+NWV, ...; lanes take dims (one
     // coalesced 256-byte row per key); four independent accumulators keep
     // four rows in flight per lane.
     for (int d0 = 0; d0 < hd; d0 += 64) {
@@ -112,28 +115,35 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_cached(AttnArgs a) {
             const float* Vd = V + d;
             float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
             int j = wave;
-            for (; j + 12 < T; j += 16) {
-                a0 += sc[j] * Vd[(size_t)j * a.dim];
-                a1 += sc[j + 4] * Vd[(size_t)(j + 4) * a.dim];
-                a2 += sc[j + 8] * Vd[(size_t)(j + 8) * a.dim];
-                a3 += sc[j + 12] * Vd[(size_t)(j + 12) * a.dim];
+            for (; j + 3 * NWV < T; j += 4 * NWV) {
+                a0 += sc[j] * Vd[(size_t)j * kvd];
+                a1 += sc[j + NWV] * Vd[(size_t)(j + NWV) * kvd];
+                a2 += sc[j + 2 * NWV] * Vd[(size_t)(j + 2 * NWV) * kvd];
+                a3 += sc[j + 3 * NWV] * Vd[(size_t)(j + 3 * NWV) * kvd];
             }
-            for (; j < T; j += 4) a0 += sc[j] * Vd[(size_t)j * a.dim];
+            for (; j < T; j += NWV) a0 += sc[j] * Vd[(size_t)j * kvd];
             pv[wave][d] = (a0 + a1) + (a2 + a3);
         }
     }
     __syncthreads();
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-        float o = pv[0][d] + pv[1][d];
-        o = o + pv[2][d];
-        o = o + pv[3][d];
+        float o = pv[0][d];
+#pragma unroll
+        for (int w = 1; w < NWV; w++) o = o + pv[w][d];
         a.out[(size_t)row * a.dim + h * hd + d] = o;
     }
 }
 
+// 4 waves per (head, row) block when there are enough blocks to fill the
+// GPU; 16 waves when the visible context is long and blocks are few, so each
+// block keeps more of the KV stream in flight.
 int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
     size_t lds = (size_t)a.max_seq * sizeof(float);
-    hipLaunchKernelGGL(k_attn_cached, dim3(heads, rows), dim3(kAttnThreads), lds, s, a);
+    const int blocks = heads * rows;
+    if (blocks < 1024 && a.max_seq >= 128)
+        hipLaunchKernelGGL(k_attn_cached<16>, dim3(heads, rows), dim3(1024), lds, s, a);
+    else
+        hipLaunchKernelGGL(k_attn_cached<4>, dim3(heads, rows), dim3(256), lds, s, a);
     count(CNT_ATTENTION);
     return check_launch("attn_cached");
 }
@@ -196,8 +206,9 @@ extern "C" int gorch_hip_attention_cached(void* stream, const float* q, const fl
     GH_REQUIRE(q && k_cache && v_cache && out, "gorch_hip_attention_cached: null pointer");
     const int dim = heads * head_dim;
     GH_REQUIRE(((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0, "gorch_hip_attention_cached: cache must be 16-byte aligned");
+    // invScale = float32(1.0 / sqrtFloat32(float32(headDim))) (nn/attention.go:348)
     AttnArgs a{q, k_cache, v_cache, out, nullptr, pos_offset, new_seq, dim, head_dim, max_seq, dim, causal ? 1 : 0,
-               1.0f / sqrtf((float)head_dim)};
+               1.0f / (float)sqrt((double)head_dim)};
     return launch_attn_cached(stream_of(stream), a, heads, batch * new_seq);
 }
 
@@ -218,4 +229,24 @@ extern "C" int gorch_hip_softmax_rows(void* stream, float* x, int rows, int cols
     hipLaunchKernelGGL(k_softmax_rows, dim3(rows), dim3(256), 0, stream_of(stream), x, cols);
     count(CNT_ATTENTION);
     return check_launch("softmax_rows");
+}
+
+extern "C" int gorch_hip_gqa_attention_cached(void* stream, const float* q, const float* k_cache, const float* v_cache,
+                                              float* out, int batch, int new_seq, int pos_offset, int num_q,
+                                              int num_kv, int head_dim, int max_seq, int causal) {
+    GH_REQUIRE(batch > 0 && new_seq > 0 && num_q > 0 && num_kv > 0 && head_dim > 0 && max_seq > 0,
+               "gorch_hip_gqa_attention_cached: bad shape");
+    GH_REQUIRE(num_q % num_kv == 0, "gorch/nn: GQA numQueryHeads must be divisible by numKVHeads");
+    GH_REQUIRE(head_dim % 4 == 0 && head_dim <= 256,
+               "gorch_hip_gqa_attention_cached: head_dim must be a multiple of 4, <= 256");
+    GH_REQUIRE(pos_offset >= 0 && pos_offset + new_seq <= max_seq,
+               "gorch_hip_gqa_attention_cached: cached sequence length exceeds max_seq");
+    GH_REQUIRE(max_seq <= 16384, "gorch_hip_gqa_attention_cached: max_seq above 16384 is not supported");
+    GH_REQUIRE(q && k_cache && v_cache && out, "gorch_hip_gqa_attention_cached: null pointer");
+    GH_REQUIRE(((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0,
+               "gorch_hip_gqa_attention_cached: cache must be 16-byte aligned");
+    const int qdim = num_q * head_dim;
+    AttnArgs a{q, k_cache, v_cache, out, nullptr, pos_offset, new_seq, qdim, head_dim, max_seq, qdim, causal ? 1 : 0,
+               (float)(1.0 / sqrt((double)head_dim)), num_kv, num_kv * head_dim, 1};
+    return launch_attn_cached(stream_of(stream), a, num_q, batch * new_seq);
 }

@@ -128,6 +128,9 @@ struct AttnArgs {
     int pos_host;        // used when pos_dev is null
     int new_seq, dim, hd, max_seq, q_stride, causal;
     float scale;
+    int kv_heads;  // grouped-query attention: KV heads (0 = one per query head)
+    int kv_dim;    // cache row stride in floats (0 = dim)
+    int recip;     // normalise by multiplying with 1/sum (GQA) instead of dividing
 };
 int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows);
 

@@ -159,7 +159,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
                                          LinearExtras{}));
         }
         AttnArgs a{g->q, kc_layer(c, l), vc_layer(c, l), g->att, pos, 0, n, d, hd, c->capacity, d, 1,
-                   1.0f / sqrtf((float)hd)};
+                   1.0f / (float)sqrt((double)hd)};
         GH_TRY(launch_attn_cached(s, a, g->heads, rows));
         GH_TRY(launch_linear_bf16(s, g->att, w.wo, w.bo, g->x, g->x, rows, d, d, GORCH_HIP_EPI_NONE));
         if (fused) {

@@ -1,0 +1,68 @@
+// gqa.hip — grouped-query attention with a KV cache (GQA.forwardCached,
+// nn/gqa.go:259-363, with ProjectQKV :213-256) as a host-side composite of
+// the library's kernels, on one stream, no allocation (caller workspace):
+//   Q, K, V projections (bf16 Linears) -> optional per-head QK RMSNorm
+//   (Qwen3 qk-norm, applied before RoPE) -> RoPE on Q and on K at absolute
+//   positions (K rotated straight into the cache rows, V projected straight
+//   into them) -> grouped-query attention over the cache -> Wo Linear.
+// Activations stay token-major [seq, heads*hd]; the reference's permutes to
+// (heads, seq, hd) only change layout, not values.
+#include "common.h"
+
+namespace gh {
+int launch_rope_rows(hipStream_t s, const float* x, float* y, int rows, int heads, int hd, int start_pos,
+                     const float* cosT, const float* sinT, int neox);
+int launch_rmsnorm(hipStream_t s, const float* x, const float* g, float* y, int M, int N, float eps);
+}  // namespace gh
+
+using namespace gh;
+
+static size_t gqa_ws(int new_seq, int num_q, int num_kv, int hd) {
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    return al((size_t)new_seq * num_q * hd * 4) * 2 + al((size_t)new_seq * num_kv * hd * 4);
+}
+
+extern "C" size_t gorch_hip_gqa_workspace_size(const gorch_hip_gqa_weights* w, int new_seq) {
+    if (!w || new_seq <= 0) return 0;
+    return gqa_ws(new_seq, w->num_q, w->num_kv, w->head_dim);
+}
+
+extern "C" int gorch_hip_gqa_forward_cached(void* stream, const gorch_hip_gqa_weights* w, const float* x,
+                                            int new_seq, float* k_cache, float* v_cache, int pos_offset,
+                                            int max_seq, float* out, void* workspace, size_t workspace_bytes) {
+    GH_REQUIRE(w && x && k_cache && v_cache && out && new_seq > 0, "gorch_hip_gqa_forward_cached: bad arguments");
+    const int S = new_seq, nq = w->num_q, nkv = w->num_kv, hd = w->head_dim, d = w->dim;
+    GH_REQUIRE(nq > 0 && nkv > 0 && hd > 0 && d > 0, "gorch/nn: GQAConfig fields must be positive");
+    GH_REQUIRE(nq % nkv == 0, "gorch/nn: GQA NumQ must be divisible by NumKV");
+    GH_REQUIRE(pos_offset >= 0 && pos_offset + S <= max_seq, "gorch_hip_gqa_forward_cached: cache overflow");
+    GH_REQUIRE(w->wq && w->wk && w->wv && w->wo, "gorch_hip_gqa_forward_cached: null projection weight");
+    GH_REQUIRE(!w->rope_cos == !w->rope_sin, "gorch_hip_gqa_forward_cached: need both RoPE tables");
+    GH_REQUIRE(!w->rope_cos || pos_offset + S <= w->rope_max_seq, "gorch/nn: RoPE startPos+seqLen exceeds MaxSeq");
+    const size_t need = gqa_ws(S, nq, nkv, hd);
+    GH_REQUIRE(workspace && workspace_bytes >= need, "gorch_hip_gqa_forward_cached: workspace too small");
+    hipStream_t s = stream_of(stream);
+    const int qdim = nq * hd, kvdim = nkv * hd;
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    char* base = (char*)workspace;
+    float* q = (float*)base;
+    float* att = (float*)(base + al((size_t)S * qdim * 4));
+    float* kt = (float*)(base + 2 * al((size_t)S * qdim * 4));
+    float* krow = k_cache + (size_t)pos_offset * kvdim;
+    float* vrow = v_cache + (size_t)pos_offset * kvdim;
+
+    GH_TRY(launch_linear_bf16(s, x, w->wq, w->bq, nullptr, q, S, qdim, d, GORCH_HIP_EPI_NONE));
+    GH_TRY(launch_linear_bf16(s, x, w->wk, w->bk, nullptr, kt, S, kvdim, d, GORCH_HIP_EPI_NONE));
+    GH_TRY(launch_linear_bf16(s, x, w->wv, w->bv, nullptr, vrow, S, kvdim, d, GORCH_HIP_EPI_NONE));
+    if (w->q_norm) GH_TRY(launch_rmsnorm(s, q, w->q_norm, q, S * nq, hd, w->norm_eps));
+    if (w->k_norm) GH_TRY(launch_rmsnorm(s, kt, w->k_norm, kt, S * nkv, hd, w->norm_eps));
+    if (w->rope_cos) {
+        GH_TRY(launch_rope_rows(s, q, q, S * nq, nq, hd, pos_offset, w->rope_cos, w->rope_sin, w->rope_neox));
+        GH_TRY(launch_rope_rows(s, kt, krow, S * nkv, nkv, hd, pos_offset, w->rope_cos, w->rope_sin, w->rope_neox));
+    } else {
+        GH_TRY(check(hipMemcpyAsync(krow, kt, (size_t)S * kvdim * 4, hipMemcpyDeviceToDevice, s), "gqa k copy"));
+    }
+    AttnArgs a{q, k_cache, v_cache, att, nullptr, pos_offset, S, qdim, hd, max_seq, qdim, w->causal ? 1 : 0,
+               (float)(1.0 / sqrt((double)hd)), nkv, kvdim, 1};
+    GH_TRY(launch_attn_cached(s, a, nq, S));
+    return launch_linear_bf16(s, att, w->wo, w->bo, nullptr, out, S, d, qdim, GORCH_HIP_EPI_NONE);
+}

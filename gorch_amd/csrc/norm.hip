@@ -45,8 +45,10 @@ __global__ __launch_bounds__(256) void k_layernorm(const float* __restrict__ x, 
     }
 }
 
-__global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x, const float* __restrict__ g,
-                                                 float* __restrict__ y, int N, float eps) {
+// (also used in place by the GQA qk-norm: each thread rewrites only the
+// elements it read after the row's sum is complete)
+__global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* __restrict__ g, float* y, int N,
+                                                 float eps) {
     __shared__ double sh[4];
     const float* row = x + (size_t)blockIdx.x * N;
     float* out = y + (size_t)blockIdx.x * N;
@@ -67,6 +69,13 @@ int launch_layernorm(hipStream_t s, const float* x, const float* g, const float*
     return check_launch("layernorm");
 }
 
+int launch_rmsnorm(hipStream_t s, const float* x, const float* g, float* y, int M, int N, float eps) {
+    if (M == 0) return GORCH_HIP_OK;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(256), 0, s, x, g, y, N, eps);
+    count(CNT_NORM);
+    return check_launch("rmsnorm");
+}
+
 }  // namespace gh
 
 using namespace gh;
@@ -84,7 +93,5 @@ extern "C" int gorch_hip_rmsnorm(void* stream, const float* x, const float* gamm
     GH_REQUIRE(M >= 0 && N > 0, "gorch_hip_rmsnorm: bad shape");
     if (M == 0) return GORCH_HIP_OK;
     GH_REQUIRE(x && gamma && y, "gorch_hip_rmsnorm: null pointer");
-    hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(256), 0, stream_of(stream), x, gamma, y, N, eps);
-    count(CNT_NORM);
-    return check_launch("rmsnorm");
+    return launch_rmsnorm(stream_of(stream), x, gamma, y, M, N, eps);
 }

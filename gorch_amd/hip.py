@@ -65,6 +65,11 @@ SIGNATURES = {
     "gorch_hip_causal_softmax": (i32, [vp, vp, vp, i32, i32, i32, f32]),
     "gorch_hip_softmax_rows": (i32, [vp, vp, i32, i32]),
     "gorch_hip_argmax": (i32, [vp, vp, i32, i32, vp]),
+    "gorch_hip_rope_tables": (i32, [vp, i32, i32, f32, vp, vp]),
+    "gorch_hip_rope_apply": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, i32, i32, f32]),
+    "gorch_hip_gqa_attention_cached": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32]),
+    "gorch_hip_gqa_workspace_size": (C.c_size_t, [vp, i32]),
+    "gorch_hip_gqa_forward_cached": (i32, [vp, vp, vp, i32, vp, vp, i32, i32, vp, vp, C.c_size_t]),
     "gorch_hip_moe_workspace_size": (C.c_size_t, [i32, i32, i32, i32, i32]),
     "gorch_hip_moe_forward": (i32, [vp, vp, vp, i32, vp, vp, vp, vp, vp, C.c_size_t]),
     "gorch_hip_gpt_create": (vp, [vp]),
@@ -413,3 +418,82 @@ class MoE:
         _ok(lib().gorch_hip_moe_forward(_stream(), C.byref(self.s), _p(x), M, _p(logits), _p(out), _p(idx),
                                         _p(wts), ws.data_ptr(), ws.numel()))
         return out, idx, wts
+
+
+# ------------------------------------------------------------------ RoPE / GQA
+
+def rope_tables(head_dim: int, max_seq: int, base: float):
+    """NewRoPE's tables on the GPU: (cos, sin) [max_seq, head_dim/2]."""
+    import torch
+
+    c = torch.empty((max_seq, head_dim // 2), dtype=torch.float32, device="cuda")
+    s_ = torch.empty_like(c)
+    _ok(lib().gorch_hip_rope_tables(_stream(), head_dim, max_seq, base, _p(c), _p(s_)))
+    return c, s_
+
+
+def rope_apply(x, y, cos_t, sin_t, start_pos=0, neox=False, sign=1.0) -> None:
+    """RoPE.Apply over x [..., seq, head_dim] (y may be x)."""
+    seq, hd = x.shape[-2], x.shape[-1]
+    outer = x.numel() // (seq * hd)
+    _ok(lib().gorch_hip_rope_apply(_stream(), _p(x), _p(y), outer, seq, hd, start_pos, _p(cos_t), _p(sin_t),
+                                   cos_t.shape[0], int(neox), sign))
+
+
+def gqa_attention_cached(q, k_cache, v_cache, out, batch, new_seq, pos_offset, num_q, num_kv, head_dim, max_seq,
+                         causal=True) -> None:
+    _ok(lib().gorch_hip_gqa_attention_cached(_stream(), _p(q), _p(k_cache), _p(v_cache), _p(out), batch, new_seq,
+                                             pos_offset, num_q, num_kv, head_dim, max_seq, int(causal)))
+
+
+class _GQAW(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("dim", "num_q", "num_kv", "head_dim", "causal")] + [
+        ("norm_eps", C.c_float)] + [(n, vp) for n in (
+            "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo", "q_norm", "k_norm", "rope_cos", "rope_sin")] + [
+        ("rope_max_seq", C.c_int), ("rope_neox", C.c_int)]
+
+
+class GQA:
+    """gorch's nn.GQA (nn/gqa.go) with bf16 projections on the GPU. ``w`` is a
+    dict as gorch_amd.synthetic.gqa_weights builds it; the RoPE tables are
+    computed on the GPU (rope_base, rope_max_seq) when w['rope'] is set."""
+
+    def __init__(self, w: dict):
+        import numpy as np
+        import torch
+
+        def up(a):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a)
+            return torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).cuda()
+
+        self.w = w
+        self.t = {n: up(w.get(n)) for n in ("wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo", "q_norm", "k_norm")}
+        if w.get("rope"):
+            self.t["rope_cos"], self.t["rope_sin"] = rope_tables(w["head_dim"], w["rope_max_seq"], w["rope_base"])
+        s = _GQAW()
+        for n in ("dim", "num_q", "num_kv", "head_dim"):
+            setattr(s, n, w[n])
+        s.causal = int(w.get("causal", True))
+        s.norm_eps = w.get("norm_eps", 1e-6)
+        for n, t in self.t.items():
+            setattr(s, n, None if t is None else t.data_ptr())
+        s.rope_max_seq = w["rope_max_seq"] if w.get("rope") else 0
+        s.rope_neox = int(w.get("rope_neox", 0))
+        self.s = s
+        self.ws = None
+
+    def forward_cached(self, x, k_cache, v_cache, pos_offset):
+        """x [new_seq, dim] device; caches [capacity, num_kv*head_dim] device."""
+        import torch
+
+        S = x.shape[0]
+        n = lib().gorch_hip_gqa_workspace_size(C.byref(self.s), S)
+        if self.ws is None or self.ws.numel() < n:
+            self.ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+        out = torch.empty((S, self.w["dim"]), dtype=torch.float32, device="cuda")
+        _ok(lib().gorch_hip_gqa_forward_cached(_stream(), C.byref(self.s), _p(x), S, _p(k_cache), _p(v_cache),
+                                               pos_offset, k_cache.shape[0], _p(out), self.ws.data_ptr(),
+                                               self.ws.numel()))
+        return out

@@ -98,3 +98,25 @@ def moe_inputs(M=2048, dim=1024, ffn=4096, experts=8, top_k=2, seed=0, with_rout
         w["wr"] = bf16_normal(rng, (experts, dim))
         w["br"] = np.zeros(experts, np.float32)
     return x, logits, w
+
+
+def gqa_weights(dim=64, num_q=8, num_kv=2, head_dim=16, max_seq=64, seed=0, bias=True, qk_norm=True,
+                rope=True, base=10000.0):
+    """A GQAConfig-shaped module (nn/gqa.go:64-98) with bf16 Linear weights;
+    RoPE tables are left to the caller (``rope_base``/``rope_max_seq``)."""
+    rng = np.random.default_rng(seed)
+    qdim, kvdim = num_q * head_dim, num_kv * head_dim
+    w = {"dim": dim, "num_q": num_q, "num_kv": num_kv, "head_dim": head_dim, "causal": True,
+         "norm_eps": 1e-6,
+         "wq": bf16_normal(rng, (qdim, dim), 0.1), "wk": bf16_normal(rng, (kvdim, dim), 0.1),
+         "wv": bf16_normal(rng, (kvdim, dim), 0.1), "wo": bf16_normal(rng, (dim, qdim), 0.1)}
+    if bias:
+        for n, size in (("bq", qdim), ("bk", kvdim), ("bv", kvdim), ("bo", dim)):
+            w[n] = normal(rng, (size,), 0.05)
+    if qk_norm:
+        w["q_norm"] = (1 + normal(rng, (head_dim,), 0.1)).astype(np.float32)
+        w["k_norm"] = (1 + normal(rng, (head_dim,), 0.1)).astype(np.float32)
+    w["rope"] = bool(rope)
+    w["rope_base"] = base
+    w["rope_max_seq"] = max_seq
+    return w

@@ -150,6 +150,49 @@ int gorch_hip_softmax_rows(void* stream, float* x, int rows, int cols);
  * out: device int32 [rows]. */
 int gorch_hip_argmax(void* stream, const float* logits, int rows, int n, int* out);
 
+/* Rotary tables (NewRoPE, nn/rope.go:71-96): cos/sin [max_seq, head_dim/2]
+ * device f32, invFreq = f32(base^(-2i/hd)), theta = f64(f32(pos)*invFreq). */
+int gorch_hip_rope_tables(void* stream, int head_dim, int max_seq, float base, float* cos_t, float* sin_t);
+/* RoPE.Apply / RoPEApplyMetal (nn/rope.go:172-223, rope_metal.go:35-62):
+ * x, y [outer, seq_len, head_dim] (may alias); row (o, s) rotated at
+ * position start_pos + s; neox selects interleaved pairs; sign +1 forward,
+ * -1 inverse. max_seq is the tables' row count. */
+int gorch_hip_rope_apply(void* stream, const float* x, float* y, int outer, int seq_len, int head_dim,
+                         int start_pos, const float* cos_t, const float* sin_t, int max_seq, int neox, float sign);
+
+/* Grouped-query attention of new query rows against a cache (the
+ * per-KV-head loops of GQA.forwardCached, nn/gqa.go:308-352): q/out
+ * [batch*new_seq, num_q*head_dim]; caches [batch][max_seq][num_kv*head_dim]
+ * holding the (rotated) keys and values up to pos_offset+new_seq; query head
+ * h reads KV head h / (num_q/num_kv); softmax rows scaled by 1/sum. */
+int gorch_hip_gqa_attention_cached(void* stream, const float* q, const float* k_cache, const float* v_cache,
+                                   float* out, int batch, int new_seq, int pos_offset, int num_q, int num_kv,
+                                   int head_dim, int max_seq, int causal);
+
+/* GQA module (GQAConfig, nn/gqa.go:64-98), device pointers. Linear weights
+ * bf16 [out, in]: wq [num_q*hd, dim], wk/wv [num_kv*hd, dim], wo
+ * [dim, num_q*hd]; biases f32 or NULL (= zero, the Bias=false config);
+ * q_norm / k_norm: per-head RMSNorm gammas [head_dim] or NULL; rope tables
+ * [rope_max_seq, head_dim/2] or NULL (no RoPE). */
+typedef struct {
+    int dim, num_q, num_kv, head_dim, causal;
+    float norm_eps;
+    const uint16_t* wq; const float* bq;
+    const uint16_t* wk; const float* bk;
+    const uint16_t* wv; const float* bv;
+    const uint16_t* wo; const float* bo;
+    const float* q_norm; const float* k_norm;
+    const float* rope_cos; const float* rope_sin;
+    int rope_max_seq, rope_neox;
+} gorch_hip_gqa_weights;
+size_t gorch_hip_gqa_workspace_size(const gorch_hip_gqa_weights* w, int new_seq);
+/* GQA.ForwardCached (nn/gqa.go:259-363) for one sequence: x [new_seq, dim]
+ * -> out [new_seq, dim]; appends the new (rotated) K and V rows at
+ * pos_offset of the caches [max_seq, num_kv*head_dim]. */
+int gorch_hip_gqa_forward_cached(void* stream, const gorch_hip_gqa_weights* w, const float* x, int new_seq,
+                                 float* k_cache, float* v_cache, int pos_offset, int max_seq, float* out,
+                                 void* workspace, size_t workspace_bytes);
+
 /* ------------------------------------------------------------------------
  * MoE FFN layer (nn.MoE.Forward, nn/moe.go:130-182).
  * ---------------------------------------------------------------------- */

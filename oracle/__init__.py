@@ -71,6 +71,7 @@ def _load() -> C.CDLL:
         "orc_gpt_forward": (C.c_int, [vp, i32p, C.c_int, f32p]),
         "orc_generate_cached": (C.c_int, [vp, i32p, C.c_int, C.c_int, i32p, vp, vp]),
         "orc_moe_forward": (C.c_int, [vp, f32p, C.c_int, vp, f32p, vp, vp]),
+        "orc_gqa_forward_cached": (C.c_int, [vp, f32p, f32p, C.c_int, f32p, C.c_int, f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -407,3 +408,40 @@ def moe_forward(w: dict, x, logits=None):
     if rc != 0:
         raise ValueError("gorch/nn: MoE numExpertsPerToken out of range")
     return out, idx, wts
+
+
+# ---------------------------------------------------------------- GQA
+
+class _GQAWeights(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("dim", "num_q", "num_kv", "head_dim", "causal", "linear_bf16")] + [
+        ("norm_eps", C.c_float)] + [(n, C.c_void_p) for n in (
+            "wq", "wk", "wv", "wo", "bq", "bk", "bv", "bo", "q_norm", "k_norm", "rope_cos", "rope_sin")] + [
+        ("rope_max_seq", C.c_int), ("rope_neox", C.c_int)]
+
+
+def gqa_forward_cached(w: dict, k_cache, v_cache, pos_offset, x):
+    """nn/gqa.go:259-363. ``w``: dim, num_q, num_kv, head_dim, causal,
+    norm_eps, wq/wk/wv/wo (uint16 bf16 or f32), optional bq.. bo, q_norm,
+    k_norm, rope_cos/rope_sin (+ rope_neox). k_cache/v_cache are float32
+    [capacity, num_kv*head_dim] arrays updated in place."""
+    keep = []
+    s = _GQAWeights()
+    for n in ("dim", "num_q", "num_kv", "head_dim"):
+        setattr(s, n, w[n])
+    s.causal = int(w.get("causal", True))
+    s.linear_bf16 = int(w["wq"].dtype == np.uint16)
+    s.norm_eps = w.get("norm_eps", 1e-6)
+    for n in ("wq", "wk", "wv", "wo", "bq", "bk", "bv", "bo", "q_norm", "k_norm", "rope_cos", "rope_sin"):
+        a = w.get(n)
+        if a is not None:
+            a = np.ascontiguousarray(a)
+            keep.append(a)
+        setattr(s, n, _ptr(a))
+    s.rope_max_seq = 0 if w.get("rope_cos") is None else w["rope_cos"].shape[0]
+    s.rope_neox = int(w.get("rope_neox", 0))
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty((x.shape[0], w["dim"]), np.float32)
+    rc = lib.orc_gqa_forward_cached(C.byref(s), k_cache, v_cache, pos_offset, x, x.shape[0], out)
+    if rc != 0:
+        raise ValueError("gorch/nn: GQA numQueryHeads must be divisible by numKVHeads")
+    return out

@@ -634,6 +634,94 @@ int orc_generate_cached(const orc_gpt_weights* w, const int* prompt, int n_promp
 }
 
 /* ------------------------------------------------------------------ */
+/* GQA (nn/gqa.go:213-363)                                             */
+/* ------------------------------------------------------------------ */
+
+/* softmaxRowsAccelerated (nn/gqa.go:367-385): subtract the row max, exp in
+ * f32 (vForce), sum, then scale by 1/sum when the sum is positive. */
+static void softmax_rows_recip(float* buf, int rows, int cols) {
+    for (int r = 0; r < rows; r++) {
+        float* row = buf + (int64_t)r * cols;
+        float maxv = row[0];
+        for (int j = 1; j < cols; j++) if (row[j] > maxv) maxv = row[j];
+        for (int j = 0; j < cols; j++) row[j] = row[j] - maxv;
+        float sum = 0.0f;
+        for (int j = 0; j < cols; j++) { row[j] = expf(row[j]); sum += row[j]; }
+        if (sum > 0.0f) {
+            float inv = 1.0f / sum;
+            for (int j = 0; j < cols; j++) row[j] = row[j] * inv;
+        }
+    }
+}
+
+int orc_gqa_forward_cached(const orc_gqa_weights* w, float* k_cache, float* v_cache, int pos_offset,
+                           const float* x, int new_seq, float* out) {
+    const int S = new_seq, nq = w->num_q, nkv = w->num_kv, hd = w->head_dim, d = w->dim;
+    if (nq % nkv != 0) return -1;
+    const int g = nq / nkv, qdim = nq * hd, kvdim = nkv * hd, T = pos_offset + S;
+    float* q = (float*)malloc((size_t)S * qdim * sizeof(float));
+    float* k = (float*)malloc((size_t)S * kvdim * sizeof(float));
+    float* v = (float*)malloc((size_t)S * kvdim * sizeof(float));
+    /* ProjectQKV (:213-256): projections, per-head RMSNorm, RoPE on Q, K */
+    orc_linear(x, S, d, w->wq, w->linear_bf16, w->bq, qdim, q);
+    orc_linear(x, S, d, w->wk, w->linear_bf16, w->bk, kvdim, k);
+    orc_linear(x, S, d, w->wv, w->linear_bf16, w->bv, kvdim, v);
+    if (w->q_norm) orc_rmsnorm(q, S * nq, hd, w->q_norm, w->norm_eps, q);
+    if (w->k_norm) orc_rmsnorm(k, S * nkv, hd, w->k_norm, w->norm_eps, k);
+    /* (seq, heads, hd) -> (heads, seq, hd) */
+    float* qH = (float*)malloc((size_t)S * qdim * sizeof(float));
+    float* kH = (float*)malloc((size_t)S * kvdim * sizeof(float));
+    for (int s = 0; s < S; s++) {
+        for (int h = 0; h < nq; h++)
+            memcpy(qH + ((int64_t)h * S + s) * hd, q + (int64_t)s * qdim + h * hd, (size_t)hd * sizeof(float));
+        for (int h = 0; h < nkv; h++)
+            memcpy(kH + ((int64_t)h * S + s) * hd, k + (int64_t)s * kvdim + h * hd, (size_t)hd * sizeof(float));
+    }
+    if (w->rope_cos) {
+        orc_rope_apply(qH, qH, nq, S, hd, pos_offset, w->rope_cos, w->rope_sin, w->rope_neox, 1.0f);
+        orc_rope_apply(kH, kH, nkv, S, hd, pos_offset, w->rope_cos, w->rope_sin, w->rope_neox, 1.0f);
+    }
+    /* append rotated K and V rows (token, kvDim) at pos_offset (:292-295) */
+    for (int s = 0; s < S; s++) {
+        for (int h = 0; h < nkv; h++)
+            memcpy(k_cache + ((int64_t)(pos_offset + s)) * kvdim + h * hd, kH + ((int64_t)h * S + s) * hd,
+                   (size_t)hd * sizeof(float));
+        memcpy(v_cache + ((int64_t)(pos_offset + s)) * kvdim, v + (int64_t)s * kvdim, (size_t)kvdim * sizeof(float));
+    }
+    /* per KV head: scores = invScale * qBlock kHead^T, mask, softmax, @ vHead (:308-352) */
+    float invScale = (float)(1.0 / sqrt((double)hd));
+    float* kHead = (float*)malloc((size_t)T * hd * sizeof(float));
+    float* vHead = (float*)malloc((size_t)T * hd * sizeof(float));
+    float* scores = (float*)malloc((size_t)g * S * T * sizeof(float));
+    float* attnOut = (float*)malloc((size_t)S * qdim * sizeof(float));
+    for (int kv = 0; kv < nkv; kv++) {
+        for (int j = 0; j < T; j++) {
+            memcpy(kHead + (int64_t)j * hd, k_cache + (int64_t)j * kvdim + kv * hd, (size_t)hd * sizeof(float));
+            memcpy(vHead + (int64_t)j * hd, v_cache + (int64_t)j * kvdim + kv * hd, (size_t)hd * sizeof(float));
+        }
+        const float* qBlock = qH + (int64_t)kv * g * S * hd;
+        orc_sgemm(0, 1, g * S, T, hd, qBlock, kHead, scores);
+        for (int64_t i = 0; i < (int64_t)g * S * T; i++) scores[i] = invScale * scores[i];
+        if (w->causal && S > 1) {
+            for (int r = 0; r < g * S; r++) {
+                int absPos = pos_offset + r % S;
+                for (int j = absPos + 1; j < T; j++) scores[(int64_t)r * T + j] = -INFINITY;
+            }
+        }
+        softmax_rows_recip(scores, g * S, T);
+        orc_sgemm(0, 0, g * S, hd, T, scores, vHead, attnOut + (int64_t)kv * g * S * hd);
+    }
+    /* (heads, seq, hd) -> (seq, heads*hd), then Wo */
+    float* concat = (float*)malloc((size_t)S * qdim * sizeof(float));
+    for (int h = 0; h < nq; h++)
+        for (int s = 0; s < S; s++)
+            memcpy(concat + (int64_t)s * qdim + h * hd, attnOut + ((int64_t)h * S + s) * hd, (size_t)hd * sizeof(float));
+    orc_linear(concat, S, qdim, w->wo, w->linear_bf16, w->bo, d, out);
+    free(q); free(k); free(v); free(qH); free(kH); free(kHead); free(vHead); free(scores); free(attnOut); free(concat);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
 /* MoE (nn/moe.go:130-182, softmaxRows :247-268)                       */
 /* ------------------------------------------------------------------ */
 

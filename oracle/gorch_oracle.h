@@ -123,6 +123,26 @@ int orc_gpt_forward(const orc_gpt_weights* w, const int* ids, int n, float* logi
 int orc_generate_cached(const orc_gpt_weights* w, const int* prompt, int n_prompt,
                         int max_new, int* out_ids, float* step_logits, float* gaps);
 
+/* ---- GQA with KV cache (nn/gqa.go:213-363) ----
+ * Linear weights [out, in] (bf16 when linear_bf16, else f32), biases
+ * nullable (= zero); q_norm/k_norm per-head RMSNorm gammas or NULL; RoPE
+ * tables [rope_max_seq, head_dim/2] or NULL. */
+typedef struct {
+    int dim, num_q, num_kv, head_dim, causal, linear_bf16;
+    float norm_eps;
+    const void *wq, *wk, *wv, *wo;
+    const float *bq, *bk, *bv, *bo;
+    const float *q_norm, *k_norm;
+    const float *rope_cos, *rope_sin;
+    int rope_max_seq, rope_neox;
+} orc_gqa_weights;
+/* GQA.ForwardCached: x [new_seq, dim] -> out [new_seq, dim]; the caches
+ * [>= pos_offset+new_seq, num_kv*head_dim] receive the new rows at
+ * pos_offset (the reference appends; rows before pos_offset are the
+ * existing cache). */
+int orc_gqa_forward_cached(const orc_gqa_weights* w, float* k_cache, float* v_cache, int pos_offset,
+                           const float* x, int new_seq, float* out);
+
 /* ---- MoE (nn/moe.go:130-182) ----
  * x [M, dim]; router Linear [E, dim] (wr may be null when `logits` is given:
  * injected gate logits [M, E]); expert e: wgate[e], wup[e] [ffn, dim],

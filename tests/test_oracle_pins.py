@@ -404,3 +404,57 @@ def test_attention_cached_vs_f64():
     # one visible key: the output is that key's value row (closed form)
     one = orc.attention_cached(q[:1], K[:1], V[:1], 0, heads, True)
     assert np.allclose(one, V[:1], atol=1e-7)
+
+
+def _np_gqa(w, kc, vc, pos, x, cos_t, sin_t):
+    """Independent float64 GQA.ForwardCached."""
+    f = lambda a: hb.bf16_to_f32(a).astype(np.float64) if a.dtype == np.uint16 else a.astype(np.float64)
+    S, nq, nkv, hd = x.shape[0], w["num_q"], w["num_kv"], w["head_dim"]
+    g = nq // nkv
+    xd = x.astype(np.float64)
+    q = xd @ f(w["wq"]).T + w.get("bq", 0)
+    k = xd @ f(w["wk"]).T + w.get("bk", 0)
+    v = xd @ f(w["wv"]).T + w.get("bv", 0)
+    q = q.reshape(S, nq, hd)
+    k = k.reshape(S, nkv, hd)
+    if "q_norm" in w:
+        q = q / np.sqrt((q ** 2).mean(-1, keepdims=True) + w["norm_eps"]) * w["q_norm"]
+        k = k / np.sqrt((k ** 2).mean(-1, keepdims=True) + w["norm_eps"]) * w["k_norm"]
+    if cos_t is not None:
+        half = hd // 2
+        inv = np.float32(w["rope_base"]) ** (-(2 * np.arange(half)) / hd)
+        theta = ((pos + np.arange(S))[:, None] * inv[None, :].astype(np.float64))[:, None, :]
+
+        def rot(t):
+            z = (t[..., :half] + 1j * t[..., half:]) * np.exp(1j * theta)
+            return np.concatenate([z.real, z.imag], -1)
+        q, k = rot(q), rot(k)
+    K = np.concatenate([kc[:pos].reshape(pos, nkv, hd).astype(np.float64), k])
+    V = np.concatenate([vc[:pos].reshape(pos, nkv, hd).astype(np.float64), v.reshape(S, nkv, hd)])
+    att = np.zeros((S, nq, hd))
+    for h in range(nq):
+        s = q[:, h] @ K[:, h // g].T / math.sqrt(hd)
+        for i in range(S):
+            s[i, pos + i + 1:] = -np.inf
+        att[:, h] = scipy.special.softmax(s, axis=1) @ V[:, h // g]
+    return att.reshape(S, nq * hd) @ f(w["wo"]).T + w.get("bo", 0), K, V
+
+
+@pytest.mark.parametrize("qk_norm,rope,bias", [(True, True, True), (False, False, False), (False, True, True)])
+def test_gqa_forward_cached_vs_f64(qk_norm, rope, bias):
+    w = syn.gqa_weights(seed=26, qk_norm=qk_norm, rope=rope, bias=bias)
+    cos_t, sin_t = orc.rope_tables(w["head_dim"], w["rope_max_seq"], w["rope_base"]) if rope else (None, None)
+    if rope:
+        w["rope_cos"], w["rope_sin"] = cos_t, sin_t
+    rng = np.random.default_rng(27)
+    kvdim = w["num_kv"] * w["head_dim"]
+    kc = np.zeros((20, kvdim), np.float32)
+    vc = np.zeros((20, kvdim), np.float32)
+    x0 = rng.standard_normal((5, w["dim"])).astype(np.float32)
+    orc.gqa_forward_cached(w, kc, vc, 0, x0)            # prefill 5 tokens
+    x1 = rng.standard_normal((3, w["dim"])).astype(np.float32)
+    got = orc.gqa_forward_cached(w, kc, vc, 5, x1)      # 3 more (staircase mask)
+    ref, K, V = _np_gqa(w, kc, vc, 5, x1, cos_t, sin_t)
+    assert np.max(np.abs(got - ref)) < 1e-4 * np.max(np.abs(ref))
+    assert np.max(np.abs(kc[:8] - K.reshape(8, kvdim))) < 1e-4
+    assert np.max(np.abs(vc[:8] - V.reshape(8, kvdim))) < 1e-4
