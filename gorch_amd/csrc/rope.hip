@@ -8,7 +8,8 @@
 // (a*c - b*s, a*s + b*c), the Llama half-split pairing (x[i], x[i+hd/2]) or
 // the NeoX interleaved one (x[2i], x[2i+1]). Products and sums are rounded
 // separately (no fused multiply-add), exactly as the reference's statements
-// read, so with equal tables the GPU result is bit-identical.
+// read (contraction is switched off in rotate_pair), so with equal tables the
+// GPU result is bit-identical to that unfused order.
 #include "common.h"
 
 namespace gh {
@@ -28,11 +29,12 @@ __global__ void k_rope_tables(int hd, int max_seq, float base, float* cosT, floa
 
 __device__ __forceinline__ void rotate_pair(const float* x, float* y, int64_t row_off, int i, int half, int neox,
                                             float c, float si) {
+#pragma clang fp contract(off)
     const int ia = neox ? 2 * i : i;
     const int ib = neox ? 2 * i + 1 : half + i;
     const float a = x[row_off + ia], b = x[row_off + ib];
-    y[row_off + ia] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, si));
-    y[row_off + ib] = __fadd_rn(__fmul_rn(a, si), __fmul_rn(b, c));
+    y[row_off + ia] = a * c - b * si;
+    y[row_off + ib] = a * si + b * c;
 }
 
 // Reference layout (outer, seq, hd): row t = (o, s) is at position

@@ -83,8 +83,6 @@ def test_gqa_attention_vs_f64(gpu, nq, nkv, S, pos):
 def _run(gpu, w, chunks, cap=24):
     kvdim = w["num_kv"] * w["head_dim"]
     ow = dict(w)
-    if w.get("rope"):
-        ow["rope_cos"], ow["rope_sin"] = orc.rope_tables(w["head_dim"], w["rope_max_seq"], w["rope_base"])
     m = gpu.GQA(w)
     if w.get("rope"):  # the oracle uses the GPU's tables so the check isolates the module
         ow["rope_cos"], ow["rope_sin"] = host(m.t["rope_cos"]), host(m.t["rope_sin"])
@@ -111,7 +109,7 @@ def test_gqa_module_vs_oracle(gpu, qk_norm, rope, bias):
 
 
 def test_gqa_qwen3_shaped_decode(gpu):
-    """Qwen3-0.6B attention shape (the SURVEY §8f GQA path): d 1024, 16 query
+    """Qwen3-0.6B attention shape: d 1024, 16 query
     heads x 128, 8 KV heads, qk-norm, RoPE base 1e6; 32-token prefill then
     two decode steps."""
     w = syn.gqa_weights(dim=1024, num_q=16, num_kv=8, head_dim=128, max_seq=128, seed=7, bias=False,
