@@ -33,7 +33,12 @@ struct LinearExtras {
     float ln_eps = 1e-5f;
     unsigned long long* argmax_key = nullptr;
     long long x_stride = 0;  // activation row stride in elements (0 = K)
+    float* ws = nullptr;     // split-K partials (nullptr: the stream's own buffer)
+    size_t ws_bytes = 0;
 };
+// Per-(device, stream) scratch for split-K partials; nullptr when it would
+// have to grow during stream capture or the allocation fails.
+void* stream_workspace(hipStream_t s, size_t bytes);
 int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                        const float* residual, float* y, int M, int N, int K, int epilogue);
 int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, const float* bias,

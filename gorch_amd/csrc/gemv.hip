@@ -20,17 +20,23 @@
 // split across blocks: on gfx950 the agent-scope fence a cross-block
 // reduction needs writes back the L2 and costs tens of microseconds, while
 // a 16-wave block over a narrow N still keeps enough loads in flight.
+#include <algorithm>
+
 #include "common.h"
 
 namespace gh {
 
 // NW waves per block split K; NT 16-row weight tiles per block; U k-steps
 // of loads issued per wave before their MFMAs.
-template <int NT, int NW, int U>
+template <int NT, int NW, int U, bool LX>
 __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
     const float* __restrict__ x, const uint16_t* __restrict__ W, const float* __restrict__ bias,
     const float* residual, OutDesc od, int M, int N, int K, int kw, int epilogue, LinearExtras ex) {
     __shared__ floatx4 red[NW][NT][64];
+    // LX: per-wave exchange buffer; the weight rows are read 16 lanes per row
+    // (256 contiguous bytes per row per instruction) and re-read from LDS in
+    // the MFMA B layout. Row pitch 17 x 16 B keeps both sides conflict-free.
+    __shared__ uint4 xw[LX ? NW : 1][LX ? NT * 16 : 1][17];
     __shared__ float s_mean[16], s_inv[16];
     __shared__ unsigned long long s_key[16];
 
@@ -98,16 +104,36 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
     for (int k0 = kb; k0 < ke; k0 += 32 * U) {
         uint4 wv[U][NT];
         float f[U][8];
+        if constexpr (LX) {
+            static_assert(U == 4, "LX stages 128 k-values (4 k-steps) per iteration");
+            uint4 v[4 * NT];
+            const int sub = lane & 15;
+            const int kk = k0 + 8 * sub;
+#pragma unroll
+            for (int j = 0; j < 4 * NT; j++) {
+                const int n = n0 + 4 * j + (lane >> 4);
+                v[j] = (n < N && kk < ke) ? *reinterpret_cast<const uint4*>(W + (size_t)n * K + kk)
+                                          : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < 4 * NT; j++) xw[wave][4 * j + (lane >> 4)][sub] = v[j];
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int t = 0; t < NT; t++) wv[u][t] = xw[wave][16 * t + r][4 * u + g];
+        }
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int kc = k0 + 32 * u + 8 * g;
             const bool k_ok = kc < ke;
+            if constexpr (!LX) {
 #pragma unroll
-            for (int t = 0; t < NT; t++) {
-                if (k_ok && wrow_ok[t])
-                    wv[u][t] = *reinterpret_cast<const uint4*>(wrow[t] + kc);
-                else
-                    wv[u][t] = make_uint4(0, 0, 0, 0);
+                for (int t = 0; t < NT; t++) {
+                    if (k_ok && wrow_ok[t])
+                        wv[u][t] = *reinterpret_cast<const uint4*>(wrow[t] + kc);
+                    else
+                        wv[u][t] = make_uint4(0, 0, 0, 0);
+                }
             }
             if (k_ok && arow_ok) {
                 float4 a0 = *reinterpret_cast<const float4*>(xrow + kc);
@@ -409,6 +435,253 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
     }
 }
 
+// ---------------------------------------------------------------------------
+// Multi-row GEMV for 2 <= M <= 16 over wide N (LM-head class, >= 1024
+// 16-row weight tiles).
+//
+// Work is (16-row weight tile, K slice). The grid is S slices x bps blocks
+// of NW waves (bps ~ 256 / S, so every CU streams about the same number of
+// tiles); a block owns one slice and its waves take the tiles t = b +
+// bps * (w + NW * i). The block stages its slice of the activations once
+// in LDS, already split into bf16 hi/lo in the MFMA A layout ([k-step]
+// [k-chunk g][row r], 16 bytes each; one conflict-free LDS read per
+// k-step): loading A from global memory per k-step instead spends the
+// vector-memory slots the weight stream needs and halves its bandwidth on
+// MI355X. B fragments are read straight from HBM with 16-byte loads, ST
+// 128-wide stages per batch; the first batch is issued before the staging.
+//
+// With one slice (S == 1) each wave applies the epilogue itself. With
+// several, each slice's tile is published to flagged 64-bit slots (flag
+// word | f32 bits) with device-scope atomic stores, a per-tile arrival
+// counter picks the last slice to finish, and that wave reads the slots in
+// slice order (atomic loads; a slot not yet flagged is read again, at most
+// kSlotSpins times) and clears them, so the sum order is fixed and no
+// second kernel or memory fence is needed. Counters and slots are left
+// zeroed for the next launch on the stream.
+constexpr int kSlotSpins = 1 << 16;
+
+// LayerNorm statistics (nn/layernorm.go:61-91) in f64 over full rows.
+template <int NW>
+__device__ void mt_ln_stats(const float* x, long long xs, int M, int K, float eps, float* s_mean, float* s_inv) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int rr = wave; rr < M; rr += NW) {
+        const float* row = x + (size_t)rr * xs;
+        double s1 = 0.0;
+        for (int k = 4 * lane; k < K; k += 256) {
+            float4 a = *reinterpret_cast<const float4*>(row + k);
+            s1 += (double)a.x + (double)a.y + (double)a.z + (double)a.w;
+        }
+        const double mean = wave_sum_d(s1) / (double)K;
+        double s2 = 0.0;
+        for (int k = 4 * lane; k < K; k += 256) {
+            float4 a = *reinterpret_cast<const float4*>(row + k);
+            double d0 = (double)a.x - mean, d1 = (double)a.y - mean, d2 = (double)a.z - mean, d3 = (double)a.w - mean;
+            s2 += d0 * d0 + d1 * d1 + d2 * d2 + d3 * d3;
+        }
+        const double var = wave_sum_d(s2) / (double)K;
+        if (lane == 0) {
+            s_mean[rr] = (float)mean;
+            s_inv[rr] = (float)(1.0 / sqrt(var + (double)eps));
+        }
+    }
+}
+
+// Stage x[0..M)[kb..ke) into LDS as bf16 hi/lo A fragments (LayerNorm
+// applied first when fused): entry ((k-step * 4 + g) * mr + r) holds
+// x[r][kb + 32*kstep + 8*g .. +8] for r < mr (M rounded up to 4, 8 or 16);
+// rows >= M and k >= ke are zero.
+template <int NW>
+__device__ void mt_stage_x(const float* x, long long xs, int M, int mr, int kb, int ke, int nst,
+                           const LinearExtras& ex, const float* s_mean, const float* s_inv, uint4* xh, uint4* xl) {
+    for (int i = threadIdx.x; i < nst * 16 * mr; i += NW * 64) {
+        const int rr = i % mr, gg = (i / mr) & 3, kst = i / (4 * mr);
+        const int k = kb + 32 * kst + 8 * gg;
+        float f[8];
+        if (rr < M && k < ke) {
+            const float* src = x + (size_t)rr * xs + k;
+            const float4 a0 = *reinterpret_cast<const float4*>(src);
+            const float4 a1 = *reinterpret_cast<const float4*>(src + 4);
+            f[0] = a0.x; f[1] = a0.y; f[2] = a0.z; f[3] = a0.w;
+            f[4] = a1.x; f[5] = a1.y; f[6] = a1.z; f[7] = a1.w;
+            if (ex.ln_g) {
+                const float mu = s_mean[rr], inv = s_inv[rr];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float normalized = (f[e] - mu) * inv;
+                    f[e] = normalized * ex.ln_g[k + e] + ex.ln_b[k + e];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) f[e] = 0.f;
+        }
+        bf16x8 hi, lo;
+        split_hi_lo(f, hi, lo);
+        xh[i] = __builtin_bit_cast(uint4, hi);
+        xl[i] = __builtin_bit_cast(uint4, lo);
+    }
+}
+
+// A fragments of k-step ks for lane (r, g); zero for r >= MR.
+template <int MR>
+__device__ __forceinline__ void mt_a(const uint4* xh, const uint4* xl, int ks, int g, int r, bf16x8& hi,
+                                     bf16x8& lo) {
+    if constexpr (MR == 16) {
+        const int ai = (ks * 4 + g) * 16 + r;
+        hi = __builtin_bit_cast(bf16x8, xh[ai]);
+        lo = __builtin_bit_cast(bf16x8, xl[ai]);
+    } else {
+        const bool ok = r < MR;
+        const int ai = (ks * 4 + g) * MR + (ok ? r : 0);
+        const uint4 h = xh[ai], l = xl[ai];
+        const uint4 z = make_uint4(0, 0, 0, 0);
+        hi = __builtin_bit_cast(bf16x8, ok ? h : z);
+        lo = __builtin_bit_cast(bf16x8, ok ? l : z);
+    }
+}
+
+// Finish tile ct: combine K slices when there are several (returns false
+// on every wave but the last slice's), then bias, GELU, residual, output
+// and argmax. acc: rows 4g..4g+3 of column 16*ct + r.
+__device__ bool mt_finish(floatx4& acc, int ct, int split, int nsplit, int M, int N, const float* bias,
+                          const float* residual, const OutDesc& od, int epilogue, const LinearExtras& ex,
+                          unsigned long long* slots, unsigned int* counters, unsigned long long* s_key) {
+    const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+    if (nsplit > 1) {
+        unsigned long long* my = slots + ((size_t)ct * nsplit + split) * 256;
+#pragma unroll
+        for (int v4 = 0; v4 < 4; v4++)
+            if (4 * g + v4 < M)
+                __hip_atomic_store(&my[v4 * 64 + lane], (1ull << 32) | (unsigned long long)__float_as_uint(acc[v4]),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned int prev = 0;
+        if (lane == 0) prev = atomicAdd(&counters[ct], 1u);
+        prev = __shfl(prev, 0, 64);
+        if (prev != (unsigned int)(nsplit - 1)) return false;
+        if (lane == 0) __hip_atomic_store(&counters[ct], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        floatx4 tot = {0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < nsplit; q++) {
+            unsigned long long* sl = slots + ((size_t)ct * nsplit + q) * 256;
+            unsigned long long got[4];
+#pragma unroll
+            for (int v4 = 0; v4 < 4; v4++)
+                got[v4] = 4 * g + v4 < M
+                              ? __hip_atomic_load(&sl[v4 * 64 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                              : (1ull << 32);
+#pragma unroll
+            for (int v4 = 0; v4 < 4; v4++) {
+                int spins = 0;
+                while (!(got[v4] >> 32) && ++spins < kSlotSpins)
+                    got[v4] = __hip_atomic_load(&sl[v4 * 64 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                tot[v4] += (got[v4] >> 32) ? __uint_as_float((unsigned int)got[v4]) : __builtin_nanf("");
+                if (4 * g + v4 < M)
+                    __hip_atomic_store(&sl[v4 * 64 + lane], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        acc = tot;
+    }
+    const int on = ct * 16 + r;
+    if (on < N) {
+#pragma unroll
+        for (int v4 = 0; v4 < 4; v4++) {
+            const int om = 4 * g + v4;
+            if (om >= M) break;
+            float sum = acc[v4];
+            if (bias) sum = sum + bias[on];
+            if (epilogue == GORCH_HIP_EPI_GELU) sum = gelu_tanh(sum);
+            if (residual) sum = residual[(size_t)om * N + on] + sum;
+            *od.at(om, on) = sum;
+            if (ex.argmax_key) {
+                if (nsplit > 1)
+                    atomicMax(&ex.argmax_key[om], argmax_pack(sum, on));
+                else
+                    atomicMax(&s_key[om], argmax_pack(sum, on));
+            }
+        }
+    }
+    return true;
+}
+
+template <int NW, int ST, int MR>
+__global__ __launch_bounds__(NW * 64) void k_gemv_mt(
+    const float* __restrict__ x, const uint16_t* __restrict__ W, const float* __restrict__ bias,
+    const float* residual, OutDesc od, int M, int N, int K, int kspan, int bps, int epilogue, LinearExtras ex,
+    unsigned long long* slots, unsigned int* counters) {
+    constexpr int mr = MR;
+    extern __shared__ uint4 smem[];
+    __shared__ float s_mean[16], s_inv[16];
+    __shared__ unsigned long long s_key[16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int nsplit = gridDim.x / bps;
+    const int split = blockIdx.x % nsplit, bidx = blockIdx.x / nsplit;
+    const int kb = split * kspan;
+    const int ke = min(K, kb + kspan);
+    const int nst = (ke - kb + 127) >> 7;  // 128-wide stages in the slice
+    uint4* xh = smem;
+    uint4* xl = smem + nst * 16 * mr;
+    const long long xs = ex.x_stride ? ex.x_stride : K;
+    const int ntiles = (N + 15) >> 4;
+
+    const int nbat = (nst + ST - 1) / ST;  // load batches per tile
+    const int tstride = bps * NW;
+
+    uint4 v[ST][4];
+    auto load = [&](int t, int bat) {
+#pragma unroll
+        for (int q = 0; q < ST; q++) {
+            const int st = bat * ST + q;
+            const int n = t * 16 + r;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int k = kb + 128 * st + 32 * j + 8 * g;
+                v[q][j] = (st < nst && n < N && k < ke) ? *reinterpret_cast<const uint4*>(W + (size_t)n * K + k)
+                                                       : make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    int t = bidx + bps * wave;
+    if (t < ntiles) load(t, 0);  // the weight stream starts before the staging
+
+    if (ex.ln_g) {
+        mt_ln_stats<NW>(x, xs, M, K, ex.ln_eps, s_mean, s_inv);
+        __syncthreads();
+    }
+    if (ex.argmax_key && threadIdx.x < 16) s_key[threadIdx.x] = 0ull;
+    mt_stage_x<NW>(x, xs, M, mr, kb, ke, nst, ex, s_mean, s_inv, xh, xl);
+    __syncthreads();
+
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    // each wave walks its own tiles; the first batch was issued before
+    // the staging, later ones overlap the other waves' MFMAs
+    bool first = true;
+    for (; t < ntiles; t += tstride) {
+        for (int b0 = 0; b0 < nbat; b0++) {
+            if (!first) load(t, b0);
+            first = false;
+#pragma unroll
+            for (int q = 0; q < ST; q++) {
+                const int st = b0 * ST + q;
+                if (st >= nst) break;
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    bf16x8 ah, al;
+                    mt_a<MR>(xh, xl, 4 * st + u, g, r, ah, al);
+                    const bf16x8 bb = __builtin_bit_cast(bf16x8, v[q][u]);
+                    acc = mfma16x16x32(ah, bb, acc);
+                    acc = mfma16x16x32(al, bb, acc);
+                }
+            }
+        }
+        mt_finish(acc, t, split, nsplit, M, N, bias, residual, od, epilogue, ex, slots, counters, s_key);
+        acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (ex.argmax_key && nsplit == 1) {
+        __syncthreads();
+        if (threadIdx.x < 16 && (int)threadIdx.x < M) atomicMax(&ex.argmax_key[threadIdx.x], s_key[threadIdx.x]);
+    }
+}
+
 // (T, C) for the register-x M = 1 kernel: T lanes per row, C 16-byte chunks
 // per lane, C <= 8; {0, 0} when K does not fit.
 static void m1_shape(int K, int* T, int* C) {
@@ -446,6 +719,87 @@ static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const flo
     GH_M1(8, 1) GH_M1(8, 3) GH_M1(8, 5) GH_M1(8, 7)
 #undef GH_M1
     return -1;  // not instantiated: caller falls through
+}
+
+template <int NW, int ST, int MR>
+static int launch_mt_t(hipStream_t s, dim3 grid, size_t lds, const float* x, const uint16_t* W, const float* bias,
+                       const float* residual, const OutDesc& od, int M, int N, int K, int kspan, int bps,
+                       int epilogue, const LinearExtras& ex, unsigned long long* slots, unsigned int* counters) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        GH_TRY(check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_mt<NW, ST, MR>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, 136 * 1024),
+                     "gemv_mt attribute"));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((k_gemv_mt<NW, ST, MR>), grid, dim3(NW * 64), lds, s, x, W, bias, residual, od, M, N,
+                       K, kspan, bps, epilogue, ex, slots, counters);
+    return GORCH_HIP_OK;
+}
+
+struct MtPlan {
+    int nw, st, splits, kst, bps, mr;
+};
+
+// LDS for the staged activation slice: 64 KB, two 16-wave blocks per CU.
+constexpr int kMtLds = 64 * 1024;
+
+// Launch plan for the multi-row GEMV: K slices only when the activations
+// exceed the LDS budget; GORCH_HIP_MT_{NW,ST,S,BPS} override.
+static MtPlan plan_mt(int M, int N, int K) {
+    static const int nw_env = env_int("GORCH_HIP_MT_NW", 0);
+    static const int st_env = env_int("GORCH_HIP_MT_ST", 0);
+    static const int s_env = env_int("GORCH_HIP_MT_S", 0);
+    static const int bps_env = env_int("GORCH_HIP_MT_BPS", 0);
+    const int ntiles = (N + 15) / 16;
+    const int nst_total = (K + 127) / 128;
+    MtPlan p;
+    p.mr = M <= 4 ? 4 : (M <= 8 ? 8 : 16);
+    const int max_kst = kMtLds / (512 * p.mr);
+    int S = s_env ? s_env : (nst_total + max_kst - 1) / max_kst;
+    S = std::min(std::max(S, 1), nst_total);
+    p.kst = (nst_total + S - 1) / S;
+    p.splits = (nst_total + p.kst - 1) / p.kst;
+    p.nw = nw_env ? nw_env : 16;
+    p.st = st_env ? st_env : 2;
+    p.bps = std::min(std::max(256 / p.splits, 1), ntiles);
+    if (bps_env) p.bps = bps_env;
+    return p;
+}
+
+// Multi-row GEMV launch; returns -1 when the configuration is not covered
+// (the caller then uses the in-block-split MFMA kernel).
+static int launch_mt(hipStream_t s, const float* x, const uint16_t* W, const float* bias, const float* residual,
+                     const OutDesc& od, int M, int N, int K, int epilogue, const LinearExtras& ex) {
+    const MtPlan p = plan_mt(M, N, K);
+    const int ntiles = (N + 15) / 16;
+    const int S = p.splits;
+    unsigned long long* slots = nullptr;
+    unsigned int* counters = nullptr;
+    if (S > 1) {
+        const size_t slot_bytes = (size_t)ntiles * S * 256 * sizeof(unsigned long long);
+        const size_t need = slot_bytes + (size_t)ntiles * sizeof(unsigned int);
+        void* ws = stream_workspace(s, need);
+        if (!ws) return -1;
+        slots = static_cast<unsigned long long*>(ws);
+        counters = reinterpret_cast<unsigned int*>(static_cast<char*>(ws) + slot_bytes);
+    }
+    const size_t lds = (size_t)p.kst * 16 * p.mr * 16 * 2;
+    if (lds > (size_t)2 * kMtLds || p.bps < 1) return -1;
+    dim3 grid(S * p.bps);
+    int rc = -1;
+#define GH_MT(NWV, STV, MRV)                                                                                 \
+    if (p.nw == NWV && p.st == STV && p.mr == MRV)                                                             \
+        rc = launch_mt_t<NWV, STV, MRV>(s, grid, lds, x, W, bias, residual, od, M, N, K, p.kst * 128, p.bps,    \
+                                        epilogue, ex, slots, counters);
+#define GH_MT_R(NWV, STV) GH_MT(NWV, STV, 4) GH_MT(NWV, STV, 8) GH_MT(NWV, STV, 16)
+    GH_MT_R(8, 1) GH_MT_R(8, 2) GH_MT_R(16, 1) GH_MT_R(16, 2)
+#undef GH_MT_R
+#undef GH_MT
+    if (rc < 0) return -1;
+    if (rc != GORCH_HIP_OK) return rc;
+    count(CNT_GEMV);
+    return check_launch("gemv_mt");
 }
 
 template <int MT>
@@ -527,8 +881,16 @@ template <int NT, int NW, int U>
 static void launch_t(hipStream_t s, dim3 grid, const float* x, const uint16_t* W, const float* bias,
                      const float* residual, const OutDesc& od, int M, int N, int K, int kw, int epilogue,
                      const LinearExtras& ex) {
-    hipLaunchKernelGGL((k_linear_bf16_mfma<NT, NW, U>), grid, dim3(NW * 64), 0, s, x, W, bias, residual, od,
-                       M, N, K, kw, epilogue, ex);
+    static const int lx = env_int("GORCH_HIP_GEMV_LX", 0);
+    if constexpr (U == 4 && NT * NW <= 16) {
+        if (lx) {
+            hipLaunchKernelGGL((k_linear_bf16_mfma<NT, NW, U, true>), grid, dim3(NW * 64), 0, s, x, W, bias,
+                               residual, od, M, N, K, kw, epilogue, ex);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((k_linear_bf16_mfma<NT, NW, U, false>), grid, dim3(NW * 64), 0, s, x, W, bias, residual,
+                       od, M, N, K, kw, epilogue, ex);
 }
 
 int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
@@ -564,6 +926,11 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
             int rc = launch_m1(s, x, W, bias, residual, od, N, K, epilogue, ex, T1, C1);
             if (rc >= 0) return rc;
         }
+    }
+    static const int mt_on = env_int("GORCH_HIP_MT", 1);
+    if (M >= 2 && mt_on && (N + 15) / 16 >= 1024) {
+        int rc = launch_mt(s, x, W, bias, residual, od, M, N, K, epilogue, ex);
+        if (rc >= 0) return rc;
     }
     const int T = valu_lanes_per_row(K);
     if (M <= valu_max_m && T && (size_t)4 * K * sizeof(float) <= 64 * 1024) {
