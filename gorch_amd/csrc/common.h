@@ -33,12 +33,7 @@ struct LinearExtras {
     float ln_eps = 1e-5f;
     unsigned long long* argmax_key = nullptr;
     long long x_stride = 0;  // activation row stride in elements (0 = K)
-    float* ws = nullptr;     // split-K partials (nullptr: the stream's own buffer)
-    size_t ws_bytes = 0;
 };
-// Per-(device, stream) scratch for split-K partials; nullptr when it would
-// have to grow during stream capture or the allocation fails.
-void* stream_workspace(hipStream_t s, size_t bytes);
 int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                        const float* residual, float* y, int M, int N, int K, int epilogue);
 int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
@@ -110,16 +105,43 @@ struct OutDesc {
         return d;
     }
 
+    // Segment fields are read as wave-uniform scalars and picked with
+    // selects: a runtime-indexed (or select-addressed) kernel argument
+    // becomes a per-lane vector load, and every output element would then
+    // wait on descriptor loads.
+    __device__ static __forceinline__ long long uni(long long v) {
+        const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((int)(v & 0xffffffffll));
+        const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((int)(v >> 32));
+        return (long long)(((unsigned long long)hi << 32) | lo);
+    }
     __device__ __forceinline__ float* at(int m, int n) const {
-        int s = 0, n0 = 0;
-        while (s + 1 < nseg && n >= n_end[s]) {
-            n0 = n_end[s];
-            s++;
+        int seq = 0, r = m;
+        if (rows_per_seq < (1 << 30)) {
+            seq = m / rows_per_seq;
+            r = m - seq * rows_per_seq;
         }
-        const int seq = m / rows_per_seq;
-        int r = m - seq * rows_per_seq;
-        if (use_pos[s]) r += *pos_dev;
-        return ptr[s] + seq * seq_stride[s] + (long long)r * row_stride[s] + (n - n0);
+        if (nseg == 1) {
+            if (use_pos[0]) r += *pos_dev;
+            return ptr[0] + seq * seq_stride[0] + (long long)r * row_stride[0] + n;
+        }
+        const bool s1 = n >= __builtin_amdgcn_readfirstlane(n_end[0]);
+        const bool s2 = nseg > 2 && n >= __builtin_amdgcn_readfirstlane(n_end[1]);
+        // segment bases as element offsets from ptr[0], so the result keeps
+        // the global address space (a pointer rebuilt from integers is
+        // generic, and its flat stores wait on LDS traffic too)
+        const long long d1 = uni((long long)(ptr[1] - ptr[0])), d2 = uni((long long)(ptr[2] - ptr[0]));
+        const long long ss0 = uni(seq_stride[0]), ss1 = uni(seq_stride[1]), ss2 = uni(seq_stride[2]);
+        const long long rs0 = uni(row_stride[0]), rs1 = uni(row_stride[1]), rs2 = uni(row_stride[2]);
+        const int up0 = __builtin_amdgcn_readfirstlane(use_pos[0]), up1 = __builtin_amdgcn_readfirstlane(use_pos[1]),
+                  up2 = __builtin_amdgcn_readfirstlane(use_pos[2]);
+        const int ne0 = __builtin_amdgcn_readfirstlane(n_end[0]), ne1 = __builtin_amdgcn_readfirstlane(n_end[1]);
+        float* p = ptr[0] + (s2 ? d2 : (s1 ? d1 : 0));
+        const int nb = s2 ? ne1 : (s1 ? ne0 : 0);
+        const long long ss = s2 ? ss2 : (s1 ? ss1 : ss0);
+        const long long rs = s2 ? rs2 : (s1 ? rs1 : rs0);
+        const int up = s2 ? up2 : (s1 ? up1 : up0);
+        if (up) r += *pos_dev;
+        return p + seq * ss + (long long)r * rs + (n - nb);
     }
 };
 

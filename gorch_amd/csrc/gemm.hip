@@ -23,7 +23,7 @@ namespace gh {
 constexpr int kBK = 64;
 constexpr int kLDA = kBK + 8;  // bf16 elements per LDS row (16-byte pad)
 
-template <int BM, int BN, bool SPLIT>
+template <int BM, int BN, bool SPLIT, int PF>
 __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A, const uint16_t* __restrict__ W,
                                                     const float* __restrict__ bias, const float* residual,
                                                     OutDesc od, int M, int N, int K, int epilogue) {
@@ -38,33 +38,35 @@ __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A,
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
 
-    float4 ra[A_F4];
-    uint4 rw[W_U4];
-    auto gload = [&](int k0) {
+    // PF register stages: the loads of K-step i + PF are issued as soon as
+    // step i has been written to LDS, so PF steps of latency are in flight
+    float4 ra[PF][A_F4];
+    uint4 rw[PF][W_U4];
+    auto gload = [&](int k0, float4 (&a)[A_F4], uint4 (&wv)[W_U4]) {
 #pragma unroll
         for (int i = 0; i < A_F4; i++) {
             const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
             const int m = m0 + row, k = k0 + 4 * c4;
             if (m < M && k < K)
-                ra[i] = *reinterpret_cast<const float4*>(A + (size_t)m * K + k);
+                a[i] = *reinterpret_cast<const float4*>(A + (size_t)m * K + k);
             else
-                ra[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                a[i] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
         for (int i = 0; i < W_U4; i++) {
             const int idx = tid + 256 * i, row = idx >> 3, c8 = idx & 7;
             const int n = n0 + row, k = k0 + 8 * c8;
             if (n < N && k < K)
-                rw[i] = *reinterpret_cast<const uint4*>(W + (size_t)n * K + k);
+                wv[i] = *reinterpret_cast<const uint4*>(W + (size_t)n * K + k);
             else
-                rw[i] = make_uint4(0, 0, 0, 0);
+                wv[i] = make_uint4(0, 0, 0, 0);
         }
     };
-    auto sstore = [&]() {
+    auto sstore = [&](const float4 (&a)[A_F4], const uint4 (&wv)[W_U4]) {
 #pragma unroll
         for (int i = 0; i < A_F4; i++) {
             const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
-            const float f[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
+            const float f[4] = {a[i].x, a[i].y, a[i].z, a[i].w};
             uint16_t hi[4], lo[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -86,7 +88,7 @@ __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A,
 #pragma unroll
         for (int i = 0; i < W_U4; i++) {
             const int idx = tid + 256 * i, row = idx >> 3, c8 = idx & 7;
-            *reinterpret_cast<uint4*>(&Ws[row][8 * c8]) = rw[i];
+            *reinterpret_cast<uint4*>(&Ws[row][8 * c8]) = wv[i];
         }
     };
 
@@ -97,28 +99,43 @@ __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A,
         for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     const int r = lane & 15, g = lane >> 4;
-    gload(0);
-    for (int k0 = 0; k0 < K; k0 += kBK) {
-        __syncthreads();  // previous step's fragment reads are done
-        sstore();
-        __syncthreads();
-        if (k0 + kBK < K) gload(k0 + kBK);
+    // the epilogue's bias values, loaded while the main loop runs
+    float bn[TN];
 #pragma unroll
-        for (int kk = 0; kk < kBK; kk += 32) {
-            bf16x8 bfr[TN];
+    for (int j = 0; j < TN; j++) {
+        const int n = n0 + wn * WN + j * 16 + r;
+        bn[j] = (bias && n < N) ? bias[n] : 0.f;
+    }
+    const int nk = (K + kBK - 1) / kBK;
 #pragma unroll
-            for (int j = 0; j < TN; j++)
-                bfr[j] = *reinterpret_cast<const bf16x8*>(&Ws[wn * WN + j * 16 + r][kk + 8 * g]);
+    for (int s = 0; s < PF; s++)
+        if (s < nk) gload(s * kBK, ra[s], rw[s]);
+    for (int it0 = 0; it0 < nk; it0 += PF) {
 #pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const bf16x8 ahi = *reinterpret_cast<const bf16x8*>(&As[0][wm * WM + i * 16 + r][kk + 8 * g]);
+        for (int s = 0; s < PF; s++) {
+            const int it = it0 + s;
+            if (it >= nk) break;
+            __syncthreads();  // previous step's fragment reads are done
+            sstore(ra[s], rw[s]);
+            __syncthreads();
+            if (it + PF < nk) gload((it + PF) * kBK, ra[s], rw[s]);
 #pragma unroll
-                for (int j = 0; j < TN; j++) acc[i][j] = mfma16x16x32(ahi, bfr[j], acc[i][j]);
-                if (SPLIT) {
-                    const bf16x8 alo =
-                        *reinterpret_cast<const bf16x8*>(&As[NA - 1][wm * WM + i * 16 + r][kk + 8 * g]);
+            for (int kk = 0; kk < kBK; kk += 32) {
+                bf16x8 bfr[TN];
 #pragma unroll
-                    for (int j = 0; j < TN; j++) acc[i][j] = mfma16x16x32(alo, bfr[j], acc[i][j]);
+                for (int j = 0; j < TN; j++)
+                    bfr[j] = *reinterpret_cast<const bf16x8*>(&Ws[wn * WN + j * 16 + r][kk + 8 * g]);
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    const bf16x8 ahi = *reinterpret_cast<const bf16x8*>(&As[0][wm * WM + i * 16 + r][kk + 8 * g]);
+#pragma unroll
+                    for (int j = 0; j < TN; j++) acc[i][j] = mfma16x16x32(ahi, bfr[j], acc[i][j]);
+                    if (SPLIT) {
+                        const bf16x8 alo =
+                            *reinterpret_cast<const bf16x8*>(&As[NA - 1][wm * WM + i * 16 + r][kk + 8 * g]);
+#pragma unroll
+                        for (int j = 0; j < TN; j++) acc[i][j] = mfma16x16x32(alo, bfr[j], acc[i][j]);
+                    }
                 }
             }
         }
@@ -130,13 +147,12 @@ __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A,
         for (int j = 0; j < TN; j++) {
             const int n = n0 + wn * WN + j * 16 + r;
             if (n >= N) continue;
-            const float bn = bias ? bias[n] : 0.f;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int m = m0 + wm * WM + i * 16 + 4 * g + v;
                 if (m < M) {
                     float s = acc[i][j][v];
-                    if (bias) s = s + bn;
+                    if (bias) s = s + bn[j];
                     if (epilogue == GORCH_HIP_EPI_GELU) s = gelu_tanh(s);
                     if (residual) s = residual[(size_t)m * N + n] + s;
                     *od.at(m, n) = s;
@@ -148,9 +164,21 @@ __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A,
 template <int BM, int BN, bool SPLIT>
 static void launch_gemm_t(hipStream_t s, const float* A, const uint16_t* W, const float* bias,
                           const float* residual, const OutDesc& od, int M, int N, int K, int epilogue) {
+    static const int pf_env = [] {
+        const char* e = getenv("GORCH_HIP_GEMM_PF");
+        return e ? atoi(e) : 0;
+    }();
     dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-    hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT>), grid, dim3(256), 0, s, A, W, bias, residual, od, M, N, K,
-                       epilogue);
+    const int pf = pf_env ? pf_env : (BM * BN <= 64 * 128 ? 3 : 2);
+    if (pf == 1)
+        hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT, 1>), grid, dim3(256), 0, s, A, W, bias, residual, od, M, N,
+                           K, epilogue);
+    else if (pf == 2)
+        hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT, 2>), grid, dim3(256), 0, s, A, W, bias, residual, od, M, N,
+                           K, epilogue);
+    else
+        hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT, 3>), grid, dim3(256), 0, s, A, W, bias, residual, od, M, N,
+                           K, epilogue);
 }
 
 // Tile choice: the largest tile that still gives every CU a block.

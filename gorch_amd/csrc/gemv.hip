@@ -439,26 +439,18 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
 // Multi-row GEMV for 2 <= M <= 16 over wide N (LM-head class, >= 1024
 // 16-row weight tiles).
 //
-// Work is (16-row weight tile, K slice). The grid is S slices x bps blocks
-// of NW waves (bps ~ 256 / S, so every CU streams about the same number of
-// tiles); a block owns one slice and its waves take the tiles t = b +
-// bps * (w + NW * i). The block stages its slice of the activations once
-// in LDS, already split into bf16 hi/lo in the MFMA A layout ([k-step]
-// [k-chunk g][row r], 16 bytes each; one conflict-free LDS read per
+// bps ~ 256 blocks of NW waves (every CU streams about the same number of
+// tiles); wave w of block b takes the 16-row weight tiles t = b + bps * (w
+// + NW * i) over the whole K. The block first stages all of the
+// activations in LDS, already split into bf16 hi/lo in the MFMA A layout
+// ([k-step][k-chunk g][row r], 16 bytes each; one conflict-free LDS read per
 // k-step): loading A from global memory per k-step instead spends the
 // vector-memory slots the weight stream needs and halves its bandwidth on
 // MI355X. B fragments are read straight from HBM with 16-byte loads, ST
 // 128-wide stages per batch; the first batch is issued before the staging.
-//
-// With one slice (S == 1) each wave applies the epilogue itself. With
-// several, each slice's tile is published to flagged 64-bit slots (flag
-// word | f32 bits) with device-scope atomic stores, a per-tile arrival
-// counter picks the last slice to finish, and that wave reads the slots in
-// slice order (atomic loads; a slot not yet flagged is read again, at most
-// kSlotSpins times) and clears them, so the sum order is fixed and no
-// second kernel or memory fence is needed. Counters and slots are left
-// zeroed for the next launch on the stream.
-constexpr int kSlotSpins = 1 << 16;
+// K is never split across blocks (that would need a cross-block reduction):
+// shapes whose activations exceed the LDS budget use the in-block-split
+// kernel above.
 
 // LayerNorm statistics (nn/layernorm.go:61-91) in f64 over full rows.
 template <int NW>
@@ -540,84 +532,40 @@ __device__ __forceinline__ void mt_a(const uint4* xh, const uint4* xl, int ks, i
     }
 }
 
-// Finish tile ct: combine K slices when there are several (returns false
-// on every wave but the last slice's), then bias, GELU, residual, output
-// and argmax. acc: rows 4g..4g+3 of column 16*ct + r.
-__device__ bool mt_finish(floatx4& acc, int ct, int split, int nsplit, int M, int N, const float* bias,
-                          const float* residual, const OutDesc& od, int epilogue, const LinearExtras& ex,
-                          unsigned long long* slots, unsigned int* counters, unsigned long long* s_key) {
+// Finish tile ct: bias, GELU, residual, output and the block's argmax key.
+// acc: rows 4g..4g+3 of column 16*ct + r.
+__device__ __forceinline__ void mt_finish(const floatx4& acc, int ct, int M, int N, const float* bias,
+                                          const float* residual, const OutDesc& od, int epilogue,
+                                          const LinearExtras& ex, unsigned long long* s_key) {
     const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-    if (nsplit > 1) {
-        unsigned long long* my = slots + ((size_t)ct * nsplit + split) * 256;
-#pragma unroll
-        for (int v4 = 0; v4 < 4; v4++)
-            if (4 * g + v4 < M)
-                __hip_atomic_store(&my[v4 * 64 + lane], (1ull << 32) | (unsigned long long)__float_as_uint(acc[v4]),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        unsigned int prev = 0;
-        if (lane == 0) prev = atomicAdd(&counters[ct], 1u);
-        prev = __shfl(prev, 0, 64);
-        if (prev != (unsigned int)(nsplit - 1)) return false;
-        if (lane == 0) __hip_atomic_store(&counters[ct], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        floatx4 tot = {0.f, 0.f, 0.f, 0.f};
-        for (int q = 0; q < nsplit; q++) {
-            unsigned long long* sl = slots + ((size_t)ct * nsplit + q) * 256;
-            unsigned long long got[4];
-#pragma unroll
-            for (int v4 = 0; v4 < 4; v4++)
-                got[v4] = 4 * g + v4 < M
-                              ? __hip_atomic_load(&sl[v4 * 64 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                              : (1ull << 32);
-#pragma unroll
-            for (int v4 = 0; v4 < 4; v4++) {
-                int spins = 0;
-                while (!(got[v4] >> 32) && ++spins < kSlotSpins)
-                    got[v4] = __hip_atomic_load(&sl[v4 * 64 + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                tot[v4] += (got[v4] >> 32) ? __uint_as_float((unsigned int)got[v4]) : __builtin_nanf("");
-                if (4 * g + v4 < M)
-                    __hip_atomic_store(&sl[v4 * 64 + lane], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        acc = tot;
-    }
     const int on = ct * 16 + r;
-    if (on < N) {
+    if (on >= N) return;
 #pragma unroll
-        for (int v4 = 0; v4 < 4; v4++) {
-            const int om = 4 * g + v4;
-            if (om >= M) break;
-            float sum = acc[v4];
-            if (bias) sum = sum + bias[on];
-            if (epilogue == GORCH_HIP_EPI_GELU) sum = gelu_tanh(sum);
-            if (residual) sum = residual[(size_t)om * N + on] + sum;
-            *od.at(om, on) = sum;
-            if (ex.argmax_key) {
-                if (nsplit > 1)
-                    atomicMax(&ex.argmax_key[om], argmax_pack(sum, on));
-                else
-                    atomicMax(&s_key[om], argmax_pack(sum, on));
-            }
-        }
+    for (int v4 = 0; v4 < 4; v4++) {
+        const int om = 4 * g + v4;
+        if (om >= M) break;
+        float sum = acc[v4];
+        if (bias) sum = sum + bias[on];
+        if (epilogue == GORCH_HIP_EPI_GELU) sum = gelu_tanh(sum);
+        if (residual) sum = residual[(size_t)om * N + on] + sum;
+        *od.at(om, on) = sum;
+        if (ex.argmax_key) atomicMax(&s_key[om], argmax_pack(sum, on));
     }
-    return true;
 }
 
 template <int NW, int ST, int MR>
 __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
     const float* __restrict__ x, const uint16_t* __restrict__ W, const float* __restrict__ bias,
-    const float* residual, OutDesc od, int M, int N, int K, int kspan, int bps, int epilogue, LinearExtras ex,
-    unsigned long long* slots, unsigned int* counters) {
+    const float* residual, OutDesc od, int M, int N, int K, int bps, int epilogue, LinearExtras ex) {
     constexpr int mr = MR;
     extern __shared__ uint4 smem[];
     __shared__ float s_mean[16], s_inv[16];
     __shared__ unsigned long long s_key[16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int nsplit = gridDim.x / bps;
-    const int split = blockIdx.x % nsplit, bidx = blockIdx.x / nsplit;
-    const int kb = split * kspan;
-    const int ke = min(K, kb + kspan);
-    const int nst = (ke - kb + 127) >> 7;  // 128-wide stages in the slice
+    const int bidx = blockIdx.x;
+    const int kb = 0, ke = K;
+    const int nst = (K + 127) >> 7;  // 128-wide stages
     uint4* xh = smem;
     uint4* xl = smem + nst * 16 * mr;
     const long long xs = ex.x_stride ? ex.x_stride : K;
@@ -673,10 +621,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
                 }
             }
         }
-        mt_finish(acc, t, split, nsplit, M, N, bias, residual, od, epilogue, ex, slots, counters, s_key);
+        mt_finish(acc, t, M, N, bias, residual, od, epilogue, ex, s_key);
         acc = floatx4{0.f, 0.f, 0.f, 0.f};
     }
-    if (ex.argmax_key && nsplit == 1) {
+    if (ex.argmax_key) {
         __syncthreads();
         if (threadIdx.x < 16 && (int)threadIdx.x < M) atomicMax(&ex.argmax_key[threadIdx.x], s_key[threadIdx.x]);
     }
@@ -699,7 +647,7 @@ static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const flo
                      const OutDesc& od, int N, int K, int epilogue, const LinearExtras& ex, int T, int C) {
     const int rpi = 64 / T;
     const int ngroups = (N + rpi - 1) / rpi;
-    static const int max_blocks = env_int("GORCH_HIP_GEMV_M1_BLOCKS", 2048);
+    static const int max_blocks = env_int("GORCH_HIP_GEMV_M1_BLOCKS", 4096);
     int blocks = (ngroups + 3) / 4;
     if (blocks > max_blocks) blocks = max_blocks;
 #define GH_M1(TT, CC)                                                                                        \
@@ -722,9 +670,9 @@ static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const flo
 }
 
 template <int NW, int ST, int MR>
-static int launch_mt_t(hipStream_t s, dim3 grid, size_t lds, const float* x, const uint16_t* W, const float* bias,
-                       const float* residual, const OutDesc& od, int M, int N, int K, int kspan, int bps,
-                       int epilogue, const LinearExtras& ex, unsigned long long* slots, unsigned int* counters) {
+static int launch_mt_t(hipStream_t s, int grid, size_t lds, const float* x, const uint16_t* W, const float* bias,
+                       const float* residual, const OutDesc& od, int M, int N, int K, int bps, int epilogue,
+                       const LinearExtras& ex) {
     static bool attr_set = false;
     if (!attr_set) {
         GH_TRY(check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_mt<NW, ST, MR>),
@@ -732,66 +680,33 @@ static int launch_mt_t(hipStream_t s, dim3 grid, size_t lds, const float* x, con
                      "gemv_mt attribute"));
         attr_set = true;
     }
-    hipLaunchKernelGGL((k_gemv_mt<NW, ST, MR>), grid, dim3(NW * 64), lds, s, x, W, bias, residual, od, M, N,
-                       K, kspan, bps, epilogue, ex, slots, counters);
+    hipLaunchKernelGGL((k_gemv_mt<NW, ST, MR>), dim3(grid), dim3(NW * 64), lds, s, x, W, bias, residual, od, M, N, K,
+                       bps, epilogue, ex);
     return GORCH_HIP_OK;
 }
 
-struct MtPlan {
-    int nw, st, splits, kst, bps, mr;
-};
+// LDS for the staged activations: up to 128 KB (all of K).
+constexpr size_t kMtLds = 128 * 1024;
 
-// LDS for the staged activation slice: 64 KB, two 16-wave blocks per CU.
-constexpr int kMtLds = 64 * 1024;
-
-// Launch plan for the multi-row GEMV: K slices only when the activations
-// exceed the LDS budget; GORCH_HIP_MT_{NW,ST,S,BPS} override.
-static MtPlan plan_mt(int M, int N, int K) {
-    static const int nw_env = env_int("GORCH_HIP_MT_NW", 0);
-    static const int st_env = env_int("GORCH_HIP_MT_ST", 0);
-    static const int s_env = env_int("GORCH_HIP_MT_S", 0);
-    static const int bps_env = env_int("GORCH_HIP_MT_BPS", 0);
-    const int ntiles = (N + 15) / 16;
-    const int nst_total = (K + 127) / 128;
-    MtPlan p;
-    p.mr = M <= 4 ? 4 : (M <= 8 ? 8 : 16);
-    const int max_kst = kMtLds / (512 * p.mr);
-    int S = s_env ? s_env : (nst_total + max_kst - 1) / max_kst;
-    S = std::min(std::max(S, 1), nst_total);
-    p.kst = (nst_total + S - 1) / S;
-    p.splits = (nst_total + p.kst - 1) / p.kst;
-    p.nw = nw_env ? nw_env : 16;
-    p.st = st_env ? st_env : 2;
-    p.bps = std::min(std::max(256 / p.splits, 1), ntiles);
-    if (bps_env) p.bps = bps_env;
-    return p;
-}
-
-// Multi-row GEMV launch; returns -1 when the configuration is not covered
+// Multi-row GEMV launch; returns -1 when the activations do not fit LDS
 // (the caller then uses the in-block-split MFMA kernel).
+// GORCH_HIP_MT_{NW,ST,BPS} override the plan.
 static int launch_mt(hipStream_t s, const float* x, const uint16_t* W, const float* bias, const float* residual,
                      const OutDesc& od, int M, int N, int K, int epilogue, const LinearExtras& ex) {
-    const MtPlan p = plan_mt(M, N, K);
+    static const int nw_env = env_int("GORCH_HIP_MT_NW", 0);
+    static const int st_env = env_int("GORCH_HIP_MT_ST", 0);
+    static const int bps_env = env_int("GORCH_HIP_MT_BPS", 0);
     const int ntiles = (N + 15) / 16;
-    const int S = p.splits;
-    unsigned long long* slots = nullptr;
-    unsigned int* counters = nullptr;
-    if (S > 1) {
-        const size_t slot_bytes = (size_t)ntiles * S * 256 * sizeof(unsigned long long);
-        const size_t need = slot_bytes + (size_t)ntiles * sizeof(unsigned int);
-        void* ws = stream_workspace(s, need);
-        if (!ws) return -1;
-        slots = static_cast<unsigned long long*>(ws);
-        counters = reinterpret_cast<unsigned int*>(static_cast<char*>(ws) + slot_bytes);
-    }
-    const size_t lds = (size_t)p.kst * 16 * p.mr * 16 * 2;
-    if (lds > (size_t)2 * kMtLds || p.bps < 1) return -1;
-    dim3 grid(S * p.bps);
+    const int mr = M <= 4 ? 4 : (M <= 8 ? 8 : 16);
+    const size_t lds = (size_t)((K + 127) / 128) * 16 * mr * 16 * 2;
+    if (lds > kMtLds) return -1;
+    const int nw = nw_env ? nw_env : 16;
+    const int st = st_env ? st_env : 2;
+    const int bps = bps_env ? bps_env : std::min(256, ntiles);
     int rc = -1;
 #define GH_MT(NWV, STV, MRV)                                                                                 \
-    if (p.nw == NWV && p.st == STV && p.mr == MRV)                                                             \
-        rc = launch_mt_t<NWV, STV, MRV>(s, grid, lds, x, W, bias, residual, od, M, N, K, p.kst * 128, p.bps,    \
-                                        epilogue, ex, slots, counters);
+    if (nw == NWV && st == STV && mr == MRV)                                                                 \
+        rc = launch_mt_t<NWV, STV, MRV>(s, bps, lds, x, W, bias, residual, od, M, N, K, bps, epilogue, ex);
 #define GH_MT_R(NWV, STV) GH_MT(NWV, STV, 4) GH_MT(NWV, STV, 8) GH_MT(NWV, STV, 16)
     GH_MT_R(8, 1) GH_MT_R(8, 2) GH_MT_R(16, 1) GH_MT_R(16, 2)
 #undef GH_MT_R
@@ -917,9 +832,9 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
     }
     static const int valu_max_m = env_int("GORCH_HIP_GEMV_VALU_MAX_M", 1);
     static const int m1_on = env_int("GORCH_HIP_GEMV_M1", 1);
-    // M = 1: the register-activation kernel for narrow/medium N (lowest
-    // latency), the LDS-staged one for LM-head-sized N (more waves in flight).
-    if (M == 1 && valu_max_m >= 1 && m1_on && N < 16384) {
+    // M = 1: the register-activation kernel whenever K fits its shape table
+    // (K/8 = T*C with C <= 8), else the LDS-staged VALU kernel.
+    if (M == 1 && valu_max_m >= 1 && m1_on) {
         int T1, C1;
         m1_shape(K, &T1, &C1);
         if (T1) {

@@ -2,9 +2,7 @@
 // metal/shim.m:120-437 (device, queue, buffers) and ops.go:15-78 (counters).
 #include <atomic>
 #include <cstring>
-#include <mutex>
 #include <string>
-#include <vector>
 
 #include "common.h"
 
@@ -28,55 +26,6 @@ hipStream_t stream_of(void* s) { return reinterpret_cast<hipStream_t>(s); }
 static std::atomic<uint64_t> g_counts[CNT_COUNT];
 
 void count(Counter c) { g_counts[c].fetch_add(1, std::memory_order_relaxed); }
-
-// Zero-initialised scratch, one buffer per (device, stream): work on one
-// stream is ordered, so consecutive launches on it can share the buffer.
-// A buffer is only grown outside stream capture and is never freed (a
-// captured graph may still reference it); its users leave it zeroed.
-namespace {
-struct StreamWs {
-    int dev;
-    hipStream_t stream;
-    void* ptr;
-    size_t bytes;
-};
-std::mutex g_ws_mu;
-std::vector<StreamWs> g_ws;
-}  // namespace
-
-void* stream_workspace(hipStream_t s, size_t bytes) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    StreamWs* e = nullptr;
-    for (auto& w : g_ws)
-        if (w.dev == dev && w.stream == s) e = &w;
-    if (e && e->bytes >= bytes) return e->ptr;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-        (void)hipGetLastError();
-        return nullptr;
-    }
-    size_t want = bytes < (size_t)(1 << 20) ? (size_t)(1 << 20) : bytes;
-    void* p = nullptr;
-    if (hipMalloc(&p, want) != hipSuccess) {
-        (void)hipGetLastError();
-        return nullptr;
-    }
-    // users of the buffer rely on it starting zeroed (and leave it zeroed)
-    if (hipMemset(p, 0, want) != hipSuccess) {
-        (void)hipGetLastError();
-        (void)hipFree(p);
-        return nullptr;
-    }
-    if (e) {
-        e->ptr = p;
-        e->bytes = want;
-    } else {
-        g_ws.push_back({dev, s, p, want});
-    }
-    return p;
-}
 
 }  // namespace gh
 

@@ -147,3 +147,29 @@ def test_generate_batch_above_16(tiny):
     for b in (0, 9, 16):
         ref, _, _ = o.generate_cached(prompts[b], 5)
         assert list(ids[b]) == list(ref)
+
+
+WIDE = dict(vocab=16400, dim=1600, heads=25, layers=1, max_seq=24)
+
+
+@pytest.fixture(scope="module")
+def wide(gpu):
+    w = syn.gpt2_weights(WIDE, seed=41, random_affine=True)
+    return w, gpu.GPT(w), orc.GPT(w)
+
+
+@pytest.mark.parametrize("batch", [4, 16])
+def test_generate_batch_wide_lm_head(wide, batch):
+    """Batched decode whose LM head has >= 1024 16-row weight tiles and
+    K = 1600 (the GPT-2 XL width): the multi-row GEMV with the final
+    LayerNorm and the argmax fused, activations staged in LDS. Tokens
+    identical to the oracle run per sequence, eager and graph-replayed."""
+    w, g, o = wide
+    prompts = np.stack([syn.prompt_ids(6, WIDE["vocab"], seed=60 + b) for b in range(batch)])
+    ids, logits, _ = g.generate_cached(prompts, 8, want_logits=True)
+    for b in range(batch):
+        ref, ref_logits, _ = o.generate_cached(prompts[b], 8, want_logits=True)
+        assert list(ids[b]) == list(ref)
+        assert rel_err(logits[0, b], ref_logits[0]) <= 1e-3
+    ids_graph, _, _ = g.generate_cached(prompts, 8, use_graph=True)
+    assert np.array_equal(ids_graph, ids)
