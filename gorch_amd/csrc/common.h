@@ -33,7 +33,26 @@ struct LinearExtras {
     float ln_eps = 1e-5f;
     unsigned long long* argmax_key = nullptr;
     long long x_stride = 0;  // activation row stride in elements (0 = K)
+    // LayerNorm row statistics (mean, 1/sqrt(var + eps)) computed by an
+    // earlier kernel; null: the GEMV computes them itself
+    const float2* ln_stats = nullptr;
+    // K split across ksplit blocks: raw partial sums to part[s][m][n]
+    // (bias, activation and residual are then applied by the reduction)
+    float* part = nullptr;
+    int ksplit = 1;
+    int kslice = 0;  // K per slice (set by the launcher)
 };
+// Number of K slices a K-split Linear actually uses for a requested count
+// (slices are multiples of 32 wide).
+inline int ksplit_slices(int K, int S) {
+    const int ks = ((K + S - 1) / S + 31) / 32 * 32;
+    return (K + ks - 1) / ks;
+}
+// Row reduction after a K-split Linear: x[m] = x[m] + bias + sum_s part[s][m]
+// (slices added in order; S = 0 leaves x as is), then the LayerNorm
+// statistics of the new row into stats[m] when stats is not null.
+int launch_reduce_rows(hipStream_t s, const float* part, int S, const float* bias, float* x, int M, int N,
+                       float eps, float2* stats);
 int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                        const float* residual, float* y, int M, int N, int K, int epilogue);
 int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, const float* bias,

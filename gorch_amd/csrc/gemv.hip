@@ -45,10 +45,13 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
     const int r = lane & 15;  // A: activation row; B: weight row within tile
     const int g = lane >> 4;  // k-chunk group within a 32-wide k-step
     const int n0 = blockIdx.x * (16 * NT);
-    const int m0 = blockIdx.y * 16;
+    // partial mode: blockIdx.y is the K slice (M <= 16), else the row group
+    const int m0 = ex.part ? 0 : blockIdx.y * 16;
+    const int kbase = ex.part ? blockIdx.y * ex.kslice : 0;
+    const int kend = ex.part ? min(K, kbase + ex.kslice) : K;
     const int mrow = m0 + r;
-    const int kb = wave * kw;
-    const int ke = min(kb + kw, K);
+    const int kb = kbase + wave * kw;
+    const int ke = min(kb + kw, kend);
 
     const long long xs = ex.x_stride ? ex.x_stride : K;
     const bool arow_ok = mrow < M;
@@ -63,7 +66,14 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
         wrow[t] = W + (size_t)(wrow_ok[t] ? n : 0) * K;
     }
 
-    if (ex.ln_g) {
+    if (ex.ln_g && ex.ln_stats) {
+        if (threadIdx.x < 16 && m0 + (int)threadIdx.x < M) {
+            const float2 st = ex.ln_stats[m0 + threadIdx.x];
+            s_mean[threadIdx.x] = st.x;
+            s_inv[threadIdx.x] = st.y;
+        }
+        __syncthreads();
+    } else if (ex.ln_g) {
         // LayerNorm prologue (nn/layernorm.go:61-91): per-row mean and
         // variance in f64 over the whole K, computed by each block for its
         // (at most 16) rows; the A operand is normalised as it is loaded.
@@ -188,6 +198,10 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
             float s = red[0][t][e][v];
 #pragma unroll
             for (int w = 1; w < NW; w++) s += red[w][t][e][v];
+            if (ex.part) {
+                ex.part[((size_t)blockIdx.y * M + om) * N + on] = s;
+                continue;
+            }
             if (bias) s = s + bias[on];
             if (epilogue == GORCH_HIP_EPI_GELU) s = gelu_tanh(s);
             if (residual) s = residual[(size_t)om * N + on] + s;
@@ -591,7 +605,14 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
     int t = bidx + bps * wave;
     if (t < ntiles) load(t, 0);  // the weight stream starts before the staging
 
-    if (ex.ln_g) {
+    if (ex.ln_g && ex.ln_stats) {
+        if (threadIdx.x < 16 && (int)threadIdx.x < M) {
+            const float2 st = ex.ln_stats[threadIdx.x];
+            s_mean[threadIdx.x] = st.x;
+            s_inv[threadIdx.x] = st.y;
+        }
+        __syncthreads();
+    } else if (ex.ln_g) {
         mt_ln_stats<NW>(x, xs, M, K, ex.ln_eps, s_mean, s_inv);
         __syncthreads();
     }
@@ -818,6 +839,45 @@ int launch_gemm_bf16w(hipStream_t s, const float* A, const uint16_t* W, const fl
                       const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
                       bool act_bf16);
 
+// The in-block-split MFMA GEMV; with ex.part the grid's y dimension is the
+// K slice and the kernel writes raw partial sums.
+static int launch_mfma_gemv(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
+                            const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
+                            const LinearExtras& ex_in) {
+    LinearExtras ex = ex_in;
+    GemvPlan p = plan_gemv(M, N, K);
+    int span = K, gy = (M + 15) / 16;
+    if (ex.part) {
+        // more tiles per block: each block's activation slice then feeds
+        // more weight rows
+        static const int split_nt = env_int("GORCH_HIP_SPLIT_NT", 4);
+        if ((N + 15) / 16 >= 4 * split_nt) p.nt = split_nt;
+        ex.kslice = ((K + ex.ksplit - 1) / ex.ksplit + 31) / 32 * 32;
+        span = ex.kslice;
+        gy = (K + ex.kslice - 1) / ex.kslice;
+        ex.ksplit = gy;
+        while (p.nw > 1 && (span + p.nw - 1) / p.nw < 32) p.nw /= 2;
+    }
+    int per = (span + p.nw - 1) / p.nw;
+    int kw = (per + 31) / 32 * 32;
+    dim3 grid((N + 16 * p.nt - 1) / (16 * p.nt), gy);
+#define GH_CASE(T, WV, UV)                                                                   \
+    if (p.nt == T && p.nw == WV && p.u == UV) {                                              \
+        launch_t<T, WV, UV>(s, grid, x, W, bias, residual, od, M, N, K, kw, epilogue, ex);   \
+        count(M <= 16 ? CNT_GEMV : CNT_GEMM);                                                \
+        return check_launch("linear_bf16");                                                  \
+    }
+#define GH_CASES_U(T, WV) GH_CASE(T, WV, 2) GH_CASE(T, WV, 4) GH_CASE(T, WV, 8)
+#define GH_CASES_W(T) GH_CASES_U(T, 1) GH_CASES_U(T, 2) GH_CASES_U(T, 4) GH_CASES_U(T, 8) GH_CASES_U(T, 16)
+    GH_CASES_W(1) GH_CASES_W(2) GH_CASES_W(4)
+#undef GH_CASES_W
+#undef GH_CASES_U
+#undef GH_CASE
+    set_error("linear_bf16: unsupported tile plan");
+    return GORCH_HIP_EUNSUPPORTED;
+}
+
+
 // M <= 16: the weight-streaming GEMV below; larger M: the tiled MFMA GEMM
 // (gemm.hip), which re-reads each weight tile only once per BM rows.
 int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
@@ -829,6 +889,13 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
             return GORCH_HIP_EUNSUPPORTED;
         }
         return launch_gemm_bf16w(s, x, W, bias, residual, od, M, N, K, epilogue, false);
+    }
+    if (ex.part) {
+        if (M > 16 || ex.ksplit < 1) {
+            set_error("linear_bf16: K-split partials need 1 <= M <= 16");
+            return GORCH_HIP_EUNSUPPORTED;
+        }
+        return launch_mfma_gemv(s, x, W, bias, residual, od, M, N, K, epilogue, ex);
     }
     static const int valu_max_m = env_int("GORCH_HIP_GEMV_VALU_MAX_M", 1);
     static const int m1_on = env_int("GORCH_HIP_GEMV_M1", 1);
@@ -853,24 +920,7 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
         if (M == 2) return launch_valu_mt<2>(s, x, W, bias, residual, od, M, N, K, epilogue, ex, T);
         return launch_valu_mt<4>(s, x, W, bias, residual, od, M, N, K, epilogue, ex, T);
     }
-    GemvPlan p = plan_gemv(M, N, K);
-    int per = (K + p.nw - 1) / p.nw;
-    int kw = (per + 31) / 32 * 32;
-    dim3 grid((N + 16 * p.nt - 1) / (16 * p.nt), (M + 15) / 16);
-#define GH_CASE(T, WV, UV)                                                                   \
-    if (p.nt == T && p.nw == WV && p.u == UV) {                                              \
-        launch_t<T, WV, UV>(s, grid, x, W, bias, residual, od, M, N, K, kw, epilogue, ex);   \
-        count(M <= 16 ? CNT_GEMV : CNT_GEMM);                                                \
-        return check_launch("linear_bf16");                                                  \
-    }
-#define GH_CASES_U(T, WV) GH_CASE(T, WV, 2) GH_CASE(T, WV, 4) GH_CASE(T, WV, 8)
-#define GH_CASES_W(T) GH_CASES_U(T, 1) GH_CASES_U(T, 2) GH_CASES_U(T, 4) GH_CASES_U(T, 8) GH_CASES_U(T, 16)
-    GH_CASES_W(1) GH_CASES_W(2) GH_CASES_W(4)
-#undef GH_CASES_W
-#undef GH_CASES_U
-#undef GH_CASE
-    set_error("linear_bf16: unsupported tile plan");
-    return GORCH_HIP_EUNSUPPORTED;
+    return launch_mfma_gemv(s, x, W, bias, residual, od, M, N, K, epilogue, ex);
 }
 
 }  // namespace gh

@@ -22,6 +22,8 @@
 #include <cstring>
 #include <vector>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace gh {
@@ -54,6 +56,10 @@ struct gorch_hip_gpt {
     // activations, grown on demand
     size_t rows_cap = 0, logit_rows_cap = 0;
     float *x = nullptr, *h = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr;
+    // batched decode (2..16 rows): K-split partials of the residual Linears
+    // and the LayerNorm row statistics they leave for the next GEMV
+    float* part = nullptr;
+    float2* stats = nullptr;
     int* ids = nullptr;
     size_t ids_cap = 0;
     hipStream_t stream = nullptr;  // engine stream (default priority), used for graph capture
@@ -77,6 +83,8 @@ static float* vc_layer(gorch_hip_kvcache* c, int l) {
     return c->v + (size_t)l * c->batch * c->capacity * c->gpt->dim;
 }
 
+constexpr int kMaxSplit = 8;  // K slices of the batched-decode residual Linears
+
 static int ensure_acts(gorch_hip_gpt* g, size_t rows, size_t logit_rows) {
     if (rows > g->rows_cap) {
         (void)hipFree(g->x);
@@ -93,6 +101,10 @@ static int ensure_acts(gorch_hip_gpt* g, size_t rows, size_t logit_rows) {
         GH_TRY(check(hipMalloc(&g->att, rows * d * 4), "hipMalloc att"));
         GH_TRY(check(hipMalloc(&g->ff, rows * 4 * d * 4), "hipMalloc ff"));
         g->rows_cap = rows;
+        if (!g->part) {
+            GH_TRY(check(hipMalloc(&g->part, (size_t)kMaxSplit * 16 * d * 4), "hipMalloc part"));
+            GH_TRY(check(hipMalloc(&g->stats, 16 * sizeof(float2)), "hipMalloc stats"));
+        }
     }
     if (logit_rows > g->logit_rows_cap) {
         (void)hipFree(g->logits);
@@ -123,7 +135,27 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
     const float eps = 1e-5f;
     const int* pos = c->state;
     const bool fused = rows <= 16;
+    // 2..16 rows: the residual Linears (Wo, FFN2) are split over K across
+    // blocks (their N = d alone gives too few blocks to pull HBM at full
+    // rate); one small per-row kernel adds the slices, bias and residual and
+    // leaves the next LayerNorm's statistics, which the following fused GEMV
+    // reads instead of recomputing them in every block.
+    const bool batched = fused && rows >= 2;
+    static const int split_blocks = [] {
+        const char* e = getenv("GORCH_HIP_SPLIT_BLOCKS");
+        return e ? atoi(e) : 300;
+    }();
+    static const int split_nt = [] {
+        const char* e = getenv("GORCH_HIP_SPLIT_NT");
+        return e ? atoi(e) : 4;
+    }();
+    auto split_for = [&](int K) {
+        const int tiles = ((d + 15) / 16 + split_nt - 1) / split_nt;
+        int S = std::min(kMaxSplit, std::max(1, split_blocks / tiles));
+        return ksplit_slices(K, S);
+    };
     GH_TRY(launch_embed_pos(s, g->wte, g->wpe, g->ids, pos, g->x, d, n, rows));
+    if (batched) GH_TRY(launch_reduce_rows(s, nullptr, 0, nullptr, g->x, rows, d, eps, g->stats));
     for (int l = 0; l < g->layers; l++) {
         const LayerW& w = g->L[l];
         OutDesc od{};
@@ -151,6 +183,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             ln2.ln_g = w.ln2_g;
             ln2.ln_b = w.ln2_b;
             ln1.ln_eps = ln2.ln_eps = eps;
+            if (batched) ln1.ln_stats = ln2.ln_stats = g->stats;
             GH_TRY(launch_linear_bf16_od(s, g->x, w.wqkv, w.bqkv, nullptr, od, rows, 3 * d, d, GORCH_HIP_EPI_NONE,
                                          ln1));
         } else {
@@ -161,7 +194,16 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         AttnArgs a{g->q, kc_layer(c, l), vc_layer(c, l), g->att, pos, 0, n, d, hd, c->capacity, d, 1,
                    1.0f / (float)sqrt((double)hd)};
         GH_TRY(launch_attn_cached(s, a, g->heads, rows));
-        GH_TRY(launch_linear_bf16(s, g->att, w.wo, w.bo, g->x, g->x, rows, d, d, GORCH_HIP_EPI_NONE));
+        if (batched) {
+            LinearExtras sp;
+            sp.part = g->part;
+            sp.ksplit = split_for(d);
+            GH_TRY(launch_linear_bf16_od(s, g->att, w.wo, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d, d,
+                                         GORCH_HIP_EPI_NONE, sp));
+            GH_TRY(launch_reduce_rows(s, g->part, sp.ksplit, w.bo, g->x, rows, d, eps, g->stats));
+        } else {
+            GH_TRY(launch_linear_bf16(s, g->att, w.wo, w.bo, g->x, g->x, rows, d, d, GORCH_HIP_EPI_NONE));
+        }
         if (fused) {
             GH_TRY(launch_linear_bf16_od(s, g->x, w.w1, w.b1, nullptr, OutDesc::plain(g->ff, 4 * d), rows, 4 * d,
                                          d, GORCH_HIP_EPI_GELU, ln2));
@@ -169,7 +211,16 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             GH_TRY(launch_layernorm(s, g->x, w.ln2_g, w.ln2_b, g->h, rows, d, eps, d));
             GH_TRY(launch_linear_bf16(s, g->h, w.w1, w.b1, nullptr, g->ff, rows, 4 * d, d, GORCH_HIP_EPI_GELU));
         }
-        GH_TRY(launch_linear_bf16(s, g->ff, w.w2, w.b2, g->x, g->x, rows, d, 4 * d, GORCH_HIP_EPI_NONE));
+        if (batched) {
+            LinearExtras sp;
+            sp.part = g->part;
+            sp.ksplit = split_for(4 * d);
+            GH_TRY(launch_linear_bf16_od(s, g->ff, w.w2, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d, 4 * d,
+                                         GORCH_HIP_EPI_NONE, sp));
+            GH_TRY(launch_reduce_rows(s, g->part, sp.ksplit, w.b2, g->x, rows, d, eps, g->stats));
+        } else {
+            GH_TRY(launch_linear_bf16(s, g->ff, w.w2, w.b2, g->x, g->x, rows, d, 4 * d, GORCH_HIP_EPI_NONE));
+        }
     }
     const int head_rows = all_rows ? rows : B;
     const float* head_in = all_rows ? g->x : g->x + (size_t)(n - 1) * d;
@@ -181,6 +232,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         lf.ln_eps = eps;
         lf.x_stride = head_stride;
         lf.argmax_key = all_rows ? nullptr : argmax_key;
+        if (batched && head_stride == d) lf.ln_stats = g->stats;  // the head's rows are x's rows
         GH_TRY(launch_linear_bf16_od(s, head_in, g->wlm, g->blm, nullptr, OutDesc::plain(g->logits, g->vocab),
                                      head_rows, g->vocab, d, GORCH_HIP_EPI_NONE, lf));
     } else {
@@ -363,6 +415,8 @@ void gorch_hip_gpt_free(gorch_hip_gpt* g) {
     (void)hipFree(g->att);
     (void)hipFree(g->ff);
     (void)hipFree(g->logits);
+    (void)hipFree(g->part);
+    (void)hipFree(g->stats);
     (void)hipFree(g->ids);
     delete g;
 }

@@ -59,6 +59,72 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* __
     for (int j = threadIdx.x; j < N; j += blockDim.x) out[j] = row[j] * inv * g[j];
 }
 
+// One block per row: x[m] += bias + sum_s part[s][m] (slices in order, the
+// residual add of a K-split Linear), then the row's LayerNorm statistics in
+// f64 (nn/layernorm.go:61-91) for the next fused-LayerNorm GEMV. Each thread
+// owns up to kRedCols columns and issues all of their slice loads before
+// adding (S <= kRedSlices), so the row costs one memory round trip.
+constexpr int kRedCols = 8, kRedSlices = 8;
+
+__global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ part, int S,
+                                                     const float* __restrict__ bias, float* __restrict__ x, int M,
+                                                     int N, float eps, float2* __restrict__ stats) {
+    __shared__ double sh[4];
+    const int m = blockIdx.x;
+    float* row = x + (size_t)m * N;
+    float v[kRedCols];
+    float p[kRedCols][kRedSlices];
+#pragma unroll
+    for (int c = 0; c < kRedCols; c++) {
+        const int j = threadIdx.x + 256 * c;
+        const bool ok = j < N;
+        v[c] = ok ? row[j] : 0.f;
+#pragma unroll
+        for (int q = 0; q < kRedSlices; q++)
+            p[c][q] = (ok && q < S) ? part[((size_t)q * M + m) * N + j] : 0.f;
+    }
+    double s1 = 0.0;
+#pragma unroll
+    for (int c = 0; c < kRedCols; c++) {
+        const int j = threadIdx.x + 256 * c;
+        if (j >= N) continue;
+        if (S > 0) {
+            float acc = p[c][0];
+#pragma unroll
+            for (int q = 1; q < kRedSlices; q++)
+                if (q < S) acc += p[c][q];
+            if (bias) acc = acc + bias[j];
+            v[c] = v[c] + acc;
+            row[j] = v[c];
+        }
+        s1 += (double)v[c];
+    }
+    if (!stats) return;
+    const double mean = block_sum_d(s1, sh) / (double)N;
+    double s2 = 0.0;
+#pragma unroll
+    for (int c = 0; c < kRedCols; c++) {
+        const int j = threadIdx.x + 256 * c;
+        if (j >= N) continue;
+        const double d = (double)v[c] - mean;
+        s2 += d * d;
+    }
+    const double var = block_sum_d(s2, sh) / (double)N;
+    if (threadIdx.x == 0) stats[m] = make_float2((float)mean, (float)(1.0 / sqrt(var + (double)eps)));
+}
+
+int launch_reduce_rows(hipStream_t s, const float* part, int S, const float* bias, float* x, int M, int N,
+                       float eps, float2* stats) {
+    if (M == 0) return GORCH_HIP_OK;
+    if (N > 256 * kRedCols || S > kRedSlices) {
+        set_error("reduce_rows: at most 2048 columns and 8 slices");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
+    hipLaunchKernelGGL(k_reduce_rows, dim3(M), dim3(256), 0, s, part, S, bias, x, M, N, eps, stats);
+    count(CNT_NORM);
+    return check_launch("reduce_rows");
+}
+
 // Row i of the input starts at x + i * in_stride (in_stride = N for a dense
 // matrix); the output is dense [M, N].
 int launch_layernorm(hipStream_t s, const float* x, const float* g, const float* b, float* y, int M, int N,
