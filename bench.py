@@ -154,6 +154,36 @@ def gpu_leg(args, shapes):
 MFMA_PEAK_TFLOPS = 2516.6  # dense bf16: 256 CU x 2.4 GHz x 4096 FLOP/clk
 
 
+def gemv_kernel(M, K, N):
+    """Which kernel libgorch_hip.so runs for a GEMV of this shape (the
+    routing of launch_linear_bf16_od in gorch_amd/csrc/gemv.hip)."""
+    if M == 1:
+        chunks = K // 8
+        if any(chunks % t == 0 and chunks // t <= 8 for t in (64, 32, 16, 8)):
+            return "k_gemv_m1"
+        return "k_gemv_valu"
+    mr = 4 if M <= 4 else (8 if M <= 8 else 16)
+    if (N + 15) // 16 >= 1024 and ((K + 127) // 128) * 16 * mr * 32 <= 128 * 1024:
+        return "k_gemv_mt"
+    return "k_linear_bf16_mfma"
+
+
+def measured_traffic(kernel, M, K, N):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 PMC summary (FETCH_SIZE / WRITE_SIZE, copy-calibrated), when
+    one exists for this kernel and shape; else None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rows = json.load(f)
+    except (OSError, ValueError):
+        return None
+    for r in rows:
+        if r.get("kernel") == kernel and tuple(r.get("shape", ())) == (M, K, N):
+            return r.get("traffic_bytes")
+    return None
+
+
 def gemm_leg(M=512, K=768, Ns=(2304, 3072)):
     """Prefill GEMM: operands resident (re-used across
     launches), timed over a graph of back-to-back launches."""
@@ -319,6 +349,7 @@ def main():
     moe = None if args.shape else moe_leg()
     cpu = None if args.no_cpu else cpu_leg(shapes, args.cpu_seconds)
     dom_bytes = algo_bytes(dom["M"], dom["K"], dom["N"])
+    dom_kernel = gemv_kernel(dom["M"], dom["K"], dom["N"])
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -340,12 +371,12 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"k_linear_bf16_mfma M={dom['M']} K={dom['K']} N={dom['N']}",
+            "kernel": f"{dom_kernel} M={dom['M']} K={dom['K']} N={dom['N']}",
             "achieved": round(dom_bytes / dom["us"] / 1e3, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom_bytes / dom["us"] / 1e3 / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(dom_kernel, dom["M"], dom["K"], dom["N"]),
             "algorithmic_bytes_per_launch": dom_bytes,
             "avg_launch_us": dom["us"],
         },
