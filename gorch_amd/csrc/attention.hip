@@ -134,12 +134,136 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_cached(AttnArgs a) {
     }
 }
 
+// k_attn_rows: the same computation with lanes over (key, 16-byte chunk of
+// the head): HD4 = hd/4 lanes read one key's 64..512-byte head slice, so a
+// wavefront instruction covers 64/HD4 keys and a lane issues the loads of
+// UNR keys at once. Scores, softmax and P.V then take about one memory round
+// trip each, instead of one per key-loop iteration (what limits the
+// per-(head, row) block when the context is short and blocks are few).
+template <int HD4, int UNR>
+__global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
+    extern __shared__ float sc[];  // [visible keys]
+    __shared__ float red[16];
+    __shared__ float4 po[4][HD4];
+    constexpr int KPI = 64 / HD4;  // keys per wavefront instruction
+    constexpr int KB = 4 * KPI;    // keys per block instruction
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane % HD4, slot = wave * KPI + lane / HD4;
+
+    const int h = blockIdx.x;
+    const int row = blockIdx.y;
+    const int b = row / a.new_seq;
+    const int i = row - b * a.new_seq;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    const int T = a.causal ? pos + i + 1 : pos + a.new_seq;
+    const int kvh = a.kv_heads ? h / ((int)gridDim.x / a.kv_heads) : h;
+    const int kvd = a.kv_dim ? a.kv_dim : a.dim;
+    const size_t base = ((size_t)b * a.max_seq) * kvd + (size_t)kvh * (4 * HD4);
+    const float4* K4 = reinterpret_cast<const float4*>(a.kc + base);
+    const float4* V4 = reinterpret_cast<const float4*>(a.vc + base);
+    const int kvd4 = kvd >> 2;
+    const float4 q = *reinterpret_cast<const float4*>(a.q + (size_t)row * a.q_stride + h * (4 * HD4) + 4 * c);
+
+    float lmax = -INFINITY;
+    for (int j0 = 0; j0 < T; j0 += KB * UNR) {
+        float4 kv[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int j = j0 + KB * u + slot;
+            kv[u] = j < T ? K4[(size_t)j * kvd4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            float d = q.x * kv[u].x + q.y * kv[u].y + q.z * kv[u].z + q.w * kv[u].w;
+#pragma unroll
+            for (int o = 1; o < HD4; o <<= 1) d += __shfl_xor(d, o, 64);
+            const int j = j0 + KB * u + slot;
+            if (c == 0 && j < T) {
+                const float sj = d * a.scale;
+                sc[j] = sj;
+                lmax = fmaxf(lmax, sj);
+            }
+        }
+    }
+    const float mx = block_max(lmax, red);
+    float lsum = 0.f;
+    for (int j = threadIdx.x; j < T; j += blockDim.x) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        lsum += e;
+    }
+    const float sum = block_sum(lsum, red);
+    const float rs = 1.0f / sum;
+    for (int j = threadIdx.x; j < T; j += blockDim.x) sc[j] = a.recip ? sc[j] * rs : sc[j] / sum;
+    __syncthreads();
+
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j0 = 0; j0 < T; j0 += KB * UNR) {
+        float4 vv[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int j = j0 + KB * u + slot;
+            vv[u] = j < T ? V4[(size_t)j * kvd4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int j = j0 + KB * u + slot;
+            const float p = j < T ? sc[j] : 0.f;
+            o.x += p * vv[u].x;
+            o.y += p * vv[u].y;
+            o.z += p * vv[u].z;
+            o.w += p * vv[u].w;
+        }
+    }
+    // the wave's key slots, then the 4 waves in order
+#pragma unroll
+    for (int off = HD4; off < 64; off <<= 1) {
+        o.x += __shfl_xor(o.x, off, 64);
+        o.y += __shfl_xor(o.y, off, 64);
+        o.z += __shfl_xor(o.z, off, 64);
+        o.w += __shfl_xor(o.w, off, 64);
+    }
+    if (lane < HD4) po[wave][c] = o;
+    __syncthreads();
+    if (wave == 0 && lane < HD4) {
+        float4 t = po[0][c];
+#pragma unroll
+        for (int w = 1; w < 4; w++) {
+            t.x += po[w][c].x;
+            t.y += po[w][c].y;
+            t.z += po[w][c].z;
+            t.w += po[w][c].w;
+        }
+        *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + h * (4 * HD4) + 4 * c) = t;
+    }
+}
+
 // 4 waves per (head, row) block when there are enough blocks to fill the
 // GPU; 16 waves when the visible context is long and blocks are few, so each
 // block keeps more of the KV stream in flight.
 int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
     size_t lds = (size_t)a.max_seq * sizeof(float);
     const int blocks = heads * rows;
+    static const int rows_kernel = [] {
+        const char* e = getenv("GORCH_HIP_ATTN_ROWS");
+        return e ? atoi(e) : 1;
+    }();
+    const bool aligned = (a.q_stride % 4 == 0) && (a.dim % 4 == 0) && ((a.kv_dim ? a.kv_dim : a.dim) % 4 == 0) &&
+                         ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.kc) |
+                           reinterpret_cast<uintptr_t>(a.vc) | reinterpret_cast<uintptr_t>(a.out)) % 16 == 0);
+    // short caches: the (key, chunk)-lane kernel; long ones stream better
+    // through the per-dim kernel below
+    if (rows_kernel && aligned && a.max_seq <= 256 && (a.hd == 64 || a.hd == 128 || a.hd == 32 || a.hd == 16)) {
+        const dim3 grid(heads, rows);
+        switch (a.hd) {
+            case 128: hipLaunchKernelGGL((k_attn_rows<32, 8>), grid, dim3(256), lds, s, a); break;
+            case 64: hipLaunchKernelGGL((k_attn_rows<16, 8>), grid, dim3(256), lds, s, a); break;
+            case 32: hipLaunchKernelGGL((k_attn_rows<8, 8>), grid, dim3(256), lds, s, a); break;
+            default: hipLaunchKernelGGL((k_attn_rows<4, 8>), grid, dim3(256), lds, s, a); break;
+        }
+        count(CNT_ATTENTION);
+        return check_launch("attn_rows");
+    }
     if (blocks < 1024 && a.max_seq >= 128)
         hipLaunchKernelGGL(k_attn_cached<16>, dim3(heads, rows), dim3(1024), lds, s, a);
     else

@@ -364,6 +364,11 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
         xr[c][4] = a1.x; xr[c][5] = a1.y; xr[c][6] = a1.z; xr[c][7] = a1.w;
     }
     if (LN) {
+        float fm, inv;
+        if (ex.ln_stats) {
+            fm = ex.ln_stats[0].x;
+            inv = ex.ln_stats[0].y;
+        } else {
         // the wave's lanes hold the row RPI times over (one copy per rloc):
         // sum over the first T lanes only
         double s1 = 0.0;
@@ -383,8 +388,9 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
                     s2 += dd * dd;
                 }
         const double var = wave_sum_d(s2) / (double)K;
-        const float inv = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
-        const float fm = (float)mean;
+        inv = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
+        fm = (float)mean;
+        }
 #pragma unroll
         for (int c = 0; c < C; c++) {
             const int k = 8 * (sub + T * c);

@@ -233,6 +233,12 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         lf.x_stride = head_stride;
         lf.argmax_key = all_rows ? nullptr : argmax_key;
         if (batched && head_stride == d) lf.ln_stats = g->stats;  // the head's rows are x's rows
+        if (head_rows == 1 && g->vocab >= 16384) {
+            // one row, many weight rows: every wave of the register GEMV
+            // would recompute the statistics; one small kernel does it once
+            GH_TRY(launch_reduce_rows(s, nullptr, 0, nullptr, const_cast<float*>(head_in), 1, d, eps, g->stats));
+            lf.ln_stats = g->stats;
+        }
         GH_TRY(launch_linear_bf16_od(s, head_in, g->wlm, g->blm, nullptr, OutDesc::plain(g->logits, g->vocab),
                                      head_rows, g->vocab, d, GORCH_HIP_EPI_NONE, lf));
     } else {
