@@ -40,7 +40,8 @@ struct LinearExtras {
     // (bias, activation and residual are then applied by the reduction)
     float* part = nullptr;
     int ksplit = 1;
-    int kslice = 0;  // K per slice (set by the launcher)
+    int kslice = 0;    // K per slice (set by the launcher)
+    int split_nt = 0;  // 16-row tiles per block in split mode (0: 4)
 };
 // Number of K slices a K-split Linear actually uses for a requested count
 // (slices are multiples of 32 wide).
@@ -48,6 +49,12 @@ inline int ksplit_slices(int K, int S) {
     const int ks = ((K + S - 1) / S + 31) / 32 * 32;
     return (K + ks - 1) / ks;
 }
+// Per-(device, stream) scratch for K-split partials; nullptr when it would
+// have to grow during stream capture or the allocation fails.
+void* stream_scratch(hipStream_t s, size_t bytes);
+// Epilogue of a K-split Linear over partials part[S][M][N] (S <= 8).
+int launch_splitk_epilogue(hipStream_t s, const float* part, int S, int M, int N, const float* bias,
+                           const float* residual, const OutDesc& od, int epilogue);
 // Row reduction after a K-split Linear: x[m] = x[m] + bias + sum_s part[s][m]
 // (slices added in order; S = 0 leaves x as is), then the LayerNorm
 // statistics of the new row into stats[m] when stats is not null.

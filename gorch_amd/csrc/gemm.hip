@@ -188,6 +188,11 @@ int launch_gemm_bf16w(hipStream_t s, const float* A, const uint16_t* W, const fl
     const long long big = (long long)((M + 127) / 128) * ((N + 127) / 128);
     const long long mid = (long long)((M + 63) / 64) * ((N + 127) / 128);
     int tile = big >= 256 ? 2 : (mid >= 256 ? 1 : 0);
+    static const int tile_env = [] {
+        const char* e = getenv("GORCH_HIP_GEMM_TILE");
+        return e ? atoi(e) : -1;
+    }();
+    if (tile_env >= 0) tile = tile_env;
     if (act_bf16) {
         if (tile == 2) launch_gemm_t<128, 128, false>(s, A, W, bias, residual, od, M, N, K, epilogue);
         else if (tile == 1) launch_gemm_t<64, 128, false>(s, A, W, bias, residual, od, M, N, K, epilogue);

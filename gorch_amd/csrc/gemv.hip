@@ -657,6 +657,44 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
     }
 }
 
+// Epilogue of a K-split Linear: y[m, n] = epi(sum_s part[s][m][n] + bias[n])
+// (+ residual), slices added in order, written through the output
+// descriptor. All slice loads of an element are issued before the adds.
+constexpr int kEpiSlices = 8;
+__global__ __launch_bounds__(256) void k_splitk_epilogue(const float* __restrict__ part, int S, int M, int N,
+                                                         const float* __restrict__ bias, const float* residual,
+                                                         OutDesc od, int epilogue) {
+    const int64_t total = (int64_t)M * N;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+    float p[kEpiSlices];
+#pragma unroll
+    for (int q = 0; q < kEpiSlices; q++) p[q] = q < S ? part[(size_t)q * total + i] : 0.f;
+    float sum = p[0];
+#pragma unroll
+    for (int q = 1; q < kEpiSlices; q++)
+        if (q < S) sum += p[q];
+    if (bias) sum = sum + bias[n];
+    if (epilogue == GORCH_HIP_EPI_GELU) sum = gelu_tanh(sum);
+    if (residual) sum = residual[i] + sum;
+    *od.at(m, n) = sum;
+}
+
+int launch_splitk_epilogue(hipStream_t s, const float* part, int S, int M, int N, const float* bias,
+                           const float* residual, const OutDesc& od, int epilogue) {
+    if (S < 1 || S > kEpiSlices) {
+        set_error("splitk_epilogue: 1..8 slices");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
+    const int64_t total = (int64_t)M * N;
+    if (total == 0) return GORCH_HIP_OK;
+    hipLaunchKernelGGL(k_splitk_epilogue, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, S, M, N,
+                       bias, residual, od, epilogue);
+    count(CNT_GEMV);
+    return check_launch("splitk_epilogue");
+}
+
 // (T, C) for the register-x M = 1 kernel: T lanes per row, C 16-byte chunks
 // per lane, C <= 8; {0, 0} when K does not fit.
 static void m1_shape(int K, int* T, int* C) {
@@ -856,7 +894,8 @@ static int launch_mfma_gemv(hipStream_t s, const float* x, const uint16_t* W, co
     if (ex.part) {
         // more tiles per block: each block's activation slice then feeds
         // more weight rows
-        static const int split_nt = env_int("GORCH_HIP_SPLIT_NT", 4);
+        static const int split_nt_env = env_int("GORCH_HIP_SPLIT_NT", 0);
+        const int split_nt = split_nt_env ? split_nt_env : (ex.split_nt ? ex.split_nt : 4);
         if ((N + 15) / 16 >= 4 * split_nt) p.nt = split_nt;
         ex.kslice = ((K + ex.ksplit - 1) / ex.ksplit + 31) / 32 * 32;
         span = ex.kslice;
@@ -902,6 +941,26 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
             return GORCH_HIP_EUNSUPPORTED;
         }
         return launch_mfma_gemv(s, x, W, bias, residual, od, M, N, K, epilogue, ex);
+    }
+    // 2..16 rows over a narrow weight (few 16-row tiles) and a long K: split
+    // K across blocks into partials in the stream's scratch, then one small
+    // epilogue kernel (a CU streams only ~20 GB/s, so 48..128 tiles alone
+    // cannot pull the weight at full rate)
+    static const int auto_split = env_int("GORCH_HIP_GEMV_SPLIT", 1);
+    const int ntiles_all = (N + 15) / 16;
+    if (auto_split && M >= 2 && !ex.argmax_key && ntiles_all < 128 && K >= 1024) {
+        const int blocks_per_slice = (ntiles_all + 1) / 2;  // 2 tiles per block
+        const int S = ksplit_slices(K, std::min(kEpiSlices, std::max(2, 300 / blocks_per_slice)));
+        void* part = S >= 2 ? stream_scratch(s, (size_t)S * M * N * sizeof(float)) : nullptr;
+        if (part) {
+            LinearExtras sx = ex;
+            sx.part = static_cast<float*>(part);
+            sx.ksplit = S;
+            sx.split_nt = 2;
+            GH_TRY(launch_mfma_gemv(s, x, W, nullptr, nullptr, OutDesc::plain(nullptr, N), M, N, K,
+                                    GORCH_HIP_EPI_NONE, sx));
+            return launch_splitk_epilogue(s, sx.part, S, M, N, bias, residual, od, epilogue);
+        }
     }
     static const int valu_max_m = env_int("GORCH_HIP_GEMV_VALU_MAX_M", 1);
     static const int m1_on = env_int("GORCH_HIP_GEMV_M1", 1);

@@ -22,7 +22,11 @@
 
 namespace gh {
 
-constexpr int kMoeBM = 64, kMoeBN = 64, kMoeBK = 64, kMoeLD = kMoeBK + 8;
+// Grouped-GEMM tiles: kMoeBM packed rows (the routing tile table's unit) x
+// BN output columns, K stepped by kMoeBK. 128-row tiles halve the weight
+// re-reads through L2 (the bound of these GEMMs) against 64-row ones.
+constexpr int kMoeBM = 128, kMoeBK = 64, kMoeLD = kMoeBK + 8;
+constexpr int kMoeBNDual = 64, kMoeBNDown = 128;
 constexpr int kMaxExperts = 64;
 constexpr int kMaxTopK = 8;
 
@@ -71,87 +75,136 @@ static size_t moe_layout(int M, int dim, int ffn, int E, int K, char* base, MoeW
     return off;
 }
 
-// One 128-thread block. Thread t owns tokens [t*chunk, (t+1)*chunk).
-constexpr int kRouteThreads = 128;
+// One 1024-thread block; thread t takes tokens t, t + 1024, ... (rounds).
+// Per round: top-K and the routing weights of its token, then the token's
+// rank inside each chosen expert's group — earlier rounds' counts, then the
+// counts of lower waves and lower lanes of this round from wavefront
+// ballots — so the grouping is stable in token order like the reference's
+// per-expert token lists. Ranks are parked in inv; once every expert's size
+// is known the bases, the GEMM tile table (one thread per expert) and the
+// packed-row maps follow.
+constexpr int kRouteThreads = 1024, kRouteWaves = kRouteThreads / 64;
 __global__ __launch_bounds__(kRouteThreads) void k_moe_route(const float* __restrict__ logits, int M, int E, int K,
                                                              MoeWs ws) {
-    __shared__ int cnt[kRouteThreads][kMaxExperts + 1];
+    __shared__ int wtot[kRouteWaves][kMaxExperts];
+    __shared__ int run[kMaxExperts];
     __shared__ int base[kMaxExperts + 1];
-    const int t = threadIdx.x;
-    const int chunk = (M + kRouteThreads - 1) / kRouteThreads;
-    const int t0 = min(M, t * chunk), t1 = min(M, t0 + chunk);
-    for (int e = 0; e < E; e++) cnt[t][e] = 0;
-    for (int tok = t0; tok < t1; tok++) {
-        const float* row = logits + (size_t)tok * E;
+    __shared__ int tbase[kMaxExperts + 1];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const unsigned long long lt_mask = (1ull << lane) - 1ull;
+    if (t < E) run[t] = 0;
+    __syncthreads();
+    for (int r0 = 0; r0 < M; r0 += kRouteThreads) {
+        const int tok = r0 + t;
+        const bool live = tok < M;
         int idx[kMaxTopK];
-        float val[kMaxTopK];
-        // top-K, descending; ties keep the lower index first
-        for (int s = 0; s < K; s++) {
-            int best = -1;
-            float bv = 0.f;
-            for (int j = 0; j < E; j++) {
-                bool taken = false;
-                for (int u = 0; u < s; u++) taken |= (idx[u] == j);
-                if (taken) continue;
-                const float v = row[j];
-                if (best < 0 || v > bv) {
-                    best = j;
-                    bv = v;
+#pragma unroll
+        for (int s = 0; s < kMaxTopK; s++) idx[s] = -1;
+        if (live) {
+            // the token's logits in registers (one load each, all in flight)
+            const float* row = logits + (size_t)tok * E;
+            float lv[kMaxExperts];
+#pragma unroll
+            for (int j = 0; j < kMaxExperts; j++) lv[j] = j < E ? row[j] : 0.f;
+            float val[kMaxTopK];
+            unsigned long long taken = 0ull;
+            // top-K, descending; ties keep the lower index first (a NaN never
+            // replaces the running best, as in the reference's > compare)
+#pragma unroll
+            for (int s = 0; s < kMaxTopK; s++) {
+                if (s >= K) break;
+                int best = -1;
+                float bv = 0.f;
+#pragma unroll
+                for (int j = 0; j < kMaxExperts; j++) {
+                    if (j >= E || ((taken >> j) & 1ull)) continue;
+                    if (best < 0 || lv[j] > bv) {
+                        best = j;
+                        bv = lv[j];
+                    }
                 }
+                idx[s] = best;
+                val[s] = bv;
+                taken |= 1ull << best;
             }
-            idx[s] = best;
-            val[s] = bv;
+            // softmaxRows: max, exp in f64 rounded to f32, f32 sum, divide
+            float mx = val[0];
+#pragma unroll
+            for (int s = 1; s < kMaxTopK; s++)
+                if (s < K) mx = val[s] > mx ? val[s] : mx;
+            float e_[kMaxTopK];
+            float sum = 0.f;
+#pragma unroll
+            for (int s = 0; s < kMaxTopK; s++)
+                if (s < K) {
+                    e_[s] = (float)exp((double)(val[s] - mx));
+                    sum += e_[s];
+                }
+#pragma unroll
+            for (int s = 0; s < kMaxTopK; s++)
+                if (s < K) {
+                    ws.topi[(size_t)tok * K + s] = idx[s];
+                    ws.topw[(size_t)tok * K + s] = e_[s] / sum;
+                }
         }
-        // softmaxRows: max, exp in f64 rounded to f32, f32 sum, divide
-        float mx = val[0];
-        for (int s = 1; s < K; s++) mx = val[s] > mx ? val[s] : mx;
-        float e_[kMaxTopK];
-        float sum = 0.f;
-        for (int s = 0; s < K; s++) {
-            e_[s] = (float)exp((double)(val[s] - mx));
-            sum += e_[s];
-        }
-        for (int s = 0; s < K; s++) {
-            ws.topi[(size_t)tok * K + s] = idx[s];
-            ws.topw[(size_t)tok * K + s] = e_[s] / sum;
-            cnt[t][idx[s]]++;
-        }
-    }
-    __syncthreads();
-    // per-expert exclusive scan over threads (token order), expert bases
-    if (t < E) {
-        int run = 0;
-        for (int u = 0; u < kRouteThreads; u++) {
-            int c = cnt[u][t];
-            cnt[u][t] = run;
-            run += c;
-        }
-        base[t] = run;  // total for expert t, turned into a base below
-    }
-    __syncthreads();
-    if (t == 0) {
-        int run = 0, nt = 0;
+        // this round's per-wave counts and lane prefixes, expert by expert
+        int pre[kMaxTopK];
+#pragma unroll
+        for (int s = 0; s < kMaxTopK; s++) pre[s] = 0;
         for (int e = 0; e < E; e++) {
-            int n = base[e];
-            base[e] = run;
-            for (int r = 0; r < n; r += kMoeBM) {
-                ws.tile_e[nt] = e;
-                ws.tile_r0[nt] = run + r;
-                ws.tile_n[nt] = min(kMoeBM, n - r);
-                nt++;
-            }
-            run += n;
+            bool mine = false;
+#pragma unroll
+            for (int s = 0; s < kMaxTopK; s++) mine |= (idx[s] == e);
+            const unsigned long long bits = __ballot(mine);
+            if (lane == 0) wtot[wave][e] = __popcll(bits);
+            const int lp = __popcll(bits & lt_mask);
+#pragma unroll
+            for (int s = 0; s < kMaxTopK; s++)
+                if (idx[s] == e) pre[s] = lp;
         }
+        __syncthreads();
+        if (live)
+#pragma unroll
+            for (int s = 0; s < kMaxTopK; s++) {
+                if (s >= K) break;
+                const int e = idx[s];
+                int rank = run[e] + pre[s];
+                for (int w = 0; w < wave; w++) rank += wtot[w][e];
+                ws.inv[(size_t)tok * K + s] = rank;  // rank inside expert e for now
+            }
+        __syncthreads();
+        if (t < E)
+            for (int w = 0; w < kRouteWaves; w++) run[t] += wtot[w][t];
+        __syncthreads();
+    }
+    if (t == 0) {
+        int b = 0, nt = 0;
+        for (int e = 0; e < E; e++) {
+            base[e] = b;
+            tbase[e] = nt;
+            b += run[e];
+            nt += (run[e] + kMoeBM - 1) / kMoeBM;
+        }
+        base[E] = b;
+        tbase[E] = nt;
         *ws.ntiles = nt;
     }
     __syncthreads();
-    for (int tok = t0; tok < t1; tok++)
+    if (t < E) {
+        const int n = run[t];
+        for (int r = 0, i = tbase[t]; r < n; r += kMoeBM, i++) {
+            ws.tile_e[i] = t;
+            ws.tile_r0[i] = base[t] + r;
+            ws.tile_n[i] = min(kMoeBM, n - r);
+        }
+    }
+    for (int tok = t; tok < M; tok += kRouteThreads)
         for (int s = 0; s < K; s++) {
-            const int e = ws.topi[(size_t)tok * K + s];
-            const int p = base[e] + cnt[t][e]++;
+            const size_t a = (size_t)tok * K + s;
+            const int p = base[ws.topi[a]] + ws.inv[a];
             ws.perm_tok[p] = tok;
-            ws.perm_w[p] = ws.topw[(size_t)tok * K + s];
-            ws.inv[(size_t)tok * K + s] = p;
+            ws.perm_w[p] = ws.topw[a];
+            ws.inv[a] = p;
         }
 }
 
@@ -191,28 +244,31 @@ __global__ void k_moe_combine(const float* __restrict__ yg, const int* __restric
 // expert's weights bf16 [N, Kd]. DUAL: a second weight (up) accumulates
 // beside the first (gate) and the epilogue writes SwiGLU(gate, up). Else the
 // epilogue multiplies by the packed row's routing weight.
-template <bool DUAL>
+template <bool DUAL, int BN>
 __global__ __launch_bounds__(256) void k_moe_gemm(const float* __restrict__ A, const uint16_t* __restrict__ W1,
                                                   const uint16_t* __restrict__ W2, const float* __restrict__ b1,
                                                   const float* __restrict__ b2, float* __restrict__ C, int N,
                                                   int Kd, MoeWs ws) {
     constexpr int NB = DUAL ? 2 : 1;
-    __shared__ __align__(16) uint16_t As[2][kMoeBM][kMoeLD];
-    __shared__ __align__(16) uint16_t Ws[NB][kMoeBN][kMoeLD];
+    constexpr int BM = kMoeBM;
+    constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;  // 2x2 waves
+    constexpr int A_F4 = BM * kMoeBK / 4 / 256, W_U4 = BN * kMoeBK / 8 / 256;
+    __shared__ __align__(16) uint16_t As[2][BM][kMoeLD];
+    __shared__ __align__(16) uint16_t Ws[NB][BN][kMoeLD];
     if ((int)blockIdx.y >= *ws.ntiles) return;
     const int e = ws.tile_e[blockIdx.y], r0 = ws.tile_r0[blockIdx.y], nrows = ws.tile_n[blockIdx.y];
-    const int n0 = blockIdx.x * kMoeBN;
+    const int n0 = blockIdx.x * BN;
     const uint16_t* Wb[2] = {W1 + (size_t)e * N * Kd, DUAL ? W2 + (size_t)e * N * Kd : nullptr};
     const float* bb[2] = {b1 ? b1 + (size_t)e * N : nullptr, (DUAL && b2) ? b2 + (size_t)e * N : nullptr};
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;  // 2x2 waves, 32x32 each
+    const int wm = wave >> 1, wn = wave & 1;
     const int r = lane & 15, g = lane >> 4;
-    float4 ra[4];
-    uint4 rw[NB][2];
+    float4 ra[A_F4];
+    uint4 rw[NB][W_U4];
     auto gload = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < A_F4; i++) {
             const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
             const int k = k0 + 4 * c4;
             ra[i] = (row < nrows && k < Kd) ? *reinterpret_cast<const float4*>(A + (size_t)(r0 + row) * Kd + k)
@@ -221,7 +277,7 @@ __global__ __launch_bounds__(256) void k_moe_gemm(const float* __restrict__ A, c
 #pragma unroll
         for (int b = 0; b < NB; b++)
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
+            for (int i = 0; i < W_U4; i++) {
                 const int idx = tid + 256 * i, row = idx >> 3, c8 = idx & 7;
                 const int n = n0 + row, k = k0 + 8 * c8;
                 rw[b][i] = (n < N && k < Kd) ? *reinterpret_cast<const uint4*>(Wb[b] + (size_t)n * Kd + k)
@@ -230,7 +286,7 @@ __global__ __launch_bounds__(256) void k_moe_gemm(const float* __restrict__ A, c
     };
     auto sstore = [&]() {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < A_F4; i++) {
             const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
             const float f[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
             uint16_t hi[4], lo[4];
@@ -248,19 +304,19 @@ __global__ __launch_bounds__(256) void k_moe_gemm(const float* __restrict__ A, c
 #pragma unroll
         for (int b = 0; b < NB; b++)
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
+            for (int i = 0; i < W_U4; i++) {
                 const int idx = tid + 256 * i, row = idx >> 3, c8 = idx & 7;
                 *reinterpret_cast<uint4*>(&Ws[b][row][8 * c8]) = rw[b][i];
             }
     };
 
-    floatx4 acc[NB][2][2];
+    floatx4 acc[NB][TM][TN];
 #pragma unroll
     for (int b = 0; b < NB; b++)
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) acc[b][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < TN; j++) acc[b][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     gload(0);
     for (int k0 = 0; k0 < Kd; k0 += kMoeBK) {
@@ -270,38 +326,51 @@ __global__ __launch_bounds__(256) void k_moe_gemm(const float* __restrict__ A, c
         if (k0 + kMoeBK < Kd) gload(k0 + kMoeBK);
 #pragma unroll
         for (int kk = 0; kk < kMoeBK; kk += 32) {
+            bf16x8 wf[NB][TN];
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const bf16x8 ahi = *reinterpret_cast<const bf16x8*>(&As[0][wm * 32 + i * 16 + r][kk + 8 * g]);
-                const bf16x8 alo = *reinterpret_cast<const bf16x8*>(&As[1][wm * 32 + i * 16 + r][kk + 8 * g]);
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    wf[b][j] = *reinterpret_cast<const bf16x8*>(&Ws[b][wn * WN + j * 16 + r][kk + 8 * g]);
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const bf16x8 ahi = *reinterpret_cast<const bf16x8*>(&As[0][wm * WM + i * 16 + r][kk + 8 * g]);
+                const bf16x8 alo = *reinterpret_cast<const bf16x8*>(&As[1][wm * WM + i * 16 + r][kk + 8 * g]);
 #pragma unroll
                 for (int b = 0; b < NB; b++)
 #pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        const bf16x8 wf = *reinterpret_cast<const bf16x8*>(&Ws[b][wn * 32 + j * 16 + r][kk + 8 * g]);
-                        acc[b][i][j] = mfma16x16x32(ahi, wf, acc[b][i][j]);
-                        acc[b][i][j] = mfma16x16x32(alo, wf, acc[b][i][j]);
+                    for (int j = 0; j < TN; j++) {
+                        acc[b][i][j] = mfma16x16x32(ahi, wf[b][j], acc[b][i][j]);
+                        acc[b][i][j] = mfma16x16x32(alo, wf[b][j], acc[b][i][j]);
                     }
             }
         }
     }
 
+    float bn[NB][TN];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int b = 0; b < NB; b++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int n = n0 + wn * 32 + j * 16 + r;
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn * WN + j * 16 + r;
+            bn[b][j] = (bb[b] && n < N) ? bb[b][n] : 0.f;
+        }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn * WN + j * 16 + r;
             if (n >= N) continue;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                const int row = wm * 32 + i * 16 + 4 * g + v;
+                const int row = wm * WM + i * 16 + 4 * g + v;
                 if (row >= nrows) continue;
                 const int p = r0 + row;
                 float s = acc[0][i][j][v];
-                if (bb[0]) s = s + bb[0][n];
+                if (bb[0]) s = s + bn[0][j];
                 if (DUAL) {
                     float u = acc[NB - 1][i][j][v];
-                    if (bb[1]) u = u + bb[1][n];
+                    if (bb[1]) u = u + bn[NB - 1][j];
                     s = s * sigmoidf_ref(s) * u;  // SwiGLU: gate * sigma(gate) * up
                 } else {
                     s = s * ws.perm_w[p];          // weighted = exOut * w
@@ -347,11 +416,11 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
     hipLaunchKernelGGL(k_moe_gather, dim3(gblocks), dim3(256), 0, s, x, ws.perm_tok, ws.xg, MK, d);
     GH_TRY(check_launch("moe_gather"));
     const int max_tiles = MK / kMoeBM + E + 1;
-    hipLaunchKernelGGL(k_moe_gemm<true>, dim3((F + kMoeBN - 1) / kMoeBN, max_tiles), dim3(256), 0, s, ws.xg,
-                       w->wgate, w->wup, w->bgate, w->bup, ws.h, F, d, ws);
+    hipLaunchKernelGGL((k_moe_gemm<true, kMoeBNDual>), dim3((F + kMoeBNDual - 1) / kMoeBNDual, max_tiles),
+                       dim3(256), 0, s, ws.xg, w->wgate, w->wup, w->bgate, w->bup, ws.h, F, d, ws);
     GH_TRY(check_launch("moe_gemm_gate_up"));
-    hipLaunchKernelGGL(k_moe_gemm<false>, dim3((d + kMoeBN - 1) / kMoeBN, max_tiles), dim3(256), 0, s, ws.h,
-                       w->wdown, nullptr, w->bdown, nullptr, ws.yg, d, F, ws);
+    hipLaunchKernelGGL((k_moe_gemm<false, kMoeBNDown>), dim3((d + kMoeBNDown - 1) / kMoeBNDown, max_tiles),
+                       dim3(256), 0, s, ws.h, w->wdown, nullptr, w->bdown, nullptr, ws.yg, d, F, ws);
     GH_TRY(check_launch("moe_gemm_down"));
     const int cblocks = (int)std::min<int64_t>(8192, ((int64_t)M * d + 255) / 256);
     hipLaunchKernelGGL(k_moe_combine, dim3(cblocks), dim3(256), 0, s, ws.yg, ws.inv, ws.topi, out, M, K, d);

@@ -2,7 +2,9 @@
 // metal/shim.m:120-437 (device, queue, buffers) and ops.go:15-78 (counters).
 #include <atomic>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "common.h"
 
@@ -26,6 +28,49 @@ hipStream_t stream_of(void* s) { return reinterpret_cast<hipStream_t>(s); }
 static std::atomic<uint64_t> g_counts[CNT_COUNT];
 
 void count(Counter c) { g_counts[c].fetch_add(1, std::memory_order_relaxed); }
+
+// Scratch for K-split partial sums, one buffer per (device, stream): work on
+// one stream is ordered, so consecutive launches on it can share it. A
+// buffer only grows outside stream capture (capture then uses the unsplit
+// kernel) and is never freed, since a captured graph may still point at it.
+namespace {
+struct StreamScratch {
+    int dev;
+    hipStream_t stream;
+    void* ptr;
+    size_t bytes;
+};
+std::mutex g_scratch_mu;
+std::vector<StreamScratch> g_scratch;
+}  // namespace
+
+void* stream_scratch(hipStream_t s, size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    StreamScratch* e = nullptr;
+    for (auto& w : g_scratch)
+        if (w.dev == dev && w.stream == s) e = &w;
+    if (e && e->bytes >= bytes) return e->ptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    const size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    void* p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (e) {
+        e->ptr = p;
+        e->bytes = want;
+    } else {
+        g_scratch.push_back({dev, s, p, want});
+    }
+    return p;
+}
 
 }  // namespace gh
 

@@ -64,7 +64,9 @@ def test_gemv_microbench_shapes(gpu, M, K, N):
     x, W, b = syn.gemv_inputs(M, K, N, seed=M * 7 + K)
     gpu.reset_dispatch_counts()
     got = run_linear(gpu, x, W, b)
-    assert gpu.dispatch_counts()["gemv"] == 1          # the HIP kernel ran
+    # the HIP GEMV ran: one launch, or two when K is split across blocks
+    # (narrow N, M >= 2: partials, then the epilogue kernel)
+    assert gpu.dispatch_counts()["gemv"] in (1, 2)
     ref = orc.linear(x, W, b)
     assert rel_err(got, ref) <= 1e-3
     f64 = x.astype(np.float64) @ orc.bf16_to_f32(W).astype(np.float64).T
@@ -73,7 +75,7 @@ def test_gemv_microbench_shapes(gpu, M, K, N):
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 8), (3, 7, 40), (16, 65, 128), (5, 16, 3072), (2, 33, 6400),
                                    (16, 6400, 1600), (16, 1600, 6400), (13, 4800, 1600), (17, 100, 96),
-                                   (33, 65, 128), (64, 300, 256)])
+                                   (33, 65, 128), (64, 300, 256), (7, 200, 4104), (16, 1000, 1032)])
 def test_linear_ragged_shapes(gpu, M, N, K):
     rng = np.random.default_rng(M * 1000 + N + K)
     x = rng.standard_normal((M, K)).astype(np.float32)
