@@ -63,6 +63,14 @@ struct gorch_hip_gpt {
     int* ids = nullptr;
     size_t ids_cap = 0;
     hipStream_t stream = nullptr;  // engine stream (default priority), used for graph capture
+    // generate_cached keeps its KV cache and the captured decode-step graph
+    // between calls with the same (batch, capacity) while the buffers the
+    // graph points at are unchanged, so repeated generation does not pay the
+    // capture and instantiation again
+    gorch_hip_kvcache* gen_cache = nullptr;
+    hipGraph_t gen_graph = nullptr;
+    hipGraphExec_t gen_exec = nullptr;
+    std::vector<const void*> gen_sig;
 };
 
 struct gorch_hip_kvcache {
@@ -414,6 +422,9 @@ void gorch_hip_gpt_free(gorch_hip_gpt* g) {
         (void)hipStreamSynchronize(g->stream);
         (void)hipStreamDestroy(g->stream);
     }
+    if (g->gen_exec) (void)hipGraphExecDestroy(g->gen_exec);
+    if (g->gen_graph) (void)hipGraphDestroy(g->gen_graph);
+    gorch_hip_kvcache_free(g->gen_cache);
     (void)hipFree(g->blob);
     (void)hipFree(g->x);
     (void)hipFree(g->h);
@@ -526,12 +537,26 @@ int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* g, const int* prompts
     }
     const int capacity = len;
     GH_TRY(check(hipStreamSynchronize(stream_of(stream)), "caller stream sync"));
-    gorch_hip_kvcache* c = gorch_hip_kvcache_create(g, batch, capacity);
-    if (!c) return GORCH_HIP_ENOMEM;
     hipStream_t s = g->stream;
+    gorch_hip_kvcache* c = g->gen_cache;
+    if (c && c->batch == batch && c->capacity == capacity) {
+        // reuse: empty cache, zero keys (the graph reads both from device memory)
+        c->len = 0;
+        GH_TRY(check(hipMemsetAsync(c->state, 0, 2 * sizeof(int), s), "reset state"));
+        GH_TRY(check(hipMemsetAsync(c->key, 0, (size_t)batch * sizeof(unsigned long long), s), "reset keys"));
+    } else {
+        if (g->gen_exec) (void)hipGraphExecDestroy(g->gen_exec);
+        if (g->gen_graph) (void)hipGraphDestroy(g->gen_graph);
+        g->gen_exec = nullptr;
+        g->gen_graph = nullptr;
+        g->gen_sig.clear();
+        gorch_hip_kvcache_free(g->gen_cache);
+        g->gen_cache = nullptr;
+        c = gorch_hip_kvcache_create(g, batch, capacity);
+        if (!c) return GORCH_HIP_ENOMEM;
+        g->gen_cache = c;
+    }
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
     int rc = GORCH_HIP_OK;
     const bool use_graph = (flags & 1) && !step_logits;
     auto fail = [&](int r) {
@@ -564,18 +589,30 @@ int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* g, const int* prompts
             return choose_tokens(g, c, 1, s);
         };
         if (use_graph && forwards > 0) {
-            if (check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture")) {
-                fail(GORCH_HIP_ERUNTIME);
-                break;
-            }
-            int r = step();
-            hipError_t e = hipStreamEndCapture(s, &graph);
-            if (r || check(e, "end capture") || check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate")) {
-                fail(GORCH_HIP_ERUNTIME);
-                break;
+            const std::vector<const void*> sig = {g->x,    g->h,    g->q,    g->att,      g->ff,
+                                                  g->logits, g->ids, g->part, g->stats, c->k,
+                                                  c->v,    c->state, c->hist, c->key};
+            if (!g->gen_exec || g->gen_sig != sig) {
+                if (g->gen_exec) (void)hipGraphExecDestroy(g->gen_exec);
+                if (g->gen_graph) (void)hipGraphDestroy(g->gen_graph);
+                g->gen_exec = nullptr;
+                g->gen_graph = nullptr;
+                g->gen_sig.clear();
+                if (check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture")) {
+                    fail(GORCH_HIP_ERUNTIME);
+                    break;
+                }
+                int r = step();
+                hipError_t e = hipStreamEndCapture(s, &g->gen_graph);
+                if (r || check(e, "end capture") ||
+                    check(hipGraphInstantiate(&g->gen_exec, g->gen_graph, nullptr, nullptr, 0), "instantiate")) {
+                    fail(GORCH_HIP_ERUNTIME);
+                    break;
+                }
+                g->gen_sig = sig;
             }
             for (int i = 0; i < forwards; i++)
-                if (check(hipGraphLaunch(exec, s), "graph launch")) { fail(GORCH_HIP_ERUNTIME); break; }
+                if (check(hipGraphLaunch(g->gen_exec, s), "graph launch")) { fail(GORCH_HIP_ERUNTIME); break; }
         } else {
             for (int i = 0; i < forwards && !rc; i++) {
                 if (step()) { fail(GORCH_HIP_ERUNTIME); break; }
@@ -611,12 +648,9 @@ int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* g, const int* prompts
             timing_ms[2] = (float)forwards;
         }
     } while (false);
-    if (exec) (void)hipGraphExecDestroy(exec);
-    if (graph) (void)hipGraphDestroy(graph);
     for (auto& e : ev)
         if (e) (void)hipEventDestroy(e);
     (void)hipStreamSynchronize(s);
-    gorch_hip_kvcache_free(c);
     return rc;
 }
 

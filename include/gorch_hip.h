@@ -273,7 +273,10 @@ int gorch_hip_gpt_forward_cached(void* stream, gorch_hip_gpt* gpt, gorch_hip_kvc
  * *out_len. step_logits (host, may be NULL): [max_new, batch, vocab], row i
  * = logits that chose token i (forces eager launches). timing_ms (may be
  * NULL): {prefill ms, decode ms, decode forwards}. flags bit 0: replay the
- * decode step from a HIP graph. Synchronous. */
+ * decode step from a HIP graph. The engine keeps the KV cache and the
+ * captured step graph between calls with the same batch and cache length
+ * (capture and instantiation are paid once; decode ms then measures the
+ * replays only). Synchronous. */
 int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* gpt, const int* prompts, int batch, int n_prompt,
                               int max_new, int* out_ids, int* out_len, float* step_logits, float* timing_ms,
                               int flags);
