@@ -55,6 +55,8 @@ void* stream_scratch(hipStream_t s, size_t bytes);
 // Epilogue of a K-split Linear over partials part[S][M][N] (S <= 8).
 int launch_splitk_epilogue(hipStream_t s, const float* part, int S, int M, int N, const float* bias,
                            const float* residual, const OutDesc& od, int epilogue);
+// Widest row launch_reduce_rows handles.
+constexpr int kReduceRowsMaxCols = 2048;
 // Row reduction after a K-split Linear: x[m] = x[m] + bias + sum_s part[s][m]
 // (slices added in order; S = 0 leaves x as is), then the LayerNorm
 // statistics of the new row into stats[m] when stats is not null.

@@ -148,7 +148,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
     // rate); one small per-row kernel adds the slices, bias and residual and
     // leaves the next LayerNorm's statistics, which the following fused GEMV
     // reads instead of recomputing them in every block.
-    const bool batched = fused && rows >= 2;
+    const bool batched = fused && rows >= 2 && d <= kReduceRowsMaxCols;
     static const int split_blocks = [] {
         const char* e = getenv("GORCH_HIP_SPLIT_BLOCKS");
         return e ? atoi(e) : 300;

@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* __
 // f64 (nn/layernorm.go:61-91) for the next fused-LayerNorm GEMV. Each thread
 // owns up to kRedCols columns and issues all of their slice loads before
 // adding (S <= kRedSlices), so the row costs one memory round trip.
-constexpr int kRedCols = 8, kRedSlices = 8;
+constexpr int kRedCols = kReduceRowsMaxCols / 256, kRedSlices = 8;
 
 __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ part, int S,
                                                      const float* __restrict__ bias, float* __restrict__ x, int M,

@@ -173,3 +173,18 @@ def test_generate_batch_wide_lm_head(wide, batch):
         assert rel_err(logits[0, b], ref_logits[0]) <= 1e-3
     ids_graph, _, _ = g.generate_cached(prompts, 8, use_graph=True)
     assert np.array_equal(ids_graph, ids)
+
+
+def test_generate_batch_wide_model(gpu):
+    """Batched decode of a model wider than the per-row reducer (d = 2176 >
+    2048): the engine keeps the unsplit fused GEMVs; tokens identical to the
+    oracle per sequence."""
+    cfg = dict(vocab=64, dim=2176, heads=17, layers=1, max_seq=16)
+    w = syn.gpt2_weights(cfg, seed=43, random_affine=True)
+    g, o = gpu.GPT(w), orc.GPT(w)
+    prompts = np.stack([syn.prompt_ids(4, cfg["vocab"], seed=70 + b) for b in range(2)])
+    ids, _, _ = g.generate_cached(prompts, 5)
+    for b in range(2):
+        ref, _, _ = o.generate_cached(prompts[b], 5)
+        assert list(ids[b]) == list(ref)
+    g.close()
