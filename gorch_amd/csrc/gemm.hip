@@ -21,7 +21,7 @@
 namespace gh {
 
 constexpr int kBK = 64;
-constexpr int kLDA = kBK + 8;  // bf16 elements per LDS row (16-byte pad)
+constexpr int kLDA = kBK + 16;  // bf16 elements per LDS row (160 bytes: conflict-free 16-byte fragment reads)
 
 template <int BM, int BN, bool SPLIT, int PF>
 __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A, const uint16_t* __restrict__ W,

@@ -1,0 +1,193 @@
+// gemm_wide.h — a wide-tile MFMA main loop for the MoE expert GEMMs.
+//
+//   acc[b] = A[rows, K] x W_b[cols, K]^T   (b < NB weights, BNW columns each)
+//
+// A arrives as bf16 planes (hi, and lo when SPLIT: x = hi + lo, ~2^-16
+// relative), written once by the producer kernel, so the main loop only
+// moves bytes: every global load and LDS store is 16 bytes. W is bf16 in the
+// nn.Linear [out, in] layout.
+//
+// What bounds these GEMMs on MI355X is the L2 -> CU path, ~16 B/clock per CU
+// (~9.6 TB/s over the chip, measured), not the matrix cores: the time is the
+// L2 traffic — A re-read once per column tile, W once per row tile. Wide
+// tiles (128 rows x up to 256 weight columns, 8 waves in a 2 x 4 grid, each
+// a region of 16x16 v_mfma_f32_16x16x32_bf16 accumulators) cut that traffic,
+// and 64-wide K stages read whole 128-byte cache lines (a 32-wide stage
+// reads half a line per row and fetches every line twice).
+//
+// Pipeline: LDS is double-buffered and registers hold two stages, so stage
+// i+3's loads are issued while stage i runs on the matrix cores; one barrier
+// per stage. The loads are raw buffer loads, branch-free: rows and columns
+// past the tile's edge are clamped into it (computed, never stored) and a
+// K-tail chunk gets an out-of-range offset, which the buffer unit returns as
+// zeros. A load under a branch (or a flat load) would make the compiler wait
+// for every outstanding load (vmcnt(0)) before the next LDS store, draining
+// the prefetch each stage. K % 8 == 0. LDS rows are unpadded with
+// XOR-swizzled 16-byte chunks (no bank conflicts).
+#pragma once
+#include "common.h"
+
+namespace gh {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource over [p, p + bytes): loads at offsets >= bytes return
+// zero. Word 3 selects 32-bit data format, the gfx9 untyped-access setting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, long long bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+constexpr int kOutOfRange = 0x7ffffff0;
+
+template <int BM, int BNW, int NB, bool SPLIT, int BK = 64>
+struct WideGemm {
+    static constexpr int kThreads = 512;  // 8 waves: 2 (rows) x 4 (columns)
+    static constexpr int CH = BK / 8;     // 16-byte chunks per row and stage
+    static constexpr int NA = SPLIT ? 2 : 1;
+    static constexpr int WM = BM / 2, WNW = BNW / 4;
+    static constexpr int TM = WM / 16, TN = WNW / 16;
+    static constexpr int A_U4 = NA * BM * CH / kThreads;  // 16-byte loads per thread per stage
+    static constexpr int W_U4 = NB * BNW * CH / kThreads;
+    static_assert(BK == 32 || BK == 64, "stage width");
+    static_assert(A_U4 >= 1 && W_U4 >= 1 && TM >= 1 && TN >= 1, "tile too small");
+    static_assert(NA * BM * CH % kThreads == 0 && NB * BNW * CH % kThreads == 0, "uneven loads");
+    // each load instruction stays inside one plane / weight (uniform resource)
+    static_assert((BM * CH) % kThreads == 0 && (BNW * CH) % kThreads == 0, "plane split across a load");
+
+    // Chunk c of LDS row `row` sits at c ^ (row & 7) (64-wide rows) or
+    // c ^ ((row >> 1) & 3) (32-wide rows): conflict-free for both the row
+    // stores and the 16-row fragment reads (measured on gfx950).
+    __device__ static __forceinline__ int swz(int row, int c) {
+        return BK == 64 ? (c ^ (row & 7)) : (c ^ ((row >> 1) & 3));
+    }
+
+    struct Smem {
+        uint16_t a[2][NA][BM][BK];
+        uint16_t w[2][NB][BNW][BK];
+    };
+
+    // a[p] + row * lda: row of plane p (nrows valid); w[b] + n * K: column n
+    // of weight b (ncols valid). epi(row, col, vals[NB]) per output.
+    template <class Epi>
+    __device__ static void run(Smem& sm, const uint16_t* const* a, long long lda, int nrows,
+                               const uint16_t* const* w, int ncols, int K, Epi& epi) {
+        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+        const int wm = wave >> 2, wn = wave & 3;
+        const int r = lane & 15, g = lane >> 4;
+        const int nk = (K + BK - 1) / BK;
+
+        // one buffer resource per plane / weight, covering the tile's rows
+        __amdgpu_buffer_rsrc_t rsa[NA], rsw[NB];
+#pragma unroll
+        for (int p = 0; p < NA; p++) rsa[p] = make_rsrc(a[p], (long long)nrows * lda * 2);
+#pragma unroll
+        for (int b = 0; b < NB; b++) rsw[b] = make_rsrc(w[b], (long long)ncols * K * 2);
+
+        u32x4 ra[2][A_U4], rw[2][W_U4];
+        auto gload = [&](int st, u32x4 (&ar)[A_U4], u32x4 (&wr)[W_U4]) {
+            const int k0 = st * BK;
+#pragma unroll
+            for (int i = 0; i < A_U4; i++) {
+                const int idx = tid + kThreads * i;
+                const int p = kThreads * i / (BM * CH), rem = idx % (BM * CH), row = rem / CH, c = rem % CH;
+                const int k = k0 + 8 * c;
+                const int off = k < K ? (min(row, nrows - 1) * (int)lda + k) * 2 : kOutOfRange;
+                ar[i] = __builtin_amdgcn_raw_buffer_load_b128(rsa[p], off, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < W_U4; i++) {
+                const int idx = tid + kThreads * i;
+                const int b = kThreads * i / (BNW * CH), rem = idx % (BNW * CH), row = rem / CH, c = rem % CH;
+                const int k = k0 + 8 * c;
+                const int off = k < K ? (min(row, ncols - 1) * K + k) * 2 : kOutOfRange;
+                wr[i] = __builtin_amdgcn_raw_buffer_load_b128(rsw[b], off, 0, 0);
+            }
+        };
+        auto sstore = [&](int buf, const u32x4 (&ar)[A_U4], const u32x4 (&wr)[W_U4]) {
+#pragma unroll
+            for (int i = 0; i < A_U4; i++) {
+                const int idx = tid + kThreads * i;
+                const int p = kThreads * i / (BM * CH), rem = idx % (BM * CH), row = rem / CH, c = rem % CH;
+                *reinterpret_cast<u32x4*>(&sm.a[buf][p][row][8 * swz(row, c)]) = ar[i];
+            }
+#pragma unroll
+            for (int i = 0; i < W_U4; i++) {
+                const int idx = tid + kThreads * i;
+                const int b = kThreads * i / (BNW * CH), rem = idx % (BNW * CH), row = rem / CH, c = rem % CH;
+                *reinterpret_cast<u32x4*>(&sm.w[buf][b][row][8 * swz(row, c)]) = wr[i];
+            }
+        };
+
+        floatx4 acc[NB][TM][TN];
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) acc[b][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+        auto compute = [&](int buf) {
+#pragma unroll
+            for (int kk = 0; kk < BK / 32; kk++) {
+                bf16x8 bfr[NB][TN];
+#pragma unroll
+                for (int b = 0; b < NB; b++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        bfr[b][j] = *reinterpret_cast<const bf16x8*>(
+                            &sm.w[buf][b][wn * WNW + j * 16 + r][8 * swz(r, 4 * kk + g)]);
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+#pragma unroll
+                    for (int p = 0; p < NA; p++) {
+                        const bf16x8 af = *reinterpret_cast<const bf16x8*>(
+                            &sm.a[buf][p][wm * WM + i * 16 + r][8 * swz(r, 4 * kk + g)]);
+#pragma unroll
+                        for (int b = 0; b < NB; b++)
+#pragma unroll
+                            for (int j = 0; j < TN; j++) acc[b][i][j] = mfma16x16x32(af, bfr[b][j], acc[b][i][j]);
+                    }
+                }
+            }
+        };
+
+        // stage s lives in register set s % 2 until it is stored to LDS
+        // buffer s % 2; stage s + 3 is requested once stage s + 1 has left
+        // its registers. The body is unconditional (stages past K load
+        // zeros; an odd stage count runs one all-zero stage) so the compiler
+        // can keep the newer stage's loads in flight across the wait.
+        const int nk2 = (nk + 1) & ~1;
+        gload(0, ra[0], rw[0]);
+        gload(1, ra[1], rw[1]);
+        sstore(0, ra[0], rw[0]);
+        gload(2, ra[0], rw[0]);
+        __syncthreads();
+        for (int it = 0; it < nk2; it += 2) {
+            compute(0);
+            sstore(1, ra[1], rw[1]);
+            gload(it + 3, ra[1], rw[1]);
+            __syncthreads();
+            compute(1);
+            sstore(0, ra[0], rw[0]);
+            gload(it + 4, ra[0], rw[0]);
+            __syncthreads();
+        }
+
+        // lane holds rows 4g..4g+3 of column r in each 16x16 fragment
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int col = wn * WNW + j * 16 + r;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int row = wm * WM + i * 16 + 4 * g + v;
+                    float vals[NB];
+#pragma unroll
+                    for (int b = 0; b < NB; b++) vals[b] = acc[b][i][j][v];
+                    if (row < nrows && col < ncols) epi(row, col, vals);
+                }
+            }
+    }
+};
+
+}  // namespace gh

@@ -6,10 +6,12 @@
 // experts accumulated in ascending index (:155-180).
 //
 // On the GPU (one stream, no host round trip, no allocation):
-//   k_moe_route      one block: top-K, weights, stable counting sort of the
-//                    (token, slot) assignments by expert, the inverse map,
-//                    and the tile table of the grouped GEMMs;
-//   k_moe_gather     packs each expert's rows contiguously (Xg);
+//   k_moe_topk       one thread per token: top-K and the routing weights;
+//   k_moe_route      one block: stable counting sort of the (token, slot)
+//                    assignments by expert, the inverse map, and the tile
+//                    table of the grouped GEMMs;
+//   k_moe_gather     packs each expert's rows contiguously (Xg), as bf16
+//                    hi/lo planes for the wide-tile GEMMs (gemm_wide.h);
 //   grouped GEMM 1   H = SwiGLU(Xg We_gate^T + bg, Xg We_up^T + bu): gate and
 //                    up tiles accumulate side by side, SwiGLU in the epilogue;
 //   grouped GEMM 2   Yg = (H We_down^T + bd) * w(row), the routing weight
@@ -19,6 +21,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "gemm_wide.h"
 
 namespace gh {
 
@@ -26,13 +29,13 @@ namespace gh {
 // BN output columns, K stepped by kMoeBK. 64 x 64 measured faster than
 // 128-row tiles here (more resident blocks per CU), although the larger
 // tile halves the weight re-reads through L2.
-constexpr int kMoeBM = 64, kMoeBK = 64, kMoeLD = kMoeBK + 8;
+constexpr int kMoeBM = 64, kMoeBK = 64, kMoeLD = kMoeBK + 16;
 constexpr int kMoeBNDual = 64, kMoeBNDown = 64;
 constexpr int kMaxExperts = 64;
 constexpr int kMaxTopK = 8;
 
 struct MoeWs {
-    float* logits;   // [M, E] (router output, or a copy of injected logits)
+    float* logits;   // [M, E] router output (injected logits are read in place)
     int* topi;       // [M, K]
     float* topw;     // [M, K]
     int* perm_tok;   // [M*K] token of packed row p
@@ -76,17 +79,73 @@ static size_t moe_layout(int M, int dim, int ffn, int E, int K, char* base, MoeW
     return off;
 }
 
-// One 1024-thread block; thread t takes tokens t, t + 1024, ... (rounds).
-// Per round: top-K and the routing weights of its token, then the token's
-// rank inside each chosen expert's group — earlier rounds' counts, then the
-// counts of lower waves and lower lanes of this round from wavefront
-// ballots — so the grouping is stable in token order like the reference's
-// per-expert token lists. Ranks are parked in inv; once every expert's size
-// is known the bases, the GEMM tile table (one thread per expert) and the
-// packed-row maps follow.
+// One thread per token: top-K of the router logits (descending; ties keep
+// the lower index first, and a NaN never replaces the running best, as in
+// the reference's > compare) and the routing weights, softmaxRows over the
+// K values: max, exp in f64 rounded to f32, f32 sum, divide. Written to the
+// workspace and, when given, to the caller's arrays.
+__global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ logits, int M, int E, int K,
+                                                  int* __restrict__ topi, float* __restrict__ topw,
+                                                  int* __restrict__ topi_out, float* __restrict__ topw_out) {
+    const int tok = blockIdx.x * blockDim.x + threadIdx.x;
+    if (tok >= M) return;
+    const float* row = logits + (size_t)tok * E;
+    float lv[kMaxExperts];  // the token's logits in registers, all loads in flight
+#pragma unroll
+    for (int j = 0; j < kMaxExperts; j++) lv[j] = j < E ? row[j] : 0.f;
+    int idx[kMaxTopK];
+    float val[kMaxTopK];
+    unsigned long long taken = 0ull;
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; s++) {
+        if (s >= K) break;
+        int best = -1;
+        float bv = 0.f;
+#pragma unroll
+        for (int j = 0; j < kMaxExperts; j++) {
+            if (j >= E || ((taken >> j) & 1ull)) continue;
+            if (best < 0 || lv[j] > bv) {
+                best = j;
+                bv = lv[j];
+            }
+        }
+        idx[s] = best;
+        val[s] = bv;
+        taken |= 1ull << best;
+    }
+    float mx = val[0];
+#pragma unroll
+    for (int s = 1; s < kMaxTopK; s++)
+        if (s < K) mx = val[s] > mx ? val[s] : mx;
+    float e_[kMaxTopK];
+    float sum = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; s++)
+        if (s < K) {
+            e_[s] = (float)exp((double)(val[s] - mx));
+            sum += e_[s];
+        }
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; s++)
+        if (s < K) {
+            const size_t a = (size_t)tok * K + s;
+            const float wgt = e_[s] / sum;
+            topi[a] = idx[s];
+            topw[a] = wgt;
+            if (topi_out) topi_out[a] = idx[s];
+            if (topw_out) topw_out[a] = wgt;
+        }
+}
+
+// One 1024-thread block over the top-K table; thread t takes tokens t,
+// t + 1024, ... (rounds). Per round: the token's rank inside each chosen
+// expert's group — earlier rounds' counts, then the counts of lower waves
+// and lower lanes of this round from wavefront ballots — so the grouping is
+// stable in token order like the reference's per-expert token lists. Ranks
+// are parked in inv; once every expert's size is known the bases, the GEMM
+// tile table (one thread per expert) and the packed-row maps follow.
 constexpr int kRouteThreads = 1024, kRouteWaves = kRouteThreads / 64;
-__global__ __launch_bounds__(kRouteThreads) void k_moe_route(const float* __restrict__ logits, int M, int E, int K,
-                                                             MoeWs ws) {
+__global__ __launch_bounds__(kRouteThreads) void k_moe_route(int M, int E, int K, int tile_rows, MoeWs ws) {
     __shared__ int wtot[kRouteWaves][kMaxExperts];
     __shared__ int run[kMaxExperts];
     __shared__ int base[kMaxExperts + 1];
@@ -100,54 +159,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_moe_route(const float* __rest
         const bool live = tok < M;
         int idx[kMaxTopK];
 #pragma unroll
-        for (int s = 0; s < kMaxTopK; s++) idx[s] = -1;
-        if (live) {
-            // the token's logits in registers (one load each, all in flight)
-            const float* row = logits + (size_t)tok * E;
-            float lv[kMaxExperts];
-#pragma unroll
-            for (int j = 0; j < kMaxExperts; j++) lv[j] = j < E ? row[j] : 0.f;
-            float val[kMaxTopK];
-            unsigned long long taken = 0ull;
-            // top-K, descending; ties keep the lower index first (a NaN never
-            // replaces the running best, as in the reference's > compare)
-#pragma unroll
-            for (int s = 0; s < kMaxTopK; s++) {
-                if (s >= K) break;
-                int best = -1;
-                float bv = 0.f;
-#pragma unroll
-                for (int j = 0; j < kMaxExperts; j++) {
-                    if (j >= E || ((taken >> j) & 1ull)) continue;
-                    if (best < 0 || lv[j] > bv) {
-                        best = j;
-                        bv = lv[j];
-                    }
-                }
-                idx[s] = best;
-                val[s] = bv;
-                taken |= 1ull << best;
-            }
-            // softmaxRows: max, exp in f64 rounded to f32, f32 sum, divide
-            float mx = val[0];
-#pragma unroll
-            for (int s = 1; s < kMaxTopK; s++)
-                if (s < K) mx = val[s] > mx ? val[s] : mx;
-            float e_[kMaxTopK];
-            float sum = 0.f;
-#pragma unroll
-            for (int s = 0; s < kMaxTopK; s++)
-                if (s < K) {
-                    e_[s] = (float)exp((double)(val[s] - mx));
-                    sum += e_[s];
-                }
-#pragma unroll
-            for (int s = 0; s < kMaxTopK; s++)
-                if (s < K) {
-                    ws.topi[(size_t)tok * K + s] = idx[s];
-                    ws.topw[(size_t)tok * K + s] = e_[s] / sum;
-                }
-        }
+        for (int s = 0; s < kMaxTopK; s++) idx[s] = (live && s < K) ? ws.topi[(size_t)tok * K + s] : -1;
         // this round's per-wave counts and lane prefixes, expert by expert
         int pre[kMaxTopK];
 #pragma unroll
@@ -184,7 +196,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_moe_route(const float* __rest
             base[e] = b;
             tbase[e] = nt;
             b += run[e];
-            nt += (run[e] + kMoeBM - 1) / kMoeBM;
+            nt += (run[e] + tile_rows - 1) / tile_rows;
         }
         base[E] = b;
         tbase[E] = nt;
@@ -193,10 +205,10 @@ __global__ __launch_bounds__(kRouteThreads) void k_moe_route(const float* __rest
     __syncthreads();
     if (t < E) {
         const int n = run[t];
-        for (int r = 0, i = tbase[t]; r < n; r += kMoeBM, i++) {
+        for (int r = 0, i = tbase[t]; r < n; r += tile_rows, i++) {
             ws.tile_e[i] = t;
             ws.tile_r0[i] = base[t] + r;
-            ws.tile_n[i] = min(kMoeBM, n - r);
+            ws.tile_n[i] = min(tile_rows, n - r);
         }
     }
     for (int tok = t; tok < M; tok += kRouteThreads)
@@ -220,12 +232,14 @@ __global__ void k_moe_gather(const float* __restrict__ x, const int* __restrict_
 }
 
 // out[t] = sum over the token's K packed rows in ascending expert order
-// (the reference adds each expert's ScatterAdd contribution in order).
+// (the reference adds each expert's ScatterAdd contribution in order). One
+// thread per (token, 4 columns); dim % 4 == 0.
 __global__ void k_moe_combine(const float* __restrict__ yg, const int* __restrict__ inv,
                               const int* __restrict__ topi, float* out, int M, int K, int dim) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)M * dim;
+    const int d4 = dim / 4;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)M * d4;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int t = (int)(i / dim), c = (int)(i - (int64_t)t * dim);
+        const int t = (int)(i / d4), c = (int)(i - (int64_t)t * d4);
         int order[kMaxTopK];
         for (int s = 0; s < K; s++) order[s] = s;
         for (int a = 1; a < K; a++)  // insertion sort of slots by expert index
@@ -234,9 +248,15 @@ __global__ void k_moe_combine(const float* __restrict__ yg, const int* __restric
                 order[b] = order[b - 1];
                 order[b - 1] = tmp;
             }
-        float acc = 0.f;
-        for (int s = 0; s < K; s++) acc = acc + yg[(size_t)inv[(size_t)t * K + order[s]] * dim + c];
-        out[i] = acc;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s = 0; s < K; s++) {
+            const float4 v = reinterpret_cast<const float4*>(yg + (size_t)inv[(size_t)t * K + order[s]] * dim)[c];
+            acc.x = acc.x + v.x;
+            acc.y = acc.y + v.y;
+            acc.z = acc.z + v.z;
+            acc.w = acc.w + v.w;
+        }
+        reinterpret_cast<float4*>(out)[i] = acc;
     }
 }
 
@@ -381,6 +401,86 @@ __global__ __launch_bounds__(256) void k_moe_gemm(const float* __restrict__ A, c
         }
 }
 
+// Wide-tile path. The gather writes Xg as two bf16 planes (hi, lo: x = hi +
+// lo to ~2^-16 relative, the split the MFMA kernels use) in the space of the
+// f32 Xg, and GEMM 1's epilogue writes H the same way, so both GEMMs load
+// 16-byte bf16 words only. Rows are grouped in 128-row tiles. The down GEMM
+// keeps 256-wide tiles although at d = 1024 that leaves half the CUs idle:
+// 128-wide tiles on every CU measured slower (148 vs 121 us, 2048 tokens).
+// GORCH_HIP_MOE_WIDE=0 selects the 64 x 64 f32-activation kernels;
+// GORCH_HIP_MOE_DOWN_BN=128 the narrower down tile.
+constexpr int kWideBM = 128, kWideBNDual = 128, kWideBNDown = 256;
+
+__global__ void k_moe_gather_split(const float* __restrict__ x, const int* __restrict__ perm_tok, uint16_t* hi,
+                                   uint16_t* lo, int rows, int dim) {
+    const int d8 = dim / 8;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)rows * d8;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int p = (int)(i / d8), c = (int)(i - (int64_t)p * d8);
+        const float4* src = reinterpret_cast<const float4*>(x + (size_t)perm_tok[p] * dim + 8 * c);
+        const float4 u = src[0], v = src[1];
+        const float f[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+        bf16x8 h, l;
+        split_hi_lo(f, h, l);
+        *reinterpret_cast<bf16x8*>(hi + (size_t)p * dim + 8 * c) = h;
+        *reinterpret_cast<bf16x8*>(lo + (size_t)p * dim + 8 * c) = l;
+    }
+}
+
+// blockIdx.y = 128-row tile of the table, blockIdx.x = BNW output columns.
+// A: planes (hi, lo) of [rows, Kd]. DUAL: gate and up side by side, H =
+// SwiGLU(gate, up) written as planes (Chi, Clo); else C = (acc + b) * w(row)
+// in f32.
+template <bool DUAL, int BNW>
+__global__ __launch_bounds__(512) void k_moe_wide(const uint16_t* __restrict__ Ahi, const uint16_t* __restrict__ Alo,
+                                                  const uint16_t* __restrict__ W1, const uint16_t* __restrict__ W2,
+                                                  const float* __restrict__ b1, const float* __restrict__ b2,
+                                                  float* __restrict__ C, uint16_t* __restrict__ Chi,
+                                                  uint16_t* __restrict__ Clo, int N, int Kd, MoeWs ws) {
+    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true>;
+    extern __shared__ __align__(16) uint4 moe_smem[];
+    if ((int)blockIdx.y >= *ws.ntiles) return;
+    const int e = ws.tile_e[blockIdx.y], r0 = ws.tile_r0[blockIdx.y], nrows = ws.tile_n[blockIdx.y];
+    const int n0 = blockIdx.x * BNW;
+    const uint16_t* a[2] = {Ahi + (size_t)r0 * Kd, Alo + (size_t)r0 * Kd};
+    const uint16_t* w[2] = {W1 + ((size_t)e * N + n0) * Kd, DUAL ? W2 + ((size_t)e * N + n0) * Kd : nullptr};
+    const float* bg = b1 ? b1 + (size_t)e * N + n0 : nullptr;
+    const float* bu = (DUAL && b2) ? b2 + (size_t)e * N + n0 : nullptr;
+    auto epi = [&](int row, int col, const float* v) {
+        const size_t o = (size_t)(r0 + row) * N + n0 + col;
+        float s = v[0];
+        if (bg) s = s + bg[col];
+        if constexpr (DUAL) {
+            float u = v[1];
+            if (bu) u = u + bu[col];
+            s = s * sigmoidf_ref(s) * u;  // SwiGLU: gate * sigma(gate) * up
+            const uint32_t hb = __float_as_uint(s) & 0xffff0000u;
+            Chi[o] = (uint16_t)(hb >> 16);
+            Clo[o] = __builtin_bit_cast(uint16_t, (__bf16)(s - __uint_as_float(hb)));
+        } else {
+            C[o] = s * ws.perm_w[r0 + row];  // weighted = exOut * w
+        }
+    };
+    G::run(*reinterpret_cast<typename G::Smem*>(moe_smem), a, Kd, nrows, w, min(BNW, N - n0), Kd, epi);
+}
+
+template <bool DUAL, int BNW>
+static int launch_moe_wide(hipStream_t s, dim3 grid, const uint16_t* Ahi, const uint16_t* Alo, const uint16_t* W1,
+                           const uint16_t* W2, const float* b1, const float* b2, float* C, uint16_t* Chi,
+                           uint16_t* Clo, int N, int Kd, const MoeWs& ws) {
+    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        GH_TRY(check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_moe_wide<DUAL, BNW>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(typename G::Smem)),
+                     "moe_wide attribute"));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((k_moe_wide<DUAL, BNW>), grid, dim3(G::kThreads), sizeof(typename G::Smem), s, Ahi, Alo, W1,
+                       W2, b1, b2, C, Chi, Clo, N, Kd, ws);
+    return check_launch(DUAL ? "moe_wide_gate_up" : "moe_wide_down");
+}
+
 }  // namespace gh
 
 using namespace gh;
@@ -405,31 +505,59 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
     MoeWs ws;
     moe_layout(M, d, F, E, K, (char*)workspace, &ws);
     hipStream_t s = stream_of(stream);
-    if (logits) {
-        GH_TRY(check(hipMemcpyAsync(ws.logits, logits, (size_t)M * E * 4, hipMemcpyDeviceToDevice, s), "logits"));
-    } else {
+    const float* lg = logits;
+    if (!lg) {
         GH_TRY(launch_linear_bf16(s, x, w->wr, w->br, nullptr, ws.logits, M, E, d, GORCH_HIP_EPI_NONE));
+        lg = ws.logits;
     }
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(kRouteThreads), 0, s, ws.logits, M, E, K, ws);
+    hipLaunchKernelGGL(k_moe_topk, dim3((M + 255) / 256), dim3(256), 0, s, lg, M, E, K, ws.topi, ws.topw, topk_idx,
+                       topk_w);
+    GH_TRY(check_launch("moe_topk"));
+    static const bool wide = [] {
+        const char* e = getenv("GORCH_HIP_MOE_WIDE");
+        return !e || atoi(e) != 0;
+    }();
+    const int tile_rows = wide ? kWideBM : kMoeBM;
+    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(kRouteThreads), 0, s, M, E, K, tile_rows, ws);
     GH_TRY(check_launch("moe_route"));
     const int MK = M * K;
-    const int gblocks = (int)std::min<int64_t>(8192, ((int64_t)MK * d / 4 + 255) / 256);
-    hipLaunchKernelGGL(k_moe_gather, dim3(gblocks), dim3(256), 0, s, x, ws.perm_tok, ws.xg, MK, d);
-    GH_TRY(check_launch("moe_gather"));
-    const int max_tiles = MK / kMoeBM + E + 1;
-    hipLaunchKernelGGL((k_moe_gemm<true, kMoeBNDual>), dim3((F + kMoeBNDual - 1) / kMoeBNDual, max_tiles),
-                       dim3(256), 0, s, ws.xg, w->wgate, w->wup, w->bgate, w->bup, ws.h, F, d, ws);
-    GH_TRY(check_launch("moe_gemm_gate_up"));
-    hipLaunchKernelGGL((k_moe_gemm<false, kMoeBNDown>), dim3((d + kMoeBNDown - 1) / kMoeBNDown, max_tiles),
-                       dim3(256), 0, s, ws.h, w->wdown, nullptr, w->bdown, nullptr, ws.yg, d, F, ws);
-    GH_TRY(check_launch("moe_gemm_down"));
-    const int cblocks = (int)std::min<int64_t>(8192, ((int64_t)M * d + 255) / 256);
+    const int max_tiles = MK / tile_rows + E + 1;
+    if (wide) {
+        // Xg and H hold (hi, lo) bf16 planes in the space of their f32 form
+        uint16_t* xhi = reinterpret_cast<uint16_t*>(ws.xg);
+        uint16_t* xlo = xhi + (size_t)MK * d;
+        uint16_t* hhi = reinterpret_cast<uint16_t*>(ws.h);
+        uint16_t* hlo = hhi + (size_t)MK * F;
+        const int gblocks = (int)std::min<int64_t>(8192, ((int64_t)MK * d / 8 + 255) / 256);
+        hipLaunchKernelGGL(k_moe_gather_split, dim3(gblocks), dim3(256), 0, s, x, ws.perm_tok, xhi, xlo, MK, d);
+        GH_TRY(check_launch("moe_gather"));
+        GH_TRY((launch_moe_wide<true, kWideBNDual>(s, dim3((F + kWideBNDual - 1) / kWideBNDual, max_tiles), xhi,
+                                                  xlo, w->wgate, w->wup, w->bgate, w->bup, nullptr, hhi, hlo, F, d,
+                                                  ws)));
+        static const int down_bn = [] {
+            const char* e = getenv("GORCH_HIP_MOE_DOWN_BN");
+            return e ? atoi(e) : kWideBNDown;
+        }();
+        if (down_bn == 256)
+            GH_TRY((launch_moe_wide<false, 256>(s, dim3((d + 255) / 256, max_tiles), hhi, hlo, w->wdown, nullptr,
+                                                w->bdown, nullptr, ws.yg, nullptr, nullptr, d, F, ws)));
+        else
+            GH_TRY((launch_moe_wide<false, 128>(s, dim3((d + 127) / 128, max_tiles), hhi, hlo, w->wdown, nullptr,
+                                                w->bdown, nullptr, ws.yg, nullptr, nullptr, d, F, ws)));
+    } else {
+        const int gblocks = (int)std::min<int64_t>(8192, ((int64_t)MK * d / 4 + 255) / 256);
+        hipLaunchKernelGGL(k_moe_gather, dim3(gblocks), dim3(256), 0, s, x, ws.perm_tok, ws.xg, MK, d);
+        GH_TRY(check_launch("moe_gather"));
+        hipLaunchKernelGGL((k_moe_gemm<true, kMoeBNDual>), dim3((F + kMoeBNDual - 1) / kMoeBNDual, max_tiles),
+                           dim3(256), 0, s, ws.xg, w->wgate, w->wup, w->bgate, w->bup, ws.h, F, d, ws);
+        GH_TRY(check_launch("moe_gemm_gate_up"));
+        hipLaunchKernelGGL((k_moe_gemm<false, kMoeBNDown>), dim3((d + kMoeBNDown - 1) / kMoeBNDown, max_tiles),
+                           dim3(256), 0, s, ws.h, w->wdown, nullptr, w->bdown, nullptr, ws.yg, d, F, ws);
+        GH_TRY(check_launch("moe_gemm_down"));
+    }
+    const int cblocks = (int)std::min<int64_t>(8192, ((int64_t)M * d / 4 + 255) / 256);
     hipLaunchKernelGGL(k_moe_combine, dim3(cblocks), dim3(256), 0, s, ws.yg, ws.inv, ws.topi, out, M, K, d);
     GH_TRY(check_launch("moe_combine"));
-    if (topk_idx)
-        GH_TRY(check(hipMemcpyAsync(topk_idx, ws.topi, (size_t)M * K * 4, hipMemcpyDeviceToDevice, s), "topk idx"));
-    if (topk_w)
-        GH_TRY(check(hipMemcpyAsync(topk_w, ws.topw, (size_t)M * K * 4, hipMemcpyDeviceToDevice, s), "topk w"));
     count(CNT_MOE);
     return GORCH_HIP_OK;
 }
