@@ -224,6 +224,21 @@ __device__ __forceinline__ void split_hi_lo(const float (&f)[8], bf16x8& hi, bf1
     }
 }
 
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource over [p, p + bytes) (bytes < 2^31): buffer loads at
+// offsets >= bytes return zero without touching memory, which lets a kernel
+// drop its bounds-check branches (a load under a branch makes the compiler
+// wait for every outstanding load before the next use). Word 3 selects the
+// 32-bit data format, the gfx9 setting for untyped buffer access. p and
+// bytes must be wave-uniform; the size is read back as a scalar so a clamp
+// computed on the vector unit does not force a per-lane (waterfall) loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, long long bytes) {
+    const int n = __builtin_amdgcn_readfirstlane((int)bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, n, 0x00020000);
+}
+constexpr int kOutOfRange = 0x7ffffff0;  // an offset past any resource
+
 __device__ __forceinline__ floatx4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const floatx4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

@@ -5,10 +5,11 @@
 // Block tile BM x BN, K stepped by 64. 256 threads = 4 waves in a 2x2 grid,
 // each wave owning a (BM/2) x (BN/2) sub-tile of 16x16 MFMA accumulators
 // (v_mfma_f32_16x16x32_bf16). Each K step stages the A tile (converted from
-// f32 as it is written to LDS) and the W tile in LDS; the next step's global
-// loads are issued into registers before the current step's MFMAs so HBM
-// latency overlaps the math. LDS rows are padded by 16 bytes to spread the
-// 16-byte fragment reads across banks.
+// f32 as it is written to LDS) and the W tile in LDS; later steps' global
+// loads (raw buffer loads, no branches) are issued into registers before the
+// current step's MFMAs so memory latency overlaps the math. LDS rows are
+// padded to 160 bytes, which makes the 16-byte fragment reads conflict-free
+// on gfx950 (a 144-byte row measured 2-way conflicted).
 //
 // Activation modes:
 //   split (default): A = hi + lo in bf16 (two MFMAs per fragment pair),
@@ -39,27 +40,31 @@ __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A,
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
 
     // PF register stages: the loads of K-step i + PF are issued as soon as
-    // step i has been written to LDS, so PF steps of latency are in flight
+    // step i has been written to LDS, so PF steps of latency are in flight.
+    // Raw buffer loads over the block's rows, branch-free: rows past M or N
+    // are clamped into the tile (computed, never stored) and a K-tail chunk
+    // gets an out-of-range offset, which reads as zeros. (A load under a
+    // branch makes the compiler drain every outstanding load before each
+    // LDS store, so no prefetch would survive a step.)
+    const int mrows = min(BM, M - m0), ncols = min(BN, N - n0);
+    const __amdgpu_buffer_rsrc_t rsa = make_rsrc(A + (size_t)m0 * K, (long long)mrows * K * 4);
+    const __amdgpu_buffer_rsrc_t rsw = make_rsrc(W + (size_t)n0 * K, (long long)ncols * K * 2);
     float4 ra[PF][A_F4];
     uint4 rw[PF][W_U4];
     auto gload = [&](int k0, float4 (&a)[A_F4], uint4 (&wv)[W_U4]) {
 #pragma unroll
         for (int i = 0; i < A_F4; i++) {
             const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
-            const int m = m0 + row, k = k0 + 4 * c4;
-            if (m < M && k < K)
-                a[i] = *reinterpret_cast<const float4*>(A + (size_t)m * K + k);
-            else
-                a[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            const int k = k0 + 4 * c4;
+            const int off = k < K ? (min(row, mrows - 1) * K + k) * 4 : kOutOfRange;
+            a[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsa, off, 0, 0));
         }
 #pragma unroll
         for (int i = 0; i < W_U4; i++) {
             const int idx = tid + 256 * i, row = idx >> 3, c8 = idx & 7;
-            const int n = n0 + row, k = k0 + 8 * c8;
-            if (n < N && k < K)
-                wv[i] = *reinterpret_cast<const uint4*>(W + (size_t)n * K + k);
-            else
-                wv[i] = make_uint4(0, 0, 0, 0);
+            const int k = k0 + 8 * c8;
+            const int off = k < K ? (min(row, ncols - 1) * K + k) * 2 : kOutOfRange;
+            wv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, off, 0, 0));
         }
     };
     auto sstore = [&](const float4 (&a)[A_F4], const uint4 (&wv)[W_U4]) {
@@ -106,19 +111,20 @@ __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A,
         const int n = n0 + wn * WN + j * 16 + r;
         bn[j] = (bias && n < N) ? bias[n] : 0.f;
     }
+    // the step count is padded to a multiple of PF (padding steps read
+    // zeros) so the loop body has no branch around its loads
     const int nk = (K + kBK - 1) / kBK;
+    const int nkp = (nk + PF - 1) / PF * PF;
 #pragma unroll
-    for (int s = 0; s < PF; s++)
-        if (s < nk) gload(s * kBK, ra[s], rw[s]);
-    for (int it0 = 0; it0 < nk; it0 += PF) {
+    for (int s = 0; s < PF; s++) gload(s * kBK, ra[s], rw[s]);
+    for (int it0 = 0; it0 < nkp; it0 += PF) {
 #pragma unroll
         for (int s = 0; s < PF; s++) {
             const int it = it0 + s;
-            if (it >= nk) break;
             __syncthreads();  // previous step's fragment reads are done
             sstore(ra[s], rw[s]);
             __syncthreads();
-            if (it + PF < nk) gload((it + PF) * kBK, ra[s], rw[s]);
+            gload((it + PF) * kBK, ra[s], rw[s]);
 #pragma unroll
             for (int kk = 0; kk < kBK; kk += 32) {
                 bf16x8 bfr[TN];
@@ -169,7 +175,9 @@ static void launch_gemm_t(hipStream_t s, const float* A, const uint16_t* W, cons
         return e ? atoi(e) : 0;
     }();
     dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-    const int pf = pf_env ? pf_env : (BM * BN <= 64 * 128 ? 3 : 2);
+    // measured: one register stage for 128 x 128 tiles (more stages cost
+    // occupancy: 4096^3 247 vs 301 us), two for the smaller tiles
+    const int pf = pf_env ? pf_env : (BM * BN >= 128 * 128 ? 1 : 2);
     if (pf == 1)
         hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT, 1>), grid, dim3(256), 0, s, A, W, bias, residual, od, M, N,
                            K, epilogue);

@@ -29,15 +29,6 @@
 
 namespace gh {
 
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-
-// Raw buffer resource over [p, p + bytes): loads at offsets >= bytes return
-// zero. Word 3 selects 32-bit data format, the gfx9 untyped-access setting.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, long long bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-constexpr int kOutOfRange = 0x7ffffff0;
-
 template <int BM, int BNW, int NB, bool SPLIT, int BK = 64>
 struct WideGemm {
     static constexpr int kThreads = 512;  // 8 waves: 2 (rows) x 4 (columns)

@@ -553,8 +553,8 @@ __device__ __forceinline__ void mt_a(const uint4* xh, const uint4* xl, int ks, i
 }
 
 // Finish tile ct: bias, GELU, residual, output and the block's argmax key.
-// acc: rows 4g..4g+3 of column 16*ct + r.
-__device__ __forceinline__ void mt_finish(const floatx4& acc, int ct, int M, int N, const float* bias,
+// acc: rows 4g..4g+3 of column 16*ct + r; bv = bias[16*ct + r].
+__device__ __forceinline__ void mt_finish(const floatx4& acc, int ct, int M, int N, const float* bias, float bv,
                                           const float* residual, const OutDesc& od, int epilogue,
                                           const LinearExtras& ex, unsigned long long* s_key) {
     const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
@@ -565,7 +565,7 @@ __device__ __forceinline__ void mt_finish(const floatx4& acc, int ct, int M, int
         const int om = 4 * g + v4;
         if (om >= M) break;
         float sum = acc[v4];
-        if (bias) sum = sum + bias[on];
+        if (bias) sum = sum + bv;  // bias[on], loaded with the tile's weights
         if (epilogue == GORCH_HIP_EPI_GELU) sum = gelu_tanh(sum);
         if (residual) sum = residual[(size_t)om * N + on] + sum;
         *od.at(om, on) = sum;
@@ -581,7 +581,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
     extern __shared__ uint4 smem[];
     __shared__ float s_mean[16], s_inv[16];
     __shared__ unsigned long long s_key[16];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // wave index read as a scalar: the tile (and so each buffer resource) is
+    // wave-uniform, so the resources live in SGPRs
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
     const int bidx = blockIdx.x;
     const int kb = 0, ke = K;
@@ -593,23 +595,38 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
 
     const int nbat = (nst + ST - 1) / ST;  // load batches per tile
     const int tstride = bps * NW;
+    const int t0 = bidx + bps * wave;
+    const int my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    const int total = my_tiles * nbat;  // this wave's batches, tile-major
 
-    uint4 v[ST][4];
-    auto load = [&](int t, int bat) {
+    // Batch j: stages (j % nbat) * ST .. of tile t0 + tstride * (j / nbat),
+    // with the tile's bias value. Raw buffer resources over the tile's rows
+    // make rows past N, stages past K and batches past the wave's last read
+    // as zeros with no branch around the loads, so the compiler can keep the
+    // next batch in flight while this one feeds the matrix cores.
+    uint4 va[ST][4], vb[ST][4];
+    float ba, bb;
+    auto load = [&](int j, uint4 (&v)[ST][4], float& bv) {
+        // (the division runs on the vector unit; readfirstlane hands the
+        // uniform results back as scalars for the resources)
+        const int ti = __builtin_amdgcn_readfirstlane(j / nbat), bat = j - ti * nbat;
+        const int t = t0 + tstride * ti;
+        const int rows = max(0, min(16, N - 16 * t));
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(W + (size_t)t * 16 * K, (long long)rows * K * 2);
 #pragma unroll
         for (int q = 0; q < ST; q++) {
             const int st = bat * ST + q;
-            const int n = t * 16 + r;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int k = kb + 128 * st + 32 * j + 8 * g;
-                v[q][j] = (st < nst && n < N && k < ke) ? *reinterpret_cast<const uint4*>(W + (size_t)n * K + k)
-                                                       : make_uint4(0, 0, 0, 0);
+            for (int jj = 0; jj < 4; jj++) {
+                const int k = 128 * st + 32 * jj + 8 * g;
+                const int off = k < K ? (r * K + k) * 2 : kOutOfRange;
+                v[q][jj] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
             }
         }
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias + (size_t)t * 16, bias ? (long long)rows * 4 : 0);
+        bv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, r * 4, 0, 0));
     };
-    int t = bidx + bps * wave;
-    if (t < ntiles) load(t, 0);  // the weight stream starts before the staging
+    load(0, va, ba);  // the weight stream starts before the staging
 
     if (ex.ln_g && ex.ln_stats) {
         if (threadIdx.x < 16 && (int)threadIdx.x < M) {
@@ -627,29 +644,31 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
     __syncthreads();
 
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    // each wave walks its own tiles; the first batch was issued before
-    // the staging, later ones overlap the other waves' MFMAs
-    bool first = true;
-    for (; t < ntiles; t += tstride) {
-        for (int b0 = 0; b0 < nbat; b0++) {
-            if (!first) load(t, b0);
-            first = false;
+    auto compute = [&](int j, const uint4 (&v)[ST][4], float bv) {
+        const int ti = j / nbat, bat = j - ti * nbat;
 #pragma unroll
-            for (int q = 0; q < ST; q++) {
-                const int st = b0 * ST + q;
-                if (st >= nst) break;
+        for (int q = 0; q < ST; q++) {
+            const int st = bat * ST + q;
+            if (st >= nst) break;
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    bf16x8 ah, al;
-                    mt_a<MR>(xh, xl, 4 * st + u, g, r, ah, al);
-                    const bf16x8 bb = __builtin_bit_cast(bf16x8, v[q][u]);
-                    acc = mfma16x16x32(ah, bb, acc);
-                    acc = mfma16x16x32(al, bb, acc);
-                }
+            for (int u = 0; u < 4; u++) {
+                bf16x8 ah, al;
+                mt_a<MR>(xh, xl, 4 * st + u, g, r, ah, al);
+                const bf16x8 wb = __builtin_bit_cast(bf16x8, v[q][u]);
+                acc = mfma16x16x32(ah, wb, acc);
+                acc = mfma16x16x32(al, wb, acc);
             }
         }
-        mt_finish(acc, t, M, N, bias, residual, od, epilogue, ex, s_key);
-        acc = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (bat == nbat - 1) {
+            mt_finish(acc, t0 + tstride * ti, M, N, bias, bv, residual, od, epilogue, ex, s_key);
+            acc = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    for (int j = 0; j < total; j += 2) {
+        load(j + 1, vb, bb);
+        compute(j, va, ba);
+        load(j + 2, va, ba);
+        if (j + 1 < total) compute(j + 1, vb, bb);
     }
     if (ex.argmax_key) {
         __syncthreads();
