@@ -59,9 +59,11 @@ int launch_splitk_epilogue(hipStream_t s, const float* part, int S, int M, int N
 constexpr int kReduceRowsMaxCols = 2048;
 // Row reduction after a K-split Linear: x[m] = x[m] + bias + sum_s part[s][m]
 // (slices added in order; S = 0 leaves x as is), then the LayerNorm
-// statistics of the new row into stats[m] when stats is not null.
+// statistics of the new row into stats[m] when stats is not null, and with
+// h the normalised row h[m] = LayerNorm(x[m]; ln_g, ln_b) as well.
 int launch_reduce_rows(hipStream_t s, const float* part, int S, const float* bias, float* x, int M, int N,
-                       float eps, float2* stats);
+                       float eps, float2* stats, const float* ln_g = nullptr, const float* ln_b = nullptr,
+                       float* h = nullptr);
 int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                        const float* residual, float* y, int M, int N, int K, int epilogue);
 int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
@@ -237,7 +239,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, long 
     const int n = __builtin_amdgcn_readfirstlane((int)bytes);
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, n, 0x00020000);
 }
-constexpr int kOutOfRange = 0x7ffffff0;  // an offset past any resource
+constexpr int kOutOfRange = 0x7fff0000;  // an offset past any resource (+ small immediates)
 
 __device__ __forceinline__ floatx4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const floatx4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

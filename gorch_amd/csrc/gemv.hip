@@ -27,21 +27,22 @@
 namespace gh {
 
 // NW waves per block split K; NT 16-row weight tiles per block; U k-steps
-// of loads issued per wave before their MFMAs.
-template <int NT, int NW, int U, bool LX>
+// per load group. Each wave walks its K range in groups of U k-steps with
+// two register sets: group i + 1's loads (weights, activation rows and, with
+// LN, gamma/beta) are in flight while group i feeds the matrix cores. All
+// loads are raw buffer loads without branches: rows past M or N and k past
+// the wave's range read as zeros (a load under a branch would make the
+// compiler wait for every outstanding load before each use).
+template <int NT, int NW, int U, bool LN>
 __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
     const float* __restrict__ x, const uint16_t* __restrict__ W, const float* __restrict__ bias,
     const float* residual, OutDesc od, int M, int N, int K, int kw, int epilogue, LinearExtras ex) {
     __shared__ floatx4 red[NW][NT][64];
-    // LX: per-wave exchange buffer; the weight rows are read 16 lanes per row
-    // (256 contiguous bytes per row per instruction) and re-read from LDS in
-    // the MFMA B layout. Row pitch 17 x 16 B keeps both sides conflict-free.
-    __shared__ uint4 xw[LX ? NW : 1][LX ? NT * 16 : 1][17];
     __shared__ float s_mean[16], s_inv[16];
     __shared__ unsigned long long s_key[16];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15;  // A: activation row; B: weight row within tile
     const int g = lane >> 4;  // k-chunk group within a 32-wide k-step
     const int n0 = blockIdx.x * (16 * NT);
@@ -49,31 +50,29 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
     const int m0 = ex.part ? 0 : blockIdx.y * 16;
     const int kbase = ex.part ? blockIdx.y * ex.kslice : 0;
     const int kend = ex.part ? min(K, kbase + ex.kslice) : K;
-    const int mrow = m0 + r;
     const int kb = kbase + wave * kw;
     const int ke = min(kb + kw, kend);
 
     const long long xs = ex.x_stride ? ex.x_stride : K;
-    const bool arow_ok = mrow < M;
-    const float* xrow = x + (size_t)(arow_ok ? mrow : 0) * xs;
-
-    const uint16_t* wrow[NT];
-    bool wrow_ok[NT];
+    const int mrows = max(0, min(16, M - m0));
+    const __amdgpu_buffer_rsrc_t rsx = make_rsrc(x + (size_t)m0 * xs, (long long)mrows * xs * 4);
+    __amdgpu_buffer_rsrc_t rsw[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        int n = n0 + 16 * t + r;
-        wrow_ok[t] = n < N;
-        wrow[t] = W + (size_t)(wrow_ok[t] ? n : 0) * K;
+        const int rows = max(0, min(16, N - n0 - 16 * t));
+        rsw[t] = make_rsrc(W + (size_t)(n0 + 16 * t) * K, (long long)rows * K * 2);
     }
+    const __amdgpu_buffer_rsrc_t rsg = make_rsrc(ex.ln_g, LN ? (long long)K * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rsb = make_rsrc(ex.ln_b, LN ? (long long)K * 4 : 0);
 
-    if (ex.ln_g && ex.ln_stats) {
+    if (LN && ex.ln_stats) {
         if (threadIdx.x < 16 && m0 + (int)threadIdx.x < M) {
             const float2 st = ex.ln_stats[m0 + threadIdx.x];
             s_mean[threadIdx.x] = st.x;
             s_inv[threadIdx.x] = st.y;
         }
         __syncthreads();
-    } else if (ex.ln_g) {
+    } else if (LN) {
         // LayerNorm prologue (nn/layernorm.go:61-91): per-row mean and
         // variance in f64 over the whole K, computed by each block for its
         // (at most 16) rows; the A operand is normalised as it is loaded.
@@ -102,83 +101,76 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
         }
         __syncthreads();
     }
-    const float ln_mean = ex.ln_g ? s_mean[r] : 0.f;
-    const float ln_inv = ex.ln_g ? s_inv[r] : 1.f;
+    const float ln_mean = LN ? s_mean[r] : 0.f;
+    const float ln_inv = LN ? s_inv[r] : 1.f;
 
     floatx4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // U k-steps per iteration: all weight loads of the group are issued
-    // before any MFMA so several 16-byte loads per lane are in flight.
-    for (int k0 = kb; k0 < ke; k0 += 32 * U) {
-        uint4 wv[U][NT];
-        float f[U][8];
-        if constexpr (LX) {
-            static_assert(U == 4, "LX stages 128 k-values (4 k-steps) per iteration");
-            uint4 v[4 * NT];
-            const int sub = lane & 15;
-            const int kk = k0 + 8 * sub;
-#pragma unroll
-            for (int j = 0; j < 4 * NT; j++) {
-                const int n = n0 + 4 * j + (lane >> 4);
-                v[j] = (n < N && kk < ke) ? *reinterpret_cast<const uint4*>(W + (size_t)n * K + kk)
-                                          : make_uint4(0, 0, 0, 0);
-            }
-#pragma unroll
-            for (int j = 0; j < 4 * NT; j++) xw[wave][4 * j + (lane >> 4)][sub] = v[j];
-#pragma unroll
-            for (int u = 0; u < U; u++)
-#pragma unroll
-                for (int t = 0; t < NT; t++) wv[u][t] = xw[wave][16 * t + r][4 * u + g];
-        }
+    struct Group {
+        u32x4 w[U][NT];
+        u32x4 xa[U][2];
+        u32x4 lg[LN ? U : 1][2], lb[LN ? U : 1][2];
+    };
+    auto load = [&](int k0, Group& gr) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int kc = k0 + 32 * u + 8 * g;
-            const bool k_ok = kc < ke;
-            if constexpr (!LX) {
+            const bool ok = kc < ke;
 #pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    if (k_ok && wrow_ok[t])
-                        wv[u][t] = *reinterpret_cast<const uint4*>(wrow[t] + kc);
-                    else
-                        wv[u][t] = make_uint4(0, 0, 0, 0);
-                }
-            }
-            if (k_ok && arow_ok) {
-                float4 a0 = *reinterpret_cast<const float4*>(xrow + kc);
-                float4 a1 = *reinterpret_cast<const float4*>(xrow + kc + 4);
-                f[u][0] = a0.x; f[u][1] = a0.y; f[u][2] = a0.z; f[u][3] = a0.w;
-                f[u][4] = a1.x; f[u][5] = a1.y; f[u][6] = a1.z; f[u][7] = a1.w;
-                if (ex.ln_g) {
-                    float4 g0 = *reinterpret_cast<const float4*>(ex.ln_g + kc);
-                    float4 g1 = *reinterpret_cast<const float4*>(ex.ln_g + kc + 4);
-                    float4 b0 = *reinterpret_cast<const float4*>(ex.ln_b + kc);
-                    float4 b1 = *reinterpret_cast<const float4*>(ex.ln_b + kc + 4);
-                    const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-                    const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-                    for (int i = 0; i < 8; i++) {
-                        float normalized = (f[u][i] - ln_mean) * ln_inv;
-                        f[u][i] = normalized * gg[i] + bb[i];
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; i++) f[u][i] = 0.f;
+            for (int t = 0; t < NT; t++)
+                gr.w[u][t] = __builtin_amdgcn_raw_buffer_load_b128(rsw[t], ok ? (r * K + kc) * 2 : kOutOfRange, 0, 0);
+            const int xo = ok ? (int)((r * xs + kc) * 4) : kOutOfRange;
+            gr.xa[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rsx, xo, 0, 0);
+            gr.xa[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rsx, xo + 16, 0, 0);
+            if constexpr (LN) {
+                const int go = ok ? kc * 4 : kOutOfRange;
+                gr.lg[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rsg, go, 0, 0);
+                gr.lg[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rsg, go + 16, 0, 0);
+                gr.lb[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rsb, go, 0, 0);
+                gr.lb[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rsb, go + 16, 0, 0);
             }
         }
+    };
+    auto compute = [&](int k0, const Group& gr) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
+            float f[8];
+#pragma unroll
+            // element by value: __builtin_bit_cast on a vector-element
+            // lvalue reads element 0 with this compiler
+            for (int i = 0; i < 8; i++) f[i] = __uint_as_float(gr.xa[u][i >> 2][i & 3]);
+            if constexpr (LN) {
+                // k past the range: the normalised zero is masked so it can
+                // never meet an infinite inverse deviation
+                const bool ok = k0 + 32 * u + 8 * g < ke;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float gg = __uint_as_float(gr.lg[u][i >> 2][i & 3]);
+                    const float bb = __uint_as_float(gr.lb[u][i >> 2][i & 3]);
+                    const float normalized = (f[i] - ln_mean) * ln_inv;
+                    f[i] = ok ? normalized * gg + bb : 0.f;
+                }
+            }
             bf16x8 hi, lo;
-            split_hi_lo(f[u], hi, lo);
+            split_hi_lo(f, hi, lo);
 #pragma unroll
             for (int t = 0; t < NT; t++) {
-                bf16x8 b = __builtin_bit_cast(bf16x8, wv[u][t]);
+                const bf16x8 b = __builtin_bit_cast(bf16x8, gr.w[u][t]);
                 acc[t] = mfma16x16x32(hi, b, acc[t]);
                 acc[t] = mfma16x16x32(lo, b, acc[t]);
             }
         }
+    };
+    const int nit = ke > kb ? (ke - kb + 32 * U - 1) / (32 * U) : 0;
+    Group ga, gb;
+    load(kb, ga);
+    for (int i = 0; i < nit; i += 2) {
+        load(kb + 32 * U * (i + 1), gb);
+        compute(kb + 32 * U * i, ga);
+        load(kb + 32 * U * (i + 2), ga);
+        if (i + 1 < nit) compute(kb + 32 * U * (i + 1), gb);
     }
 
 #pragma unroll
@@ -687,16 +679,26 @@ __global__ __launch_bounds__(256) void k_splitk_epilogue(const float* __restrict
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
     const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+    // raw buffer loads with no branch around them (slices past S, a missing
+    // bias or residual read as zeros), all in flight before the adds
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, (long long)S * total * 4);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias, bias ? (long long)N * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(residual, residual ? total * 4 : 0);
     float p[kEpiSlices];
 #pragma unroll
-    for (int q = 0; q < kEpiSlices; q++) p[q] = q < S ? part[(size_t)q * total + i] : 0.f;
+    for (int q = 0; q < kEpiSlices; q++) {
+        const int off = q < S ? (int)(((int64_t)q * total + i) * 4) : kOutOfRange;
+        p[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, off, 0, 0));
+    }
+    const float bv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, n * 4, 0, 0));
+    const float rv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, (int)(i * 4), 0, 0));
     float sum = p[0];
 #pragma unroll
     for (int q = 1; q < kEpiSlices; q++)
         if (q < S) sum += p[q];
-    if (bias) sum = sum + bias[n];
+    if (bias) sum = sum + bv;
     if (epilogue == GORCH_HIP_EPI_GELU) sum = gelu_tanh(sum);
-    if (residual) sum = residual[i] + sum;
+    if (residual) sum = rv + sum;
     *od.at(m, n) = sum;
 }
 
@@ -880,16 +882,12 @@ template <int NT, int NW, int U>
 static void launch_t(hipStream_t s, dim3 grid, const float* x, const uint16_t* W, const float* bias,
                      const float* residual, const OutDesc& od, int M, int N, int K, int kw, int epilogue,
                      const LinearExtras& ex) {
-    static const int lx = env_int("GORCH_HIP_GEMV_LX", 0);
-    if constexpr (U == 4 && NT * NW <= 16) {
-        if (lx) {
-            hipLaunchKernelGGL((k_linear_bf16_mfma<NT, NW, U, true>), grid, dim3(NW * 64), 0, s, x, W, bias,
-                               residual, od, M, N, K, kw, epilogue, ex);
-            return;
-        }
-    }
-    hipLaunchKernelGGL((k_linear_bf16_mfma<NT, NW, U, false>), grid, dim3(NW * 64), 0, s, x, W, bias, residual,
-                       od, M, N, K, kw, epilogue, ex);
+    if (ex.ln_g)
+        hipLaunchKernelGGL((k_linear_bf16_mfma<NT, NW, U, true>), grid, dim3(NW * 64), 0, s, x, W, bias, residual,
+                           od, M, N, K, kw, epilogue, ex);
+    else
+        hipLaunchKernelGGL((k_linear_bf16_mfma<NT, NW, U, false>), grid, dim3(NW * 64), 0, s, x, W, bias, residual,
+                           od, M, N, K, kw, epilogue, ex);
 }
 
 int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
@@ -920,8 +918,13 @@ static int launch_mfma_gemv(hipStream_t s, const float* x, const uint16_t* W, co
         span = ex.kslice;
         gy = (K + ex.kslice - 1) / ex.kslice;
         ex.ksplit = gy;
-        while (p.nw > 1 && (span + p.nw - 1) / p.nw < 32) p.nw /= 2;
+        // about one 64-wide load group (U = 2) per wave and slice
+        while (p.nw > 1 && (span + p.nw - 1) / p.nw < 64) p.nw /= 2;
+        p.u = 2;
     }
+    // the double-buffered load groups spill beyond these (NW * U) sizes
+    if (p.nw >= 8 && p.u > 4) p.u = 4;
+    if (p.nw >= 16 && p.u > 2) p.u = 2;
     int per = (span + p.nw - 1) / p.nw;
     int kw = (per + 31) / 32 * 32;
     dim3 grid((N + 16 * p.nt - 1) / (16 * p.nt), gy);
@@ -932,7 +935,8 @@ static int launch_mfma_gemv(hipStream_t s, const float* x, const uint16_t* W, co
         return check_launch("linear_bf16");                                                  \
     }
 #define GH_CASES_U(T, WV) GH_CASE(T, WV, 2) GH_CASE(T, WV, 4) GH_CASE(T, WV, 8)
-#define GH_CASES_W(T) GH_CASES_U(T, 1) GH_CASES_U(T, 2) GH_CASES_U(T, 4) GH_CASES_U(T, 8) GH_CASES_U(T, 16)
+#define GH_CASES_W(T) \
+    GH_CASES_U(T, 1) GH_CASES_U(T, 2) GH_CASES_U(T, 4) GH_CASE(T, 8, 2) GH_CASE(T, 8, 4) GH_CASE(T, 16, 2)
     GH_CASES_W(1) GH_CASES_W(2) GH_CASES_W(4)
 #undef GH_CASES_W
 #undef GH_CASES_U
@@ -964,18 +968,22 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
     // 2..16 rows over a narrow weight (few 16-row tiles) and a long K: split
     // K across blocks into partials in the stream's scratch, then one small
     // epilogue kernel (a CU streams only ~20 GB/s, so 48..128 tiles alone
-    // cannot pull the weight at full rate)
+    // cannot pull the weight at full rate). Wider weights stay unsplit:
+    // 8-tile K-slice blocks measured slower at 16 rows (12.5 vs 9.4 us at
+    // K 1600, N 4800) once the epilogue kernel is counted.
     static const int auto_split = env_int("GORCH_HIP_GEMV_SPLIT", 1);
+    static const int split_blocks = env_int("GORCH_HIP_GEMV_SPLIT_BLOCKS", 300);
     const int ntiles_all = (N + 15) / 16;
     if (auto_split && M >= 2 && !ex.argmax_key && ntiles_all < 128 && K >= 1024) {
-        const int blocks_per_slice = (ntiles_all + 1) / 2;  // 2 tiles per block
-        const int S = ksplit_slices(K, std::min(kEpiSlices, std::max(2, 300 / blocks_per_slice)));
+        const int nt = 2;
+        const int blocks_per_slice = (ntiles_all + nt - 1) / nt;
+        const int S = ksplit_slices(K, std::min(kEpiSlices, std::max(2, split_blocks / blocks_per_slice)));
         void* part = S >= 2 ? stream_scratch(s, (size_t)S * M * N * sizeof(float)) : nullptr;
         if (part) {
             LinearExtras sx = ex;
             sx.part = static_cast<float*>(part);
             sx.ksplit = S;
-            sx.split_nt = 2;
+            sx.split_nt = nt;
             GH_TRY(launch_mfma_gemv(s, x, W, nullptr, nullptr, OutDesc::plain(nullptr, N), M, N, K,
                                     GORCH_HIP_EPI_NONE, sx));
             return launch_splitk_epilogue(s, sx.part, S, M, N, bias, residual, od, epilogue);

@@ -146,8 +146,9 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
     // 2..16 rows: the residual Linears (Wo, FFN2) are split over K across
     // blocks (their N = d alone gives too few blocks to pull HBM at full
     // rate); one small per-row kernel adds the slices, bias and residual and
-    // leaves the next LayerNorm's statistics, which the following fused GEMV
-    // reads instead of recomputing them in every block.
+    // writes the next LayerNorm's output h, which the following GEMV reads
+    // as a plain operand (a LayerNorm fused into the GEMV's loads costs
+    // ~3.5 us per call at 16 rows, d 1600, for its gamma/beta loads).
     const bool batched = fused && rows >= 2 && d <= kReduceRowsMaxCols;
     static const int split_blocks = [] {
         const char* e = getenv("GORCH_HIP_SPLIT_BLOCKS");
@@ -163,7 +164,9 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         return ksplit_slices(K, S);
     };
     GH_TRY(launch_embed_pos(s, g->wte, g->wpe, g->ids, pos, g->x, d, n, rows));
-    if (batched) GH_TRY(launch_reduce_rows(s, nullptr, 0, nullptr, g->x, rows, d, eps, g->stats));
+    if (batched)
+        GH_TRY(launch_reduce_rows(s, nullptr, 0, nullptr, g->x, rows, d, eps, g->stats, g->L[0].ln1_g,
+                                  g->L[0].ln1_b, g->h));
     for (int l = 0; l < g->layers; l++) {
         const LayerW& w = g->L[l];
         OutDesc od{};
@@ -185,13 +188,15 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             od.use_pos[sgi] = 1;
         }
         LinearExtras ln1, ln2;
-        if (fused) {
+        if (batched) {
+            GH_TRY(launch_linear_bf16_od(s, g->h, w.wqkv, w.bqkv, nullptr, od, rows, 3 * d, d, GORCH_HIP_EPI_NONE,
+                                         LinearExtras{}));
+        } else if (fused) {
             ln1.ln_g = w.ln1_g;
             ln1.ln_b = w.ln1_b;
             ln2.ln_g = w.ln2_g;
             ln2.ln_b = w.ln2_b;
             ln1.ln_eps = ln2.ln_eps = eps;
-            if (batched) ln1.ln_stats = ln2.ln_stats = g->stats;
             GH_TRY(launch_linear_bf16_od(s, g->x, w.wqkv, w.bqkv, nullptr, od, rows, 3 * d, d, GORCH_HIP_EPI_NONE,
                                          ln1));
         } else {
@@ -208,11 +213,14 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             sp.ksplit = split_for(d);
             GH_TRY(launch_linear_bf16_od(s, g->att, w.wo, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d, d,
                                          GORCH_HIP_EPI_NONE, sp));
-            GH_TRY(launch_reduce_rows(s, g->part, sp.ksplit, w.bo, g->x, rows, d, eps, g->stats));
+            GH_TRY(launch_reduce_rows(s, g->part, sp.ksplit, w.bo, g->x, rows, d, eps, g->stats, w.ln2_g, w.ln2_b,
+                                      g->h));
         } else {
             GH_TRY(launch_linear_bf16(s, g->att, w.wo, w.bo, g->x, g->x, rows, d, d, GORCH_HIP_EPI_NONE));
         }
-        if (fused) {
+        if (batched) {
+            GH_TRY(launch_linear_bf16(s, g->h, w.w1, w.b1, nullptr, g->ff, rows, 4 * d, d, GORCH_HIP_EPI_GELU));
+        } else if (fused) {
             GH_TRY(launch_linear_bf16_od(s, g->x, w.w1, w.b1, nullptr, OutDesc::plain(g->ff, 4 * d), rows, 4 * d,
                                          d, GORCH_HIP_EPI_GELU, ln2));
         } else {
@@ -225,7 +233,11 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             sp.ksplit = split_for(4 * d);
             GH_TRY(launch_linear_bf16_od(s, g->ff, w.w2, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d, 4 * d,
                                          GORCH_HIP_EPI_NONE, sp));
-            GH_TRY(launch_reduce_rows(s, g->part, sp.ksplit, w.b2, g->x, rows, d, eps, g->stats));
+            // the next LayerNorm: the next layer's first, or the final one
+            const bool last = l + 1 == g->layers;
+            GH_TRY(launch_reduce_rows(s, g->part, sp.ksplit, w.b2, g->x, rows, d, eps, g->stats,
+                                      last ? g->lnf_g : g->L[l + 1].ln1_g, last ? g->lnf_b : g->L[l + 1].ln1_b,
+                                      g->h));
         } else {
             GH_TRY(launch_linear_bf16(s, g->ff, w.w2, w.b2, g->x, g->x, rows, d, 4 * d, GORCH_HIP_EPI_NONE));
         }
@@ -233,14 +245,21 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
     const int head_rows = all_rows ? rows : B;
     const float* head_in = all_rows ? g->x : g->x + (size_t)(n - 1) * d;
     const long long head_stride = all_rows ? d : (long long)n * d;
-    if (head_rows <= 16) {
+    if (batched) {
+        // h holds LayerNorm_f of every row of x, laid out like x
+        LinearExtras lf;
+        lf.x_stride = head_stride;
+        lf.argmax_key = all_rows ? nullptr : argmax_key;
+        const float* head_h = g->h + (head_in - g->x);
+        GH_TRY(launch_linear_bf16_od(s, head_h, g->wlm, g->blm, nullptr, OutDesc::plain(g->logits, g->vocab),
+                                     head_rows, g->vocab, d, GORCH_HIP_EPI_NONE, lf));
+    } else if (head_rows <= 16) {
         LinearExtras lf;
         lf.ln_g = g->lnf_g;
         lf.ln_b = g->lnf_b;
         lf.ln_eps = eps;
         lf.x_stride = head_stride;
         lf.argmax_key = all_rows ? nullptr : argmax_key;
-        if (batched && head_stride == d) lf.ln_stats = g->stats;  // the head's rows are x's rows
         if (head_rows == 1 && g->vocab >= 16384) {
             // one row, many weight rows: every wave of the register GEMV
             // would recompute the statistics; one small kernel does it once
@@ -598,6 +617,10 @@ int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* g, const int* prompts
                 g->gen_exec = nullptr;
                 g->gen_graph = nullptr;
                 g->gen_sig.clear();
+                // the step's K-split Linears take their partials from the
+                // stream's scratch, which cannot grow under capture: size
+                // it for the widest of them (the FFN-up, 4d) first
+                (void)stream_scratch(s, (size_t)kMaxSplit * std::min(batch, 16) * 4 * g->dim * sizeof(float));
                 if (check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture")) {
                     fail(GORCH_HIP_ERUNTIME);
                     break;

@@ -68,20 +68,37 @@ constexpr int kRedCols = kReduceRowsMaxCols / 256, kRedSlices = 8;
 
 __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ part, int S,
                                                      const float* __restrict__ bias, float* __restrict__ x, int M,
-                                                     int N, float eps, float2* __restrict__ stats) {
+                                                     int N, float eps, float2* __restrict__ stats,
+                                                     const float* __restrict__ ln_g, const float* __restrict__ ln_b,
+                                                     float* __restrict__ h) {
     __shared__ double sh[4];
     const int m = blockIdx.x;
     float* row = x + (size_t)m * N;
-    float v[kRedCols];
+    // raw buffer loads, all issued before any add and with no branch around
+    // them: columns past N, slices past S and a missing bias read as zeros
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(row, (long long)N * 4);
+    // slice q of row m sits at part + (q * M + m) * N; the resource spans
+    // slice 0's row through slice S - 1's row (empty when S == 0)
+    const long long pspan = S > 0 ? ((long long)(S - 1) * M + 1) * N * 4 : 0;
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(part + (S > 0 ? (size_t)m * N : 0), pspan);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias, bias ? (long long)N * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(ln_g, h ? (long long)N * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rbe = make_rsrc(ln_b, h ? (long long)N * 4 : 0);
+    float v[kRedCols], bv[kRedCols], gv[kRedCols], be[kRedCols];
     float p[kRedCols][kRedSlices];
 #pragma unroll
     for (int c = 0; c < kRedCols; c++) {
         const int j = threadIdx.x + 256 * c;
-        const bool ok = j < N;
-        v[c] = ok ? row[j] : 0.f;
+        const int off = j < N ? j * 4 : kOutOfRange;
+        v[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0));
+        bv[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0));
+        gv[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, off, 0, 0));
+        be[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbe, off, 0, 0));
 #pragma unroll
-        for (int q = 0; q < kRedSlices; q++)
-            p[c][q] = (ok && q < S) ? part[((size_t)q * M + m) * N + j] : 0.f;
+        for (int q = 0; q < kRedSlices; q++) {
+            const int po = (j < N && q < S) ? (int)(((size_t)q * M * N + j) * 4) : kOutOfRange;
+            p[c][q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, po, 0, 0));
+        }
     }
     double s1 = 0.0;
 #pragma unroll
@@ -93,13 +110,13 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
 #pragma unroll
             for (int q = 1; q < kRedSlices; q++)
                 if (q < S) acc += p[c][q];
-            if (bias) acc = acc + bias[j];
+            if (bias) acc = acc + bv[c];
             v[c] = v[c] + acc;
             row[j] = v[c];
         }
         s1 += (double)v[c];
     }
-    if (!stats) return;
+    if (!stats && !h) return;
     const double mean = block_sum_d(s1, sh) / (double)N;
     double s2 = 0.0;
 #pragma unroll
@@ -110,17 +127,31 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
         s2 += d * d;
     }
     const double var = block_sum_d(s2, sh) / (double)N;
-    if (threadIdx.x == 0) stats[m] = make_float2((float)mean, (float)(1.0 / sqrt(var + (double)eps)));
+    const float fm = (float)mean, inv = (float)(1.0 / sqrt(var + (double)eps));
+    if (stats && threadIdx.x == 0) stats[m] = make_float2(fm, inv);
+    if (!h) return;
+    // the same f32 operations as a LayerNorm fused into a GEMV's operand load
+#pragma unroll
+    for (int c = 0; c < kRedCols; c++) {
+        const int j = threadIdx.x + 256 * c;
+        if (j >= N) continue;
+        const float normalized = (v[c] - fm) * inv;
+        h[(size_t)m * N + j] = normalized * gv[c] + be[c];
+    }
 }
 
 int launch_reduce_rows(hipStream_t s, const float* part, int S, const float* bias, float* x, int M, int N,
-                       float eps, float2* stats) {
+                       float eps, float2* stats, const float* ln_g, const float* ln_b, float* h) {
     if (M == 0) return GORCH_HIP_OK;
     if (N > 256 * kRedCols || S > kRedSlices) {
         set_error("reduce_rows: at most 2048 columns and 8 slices");
         return GORCH_HIP_EUNSUPPORTED;
     }
-    hipLaunchKernelGGL(k_reduce_rows, dim3(M), dim3(256), 0, s, part, S, bias, x, M, N, eps, stats);
+    if (h && (!ln_g || !ln_b)) {
+        set_error("reduce_rows: the normalised output needs gamma and beta");
+        return GORCH_HIP_EINVAL;
+    }
+    hipLaunchKernelGGL(k_reduce_rows, dim3(M), dim3(256), 0, s, part, S, bias, x, M, N, eps, stats, ln_g, ln_b, h);
     count(CNT_NORM);
     return check_launch("reduce_rows");
 }
