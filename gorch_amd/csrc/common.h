@@ -144,14 +144,17 @@ struct OutDesc {
         const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((int)(v >> 32));
         return (long long)(((unsigned long long)hi << 32) | lo);
     }
-    __device__ __forceinline__ float* at(int m, int n) const {
+    __device__ __forceinline__ float* at(int m, int n) const { return at_p(m, n, pos_dev ? *pos_dev : 0); }
+    // pos: the value of *pos_dev, read once by a caller that writes in a
+    // loop (a load in its epilogue would wait for its prefetched weights)
+    __device__ __forceinline__ float* at_p(int m, int n, int pos) const {
         int seq = 0, r = m;
         if (rows_per_seq < (1 << 30)) {
             seq = m / rows_per_seq;
             r = m - seq * rows_per_seq;
         }
         if (nseg == 1) {
-            if (use_pos[0]) r += *pos_dev;
+            if (use_pos[0]) r += pos;
             return ptr[0] + seq * seq_stride[0] + (long long)r * row_stride[0] + n;
         }
         const bool s1 = n >= __builtin_amdgcn_readfirstlane(n_end[0]);
@@ -170,7 +173,7 @@ struct OutDesc {
         const long long ss = s2 ? ss2 : (s1 ? ss1 : ss0);
         const long long rs = s2 ? rs2 : (s1 ? rs1 : rs0);
         const int up = s2 ? up2 : (s1 ? up1 : up0);
-        if (up) r += *pos_dev;
+        if (up) r += pos;
         return p + seq * ss + (long long)r * rs + (n - nb);
     }
 };

@@ -340,108 +340,142 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
                                                  const float* __restrict__ bias, const float* residual, OutDesc od,
                                                  int N, int K, int epilogue, LinearExtras ex) {
     __shared__ unsigned long long s_key;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int sub = lane % T, rloc = lane / T;
+    constexpr int RPI = 64 / T;
+    const int ngroups = (N + RPI - 1) / RPI;
+    const int stride = gridDim.x * 4;
+    int rg = blockIdx.x * 4 + wave;
+
+    // Group g = rows g*RPI .. of W with their bias and residual values, as
+    // raw buffer loads over the group's rows: rows past N (and groups past
+    // the wave's last) read zeros, with no branch around the loads, so the
+    // next group stays in flight while this one is reduced and written.
+    struct Group {
+        uint4 w[C];
+        float b, r;
+    };
+    auto load = [&](int g, Group& gr) {
+        const int rows = max(0, min(RPI, N - g * RPI));
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(W + (size_t)g * RPI * K, (long long)rows * K * 2);
+#pragma unroll
+        for (int c = 0; c < C; c++)
+            gr.w[c] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (rloc * K + 8 * (sub + T * c)) * 2, 0, 0));
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias + (size_t)g * RPI, bias ? (long long)rows * 4 : 0);
+        const __amdgpu_buffer_rsrc_t rr = make_rsrc(residual + (size_t)g * RPI, residual ? (long long)rows * 4 : 0);
+        gr.b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, rloc * 4, 0, 0));
+        gr.r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, rloc * 4, 0, 0));
+    };
+    Group ga, gb;
+    load(rg, ga);  // the weight stream starts before the activations are ready
+
+    // the activation row (K = 8*T*C exactly), LayerNorm gamma/beta with it
+    float xr[C][8], gg[LN ? C : 1][8], bb[LN ? C : 1][8];
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        const int k = 8 * (sub + T * c);
+        const float4 a0 = *reinterpret_cast<const float4*>(x + k);
+        const float4 a1 = *reinterpret_cast<const float4*>(x + k + 4);
+        xr[c][0] = a0.x; xr[c][1] = a0.y; xr[c][2] = a0.z; xr[c][3] = a0.w;
+        xr[c][4] = a1.x; xr[c][5] = a1.y; xr[c][6] = a1.z; xr[c][7] = a1.w;
+        if constexpr (LN) {
+            const float4 g0 = *reinterpret_cast<const float4*>(ex.ln_g + k);
+            const float4 g1 = *reinterpret_cast<const float4*>(ex.ln_g + k + 4);
+            const float4 b0 = *reinterpret_cast<const float4*>(ex.ln_b + k);
+            const float4 b1 = *reinterpret_cast<const float4*>(ex.ln_b + k + 4);
+            gg[c][0] = g0.x; gg[c][1] = g0.y; gg[c][2] = g0.z; gg[c][3] = g0.w;
+            gg[c][4] = g1.x; gg[c][5] = g1.y; gg[c][6] = g1.z; gg[c][7] = g1.w;
+            bb[c][0] = b0.x; bb[c][1] = b0.y; bb[c][2] = b0.z; bb[c][3] = b0.w;
+            bb[c][4] = b1.x; bb[c][5] = b1.y; bb[c][6] = b1.z; bb[c][7] = b1.w;
+        }
+    }
+    const int posv = od.pos_dev ? *od.pos_dev : 0;
     if (ex.argmax_key) {
         if (tid == 0) s_key = 0ull;
         __syncthreads();
     }
-    const int sub = lane % T, rloc = lane / T;
-    constexpr int RPI = 64 / T;
-    float xr[C][8];
-#pragma unroll
-    for (int c = 0; c < C; c++) {
-        const float4 a0 = *reinterpret_cast<const float4*>(x + 8 * (sub + T * c));
-        const float4 a1 = *reinterpret_cast<const float4*>(x + 8 * (sub + T * c) + 4);
-        xr[c][0] = a0.x; xr[c][1] = a0.y; xr[c][2] = a0.z; xr[c][3] = a0.w;
-        xr[c][4] = a1.x; xr[c][5] = a1.y; xr[c][6] = a1.z; xr[c][7] = a1.w;
-    }
-    if (LN) {
+    if constexpr (LN) {
         float fm, inv;
         if (ex.ln_stats) {
             fm = ex.ln_stats[0].x;
             inv = ex.ln_stats[0].y;
         } else {
-        // the wave's lanes hold the row RPI times over (one copy per rloc):
-        // sum over the first T lanes only
-        double s1 = 0.0;
-        if (rloc == 0)
+            // the wave's lanes hold the row RPI times over (one copy per
+            // rloc): sum over the first T lanes only
+            double s1 = 0.0;
+            if (rloc == 0)
 #pragma unroll
-            for (int c = 0; c < C; c++)
+                for (int c = 0; c < C; c++)
 #pragma unroll
-                for (int i = 0; i < 8; i++) s1 += (double)xr[c][i];
-        const double mean = wave_sum_d(s1) / (double)K;
-        double s2 = 0.0;
-        if (rloc == 0)
+                    for (int i = 0; i < 8; i++) s1 += (double)xr[c][i];
+            const double mean = wave_sum_d(s1) / (double)K;
+            double s2 = 0.0;
+            if (rloc == 0)
 #pragma unroll
-            for (int c = 0; c < C; c++)
+                for (int c = 0; c < C; c++)
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const double dd = (double)xr[c][i] - mean;
-                    s2 += dd * dd;
-                }
-        const double var = wave_sum_d(s2) / (double)K;
-        inv = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
-        fm = (float)mean;
+                    for (int i = 0; i < 8; i++) {
+                        const double dd = (double)xr[c][i] - mean;
+                        s2 += dd * dd;
+                    }
+            const double var = wave_sum_d(s2) / (double)K;
+            inv = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
+            fm = (float)mean;
         }
 #pragma unroll
-        for (int c = 0; c < C; c++) {
-            const int k = 8 * (sub + T * c);
-            const float4 g0 = *reinterpret_cast<const float4*>(ex.ln_g + k);
-            const float4 g1 = *reinterpret_cast<const float4*>(ex.ln_g + k + 4);
-            const float4 b0 = *reinterpret_cast<const float4*>(ex.ln_b + k);
-            const float4 b1 = *reinterpret_cast<const float4*>(ex.ln_b + k + 4);
-            const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-            const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        for (int c = 0; c < C; c++)
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const float normalized = (xr[c][i] - fm) * inv;
-                xr[c][i] = normalized * gg[i] + bb[i];
+                xr[c][i] = normalized * gg[c][i] + bb[c][i];
             }
-        }
     }
 
-    const int ngroups = (N + RPI - 1) / RPI;
-    const int stride = gridDim.x * 4;
-    int rg = blockIdx.x * 4 + wave;
-    uint4 wv[C];
-    auto load = [&](int g) {
-        const int row = g * RPI + rloc;
-        const bool ok = g < ngroups && row < N;
-        const uint4* wr = reinterpret_cast<const uint4*>(W + (size_t)(ok ? row : 0) * K) + sub;
-#pragma unroll
-        for (int c = 0; c < C; c++) wv[c] = ok ? wr[(size_t)T * c] : make_uint4(0, 0, 0, 0);
-    };
-    load(rg);
     unsigned long long best = 0ull;
-    for (; rg < ngroups; rg += stride) {
-        uint4 cur[C];
-#pragma unroll
-        for (int c = 0; c < C; c++) cur[c] = wv[c];
-        load(rg + stride);  // next group's stream starts before this one is reduced
+    auto compute = [&](int g, const Group& gr) {
         float acc = 0.f;
 #pragma unroll
         for (int c = 0; c < C; c++) {
-            acc += xr[c][0] * bf16_lo(cur[c].x) + xr[c][1] * bf16_hi(cur[c].x) + xr[c][2] * bf16_lo(cur[c].y) +
-                   xr[c][3] * bf16_hi(cur[c].y) + xr[c][4] * bf16_lo(cur[c].z) + xr[c][5] * bf16_hi(cur[c].z) +
-                   xr[c][6] * bf16_lo(cur[c].w) + xr[c][7] * bf16_hi(cur[c].w);
+            const uint4 cw = gr.w[c];
+            acc += xr[c][0] * bf16_lo(cw.x) + xr[c][1] * bf16_hi(cw.x) + xr[c][2] * bf16_lo(cw.y) +
+                   xr[c][3] * bf16_hi(cw.y) + xr[c][4] * bf16_lo(cw.z) + xr[c][5] * bf16_hi(cw.z) +
+                   xr[c][6] * bf16_lo(cw.w) + xr[c][7] * bf16_hi(cw.w);
         }
 #pragma unroll
         for (int o = T / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-        const int row = rg * RPI + rloc;
+        const int row = g * RPI + rloc;
         if (sub == 0 && row < N) {
             float v = acc;
-            if (bias) v = v + bias[row];
+            if (bias) v = v + gr.b;
             if (epilogue == GORCH_HIP_EPI_GELU) v = gelu_tanh(v);
-            if (residual) v = residual[row] + v;
-            *od.at(0, row) = v;
+            if (residual) v = gr.r + v;
+            *od.at_p(0, row, posv) = v;
             if (ex.argmax_key) {
                 const unsigned long long key = argmax_pack(v, row);
                 best = key > best ? key : best;
             }
         }
+    };
+    // two register sets: the next group's stream is in flight while this
+    // one is reduced and written
+    for (; rg < ngroups; rg += 2 * stride) {
+        load(rg + stride, gb);
+        compute(rg, ga);
+        load(rg + 2 * stride, ga);
+        if (rg + stride < ngroups) compute(rg + stride, gb);
     }
     if (ex.argmax_key) {
-        atomicMax(&s_key, best);
+        // the wave's maximum by shuffles, then one LDS atomic per wave
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const unsigned long long other =
+                ((unsigned long long)(unsigned)__shfl_xor((int)(best >> 32), o, 64) << 32) |
+                (unsigned)__shfl_xor((int)(best & 0xffffffffull), o, 64);
+            best = other > best ? other : best;
+        }
+        if (lane == 0) atomicMax(&s_key, best);
         __syncthreads();
         if (tid == 0) atomicMax(ex.argmax_key, s_key);
     }
@@ -734,8 +768,13 @@ static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const flo
     const int rpi = 64 / T;
     const int ngroups = (N + rpi - 1) / rpi;
     static const int max_blocks = env_int("GORCH_HIP_GEMV_M1_BLOCKS", 4096);
+    // with the argmax fusion every block ends in one 64-bit atomicMax on the
+    // same global word, and those serialise at one L2 channel (4096 of them
+    // cost ~40 us): fewer, longer-running blocks
+    static const int max_blocks_argmax = env_int("GORCH_HIP_GEMV_M1_ARGMAX_BLOCKS", 512);
     int blocks = (ngroups + 3) / 4;
     if (blocks > max_blocks) blocks = max_blocks;
+    if (ex.argmax_key && blocks > max_blocks_argmax) blocks = max_blocks_argmax;
 #define GH_M1(TT, CC)                                                                                        \
     if (T == TT && C == CC) {                                                                                \
         if (ex.ln_g)                                                                                         \
