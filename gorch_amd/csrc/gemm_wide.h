@@ -57,14 +57,15 @@ struct WideGemm {
     };
 
     // a[p] + row * lda: row of plane p (nrows valid); w[b] + n * K: column n
-    // of weight b (ncols valid). epi(row, col, vals[NB]) per output.
+    // of weight b (ncols valid). Sums k in [kb, ke) (a K slice; kb % 8 ==
+    // 0). epi(row, col, vals[NB]) per output.
     template <class Epi>
     __device__ static void run(Smem& sm, const uint16_t* const* a, long long lda, int nrows,
-                               const uint16_t* const* w, int ncols, int K, Epi& epi) {
+                               const uint16_t* const* w, int ncols, int K, int kb, int ke, Epi& epi) {
         const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
         const int wm = wave >> 2, wn = wave & 3;
         const int r = lane & 15, g = lane >> 4;
-        const int nk = (K + BK - 1) / BK;
+        const int nk = (ke - kb + BK - 1) / BK;
 
         // one buffer resource per plane / weight, covering the tile's rows
         __amdgpu_buffer_rsrc_t rsa[NA], rsw[NB];
@@ -75,13 +76,13 @@ struct WideGemm {
 
         u32x4 ra[2][A_U4], rw[2][W_U4];
         auto gload = [&](int st, u32x4 (&ar)[A_U4], u32x4 (&wr)[W_U4]) {
-            const int k0 = st * BK;
+            const int k0 = kb + st * BK;
 #pragma unroll
             for (int i = 0; i < A_U4; i++) {
                 const int idx = tid + kThreads * i;
                 const int p = kThreads * i / (BM * CH), rem = idx % (BM * CH), row = rem / CH, c = rem % CH;
                 const int k = k0 + 8 * c;
-                const int off = k < K ? (min(row, nrows - 1) * (int)lda + k) * 2 : kOutOfRange;
+                const int off = k < ke ? (min(row, nrows - 1) * (int)lda + k) * 2 : kOutOfRange;
                 ar[i] = __builtin_amdgcn_raw_buffer_load_b128(rsa[p], off, 0, 0);
             }
 #pragma unroll
@@ -89,7 +90,7 @@ struct WideGemm {
                 const int idx = tid + kThreads * i;
                 const int b = kThreads * i / (BNW * CH), rem = idx % (BNW * CH), row = rem / CH, c = rem % CH;
                 const int k = k0 + 8 * c;
-                const int off = k < K ? (min(row, ncols - 1) * K + k) * 2 : kOutOfRange;
+                const int off = k < ke ? (min(row, ncols - 1) * K + k) * 2 : kOutOfRange;
                 wr[i] = __builtin_amdgcn_raw_buffer_load_b128(rsw[b], off, 0, 0);
             }
         };

@@ -578,11 +578,13 @@ __device__ __forceinline__ void mt_a(const uint4* xh, const uint4* xl, int ks, i
     }
 }
 
-// Finish tile ct: bias, GELU, residual, output and the block's argmax key.
-// acc: rows 4g..4g+3 of column 16*ct + r; bv = bias[16*ct + r].
+// Finish tile ct: bias, GELU, output and the block's argmax key (no
+// residual: a residual load here would wait for the prefetched weights).
+// acc: rows 4g..4g+3 of column 16*ct + r; bv = bias[16*ct + r], loaded with
+// the tile's weights.
 __device__ __forceinline__ void mt_finish(const floatx4& acc, int ct, int M, int N, const float* bias, float bv,
-                                          const float* residual, const OutDesc& od, int epilogue,
-                                          const LinearExtras& ex, unsigned long long* s_key) {
+                                          const OutDesc& od, int epilogue, const LinearExtras& ex,
+                                          unsigned long long* s_key) {
     const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
     const int on = ct * 16 + r;
     if (on >= N) return;
@@ -593,7 +595,6 @@ __device__ __forceinline__ void mt_finish(const floatx4& acc, int ct, int M, int
         float sum = acc[v4];
         if (bias) sum = sum + bv;  // bias[on], loaded with the tile's weights
         if (epilogue == GORCH_HIP_EPI_GELU) sum = gelu_tanh(sum);
-        if (residual) sum = residual[(size_t)om * N + on] + sum;
         *od.at(om, on) = sum;
         if (ex.argmax_key) atomicMax(&s_key[om], argmax_pack(sum, on));
     }
@@ -686,7 +687,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
             }
         }
         if (bat == nbat - 1) {
-            mt_finish(acc, t0 + tstride * ti, M, N, bias, bv, residual, od, epilogue, ex, s_key);
+            mt_finish(acc, t0 + tstride * ti, M, N, bias, bv, od, epilogue, ex, s_key);
             acc = floatx4{0.f, 0.f, 0.f, 0.f};
         }
     };
@@ -824,7 +825,7 @@ static int launch_mt(hipStream_t s, const float* x, const uint16_t* W, const flo
     const int ntiles = (N + 15) / 16;
     const int mr = M <= 4 ? 4 : (M <= 8 ? 8 : 16);
     const size_t lds = (size_t)((K + 127) / 128) * 16 * mr * 16 * 2;
-    if (lds > kMtLds) return -1;
+    if (lds > kMtLds || residual) return -1;  // the kernel has no residual add
     const int nw = nw_env ? nw_env : 16;
     const int st = st_env ? st_env : 2;
     const int bps = bps_env ? bps_env : std::min(256, ntiles);

@@ -32,6 +32,7 @@ namespace gh {
 constexpr int kMoeBM = 64, kMoeBK = 64, kMoeLD = kMoeBK + 16;
 constexpr int kMoeBNDual = 64, kMoeBNDown = 64;
 constexpr int kMaxExperts = 64;
+constexpr int kDownSlices = 2;  // K slices of the wide down GEMM at most
 constexpr int kMaxTopK = 8;
 
 struct MoeWs {
@@ -47,7 +48,7 @@ struct MoeWs {
     int* ntiles;     // [1]
     float* xg;       // [M*K, dim]
     float* h;        // [M*K, ffn]
-    float* yg;       // [M*K, dim]
+    float* yg;       // [kDownSlices][M*K, dim] (slice 0 only when unsplit)
 };
 
 static size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -74,7 +75,7 @@ static size_t moe_layout(int M, int dim, int ffn, int E, int K, char* base, MoeW
     w.ntiles = (int*)take(4);
     w.xg = (float*)take(MK * dim * 4);
     w.h = (float*)take(MK * ffn * 4);
-    w.yg = (float*)take(MK * dim * 4);
+    w.yg = (float*)take(kDownSlices * MK * dim * 4);
     if (ws) *ws = w;
     return off;
 }
@@ -233,9 +234,12 @@ __global__ void k_moe_gather(const float* __restrict__ x, const int* __restrict_
 
 // out[t] = sum over the token's K packed rows in ascending expert order
 // (the reference adds each expert's ScatterAdd contribution in order). One
-// thread per (token, 4 columns); dim % 4 == 0.
+// thread per (token, 4 columns); dim % 4 == 0. nsl > 1: the down GEMM left
+// raw K-slice partials, and a row's value is ((sum of slices) + bias) * w.
 __global__ void k_moe_combine(const float* __restrict__ yg, const int* __restrict__ inv,
-                              const int* __restrict__ topi, float* out, int M, int K, int dim) {
+                              const int* __restrict__ topi, float* out, int M, int K, int dim, int nsl,
+                              long long cslice, const float* __restrict__ bdown,
+                              const float* __restrict__ perm_w) {
     const int d4 = dim / 4;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)M * d4;
          i += (int64_t)gridDim.x * blockDim.x) {
@@ -250,7 +254,30 @@ __global__ void k_moe_combine(const float* __restrict__ yg, const int* __restric
             }
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
         for (int s = 0; s < K; s++) {
-            const float4 v = reinterpret_cast<const float4*>(yg + (size_t)inv[(size_t)t * K + order[s]] * dim)[c];
+            const int p = inv[(size_t)t * K + order[s]];
+            float4 v = reinterpret_cast<const float4*>(yg + (size_t)p * dim)[c];
+            if (nsl > 1) {
+                for (int z = 1; z < nsl; z++) {
+                    const float4 u = reinterpret_cast<const float4*>(yg + z * cslice + (size_t)p * dim)[c];
+                    v.x = v.x + u.x;
+                    v.y = v.y + u.y;
+                    v.z = v.z + u.z;
+                    v.w = v.w + u.w;
+                }
+                if (bdown) {
+                    const float4 b =
+                        reinterpret_cast<const float4*>(bdown + (size_t)topi[(size_t)t * K + order[s]] * dim)[c];
+                    v.x = v.x + b.x;
+                    v.y = v.y + b.y;
+                    v.z = v.z + b.z;
+                    v.w = v.w + b.w;
+                }
+                const float wgt = perm_w[p];  // weighted = exOut * w
+                v.x = v.x * wgt;
+                v.y = v.y * wgt;
+                v.z = v.z * wgt;
+                v.w = v.w * wgt;
+            }
             acc.x = acc.x + v.x;
             acc.y = acc.y + v.y;
             acc.z = acc.z + v.z;
@@ -408,7 +435,11 @@ __global__ __launch_bounds__(256) void k_moe_gemm(const float* __restrict__ A, c
 // keeps 256-wide tiles although at d = 1024 that leaves half the CUs idle:
 // 128-wide tiles on every CU measured slower (148 vs 121 us, 2048 tokens).
 // GORCH_HIP_MOE_WIDE=0 selects the 64 x 64 f32-activation kernels;
-// GORCH_HIP_MOE_DOWN_BN=128 the narrower down tile.
+// GORCH_HIP_MOE_DOWN_BN=128 the narrower down tile; GORCH_HIP_MOE_DOWN_SPLIT=2
+// splits the down GEMM's K over twice the blocks (raw partials, summed with
+// bias and routing weight by the combine), which measured within noise of
+// the unsplit kernel (118 vs 121 us): these GEMMs are bound by the traffic
+// from beyond L2, not by the number of busy CUs.
 constexpr int kWideBM = 128, kWideBNDual = 128, kWideBNDown = 256;
 
 __global__ void k_moe_gather_split(const float* __restrict__ x, const int* __restrict__ perm_tok, uint16_t* hi,
@@ -436,7 +467,8 @@ __global__ __launch_bounds__(512) void k_moe_wide(const uint16_t* __restrict__ A
                                                   const uint16_t* __restrict__ W1, const uint16_t* __restrict__ W2,
                                                   const float* __restrict__ b1, const float* __restrict__ b2,
                                                   float* __restrict__ C, uint16_t* __restrict__ Chi,
-                                                  uint16_t* __restrict__ Clo, int N, int Kd, MoeWs ws) {
+                                                  uint16_t* __restrict__ Clo, int N, int Kd, long long cslice,
+                                                  MoeWs ws) {
     using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true>;
     extern __shared__ __align__(16) uint4 moe_smem[];
     if ((int)blockIdx.y >= *ws.ntiles) return;
@@ -446,8 +478,21 @@ __global__ __launch_bounds__(512) void k_moe_wide(const uint16_t* __restrict__ A
     const uint16_t* w[2] = {W1 + ((size_t)e * N + n0) * Kd, DUAL ? W2 + ((size_t)e * N + n0) * Kd : nullptr};
     const float* bg = b1 ? b1 + (size_t)e * N + n0 : nullptr;
     const float* bu = (DUAL && b2) ? b2 + (size_t)e * N + n0 : nullptr;
+    // gridDim.z > 1 (down GEMM only): K slice blockIdx.z, raw partial sums
+    // to C + blockIdx.z * cslice; the combine adds the slices, bias and
+    // routing weight
+    // (the grid's default order already keeps each weight column tile on one
+    // XCD, blocks being dealt round-robin; an XCD-contiguous order of whole
+    // row tiles measured slower: 238 vs 194 us for the gate/up GEMM)
+    const int nsl = gridDim.z;
+    const int kslice = (Kd + nsl * 64 - 1) / (nsl * 64) * 64;
+    const int kb = blockIdx.z * kslice, ke = min(Kd, kb + kslice);
     auto epi = [&](int row, int col, const float* v) {
         const size_t o = (size_t)(r0 + row) * N + n0 + col;
+        if (!DUAL && nsl > 1) {
+            C[(size_t)blockIdx.z * cslice + o] = v[0];
+            return;
+        }
         float s = v[0];
         if (bg) s = s + bg[col];
         if constexpr (DUAL) {
@@ -461,13 +506,13 @@ __global__ __launch_bounds__(512) void k_moe_wide(const uint16_t* __restrict__ A
             C[o] = s * ws.perm_w[r0 + row];  // weighted = exOut * w
         }
     };
-    G::run(*reinterpret_cast<typename G::Smem*>(moe_smem), a, Kd, nrows, w, min(BNW, N - n0), Kd, epi);
+    G::run(*reinterpret_cast<typename G::Smem*>(moe_smem), a, Kd, nrows, w, min(BNW, N - n0), Kd, kb, ke, epi);
 }
 
 template <bool DUAL, int BNW>
 static int launch_moe_wide(hipStream_t s, dim3 grid, const uint16_t* Ahi, const uint16_t* Alo, const uint16_t* W1,
                            const uint16_t* W2, const float* b1, const float* b2, float* C, uint16_t* Chi,
-                           uint16_t* Clo, int N, int Kd, const MoeWs& ws) {
+                           uint16_t* Clo, int N, int Kd, long long cslice, const MoeWs& ws) {
     using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true>;
     static bool attr_set = false;
     if (!attr_set) {
@@ -477,7 +522,7 @@ static int launch_moe_wide(hipStream_t s, dim3 grid, const uint16_t* Ahi, const 
         attr_set = true;
     }
     hipLaunchKernelGGL((k_moe_wide<DUAL, BNW>), grid, dim3(G::kThreads), sizeof(typename G::Smem), s, Ahi, Alo, W1,
-                       W2, b1, b2, C, Chi, Clo, N, Kd, ws);
+                       W2, b1, b2, C, Chi, Clo, N, Kd, cslice, ws);
     return check_launch(DUAL ? "moe_wide_gate_up" : "moe_wide_down");
 }
 
@@ -522,6 +567,8 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
     GH_TRY(check_launch("moe_route"));
     const int MK = M * K;
     const int max_tiles = MK / tile_rows + E + 1;
+    int nsl = 1;            // K slices of the down GEMM's partials in yg
+    long long cslice = 0;   // their stride in floats
     if (wide) {
         // Xg and H hold (hi, lo) bf16 planes in the space of their f32 form
         uint16_t* xhi = reinterpret_cast<uint16_t*>(ws.xg);
@@ -533,17 +580,25 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
         GH_TRY(check_launch("moe_gather"));
         GH_TRY((launch_moe_wide<true, kWideBNDual>(s, dim3((F + kWideBNDual - 1) / kWideBNDual, max_tiles), xhi,
                                                   xlo, w->wgate, w->wup, w->bgate, w->bup, nullptr, hhi, hlo, F, d,
-                                                  ws)));
+                                                  0, ws)));
         static const int down_bn = [] {
             const char* e = getenv("GORCH_HIP_MOE_DOWN_BN");
             return e ? atoi(e) : kWideBNDown;
         }();
+        static const int down_split = [] {
+            const char* e = getenv("GORCH_HIP_MOE_DOWN_SPLIT");
+            return e ? std::max(1, std::min(kDownSlices, atoi(e))) : 1;
+        }();
+        nsl = F >= 64 * down_split ? down_split : 1;
+        cslice = (long long)MK * d;
         if (down_bn == 256)
-            GH_TRY((launch_moe_wide<false, 256>(s, dim3((d + 255) / 256, max_tiles), hhi, hlo, w->wdown, nullptr,
-                                                w->bdown, nullptr, ws.yg, nullptr, nullptr, d, F, ws)));
+            GH_TRY((launch_moe_wide<false, 256>(s, dim3((d + 255) / 256, max_tiles, nsl), hhi, hlo, w->wdown,
+                                                nullptr, w->bdown, nullptr, ws.yg, nullptr, nullptr, d, F, cslice,
+                                                ws)));
         else
-            GH_TRY((launch_moe_wide<false, 128>(s, dim3((d + 127) / 128, max_tiles), hhi, hlo, w->wdown, nullptr,
-                                                w->bdown, nullptr, ws.yg, nullptr, nullptr, d, F, ws)));
+            GH_TRY((launch_moe_wide<false, 128>(s, dim3((d + 127) / 128, max_tiles, nsl), hhi, hlo, w->wdown,
+                                                nullptr, w->bdown, nullptr, ws.yg, nullptr, nullptr, d, F, cslice,
+                                                ws)));
     } else {
         const int gblocks = (int)std::min<int64_t>(8192, ((int64_t)MK * d / 4 + 255) / 256);
         hipLaunchKernelGGL(k_moe_gather, dim3(gblocks), dim3(256), 0, s, x, ws.perm_tok, ws.xg, MK, d);
@@ -556,7 +611,8 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
         GH_TRY(check_launch("moe_gemm_down"));
     }
     const int cblocks = (int)std::min<int64_t>(8192, ((int64_t)M * d / 4 + 255) / 256);
-    hipLaunchKernelGGL(k_moe_combine, dim3(cblocks), dim3(256), 0, s, ws.yg, ws.inv, ws.topi, out, M, K, d);
+    hipLaunchKernelGGL(k_moe_combine, dim3(cblocks), dim3(256), 0, s, ws.yg, ws.inv, ws.topi, out, M, K, d, nsl,
+                       cslice, w->bdown, ws.perm_w);
     GH_TRY(check_launch("moe_combine"));
     count(CNT_MOE);
     return GORCH_HIP_OK;
