@@ -61,10 +61,11 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* __
 
 // One block per row: x[m] += bias + sum_s part[s][m] (slices in order, the
 // residual add of a K-split Linear), then the row's LayerNorm statistics in
-// f64 (nn/layernorm.go:61-91) for the next fused-LayerNorm GEMV. Each thread
-// owns up to kRedCols columns and issues all of their slice loads before
-// adding (S <= kRedSlices), so the row costs one memory round trip.
-constexpr int kRedCols = kReduceRowsMaxCols / 256, kRedSlices = 8;
+// f64 (nn/layernorm.go:61-91) and, given gamma/beta, the normalised row h.
+// Each thread owns up to kRedVec groups of 4 consecutive columns and issues
+// all of their 16-byte loads (row, S <= kRedSlices slices, bias, gamma,
+// beta) before adding, so the row costs one memory round trip. N % 4 == 0.
+constexpr int kRedVec = kReduceRowsMaxCols / 4 / 256, kRedSlices = 8;
 
 __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ part, int S,
                                                      const float* __restrict__ bias, float* __restrict__ x, int M,
@@ -84,47 +85,57 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias, bias ? (long long)N * 4 : 0);
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(ln_g, h ? (long long)N * 4 : 0);
     const __amdgpu_buffer_rsrc_t rbe = make_rsrc(ln_b, h ? (long long)N * 4 : 0);
-    float v[kRedCols], bv[kRedCols], gv[kRedCols], be[kRedCols];
-    float p[kRedCols][kRedSlices];
+    float4 v[kRedVec], bv[kRedVec], gv[kRedVec], be[kRedVec];
+    float4 p[kRedVec][kRedSlices];
+    auto ld = [](__amdgpu_buffer_rsrc_t r, int off) {
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    };
 #pragma unroll
-    for (int c = 0; c < kRedCols; c++) {
-        const int j = threadIdx.x + 256 * c;
+    for (int c = 0; c < kRedVec; c++) {
+        const int j = 4 * (threadIdx.x + 256 * c);
         const int off = j < N ? j * 4 : kOutOfRange;
-        v[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0));
-        bv[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0));
-        gv[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, off, 0, 0));
-        be[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rbe, off, 0, 0));
+        v[c] = ld(rx, off);
+        bv[c] = ld(rb, off);
+        gv[c] = ld(rg, off);
+        be[c] = ld(rbe, off);
 #pragma unroll
-        for (int q = 0; q < kRedSlices; q++) {
-            const int po = (j < N && q < S) ? (int)(((size_t)q * M * N + j) * 4) : kOutOfRange;
-            p[c][q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, po, 0, 0));
-        }
+        for (int q = 0; q < kRedSlices; q++)
+            p[c][q] = ld(rp, (j < N && q < S) ? (int)(((size_t)q * M * N + j) * 4) : kOutOfRange);
     }
     double s1 = 0.0;
 #pragma unroll
-    for (int c = 0; c < kRedCols; c++) {
-        const int j = threadIdx.x + 256 * c;
+    for (int c = 0; c < kRedVec; c++) {
+        const int j = 4 * (threadIdx.x + 256 * c);
         if (j >= N) continue;
+        float* vc = reinterpret_cast<float*>(&v[c]);
         if (S > 0) {
-            float acc = p[c][0];
 #pragma unroll
-            for (int q = 1; q < kRedSlices; q++)
-                if (q < S) acc += p[c][q];
-            if (bias) acc = acc + bv[c];
-            v[c] = v[c] + acc;
-            row[j] = v[c];
+            for (int e = 0; e < 4; e++) {
+                float acc = reinterpret_cast<const float*>(&p[c][0])[e];
+#pragma unroll
+                for (int q = 1; q < kRedSlices; q++)
+                    if (q < S) acc += reinterpret_cast<const float*>(&p[c][q])[e];
+                if (bias) acc = acc + reinterpret_cast<const float*>(&bv[c])[e];
+                vc[e] = vc[e] + acc;
+            }
+            *reinterpret_cast<float4*>(row + j) = v[c];
         }
-        s1 += (double)v[c];
+#pragma unroll
+        for (int e = 0; e < 4; e++) s1 += (double)vc[e];
     }
     if (!stats && !h) return;
     const double mean = block_sum_d(s1, sh) / (double)N;
     double s2 = 0.0;
 #pragma unroll
-    for (int c = 0; c < kRedCols; c++) {
-        const int j = threadIdx.x + 256 * c;
+    for (int c = 0; c < kRedVec; c++) {
+        const int j = 4 * (threadIdx.x + 256 * c);
         if (j >= N) continue;
-        const double d = (double)v[c] - mean;
-        s2 += d * d;
+        const float* vc = reinterpret_cast<const float*>(&v[c]);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const double d = (double)vc[e] - mean;
+            s2 += d * d;
+        }
     }
     const double var = block_sum_d(s2, sh) / (double)N;
     const float fm = (float)mean, inv = (float)(1.0 / sqrt(var + (double)eps));
@@ -132,19 +143,28 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
     if (!h) return;
     // the same f32 operations as a LayerNorm fused into a GEMV's operand load
 #pragma unroll
-    for (int c = 0; c < kRedCols; c++) {
-        const int j = threadIdx.x + 256 * c;
+    for (int c = 0; c < kRedVec; c++) {
+        const int j = 4 * (threadIdx.x + 256 * c);
         if (j >= N) continue;
-        const float normalized = (v[c] - fm) * inv;
-        h[(size_t)m * N + j] = normalized * gv[c] + be[c];
+        const float* vc = reinterpret_cast<const float*>(&v[c]);
+        const float* gc = reinterpret_cast<const float*>(&gv[c]);
+        const float* bc = reinterpret_cast<const float*>(&be[c]);
+        float4 o;
+        float* oc = reinterpret_cast<float*>(&o);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float normalized = (vc[e] - fm) * inv;
+            oc[e] = normalized * gc[e] + bc[e];
+        }
+        *reinterpret_cast<float4*>(h + (size_t)m * N + j) = o;
     }
 }
 
 int launch_reduce_rows(hipStream_t s, const float* part, int S, const float* bias, float* x, int M, int N,
                        float eps, float2* stats, const float* ln_g, const float* ln_b, float* h) {
     if (M == 0) return GORCH_HIP_OK;
-    if (N > 256 * kRedCols || S > kRedSlices) {
-        set_error("reduce_rows: at most 2048 columns and 8 slices");
+    if (N > 1024 * kRedVec || S > kRedSlices || N % 4) {
+        set_error("reduce_rows: at most 2048 columns (a multiple of 4) and 8 slices");
         return GORCH_HIP_EUNSUPPORTED;
     }
     if (h && (!ln_g || !ln_b)) {
