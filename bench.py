@@ -344,7 +344,10 @@ def main():
         shapes = [(M, K, N) for (K, N) in KN for M in MS]
 
     value, wall, per_shape, dom = gpu_leg(args, shapes)
-    decode = [] if (args.shape or args.no_decode) else [decode_leg("gpt2-small", 1, 32, 64)]
+    # the metric's two decode rates: GPT-2 small at batch 1 (configs[0]'s
+    # workload) and the GPT-2 XL shape at batch 16
+    decode = [] if (args.shape or args.no_decode) else [decode_leg("gpt2-small", 1, 32, 64),
+                                                         decode_leg("gpt2-xl", 16, 512, 256, reps=1)]
     gemm = [] if args.shape else gemm_leg()
     moe = None if args.shape else moe_leg()
     cpu = None if args.no_cpu else cpu_leg(shapes, args.cpu_seconds)
