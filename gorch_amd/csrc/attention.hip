@@ -85,8 +85,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_cached(AttnArgs a) {
                 acc += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
             }
         }
-        acc += __shfl_xor(acc, 2, 64);
-        acc += __shfl_xor(acc, 1, 64);
+        acc = seg_sum<4>(acc);
         if (j < T && sub == 0) {
             float s = acc * a.scale;
             sc[j] = s;
@@ -140,11 +139,17 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_cached(AttnArgs a) {
 // UNR keys at once. Scores, softmax and P.V then take about one memory round
 // trip each, instead of one per key-loop iteration (what limits the
 // per-(head, row) block when the context is short and blocks are few).
-template <int HD4, int UNR>
+//
+// FULL: KB * UNR >= max_seq, so one chunk covers the whole cache. The K and
+// V loads then span the cache's capacity rather than the visible length,
+// and are issued before the cache length (written by the previous kernel)
+// has arrived; keys at or past it are masked in the arithmetic (selects, so
+// whatever the unused rows hold never reaches the result).
+template <int HD4, int UNR, bool FULL>
 __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     extern __shared__ float sc[];  // [visible keys]
     __shared__ float red[16];
-    __shared__ float4 po[4][HD4];
+    __shared__ float4 po[4][64];
     constexpr int KPI = 64 / HD4;  // keys per wavefront instruction
     constexpr int KB = 4 * KPI;    // keys per block instruction
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -154,29 +159,59 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     const int row = blockIdx.y;
     const int b = row / a.new_seq;
     const int i = row - b * a.new_seq;
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
-    const int T = a.causal ? pos + i + 1 : pos + a.new_seq;
     const int kvh = a.kv_heads ? h / ((int)gridDim.x / a.kv_heads) : h;
     const int kvd = a.kv_dim ? a.kv_dim : a.dim;
     const size_t base = ((size_t)b * a.max_seq) * kvd + (size_t)kvh * (4 * HD4);
-    const float4* K4 = reinterpret_cast<const float4*>(a.kc + base);
-    const float4* V4 = reinterpret_cast<const float4*>(a.vc + base);
-    const int kvd4 = kvd >> 2;
+    // the cache length as a vector load issued after the K/V loads when FULL
+    // (a scalar load would share its wait counter with the kernel arguments
+    // and hold back the K/V stream)
+    auto load_pos = [&]() {
+        if (!a.pos_dev) return a.pos_host;
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.pos_dev, 4);
+        return __builtin_amdgcn_readfirstlane((int)__builtin_amdgcn_raw_buffer_load_b32(rp, 0, 0, 0));
+    };
+    int T = 0;
+    if constexpr (!FULL) {
+        const int pos = load_pos();
+        T = a.causal ? pos + i + 1 : pos + a.new_seq;
+    }
+    // raw buffer resources over this head's slices of keys 0..T-1: keys at
+    // or past T fall outside and read as zeros, with no branch around the
+    // loads (a load under a branch makes the compiler wait for every
+    // outstanding load before its first use)
+    const int rows_read = FULL ? a.max_seq : T;
+    const long long span = rows_read > 0 ? ((long long)(rows_read - 1) * kvd + 4 * HD4) * 4 : 0;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.kc + base, span);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.vc + base, span);
+    auto kv_off = [&](int j) { return j * kvd * 4 + 16 * c; };
+    auto ld4 = [](__amdgpu_buffer_rsrc_t rs, int off) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+        return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                           __uint_as_float(v[3]));
+    };
     const float4 q = *reinterpret_cast<const float4*>(a.q + (size_t)row * a.q_stride + h * (4 * HD4) + 4 * c);
+    // the first chunk's keys and values in one round trip: V does not
+    // depend on the scores
+    float4 kv[UNR], vpre[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; u++) kv[u] = ld4(rk, kv_off(KB * u + slot));
+#pragma unroll
+    for (int u = 0; u < UNR; u++) vpre[u] = ld4(rv, kv_off(KB * u + slot));
+    if constexpr (FULL) {
+        const int pos = load_pos();
+        T = a.causal ? pos + i + 1 : pos + a.new_seq;
+    }
 
     float lmax = -INFINITY;
     for (int j0 = 0; j0 < T; j0 += KB * UNR) {
-        float4 kv[UNR];
+        if (j0 > 0) {
 #pragma unroll
-        for (int u = 0; u < UNR; u++) {
-            const int j = j0 + KB * u + slot;
-            kv[u] = j < T ? K4[(size_t)j * kvd4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int u = 0; u < UNR; u++) kv[u] = ld4(rk, kv_off(j0 + KB * u + slot));
         }
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
             float d = q.x * kv[u].x + q.y * kv[u].y + q.z * kv[u].z + q.w * kv[u].w;
-#pragma unroll
-            for (int o = 1; o < HD4; o <<= 1) d += __shfl_xor(d, o, 64);
+            d = seg_sum<HD4>(d);
             const int j = j0 + KB * u + slot;
             if (c == 0 && j < T) {
                 const float sj = d * a.scale;
@@ -201,39 +236,34 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     for (int j0 = 0; j0 < T; j0 += KB * UNR) {
         float4 vv[UNR];
 #pragma unroll
-        for (int u = 0; u < UNR; u++) {
-            const int j = j0 + KB * u + slot;
-            vv[u] = j < T ? V4[(size_t)j * kvd4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int u = 0; u < UNR; u++) vv[u] = j0 == 0 ? vpre[u] : ld4(rv, kv_off(j0 + KB * u + slot));
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
             const int j = j0 + KB * u + slot;
-            const float p = j < T ? sc[j] : 0.f;
-            o.x += p * vv[u].x;
-            o.y += p * vv[u].y;
-            o.z += p * vv[u].z;
-            o.w += p * vv[u].w;
+            if (j < T) {
+                const float p = sc[j];
+                o.x += p * vv[u].x;
+                o.y += p * vv[u].y;
+                o.z += p * vv[u].z;
+                o.w += p * vv[u].w;
+            }
         }
     }
-    // the wave's key slots, then the 4 waves in order
-#pragma unroll
-    for (int off = HD4; off < 64; off <<= 1) {
-        o.x += __shfl_xor(o.x, off, 64);
-        o.y += __shfl_xor(o.y, off, 64);
-        o.z += __shfl_xor(o.z, off, 64);
-        o.w += __shfl_xor(o.w, off, 64);
-    }
-    if (lane < HD4) po[wave][c] = o;
+    // the 4 waves' key slots, in order (wave, slot)
+    po[wave][lane] = o;
     __syncthreads();
-    if (wave == 0 && lane < HD4) {
-        float4 t = po[0][c];
+    if (threadIdx.x < HD4) {
+        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int w = 1; w < 4; w++) {
-            t.x += po[w][c].x;
-            t.y += po[w][c].y;
-            t.z += po[w][c].z;
-            t.w += po[w][c].w;
-        }
+        for (int w = 0; w < 4; w++)
+#pragma unroll
+            for (int sl = 0; sl < KPI; sl++) {
+                const float4 pv = po[w][sl * HD4 + c];
+                t.x += pv.x;
+                t.y += pv.y;
+                t.z += pv.z;
+                t.w += pv.w;
+            }
         *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + h * (4 * HD4) + 4 * c) = t;
     }
 }
@@ -255,11 +285,19 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
     // through the per-dim kernel below
     if (rows_kernel && aligned && a.max_seq <= 256 && (a.hd == 64 || a.hd == 128 || a.hd == 32 || a.hd == 16)) {
         const dim3 grid(heads, rows);
+        // one chunk of KB * UNR keys (KB = 256 / HD4) covers the cache: FULL
+        const int ms = a.max_seq;
         switch (a.hd) {
-            case 128: hipLaunchKernelGGL((k_attn_rows<32, 8>), grid, dim3(256), lds, s, a); break;
-            case 64: hipLaunchKernelGGL((k_attn_rows<16, 8>), grid, dim3(256), lds, s, a); break;
-            case 32: hipLaunchKernelGGL((k_attn_rows<8, 8>), grid, dim3(256), lds, s, a); break;
-            default: hipLaunchKernelGGL((k_attn_rows<4, 8>), grid, dim3(256), lds, s, a); break;
+            case 128:
+                if (ms <= 128) hipLaunchKernelGGL((k_attn_rows<32, 16, true>), grid, dim3(256), lds, s, a);
+                else hipLaunchKernelGGL((k_attn_rows<32, 8, false>), grid, dim3(256), lds, s, a);
+                break;
+            case 64:
+                if (ms <= 128) hipLaunchKernelGGL((k_attn_rows<16, 8, true>), grid, dim3(256), lds, s, a);
+                else hipLaunchKernelGGL((k_attn_rows<16, 16, true>), grid, dim3(256), lds, s, a);
+                break;
+            case 32: hipLaunchKernelGGL((k_attn_rows<8, 8, true>), grid, dim3(256), lds, s, a); break;
+            default: hipLaunchKernelGGL((k_attn_rows<4, 4, true>), grid, dim3(256), lds, s, a); break;
         }
         count(CNT_ATTENTION);
         return check_launch("attn_rows");

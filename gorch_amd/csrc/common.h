@@ -4,6 +4,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 
 #include <cstdio>
@@ -272,21 +273,89 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 
 __device__ __forceinline__ float sigmoidf_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Wavefront (64-lane) reductions.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Wavefront (64-lane) reductions on the VALU's DPP lane network, with
+// v_readlane for the last step across the four 16-lane rows (a __shfl_xor
+// compiles to ds_bpermute, an LDS round trip per step, each waited for).
+// All 64 lanes must be active. Every lane returns the same value: within a
+// row, lane pairs (i, i^1), (i, i^2), half-row mirrors and row mirrors
+// exchange and add partial sums, which gives all 16 lanes the same
+// operands in the same order; the rows are then combined as
+// (row0 + row1) + (row2 + row3).
+constexpr int kDppQuadSwap1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141; // lane i <- lane 7-i within each 8 lanes
+constexpr int kDppRowMirror = 0x140;     // lane i <- lane 15-i within each 16 lanes
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL, 0xF, 0xF, false);
+    return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+// Sum over aligned segments of T lanes (T = 4, 8, 16, 32 or 64): every lane
+// of a segment returns the segment's sum.
+template <int T>
+__device__ __forceinline__ float seg_sum(float v) {
+    static_assert(T == 4 || T == 8 || T == 16 || T == 32 || T == 64, "segment of 4..64 lanes");
+    v += dpp_f<kDppQuadSwap1>(v);
+    v += dpp_f<kDppQuadSwap2>(v);
+    if constexpr (T >= 8) v += dpp_f<kDppRowHalfMirror>(v);
+    if constexpr (T >= 16) v += dpp_f<kDppRowMirror>(v);
+    if constexpr (T == 32) {
+        const float a = readlane_f(v, 0) + readlane_f(v, 16);
+        const float b = readlane_f(v, 32) + readlane_f(v, 48);
+        v = (threadIdx.x & 32) ? b : a;
+    } else if constexpr (T == 64) {
+        v = (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+    }
     return v;
 }
+__device__ __forceinline__ float wave_sum(float v) { return seg_sum<64>(v); }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp_f<kDppQuadSwap1>(v));
+    v = fmaxf(v, dpp_f<kDppQuadSwap2>(v));
+    v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppRowMirror>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 __device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp_d<kDppQuadSwap1>(v);
+    v += dpp_d<kDppQuadSwap2>(v);
+    v += dpp_d<kDppRowHalfMirror>(v);
+    v += dpp_d<kDppRowMirror>(v);
+    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
+// Maximum of a 64-bit key over the wavefront (all lanes active).
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+    auto step = [](unsigned long long x, unsigned long long y) { return y > x ? y : x; };
+    auto dpp_u64 = [](unsigned long long x, auto ctrl_tag) {
+        constexpr int C = decltype(ctrl_tag)::value;
+        const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)x, C, 0xF, 0xF, false);
+        const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(x >> 32), C, 0xF, 0xF, false);
+        return ((unsigned long long)hi << 32) | lo;
+    };
+    v = step(v, dpp_u64(v, std::integral_constant<int, kDppQuadSwap1>{}));
+    v = step(v, dpp_u64(v, std::integral_constant<int, kDppQuadSwap2>{}));
+    v = step(v, dpp_u64(v, std::integral_constant<int, kDppRowHalfMirror>{}));
+    v = step(v, dpp_u64(v, std::integral_constant<int, kDppRowMirror>{}));
+    auto rl = [&](int l) {
+        return ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v >> 32), l) << 32) |
+               (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, l);
+    };
+    return step(step(rl(0), rl(16)), step(rl(32), rl(48)));
 }
 
 }  // namespace gh

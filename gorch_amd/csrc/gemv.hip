@@ -307,9 +307,7 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const float* __restrict__ x, 
             }
         }
 #pragma unroll
-        for (int m = 0; m < MT; m++)
-#pragma unroll
-            for (int o = T / 2; o > 0; o >>= 1) acc[m] += __shfl_xor(acc[m], o, 64);
+        for (int m = 0; m < MT; m++) acc[m] = seg_sum<T>(acc[m]);
         if (sub == 0 && row_ok) {
 #pragma unroll
             for (int m = 0; m < MT; m++) {
@@ -368,9 +366,6 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
         gr.b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, rloc * 4, 0, 0));
         gr.r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, rloc * 4, 0, 0));
     };
-    Group ga, gb;
-    load(rg, ga);  // the weight stream starts before the activations are ready
-
     // the activation row (K = 8*T*C exactly), LayerNorm gamma/beta with it
     float xr[C][8], gg[LN ? C : 1][8], bb[LN ? C : 1][8];
 #pragma unroll
@@ -391,6 +386,12 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
             bb[c][4] = b1.x; bb[c][5] = b1.y; bb[c][6] = b1.z; bb[c][7] = b1.w;
         }
     }
+    // then two row groups of the weight stream: the activation loads above
+    // come from L2 and were issued first, so using them waits for them
+    // alone, not for the weights (a wave's loads complete in issue order)
+    Group ga, gb;
+    load(rg, ga);
+    load(rg + stride, gb);
     const int posv = od.pos_dev ? *od.pos_dev : 0;
     if (ex.argmax_key) {
         if (tid == 0) s_key = 0ull;
@@ -443,8 +444,7 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
                    xr[c][3] * bf16_hi(cw.y) + xr[c][4] * bf16_lo(cw.z) + xr[c][5] * bf16_hi(cw.z) +
                    xr[c][6] * bf16_lo(cw.w) + xr[c][7] * bf16_hi(cw.w);
         }
-#pragma unroll
-        for (int o = T / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        acc = seg_sum<T>(acc);
         const int row = g * RPI + rloc;
         if (sub == 0 && row < N) {
             float v = acc;
@@ -461,20 +461,14 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
     // two register sets: the next group's stream is in flight while this
     // one is reduced and written
     for (; rg < ngroups; rg += 2 * stride) {
-        load(rg + stride, gb);
         compute(rg, ga);
         load(rg + 2 * stride, ga);
         if (rg + stride < ngroups) compute(rg + stride, gb);
+        load(rg + 3 * stride, gb);
     }
     if (ex.argmax_key) {
-        // the wave's maximum by shuffles, then one LDS atomic per wave
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const unsigned long long other =
-                ((unsigned long long)(unsigned)__shfl_xor((int)(best >> 32), o, 64) << 32) |
-                (unsigned)__shfl_xor((int)(best & 0xffffffffull), o, 64);
-            best = other > best ? other : best;
-        }
+        // the wave's maximum, then one LDS atomic per wave
+        best = wave_max_u64(best);
         if (lane == 0) atomicMax(&s_key, best);
         __syncthreads();
         if (tid == 0) atomicMax(ex.argmax_key, s_key);
@@ -527,36 +521,72 @@ __device__ void mt_ln_stats(const float* x, long long xs, int M, int K, float ep
 // Stage x[0..M)[kb..ke) into LDS as bf16 hi/lo A fragments (LayerNorm
 // applied first when fused): entry ((k-step * 4 + g) * mr + r) holds
 // x[r][kb + 32*kstep + 8*g .. +8] for r < mr (M rounded up to 4, 8 or 16);
-// rows >= M and k >= ke are zero.
-template <int NW>
-__device__ void mt_stage_x(const float* x, long long xs, int M, int mr, int kb, int ke, int nst,
-                           const LinearExtras& ex, const float* s_mean, const float* s_inv, uint4* xh, uint4* xl) {
-    for (int i = threadIdx.x; i < nst * 16 * mr; i += NW * 64) {
-        const int rr = i % mr, gg = (i / mr) & 3, kst = i / (4 * mr);
-        const int k = kb + 32 * kst + 8 * gg;
-        float f[8];
-        if (rr < M && k < ke) {
-            const float* src = x + (size_t)rr * xs + k;
-            const float4 a0 = *reinterpret_cast<const float4*>(src);
-            const float4 a1 = *reinterpret_cast<const float4*>(src + 4);
-            f[0] = a0.x; f[1] = a0.y; f[2] = a0.z; f[3] = a0.w;
-            f[4] = a1.x; f[5] = a1.y; f[6] = a1.z; f[7] = a1.w;
-            if (ex.ln_g) {
-                const float mu = s_mean[rr], inv = s_inv[rr];
+// rows >= M and k >= ke are zero. Thread t owns entries t + NW*64*p. The
+// first PX of them are fetched into registers by mt_fetch_x before the
+// weight stream is issued (a wave's loads complete in issue order, so
+// activations loaded after the weights would wait for them); mt_stage_x
+// converts those and loads any further entries itself.
+struct MtX {
+    __amdgpu_buffer_rsrc_t rs;
+    long long xs;
+    int M, mr, kb, ke, n;  // n = number of entries
+};
+__device__ __forceinline__ int mt_x_off(const MtX& X, int i) {
+    const int rr = i % X.mr, gg = (i / X.mr) & 3, kst = i / (4 * X.mr);
+    const int k = X.kb + 32 * kst + 8 * gg;
+    return (i < X.n && rr < X.M && k < X.ke) ? (int)((rr * X.xs + k) * 4) : kOutOfRange;
+}
+template <int NW, int PX>
+__device__ __forceinline__ void mt_fetch_x(const MtX& X, u32x4 (&xv)[PX][2]) {
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float normalized = (f[e] - mu) * inv;
-                    f[e] = normalized * ex.ln_g[k + e] + ex.ln_b[k + e];
-                }
+    for (int p = 0; p < PX; p++) {
+        const int off = mt_x_off(X, threadIdx.x + NW * 64 * p);
+        xv[p][0] = __builtin_amdgcn_raw_buffer_load_b128(X.rs, off, 0, 0);
+        xv[p][1] = __builtin_amdgcn_raw_buffer_load_b128(X.rs, off + 16, 0, 0);
+    }
+}
+__device__ __forceinline__ void mt_put_x(const MtX& X, int i, float (&f)[8], const LinearExtras& ex,
+                                         const float* s_mean, const float* s_inv, uint4* xh, uint4* xl) {
+    const int rr = i % X.mr, gg = (i / X.mr) & 3, kst = i / (4 * X.mr);
+    const int k = X.kb + 32 * kst + 8 * gg;
+    if (ex.ln_g) {
+        if (rr < X.M && k < X.ke) {
+            const float mu = s_mean[rr], inv = s_inv[rr];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float normalized = (f[e] - mu) * inv;
+                f[e] = normalized * ex.ln_g[k + e] + ex.ln_b[k + e];
             }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; e++) f[e] = 0.f;
         }
-        bf16x8 hi, lo;
-        split_hi_lo(f, hi, lo);
-        xh[i] = __builtin_bit_cast(uint4, hi);
-        xl[i] = __builtin_bit_cast(uint4, lo);
+    }
+    bf16x8 hi, lo;
+    split_hi_lo(f, hi, lo);
+    xh[i] = __builtin_bit_cast(uint4, hi);
+    xl[i] = __builtin_bit_cast(uint4, lo);
+}
+template <int NW, int PX>
+__device__ void mt_stage_x(const MtX& X, const u32x4 (&xv)[PX][2], const LinearExtras& ex, const float* s_mean,
+                           const float* s_inv, uint4* xh, uint4* xl) {
+#pragma unroll
+    for (int p = 0; p < PX; p++) {
+        const int i = threadIdx.x + NW * 64 * p;
+        if (i >= X.n) break;
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) f[e] = __uint_as_float(xv[p][e >> 2][e & 3]);
+        mt_put_x(X, i, f, ex, s_mean, s_inv, xh, xl);
+    }
+    for (int i = threadIdx.x + NW * 64 * PX; i < X.n; i += NW * 64) {
+        const int off = mt_x_off(X, i);
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(X.rs, off, 0, 0);
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(X.rs, off + 16, 0, 0);
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            f[e] = __uint_as_float(a[e]);
+            f[4 + e] = __uint_as_float(b[e]);
+        }
+        mt_put_x(X, i, f, ex, s_mean, s_inv, xh, xl);
     }
 }
 
@@ -653,7 +683,21 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
         const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias + (size_t)t * 16, bias ? (long long)rows * 4 : 0);
         bv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, r * 4, 0, 0));
     };
-    load(0, va, ba);  // the weight stream starts before the staging
+    // activations first (from L2), then two weight batches: staging waits
+    // for the activation loads only
+    MtX X;
+    X.xs = xs;
+    X.M = M;
+    X.mr = mr;
+    X.kb = kb;
+    X.ke = ke;
+    X.n = nst * 16 * mr;
+    X.rs = make_rsrc(x, M > 0 ? ((long long)(M - 1) * xs + K) * 4 : 0);
+    constexpr int PX = NW >= 16 ? 2 : (NW == 8 ? 3 : 2);
+    u32x4 xv[PX][2];
+    mt_fetch_x<NW, PX>(X, xv);
+    load(0, va, ba);
+    load(1, vb, bb);
 
     if (ex.ln_g && ex.ln_stats) {
         if (threadIdx.x < 16 && (int)threadIdx.x < M) {
@@ -667,7 +711,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
         __syncthreads();
     }
     if (ex.argmax_key && threadIdx.x < 16) s_key[threadIdx.x] = 0ull;
-    mt_stage_x<NW>(x, xs, M, mr, kb, ke, nst, ex, s_mean, s_inv, xh, xl);
+    mt_stage_x<NW, PX>(X, xv, ex, s_mean, s_inv, xh, xl);
     __syncthreads();
 
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -692,10 +736,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
         }
     };
     for (int j = 0; j < total; j += 2) {
-        load(j + 1, vb, bb);
         compute(j, va, ba);
         load(j + 2, va, ba);
         if (j + 1 < total) compute(j + 1, vb, bb);
+        load(j + 3, vb, bb);
     }
     if (ex.argmax_key) {
         __syncthreads();
@@ -768,7 +812,7 @@ static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const flo
                      const OutDesc& od, int N, int K, int epilogue, const LinearExtras& ex, int T, int C) {
     const int rpi = 64 / T;
     const int ngroups = (N + rpi - 1) / rpi;
-    static const int max_blocks = env_int("GORCH_HIP_GEMV_M1_BLOCKS", 4096);
+    static const int max_blocks = env_int("GORCH_HIP_GEMV_M1_BLOCKS", 768);
     // with the argmax fusion every block ends in one 64-bit atomicMax on the
     // same global word, and those serialise at one L2 channel (4096 of them
     // cost ~40 us): fewer, longer-running blocks
@@ -834,7 +878,7 @@ static int launch_mt(hipStream_t s, const float* x, const uint16_t* W, const flo
     if (nw == NWV && st == STV && mr == MRV)                                                                 \
         rc = launch_mt_t<NWV, STV, MRV>(s, bps, lds, x, W, bias, residual, od, M, N, K, bps, epilogue, ex);
 #define GH_MT_R(NWV, STV) GH_MT(NWV, STV, 4) GH_MT(NWV, STV, 8) GH_MT(NWV, STV, 16)
-    GH_MT_R(8, 1) GH_MT_R(8, 2) GH_MT_R(16, 1) GH_MT_R(16, 2)
+    GH_MT_R(4, 2) GH_MT_R(4, 3) GH_MT_R(4, 6) GH_MT_R(8, 1) GH_MT_R(8, 2) GH_MT_R(8, 3) GH_MT_R(16, 1) GH_MT_R(16, 2)
 #undef GH_MT_R
 #undef GH_MT
     if (rc < 0) return -1;
@@ -905,6 +949,10 @@ static GemvPlan plan_gemv(int M, int N, int K) {
         p.nt = N >= 4096 ? 2 : 1;
         p.nw = 8;
         p.u = 2;
+    } else if (ntiles >= 128 && K <= 1024) {  // 2048..4095 rows over a short K
+        p.nt = 1;
+        p.nw = 4;
+        p.u = M <= 4 ? 4 : 2;
     } else {                       // narrow N: deep K split inside the block
         p.nt = 1;
         p.nw = 8;
