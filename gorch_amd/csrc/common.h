@@ -338,6 +338,20 @@ __device__ __forceinline__ double wave_sum_d(double v) {
     v += dpp_d<kDppRowMirror>(v);
     return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
 }
+// Two f64 sums over the wavefront at once (independent chains, one
+// latency); every lane returns both totals.
+__device__ __forceinline__ void wave_sum2_d(double& a, double& b) {
+    a += dpp_d<kDppQuadSwap1>(a);
+    b += dpp_d<kDppQuadSwap1>(b);
+    a += dpp_d<kDppQuadSwap2>(a);
+    b += dpp_d<kDppQuadSwap2>(b);
+    a += dpp_d<kDppRowHalfMirror>(a);
+    b += dpp_d<kDppRowHalfMirror>(b);
+    a += dpp_d<kDppRowMirror>(a);
+    b += dpp_d<kDppRowMirror>(b);
+    a = (readlane_d(a, 0) + readlane_d(a, 16)) + (readlane_d(a, 32) + readlane_d(a, 48));
+    b = (readlane_d(b, 0) + readlane_d(b, 16)) + (readlane_d(b, 32) + readlane_d(b, 48));
+}
 // Maximum of a 64-bit key over the wavefront (all lanes active).
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
     auto step = [](unsigned long long x, unsigned long long y) { return y > x ? y : x; };

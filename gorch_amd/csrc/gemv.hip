@@ -403,25 +403,29 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
             fm = ex.ln_stats[0].x;
             inv = ex.ln_stats[0].y;
         } else {
-            // the wave's lanes hold the row RPI times over (one copy per
-            // rloc): sum over the first T lanes only
-            double s1 = 0.0;
-            if (rloc == 0)
-#pragma unroll
-                for (int c = 0; c < C; c++)
-#pragma unroll
-                    for (int i = 0; i < 8; i++) s1 += (double)xr[c][i];
-            const double mean = wave_sum_d(s1) / (double)K;
-            double s2 = 0.0;
+            // The row's mean and variance in f64 (nn/layernorm.go:61-75) as
+            // shifted moments in one pass: with c = x[0], s1 = sum(x - c)
+            // and s2 = sum((x - c)^2), mean = c + s1/K and var = s2/K -
+            // (s1/K)^2 — the reference's two-pass values to f64 rounding
+            // (the shift keeps the subtraction well conditioned), with one
+            // joint wave reduction instead of two dependent ones. The
+            // wave's lanes hold the row RPI times over (one copy per rloc):
+            // sum over the first T lanes only.
+            const double cs = (double)readlane_f(xr[0][0], 0);
+            double s1 = 0.0, s2 = 0.0;
             if (rloc == 0)
 #pragma unroll
                 for (int c = 0; c < C; c++)
 #pragma unroll
                     for (int i = 0; i < 8; i++) {
-                        const double dd = (double)xr[c][i] - mean;
+                        const double dd = (double)xr[c][i] - cs;
+                        s1 += dd;
                         s2 += dd * dd;
                     }
-            const double var = wave_sum_d(s2) / (double)K;
+            wave_sum2_d(s1, s2);
+            const double ms = s1 / (double)K;
+            const double mean = cs + ms;
+            const double var = fmax(s2 / (double)K - ms * ms, 0.0);
             inv = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
             fm = (float)mean;
         }
@@ -817,7 +821,9 @@ static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const flo
     // same global word, and those serialise at one L2 channel (4096 of them
     // cost ~40 us): fewer, longer-running blocks
     static const int max_blocks_argmax = env_int("GORCH_HIP_GEMV_M1_ARGMAX_BLOCKS", 512);
-    int blocks = (ngroups + 3) / 4;
+    // one row group per wave; two with a fused LayerNorm, whose activation,
+    // gamma and beta rows every wave loads whole
+    int blocks = ex.ln_g ? (ngroups + 7) / 8 : (ngroups + 3) / 4;
     if (blocks > max_blocks) blocks = max_blocks;
     if (ex.argmax_key && blocks > max_blocks_argmax) blocks = max_blocks_argmax;
 #define GH_M1(TT, CC)                                                                                        \
