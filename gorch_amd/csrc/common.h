@@ -67,6 +67,13 @@ int launch_reduce_rows(hipStream_t s, const float* part, int S, const float* bia
                        float* h = nullptr);
 int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                        const float* residual, float* y, int M, int N, int K, int epilogue);
+// Tile-packed bf16 weights (gemv.hip): element count of the packed copy,
+// the pack kernel, and the M <= 16 Linear over it.
+size_t packed_bf16_elems(int N, int K);
+int launch_pack_bf16(hipStream_t s, const uint16_t* W, uint16_t* Wp, int N, int K);
+int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, const float* bias,
+                            const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
+                            const LinearExtras& ex);
 int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                           const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
                           const LinearExtras& ex);
@@ -351,6 +358,26 @@ __device__ __forceinline__ void wave_sum2_d(double& a, double& b) {
     b += dpp_d<kDppRowMirror>(b);
     a = (readlane_d(a, 0) + readlane_d(a, 16)) + (readlane_d(a, 32) + readlane_d(a, 48));
     b = (readlane_d(b, 0) + readlane_d(b, 16)) + (readlane_d(b, 32) + readlane_d(b, 48));
+}
+// Maximum of a 64-bit key over each row of 16 lanes (all lanes active);
+// every lane of the row returns it.
+__device__ __forceinline__ unsigned long long row16_max_u64(unsigned long long v) {
+    auto dpp_u64 = [](unsigned long long x, auto ctrl_tag) {
+        constexpr int C = decltype(ctrl_tag)::value;
+        const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)x, C, 0xF, 0xF, false);
+        const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(x >> 32), C, 0xF, 0xF, false);
+        return ((unsigned long long)hi << 32) | lo;
+    };
+    unsigned long long o;
+    o = dpp_u64(v, std::integral_constant<int, kDppQuadSwap1>{});
+    v = o > v ? o : v;
+    o = dpp_u64(v, std::integral_constant<int, kDppQuadSwap2>{});
+    v = o > v ? o : v;
+    o = dpp_u64(v, std::integral_constant<int, kDppRowHalfMirror>{});
+    v = o > v ? o : v;
+    o = dpp_u64(v, std::integral_constant<int, kDppRowMirror>{});
+    v = o > v ? o : v;
+    return v;
 }
 // Maximum of a 64-bit key over the wavefront (all lanes active).
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {

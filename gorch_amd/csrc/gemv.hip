@@ -751,6 +751,144 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Persistent multi-row GEMV for 2 <= M <= 16 over 128+ weight tiles.
+//
+// A block is NW waves; wave w owns k-steps [w*ks, (w+1)*ks) of every 16-row
+// weight tile. It loads the activation A fragments of that K range once, as
+// bf16 hi/lo in registers (x = hi + lo, two MFMAs per fragment), and keeps
+// them for the whole kernel; then the block walks the tiles t = blockIdx.x
+// + gridDim.x * i with two register sets of B fragments, so the next tile's
+// weights are in flight while this one feeds the matrix cores. Per tile the
+// NW partial 16x16 results go through LDS (two buffers by tile parity) and
+// wave 0 sums them in wave order and finishes the tile (bias, GELU,
+// residual, output, argmax keys). Every load is a raw buffer load with no
+// branch around it: k past the wave's range, rows past M or N and tiles
+// past the last read as zeros.
+template <int NW, int KS, bool PACKED>
+__global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict__ x, const uint16_t* __restrict__ W,
+                                                        const float* __restrict__ bias, const float* residual,
+                                                        OutDesc od, int M, int N, int K, int ks, int epilogue,
+                                                        LinearExtras ex) {
+    __shared__ floatx4 red[2][NW][64];
+    __shared__ unsigned long long s_key[16];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int kb = wave * ks * 32, ke = min(K, kb + ks * 32);
+    const long long xs = ex.x_stride ? ex.x_stride : K;
+    const int ntiles = (N + 15) >> 4;
+    const int G = gridDim.x;
+
+    // activations first (they come from L2): converting them waits for
+    // them alone, not for the weights issued after them
+    const __amdgpu_buffer_rsrc_t rsx = make_rsrc(x, ((long long)(M - 1) * xs + K) * 4);
+    u32x4 xa[KS][2];
+#pragma unroll
+    for (int u = 0; u < KS; u++) {
+        const int kc = kb + 32 * u + 8 * g;
+        const int off = (r < M && kc < ke) ? (int)((r * xs + kc) * 4) : kOutOfRange;
+        xa[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rsx, off, 0, 0);
+        xa[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rsx, off + 16, 0, 0);
+    }
+    const __amdgpu_buffer_rsrc_t rsr = make_rsrc(residual, residual ? (long long)M * N * 4 : 0);
+    // Tile epilogue split over the waves: wave w finishes outputs o = w *
+    // OPW + lane (lane < OPW, OPW = 256 / NW), o = 16 * m + c for row m and
+    // column c of the tile; the partial 16x16 results hold (m, c) in lane
+    // 16 * (m / 4) + c, component m % 4.
+    constexpr int OPW = 256 / NW;
+    const bool out_lane = lane < OPW;
+    const int o = wave * OPW + (out_lane ? lane : 0);
+    const int om = o >> 4, oc = o & 15;
+    struct Tile {
+        u32x4 w[KS];
+        float b, res;
+    };
+    // packed: tile t is 16 * K32 bf16 from W + t * 16 * K32 (K32 = K rounded
+    // up to 32), fragment (t, k-step j) the 1 KB at byte 1024 * j, lane l's
+    // 16 bytes at 16 * l; row-major: row n at W + n * K
+    const int K32 = (K + 31) & ~31;
+    auto load = [&](int t, Tile& tl) {
+        const int rows = max(0, min(16, N - 16 * t));
+        const __amdgpu_buffer_rsrc_t rs =
+            PACKED ? make_rsrc(W + (size_t)t * 16 * K32, t < ntiles ? (long long)16 * K32 * 2 : 0)
+                   : make_rsrc(W + (size_t)t * 16 * K, (long long)rows * K * 2);
+#pragma unroll
+        for (int u = 0; u < KS; u++) {
+            const int kc = kb + 32 * u + 8 * g;
+            const int off = PACKED ? (kb + 32 * u) * 32 + 16 * lane : (r * K + kc) * 2;
+            tl.w[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, kc < ke ? off : kOutOfRange, 0, 0);
+        }
+        // this lane's output column's bias and residual
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias + (size_t)t * 16, bias ? (long long)rows * 4 : 0);
+        tl.b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, oc * 4, 0, 0));
+        const int on = 16 * t + oc;
+        const int roff = (om < M && on < N) ? (om * N + on) * 4 : kOutOfRange;
+        tl.res = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsr, roff, 0, 0));
+    };
+    Tile ta, tb;
+    int t = blockIdx.x;
+    load(t, ta);
+    load(t + G, tb);
+
+    bf16x8 ah[KS], al[KS];
+#pragma unroll
+    for (int u = 0; u < KS; u++) {
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) f[e] = __uint_as_float(xa[u][e >> 2][e & 3]);
+        split_hi_lo(f, ah[u], al[u]);
+    }
+    const int posv = od.pos_dev ? *od.pos_dev : 0;
+    if (ex.argmax_key) {
+        if (threadIdx.x < 16) s_key[threadIdx.x] = 0ull;
+        __syncthreads();
+    }
+    unsigned long long best = 0ull;
+    const float* redf = reinterpret_cast<const float*>(&red[0][0][0]);
+
+    auto step = [&](int tt, const Tile& tl, int buf) {
+        // hi and lo products in two accumulators: two independent MFMA chains
+        floatx4 acc_h = {0.f, 0.f, 0.f, 0.f}, acc_l = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < KS; u++) {
+            const bf16x8 b = __builtin_bit_cast(bf16x8, tl.w[u]);
+            acc_h = mfma16x16x32(ah[u], b, acc_h);
+            acc_l = mfma16x16x32(al[u], b, acc_l);
+        }
+        red[buf][wave][lane] = acc_h + acc_l;
+        __syncthreads();
+        const int on = 16 * tt + oc;
+        if (out_lane && om < M && on < N) {
+            const int src = 16 * (om >> 2) + oc, comp = om & 3;
+            float val = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) val += redf[((buf * NW + w) * 64 + src) * 4 + comp];
+            if (bias) val = val + tl.b;
+            if (epilogue == GORCH_HIP_EPI_GELU) val = gelu_tanh(val);
+            if (residual) val = tl.res + val;
+            *od.at_p(om, on, posv) = val;
+            if (ex.argmax_key) {
+                const unsigned long long key = argmax_pack(val, on);
+                best = key > best ? key : best;
+            }
+        }
+    };
+    for (; t < ntiles; t += 2 * G) {
+        step(t, ta, 0);
+        load(t + 2 * G, ta);
+        if (t + G < ntiles) step(t + G, tb, 1);
+        load(t + 3 * G, tb);
+    }
+    if (ex.argmax_key) {
+        // row om's maximum over the 16 columns (the 16 lanes of one DPP row
+        // share om), then one LDS atomic per row and block
+        best = row16_max_u64(best);
+        if (out_lane && oc == 0 && om < M) atomicMax(&s_key[om], best);
+        __syncthreads();
+        if (threadIdx.x < 16 && (int)threadIdx.x < M) atomicMax(&ex.argmax_key[threadIdx.x], s_key[threadIdx.x]);
+    }
+}
+
 // Epilogue of a K-split Linear: y[m, n] = epi(sum_s part[s][m][n] + bias[n])
 // (+ residual), slices added in order, written through the output
 // descriptor. All slice loads of an element are issued before the adds.
@@ -893,6 +1031,45 @@ static int launch_mt(hipStream_t s, const float* x, const uint16_t* W, const flo
     return check_launch("gemv_mt");
 }
 
+// Persistent multi-row GEMV launch; -1 when K exceeds 8 x 12 k-steps.
+// GORCH_HIP_TILES_{NW,BLOCKS} override the plan.
+static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const float* bias, const float* residual,
+                        const OutDesc& od, int M, int N, int K, int epilogue, const LinearExtras& ex, bool packed) {
+    static const int nw_env = env_int("GORCH_HIP_TILES_NW", 0);
+    static const int blocks_env = env_int("GORCH_HIP_TILES_BLOCKS", 0);
+    const int ntiles = (N + 15) / 16;
+    const int ksteps = (K + 31) / 32;
+    const int nw = nw_env ? nw_env : 8;
+    const int ks = (ksteps + nw - 1) / nw;
+    // one round of resident blocks: a block beyond what the CUs hold at once
+    // would run as a second, mostly idle round (measured 10 vs 7 us)
+    auto blocks_for = [&](const void* kern, int threads) {
+        int per_cu = 0, cus = 0, dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0) != hipSuccess || per_cu < 1)
+            per_cu = 1, cus = cus > 0 ? cus : 256;
+        return blocks_env ? blocks_env : per_cu * cus;
+    };
+#define GH_TILES(NWV, KSV)                                                                                \
+    if (nw == NWV && ks <= KSV) {                                                                         \
+        static const int blocks_p = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, true>), NWV * 64); \
+        static const int blocks_r = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, false>), NWV * 64); \
+        const int blocks = std::min(packed ? blocks_p : blocks_r, ntiles);                                \
+        if (packed)                                                                                       \
+            hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, true>), dim3(blocks), dim3(NWV * 64), 0, s, x, W, bias, \
+                               residual, od, M, N, K, ks, epilogue, ex);                                  \
+        else                                                                                              \
+            hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, false>), dim3(blocks), dim3(NWV * 64), 0, s, x, W, bias, \
+                               residual, od, M, N, K, ks, epilogue, ex);                                  \
+        count(CNT_GEMV);                                                                                  \
+        return check_launch("gemv_tiles");                                                                \
+    }
+    GH_TILES(4, 4) GH_TILES(4, 8) GH_TILES(8, 4) GH_TILES(8, 8) GH_TILES(8, 12) GH_TILES(16, 4)
+#undef GH_TILES
+    return -1;
+}
+
 template <int MT>
 static int launch_valu_mt(hipStream_t s, const float* x, const uint16_t* W, const float* bias, const float* residual,
                           const OutDesc& od, int M, int N, int K, int epilogue, const LinearExtras& ex, int T) {
@@ -1031,7 +1208,7 @@ static int launch_mfma_gemv(hipStream_t s, const float* x, const uint16_t* W, co
 #define GH_CASES_U(T, WV) GH_CASE(T, WV, 2) GH_CASE(T, WV, 4) GH_CASE(T, WV, 8)
 #define GH_CASES_W(T) \
     GH_CASES_U(T, 1) GH_CASES_U(T, 2) GH_CASES_U(T, 4) GH_CASE(T, 8, 2) GH_CASE(T, 8, 4) GH_CASE(T, 16, 2)
-    GH_CASES_W(1) GH_CASES_W(2) GH_CASES_W(4)
+    GH_CASES_W(1) GH_CASES_W(2) GH_CASES_W(4) GH_CASE(8, 1, 2) GH_CASE(8, 2, 2) GH_CASE(8, 4, 2)
 #undef GH_CASES_W
 #undef GH_CASES_U
 #undef GH_CASE
@@ -1067,9 +1244,11 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
     // K 1600, N 4800) once the epilogue kernel is counted.
     static const int auto_split = env_int("GORCH_HIP_GEMV_SPLIT", 1);
     static const int split_blocks = env_int("GORCH_HIP_GEMV_SPLIT_BLOCKS", 300);
+    static const int split_max_tiles = env_int("GORCH_HIP_GEMV_SPLIT_MAX_TILES", 128);
+    static const int split_nt_wide = env_int("GORCH_HIP_GEMV_SPLIT_NT_WIDE", 2);
     const int ntiles_all = (N + 15) / 16;
-    if (auto_split && M >= 2 && !ex.argmax_key && ntiles_all < 128 && K >= 1024) {
-        const int nt = 2;
+    if (auto_split && M >= 2 && !ex.argmax_key && ntiles_all < split_max_tiles && K >= 1024) {
+        const int nt = ntiles_all >= 128 ? split_nt_wide : 2;
         const int blocks_per_slice = (ntiles_all + nt - 1) / nt;
         const int S = ksplit_slices(K, std::min(kEpiSlices, std::max(2, split_blocks / blocks_per_slice)));
         void* part = S >= 2 ? stream_scratch(s, (size_t)S * M * N * sizeof(float)) : nullptr;
@@ -1095,6 +1274,11 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
             if (rc >= 0) return rc;
         }
     }
+    static const int tiles_on = env_int("GORCH_HIP_GEMV_TILES", 0);
+    if (tiles_on && M >= 2 && !ex.ln_g && (N + 15) / 16 >= 128) {
+        int rc = launch_tiles(s, x, W, bias, residual, od, M, N, K, epilogue, ex, false);
+        if (rc >= 0) return rc;
+    }
     static const int mt_on = env_int("GORCH_HIP_MT", 1);
     if (M >= 2 && mt_on && (N + 15) / 16 >= 1024) {
         int rc = launch_mt(s, x, W, bias, residual, od, M, N, K, epilogue, ex);
@@ -1107,6 +1291,53 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
         return launch_valu_mt<4>(s, x, W, bias, residual, od, M, N, K, epilogue, ex, T);
     }
     return launch_mfma_gemv(s, x, W, bias, residual, od, M, N, K, epilogue, ex);
+}
+
+// Tile-packed weights: W [N, K] bf16 row-major -> ceil(N/16) tiles of
+// ceil(K/32) 1 KB fragments, each in v_mfma_f32_16x16x32_bf16 B-operand
+// lane order (lane l: row l % 16, k 8*(l/16) .. +8 of the 32-wide step),
+// zero beyond N and K. A wave then reads every fragment as one contiguous
+// 1 KB; row-major B fragments touch 16 rows K*2 bytes apart per load, which
+// on MI355X streams at ~60-70% of the rate (measured 7.6 vs 5.3 us for a
+// 15.4 MB weight at K = 1600).
+size_t packed_bf16_elems(int N, int K) { return (size_t)((N + 15) / 16) * 16 * (size_t)((K + 31) & ~31); }
+
+__global__ __launch_bounds__(256) void k_pack_bf16_tiles(const uint16_t* __restrict__ W, uint16_t* __restrict__ Wp,
+                                                         int N, int K, long long chunks) {
+    const long long c = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= chunks) return;
+    const int nks = (K + 31) / 32;
+    const int l = (int)(c & 63);
+    const long long f = c >> 6;  // fragment index = tile * nks + k-step
+    const int t = (int)(f / nks), j = (int)(f - (long long)t * nks);
+    const int row = 16 * t + (l & 15), k0 = 32 * j + 8 * (l >> 4);
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row < N && k0 < K) v = *reinterpret_cast<const uint4*>(W + (size_t)row * K + k0);
+    *reinterpret_cast<uint4*>(Wp + (size_t)c * 8) = v;
+}
+
+int launch_pack_bf16(hipStream_t s, const uint16_t* W, uint16_t* Wp, int N, int K) {
+    const long long chunks = (long long)packed_bf16_elems(N, K) / 8;
+    if (chunks == 0) return GORCH_HIP_OK;
+    hipLaunchKernelGGL(k_pack_bf16_tiles, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s, W, Wp, N, K,
+                       chunks);
+    return check_launch("pack_bf16");
+}
+
+// Linear over tile-packed weights, 1 <= M <= 16 (the decode GEMV).
+int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, const float* bias,
+                            const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
+                            const LinearExtras& ex) {
+    if (M < 1 || M > 16 || ex.part || ex.ln_g) {
+        set_error("linear_bf16_packed: needs 1 <= M <= 16, no K split, no fused LayerNorm");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
+    const int rc = launch_tiles(s, x, Wp, bias, residual, od, M, N, K, epilogue, ex, true);
+    if (rc < 0) {
+        set_error("linear_bf16_packed: K above 3072 is not supported");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
+    return rc;
 }
 
 }  // namespace gh

@@ -41,6 +41,9 @@ __global__ void k_pos_add(int* pos_dev, int n) { *pos_dev += n; }
 struct LayerW {
     uint16_t *wqkv, *wo, *w1, *w2;
     float *bqkv, *bo, *b1, *b2, *ln1_g, *ln1_b, *ln2_g, *ln2_b;
+    // tile-packed copies of the wide weights for the 2..16-row decode GEMV
+    // (null when not packed)
+    uint16_t *wqkv_p = nullptr, *w1_p = nullptr;
 };
 
 }  // namespace gh
@@ -50,8 +53,10 @@ using namespace gh;
 struct gorch_hip_gpt {
     int vocab = 0, dim = 0, heads = 0, layers = 0, max_seq = 0;
     char* blob = nullptr;
+    char* pblob = nullptr;  // tile-packed weights
     float *wte = nullptr, *wpe = nullptr, *lnf_g = nullptr, *lnf_b = nullptr, *blm = nullptr;
     uint16_t* wlm = nullptr;
+    uint16_t* wlm_p = nullptr;
     std::vector<LayerW> L;
     // activations, grown on demand
     size_t rows_cap = 0, logit_rows_cap = 0;
@@ -188,7 +193,10 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             od.use_pos[sgi] = 1;
         }
         LinearExtras ln1, ln2;
-        if (batched) {
+        if (batched && w.wqkv_p) {
+            GH_TRY(launch_linear_packed_od(s, g->h, w.wqkv_p, w.bqkv, nullptr, od, rows, 3 * d, d,
+                                           GORCH_HIP_EPI_NONE, LinearExtras{}));
+        } else if (batched) {
             GH_TRY(launch_linear_bf16_od(s, g->h, w.wqkv, w.bqkv, nullptr, od, rows, 3 * d, d, GORCH_HIP_EPI_NONE,
                                          LinearExtras{}));
         } else if (fused) {
@@ -218,7 +226,10 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         } else {
             GH_TRY(launch_linear_bf16(s, g->att, w.wo, w.bo, g->x, g->x, rows, d, d, GORCH_HIP_EPI_NONE));
         }
-        if (batched) {
+        if (batched && w.w1_p) {
+            GH_TRY(launch_linear_packed_od(s, g->h, w.w1_p, w.b1, nullptr, OutDesc::plain(g->ff, 4 * d), rows, 4 * d,
+                                           d, GORCH_HIP_EPI_GELU, LinearExtras{}));
+        } else if (batched) {
             GH_TRY(launch_linear_bf16(s, g->h, w.w1, w.b1, nullptr, g->ff, rows, 4 * d, d, GORCH_HIP_EPI_GELU));
         } else if (fused) {
             GH_TRY(launch_linear_bf16_od(s, g->x, w.w1, w.b1, nullptr, OutDesc::plain(g->ff, 4 * d), rows, 4 * d,
@@ -251,8 +262,12 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         lf.x_stride = head_stride;
         lf.argmax_key = all_rows ? nullptr : argmax_key;
         const float* head_h = g->h + (head_in - g->x);
-        GH_TRY(launch_linear_bf16_od(s, head_h, g->wlm, g->blm, nullptr, OutDesc::plain(g->logits, g->vocab),
-                                     head_rows, g->vocab, d, GORCH_HIP_EPI_NONE, lf));
+        if (g->wlm_p)
+            GH_TRY(launch_linear_packed_od(s, head_h, g->wlm_p, g->blm, nullptr, OutDesc::plain(g->logits, g->vocab),
+                                           head_rows, g->vocab, d, GORCH_HIP_EPI_NONE, lf));
+        else
+            GH_TRY(launch_linear_bf16_od(s, head_h, g->wlm, g->blm, nullptr, OutDesc::plain(g->logits, g->vocab),
+                                         head_rows, g->vocab, d, GORCH_HIP_EPI_NONE, lf));
     } else if (head_rows <= 16) {
         LinearExtras lf;
         lf.ln_g = g->lnf_g;
@@ -439,6 +454,36 @@ gorch_hip_gpt* gorch_hip_gpt_create(const gorch_hip_gpt_weights* w) {
         gorch_hip_gpt_free(g);
         return nullptr;
     }
+    // The wide weights (fused QKV, FFN1, LM head; K = dim) also get a
+    // tile-packed copy, the layout the 2..16-row decode GEMV streams with
+    // contiguous 1 KB fragment loads; the row-major originals serve the
+    // single-row decode (LayerNorm fused) and prefill.
+    static const int packed_on = [] {
+        const char* e = getenv("GORCH_HIP_PACKED");
+        return e ? atoi(e) : 1;
+    }();
+    if (packed_on && w->dim <= 3072) {
+        const int D = w->dim;
+        const size_t pq = align256(packed_bf16_elems(3 * D, D) * 2), p1 = align256(packed_bf16_elems(4 * D, D) * 2);
+        const size_t plm = align256(packed_bf16_elems(w->vocab, D) * 2);
+        if (check(hipMalloc(&g->pblob, plm + (size_t)w->layers * (pq + p1)), "hipMalloc packed weights")) {
+            gorch_hip_gpt_free(g);
+            return nullptr;
+        }
+        g->wlm_p = reinterpret_cast<uint16_t*>(g->pblob);
+        int rc = launch_pack_bf16(g->stream, g->wlm, g->wlm_p, w->vocab, D);
+        for (int l = 0; l < w->layers && rc == 0; l++) {
+            LayerW& L = g->L[l];
+            L.wqkv_p = reinterpret_cast<uint16_t*>(g->pblob + plm + (size_t)l * (pq + p1));
+            L.w1_p = reinterpret_cast<uint16_t*>(g->pblob + plm + (size_t)l * (pq + p1) + pq);
+            rc = launch_pack_bf16(g->stream, L.wqkv, L.wqkv_p, 3 * D, D);
+            if (rc == 0) rc = launch_pack_bf16(g->stream, L.w1, L.w1_p, 4 * D, D);
+        }
+        if (rc != 0 || check(hipStreamSynchronize(g->stream), "pack weights")) {
+            gorch_hip_gpt_free(g);
+            return nullptr;
+        }
+    }
     return g;
 }
 
@@ -452,6 +497,7 @@ void gorch_hip_gpt_free(gorch_hip_gpt* g) {
     if (g->gen_graph) (void)hipGraphDestroy(g->gen_graph);
     gorch_hip_kvcache_free(g->gen_cache);
     (void)hipFree(g->blob);
+    (void)hipFree(g->pblob);
     (void)hipFree(g->x);
     (void)hipFree(g->h);
     (void)hipFree(g->q);

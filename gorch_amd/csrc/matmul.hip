@@ -89,6 +89,35 @@ extern "C" int gorch_hip_linear_bf16(void* stream, const float* x, const uint16_
     return gorch_hip_linear_bf16_ex(stream, x, W, bias, residual, y, M, N, K, epilogue, 0);
 }
 
+extern "C" size_t gorch_hip_packed_bf16_bytes(int N, int K) {
+    if (N <= 0 || K <= 0) return 0;
+    return packed_bf16_elems(N, K) * sizeof(uint16_t);
+}
+
+extern "C" int gorch_hip_pack_bf16(void* stream, const uint16_t* W, uint16_t* Wp, int N, int K) {
+    GH_REQUIRE(N >= 0 && K >= 0, "gorch_hip_pack_bf16: negative dimension");
+    if (N == 0 || K == 0) return GORCH_HIP_OK;
+    GH_REQUIRE(W && Wp, "gorch_hip_pack_bf16: null pointer");
+    GH_REQUIRE(K % 8 == 0 && ((uintptr_t)W | (uintptr_t)Wp) % 16 == 0,
+               "gorch_hip_pack_bf16: needs K % 8 == 0 and 16-byte aligned buffers");
+    return launch_pack_bf16(stream_of(stream), W, Wp, N, K);
+}
+
+extern "C" int gorch_hip_linear_bf16_packed(void* stream, const float* x, const uint16_t* Wp, const float* bias,
+                                            const float* residual, float* y, int M, int N, int K, int epilogue) {
+    GH_REQUIRE(M >= 0 && N >= 0 && K >= 0, "gorch_hip_linear_bf16_packed: negative dimension");
+    GH_REQUIRE(epilogue == GORCH_HIP_EPI_NONE || epilogue == GORCH_HIP_EPI_GELU,
+               "gorch_hip_linear_bf16_packed: unknown epilogue");
+    if (M == 0 || N == 0) return GORCH_HIP_OK;
+    GH_REQUIRE(M <= 16, "gorch_hip_linear_bf16_packed: M must be <= 16 (decode GEMV)");
+    GH_REQUIRE(x && Wp && y, "gorch_hip_linear_bf16_packed: null pointer");
+    GH_REQUIRE((const void*)x != (const void*)y, "gorch_hip_linear_bf16_packed: x must not alias y");
+    GH_REQUIRE(K % 8 == 0 && ((uintptr_t)x | (uintptr_t)Wp) % 16 == 0,
+               "gorch_hip_linear_bf16_packed: needs K % 8 == 0 and 16-byte aligned x and Wp");
+    return launch_linear_packed_od(stream_of(stream), x, Wp, bias, residual, OutDesc::plain(y, N), M, N, K,
+                                   epilogue, LinearExtras{});
+}
+
 static int matmul_dt_impl(void* stream, const void* A, const void* B, float* C, uint32_t M, uint32_t N,
                           uint32_t K, uint32_t batch, int transA, int transB, int aBF16, int bBF16) {
     if (transA && transB) {

@@ -53,6 +53,9 @@ SIGNATURES = {
     "gorch_hip_batched_matmul_dt": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, i32, i32, i32, i32]),
     "gorch_hip_linear_bf16": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
     "gorch_hip_linear_bf16_ex": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]),
+    "gorch_hip_packed_bf16_bytes": (C.c_size_t, [i32, i32]),
+    "gorch_hip_pack_bf16": (i32, [vp, vp, vp, i32, i32]),
+    "gorch_hip_linear_bf16_packed": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
     "gorch_hip_layernorm": (i32, [vp, vp, vp, vp, vp, i32, i32, f32]),
     "gorch_hip_rmsnorm": (i32, [vp, vp, vp, vp, i32, i32, f32]),
     "gorch_hip_add": (i32, [vp, vp, vp, vp, i64]),
@@ -237,6 +240,25 @@ def linear_bf16(x, W, bias, y, residual=None, epilogue=EPI_NONE, act_bf16=False)
     N = W.shape[0]
     _ok(lib().gorch_hip_linear_bf16_ex(_stream(), _p(x), _p(W), _p(bias), _p(residual), _p(y), M, N, K,
                                        epilogue, LINEAR_ACT_BF16 if act_bf16 else 0))
+
+
+def pack_bf16(W):
+    """Tile-packed device copy of a row-major bf16 weight W [N,K] (int16
+    storage): a flat int16 tensor in the decode GEMV's resident format."""
+    import torch
+
+    N, K = W.shape
+    n = lib().gorch_hip_packed_bf16_bytes(N, K) // 2
+    Wp = torch.empty(n, dtype=torch.int16, device=W.device)
+    _ok(lib().gorch_hip_pack_bf16(_stream(), _p(W), _p(Wp), N, K))
+    return Wp
+
+
+def linear_bf16_packed(x, Wp, N, bias, y, residual=None, epilogue=EPI_NONE) -> None:
+    """linear_bf16 over a pack_bf16 weight of N rows; M = x.shape[0] <= 16."""
+    M, K = x.shape
+    _ok(lib().gorch_hip_linear_bf16_packed(_stream(), _p(x), _p(Wp), _p(bias), _p(residual), _p(y), M, N, K,
+                                           epilogue))
 
 
 # ------------------------------------------------------------------ GPT engine

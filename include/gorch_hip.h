@@ -110,6 +110,21 @@ int gorch_hip_linear_bf16(void* stream, const float* x, const uint16_t* W, const
 int gorch_hip_linear_bf16_ex(void* stream, const float* x, const uint16_t* W, const float* bias,
                              const float* residual, float* y, int M, int N, int K, int epilogue, int flags);
 
+/* Device-resident weight format for decode (replaces the row-major bf16
+ * buffer gorch's Tensor.ToMetal uploads, tensor.go:388-406, for a weight
+ * that only feeds Linear.Forward): ceil(N/16) tiles of ceil(K/32) 1 KB
+ * fragments in matrix-core operand order, zero-padded; the values are the
+ * weight's bf16 bits unchanged. gorch_hip_packed_bf16_bytes gives the size,
+ * gorch_hip_pack_bf16 converts a row-major [N,K] device weight (K % 8 == 0,
+ * 16-byte aligned buffers). */
+size_t gorch_hip_packed_bf16_bytes(int N, int K);
+int gorch_hip_pack_bf16(void* stream, const uint16_t* W, uint16_t* Wp, int N, int K);
+/* gorch_hip_linear_bf16 (nn/module.go:61-88) over a packed weight, for
+ * decode-sized M (1..16) and K <= 3072: same arguments, semantics and
+ * accuracy. */
+int gorch_hip_linear_bf16_packed(void* stream, const float* x, const uint16_t* Wp, const float* bias,
+                                 const float* residual, float* y, int M, int N, int K, int epilogue);
+
 /* ------------------------------------------------------------------------
  * Decode-step ops (the forward halves of gorch's op layer on this path).
  * ---------------------------------------------------------------------- */
