@@ -87,14 +87,25 @@ def gpu_leg(args, shapes):
         wbytes = 2 * K * N
         copies = max(2, -(-ROTATE_BYTES // wbytes))
         Wd = torch.from_numpy(W.view(np.int16)).cuda()
-        Ws = [Wd] + [Wd.clone() for _ in range(copies - 1)]
-        bufs.append(dict(M=M, K=K, N=N, x=torch.from_numpy(x).cuda(), W=Ws,
+        layout = resident_layout(M, K, N)
+        if layout == "packed":
+            # the resident decode format, converted once outside the timing
+            Wp = hip.pack_bf16(Wd)
+            del Wd
+            Ws = [Wp] + [Wp.clone() for _ in range(copies - 1)]
+        else:
+            Ws = [Wd] + [Wd.clone() for _ in range(copies - 1)]
+        bufs.append(dict(M=M, K=K, N=N, x=torch.from_numpy(x).cuda(), W=Ws, layout=layout,
                          b=torch.from_numpy(b).cuda(),
                          y=torch.empty((M, N), dtype=torch.float32, device="cuda")))
     torch.cuda.synchronize()
 
     def launch(buf, i):
-        hip.linear_bf16(buf["x"], buf["W"][i % len(buf["W"])], buf["b"], buf["y"])
+        Wi = buf["W"][i % len(buf["W"])]
+        if buf["layout"] == "packed":
+            hip.linear_bf16_packed(buf["x"], Wi, buf["N"], buf["b"], buf["y"])
+        else:
+            hip.linear_bf16(buf["x"], Wi, buf["b"], buf["y"])
 
     # eager warm-up reserves any split-K workspace before graph capture
     for buf in bufs:
@@ -120,7 +131,7 @@ def gpu_leg(args, shapes):
         e1.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / (reps * L)
         nbytes = algo_bytes(buf["M"], buf["K"], buf["N"])
-        per_shape.append(dict(M=buf["M"], K=buf["K"], N=buf["N"], us=round(us, 3),
+        per_shape.append(dict(M=buf["M"], K=buf["K"], N=buf["N"], layout=buf["layout"], us=round(us, 3),
                               GBs=round(nbytes / us / 1e3, 1), copies=len(buf["W"]),
                               frac=round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)))
         del g
@@ -154,9 +165,22 @@ def gpu_leg(args, shapes):
 MFMA_PEAK_TFLOPS = 2516.6  # dense bf16: 256 CU x 2.4 GHz x 4096 FLOP/clk
 
 
+def resident_layout(M, K, N):
+    """Weight layout the decode path keeps resident for a GEMV of this
+    shape, as the GPT engine does (gorch_amd/csrc/gpt.hip): the tile-packed
+    format for 2..16 rows over wide weights (>= 128 16-row tiles) with
+    K <= 3072; row-major for one row (the register GEMV) and for narrow
+    weights (K split across blocks)."""
+    if 2 <= M <= 16 and (N + 15) // 16 >= 128 and K <= 3072:
+        return "packed"
+    return "row-major"
+
+
 def gemv_kernel(M, K, N):
     """Which kernel libgorch_hip.so runs for a GEMV of this shape (the
     routing of launch_linear_bf16_od in gorch_amd/csrc/gemv.hip)."""
+    if resident_layout(M, K, N) == "packed":
+        return "k_gemv_tiles"
     if M == 1:
         chunks = K // 8
         if any(chunks % t == 0 and chunks // t <= 8 for t in (64, 32, 16, 8)):
@@ -371,6 +395,9 @@ def main():
                         "W bf16 N(0,0.02) [N,K], f32 out; one step = one launch per shape",
             "shapes": [f"M={s[0]},K={s[1]},N={s[2]}" for s in shapes],
             "weights_rotated_over_bytes": ROTATE_BYTES,
+            "weight_layout": "each shape on the decode path's resident format (per_shape.layout): "
+                             "tile-packed 1 KB matrix-core fragments for 2..16 rows over weights of >= 128 "
+                             "16-row tiles with K <= 3072, packed once before timing; row-major otherwise",
         },
         "roofline": {
             "bound": "hbm",
