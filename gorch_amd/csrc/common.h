@@ -9,6 +9,7 @@
 
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "../../include/gorch_hip.h"
 
@@ -201,6 +202,18 @@ struct AttnArgs {
     int recip;     // normalise by multiplying with 1/sum (GQA) instead of dividing
 };
 int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows);
+
+// A tensor entry of a safetensors header (safetensors.hip): dtype
+// GORCH_HIP_ST_*, shape, byte range relative to the data section.
+struct StTensor {
+    std::string name;
+    int dtype = -1;
+    std::vector<long long> shape;
+    long long begin = 0, end = 0;
+};
+const StTensor* st_tensor(const gorch_hip_st* f, const char* name);
+// gorch_hip_st_load without the argument checks of the C entry point.
+int st_load_tensor(hipStream_t s, const gorch_hip_st* f, const char* name, void* dst, int dst_dtype, int transpose);
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));

@@ -335,29 +335,35 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 extern "C" {
 
-gorch_hip_gpt* gorch_hip_gpt_create(const gorch_hip_gpt_weights* w) {
-    if (!w || w->vocab <= 0 || w->dim <= 0 || w->heads <= 0 || w->layers <= 0 || w->max_seq <= 0 ||
-        w->dim % w->heads != 0) {
-        set_error("gorch_hip_gpt_create: bad configuration");
-        return nullptr;
+namespace gh {
+
+static bool gpt_config_ok(int vocab, int dim, int heads, int layers, int max_seq, const char* who) {
+    if (vocab <= 0 || dim <= 0 || heads <= 0 || layers <= 0 || max_seq <= 0 || dim % heads != 0) {
+        set_error(std::string(who) + ": bad configuration");
+        return false;
     }
-    const int hd = w->dim / w->heads;
-    if (hd % 4 != 0 || hd > 256 || w->dim % 8 != 0) {
-        set_error("gorch_hip_gpt_create: needs dim % 8 == 0 and head_dim a multiple of 4, <= 256");
-        return nullptr;
+    const int hd = dim / heads;
+    if (hd % 4 != 0 || hd > 256 || dim % 8 != 0) {
+        set_error(std::string(who) + ": needs dim % 8 == 0 and head_dim a multiple of 4, <= 256");
+        return false;
     }
-    if (w->max_seq > 16384) {
-        set_error("gorch_hip_gpt_create: max_seq above 16384 is not supported");
-        return nullptr;
+    if (max_seq > 16384) {
+        set_error(std::string(who) + ": max_seq above 16384 is not supported");
+        return false;
     }
+    return true;
+}
+
+// Allocates the engine and its weight blob (256-byte aligned slices) and
+// points every weight at its slice; the contents are filled by the caller.
+static gorch_hip_gpt* gpt_alloc(int vocab, int dim, int heads, int layers, int max_seq) {
     auto* g = new gorch_hip_gpt();
-    g->vocab = w->vocab;
-    g->dim = w->dim;
-    g->heads = w->heads;
-    g->layers = w->layers;
-    g->max_seq = w->max_seq;
-    const size_t d = w->dim, V = w->vocab, S = w->max_seq;
-    // blob layout
+    g->vocab = vocab;
+    g->dim = dim;
+    g->heads = heads;
+    g->layers = layers;
+    g->max_seq = max_seq;
+    const size_t d = dim, V = vocab, S = max_seq;
     size_t off = 0;
     auto take = [&](size_t bytes) {
         size_t o = off;
@@ -369,8 +375,8 @@ gorch_hip_gpt* gorch_hip_gpt_create(const gorch_hip_gpt_weights* w) {
     struct LOff {
         size_t wqkv, bqkv, wo, bo, w1, b1, w2, b2, ln1_g, ln1_b, ln2_g, ln2_b;
     };
-    std::vector<LOff> lo(w->layers);
-    for (int l = 0; l < w->layers; l++) {
+    std::vector<LOff> lo(layers);
+    for (int l = 0; l < layers; l++) {
         lo[l].wqkv = take(3 * d * d * 2);
         lo[l].bqkv = take(3 * d * 4);
         lo[l].wo = take(d * d * 2);
@@ -388,44 +394,6 @@ gorch_hip_gpt* gorch_hip_gpt_create(const gorch_hip_gpt_weights* w) {
         delete g;
         return nullptr;
     }
-    bool ok = true;
-    auto put = [&](size_t o, const void* src, size_t bytes) {
-        if (!ok) return;
-        if (!src) {
-            set_error("gorch_hip_gpt_create: null weight pointer");
-            ok = false;
-            return;
-        }
-        ok = check(hipMemcpy(g->blob + o, src, bytes, hipMemcpyHostToDevice), "upload weights") == 0;
-    };
-    put(o_wte, w->wte, V * d * 4);
-    put(o_wpe, w->wpe, S * d * 4);
-    put(o_lnf_g, w->lnf_g, d * 4);
-    put(o_lnf_b, w->lnf_b, d * 4);
-    put(o_wlm, w->wlm, V * d * 2);
-    put(o_blm, w->blm, V * 4);
-    for (int l = 0; l < w->layers && ok; l++) {
-        put(lo[l].wqkv, w->wq[l], d * d * 2);
-        put(lo[l].wqkv + d * d * 2, w->wk[l], d * d * 2);
-        put(lo[l].wqkv + 2 * d * d * 2, w->wv[l], d * d * 2);
-        put(lo[l].bqkv, w->bq[l], d * 4);
-        put(lo[l].bqkv + d * 4, w->bk[l], d * 4);
-        put(lo[l].bqkv + 2 * d * 4, w->bv[l], d * 4);
-        put(lo[l].wo, w->wo[l], d * d * 2);
-        put(lo[l].bo, w->bo[l], d * 4);
-        put(lo[l].w1, w->w1[l], 4 * d * d * 2);
-        put(lo[l].b1, w->b1[l], 4 * d * 4);
-        put(lo[l].w2, w->w2[l], 4 * d * d * 2);
-        put(lo[l].b2, w->b2[l], d * 4);
-        put(lo[l].ln1_g, w->ln1_g[l], d * 4);
-        put(lo[l].ln1_b, w->ln1_b[l], d * 4);
-        put(lo[l].ln2_g, w->ln2_g[l], d * 4);
-        put(lo[l].ln2_b, w->ln2_b[l], d * 4);
-    }
-    if (!ok) {
-        gorch_hip_gpt_free(g);
-        return nullptr;
-    }
     auto F = [&](size_t o) { return reinterpret_cast<float*>(g->blob + o); };
     auto H = [&](size_t o) { return reinterpret_cast<uint16_t*>(g->blob + o); };
     g->wte = F(o_wte);
@@ -434,8 +402,8 @@ gorch_hip_gpt* gorch_hip_gpt_create(const gorch_hip_gpt_weights* w) {
     g->lnf_b = F(o_lnf_b);
     g->wlm = H(o_wlm);
     g->blm = F(o_blm);
-    g->L.resize(w->layers);
-    for (int l = 0; l < w->layers; l++) {
+    g->L.resize(layers);
+    for (int l = 0; l < layers; l++) {
         LayerW& L = g->L[l];
         L.wqkv = H(lo[l].wqkv);
         L.bqkv = F(lo[l].bqkv);
@@ -450,29 +418,33 @@ gorch_hip_gpt* gorch_hip_gpt_create(const gorch_hip_gpt_weights* w) {
         L.ln2_g = F(lo[l].ln2_g);
         L.ln2_b = F(lo[l].ln2_b);
     }
+    return g;
+}
+
+// Creates the engine stream and the tile-packed copies of the wide weights
+// (fused QKV, FFN1, LM head; K = dim), the layout the 2..16-row decode GEMV
+// streams with contiguous 1 KB fragment loads; the row-major originals serve
+// the single-row decode (LayerNorm fused) and prefill. Frees g on failure.
+static gorch_hip_gpt* gpt_finish(gorch_hip_gpt* g) {
     if (check(hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking), "hipStreamCreate")) {
         gorch_hip_gpt_free(g);
         return nullptr;
     }
-    // The wide weights (fused QKV, FFN1, LM head; K = dim) also get a
-    // tile-packed copy, the layout the 2..16-row decode GEMV streams with
-    // contiguous 1 KB fragment loads; the row-major originals serve the
-    // single-row decode (LayerNorm fused) and prefill.
     static const int packed_on = [] {
         const char* e = getenv("GORCH_HIP_PACKED");
         return e ? atoi(e) : 1;
     }();
-    if (packed_on && w->dim <= 3072) {
-        const int D = w->dim;
+    if (packed_on && g->dim <= 3072) {
+        const int D = g->dim;
         const size_t pq = align256(packed_bf16_elems(3 * D, D) * 2), p1 = align256(packed_bf16_elems(4 * D, D) * 2);
-        const size_t plm = align256(packed_bf16_elems(w->vocab, D) * 2);
-        if (check(hipMalloc(&g->pblob, plm + (size_t)w->layers * (pq + p1)), "hipMalloc packed weights")) {
+        const size_t plm = align256(packed_bf16_elems(g->vocab, D) * 2);
+        if (check(hipMalloc(&g->pblob, plm + (size_t)g->layers * (pq + p1)), "hipMalloc packed weights")) {
             gorch_hip_gpt_free(g);
             return nullptr;
         }
         g->wlm_p = reinterpret_cast<uint16_t*>(g->pblob);
-        int rc = launch_pack_bf16(g->stream, g->wlm, g->wlm_p, w->vocab, D);
-        for (int l = 0; l < w->layers && rc == 0; l++) {
+        int rc = launch_pack_bf16(g->stream, g->wlm, g->wlm_p, g->vocab, D);
+        for (int l = 0; l < g->layers && rc == 0; l++) {
             LayerW& L = g->L[l];
             L.wqkv_p = reinterpret_cast<uint16_t*>(g->pblob + plm + (size_t)l * (pq + p1));
             L.w1_p = reinterpret_cast<uint16_t*>(g->pblob + plm + (size_t)l * (pq + p1) + pq);
@@ -485,6 +457,133 @@ gorch_hip_gpt* gorch_hip_gpt_create(const gorch_hip_gpt_weights* w) {
         }
     }
     return g;
+}
+
+}  // namespace gh
+
+gorch_hip_gpt* gorch_hip_gpt_create(const gorch_hip_gpt_weights* w) {
+    if (!w) {
+        set_error("gorch_hip_gpt_create: null weights");
+        return nullptr;
+    }
+    if (!gpt_config_ok(w->vocab, w->dim, w->heads, w->layers, w->max_seq, "gorch_hip_gpt_create")) return nullptr;
+    gorch_hip_gpt* g = gpt_alloc(w->vocab, w->dim, w->heads, w->layers, w->max_seq);
+    if (!g) return nullptr;
+    const size_t d = w->dim, V = w->vocab, S = w->max_seq;
+    bool ok = true;
+    auto put = [&](void* dst, const void* src, size_t bytes) {
+        if (!ok) return;
+        if (!src) {
+            set_error("gorch_hip_gpt_create: null weight pointer");
+            ok = false;
+            return;
+        }
+        ok = check(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "upload weights") == 0;
+    };
+    put(g->wte, w->wte, V * d * 4);
+    put(g->wpe, w->wpe, S * d * 4);
+    put(g->lnf_g, w->lnf_g, d * 4);
+    put(g->lnf_b, w->lnf_b, d * 4);
+    put(g->wlm, w->wlm, V * d * 2);
+    put(g->blm, w->blm, V * 4);
+    for (int l = 0; l < w->layers && ok; l++) {
+        LayerW& L = g->L[l];
+        // the rows of Wq, Wk, Wv back to back: one fused [3d, d] weight
+        put(L.wqkv, w->wq[l], d * d * 2);
+        put(L.wqkv + d * d, w->wk[l], d * d * 2);
+        put(L.wqkv + 2 * d * d, w->wv[l], d * d * 2);
+        put(L.bqkv, w->bq[l], d * 4);
+        put(L.bqkv + d, w->bk[l], d * 4);
+        put(L.bqkv + 2 * d, w->bv[l], d * 4);
+        put(L.wo, w->wo[l], d * d * 2);
+        put(L.bo, w->bo[l], d * 4);
+        put(L.w1, w->w1[l], 4 * d * d * 2);
+        put(L.b1, w->b1[l], 4 * d * 4);
+        put(L.w2, w->w2[l], 4 * d * d * 2);
+        put(L.b2, w->b2[l], d * 4);
+        put(L.ln1_g, w->ln1_g[l], d * 4);
+        put(L.ln1_b, w->ln1_b[l], d * 4);
+        put(L.ln2_g, w->ln2_g[l], d * 4);
+        put(L.ln2_b, w->ln2_b[l], d * 4);
+    }
+    if (!ok) {
+        gorch_hip_gpt_free(g);
+        return nullptr;
+    }
+    return gpt_finish(g);
+}
+
+gorch_hip_gpt* gorch_hip_gpt_load_gpt2(const char* path, int vocab, int dim, int heads, int layers, int max_seq) {
+    if (!gpt_config_ok(vocab, dim, heads, layers, max_seq, "gorch_hip_gpt_load_gpt2")) return nullptr;
+    gorch_hip_st* f = gorch_hip_st_open(path);
+    if (!f) return nullptr;
+    gorch_hip_gpt* g = gpt_alloc(vocab, dim, heads, layers, max_seq);
+    if (!g) {
+        gorch_hip_st_close(f);
+        return nullptr;
+    }
+    const long long d = dim, V = vocab, S = max_seq;
+    bool ok = true;
+    // name with or without the GPT2LMHeadModel "transformer." prefix
+    auto resolve = [&](const std::string& n) -> std::string {
+        if (st_tensor(f, n.c_str())) return n;
+        const std::string p = "transformer." + n;
+        if (st_tensor(f, p.c_str())) return p;
+        return n;
+    };
+    // copyTensor's checks (model/gpt2_loader.go:139-150): present, same size
+    auto load = [&](const std::string& n0, void* dst, long long want_elems, std::vector<long long> want_shape,
+                    int dst_dtype, int transpose) {
+        if (!ok) return;
+        const std::string n = resolve(n0);
+        const StTensor* t = st_tensor(f, n.c_str());
+        if (!t) {
+            set_error("tensor \"" + n0 + "\" not found in safetensors");
+            ok = false;
+            return;
+        }
+        long long elems = 1;
+        for (long long x : t->shape) elems *= x;
+        if (elems != want_elems || (!want_shape.empty() && t->shape != want_shape)) {
+            set_error("size mismatch for \"" + n + "\": file=" + std::to_string(elems) +
+                      " model=" + std::to_string(want_elems));
+            ok = false;
+            return;
+        }
+        ok = st_load_tensor(nullptr, f, n.c_str(), dst, dst_dtype, transpose) == 0;
+    };
+    constexpr int F32 = GORCH_HIP_ST_F32, B16 = GORCH_HIP_ST_BF16;
+    load("wte.weight", g->wte, V * d, {V, d}, F32, 0);
+    load("wpe.weight", g->wpe, S * d, {S, d}, F32, 0);
+    for (int l = 0; l < layers && ok; l++) {
+        const std::string p = "h." + std::to_string(l) + ".";
+        LayerW& L = g->L[l];
+        load(p + "ln_1.weight", L.ln1_g, d, {}, F32, 0);
+        load(p + "ln_1.bias", L.ln1_b, d, {}, F32, 0);
+        // Conv1D (d, 3d) -> its transpose [3d, d]: rows 0..d-1 are Q's
+        // output features, then K's, then V's (loadFusedQKV, :190-244)
+        load(p + "attn.c_attn.weight", L.wqkv, 3 * d * d, {d, 3 * d}, B16, 1);
+        load(p + "attn.c_attn.bias", L.bqkv, 3 * d, {}, F32, 0);
+        load(p + "attn.c_proj.weight", L.wo, d * d, {d, d}, B16, 1);
+        load(p + "attn.c_proj.bias", L.bo, d, {}, F32, 0);
+        load(p + "ln_2.weight", L.ln2_g, d, {}, F32, 0);
+        load(p + "ln_2.bias", L.ln2_b, d, {}, F32, 0);
+        load(p + "mlp.c_fc.weight", L.w1, 4 * d * d, {d, 4 * d}, B16, 1);
+        load(p + "mlp.c_fc.bias", L.b1, 4 * d, {}, F32, 0);
+        load(p + "mlp.c_proj.weight", L.w2, 4 * d * d, {4 * d, d}, B16, 1);
+        load(p + "mlp.c_proj.bias", L.b2, d, {}, F32, 0);
+    }
+    load("ln_f.weight", g->lnf_g, d, {}, F32, 0);
+    load("ln_f.bias", g->lnf_b, d, {}, F32, 0);
+    // tied LM head (TieLMHeadToEmbedding): the bf16 rounding of wte, no bias
+    load("wte.weight", g->wlm, V * d, {V, d}, B16, 0);
+    if (ok) ok = check(hipMemset(g->blm, 0, (size_t)V * 4), "zero LM-head bias") == 0;
+    gorch_hip_st_close(f);
+    if (!ok) {
+        gorch_hip_gpt_free(g);
+        return nullptr;
+    }
+    return gpt_finish(g);
 }
 
 void gorch_hip_gpt_free(gorch_hip_gpt* g) {

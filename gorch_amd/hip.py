@@ -76,6 +76,14 @@ SIGNATURES = {
     "gorch_hip_moe_workspace_size": (C.c_size_t, [i32, i32, i32, i32, i32]),
     "gorch_hip_moe_forward": (i32, [vp, vp, vp, i32, vp, vp, vp, vp, vp, C.c_size_t]),
     "gorch_hip_gpt_create": (vp, [vp]),
+    "gorch_hip_gpt_load_gpt2": (vp, [C.c_char_p, i32, i32, i32, i32, i32]),
+    "gorch_hip_st_open": (vp, [C.c_char_p]),
+    "gorch_hip_st_close": (None, [vp]),
+    "gorch_hip_st_count": (i32, [vp]),
+    "gorch_hip_st_name": (C.c_char_p, [vp, i32]),
+    "gorch_hip_st_info": (i32, [vp, C.c_char_p, C.POINTER(i32), C.POINTER(i32), C.POINTER(i64),
+                                C.POINTER(i64)]),
+    "gorch_hip_st_load": (i32, [vp, vp, C.c_char_p, vp, i32, i32]),
     "gorch_hip_gpt_free": (None, [vp]),
     "gorch_hip_kvcache_create": (vp, [vp, i32, i32]),
     "gorch_hip_kvcache_free": (None, [vp]),
@@ -277,10 +285,65 @@ _LAYER_KEYS = ("ln1_g", "ln1_b", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo",
                "ln2_g", "ln2_b", "w1", "b1", "w2", "b2")
 
 
+ST_F32, ST_F16, ST_BF16 = 0, 1, 2
+_ST_NAMES = {ST_F32: "F32", ST_F16: "F16", ST_BF16: "BF16"}
+
+
+class SafeTensors:
+    """A safetensors checkpoint opened through the C-ABI
+    (model/safetensors.go:52-130): the header is parsed and validated on
+    open (host only); tensors load on demand into device tensors."""
+
+    def __init__(self, path: str):
+        self.h = lib().gorch_hip_st_open(os.fsencode(path))
+        if not self.h:
+            raise HipError(2, last_error())
+
+    def names(self) -> list:
+        n = lib().gorch_hip_st_count(self.h)
+        return [lib().gorch_hip_st_name(self.h, i).decode() for i in range(n)]
+
+    def info(self, name: str):
+        """(dtype name, shape tuple, stored bytes)."""
+        dt, nd = C.c_int(), C.c_int()
+        shape = (C.c_int64 * 8)()
+        nb = C.c_int64()
+        _ok(lib().gorch_hip_st_info(self.h, name.encode(), C.byref(dt), C.byref(nd), shape, C.byref(nb)))
+        return _ST_NAMES[dt.value], tuple(shape[i] for i in range(nd.value)), nb.value
+
+    def load(self, name: str, dst, dtype: int, transpose: bool = False) -> None:
+        """Reads tensor ``name`` into the device tensor ``dst`` as F32 or BF16."""
+        _ok(lib().gorch_hip_st_load(_stream(), self.h, name.encode(), _p(dst), dtype, 1 if transpose else 0))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().gorch_hip_st_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class GPT:
     """gorch's nn.GPT on the GPU (nn/gpt.go:12-121). ``weights`` is a dict
     of numpy arrays in the layout gorch_amd.synthetic produces (Linear
     weights bf16 as uint16 [out, in])."""
+
+    @classmethod
+    def from_gpt2_safetensors(cls, path: str, cfg: dict) -> "GPT":
+        """LoadGPT2 (model/gpt2_loader.go:56-133) from a Hugging Face GPT-2
+        model.safetensors, straight into device memory."""
+        h = lib().gorch_hip_gpt_load_gpt2(os.fsencode(path), cfg["vocab"], cfg["dim"], cfg["heads"],
+                                          cfg["layers"], cfg["max_seq"])
+        if not h:
+            raise HipError(2, last_error())
+        g = cls.__new__(cls)
+        g.cfg = dict(cfg)
+        g.h = h
+        return g
 
     def __init__(self, weights: dict):
         import numpy as np

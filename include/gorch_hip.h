@@ -259,12 +259,52 @@ typedef struct {
     const uint16_t* wlm; const float* blm;               /* LM head [vocab, d] */
 } gorch_hip_gpt_weights;
 
+/* ------------------------------------------------------------------------
+ * safetensors checkpoints (model/safetensors.go:52-184).
+ * ---------------------------------------------------------------------- */
+
+#define GORCH_HIP_ST_F32 0
+#define GORCH_HIP_ST_F16 1
+#define GORCH_HIP_ST_BF16 2
+
+typedef struct gorch_hip_st gorch_hip_st;
+/* Parses and validates the header (LoadSafetensors' checks: unsupported
+ * dtype, offsets outside the data, byte count vs shape); tensor data is read
+ * on demand. NULL on failure (gorch_hip_last_error). Host-only. */
+gorch_hip_st* gorch_hip_st_open(const char* path);
+void gorch_hip_st_close(gorch_hip_st* f);
+/* Tensor names in sorted order (SafetensorsFile.Names). */
+int gorch_hip_st_count(const gorch_hip_st* f);
+const char* gorch_hip_st_name(const gorch_hip_st* f, int i);
+/* dtype (GORCH_HIP_ST_*), rank, shape (up to 8 dims) and stored bytes;
+ * any output may be NULL. */
+int gorch_hip_st_info(const gorch_hip_st* f, const char* name, int* dtype, int* ndim, int64_t* shape,
+                      int64_t* nbytes);
+/* Reads one tensor into device memory `dst` as F32 (F32 copied, F16/BF16
+ * widened exactly: decodeF16 / decodeBF16) or BF16 (BF16 bits kept, the
+ * native loader's decodeBF16Raw; F32/F16 rounded with f32ToBF16,
+ * tensor.go:85-101). transpose: a 2-D [R, C] tensor lands as [C, R] (a
+ * GPT-2 Conv1D weight (in, out) as a Linear weight (out, in),
+ * model/gpt2_loader.go:170-184). Synchronous. */
+int gorch_hip_st_load(void* stream, const gorch_hip_st* f, const char* name, void* dst, int dst_dtype,
+                      int transpose);
+
 typedef struct gorch_hip_gpt gorch_hip_gpt;
 typedef struct gorch_hip_kvcache gorch_hip_kvcache;
 
 /* Uploads the weights to the current device (gpt.ToMetal, nn/gpt.go:241-257),
  * fusing Wq/Wk/Wv into one [3d, d] weight. NULL on failure. */
 gorch_hip_gpt* gorch_hip_gpt_create(const gorch_hip_gpt_weights* w);
+/* LoadGPT2 (model/gpt2_loader.go:56-133) from a Hugging Face GPT-2
+ * model.safetensors straight into device memory: Conv1D weights transposed
+ * on the GPU, c_attn kept as the fused [3d, d] QKV weight (its transpose;
+ * the reference splits the same rows into Wq, Wk, Wv), Linear weights in
+ * bf16 (BF16 files bit-exact, F32 files rounded with f32ToBF16), embeddings,
+ * biases and LayerNorms in f32, the LM head tied to wte (TieLMHeadToEmbedding)
+ * as its bf16 rounding with a zero bias. Tensor names with or without the
+ * "transformer." prefix. A missing tensor or a size that differs from the
+ * configuration fails, as in copyTensor. NULL on failure. */
+gorch_hip_gpt* gorch_hip_gpt_load_gpt2(const char* path, int vocab, int dim, int heads, int layers, int max_seq);
 void gorch_hip_gpt_free(gorch_hip_gpt* gpt);
 /* KV cache for `batch` independent sequences of up to `capacity` tokens
  * (NewKVCache, nn/kvcache.go:23-36; one reference cache per sequence). */
