@@ -268,6 +268,138 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// k_attn_flash: attention for many new rows at once (prefill; MHA.Forward's
+// causal case, nn/attention.go:64-145, as the cached path's prompt pass) on
+// the f32 matrix cores (v_mfma_f32_16x16x4_f32: products and sums in f32).
+//
+// A block of NW waves takes 16 * NW consecutive query rows of one (sequence,
+// head); wave w owns 16 of them. Keys stream through LDS in stages of KT:
+// K row-major [key][dim] and V transposed [dim][key], loaded once per block
+// for all its waves. Per 16-key slice a wave computes S^T = K Q^T (lane
+// (r, g) then holds keys 4g .. 4g+3 of query r), applies the scale
+// ((q.k) * scale, as the reference), the causal mask and an online softmax
+// per query (running max m and per-lane partial sums l rescaled by
+// exp(m_old - m_new)), and accumulates O^T += V^T P^T: the probabilities are
+// already in the B-operand position when the MFMA's k index runs over the
+// keys a lane holds, so P never leaves registers. O = O^T / l at the end
+// (the reference normalises P before P.V: same values up to rounding).
+// The dims of the QK^T product are visited as 16u + 4g + c by (step, lane
+// group), so both Q and K fragments are 16-byte reads.
+__device__ __forceinline__ floatx4 mfma_f32x4(float a, float b, const floatx4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int HD, int NW>
+__global__ __launch_bounds__(NW * 64) void k_attn_flash(AttnArgs a) {
+    constexpr int KT = 32;   // keys per LDS stage
+    constexpr int QU = HD / 16;
+    __shared__ float4 Ks[KT][HD / 4 + 1];   // K[key][dims 4c..4c+3]
+    __shared__ float4 Vt[HD][KT / 4 + 1];   // V^T[dim][keys 4c..4c+3]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int b = blockIdx.z, h = blockIdx.y;
+    const int qbase = blockIdx.x * 16 * NW;
+    const int qi = qbase + wave * 16 + r;  // this lane's query (column of S^T)
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    const int kvh = a.kv_heads ? h / ((int)gridDim.y / a.kv_heads) : h;
+    const int kvd = a.kv_dim ? a.kv_dim : a.dim;
+    const size_t cbase = (size_t)b * a.max_seq * kvd + (size_t)kvh * HD;
+    const float4* K4 = reinterpret_cast<const float4*>(a.kc + cbase);
+    const float4* V4 = reinterpret_cast<const float4*>(a.vc + cbase);
+    const int kvd4 = kvd >> 2;
+    const int t_all = pos + a.new_seq;
+    const int qlast = min(a.new_seq, qbase + 16 * NW) - 1;
+    const int kend = a.causal ? pos + qlast + 1 : t_all;
+
+    const bool qok = qi < a.new_seq;
+    const float* qrow = a.q + (size_t)(b * a.new_seq + (qok ? qi : 0)) * a.q_stride + h * HD;
+    float4 qf[QU];
+#pragma unroll
+    for (int u = 0; u < QU; u++)
+        qf[u] = qok ? *reinterpret_cast<const float4*>(qrow + 16 * u + 4 * g) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const int P = pos + qi;  // absolute position of this lane's query
+
+    floatx4 o[QU];
+#pragma unroll
+    for (int t = 0; t < QU; t++) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+
+    for (int k0 = 0; k0 < kend; k0 += KT) {
+        __syncthreads();  // the previous stage has been read
+        for (int i = threadIdx.x; i < KT * HD / 4; i += NW * 64) {
+            const int kr = i / (HD / 4), c4 = i - kr * (HD / 4);
+            const int key = k0 + kr;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (key < t_all) {
+                kv = K4[(size_t)key * kvd4 + c4];
+                vv = V4[(size_t)key * kvd4 + c4];
+            }
+            Ks[kr][c4] = kv;
+            float* vt = reinterpret_cast<float*>(&Vt[0][0]);
+            constexpr int VS = 4 * (KT / 4 + 1);  // floats per V^T row
+            vt[(4 * c4 + 0) * VS + kr] = vv.x;
+            vt[(4 * c4 + 1) * VS + kr] = vv.y;
+            vt[(4 * c4 + 2) * VS + kr] = vv.z;
+            vt[(4 * c4 + 3) * VS + kr] = vv.w;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int sub = 0; sub < KT / 16; sub++) {
+            floatx4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < QU; u++) {
+                const float4 kf = Ks[sub * 16 + r][4 * u + g];
+                s = mfma_f32x4(kf.x, qf[u].x, s);
+                s = mfma_f32x4(kf.y, qf[u].y, s);
+                s = mfma_f32x4(kf.z, qf[u].z, s);
+                s = mfma_f32x4(kf.w, qf[u].w, s);
+            }
+            float sv[4];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int key = k0 + sub * 16 + 4 * g + v;
+                const bool ok = qok && key < t_all && (!a.causal || key <= P);
+                sv[v] = ok ? s[v] * a.scale : -INFINITY;
+                tmax = fmaxf(tmax, sv[v]);
+            }
+            // the query's maximum over the 4 lane groups holding its keys
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+            const float mnew = fmaxf(m, tmax);
+            const float alpha = mnew == -INFINITY ? 1.f : expf(m - mnew);
+            float p[4], psum = 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                p[v] = sv[v] == -INFINITY ? 0.f : expf(sv[v] - mnew);
+                psum += p[v];
+            }
+            l = l * alpha + psum;
+            m = mnew;
+#pragma unroll
+            for (int t = 0; t < QU; t++) {
+                o[t] *= alpha;
+                const float4 vf = Vt[16 * t + r][4 * sub + g];
+                o[t] = mfma_f32x4(vf.x, p[0], o[t]);
+                o[t] = mfma_f32x4(vf.y, p[1], o[t]);
+                o[t] = mfma_f32x4(vf.z, p[2], o[t]);
+                o[t] = mfma_f32x4(vf.w, p[3], o[t]);
+            }
+        }
+    }
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (qok) {
+        float* orow = a.out + (size_t)(b * a.new_seq + qi) * a.dim + h * HD;
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int t = 0; t < QU; t++)
+            *reinterpret_cast<float4*>(orow + 16 * t + 4 * g) =
+                make_float4(o[t][0] * inv, o[t][1] * inv, o[t][2] * inv, o[t][3] * inv);
+    }
+}
+
 // 4 waves per (head, row) block when there are enough blocks to fill the
 // GPU; 16 waves when the visible context is long and blocks are few, so each
 // block keeps more of the KV stream in flight.
@@ -281,6 +413,21 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
     const bool aligned = (a.q_stride % 4 == 0) && (a.dim % 4 == 0) && ((a.kv_dim ? a.kv_dim : a.dim) % 4 == 0) &&
                          ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.kc) |
                            reinterpret_cast<uintptr_t>(a.vc) | reinterpret_cast<uintptr_t>(a.out)) % 16 == 0);
+    // many new rows per sequence (prefill): the matrix-core kernel, 128
+    // query rows per block sharing each staged K/V tile
+    static const int flash_min = [] {
+        const char* e = getenv("GORCH_HIP_ATTN_FLASH_MIN_ROWS");
+        return e ? atoi(e) : 32;
+    }();
+    if (flash_min > 0 && aligned && a.new_seq >= flash_min && (a.hd == 64 || a.hd == 128) &&
+        (a.q_stride % 4) == 0) {
+        const int batch = rows / a.new_seq;
+        const dim3 grid((a.new_seq + 127) / 128, heads, batch);
+        if (a.hd == 64) hipLaunchKernelGGL((k_attn_flash<64, 8>), grid, dim3(512), 0, s, a);
+        else hipLaunchKernelGGL((k_attn_flash<128, 8>), grid, dim3(512), 0, s, a);
+        count(CNT_ATTENTION);
+        return check_launch("attn_flash");
+    }
     // short caches: the (key, chunk)-lane kernel; long ones stream better
     // through the per-dim kernel below
     if (rows_kernel && aligned && a.max_seq <= 256 && (a.hd == 64 || a.hd == 128 || a.hd == 32 || a.hd == 16)) {

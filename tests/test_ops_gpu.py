@@ -100,6 +100,30 @@ def test_attention_cached(gpu, batch, new_seq, pos, heads, hd):
         assert np.max(np.abs(got[b * new_seq:(b + 1) * new_seq] - ref)) < 1e-5
 
 
+@pytest.mark.parametrize("batch,new_seq,pos,heads,hd,causal", [
+    (1, 32, 0, 12, 64, True), (2, 100, 0, 4, 64, True), (1, 257, 37, 3, 64, True), (3, 64, 5, 2, 128, True),
+    (1, 130, 0, 2, 64, False), (2, 48, 20, 2, 128, False), (16, 64, 0, 2, 64, True)])
+def test_attention_prefill_rows(gpu, batch, new_seq, pos, heads, hd, causal):
+    # many new rows per sequence: the matrix-core (flash) kernel; held to
+    # 1e-4 absolute (the reference bounds cached vs one-shot logits at 1e-3)
+    rng = np.random.default_rng(new_seq * 7 + pos + hd)
+    d = heads * hd
+    max_seq = pos + new_seq + 5
+    q = rng.standard_normal((batch * new_seq, d)).astype(np.float32)
+    kc = rng.standard_normal((batch, max_seq, d)).astype(np.float32)
+    vc = rng.standard_normal((batch, max_seq, d)).astype(np.float32)
+    out = torch.empty((batch * new_seq, d), device="cuda")
+    gpu.reset_dispatch_counts()
+    gpu.attention_cached(dev(q), dev(kc), dev(vc), out, batch, new_seq, pos, heads, hd, max_seq, causal=causal)
+    assert gpu.dispatch_counts()["attention"] == 1
+    got = host(out)
+    for b in range(batch):
+        T = pos + new_seq
+        ref = orc.attention_cached(q[b * new_seq:(b + 1) * new_seq], kc[b, :T], vc[b, :T], pos, heads,
+                                   causal=causal)
+        assert np.max(np.abs(got[b * new_seq:(b + 1) * new_seq] - ref)) < 1e-4
+
+
 def test_attention_noncausal(gpu):
     rng = np.random.default_rng(5)
     heads, hd, pos, n = 4, 64, 6, 3
