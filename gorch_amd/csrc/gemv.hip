@@ -765,7 +765,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
 // residual, output, argmax keys). Every load is a raw buffer load with no
 // branch around it: k past the wave's range, rows past M or N and tiles
 // past the last read as zeros.
-template <int NW, int KS, bool PACKED>
+template <int NW, int KS, bool PACKED, bool EARLY>
 __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict__ x, const uint16_t* __restrict__ W,
                                                         const float* __restrict__ bias, const float* residual,
                                                         OutDesc od, int M, int N, int K, int ks, int epilogue,
@@ -846,7 +846,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
     unsigned long long best = 0ull;
     const float* redf = reinterpret_cast<const float*>(&red[0][0][0]);
 
-    auto step = [&](int tt, const Tile& tl, int buf) {
+    // Tile tt from register set tl, whose registers are then refilled with
+    // tile next: with EARLY as soon as the matrix cores have read them
+    // (before the barrier and the epilogue: measured faster with one or two
+    // tiles per block), else after the epilogue (faster with many)
+    auto step = [&](int tt, Tile& tl, int buf, int next) {
         // hi and lo products in two accumulators: two independent MFMA chains
         floatx4 acc_h = {0.f, 0.f, 0.f, 0.f}, acc_l = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -854,6 +858,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
             const bf16x8 b = __builtin_bit_cast(bf16x8, tl.w[u]);
             acc_h = mfma16x16x32(ah[u], b, acc_h);
             acc_l = mfma16x16x32(al[u], b, acc_l);
+        }
+        float bv = 0.f, rv = 0.f;
+        if constexpr (EARLY) {
+            bv = tl.b;
+            rv = tl.res;
+            load(next, tl);
         }
         red[buf][wave][lane] = acc_h + acc_l;
         __syncthreads();
@@ -863,9 +873,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
             float val = 0.f;
 #pragma unroll
             for (int w = 0; w < NW; w++) val += redf[((buf * NW + w) * 64 + src) * 4 + comp];
-            if (bias) val = val + tl.b;
+            if (bias) val = val + (EARLY ? bv : tl.b);
             if (epilogue == GORCH_HIP_EPI_GELU) val = gelu_tanh(val);
-            if (residual) val = tl.res + val;
+            if (residual) val = (EARLY ? rv : tl.res) + val;
             *od.at_p(om, on, posv) = val;
             if (ex.argmax_key) {
                 const unsigned long long key = argmax_pack(val, on);
@@ -874,10 +884,15 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
         }
     };
     for (; t < ntiles; t += 2 * G) {
-        step(t, ta, 0);
-        load(t + 2 * G, ta);
-        if (t + G < ntiles) step(t + G, tb, 1);
-        load(t + 3 * G, tb);
+        if constexpr (EARLY) {
+            step(t, ta, 0, t + 2 * G);
+            if (t + G < ntiles) step(t + G, tb, 1, t + 3 * G);
+        } else {
+            step(t, ta, 0, 0);
+            load(t + 2 * G, ta);
+            if (t + G < ntiles) step(t + G, tb, 1, 0);
+            load(t + 3 * G, tb);
+        }
     }
     if (ex.argmax_key) {
         // row om's maximum over the 16 columns (the 16 lanes of one DPP row
@@ -1051,22 +1066,25 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
             per_cu = 1, cus = cus > 0 ? cus : 256;
         return blocks_env ? blocks_env : per_cu * cus;
     };
+#define GH_TILES_L(NWV, KSV, PK, EA)                                                                    \
+    hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, PK, EA>), dim3(blocks), dim3(NWV * 64), 0, s, x, W, bias,    \
+                       residual, od, M, N, K, ks, epilogue, ex)
 #define GH_TILES(NWV, KSV)                                                                                \
     if (nw == NWV && ks <= KSV) {                                                                         \
-        static const int blocks_p = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, true>), NWV * 64); \
-        static const int blocks_r = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, false>), NWV * 64); \
+        static const int blocks_p = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, true, false>), NWV * 64); \
+        static const int blocks_r = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, false, false>), NWV * 64); \
         const int blocks = std::min(packed ? blocks_p : blocks_r, ntiles);                                \
-        if (packed)                                                                                       \
-            hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, true>), dim3(blocks), dim3(NWV * 64), 0, s, x, W, bias, \
-                               residual, od, M, N, K, ks, epilogue, ex);                                  \
-        else                                                                                              \
-            hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, false>), dim3(blocks), dim3(NWV * 64), 0, s, x, W, bias, \
-                               residual, od, M, N, K, ks, epilogue, ex);                                  \
+        const bool early = ntiles <= 2 * blocks;                                                          \
+        if (packed && early) GH_TILES_L(NWV, KSV, true, true);                                            \
+        else if (packed) GH_TILES_L(NWV, KSV, true, false);                                               \
+        else if (early) GH_TILES_L(NWV, KSV, false, true);                                                \
+        else GH_TILES_L(NWV, KSV, false, false);                                                          \
         count(CNT_GEMV);                                                                                  \
         return check_launch("gemv_tiles");                                                                \
     }
     GH_TILES(4, 4) GH_TILES(4, 8) GH_TILES(8, 4) GH_TILES(8, 8) GH_TILES(8, 12) GH_TILES(16, 4)
 #undef GH_TILES
+#undef GH_TILES_L
     return -1;
 }
 
