@@ -168,10 +168,11 @@ MFMA_PEAK_TFLOPS = 2516.6  # dense bf16: 256 CU x 2.4 GHz x 4096 FLOP/clk
 def resident_layout(M, K, N):
     """Weight layout the decode path keeps resident for a GEMV of this
     shape, as the GPT engine does (gorch_amd/csrc/gpt.hip): the tile-packed
-    format for 2..16 rows over wide weights (>= 128 16-row tiles) with
-    K <= 3072; row-major for one row (the register GEMV) and for narrow
-    weights (K split across blocks)."""
-    if 2 <= M <= 16 and (N + 15) // 16 >= 128 and K <= 3072:
+    format for 2..16 rows (wide weights with K <= 3072 streamed whole,
+    narrow ones with K split across blocks); row-major for one row (the
+    register GEMV, LayerNorm fusable)."""
+    wide = (N + 15) // 16 >= 128
+    if 2 <= M <= 16 and ((wide and K <= 3072) or (not wide and K >= 1024)):
         return "packed"
     return "row-major"
 
@@ -396,8 +397,8 @@ def main():
             "shapes": [f"M={s[0]},K={s[1]},N={s[2]}" for s in shapes],
             "weights_rotated_over_bytes": ROTATE_BYTES,
             "weight_layout": "each shape on the decode path's resident format (per_shape.layout): "
-                             "tile-packed 1 KB matrix-core fragments for 2..16 rows over weights of >= 128 "
-                             "16-row tiles with K <= 3072, packed once before timing; row-major otherwise",
+                             "tile-packed 1 KB matrix-core fragments for 2..16 rows (packed once before "
+                             "timing; narrow weights with K split across blocks); row-major for one row",
         },
         "roofline": {
             "bound": "hbm",

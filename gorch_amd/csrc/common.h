@@ -75,6 +75,8 @@ int launch_pack_bf16(hipStream_t s, const uint16_t* W, uint16_t* Wp, int N, int 
 int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, const float* bias,
                             const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
                             const LinearExtras& ex);
+// K slices the packed GEMV uses for a K-split of an [N, K] weight.
+int packed_split_slices(int K, int N);
 int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                           const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
                           const LinearExtras& ex);

@@ -774,7 +774,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
     __shared__ unsigned long long s_key[16];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
-    const int kb = wave * ks * 32, ke = min(K, kb + ks * 32);
+    // K-split mode (ex.part): blockIdx.y is the K slice [ex.kslice * y, ..)
+    // and the block writes raw partial sums for a following reduction
+    const int k_off = ex.part ? (int)blockIdx.y * ex.kslice : 0;
+    const int k_end = ex.part ? min(K, k_off + ex.kslice) : K;
+    const int kb = k_off + wave * ks * 32, ke = min(k_end, kb + ks * 32);
     const long long xs = ex.x_stride ? ex.x_stride : K;
     const int ntiles = (N + 15) >> 4;
     const int G = gridDim.x;
@@ -873,6 +877,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
             float val = 0.f;
 #pragma unroll
             for (int w = 0; w < NW; w++) val += redf[((buf * NW + w) * 64 + src) * 4 + comp];
+            if (ex.part) {
+                ex.part[((size_t)blockIdx.y * M + om) * N + on] = val;
+                return;
+            }
             if (bias) val = val + (EARLY ? bv : tl.b);
             if (epilogue == GORCH_HIP_EPI_GELU) val = gelu_tanh(val);
             if (residual) val = (EARLY ? rv : tl.res) + val;
@@ -1053,7 +1061,9 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
     static const int nw_env = env_int("GORCH_HIP_TILES_NW", 0);
     static const int blocks_env = env_int("GORCH_HIP_TILES_BLOCKS", 0);
     const int ntiles = (N + 15) / 16;
-    const int ksteps = (K + 31) / 32;
+    // with ex.part the grid's y dimension is ex.ksplit K slices of ex.kslice
+    const int S = ex.part ? ex.ksplit : 1;
+    const int ksteps = ex.part ? ex.kslice / 32 : (K + 31) / 32;
     const int nw = nw_env ? nw_env : 8;
     const int ks = (ksteps + nw - 1) / nw;
     // one round of resident blocks: a block beyond what the CUs hold at once
@@ -1067,13 +1077,13 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
         return blocks_env ? blocks_env : per_cu * cus;
     };
 #define GH_TILES_L(NWV, KSV, PK, EA)                                                                    \
-    hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, PK, EA>), dim3(blocks), dim3(NWV * 64), 0, s, x, W, bias,    \
+    hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, PK, EA>), dim3(blocks, S), dim3(NWV * 64), 0, s, x, W, bias, \
                        residual, od, M, N, K, ks, epilogue, ex)
 #define GH_TILES(NWV, KSV)                                                                                \
     if (nw == NWV && ks <= KSV) {                                                                         \
         static const int blocks_p = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, true, false>), NWV * 64); \
         static const int blocks_r = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, false, false>), NWV * 64); \
-        const int blocks = std::min(packed ? blocks_p : blocks_r, ntiles);                                \
+        const int blocks = std::min(std::max(1, (packed ? blocks_p : blocks_r) / S), ntiles);             \
         const bool early = ntiles <= 2 * blocks;                                                          \
         if (packed && early) GH_TILES_L(NWV, KSV, true, true);                                            \
         else if (packed) GH_TILES_L(NWV, KSV, true, false);                                               \
@@ -1342,13 +1352,54 @@ int launch_pack_bf16(hipStream_t s, const uint16_t* W, uint16_t* Wp, int N, int 
     return check_launch("pack_bf16");
 }
 
+// K slices of a K-split packed GEMV: about 32 k-steps (1024 of K) per slice
+// and at least ~192 blocks in all, at most 8 slices (measured best at
+// K = 1600 / 3072 / 6400 over 1600 / 768 / 1600 rows: 7.2 / 7.1 / 10.9 us at
+// 16 rows against 7.7 / 7.2 / 15.6 us for the row-major split).
+int packed_split_slices(int K, int N) {
+    const int ksteps = (K + 31) / 32, ntiles = (N + 15) / 16;
+    int S = std::max((ksteps + 31) / 32, (192 + ntiles - 1) / ntiles);
+    S = std::min(std::min(S, kEpiSlices), std::max(1, ksteps / 3));
+    return ksplit_slices(K, S);
+}
+
 // Linear over tile-packed weights, 1 <= M <= 16 (the decode GEMV).
 int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, const float* bias,
                             const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
                             const LinearExtras& ex) {
-    if (M < 1 || M > 16 || ex.part || ex.ln_g) {
-        set_error("linear_bf16_packed: needs 1 <= M <= 16, no K split, no fused LayerNorm");
+    if (M < 1 || M > 16 || ex.ln_g || (ex.part && ex.argmax_key)) {
+        set_error("linear_bf16_packed: needs 1 <= M <= 16, no fused LayerNorm, no argmax with a K split");
         return GORCH_HIP_EUNSUPPORTED;
+    }
+    if (ex.part) {
+        // caller-owned partials (the engine's row reducer sums them)
+        LinearExtras sx = ex;
+        sx.kslice = ((K + ex.ksplit - 1) / ex.ksplit + 31) / 32 * 32;
+        sx.ksplit = (K + sx.kslice - 1) / sx.kslice;
+        const int rc = launch_tiles(s, x, Wp, nullptr, nullptr, OutDesc::plain(nullptr, N), M, N, K,
+                                    GORCH_HIP_EPI_NONE, sx, true);
+        if (rc < 0) set_error("linear_bf16_packed: K slice above 3072 is not supported");
+        return rc < 0 ? GORCH_HIP_EUNSUPPORTED : rc;
+    }
+    // a narrow weight (few 16-row tiles) over a long K: split K across blocks
+    // into the stream's scratch, then the ordered epilogue kernel (a CU
+    // streams ~25 GB/s, so 48..127 tiles alone leave most of the chip idle)
+    const int ntiles = (N + 15) / 16;
+    if (!ex.argmax_key && ntiles < 128 && K >= 1024) {
+        const int S = packed_split_slices(K, N);
+        void* part = S >= 2 ? stream_scratch(s, (size_t)S * M * N * sizeof(float)) : nullptr;
+        if (part) {
+            LinearExtras sx = ex;
+            sx.part = static_cast<float*>(part);
+            sx.kslice = ((K + S - 1) / S + 31) / 32 * 32;
+            sx.ksplit = (K + sx.kslice - 1) / sx.kslice;
+            const int rc = launch_tiles(s, x, Wp, nullptr, nullptr, OutDesc::plain(nullptr, N), M, N, K,
+                                        GORCH_HIP_EPI_NONE, sx, true);
+            if (rc >= 0) {
+                GH_TRY(rc);
+                return launch_splitk_epilogue(s, sx.part, sx.ksplit, M, N, bias, residual, od, epilogue);
+            }
+        }
     }
     const int rc = launch_tiles(s, x, Wp, bias, residual, od, M, N, K, epilogue, ex, true);
     if (rc < 0) {

@@ -41,9 +41,8 @@ __global__ void k_pos_add(int* pos_dev, int n) { *pos_dev += n; }
 struct LayerW {
     uint16_t *wqkv, *wo, *w1, *w2;
     float *bqkv, *bo, *b1, *b2, *ln1_g, *ln1_b, *ln2_g, *ln2_b;
-    // tile-packed copies of the wide weights for the 2..16-row decode GEMV
-    // (null when not packed)
-    uint16_t *wqkv_p = nullptr, *w1_p = nullptr;
+    // tile-packed copies for the 2..16-row decode GEMVs (null when not packed)
+    uint16_t *wqkv_p = nullptr, *w1_p = nullptr, *wo_p = nullptr, *w2_p = nullptr;
 };
 
 }  // namespace gh
@@ -218,9 +217,13 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         if (batched) {
             LinearExtras sp;
             sp.part = g->part;
-            sp.ksplit = split_for(d);
-            GH_TRY(launch_linear_bf16_od(s, g->att, w.wo, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d, d,
-                                         GORCH_HIP_EPI_NONE, sp));
+            sp.ksplit = w.wo_p ? packed_split_slices(d, d) : split_for(d);
+            if (w.wo_p)
+                GH_TRY(launch_linear_packed_od(s, g->att, w.wo_p, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d,
+                                               d, GORCH_HIP_EPI_NONE, sp));
+            else
+                GH_TRY(launch_linear_bf16_od(s, g->att, w.wo, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d, d,
+                                             GORCH_HIP_EPI_NONE, sp));
             GH_TRY(launch_reduce_rows(s, g->part, sp.ksplit, w.bo, g->x, rows, d, eps, g->stats, w.ln2_g, w.ln2_b,
                                       g->h));
         } else {
@@ -241,9 +244,13 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         if (batched) {
             LinearExtras sp;
             sp.part = g->part;
-            sp.ksplit = split_for(4 * d);
-            GH_TRY(launch_linear_bf16_od(s, g->ff, w.w2, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d, 4 * d,
-                                         GORCH_HIP_EPI_NONE, sp));
+            sp.ksplit = w.w2_p ? packed_split_slices(4 * d, d) : split_for(4 * d);
+            if (w.w2_p)
+                GH_TRY(launch_linear_packed_od(s, g->ff, w.w2_p, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d,
+                                               4 * d, GORCH_HIP_EPI_NONE, sp));
+            else
+                GH_TRY(launch_linear_bf16_od(s, g->ff, w.w2, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d,
+                                             4 * d, GORCH_HIP_EPI_NONE, sp));
             // the next LayerNorm: the next layer's first, or the final one
             const bool last = l + 1 == g->layers;
             GH_TRY(launch_reduce_rows(s, g->part, sp.ksplit, w.b2, g->x, rows, d, eps, g->stats,
@@ -421,10 +428,11 @@ static gorch_hip_gpt* gpt_alloc(int vocab, int dim, int heads, int layers, int m
     return g;
 }
 
-// Creates the engine stream and the tile-packed copies of the wide weights
-// (fused QKV, FFN1, LM head; K = dim), the layout the 2..16-row decode GEMV
-// streams with contiguous 1 KB fragment loads; the row-major originals serve
-// the single-row decode (LayerNorm fused) and prefill. Frees g on failure.
+// Creates the engine stream and tile-packed copies of the Linear weights
+// (fused QKV, Wo, FFN1, FFN2, LM head), the layout the 2..16-row decode
+// GEMVs stream with contiguous 1 KB fragment loads (Wo and FFN2 with K split
+// across blocks); the row-major originals serve the single-row decode
+// (LayerNorm fused) and prefill. Frees g on failure.
 static gorch_hip_gpt* gpt_finish(gorch_hip_gpt* g) {
     if (check(hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking), "hipStreamCreate")) {
         gorch_hip_gpt_free(g);
@@ -437,8 +445,10 @@ static gorch_hip_gpt* gpt_finish(gorch_hip_gpt* g) {
     if (packed_on && g->dim <= 3072) {
         const int D = g->dim;
         const size_t pq = align256(packed_bf16_elems(3 * D, D) * 2), p1 = align256(packed_bf16_elems(4 * D, D) * 2);
+        const size_t po = align256(packed_bf16_elems(D, D) * 2), p2 = align256(packed_bf16_elems(D, 4 * D) * 2);
         const size_t plm = align256(packed_bf16_elems(g->vocab, D) * 2);
-        if (check(hipMalloc(&g->pblob, plm + (size_t)g->layers * (pq + p1)), "hipMalloc packed weights")) {
+        const size_t per_layer = pq + p1 + po + p2;
+        if (check(hipMalloc(&g->pblob, plm + (size_t)g->layers * per_layer), "hipMalloc packed weights")) {
             gorch_hip_gpt_free(g);
             return nullptr;
         }
@@ -446,10 +456,15 @@ static gorch_hip_gpt* gpt_finish(gorch_hip_gpt* g) {
         int rc = launch_pack_bf16(g->stream, g->wlm, g->wlm_p, g->vocab, D);
         for (int l = 0; l < g->layers && rc == 0; l++) {
             LayerW& L = g->L[l];
-            L.wqkv_p = reinterpret_cast<uint16_t*>(g->pblob + plm + (size_t)l * (pq + p1));
-            L.w1_p = reinterpret_cast<uint16_t*>(g->pblob + plm + (size_t)l * (pq + p1) + pq);
+            char* base = g->pblob + plm + (size_t)l * per_layer;
+            L.wqkv_p = reinterpret_cast<uint16_t*>(base);
+            L.w1_p = reinterpret_cast<uint16_t*>(base + pq);
+            L.wo_p = reinterpret_cast<uint16_t*>(base + pq + p1);
+            L.w2_p = reinterpret_cast<uint16_t*>(base + pq + p1 + po);
             rc = launch_pack_bf16(g->stream, L.wqkv, L.wqkv_p, 3 * D, D);
             if (rc == 0) rc = launch_pack_bf16(g->stream, L.w1, L.w1_p, 4 * D, D);
+            if (rc == 0) rc = launch_pack_bf16(g->stream, L.wo, L.wo_p, D, D);
+            if (rc == 0) rc = launch_pack_bf16(g->stream, L.w2, L.w2_p, D, 4 * D);
         }
         if (rc != 0 || check(hipStreamSynchronize(g->stream), "pack weights")) {
             gorch_hip_gpt_free(g);

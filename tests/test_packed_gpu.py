@@ -58,7 +58,8 @@ def run_packed(hip, x, W, b=None, residual=None, epilogue=0):
     return host(y)
 
 
-@pytest.mark.parametrize("K,N", [(768, 3072), (768, 50257), (1600, 4800), (1600, 6400), (768, 2304)])
+@pytest.mark.parametrize("K,N", [(768, 3072), (768, 50257), (1600, 4800), (1600, 6400), (768, 2304),
+                                 (3072, 768), (6400, 1600), (1600, 1600)])
 @pytest.mark.parametrize("M", [1, 4, 16])
 def test_packed_decode_shapes(gpu, M, K, N):
     x, W, b = syn.gemv_inputs(M, K, N, seed=M * 11 + K + N)
@@ -95,13 +96,25 @@ def test_packed_epilogues_and_determinism(gpu):
         assert np.array_equal(a, run_packed(gpu, x, W, b))
 
 
+@pytest.mark.parametrize("M,N,K", [(2, 16, 4096), (16, 100, 12288), (1, 40, 1024), (5, 2020, 3080)])
+def test_packed_k_split(gpu, M, N, K):
+    # narrow weights over a long K: K split across blocks, ordered epilogue
+    rng = np.random.default_rng(N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    W = syn.bf16_normal(rng, (N, K))
+    b = rng.standard_normal(N).astype(np.float32)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    got = run_packed(gpu, x, W, b, residual=res)
+    assert rel_err(got, orc.add(res, orc.linear(x, W, b))) <= 1e-3
+
+
 def test_packed_rejects(gpu):
-    W = torch.zeros((16, 4096), dtype=torch.int16, device="cuda")
+    W = torch.zeros((2048, 4096), dtype=torch.int16, device="cuda")
     Wp = gpu.pack_bf16(W)
     x = torch.zeros((2, 4096), device="cuda")
-    y = torch.zeros((2, 16), device="cuda")
-    with pytest.raises(gpu.HipError):   # K above 3072
-        gpu.linear_bf16_packed(x, Wp, 16, None, y)
+    y = torch.zeros((2, 2048), device="cuda")
+    with pytest.raises(gpu.HipError):   # K above 3072 over a wide weight
+        gpu.linear_bf16_packed(x, Wp, 2048, None, y)
     x17 = torch.zeros((17, 32), device="cuda")
     Wp2 = gpu.pack_bf16(torch.zeros((16, 32), dtype=torch.int16, device="cuda"))
     with pytest.raises(gpu.HipError):   # M above 16
