@@ -188,3 +188,19 @@ def test_generate_batch_wide_model(gpu):
         ref, _, _ = o.generate_cached(prompts[b], 5)
         assert list(ids[b]) == list(ref)
     g.close()
+
+
+def test_generate_long_cache(gpu):
+    """Batched decode with a cache of 300 positions (the long-cache attention
+    kernel); greedy tokens identical to the oracle, logits of the first step
+    within 1e-3."""
+    cfg = dict(vocab=64, dim=64, heads=4, layers=2, max_seq=300)
+    w = syn.gpt2_weights(cfg, seed=44, random_affine=True)
+    g, o = gpu.GPT(w), orc.GPT(w)
+    prompts = np.stack([syn.prompt_ids(270, cfg["vocab"], seed=80 + b) for b in range(3)])
+    ids, logits, _ = g.generate_cached(prompts, 12, want_logits=True)
+    for b in range(3):
+        ref, ref_logits, _ = o.generate_cached(prompts[b], 12, want_logits=True)
+        assert list(ids[b]) == list(ref)
+        assert rel_err(logits[0][b], ref_logits[0]) <= 1e-3
+    g.close()
