@@ -765,7 +765,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
 // residual, output, argmax keys). Every load is a raw buffer load with no
 // branch around it: k past the wave's range, rows past M or N and tiles
 // past the last read as zeros.
-template <int NW, int KS, bool PACKED, bool EARLY>
+template <int NW, int KS, bool PACKED, bool EARLY, bool LN>
 __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict__ x, const uint16_t* __restrict__ W,
                                                         const float* __restrict__ bias, const float* residual,
                                                         OutDesc od, int M, int N, int K, int ks, int epilogue,
@@ -793,6 +793,22 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
         const int off = (r < M && kc < ke) ? (int)((r * xs + kc) * 4) : kOutOfRange;
         xa[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rsx, off, 0, 0);
         xa[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rsx, off + 16, 0, 0);
+    }
+    // LayerNorm gamma/beta fragments (nn/layernorm.go:31-91), loaded with the
+    // activations
+    u32x4 ga[LN ? KS : 1][2], be[LN ? KS : 1][2];
+    if constexpr (LN) {
+        const __amdgpu_buffer_rsrc_t rg = make_rsrc(ex.ln_g, (long long)K * 4);
+        const __amdgpu_buffer_rsrc_t rbe = make_rsrc(ex.ln_b, (long long)K * 4);
+#pragma unroll
+        for (int u = 0; u < KS; u++) {
+            const int kc = kb + 32 * u + 8 * g;
+            const int off = kc < ke ? kc * 4 : kOutOfRange;
+            ga[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0);
+            ga[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rg, off + 16, 0, 0);
+            be[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rbe, off, 0, 0);
+            be[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rbe, off + 16, 0, 0);
+        }
     }
     const __amdgpu_buffer_rsrc_t rsr = make_rsrc(residual, residual ? (long long)M * N * 4 : 0);
     // Tile epilogue split over the waves: wave w finishes outputs o = w *
@@ -834,12 +850,60 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
     load(t, ta);
     load(t + G, tb);
 
+    // Fused LayerNorm: the block holds each activation row exactly once (row
+    // r in the lanes r, r+16, r+32, r+48 of every wave, each over its K
+    // slice), so the row's f64 sums come from registers: per-lane sums, then
+    // LDS across lane groups and waves; mean = s1/K, var = s2/K - mean^2
+    // (the reference's two-pass values to f64 rounding for activations whose
+    // mean is not many orders above their spread).
+    float ln_mean = 0.f, ln_inv = 1.f;
+    if constexpr (LN) {
+        __shared__ double2 s_mom[NW][64];
+        __shared__ float s_stat[16][2];
+        double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+        for (int u = 0; u < KS; u++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const double v = (double)__uint_as_float(xa[u][e >> 2][e & 3]);
+                s1 += v;
+                s2 += v * v;
+            }
+        s_mom[wave][lane] = make_double2(s1, s2);
+        __syncthreads();
+        if (threadIdx.x < 16 && (int)threadIdx.x < M) {
+            double t1 = 0.0, t2 = 0.0;
+            for (int w = 0; w < NW; w++)
+                for (int gg = 0; gg < 4; gg++) {
+                    const double2 q = s_mom[w][16 * gg + threadIdx.x];
+                    t1 += q.x;
+                    t2 += q.y;
+                }
+            const double mean = t1 / (double)K;
+            const double var = fmax(t2 / (double)K - mean * mean, 0.0);
+            s_stat[threadIdx.x][0] = (float)mean;
+            s_stat[threadIdx.x][1] = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
+        }
+        __syncthreads();
+        ln_mean = s_stat[r][0];
+        ln_inv = s_stat[r][1];
+    }
     bf16x8 ah[KS], al[KS];
 #pragma unroll
     for (int u = 0; u < KS; u++) {
         float f[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) f[e] = __uint_as_float(xa[u][e >> 2][e & 3]);
+        if constexpr (LN) {
+            // k past the range: the normalised zero is masked
+            const bool ok = kb + 32 * u + 8 * g < ke && r < M;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float normalized = (f[e] - ln_mean) * ln_inv;
+                f[e] = ok ? normalized * __uint_as_float(ga[u][e >> 2][e & 3]) + __uint_as_float(be[u][e >> 2][e & 3])
+                          : 0.f;
+            }
+        }
         split_hi_lo(f, ah[u], al[u]);
     }
     const int posv = od.pos_dev ? *od.pos_dev : 0;
@@ -1077,12 +1141,28 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
         return blocks_env ? blocks_env : per_cu * cus;
     };
 #define GH_TILES_L(NWV, KSV, PK, EA)                                                                    \
-    hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, PK, EA>), dim3(blocks, S), dim3(NWV * 64), 0, s, x, W, bias, \
-                       residual, od, M, N, K, ks, epilogue, ex)
+    hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, PK, EA, false>), dim3(blocks, S), dim3(NWV * 64), 0, s, x, W, \
+                       bias, residual, od, M, N, K, ks, epilogue, ex)
+    // fused LayerNorm: packed weights, 8 waves, K <= 1024 (the LM head of a
+    // one-row decode step)
+    if (ex.ln_g) {
+        if (!packed || nw != 8 || ks > 4 || S != 1) return -1;
+        static const int blocks_ln =
+            blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<8, 4, true, false, true>), 512);
+        const int blocks = std::min(blocks_ln, ntiles);
+        if (ntiles <= 2 * blocks)
+            hipLaunchKernelGGL((k_gemv_tiles<8, 4, true, true, true>), dim3(blocks), dim3(512), 0, s, x, W, bias,
+                               residual, od, M, N, K, ks, epilogue, ex);
+        else
+            hipLaunchKernelGGL((k_gemv_tiles<8, 4, true, false, true>), dim3(blocks), dim3(512), 0, s, x, W, bias,
+                               residual, od, M, N, K, ks, epilogue, ex);
+        count(CNT_GEMV);
+        return check_launch("gemv_tiles_ln");
+    }
 #define GH_TILES(NWV, KSV)                                                                                \
     if (nw == NWV && ks <= KSV) {                                                                         \
-        static const int blocks_p = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, true, false>), NWV * 64); \
-        static const int blocks_r = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, false, false>), NWV * 64); \
+        static const int blocks_p = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, true, false, false>), NWV * 64); \
+        static const int blocks_r = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, false, false, false>), NWV * 64); \
         const int blocks = std::min(std::max(1, (packed ? blocks_p : blocks_r) / S), ntiles);             \
         const bool early = ntiles <= 2 * blocks;                                                          \
         if (packed && early) GH_TILES_L(NWV, KSV, true, true);                                            \
@@ -1367,8 +1447,8 @@ int packed_split_slices(int K, int N) {
 int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, const float* bias,
                             const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
                             const LinearExtras& ex) {
-    if (M < 1 || M > 16 || ex.ln_g || (ex.part && ex.argmax_key)) {
-        set_error("linear_bf16_packed: needs 1 <= M <= 16, no fused LayerNorm, no argmax with a K split");
+    if (M < 1 || M > 16 || (ex.part && (ex.argmax_key || ex.ln_g)) || (ex.ln_g && ex.ln_stats)) {
+        set_error("linear_bf16_packed: needs 1 <= M <= 16, no argmax or LayerNorm with a K split");
         return GORCH_HIP_EUNSUPPORTED;
     }
     if (ex.part) {
@@ -1385,7 +1465,7 @@ int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, c
     // into the stream's scratch, then the ordered epilogue kernel (a CU
     // streams ~25 GB/s, so 48..127 tiles alone leave most of the chip idle)
     const int ntiles = (N + 15) / 16;
-    if (!ex.argmax_key && ntiles < 128 && K >= 1024) {
+    if (!ex.argmax_key && !ex.ln_g && ntiles < 128 && K >= 1024) {
         const int S = packed_split_slices(K, N);
         void* part = S >= 2 ? stream_scratch(s, (size_t)S * M * N * sizeof(float)) : nullptr;
         if (part) {
@@ -1403,7 +1483,8 @@ int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, c
     }
     const int rc = launch_tiles(s, x, Wp, bias, residual, od, M, N, K, epilogue, ex, true);
     if (rc < 0) {
-        set_error("linear_bf16_packed: K above 3072 is not supported");
+        set_error(ex.ln_g ? "linear_bf16_packed: a fused LayerNorm needs K <= 1024"
+                          : "linear_bf16_packed: K above 3072 is not supported");
         return GORCH_HIP_EUNSUPPORTED;
     }
     return rc;

@@ -282,7 +282,17 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         lf.ln_eps = eps;
         lf.x_stride = head_stride;
         lf.argmax_key = all_rows ? nullptr : argmax_key;
-        if (head_rows == 1 && g->vocab >= 16384) {
+        static const bool head_tiles = [] {
+            const char* e = getenv("GORCH_HIP_HEAD_TILES");
+            return e ? atoi(e) != 0 : true;
+        }();
+        if (g->wlm_p && head_tiles && d <= 1024) {
+            // tile-packed head with LayerNorm_f fused: each block normalises
+            // the rows it holds in registers, so no separate LayerNorm launch
+            GH_TRY(launch_linear_packed_od(s, head_in, g->wlm_p, g->blm, nullptr,
+                                           OutDesc::plain(g->logits, g->vocab), head_rows, g->vocab, d,
+                                           GORCH_HIP_EPI_NONE, lf));
+        } else if (head_rows == 1 && g->vocab >= 16384) {
             // one row, many weight rows: one small kernel writes the
             // normalised row and the register GEMV streams the head over it
             // plainly (fused into the GEMV, the LayerNorm's registers halve
