@@ -187,6 +187,39 @@ struct OutDesc {
         if (up) r += pos;
         return p + seq * ss + (long long)r * rs + (n - nb);
     }
+    // at_p split for a writer of many rows per column: col() resolves the
+    // segment of column n once, row() adds the row part (same addresses)
+    struct Col {
+        float* p;
+        long long ss, rs;
+        int radd;
+    };
+    __device__ __forceinline__ Col col(int n, int pos) const {
+        if (nseg == 1) return Col{ptr[0] + n, seq_stride[0], row_stride[0], use_pos[0] ? pos : 0};
+        const bool s1 = n >= __builtin_amdgcn_readfirstlane(n_end[0]);
+        const bool s2 = nseg > 2 && n >= __builtin_amdgcn_readfirstlane(n_end[1]);
+        const long long d1 = uni((long long)(ptr[1] - ptr[0])), d2 = uni((long long)(ptr[2] - ptr[0]));
+        const long long ss0 = uni(seq_stride[0]), ss1 = uni(seq_stride[1]), ss2 = uni(seq_stride[2]);
+        const long long rs0 = uni(row_stride[0]), rs1 = uni(row_stride[1]), rs2 = uni(row_stride[2]);
+        const int up0 = __builtin_amdgcn_readfirstlane(use_pos[0]), up1 = __builtin_amdgcn_readfirstlane(use_pos[1]),
+                  up2 = __builtin_amdgcn_readfirstlane(use_pos[2]);
+        const int ne0 = __builtin_amdgcn_readfirstlane(n_end[0]), ne1 = __builtin_amdgcn_readfirstlane(n_end[1]);
+        const int nb = s2 ? ne1 : (s1 ? ne0 : 0);
+        Col c;
+        c.p = ptr[0] + (s2 ? d2 : (s1 ? d1 : 0)) + (n - nb);
+        c.ss = s2 ? ss2 : (s1 ? ss1 : ss0);
+        c.rs = s2 ? rs2 : (s1 ? rs1 : rs0);
+        c.radd = (s2 ? up2 : (s1 ? up1 : up0)) ? pos : 0;
+        return c;
+    }
+    __device__ __forceinline__ float* row(const Col& c, int m) const {
+        int seq = 0, r = m;
+        if (rows_per_seq < (1 << 30)) {
+            seq = m / rows_per_seq;
+            r = m - seq * rows_per_seq;
+        }
+        return c.p + seq * c.ss + (long long)(r + c.radd) * c.rs;
+    }
 };
 
 // Arguments of the cached-attention kernel (attention.hip).

@@ -24,7 +24,7 @@ namespace gh {
 constexpr int kBK = 64;
 constexpr int kLDA = kBK + 16;  // bf16 elements per LDS row (160 bytes: conflict-free 16-byte fragment reads)
 
-template <int BM, int BN, bool SPLIT, int PF>
+template <int BM, int BN, bool SPLIT, int PF, bool KT>
 __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A, const uint16_t* __restrict__ W,
                                                     const float* __restrict__ bias, const float* residual,
                                                     OutDesc od, int M, int N, int K, int epilogue) {
@@ -56,14 +56,14 @@ __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A,
         for (int i = 0; i < A_F4; i++) {
             const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
             const int k = k0 + 4 * c4;
-            const int off = k < K ? (min(row, mrows - 1) * K + k) * 4 : kOutOfRange;
+            const int off = (!KT || k < K) ? (min(row, mrows - 1) * K + k) * 4 : kOutOfRange;
             a[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsa, off, 0, 0));
         }
 #pragma unroll
         for (int i = 0; i < W_U4; i++) {
             const int idx = tid + 256 * i, row = idx >> 3, c8 = idx & 7;
             const int k = k0 + 8 * c8;
-            const int off = k < K ? (min(row, ncols - 1) * K + k) * 2 : kOutOfRange;
+            const int off = (!KT || k < K) ? (min(row, ncols - 1) * K + k) * 2 : kOutOfRange;
             wv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, off, 0, 0));
         }
     };
@@ -115,8 +115,14 @@ __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A,
     // zeros) so the loop body has no branch around its loads
     const int nk = (K + kBK - 1) / kBK;
     const int nkp = (nk + PF - 1) / PF * PF;
+    // issue the stages in order: the loop waits for stage s while later
+    // stages stay in flight (memory counters complete in issue order), and
+    // the scheduler would otherwise interleave the prologue's loads
 #pragma unroll
-    for (int s = 0; s < PF; s++) gload(s * kBK, ra[s], rw[s]);
+    for (int s = 0; s < PF; s++) {
+        gload(s * kBK, ra[s], rw[s]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     for (int it0 = 0; it0 < nkp; it0 += PF) {
 #pragma unroll
         for (int s = 0; s < PF; s++) {
@@ -147,24 +153,52 @@ __global__ __launch_bounds__(256) void k_gemm_bf16w(const float* __restrict__ A,
         }
     }
 
+    // Epilogue. Stores and loads share one memory counter, so a loaded value
+    // first used after a store makes that use wait for the store's write
+    // too (and, past a branch, for every store before it): the position and
+    // the residual are loaded and every output value computed before the
+    // first store.
+    const int pos = __builtin_amdgcn_readfirstlane(od.pos_dev ? *od.pos_dev : 0);
+    float res[TM][TN][4];
+    if (residual) {
+        const __amdgpu_buffer_rsrc_t rsr = make_rsrc(residual + (size_t)m0 * N, (long long)mrows * N * 4);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int n = n0 + wn * WN + j * 16 + r;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int ml = wm * WM + i * 16 + 4 * g + v;
+                    const int off = (n < N && ml < mrows) ? (ml * N + n) * 4 : kOutOfRange;
+                    res[i][j][v] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsr, off, 0, 0));
+                }
+            }
+    }
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int n = n0 + wn * WN + j * 16 + r;
-            if (n >= N) continue;
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                float s = acc[i][j][v];
+                if (bias) s = s + bn[j];
+                if (epilogue == GORCH_HIP_EPI_GELU) s = gelu_tanh(s);
+                if (residual) s = res[i][j][v] + s;
+                acc[i][j][v] = s;
+            }
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int n = n0 + wn * WN + j * 16 + r;
+        const OutDesc::Col c = od.col(min(n, N - 1), pos);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int m = m0 + wm * WM + i * 16 + 4 * g + v;
-                if (m < M) {
-                    float s = acc[i][j][v];
-                    if (bias) s = s + bn[j];
-                    if (epilogue == GORCH_HIP_EPI_GELU) s = gelu_tanh(s);
-                    if (residual) s = residual[(size_t)m * N + n] + s;
-                    *od.at(m, n) = s;
-                }
+                if (m < M && n < N) *od.row(c, m) = acc[i][j][v];
             }
-        }
+    }
 }
 
 template <int BM, int BN, bool SPLIT>
@@ -178,15 +212,24 @@ static void launch_gemm_t(hipStream_t s, const float* A, const uint16_t* W, cons
     // measured: one register stage for 128 x 128 tiles (more stages cost
     // occupancy: 4096^3 247 vs 301 us), two for the smaller tiles
     const int pf = pf_env ? pf_env : (BM * BN >= 128 * 128 ? 1 : 2);
-    if (pf == 1)
-        hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT, 1>), grid, dim3(256), 0, s, A, W, bias, residual, od, M, N,
-                           K, epilogue);
-    else if (pf == 2)
-        hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT, 2>), grid, dim3(256), 0, s, A, W, bias, residual, od, M, N,
-                           K, epilogue);
-    else
-        hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT, 3>), grid, dim3(256), 0, s, A, W, bias, residual, od, M, N,
-                           K, epilogue);
+    // no K tail and a step count the stages divide: loads with no bound on k
+    // (a select on every offset compiles to branches around the loads)
+    const int nk = (K + kBK - 1) / kBK;
+    const bool kt = K % kBK != 0 || nk % pf != 0;
+#define GH_GEMM_L(PFV, KTV)                                                                                    \
+    hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT, PFV, KTV>), grid, dim3(256), 0, s, A, W, bias, residual, od, M, \
+                       N, K, epilogue)
+    if (pf == 1) {
+        if (kt) GH_GEMM_L(1, true);
+        else GH_GEMM_L(1, false);
+    } else if (pf == 2) {
+        if (kt) GH_GEMM_L(2, true);
+        else GH_GEMM_L(2, false);
+    } else {
+        if (kt) GH_GEMM_L(3, true);
+        else GH_GEMM_L(3, false);
+    }
+#undef GH_GEMM_L
 }
 
 // Tile choice: the largest tile that still gives every CU a block.

@@ -58,10 +58,15 @@ struct WideGemm {
 
     // a[p] + row * lda: row of plane p (nrows valid); w[b] + n * K: column n
     // of weight b (ncols valid). Sums k in [kb, ke) (a K slice; kb % 8 ==
-    // 0). epi(row, col, vals[NB]) per output.
-    template <class Epi>
+    // 0). Per valid output, xform(row, col, vals[NB]) finishes the values in
+    // place (it may load), then store(row, col, vals) writes them: every
+    // xform runs before the first store, since stores and loads share one
+    // memory counter and a load's use after a store would wait for the
+    // store's write.
+    template <class Xform, class Store>
     __device__ static void run(Smem& sm, const uint16_t* const* a, long long lda, int nrows,
-                               const uint16_t* const* w, int ncols, int K, int kb, int ke, Epi& epi) {
+                               const uint16_t* const* w, int ncols, int K, int kb, int ke, Xform& xform,
+                               Store& store) {
         const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
         const int wm = wave >> 2, wn = wave & 3;
         const int r = lane & 15, g = lane >> 4;
@@ -176,7 +181,23 @@ struct WideGemm {
                     float vals[NB];
 #pragma unroll
                     for (int b = 0; b < NB; b++) vals[b] = acc[b][i][j][v];
-                    if (row < nrows && col < ncols) epi(row, col, vals);
+                    if (row < nrows && col < ncols) xform(row, col, vals);
+#pragma unroll
+                    for (int b = 0; b < NB; b++) acc[b][i][j][v] = vals[b];
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int col = wn * WNW + j * 16 + r;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int row = wm * WM + i * 16 + 4 * g + v;
+                    float vals[NB];
+#pragma unroll
+                    for (int b = 0; b < NB; b++) vals[b] = acc[b][i][j][v];
+                    if (row < nrows && col < ncols) store(row, col, vals);
                 }
             }
     }

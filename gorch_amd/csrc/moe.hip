@@ -487,26 +487,31 @@ __global__ __launch_bounds__(512) void k_moe_wide(const uint16_t* __restrict__ A
     const int nsl = gridDim.z;
     const int kslice = (Kd + nsl * 64 - 1) / (nsl * 64) * 64;
     const int kb = blockIdx.z * kslice, ke = min(Kd, kb + kslice);
-    auto epi = [&](int row, int col, const float* v) {
-        const size_t o = (size_t)(r0 + row) * N + n0 + col;
-        if (!DUAL && nsl > 1) {
-            C[(size_t)blockIdx.z * cslice + o] = v[0];
-            return;
-        }
+    // xform: bias, SwiGLU or routing weight (the loads); store: the writes
+    auto xform = [&](int row, int col, float* v) {
+        if (!DUAL && nsl > 1) return;
         float s = v[0];
         if (bg) s = s + bg[col];
         if constexpr (DUAL) {
             float u = v[1];
             if (bu) u = u + bu[col];
-            s = s * sigmoidf_ref(s) * u;  // SwiGLU: gate * sigma(gate) * up
-            const uint32_t hb = __float_as_uint(s) & 0xffff0000u;
-            Chi[o] = (uint16_t)(hb >> 16);
-            Clo[o] = __builtin_bit_cast(uint16_t, (__bf16)(s - __uint_as_float(hb)));
+            v[0] = s * sigmoidf_ref(s) * u;  // SwiGLU: gate * sigma(gate) * up
         } else {
-            C[o] = s * ws.perm_w[r0 + row];  // weighted = exOut * w
+            v[0] = s * ws.perm_w[r0 + row];  // weighted = exOut * w
         }
     };
-    G::run(*reinterpret_cast<typename G::Smem*>(moe_smem), a, Kd, nrows, w, min(BNW, N - n0), Kd, kb, ke, epi);
+    auto store = [&](int row, int col, const float* v) {
+        const size_t o = (size_t)(r0 + row) * N + n0 + col;
+        if constexpr (DUAL) {
+            const uint32_t hb = __float_as_uint(v[0]) & 0xffff0000u;
+            Chi[o] = (uint16_t)(hb >> 16);
+            Clo[o] = __builtin_bit_cast(uint16_t, (__bf16)(v[0] - __uint_as_float(hb)));
+        } else {
+            C[(nsl > 1 ? (size_t)blockIdx.z * cslice : 0) + o] = v[0];
+        }
+    };
+    G::run(*reinterpret_cast<typename G::Smem*>(moe_smem), a, Kd, nrows, w, min(BNW, N - n0), Kd, kb, ke, xform,
+           store);
 }
 
 template <bool DUAL, int BNW>
