@@ -72,7 +72,7 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
                                                      int N, float eps, float2* __restrict__ stats,
                                                      const float* __restrict__ ln_g, const float* __restrict__ ln_b,
                                                      float* __restrict__ h) {
-    __shared__ double sh[4];
+    __shared__ double2 sh2[4];
     const int m = blockIdx.x;
     float* row = x + (size_t)m * N;
     // raw buffer loads, all issued before any add and with no branch around
@@ -90,6 +90,15 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
     auto ld = [](__amdgpu_buffer_rsrc_t r, int off) {
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
     };
+    // the moments' shift: column 0 of the updated row (its old value plus
+    // bias and slices), the same for every thread
+    const float x0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, 0, 0, 0));
+    const float b0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, 0, 0, 0));
+    float p0[kRedSlices];
+#pragma unroll
+    for (int q = 0; q < kRedSlices; q++)
+        p0[q] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(rp, q < S ? (int)((size_t)q * M * N * 4) : kOutOfRange, 0, 0));
 #pragma unroll
     for (int c = 0; c < kRedVec; c++) {
         const int j = 4 * (threadIdx.x + 256 * c);
@@ -102,7 +111,19 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
         for (int q = 0; q < kRedSlices; q++)
             p[c][q] = ld(rp, (j < N && q < S) ? (int)(((size_t)q * M * N + j) * 4) : kOutOfRange);
     }
-    double s1 = 0.0;
+    float shift = x0;
+    if (S > 0) {
+        float acc = p0[0];
+#pragma unroll
+        for (int q = 1; q < kRedSlices; q++)
+            if (q < S) acc += p0[q];
+        if (bias) acc = acc + b0;
+        shift = x0 + acc;
+    }
+    // shifted one-pass moments in f64 (one block reduction): mean = shift +
+    // s1 / N, var = s2 / N - (s1 / N)^2, the two-pass values to f64
+    // rounding for rows whose mean is not many orders above their spread
+    double s1 = 0.0, s2 = 0.0;
 #pragma unroll
     for (int c = 0; c < kRedVec; c++) {
         const int j = 4 * (threadIdx.x + 256 * c);
@@ -118,26 +139,34 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
                 if (bias) acc = acc + reinterpret_cast<const float*>(&bv[c])[e];
                 vc[e] = vc[e] + acc;
             }
-            *reinterpret_cast<float4*>(row + j) = v[c];
         }
 #pragma unroll
-        for (int e = 0; e < 4; e++) s1 += (double)vc[e];
-    }
-    if (!stats && !h) return;
-    const double mean = block_sum_d(s1, sh) / (double)N;
-    double s2 = 0.0;
-#pragma unroll
-    for (int c = 0; c < kRedVec; c++) {
-        const int j = 4 * (threadIdx.x + 256 * c);
-        if (j >= N) continue;
-        const float* vc = reinterpret_cast<const float*>(&v[c]);
-#pragma unroll
         for (int e = 0; e < 4; e++) {
-            const double d = (double)vc[e] - mean;
+            const double d = (double)vc[e] - (double)shift;
+            s1 += d;
             s2 += d * d;
         }
     }
-    const double var = block_sum_d(s2, sh) / (double)N;
+    if (stats || h) {
+        wave_sum2_d(s1, s2);
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        if (lane == 0) sh2[wave] = make_double2(s1, s2);
+        __syncthreads();
+        s1 = (sh2[0].x + sh2[1].x) + (sh2[2].x + sh2[3].x);
+        s2 = (sh2[0].y + sh2[1].y) + (sh2[2].y + sh2[3].y);
+    }
+    // the updated row's stores after every load has been used
+    if (S > 0) {
+#pragma unroll
+        for (int c = 0; c < kRedVec; c++) {
+            const int j = 4 * (threadIdx.x + 256 * c);
+            if (j < N) *reinterpret_cast<float4*>(row + j) = v[c];
+        }
+    }
+    if (!stats && !h) return;
+    const double d1 = s1 / (double)N;
+    const double mean = (double)shift + d1;
+    const double var = fmax(s2 / (double)N - d1 * d1, 0.0);
     const float fm = (float)mean, inv = (float)(1.0 / sqrt(var + (double)eps));
     if (stats && threadIdx.x == 0) stats[m] = make_float2(fm, inv);
     if (!h) return;
