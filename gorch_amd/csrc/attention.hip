@@ -150,6 +150,7 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     extern __shared__ float sc[];  // [visible keys]
     __shared__ float red[16];
     __shared__ float4 po[4][64];
+    __shared__ float pl[4][64];
     constexpr int KPI = 64 / HD4;  // keys per wavefront instruction
     constexpr int KB = 4 * KPI;    // keys per block instruction
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -200,6 +201,59 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
     if constexpr (FULL) {
         const int pos = load_pos();
         T = a.causal ? pos + i + 1 : pos + a.new_seq;
+        // one chunk covers the cache (T <= max_seq <= KB * UNR): the scores
+        // stay in registers, each key slot weights its values by p = exp(s -
+        // max), and the slots' weighted sums and weight sums meet in LDS once
+        // (sum_j p_j v_j / sum_j p_j: the softmax-weighted sum, divided last)
+        float sj[UNR];
+        float smax = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            float d = q.x * kv[u].x + q.y * kv[u].y + q.z * kv[u].z + q.w * kv[u].w;
+            sj[u] = seg_sum<HD4>(d) * a.scale;
+            if (KB * u + slot < T) smax = fmaxf(smax, sj[u]);
+        }
+        const float mx = block_max(smax, red);
+        float l = 0.f;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            // keys past T: cache rows not written yet, never multiplied
+            if (KB * u + slot < T) {
+                const float p = expf(sj[u] - mx);
+                l += p;
+                o.x += p * vpre[u].x;
+                o.y += p * vpre[u].y;
+                o.z += p * vpre[u].z;
+                o.w += p * vpre[u].w;
+            }
+        }
+        po[wave][lane] = o;
+        pl[wave][lane] = l;
+        __syncthreads();
+        if (threadIdx.x < HD4) {
+            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+            float L = 0.f;
+#pragma unroll
+            for (int w = 0; w < 4; w++)
+#pragma unroll
+                for (int sl = 0; sl < KPI; sl++) {
+                    const float4 pv = po[w][sl * HD4 + c];
+                    t.x += pv.x;
+                    t.y += pv.y;
+                    t.z += pv.z;
+                    t.w += pv.w;
+                    L += pl[w][sl * HD4 + c];
+                }
+            if (a.recip) {
+                const float rs = 1.0f / L;
+                t = make_float4(t.x * rs, t.y * rs, t.z * rs, t.w * rs);
+            } else {
+                t = make_float4(t.x / L, t.y / L, t.z / L, t.w / L);
+            }
+            *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + h * (4 * HD4) + 4 * c) = t;
+        }
+        return;
     }
 
     float lmax = -INFINITY;
