@@ -83,7 +83,9 @@ def test_activations(gpu):
 
 @pytest.mark.parametrize("batch,new_seq,pos,heads,hd", [(1, 1, 0, 12, 64), (1, 1, 95, 12, 64),
                                                         (2, 5, 40, 12, 64), (3, 1, 767, 25, 64),
-                                                        (1, 32, 0, 12, 64), (2, 3, 9, 4, 80)])
+                                                        (1, 32, 0, 12, 64), (2, 3, 9, 4, 80),
+                                                        (2, 5, 300, 4, 128), (1, 3, 700, 2, 128),
+                                                        (64, 1, 400, 20, 64), (2, 1, 1300, 3, 64)])
 def test_attention_cached(gpu, batch, new_seq, pos, heads, hd):
     rng = np.random.default_rng(pos + heads)
     d = heads * hd
@@ -134,6 +136,21 @@ def test_attention_noncausal(gpu):
     out = torch.empty((n, d), device="cuda")
     gpu.attention_cached(dev(q), dev(kc), dev(vc), out, 1, n, pos, heads, hd, pos + n, causal=False)
     ref = orc.attention_cached(q, kc[0], vc[0], pos, heads, causal=False)
+    assert np.max(np.abs(host(out) - ref)) < 1e-5
+
+
+def test_attention_noncausal_long(gpu):
+    # a long cache (the online-softmax kernel) without the causal mask: every
+    # new row sees all pos + n keys
+    rng = np.random.default_rng(11)
+    heads, hd, pos, n = 3, 64, 500, 4
+    d = heads * hd
+    q = rng.standard_normal((n, d)).astype(np.float32)
+    kc = rng.standard_normal((1, pos + n + 2, d)).astype(np.float32)
+    vc = rng.standard_normal((1, pos + n + 2, d)).astype(np.float32)
+    out = torch.empty((n, d), device="cuda")
+    gpu.attention_cached(dev(q), dev(kc), dev(vc), out, 1, n, pos, heads, hd, pos + n + 2, causal=False)
+    ref = orc.attention_cached(q, kc[0, :pos + n], vc[0, :pos + n], pos, heads, causal=False)
     assert np.max(np.abs(host(out) - ref)) < 1e-5
 
 
