@@ -49,7 +49,7 @@ def parse():
                     help="restrict to one shape 'M,K,N' (for profiling one kernel)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the GPT decode legs")
-    ap.add_argument("--only", choices=("decode", "gemm", "decode-xl", "moe"), default=None,
+    ap.add_argument("--only", choices=("decode", "gemm", "decode-xl", "moe", "decode-qwen"), default=None,
                     help="run only one secondary leg and print its JSON (for profiling)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -285,6 +285,68 @@ def moe_leg():
             "TFLOPs": round(flops / us / 1e6, 1), "frac_mfma_peak": round(flops / us / 1e6 / MFMA_PEAK_TFLOPS, 4)}
 
 
+def qwen_leg(ctxs=(128, 512), steps=100):
+    """Qwen3-0.6B-shaped cached decode (the reference's BenchmarkQwenDecode,
+    model/qwen/bench_test.go:21-43): 28 layers, d 1024, 16 query / 8 KV heads
+    of 128, SwiGLU 3072, vocab 151936 tied head; random bf16 weights N(0,0.02)
+    generated on the device. The cache is prefilled to ctx tokens, then one
+    graph-captured single-token step at position ctx is replayed (it rewrites
+    the same cache row, as the reference trims the cache back each step)."""
+    import dataclasses
+
+    import torch
+
+    from gorch_amd import hip
+    from gorch_amd.qwen import QWEN3_0_6B, Qwen
+
+    cfg = dataclasses.replace(QWEN3_0_6B, max_seq=max(ctxs) + 8)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+
+    def bf16(shape):
+        f = torch.randn(shape, device="cuda", generator=gen) * 0.02
+        out = torch.empty(shape, dtype=torch.int16, device="cuda")
+        hip.f32_to_bf16(f, out)
+        return out
+
+    def gain(n):
+        return 1 + 0.1 * torch.randn(n, device="cuda", generator=gen)
+
+    q, kv, d = cfg.num_q * cfg.head_dim, cfg.kv_dim, cfg.hidden
+    w = {"embed": bf16((cfg.vocab, d)), "norm": gain(d), "layers": [
+        {"wq": bf16((q, d)), "wk": bf16((kv, d)), "wv": bf16((kv, d)), "wo": bf16((d, q)),
+         "q_norm": gain(cfg.head_dim), "k_norm": gain(cfg.head_dim), "norm_attn": gain(d), "norm_ffn": gain(d),
+         "wgate": bf16((cfg.inter, d)), "wup": bf16((cfg.inter, d)), "wdown": bf16((d, cfg.inter))}
+        for _ in range(cfg.layers)]}
+    m = Qwen(cfg, w)
+    stream = torch.cuda.current_stream()
+    out = []
+    for ctx in ctxs:
+        cache = m.new_cache(ctx + 1)
+        ids = torch.randint(0, cfg.vocab, (ctx,), dtype=torch.int32, device="cuda", generator=gen)
+        m.forward_cached(ids, cache, 0)
+        tok = ids[:1].clone()
+        m.forward_cached(tok, cache, ctx)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            m.forward_cached(tok, cache, ctx)
+        for _ in range(5):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        out.append({"model": "qwen3-0.6b-shaped", "batch": 1, "ctx": ctx, "tok_s": round(1e3 / ms, 1),
+                    "ms_per_token": round(ms, 4), "weights": "bf16 N(0,0.02) random init on the device"})
+        del g, cache
+    return out
+
+
 def decode_leg(cfg_name, batch, n_prompt, max_new, reps=3):
     """Greedy KV-cache decode through the engine (graph-replayed step).
     tok/s = batch * decode forwards / decode wall time (prefill timed apart)."""
@@ -355,6 +417,8 @@ def main():
             print(json.dumps(decode_leg("gpt2-xl", 16, 512, 256, reps=1)))
         elif args.only == "moe":
             print(json.dumps(moe_leg()))
+        elif args.only == "decode-qwen":
+            print(json.dumps(qwen_leg()))
         else:
             print(json.dumps(gemm_leg()))
         return
@@ -375,6 +439,7 @@ def main():
                                                          decode_leg("gpt2-xl", 16, 512, 256, reps=1)]
     gemm = [] if args.shape else gemm_leg()
     moe = None if args.shape else moe_leg()
+    qwen = [] if (args.shape or args.no_decode) else qwen_leg()
     cpu = None if args.no_cpu else cpu_leg(shapes, args.cpu_seconds)
     dom_bytes = algo_bytes(dom["M"], dom["K"], dom["N"])
     dom_kernel = gemv_kernel(dom["M"], dom["K"], dom["N"])
@@ -416,6 +481,7 @@ def main():
         "decode": decode,
         "prefill_gemm": gemm,
         "moe_layer": moe,
+        "decode_qwen": qwen,
     }
     print(json.dumps(out))
 

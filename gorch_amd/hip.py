@@ -548,8 +548,8 @@ class GQA:
         import torch
 
         def up(a):
-            if a is None:
-                return None
+            if a is None or isinstance(a, torch.Tensor):
+                return a
             a = np.ascontiguousarray(a)
             return torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).cuda()
 

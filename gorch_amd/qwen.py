@@ -1,0 +1,114 @@
+"""Qwen3-style decoder on the GPU: gorch's model/qwen (qwen.go:12-98,
+block.go:27-79) — tokens -> embedding -> L x [x1 = x + GQA(RMSNorm(x)); x =
+x1 + SwiGLU-MLP(RMSNorm(x1))] -> RMSNorm -> tied LM head — composed from the
+library's kernels through its C-ABI (gorch_amd.hip): the GQA layer
+(gorch_hip_gqa_forward_cached: Q/K/V Linears, per-head q/k RMSNorm, RoPE at
+absolute positions into the cache, grouped-query cached attention, Wo), RMSNorm,
+the bf16-weight Linears (M = 1 decode GEMV, M > 16 MFMA GEMM), SwiGLU, the
+embedding gather and the residual adds. Every launch goes on torch's current
+stream, so a decode step can be captured in a CUDA graph and replayed.
+
+Weights are host arrays as gorch_amd.synthetic.qwen_weights builds them, or
+device tensors of the same layout (bf16 as int16): bf16 Linear weights [out,
+in], f32 RMSNorm gains, a bf16 embedding table (looked up widened to f32; the tied LM head reads the bf16 table, as
+MatMulTransB(last, Embed.Weight) does for a bf16 checkpoint, qwen.go:84).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import hip
+
+
+@dataclass(frozen=True)
+class QwenConfig:
+    """model/qwen/config.go:13-27 (the fields this decoder uses)."""
+    hidden: int
+    layers: int
+    num_q: int
+    num_kv: int
+    head_dim: int
+    inter: int
+    vocab: int
+    rope_theta: float = 1_000_000.0
+    eps: float = 1e-6
+    max_seq: int = 4096
+
+    @property
+    def kv_dim(self) -> int:
+        return self.num_kv * self.head_dim
+
+
+# model/qwen/config.go:40-55 (Qwen3-0.6B)
+QWEN3_0_6B = QwenConfig(hidden=1024, layers=28, num_q=16, num_kv=8, head_dim=128, inter=3072, vocab=151936)
+
+
+class Qwen:
+    """model/qwen Model.ForwardCached (qwen.go:69-89) on the GPU."""
+
+    def __init__(self, cfg: QwenConfig, w: dict):
+        import torch
+
+        def up(a):
+            a = np.ascontiguousarray(a)
+            return torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).cuda()
+
+        self.cfg = cfg
+        self.embed_bf16 = w["embed"] if isinstance(w["embed"], torch.Tensor) else up(w["embed"])
+        self.embed = torch.empty((cfg.vocab, cfg.hidden), dtype=torch.float32, device="cuda")
+        hip.bf16_to_f32(self.embed_bf16, self.embed)
+        self.norm = w["norm"] if isinstance(w["norm"], torch.Tensor) else up(w["norm"])
+        self.layers = []
+        for lw in w["layers"]:
+            gw = {"dim": cfg.hidden, "num_q": cfg.num_q, "num_kv": cfg.num_kv, "head_dim": cfg.head_dim,
+                  "causal": True, "norm_eps": cfg.eps, "wq": lw["wq"], "wk": lw["wk"], "wv": lw["wv"],
+                  "wo": lw["wo"], "q_norm": lw["q_norm"], "k_norm": lw["k_norm"], "rope": True,
+                  "rope_base": cfg.rope_theta, "rope_max_seq": cfg.max_seq}
+            layer = {"attn": hip.GQA(gw)}
+            for n in ("norm_attn", "norm_ffn", "wgate", "wup", "wdown"):
+                layer[n] = lw[n] if isinstance(lw[n], torch.Tensor) else up(lw[n])
+            self.layers.append(layer)
+
+    def new_cache(self, capacity: int):
+        """Per-layer K and V rows [capacity, kv_dim] f32 (nn/kvcache.go:14-60)."""
+        import torch
+
+        if capacity > self.cfg.max_seq:
+            raise ValueError("qwen: cache capacity above the RoPE table length")
+        return [(torch.zeros((capacity, self.cfg.kv_dim), device="cuda"),
+                 torch.zeros((capacity, self.cfg.kv_dim), device="cuda")) for _ in self.layers]
+
+    def forward_cached(self, ids, cache, pos: int):
+        """Logits [1, vocab] of the last of ``ids`` (int32 device tensor),
+        whose rows take cache positions pos .. pos + len(ids) - 1."""
+        import torch
+
+        cfg = self.cfg
+        S = ids.numel()
+        if S == 0:
+            raise ValueError("qwen: empty token slice")
+        if pos + S > cache[0][0].shape[0]:
+            raise ValueError("qwen: cache capacity exceeded")
+        d = cfg.hidden
+        x = torch.empty((S, d), device="cuda")
+        hip.embedding(self.embed, ids, x)
+        h = torch.empty((S, d), device="cuda")
+        x1 = torch.empty((S, d), device="cuda")
+        gate = torch.empty((S, cfg.inter), device="cuda")
+        upv = torch.empty((S, cfg.inter), device="cuda")
+        for layer, (kc, vc) in zip(self.layers, cache):
+            hip.rmsnorm(x, layer["norm_attn"], h, cfg.eps)
+            a = layer["attn"].forward_cached(h, kc, vc, pos)
+            hip.add(x, a, x1)
+            hip.rmsnorm(x1, layer["norm_ffn"], h, cfg.eps)
+            hip.linear_bf16(h, layer["wgate"], None, gate)
+            hip.linear_bf16(h, layer["wup"], None, upv)
+            hip.swiglu(gate, upv, gate)
+            hip.linear_bf16(gate, layer["wdown"], None, x, residual=x1)
+        last = torch.empty((1, d), device="cuda")
+        hip.rmsnorm(x[S - 1:S], self.norm, last, cfg.eps)
+        logits = torch.empty((1, cfg.vocab), device="cuda")
+        hip.linear_bf16(last, self.embed_bf16, None, logits)
+        return logits

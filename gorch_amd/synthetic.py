@@ -120,3 +120,24 @@ def gqa_weights(dim=64, num_q=8, num_kv=2, head_dim=16, max_seq=64, seed=0, bias
     w["rope_base"] = base
     w["rope_max_seq"] = max_seq
     return w
+
+
+def qwen_weights(cfg, seed: int = 0) -> dict:
+    """Random weights for gorch_amd.qwen.Qwen (model/qwen/qwen.go:28-48,
+    block.go:27-55): bf16 Linear weights N(0, 0.02) [out, in], a bf16
+    embedding table, RMSNorm and q/k-norm gains 1 + N(0, 0.1)."""
+    rng = np.random.default_rng(seed)
+    q, kv, d = cfg.num_q * cfg.head_dim, cfg.kv_dim, cfg.hidden
+
+    def gain(n):
+        return (1 + normal(rng, (n,), 0.1)).astype(np.float32)
+
+    layers = []
+    for _ in range(cfg.layers):
+        layers.append({"wq": bf16_normal(rng, (q, d)), "wk": bf16_normal(rng, (kv, d)),
+                       "wv": bf16_normal(rng, (kv, d)), "wo": bf16_normal(rng, (d, q)),
+                       "q_norm": gain(cfg.head_dim), "k_norm": gain(cfg.head_dim),
+                       "norm_attn": gain(d), "norm_ffn": gain(d),
+                       "wgate": bf16_normal(rng, (cfg.inter, d)), "wup": bf16_normal(rng, (cfg.inter, d)),
+                       "wdown": bf16_normal(rng, (d, cfg.inter))})
+    return {"embed": bf16_normal(rng, (cfg.vocab, d)), "norm": gain(d), "layers": layers}
