@@ -69,6 +69,10 @@ class Qwen:
             layer = {"attn": hip.GQA(gw)}
             for n in ("norm_attn", "norm_ffn", "wgate", "wup", "wdown"):
                 layer[n] = lw[n] if isinstance(lw[n], torch.Tensor) else up(lw[n])
+            # gate and up rows in one weight: a one-row step reads both in
+            # one GEMV launch (its output row is [gate | up]); longer inputs
+            # use the two halves, which are contiguous row ranges of it
+            layer["wgu"] = torch.cat([layer.pop("wgate"), layer.pop("wup")], 0)
             self.layers.append(layer)
 
     def new_cache(self, capacity: int):
@@ -96,17 +100,23 @@ class Qwen:
         hip.embedding(self.embed, ids, x)
         h = torch.empty((S, d), device="cuda")
         x1 = torch.empty((S, d), device="cuda")
-        gate = torch.empty((S, cfg.inter), device="cuda")
-        upv = torch.empty((S, cfg.inter), device="cuda")
+        F = cfg.inter
+        gu = torch.empty((S, 2 * F), device="cuda")
+        gate, upv = (gu[0, :F], gu[0, F:]) if S == 1 else (torch.empty((S, F), device="cuda"),
+                                                             torch.empty((S, F), device="cuda"))
         for layer, (kc, vc) in zip(self.layers, cache):
             hip.rmsnorm(x, layer["norm_attn"], h, cfg.eps)
             a = layer["attn"].forward_cached(h, kc, vc, pos)
             hip.add(x, a, x1)
             hip.rmsnorm(x1, layer["norm_ffn"], h, cfg.eps)
-            hip.linear_bf16(h, layer["wgate"], None, gate)
-            hip.linear_bf16(h, layer["wup"], None, upv)
+            wgu = layer["wgu"]
+            if S == 1:
+                hip.linear_bf16(h, wgu, None, gu)
+            else:
+                hip.linear_bf16(h, wgu[:F], None, gate)
+                hip.linear_bf16(h, wgu[F:], None, upv)
             hip.swiglu(gate, upv, gate)
-            hip.linear_bf16(gate, layer["wdown"], None, x, residual=x1)
+            hip.linear_bf16(gate.view(S, F), layer["wdown"], None, x, residual=x1)
         last = torch.empty((1, d), device="cuda")
         hip.rmsnorm(x[S - 1:S], self.norm, last, cfg.eps)
         logits = torch.empty((1, cfg.vocab), device="cuda")
