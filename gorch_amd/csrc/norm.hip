@@ -59,6 +59,45 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* __
     for (int j = threadIdx.x; j < N; j += blockDim.x) out[j] = row[j] * inv * g[j];
 }
 
+// One wave per row for rows of at most 256 * R floats (N % 4 == 0): every
+// load of the row and the gains is issued first (raw buffer loads, columns
+// past N read as zeros), the f64 sum of squares is reduced on DPP with no
+// barrier, and the outputs are written after every load has been used (a
+// load issued after a store would make its use wait for the store). In place
+// is fine: a lane rewrites only the elements it read. Four rows per block.
+template <int R>
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* x, const float* __restrict__ g, float* y, int M,
+                                                      int N, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)m * N, (long long)N * 4);
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(g, (long long)N * 4);
+    float4 v[R], gv[R];
+#pragma unroll
+    for (int c = 0; c < R; c++) {
+        const int off = (4 * (lane + 64 * c)) * 4;
+        v[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+        gv[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0));
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int c = 0; c < R; c++)
+        s += ((double)v[c].x * (double)v[c].x + (double)v[c].y * (double)v[c].y) +
+             ((double)v[c].z * (double)v[c].z + (double)v[c].w * (double)v[c].w);
+    s = wave_sum_d(s);
+    const float inv = (float)(1.0 / sqrt(s / (double)N + (double)eps));
+    float* out = y + (size_t)m * N;
+#pragma unroll
+    for (int c = 0; c < R; c++) {
+        const int j = 4 * (lane + 64 * c);
+        if (j < N)
+            *reinterpret_cast<float4*>(out + j) =
+                make_float4(v[c].x * inv * gv[c].x, v[c].y * inv * gv[c].y, v[c].z * inv * gv[c].z,
+                            v[c].w * inv * gv[c].w);
+    }
+}
+
 // One block per row: x[m] += bias + sum_s part[s][m] (slices in order, the
 // residual add of a K-split Linear), then the row's LayerNorm statistics in
 // f64 (nn/layernorm.go:61-91) and, given gamma/beta, the normalised row h.
@@ -217,6 +256,16 @@ int launch_layernorm(hipStream_t s, const float* x, const float* g, const float*
 
 int launch_rmsnorm(hipStream_t s, const float* x, const float* g, float* y, int M, int N, float eps) {
     if (M == 0) return GORCH_HIP_OK;
+    const bool aligned = N % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % 16) == 0;
+    if (aligned && N <= 2048) {
+        const dim3 grid((M + 3) / 4);
+        if (N <= 256) hipLaunchKernelGGL(k_rmsnorm_rows<1>, grid, dim3(256), 0, s, x, g, y, M, N, eps);
+        else if (N <= 512) hipLaunchKernelGGL(k_rmsnorm_rows<2>, grid, dim3(256), 0, s, x, g, y, M, N, eps);
+        else if (N <= 1024) hipLaunchKernelGGL(k_rmsnorm_rows<4>, grid, dim3(256), 0, s, x, g, y, M, N, eps);
+        else hipLaunchKernelGGL(k_rmsnorm_rows<8>, grid, dim3(256), 0, s, x, g, y, M, N, eps);
+        count(CNT_NORM);
+        return check_launch("rmsnorm");
+    }
     hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(256), 0, s, x, g, y, N, eps);
     count(CNT_NORM);
     return check_launch("rmsnorm");
