@@ -145,14 +145,14 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_cached(AttnArgs a) {
 // and are issued before the cache length (written by the previous kernel)
 // has arrived; keys at or past it are masked in the arithmetic (selects, so
 // whatever the unused rows hold never reaches the result).
-template <int HD4, int UNR, bool FULL>
-__global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
+template <int HD4, int UNR, bool FULL, int NW = 4>
+__global__ __launch_bounds__(NW * 64) void k_attn_rows(AttnArgs a) {
     extern __shared__ float sc[];  // [visible keys]
     __shared__ float red[16];
-    __shared__ float4 po[4][64];
-    __shared__ float pl[4][64];
+    __shared__ float4 po[NW][64];
+    __shared__ float pl[NW][64];
     constexpr int KPI = 64 / HD4;  // keys per wavefront instruction
-    constexpr int KB = 4 * KPI;    // keys per block instruction
+    constexpr int KB = NW * KPI;   // keys per block instruction
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane % HD4, slot = wave * KPI + lane / HD4;
 
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
             float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
             float L = 0.f;
 #pragma unroll
-            for (int w = 0; w < 4; w++)
+            for (int w = 0; w < NW; w++)
 #pragma unroll
                 for (int sl = 0; sl < KPI; sl++) {
                     const float4 pv = po[w][sl * HD4 + c];
@@ -303,13 +303,13 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnArgs a) {
             }
         }
     }
-    // the 4 waves' key slots, in order (wave, slot)
+    // the NW waves' key slots, in order (wave, slot)
     po[wave][lane] = o;
     __syncthreads();
     if (threadIdx.x < HD4) {
         float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int w = 0; w < 4; w++)
+        for (int w = 0; w < NW; w++)
 #pragma unroll
             for (int sl = 0; sl < KPI; sl++) {
                 const float4 pv = po[w][sl * HD4 + c];
@@ -486,12 +486,13 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
     // through the per-dim kernel below
     if (rows_kernel && aligned && a.max_seq <= 256 && (a.hd == 64 || a.hd == 128 || a.hd == 32 || a.hd == 16)) {
         const dim3 grid(heads, rows);
-        // one chunk of KB * UNR keys (KB = 256 / HD4) covers the cache: FULL
+        // one chunk of KB * UNR keys (KB = 64 NW / HD4) covers the cache: FULL
+        // (head dim 128 past 128 rows: 8 waves, 256 keys)
         const int ms = a.max_seq;
         switch (a.hd) {
             case 128:
                 if (ms <= 128) hipLaunchKernelGGL((k_attn_rows<32, 16, true>), grid, dim3(256), lds, s, a);
-                else hipLaunchKernelGGL((k_attn_rows<32, 8, false>), grid, dim3(256), lds, s, a);
+                else hipLaunchKernelGGL((k_attn_rows<32, 16, true, 8>), grid, dim3(512), lds, s, a);
                 break;
             case 64:
                 if (ms <= 128) hipLaunchKernelGGL((k_attn_rows<16, 8, true>), grid, dim3(256), lds, s, a);

@@ -85,7 +85,8 @@ def test_activations(gpu):
                                                         (2, 5, 40, 12, 64), (3, 1, 767, 25, 64),
                                                         (1, 32, 0, 12, 64), (2, 3, 9, 4, 80),
                                                         (2, 5, 300, 4, 128), (1, 3, 700, 2, 128),
-                                                        (64, 1, 400, 20, 64), (2, 1, 1300, 3, 64)])
+                                                        (64, 1, 400, 20, 64), (2, 1, 1300, 3, 64),
+                                                        (2, 3, 150, 4, 128), (1, 1, 250, 16, 128)])
 def test_attention_cached(gpu, batch, new_seq, pos, heads, hd):
     rng = np.random.default_rng(pos + heads)
     d = heads * hd
