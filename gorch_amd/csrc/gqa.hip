@@ -13,6 +13,8 @@ namespace gh {
 int launch_rope_rows(hipStream_t s, const float* x, float* y, int rows, int heads, int hd, int start_pos,
                      const float* cosT, const float* sinT, int neox);
 int launch_rmsnorm(hipStream_t s, const float* x, const float* g, float* y, int M, int N, float eps);
+int launch_norm_rope_rows(hipStream_t s, const float* x, float* y, int rows, int heads, int hd, const float* g,
+                          float eps, int start_pos, const float* cosT, const float* sinT, int neox);
 }  // namespace gh
 
 using namespace gh;
@@ -53,13 +55,27 @@ extern "C" int gorch_hip_gqa_forward_cached(void* stream, const gorch_hip_gqa_we
     GH_TRY(launch_linear_bf16(s, x, w->wq, w->bq, nullptr, q, S, qdim, d, GORCH_HIP_EPI_NONE));
     GH_TRY(launch_linear_bf16(s, x, w->wk, w->bk, nullptr, kt, S, kvdim, d, GORCH_HIP_EPI_NONE));
     GH_TRY(launch_linear_bf16(s, x, w->wv, w->bv, nullptr, vrow, S, kvdim, d, GORCH_HIP_EPI_NONE));
-    if (w->q_norm) GH_TRY(launch_rmsnorm(s, q, w->q_norm, q, S * nq, hd, w->norm_eps));
-    if (w->k_norm) GH_TRY(launch_rmsnorm(s, kt, w->k_norm, kt, S * nkv, hd, w->norm_eps));
-    if (w->rope_cos) {
-        GH_TRY(launch_rope_rows(s, q, q, S * nq, nq, hd, pos_offset, w->rope_cos, w->rope_sin, w->rope_neox));
-        GH_TRY(launch_rope_rows(s, kt, krow, S * nkv, nkv, hd, pos_offset, w->rope_cos, w->rope_sin, w->rope_neox));
+    // per-head RMSNorm and RoPE in one launch each for q and k when the
+    // head fits one wave (hd % 8 == 0, hd <= 256, 16-byte rows)
+    const bool fused = w->rope_cos && hd % 8 == 0 && hd <= 256 &&
+                       ((reinterpret_cast<uintptr_t>(krow) | reinterpret_cast<uintptr_t>(q) |
+                         reinterpret_cast<uintptr_t>(kt)) % 16) == 0;
+    if (fused) {
+        GH_TRY(launch_norm_rope_rows(s, q, q, S * nq, nq, hd, w->q_norm, w->norm_eps, pos_offset, w->rope_cos,
+                                     w->rope_sin, w->rope_neox));
+        GH_TRY(launch_norm_rope_rows(s, kt, krow, S * nkv, nkv, hd, w->k_norm, w->norm_eps, pos_offset,
+                                     w->rope_cos, w->rope_sin, w->rope_neox));
     } else {
-        GH_TRY(check(hipMemcpyAsync(krow, kt, (size_t)S * kvdim * 4, hipMemcpyDeviceToDevice, s), "gqa k copy"));
+        if (w->q_norm) GH_TRY(launch_rmsnorm(s, q, w->q_norm, q, S * nq, hd, w->norm_eps));
+        if (w->k_norm) GH_TRY(launch_rmsnorm(s, kt, w->k_norm, kt, S * nkv, hd, w->norm_eps));
+        if (w->rope_cos) {
+            GH_TRY(launch_rope_rows(s, q, q, S * nq, nq, hd, pos_offset, w->rope_cos, w->rope_sin, w->rope_neox));
+            GH_TRY(launch_rope_rows(s, kt, krow, S * nkv, nkv, hd, pos_offset, w->rope_cos, w->rope_sin,
+                                    w->rope_neox));
+        } else {
+            GH_TRY(check(hipMemcpyAsync(krow, kt, (size_t)S * kvdim * 4, hipMemcpyDeviceToDevice, s),
+                         "gqa k copy"));
+        }
     }
     AttnArgs a{q, k_cache, v_cache, att, nullptr, pos_offset, S, qdim, hd, max_seq, qdim, w->causal ? 1 : 0,
                (float)(1.0 / sqrt((double)hd)), nkv, kvdim, 1};

@@ -64,6 +64,75 @@ __global__ void k_rope_rows(const float* x, float* y, int64_t rows, int heads, i
     }
 }
 
+// The GQA q/k epilogue in one launch (nn/gqa.go:300-330 order: per-head
+// RMSNorm, then RoPE at the row's absolute position): one wave per row of hd
+// floats (hd % 4 == 0, hd <= 256; lane l holds elements 4l .. 4l + 3), every
+// load first; with gains, y = x * inv * g (inv from the f64 sum of squares,
+// as k_rmsnorm_rows), then each pair rotated with rotate_pair's unfused
+// operations, the Llama partner element fetched from lane l +- hd / 8. Row r
+// is token r / heads. In place is fine: a lane writes only its own elements,
+// after every value it needs is in registers.
+__global__ __launch_bounds__(256) void k_norm_rope_rows(const float* x, float* y, int rows, int heads, int hd,
+                                                        const float* __restrict__ g, float eps, int start_pos,
+                                                        const float* __restrict__ cosT,
+                                                        const float* __restrict__ sinT, int neox) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const int half = hd / 2, nl = hd / 4;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)r * hd, (long long)hd * 4);
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(g, g ? (long long)hd * 4 : 0);
+    float4 v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, 16 * lane, 0, 0));
+    const float4 gv = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, 16 * lane, 0, 0));
+    const int p = start_pos + r / heads;
+    if (g) {
+        double s = ((double)v.x * (double)v.x + (double)v.y * (double)v.y) +
+                   ((double)v.z * (double)v.z + (double)v.w * (double)v.w);
+        s = wave_sum_d(s);
+        const float inv = (float)(1.0 / sqrt(s / (double)hd + (double)eps));
+        v = make_float4(v.x * inv * gv.x, v.y * inv * gv.y, v.z * inv * gv.z, v.w * inv * gv.w);
+    }
+    float o[4];
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    if (neox) {
+        // pairs (2i, 2i + 1) inside the lane's four elements, i = 2l, 2l + 1
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int i = 2 * lane + q;
+            const int cs = p * half + min(i, half - 1);
+            const float c = cosT[cs], si = sinT[cs];
+            o[2 * q] = e[2 * q] * c - e[2 * q + 1] * si;
+            o[2 * q + 1] = e[2 * q] * si + e[2 * q + 1] * c;
+        }
+    } else {
+        // Llama pairs (i, i + half): the partner sits hd / 8 lanes away
+        const bool lo = lane < nl / 2;
+        const int src = lo ? lane + nl / 2 : lane - nl / 2;
+        float pe[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) pe[q] = __shfl(e[q], src);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int k = 4 * lane + q;
+            const int i = lo ? k : k - half;
+            const int cs = p * half + min(max(i, 0), half - 1);
+            const float c = cosT[cs], si = sinT[cs];
+            o[q] = lo ? e[q] * c - pe[q] * si : pe[q] * si + e[q] * c;
+        }
+    }
+    if (lane < nl) *reinterpret_cast<float4*>(y + (size_t)r * hd + 4 * lane) = make_float4(o[0], o[1], o[2], o[3]);
+}
+
+int launch_norm_rope_rows(hipStream_t s, const float* x, float* y, int rows, int heads, int hd, const float* g,
+                          float eps, int start_pos, const float* cosT, const float* sinT, int neox) {
+    if (rows == 0) return GORCH_HIP_OK;
+    hipLaunchKernelGGL(k_norm_rope_rows, dim3((rows + 3) / 4), dim3(256), 0, s, x, y, rows, heads, hd, g, eps,
+                       start_pos, cosT, sinT, neox);
+    count(CNT_ELEMENTWISE);
+    return check_launch("norm_rope_rows");
+}
+
 static int grid_for(int64_t n) {
     int64_t g = (n + 255) / 256;
     return (int)(g < 1 ? 1 : (g > 16384 ? 16384 : g));

@@ -108,6 +108,26 @@ def test_gqa_module_vs_oracle(gpu, qk_norm, rope, bias):
     _run(gpu, w, chunks)
 
 
+@pytest.mark.parametrize("hd,qk_norm", [(16, True), (32, False), (40, True)])
+def test_gqa_module_neox_rope(gpu, hd, qk_norm):
+    # interleaved (GPT-NeoX) pairs through the fused per-head norm + RoPE
+    # kernel (head dims that are multiples of 8); RoPE tables from the GPU
+    w = syn.gqa_weights(head_dim=hd, seed=9, qk_norm=qk_norm, rope=True, bias=False)
+    w["rope_neox"] = 1
+    rng = np.random.default_rng(10)
+    chunks = [rng.standard_normal((n, w["dim"])).astype(np.float32) for n in (4, 1, 2)]
+    _run(gpu, w, chunks)
+
+
+def test_gqa_module_unfused_head(gpu):
+    # head dim 20 (not a multiple of 8): per-head norm and RoPE as separate
+    # kernels
+    w = syn.gqa_weights(dim=40, num_q=4, num_kv=2, head_dim=20, seed=12, qk_norm=True, rope=True, bias=False)
+    rng = np.random.default_rng(13)
+    chunks = [rng.standard_normal((n, w["dim"])).astype(np.float32) for n in (3, 1)]
+    _run(gpu, w, chunks)
+
+
 def test_gqa_qwen3_shaped_decode(gpu):
     """Qwen3-0.6B attention shape: d 1024, 16 query
     heads x 128, 8 KV heads, qk-norm, RoPE base 1e6; 32-token prefill then
