@@ -65,20 +65,30 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* __
 // barrier, and the outputs are written after every load has been used (a
 // load issued after a store would make its use wait for the store). In place
 // is fine: a lane rewrites only the elements it read. Four rows per block.
+// With b (the fused residual add of a decoder block): the row is x + b,
+// written to sum before the normalised row goes to y.
 template <int R>
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* x, const float* __restrict__ g, float* y, int M,
-                                                      int N, float eps) {
+                                                      int N, float eps, const float* b = nullptr,
+                                                      float* sum = nullptr) {
     const int lane = threadIdx.x & 63;
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (m >= M) return;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)m * N, (long long)N * 4);
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(g, (long long)N * 4);
-    float4 v[R], gv[R];
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(b ? b + (size_t)m * N : nullptr, b ? (long long)N * 4 : 0);
+    float4 v[R], gv[R], bv[R];
 #pragma unroll
     for (int c = 0; c < R; c++) {
         const int off = (4 * (lane + 64 * c)) * 4;
         v[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
         gv[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0));
+        bv[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0));
+    }
+    if (b) {
+#pragma unroll
+        for (int c = 0; c < R; c++)
+            v[c] = make_float4(v[c].x + bv[c].x, v[c].y + bv[c].y, v[c].z + bv[c].z, v[c].w + bv[c].w);
     }
     double s = 0.0;
 #pragma unroll
@@ -91,6 +101,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* x, const floa
 #pragma unroll
     for (int c = 0; c < R; c++) {
         const int j = 4 * (lane + 64 * c);
+        if (b && j < N) *reinterpret_cast<float4*>(sum + (size_t)m * N + j) = v[c];
         if (j < N)
             *reinterpret_cast<float4*>(out + j) =
                 make_float4(v[c].x * inv * gv[c].x, v[c].y * inv * gv[c].y, v[c].z * inv * gv[c].z,
@@ -281,6 +292,25 @@ extern "C" int gorch_hip_layernorm(void* stream, const float* x, const float* ga
     if (M == 0) return GORCH_HIP_OK;
     GH_REQUIRE(x && gamma && beta && y, "gorch_hip_layernorm: null pointer");
     return launch_layernorm(stream_of(stream), x, gamma, beta, y, M, N, eps, N);
+}
+
+extern "C" int gorch_hip_add_rmsnorm(void* stream, const float* x, const float* b, const float* gamma, float* sum,
+                                     float* y, int M, int N, float eps) {
+    GH_REQUIRE(M >= 0 && N > 0, "gorch_hip_add_rmsnorm: bad shape");
+    if (M == 0) return GORCH_HIP_OK;
+    GH_REQUIRE(x && b && gamma && sum && y, "gorch_hip_add_rmsnorm: null pointer");
+    GH_REQUIRE(N % 4 == 0 && N <= 2048 &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(b) |
+                     reinterpret_cast<uintptr_t>(sum) | reinterpret_cast<uintptr_t>(y)) % 16) == 0,
+               "gorch_hip_add_rmsnorm: needs N % 4 == 0, N <= 2048 and 16-byte aligned rows");
+    hipStream_t s = stream_of(stream);
+    const dim3 grid((M + 3) / 4);
+    if (N <= 256) hipLaunchKernelGGL(k_rmsnorm_rows<1>, grid, dim3(256), 0, s, x, gamma, y, M, N, eps, b, sum);
+    else if (N <= 512) hipLaunchKernelGGL(k_rmsnorm_rows<2>, grid, dim3(256), 0, s, x, gamma, y, M, N, eps, b, sum);
+    else if (N <= 1024) hipLaunchKernelGGL(k_rmsnorm_rows<4>, grid, dim3(256), 0, s, x, gamma, y, M, N, eps, b, sum);
+    else hipLaunchKernelGGL(k_rmsnorm_rows<8>, grid, dim3(256), 0, s, x, gamma, y, M, N, eps, b, sum);
+    count(CNT_NORM);
+    return check_launch("add_rmsnorm");
 }
 
 extern "C" int gorch_hip_rmsnorm(void* stream, const float* x, const float* gamma, float* y, int M, int N,

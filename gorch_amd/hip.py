@@ -58,6 +58,7 @@ SIGNATURES = {
     "gorch_hip_linear_bf16_packed": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
     "gorch_hip_layernorm": (i32, [vp, vp, vp, vp, vp, i32, i32, f32]),
     "gorch_hip_rmsnorm": (i32, [vp, vp, vp, vp, i32, i32, f32]),
+    "gorch_hip_add_rmsnorm": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, f32]),
     "gorch_hip_add": (i32, [vp, vp, vp, vp, i64]),
     "gorch_hip_bias_add": (i32, [vp, vp, vp, i32, i32]),
     "gorch_hip_gelu": (i32, [vp, vp, vp, i64]),
@@ -191,6 +192,12 @@ def layernorm(x, gamma, beta, y, eps=1e-5) -> None:
 def rmsnorm(x, gamma, y, eps=1e-6) -> None:
     M, N = x.shape
     _ok(lib().gorch_hip_rmsnorm(_stream(), _p(x), _p(gamma), _p(y), M, N, eps))
+
+
+def add_rmsnorm(x, b, gamma, s, y, eps=1e-6) -> None:
+    """s = x + b; y = RMSNorm(s) (a decoder block's residual add + next norm)."""
+    M, N = x.shape
+    _ok(lib().gorch_hip_add_rmsnorm(_stream(), _p(x), _p(b), _p(gamma), _p(s), _p(y), M, N, eps))
 
 
 def add(a, b, c) -> None:

@@ -107,8 +107,11 @@ class Qwen:
         for layer, (kc, vc) in zip(self.layers, cache):
             hip.rmsnorm(x, layer["norm_attn"], h, cfg.eps)
             a = layer["attn"].forward_cached(h, kc, vc, pos)
-            hip.add(x, a, x1)
-            hip.rmsnorm(x1, layer["norm_ffn"], h, cfg.eps)
+            if d % 4 == 0 and d <= 2048:
+                hip.add_rmsnorm(x, a, layer["norm_ffn"], x1, h, cfg.eps)
+            else:
+                hip.add(x, a, x1)
+                hip.rmsnorm(x1, layer["norm_ffn"], h, cfg.eps)
             wgu = layer["wgu"]
             if S == 1:
                 hip.linear_bf16(h, wgu, None, gu)

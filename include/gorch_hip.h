@@ -136,6 +136,12 @@ int gorch_hip_layernorm(void* stream, const float* x, const float* gamma, const 
 /* RMSNorm (nn/rmsnorm.go:39-81, RMSNormForwardMetal rmsnorm_metal.go:51):
  * y = x * (1/sqrt(sum(x^2)/N + eps)) * gamma, sum in f64. */
 int gorch_hip_rmsnorm(void* stream, const float* x, const float* gamma, float* y, int M, int N, float eps);
+/* A decoder block's residual add and the next RMSNorm in one launch
+ * (model/qwen/block.go:74-76: h1 = Add(x, attn); NormFFN.Forward(h1)):
+ * sum = x + b, y = RMSNorm(sum; gamma). N % 4 == 0, N <= 2048, 16-byte
+ * aligned rows; y may not alias x or b. */
+int gorch_hip_add_rmsnorm(void* stream, const float* x, const float* b, const float* gamma, float* sum, float* y,
+                          int M, int N, float eps);
 /* c = a + b (Add, ops.go:161-179; vec_add). */
 int gorch_hip_add(void* stream, const float* a, const float* b, float* c, int64_t n);
 /* x[m,n] += bias[n] in place (BiasAddInPlaceMetal, colreduce_metal.go:56-73). */

@@ -81,6 +81,21 @@ def test_activations(gpu):
     assert np.max(np.abs(host(y) - orc.swiglu(x, v))) < 2e-6 * 15
 
 
+@pytest.mark.parametrize("M,N", [(1, 1024), (3, 128), (5, 2048)])
+def test_add_rmsnorm(gpu, M, N):
+    # a decoder block's residual add then RMSNorm (model/qwen/block.go:74-76)
+    rng = np.random.default_rng(M + N)
+    x = rng.standard_normal((M, N)).astype(np.float32)
+    b = rng.standard_normal((M, N)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(N)).astype(np.float32)
+    s = torch.empty((M, N), device="cuda")
+    y = torch.empty((M, N), device="cuda")
+    gpu.add_rmsnorm(dev(x), dev(b), dev(g), s, y)
+    ref_s = orc.add(x, b)
+    assert np.array_equal(host(s), ref_s)
+    assert np.max(np.abs(host(y) - orc.rmsnorm(ref_s, g))) < 1e-5
+
+
 @pytest.mark.parametrize("batch,new_seq,pos,heads,hd", [(1, 1, 0, 12, 64), (1, 1, 95, 12, 64),
                                                         (2, 5, 40, 12, 64), (3, 1, 767, 25, 64),
                                                         (1, 32, 0, 12, 64), (2, 3, 9, 4, 80),
