@@ -454,6 +454,149 @@ __global__ __launch_bounds__(NW * 64) void k_attn_flash(AttnArgs a) {
     }
 }
 
+// k_attn_long: caches longer than one chunk of keys when (head, row) blocks
+// are few (a batch-1 step). Lanes over (key, 16-byte chunk of the head) as in
+// k_attn_rows; NW waves take KB = NW * KPI keys per instruction and UNR
+// instructions per chunk. Every key slot keeps an online softmax over its own
+// keys (running max m, weight sum l, weighted value sum o, rescaled by
+// exp(m_old - m_new) when the max grows), so the loop has no barrier and the
+// next chunk's K and V rows (raw buffer loads over the visible rows,
+// branch-free) are in flight while one is used. At the end every slot is
+// rescaled to the block's max and the slots are summed through LDS: out =
+// sum o / sum l.
+template <int HD4, int NW, int UNR>
+__global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
+    constexpr int KPI = 64 / HD4;  // keys per wavefront instruction
+    constexpr int KB = NW * KPI;   // keys per block instruction
+    constexpr int KC = KB * UNR;   // keys per chunk
+    __shared__ float4 po[NW][64];
+    __shared__ float pl[NW][64];
+    __shared__ float4 ps[NW][HD4];
+    __shared__ float psl[NW];
+    __shared__ float red[NW];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane % HD4, slot = wave * KPI + lane / HD4;
+    const int h = blockIdx.x;
+    const int row = blockIdx.y;
+    const int b = row / a.new_seq;
+    const int i = row - b * a.new_seq;
+    const int kvh = a.kv_heads ? h / ((int)gridDim.x / a.kv_heads) : h;
+    const int kvd = a.kv_dim ? a.kv_dim : a.dim;
+    const size_t base = ((size_t)b * a.max_seq) * kvd + (size_t)kvh * (4 * HD4);
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    const int T = a.causal ? pos + i + 1 : pos + a.new_seq;
+    const long long span = T > 0 ? ((long long)(T - 1) * kvd + 4 * HD4) * 4 : 0;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.kc + base, span);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.vc + base, span);
+    auto ld4 = [](__amdgpu_buffer_rsrc_t rs, int off) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+        return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                           __uint_as_float(v[3]));
+    };
+    const float4 q = *reinterpret_cast<const float4*>(a.q + (size_t)row * a.q_stride + h * (4 * HD4) + 4 * c);
+    // keys past T lie outside the resources and read as zeros
+    auto load = [&](int j0, float4 (&kk)[UNR], float4 (&vv)[UNR]) {
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int off = (j0 + KB * u + slot) * kvd * 4 + 16 * c;
+            kk[u] = ld4(rk, off);
+            vv[u] = ld4(rv, off);
+        }
+    };
+    float m = -INFINITY, l = 0.f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto step = [&](int j0, const float4 (&kk)[UNR], const float4 (&vv)[UNR]) {
+        float sj[UNR];
+        float cm = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const float d = q.x * kk[u].x + q.y * kk[u].y + q.z * kk[u].z + q.w * kk[u].w;
+            sj[u] = seg_sum<HD4>(d) * a.scale;
+            if (j0 + KB * u + slot < T) cm = fmaxf(cm, sj[u]);
+        }
+        if (cm > -INFINITY) {
+            const float mn = fmaxf(m, cm);
+            const float al = expf(m - mn);
+            l *= al;
+            o = make_float4(o.x * al, o.y * al, o.z * al, o.w * al);
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                if (j0 + KB * u + slot < T) {
+                    const float p = expf(sj[u] - mn);
+                    l += p;
+                    o.x += p * vv[u].x;
+                    o.y += p * vv[u].y;
+                    o.z += p * vv[u].z;
+                    o.w += p * vv[u].w;
+                }
+            }
+            m = mn;
+        }
+    };
+    float4 ka[UNR], va[UNR], kb[UNR], vb[UNR];
+    load(0, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
+    load(KC, kb, vb);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int j0 = 0; j0 < T; j0 += 2 * KC) {
+        step(j0, ka, va);
+        load(j0 + 2 * KC, ka, va);
+        __builtin_amdgcn_sched_barrier(0);
+        if (j0 + KC < T) step(j0 + KC, kb, vb);
+        load(j0 + 3 * KC, kb, vb);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // the block's max, then every slot rescaled to it (empty slots weigh 0)
+    const float wm = wave_max(m);
+    if (lane == 0) red[wave] = wm;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) M = fmaxf(M, red[w]);
+    const float f = m > -INFINITY ? expf(m - M) : 0.f;
+    po[wave][lane] = make_float4(o.x * f, o.y * f, o.z * f, o.w * f);
+    pl[wave][lane] = l * f;
+    __syncthreads();
+    // per wave, its KPI slots in order; then the waves in order
+    if (threadIdx.x < NW * HD4) {
+        const int w = threadIdx.x / HD4, cc = threadIdx.x % HD4;
+        float4 t = po[w][cc];
+        float tl = pl[w][cc];
+#pragma unroll
+        for (int sl = 1; sl < KPI; sl++) {
+            const float4 pv = po[w][sl * HD4 + cc];
+            t.x += pv.x;
+            t.y += pv.y;
+            t.z += pv.z;
+            t.w += pv.w;
+            tl += pl[w][sl * HD4 + cc];
+        }
+        ps[w][cc] = t;
+        if (cc == 0) psl[w] = tl;
+    }
+    __syncthreads();
+    if (threadIdx.x < HD4) {
+        float4 t = ps[0][c];
+        float L = psl[0];
+#pragma unroll
+        for (int w = 1; w < NW; w++) {
+            const float4 pv = ps[w][c];
+            t.x += pv.x;
+            t.y += pv.y;
+            t.z += pv.z;
+            t.w += pv.w;
+            L += psl[w];
+        }
+        if (a.recip) {
+            const float rs = 1.0f / L;
+            t = make_float4(t.x * rs, t.y * rs, t.z * rs, t.w * rs);
+        } else {
+            t = make_float4(t.x / L, t.y / L, t.z / L, t.w / L);
+        }
+        *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + h * (4 * HD4) + 4 * c) = t;
+    }
+}
+
 // 4 waves per (head, row) block when there are enough blocks to fill the
 // GPU; 16 waves when the visible context is long and blocks are few, so each
 // block keeps more of the KV stream in flight.
@@ -503,6 +646,21 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
         }
         count(CNT_ATTENTION);
         return check_launch("attn_rows");
+    }
+    // few (head, row) blocks over a long cache (a batch-1 step): the
+    // online-softmax kernel keeps two 256-key chunks in flight per block;
+    // with hundreds of blocks the two-pass kernel below streams better
+    // (measured: XL batch 16, 400 blocks, 29.4 vs 25 us per layer)
+    static const int long_kernel = [] {
+        const char* e = getenv("GORCH_HIP_ATTN_LONG");
+        return e ? atoi(e) : 1;
+    }();
+    if (long_kernel && aligned && blocks < 128 && (a.hd == 64 || a.hd == 128)) {
+        const dim3 grid(heads, rows);
+        if (a.hd == 64) hipLaunchKernelGGL((k_attn_long<16, 16, 4>), grid, dim3(1024), 0, s, a);
+        else hipLaunchKernelGGL((k_attn_long<32, 16, 4>), grid, dim3(1024), 0, s, a);
+        count(CNT_ATTENTION);
+        return check_launch("attn_long");
     }
     if (blocks < 1024 && a.max_seq >= 128)
         hipLaunchKernelGGL(k_attn_cached<16>, dim3(heads, rows), dim3(1024), lds, s, a);
