@@ -56,28 +56,37 @@ def test_rope_rejects_overflow(gpu):
         gpu.rope_apply(x, x, c, s, start_pos=6)
 
 
-@pytest.mark.parametrize("nq,nkv,S,pos", [(8, 2, 1, 30), (8, 8, 4, 12), (16, 8, 3, 0)])
-def test_gqa_attention_vs_f64(gpu, nq, nkv, S, pos):
+@pytest.mark.parametrize("batch,nq,nkv,S,pos,hd", [
+    (1, 8, 2, 1, 30, 32), (1, 8, 8, 4, 12, 32), (1, 16, 8, 3, 0, 32),
+    # Qwen3-0.6B heads (16 query / 8 KV heads of 128): the 8-wave one-pass
+    # kernel (cache 129..256 rows), the online-softmax long-cache kernel
+    # (fewer than 128 (head, row) blocks), and the 16-wave two-pass kernel
+    # (128..1023 blocks over a cache longer than 256 rows)
+    (1, 16, 8, 1, 200, 128), (1, 16, 8, 1, 500, 128), (1, 16, 8, 1, 1300, 128),
+    (2, 16, 8, 3, 300, 128), (8, 16, 8, 1, 400, 128), (8, 8, 2, 2, 290, 64)])
+def test_gqa_attention_vs_f64(gpu, batch, nq, nkv, S, pos, hd):
     import math
     import scipy.special
-    rng = np.random.default_rng(nq + S + pos)
-    hd = 32
+    rng = np.random.default_rng(nq + S + pos + batch)
     T = pos + S
-    q = rng.standard_normal((S, nq * hd)).astype(np.float32)
-    kc = rng.standard_normal((T + 2, nkv * hd)).astype(np.float32)
-    vc = rng.standard_normal((T + 2, nkv * hd)).astype(np.float32)
-    out = torch.empty((S, nq * hd), device="cuda")
-    gpu.gqa_attention_cached(dev(q), dev(kc), dev(vc), out, 1, S, pos, nq, nkv, hd, T + 2)
+    cap = T + 2
+    q = rng.standard_normal((batch * S, nq * hd)).astype(np.float32)
+    kc = rng.standard_normal((batch, cap, nkv * hd)).astype(np.float32)
+    vc = rng.standard_normal((batch, cap, nkv * hd)).astype(np.float32)
+    out = torch.empty((batch * S, nq * hd), device="cuda")
+    gpu.gqa_attention_cached(dev(q), dev(kc), dev(vc), out, batch, S, pos, nq, nkv, hd, cap)
     got = host(out)
     g = nq // nkv
-    for h in range(nq):
-        kk = kc[:T, (h // g) * hd:(h // g + 1) * hd].astype(np.float64)
-        vv = vc[:T, (h // g) * hd:(h // g + 1) * hd].astype(np.float64)
-        s = q[:, h * hd:(h + 1) * hd].astype(np.float64) @ kk.T / math.sqrt(hd)
-        for i in range(S):
-            s[i, pos + i + 1:] = -np.inf
-        ref = scipy.special.softmax(s, axis=1) @ vv
-        assert np.max(np.abs(got[:, h * hd:(h + 1) * hd] - ref)) < 1e-5
+    for b in range(batch):
+        qb, gb = q[b * S:(b + 1) * S], got[b * S:(b + 1) * S]
+        for h in range(nq):
+            kk = kc[b, :T, (h // g) * hd:(h // g + 1) * hd].astype(np.float64)
+            vv = vc[b, :T, (h // g) * hd:(h // g + 1) * hd].astype(np.float64)
+            s = qb[:, h * hd:(h + 1) * hd].astype(np.float64) @ kk.T / math.sqrt(hd)
+            for i in range(S):
+                s[i, pos + i + 1:] = -np.inf
+            ref = scipy.special.softmax(s, axis=1) @ vv
+            assert np.max(np.abs(gb[:, h * hd:(h + 1) * hd] - ref)) < 1e-5, (b, h)
 
 
 def _run(gpu, w, chunks, cap=24):

@@ -101,7 +101,12 @@ def test_add_rmsnorm(gpu, M, N):
                                                         (1, 32, 0, 12, 64), (2, 3, 9, 4, 80),
                                                         (2, 5, 300, 4, 128), (1, 3, 700, 2, 128),
                                                         (64, 1, 400, 20, 64), (2, 1, 1300, 3, 64),
-                                                        (2, 3, 150, 4, 128), (1, 1, 250, 16, 128)])
+                                                        (2, 3, 150, 4, 128), (1, 1, 250, 16, 128),
+                                                        # 128..1023 (head, row) blocks over caches longer
+                                                        # than 256 rows: the 16-wave two-pass kernel that
+                                                        # the GPT-2 XL batch-16 step runs (25 heads x 16)
+                                                        (16, 1, 511, 25, 64), (16, 1, 767, 25, 64),
+                                                        (8, 1, 600, 16, 128), (4, 1, 300, 8, 80)])
 def test_attention_cached(gpu, batch, new_seq, pos, heads, hd):
     rng = np.random.default_rng(pos + heads)
     d = heads * hd

@@ -90,3 +90,27 @@ def test_qwen_rejects_overflow(gpu):
         m.forward_cached(torch.zeros(9, dtype=torch.int32, device="cuda"), cache, 0)
     with pytest.raises(ValueError):
         m.new_cache(TINY.max_seq + 1)
+
+
+def test_qwen_greedy_long_cache(gpu):
+    """A cache longer than 256 rows: 270-row prefill (matrix-core GEMMs and
+    flash attention), then one-token steps through the online-softmax
+    long-cache attention kernel (4 query heads over 2 KV heads)."""
+    cfg = QwenConfig(hidden=64, layers=2, num_q=4, num_kv=2, head_dim=32, inter=96, vocab=300, max_seq=320)
+    w = syn.qwen_weights(cfg, seed=5)
+    m = Qwen(cfg, w)
+    ref = OracleQwen(cfg, w, m)
+    cache = m.new_cache(cfg.max_seq)
+    ids = np.random.default_rng(11).integers(0, cfg.vocab, 270).astype(np.int32)
+    pos = 0
+    for step in range(5):
+        got = host(m.forward_cached(torch.from_numpy(ids).cuda(), cache, pos))
+        want = ref.forward_cached(ids, pos)
+        assert rel_err(got, want) <= 1e-3, step
+        nxt = int(np.argmax(got[0]))
+        assert nxt == orc.argmax(want), step
+        pos += ids.size
+        ids = np.array([nxt], np.int32)
+    for (kd, vd), (kc, vc) in zip(cache, ref.cache):
+        assert rel_err(host(kd)[:pos], kc[:pos]) <= 1e-4
+        assert rel_err(host(vd)[:pos], vc[:pos]) <= 1e-4
