@@ -88,5 +88,5 @@ extern "C" int gorch_hip_argmax(void* stream, const float* logits, int rows, int
     GH_REQUIRE(rows >= 0 && n > 0, "gorch_hip_argmax: bad shape");
     if (rows == 0) return GORCH_HIP_OK;
     GH_REQUIRE(logits && out, "gorch_hip_argmax: null pointer");
-    return launch_argmax(stream_of(stream), logits, rows, n, out, nullptr, nullptr, 0, nullptr, 0);
+    return finish(stream, launch_argmax(stream_of(stream), logits, rows, n, out, nullptr, nullptr, 0, nullptr, 0));
 }

@@ -601,7 +601,12 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
 // GPU; 16 waves when the visible context is long and blocks are few, so each
 // block keeps more of the KV stream in flight.
 int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
-    size_t lds = (size_t)a.max_seq * sizeof(float);
+    // the score-staging kernels hold one f32 per visible key in LDS: at most
+    // the cache capacity when the cache length is read on the device, else
+    // the known length
+    const long long visible = a.pos_dev ? (long long)a.max_seq : (long long)a.pos_host + a.new_seq;
+    size_t lds = (size_t)visible * sizeof(float);
+    const bool lds_ok = lds <= kAttnMaxLdsBytes;
     const int blocks = heads * rows;
     static const int rows_kernel = [] {
         const char* e = getenv("GORCH_HIP_ATTN_ROWS");
@@ -655,12 +660,16 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
         const char* e = getenv("GORCH_HIP_ATTN_LONG");
         return e ? atoi(e) : 1;
     }();
-    if (long_kernel && aligned && blocks < 128 && (a.hd == 64 || a.hd == 128)) {
+    if (long_kernel && aligned && (blocks < 128 || !lds_ok) && (a.hd == 64 || a.hd == 128)) {
         const dim3 grid(heads, rows);
         if (a.hd == 64) hipLaunchKernelGGL((k_attn_long<16, 16, 4>), grid, dim3(1024), 0, s, a);
         else hipLaunchKernelGGL((k_attn_long<32, 16, 4>), grid, dim3(1024), 0, s, a);
         count(CNT_ATTENTION);
         return check_launch("attn_long");
+    }
+    if (!lds_ok) {
+        set_error("attention: a cache longer than 16384 visible rows needs head_dim 64 or 128 and 16-byte aligned rows");
+        return GORCH_HIP_EUNSUPPORTED;
     }
     if (blocks < 1024 && a.max_seq >= 128)
         hipLaunchKernelGGL(k_attn_cached<16>, dim3(heads, rows), dim3(1024), lds, s, a);
@@ -724,14 +733,13 @@ extern "C" int gorch_hip_attention_cached(void* stream, const float* q, const fl
     GH_REQUIRE(head_dim % 4 == 0 && head_dim <= 256, "gorch_hip_attention_cached: head_dim must be a multiple of 4, <= 256");
     GH_REQUIRE(pos_offset >= 0 && pos_offset + new_seq <= max_seq,
                "gorch_hip_attention_cached: cached sequence length exceeds max_seq");
-    GH_REQUIRE(max_seq <= 16384, "gorch_hip_attention_cached: max_seq above 16384 is not supported");
     GH_REQUIRE(q && k_cache && v_cache && out, "gorch_hip_attention_cached: null pointer");
     const int dim = heads * head_dim;
     GH_REQUIRE(((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0, "gorch_hip_attention_cached: cache must be 16-byte aligned");
     // invScale = float32(1.0 / sqrtFloat32(float32(headDim))) (nn/attention.go:348)
     AttnArgs a{q, k_cache, v_cache, out, nullptr, pos_offset, new_seq, dim, head_dim, max_seq, dim, causal ? 1 : 0,
                1.0f / (float)sqrt((double)head_dim)};
-    return launch_attn_cached(stream_of(stream), a, heads, batch * new_seq);
+    return finish(stream, launch_attn_cached(stream_of(stream), a, heads, batch * new_seq));
 }
 
 extern "C" int gorch_hip_causal_softmax(void* stream, const float* x, float* y, int rows, int cols, int q_seq,
@@ -741,7 +749,7 @@ extern "C" int gorch_hip_causal_softmax(void* stream, const float* x, float* y, 
     GH_REQUIRE(x && y, "gorch_hip_causal_softmax: null pointer");
     hipLaunchKernelGGL(k_causal_softmax, dim3(rows), dim3(256), 0, stream_of(stream), x, y, cols, q_seq, scale);
     count(CNT_ATTENTION);
-    return check_launch("causal_softmax");
+    return finish(stream, check_launch("causal_softmax"));
 }
 
 extern "C" int gorch_hip_softmax_rows(void* stream, float* x, int rows, int cols) {
@@ -750,7 +758,7 @@ extern "C" int gorch_hip_softmax_rows(void* stream, float* x, int rows, int cols
     GH_REQUIRE(x, "gorch_hip_softmax_rows: null pointer");
     hipLaunchKernelGGL(k_softmax_rows, dim3(rows), dim3(256), 0, stream_of(stream), x, cols);
     count(CNT_ATTENTION);
-    return check_launch("softmax_rows");
+    return finish(stream, check_launch("softmax_rows"));
 }
 
 extern "C" int gorch_hip_gqa_attention_cached(void* stream, const float* q, const float* k_cache, const float* v_cache,
@@ -763,12 +771,11 @@ extern "C" int gorch_hip_gqa_attention_cached(void* stream, const float* q, cons
                "gorch_hip_gqa_attention_cached: head_dim must be a multiple of 4, <= 256");
     GH_REQUIRE(pos_offset >= 0 && pos_offset + new_seq <= max_seq,
                "gorch_hip_gqa_attention_cached: cached sequence length exceeds max_seq");
-    GH_REQUIRE(max_seq <= 16384, "gorch_hip_gqa_attention_cached: max_seq above 16384 is not supported");
     GH_REQUIRE(q && k_cache && v_cache && out, "gorch_hip_gqa_attention_cached: null pointer");
     GH_REQUIRE(((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0,
                "gorch_hip_gqa_attention_cached: cache must be 16-byte aligned");
     const int qdim = num_q * head_dim;
     AttnArgs a{q, k_cache, v_cache, out, nullptr, pos_offset, new_seq, qdim, head_dim, max_seq, qdim, causal ? 1 : 0,
                (float)(1.0 / sqrt((double)head_dim)), num_kv, num_kv * head_dim, 1};
-    return launch_attn_cached(stream_of(stream), a, num_q, batch * new_seq);
+    return finish(stream, launch_attn_cached(stream_of(stream), a, num_q, batch * new_seq));
 }

@@ -68,7 +68,7 @@ extern "C" int gorch_hip_bf16_to_f32(void* stream, const uint16_t* in, float* ou
     hipLaunchKernelGGL(k_bf16_to_f32, dim3(grid_for(vec ? n / 8 + 1 : n)), dim3(256), 0,
                        stream_of(stream), in, out, n, vec);
     count(CNT_CODEC);
-    return check_launch("bf16_to_f32");
+    return finish(stream, check_launch("bf16_to_f32"));
 }
 
 extern "C" int gorch_hip_f32_to_bf16(void* stream, const float* in, uint16_t* out, int64_t n) {
@@ -79,5 +79,5 @@ extern "C" int gorch_hip_f32_to_bf16(void* stream, const float* in, uint16_t* ou
     hipLaunchKernelGGL(k_f32_to_bf16, dim3(grid_for(vec ? n / 8 + 1 : n)), dim3(256), 0,
                        stream_of(stream), in, out, n, vec);
     count(CNT_CODEC);
-    return check_launch("f32_to_bf16");
+    return finish(stream, check_launch("f32_to_bf16"));
 }

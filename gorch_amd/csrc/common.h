@@ -81,6 +81,13 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
                           const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
                           const LinearExtras& ex);
 
+// End of a compute entry point: in sync mode (gorch_hip_set_async(0)) waits
+// for the stream when rc is 0 and the stream is not being captured.
+int finish(void* stream, int rc);
+// GORCH_HIP_EUNSUPPORTED unless the bf16 matmul probe passed on the current
+// device (runs it first if gorch_hip_init has not).
+int bf16_gate(hipStream_t s);
+
 // Dispatch counters (the gorch ReadMetalDispatchCounts analogue).
 enum Counter {
     CNT_GEMV = 0,
@@ -236,6 +243,9 @@ struct AttnArgs {
     int kv_dim;    // cache row stride in floats (0 = dim)
     int recip;     // normalise by multiplying with 1/sum (GQA) instead of dividing
 };
+// LDS the score-staging attention kernels may take (one f32 per visible
+// key: 16384 keys); longer caches go to the online-softmax kernel.
+constexpr size_t kAttnMaxLdsBytes = 65536;
 int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows);
 
 // A tensor entry of a safetensors header (safetensors.hip): dtype

@@ -97,7 +97,7 @@ extern "C" int gorch_hip_add(void* stream, const float* a, const float* b, float
     EW_CHECK(n, a && b && c);
     hipLaunchKernelGGL(k_add, dim3(grid_1d(n)), dim3(256), 0, stream_of(stream), a, b, c, n);
     count(CNT_ELEMENTWISE);
-    return check_launch("add");
+    return finish(stream, check_launch("add"));
 }
 
 extern "C" int gorch_hip_bias_add(void* stream, float* x, const float* bias, int M, int N) {
@@ -106,26 +106,26 @@ extern "C" int gorch_hip_bias_add(void* stream, float* x, const float* bias, int
     EW_CHECK(n, x && bias);
     hipLaunchKernelGGL(k_bias_add, dim3(grid_1d(n)), dim3(256), 0, stream_of(stream), x, bias, n, N);
     count(CNT_ELEMENTWISE);
-    return check_launch("bias_add");
+    return finish(stream, check_launch("bias_add"));
 }
 
 extern "C" int gorch_hip_gelu(void* stream, const float* x, float* y, int64_t n) {
     EW_CHECK(n, x && y);
     hipLaunchKernelGGL(k_gelu, dim3(grid_1d(n)), dim3(256), 0, stream_of(stream), x, y, n);
     count(CNT_ELEMENTWISE);
-    return check_launch("gelu");
+    return finish(stream, check_launch("gelu"));
 }
 
 extern "C" int gorch_hip_silu(void* stream, const float* x, float* y, int64_t n) {
     EW_CHECK(n, x && y);
     hipLaunchKernelGGL(k_silu, dim3(grid_1d(n)), dim3(256), 0, stream_of(stream), x, y, n);
     count(CNT_ELEMENTWISE);
-    return check_launch("silu");
+    return finish(stream, check_launch("silu"));
 }
 
 extern "C" int gorch_hip_swiglu(void* stream, const float* gate, const float* value, float* y, int64_t n) {
     EW_CHECK(n, gate && value && y);
-    return launch_swiglu(stream_of(stream), gate, value, y, n);
+    return finish(stream, launch_swiglu(stream_of(stream), gate, value, y, n));
 }
 
 extern "C" int gorch_hip_embedding(void* stream, const float* weight, int dim, const int* ids, int n,
@@ -136,5 +136,5 @@ extern "C" int gorch_hip_embedding(void* stream, const float* weight, int dim, c
     hipLaunchKernelGGL(k_embedding, dim3(grid_1d(total)), dim3(256), 0, stream_of(stream), weight, ids, out, dim,
                        total);
     count(CNT_ELEMENTWISE);
-    return check_launch("embedding");
+    return finish(stream, check_launch("embedding"));
 }

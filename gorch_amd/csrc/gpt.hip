@@ -364,8 +364,8 @@ static bool gpt_config_ok(int vocab, int dim, int heads, int layers, int max_seq
         set_error(std::string(who) + ": needs dim % 8 == 0 and head_dim a multiple of 4, <= 256");
         return false;
     }
-    if (max_seq > 16384) {
-        set_error(std::string(who) + ": max_seq above 16384 is not supported");
+    if (max_seq > (int)(kAttnMaxLdsBytes / sizeof(float)) && hd != 64 && hd != 128) {
+        set_error(std::string(who) + ": max_seq above 16384 needs head_dim 64 or 128");
         return false;
     }
     return true;
@@ -687,6 +687,7 @@ int gorch_hip_kvcache_read(const gorch_hip_kvcache* c, int layer, int seq, float
 int gorch_hip_gpt_forward_cached(void* stream, gorch_hip_gpt* g, gorch_hip_kvcache* c, const int* ids, int n,
                                  float* logits) {
     GH_REQUIRE(g && c && c->gpt == g && ids && n > 0, "gorch_hip_gpt_forward_cached: bad arguments");
+    GH_TRY(bf16_gate(stream_of(stream)));
     if (c->len + n > c->capacity) {
         set_error("gorch_hip_gpt_forward_cached: cached sequence length exceeds MaxSeq");
         return GORCH_HIP_EINVAL;
@@ -707,11 +708,21 @@ int gorch_hip_gpt_forward_cached(void* stream, gorch_hip_gpt* g, gorch_hip_kvcac
     return check(hipStreamSynchronize(s), "forward sync");
 }
 
-int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* g, const int* prompts, int batch, int n_prompt,
-                              int max_new, int* out_ids, int* out_len, float* step_logits, float* timing_ms,
-                              int flags) {
-    GH_REQUIRE(g && prompts && out_ids && out_len && batch > 0 && n_prompt > 0 && max_new >= 0,
+}  // extern "C"
+
+namespace gh {
+
+// generateCached (model/generate.go:94-131) for `batch` independent prompts:
+// greedy choice, stop at StopToken (stop_token >= 0; the token is not kept)
+// or once the cache holds MaxSeq tokens. Every sequence's row of out_ids is
+// np + max_new wide; its length goes to out_lens[b] (nullable) and the
+// longest to *out_len (nullable).
+static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int batch, int n_prompt, int max_new,
+                         int stop_token, int* out_ids, int* out_lens, int* out_len, float* step_logits,
+                         float* timing_ms, int flags) {
+    GH_REQUIRE(g && prompts && out_ids && batch > 0 && n_prompt > 0 && max_new >= 0,
                "gorch_hip_generate_cached: bad arguments");
+    GH_TRY(bf16_gate(stream_of(stream)));
     // Prompt truncation to the last MaxSeq tokens (model/generate.go:101-103).
     const int np = n_prompt > g->max_seq ? g->max_seq : n_prompt;
     const int skip = n_prompt - np;
@@ -785,6 +796,7 @@ int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* g, const int* prompts
             return choose_tokens(g, c, 1, s);
         };
         if (use_graph && forwards > 0) {
+            // capture the step once (or again when a buffer it points at moved)
             const std::vector<const void*> sig = {g->x,    g->h,    g->q,    g->att,      g->ff,
                                                   g->logits, g->ids, g->part, g->stats, c->k,
                                                   c->v,    c->state, c->hist, c->key};
@@ -811,10 +823,37 @@ int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* g, const int* prompts
                 }
                 g->gen_sig = sig;
             }
-            for (int i = 0; i < forwards; i++)
+        }
+        // With a stop token, the tokens chosen so far are read back every
+        // kStopCheck steps and generation ends once every sequence has
+        // produced it (the reference's loop breaks there; a sequence that
+        // stopped early keeps decoding into ignored positions meanwhile).
+        constexpr int kStopCheck = 8;
+        std::vector<int> seen;
+        int chosen = 1;  // tokens chosen so far (the prefill chose token 0)
+        int done_forwards = 0;
+        auto all_stopped = [&]() -> int {
+            seen.resize((size_t)chosen * batch);
+            GH_TRY(check(hipMemcpyAsync(seen.data(), c->hist, seen.size() * sizeof(int), hipMemcpyDeviceToHost, s),
+                         "hist"));
+            GH_TRY(check(hipStreamSynchronize(s), "stop check sync"));
+            for (int b = 0; b < batch; b++) {
+                bool hit = false;
+                for (int i = 0; i < chosen && !hit; i++) hit = seen[(size_t)i * batch + b] == stop_token;
+                if (!hit) return 0;
+            }
+            return 1;
+        };
+        bool stopped = false;
+        if (stop_token >= 0) {
+            const int r = all_stopped();
+            if (r < 0 || r > 1) { fail(r); break; }
+            stopped = r == 1;
+        }
+        for (int i = 0; i < forwards && !rc && !stopped; i++) {
+            if (use_graph) {
                 if (check(hipGraphLaunch(g->gen_exec, s), "graph launch")) { fail(GORCH_HIP_ERUNTIME); break; }
-        } else {
-            for (int i = 0; i < forwards && !rc; i++) {
+            } else {
                 if (step()) { fail(GORCH_HIP_ERUNTIME); break; }
                 if (step_logits && i + 1 < tokens) {
                     if (check(hipMemcpyAsync(step_logits + (size_t)(i + 1) * batch * g->vocab, g->logits,
@@ -822,36 +861,84 @@ int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* g, const int* prompts
                         fail(GORCH_HIP_ERUNTIME);
                 }
             }
+            chosen++;
+            done_forwards++;
+            if (stop_token >= 0 && (chosen % kStopCheck == 0 || i + 1 == forwards)) {
+                const int r = all_stopped();
+                if (r < 0 || r > 1) { fail(r); break; }
+                stopped = r == 1;
+            }
         }
         if (rc) break;
         (void)hipEventRecord(ev[2], s);
-        std::vector<int> hist((size_t)tokens * batch);
-        if (tokens > 0 &&
+        const int have = std::min(tokens, chosen);  // tokens chosen on the device
+        std::vector<int> hist((size_t)have * batch);
+        if (have > 0 &&
             check(hipMemcpyAsync(hist.data(), c->hist, hist.size() * sizeof(int), hipMemcpyDeviceToHost, s), "hist")) {
             fail(GORCH_HIP_ERUNTIME);
             break;
         }
         if (check(hipStreamSynchronize(s), "generate sync")) { fail(GORCH_HIP_ERUNTIME); break; }
-        // result = (truncated) prompt followed by the generated tokens
-        const int total = np + tokens;
+        // result = (truncated) prompt followed by the generated tokens, each
+        // sequence cut before its first stop token
+        const int width = np + max_new;
+        int longest = np;
         for (int b = 0; b < batch; b++) {
-            for (int i = 0; i < np; i++) out_ids[(size_t)b * total + i] = ids[(size_t)b * np + i];
-            for (int i = 0; i < tokens; i++) out_ids[(size_t)b * total + np + i] = hist[(size_t)i * batch + b];
+            int* row = out_ids + (size_t)b * width;
+            for (int i = 0; i < np; i++) row[i] = ids[(size_t)b * np + i];
+            int n = 0;
+            while (n < have && !(stop_token >= 0 && hist[(size_t)n * batch + b] == stop_token)) {
+                row[np + n] = hist[(size_t)n * batch + b];
+                n++;
+            }
+            if (out_lens) out_lens[b] = np + n;
+            longest = std::max(longest, np + n);
         }
-        *out_len = total;
+        if (out_len) *out_len = longest;
         if (timing_ms) {
             float a = 0.f, bb = 0.f;
             (void)hipEventElapsedTime(&a, ev[0], ev[1]);
             (void)hipEventElapsedTime(&bb, ev[1], ev[2]);
             timing_ms[0] = a;
             timing_ms[1] = bb;
-            timing_ms[2] = (float)forwards;
+            timing_ms[2] = (float)done_forwards;
         }
     } while (false);
     for (auto& e : ev)
         if (e) (void)hipEventDestroy(e);
     (void)hipStreamSynchronize(s);
     return rc;
+}
+
+}  // namespace gh
+
+extern "C" {
+
+int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* g, const int* prompts, int batch, int n_prompt,
+                              int max_new, int* out_ids, int* out_len, float* step_logits, float* timing_ms,
+                              int flags) {
+    GH_REQUIRE(out_len, "gorch_hip_generate_cached: null out_len");
+    // rows are n_prompt + max_new wide before truncation; this entry point
+    // has no stop token, so every row has the same length: repack densely
+    const int rc = generate_impl(stream, g, prompts, batch, n_prompt, max_new, -1, out_ids, nullptr, out_len,
+                                 step_logits, timing_ms, flags);
+    if (rc) return rc;
+    const int np = n_prompt > g->max_seq ? g->max_seq : n_prompt, width = np + max_new, len = *out_len;
+    for (int b = 1; b < batch; b++)
+        std::memmove(out_ids + (size_t)b * len, out_ids + (size_t)b * width, (size_t)len * sizeof(int));
+    return GORCH_HIP_OK;
+}
+
+int gorch_hip_generate(void* stream, gorch_hip_gpt* g, const int* prompts, int batch, int n_prompt,
+                       const gorch_hip_generate_config* cfg, int* out_ids, int* out_lens, float* step_logits,
+                       float* timing_ms) {
+    GH_REQUIRE(cfg && out_lens, "gorch_hip_generate: null config or out_lens");
+    if (!cfg->use_kv_cache || cfg->temperature != 0.0f) {
+        set_error("gorch_hip_generate: only greedy decoding with the KV cache runs here (Temperature 0, UseKVCache)");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
+    return generate_impl(stream, g, prompts, batch, n_prompt, cfg->max_new_tokens, cfg->stop_token, out_ids,
+                         out_lens, nullptr, step_logits, timing_ms, cfg->flags);
 }
 
 }  // extern "C"

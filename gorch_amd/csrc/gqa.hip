@@ -33,6 +33,7 @@ extern "C" int gorch_hip_gqa_forward_cached(void* stream, const gorch_hip_gqa_we
                                             int new_seq, float* k_cache, float* v_cache, int pos_offset,
                                             int max_seq, float* out, void* workspace, size_t workspace_bytes) {
     GH_REQUIRE(w && x && k_cache && v_cache && out && new_seq > 0, "gorch_hip_gqa_forward_cached: bad arguments");
+    GH_TRY(bf16_gate(stream_of(stream)));
     const int S = new_seq, nq = w->num_q, nkv = w->num_kv, hd = w->head_dim, d = w->dim;
     GH_REQUIRE(nq > 0 && nkv > 0 && hd > 0 && d > 0, "gorch/nn: GQAConfig fields must be positive");
     GH_REQUIRE(nq % nkv == 0, "gorch/nn: GQA NumQ must be divisible by NumKV");
@@ -80,5 +81,5 @@ extern "C" int gorch_hip_gqa_forward_cached(void* stream, const gorch_hip_gqa_we
     AttnArgs a{q, k_cache, v_cache, att, nullptr, pos_offset, S, qdim, hd, max_seq, qdim, w->causal ? 1 : 0,
                (float)(1.0 / sqrt((double)hd)), nkv, kvdim, 1};
     GH_TRY(launch_attn_cached(s, a, nq, S));
-    return launch_linear_bf16(s, att, w->wo, w->bo, nullptr, out, S, d, qdim, GORCH_HIP_EPI_NONE);
+    return finish(stream, launch_linear_bf16(s, att, w->wo, w->bo, nullptr, out, S, d, qdim, GORCH_HIP_EPI_NONE));
 }

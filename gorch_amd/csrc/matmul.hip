@@ -8,6 +8,8 @@
 //   - every other transpose/dtype combination: a simple tiled kernel that
 //     reads each operand through its own layout and dtype (correct for all
 //     shapes; not a hot path of the decode step).
+#include <algorithm>
+
 #include "common.h"
 
 namespace gh {
@@ -78,10 +80,11 @@ extern "C" int gorch_hip_linear_bf16_ex(void* stream, const float* x, const uint
         return GORCH_HIP_EUNSUPPORTED;
     }
     GH_REQUIRE((flags & ~GORCH_HIP_LINEAR_ACT_BF16) == 0, "gorch_hip_linear_bf16_ex: unknown flag");
+    GH_TRY(bf16_gate(stream_of(stream)));
     if (flags & GORCH_HIP_LINEAR_ACT_BF16)
-        return launch_gemm_bf16w(stream_of(stream), x, W, bias, residual, OutDesc::plain(y, N), M, N, K, epilogue,
-                                 true);
-    return launch_linear_bf16(stream_of(stream), x, W, bias, residual, y, M, N, K, epilogue);
+        return finish(stream, launch_gemm_bf16w(stream_of(stream), x, W, bias, residual, OutDesc::plain(y, N), M, N,
+                                                K, epilogue, true));
+    return finish(stream, launch_linear_bf16(stream_of(stream), x, W, bias, residual, y, M, N, K, epilogue));
 }
 
 extern "C" int gorch_hip_linear_bf16(void* stream, const float* x, const uint16_t* W, const float* bias,
@@ -100,7 +103,7 @@ extern "C" int gorch_hip_pack_bf16(void* stream, const uint16_t* W, uint16_t* Wp
     GH_REQUIRE(W && Wp, "gorch_hip_pack_bf16: null pointer");
     GH_REQUIRE(K % 8 == 0 && ((uintptr_t)W | (uintptr_t)Wp) % 16 == 0,
                "gorch_hip_pack_bf16: needs K % 8 == 0 and 16-byte aligned buffers");
-    return launch_pack_bf16(stream_of(stream), W, Wp, N, K);
+    return finish(stream, launch_pack_bf16(stream_of(stream), W, Wp, N, K));
 }
 
 extern "C" int gorch_hip_linear_bf16_packed(void* stream, const float* x, const uint16_t* Wp, const float* bias,
@@ -114,12 +117,24 @@ extern "C" int gorch_hip_linear_bf16_packed(void* stream, const float* x, const 
     GH_REQUIRE((const void*)x != (const void*)y, "gorch_hip_linear_bf16_packed: x must not alias y");
     GH_REQUIRE(K % 8 == 0 && ((uintptr_t)x | (uintptr_t)Wp) % 16 == 0,
                "gorch_hip_linear_bf16_packed: needs K % 8 == 0 and 16-byte aligned x and Wp");
-    return launch_linear_packed_od(stream_of(stream), x, Wp, bias, residual, OutDesc::plain(y, N), M, N, K,
-                                   epilogue, LinearExtras{});
+    GH_TRY(bf16_gate(stream_of(stream)));
+    return finish(stream, launch_linear_packed_od(stream_of(stream), x, Wp, bias, residual, OutDesc::plain(y, N), M,
+                                                  N, K, epilogue, LinearExtras{}));
 }
 
-static int matmul_dt_impl(void* stream, const void* A, const void* B, float* C, uint32_t M, uint32_t N,
-                          uint32_t K, uint32_t batch, int transA, int transB, int aBF16, int bBF16) {
+// C = 0 for an empty contraction (K == 0), as a kernel rather than a memset
+// so that a captured graph holds no memset node
+__global__ void k_fill_zero(float* __restrict__ c, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        c[i] = 0.f;
+}
+
+namespace gh {
+
+// The matmul_dt routing without the probe gate (the probe itself runs
+// through it).
+int matmul_dt_raw(hipStream_t s, const void* A, const void* B, float* C, uint32_t M, uint32_t N, uint32_t K,
+                  uint32_t batch, int transA, int transB, int aBF16, int bBF16) {
     if (transA && transB) {
         set_error("gorch_hip_matmul_dt: transA && transB is not supported");
         return GORCH_HIP_EUNSUPPORTED;
@@ -128,8 +143,13 @@ static int matmul_dt_impl(void* stream, const void* A, const void* B, float* C, 
     GH_REQUIRE(A && B && C, "gorch_hip_matmul_dt: null pointer");
     GH_REQUIRE(M < (1u << 30) && N < (1u << 30) && K < (1u << 30) && batch < 65536,
                "gorch_hip_matmul_dt: dimension too large");
-    hipStream_t s = stream_of(stream);
-    if (K == 0) return check(hipMemsetAsync(C, 0, (size_t)batch * M * N * sizeof(float), s), "memset");
+    if (K == 0) {
+        const size_t n = (size_t)batch * M * N;
+        const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+        hipLaunchKernelGGL(k_fill_zero, dim3(blocks), dim3(256), 0, s, C, n);
+        count(CNT_ELEMENTWISE);
+        return check_launch("fill_zero");
+    }
     if (!transA && transB && !aBF16 && bBF16 && linear_fast_ok(A, B, (int)K)) {
         for (uint32_t b = 0; b < batch; b++) {
             const float* a = reinterpret_cast<const float*>(A) + (size_t)b * M * K;
@@ -147,13 +167,18 @@ static int matmul_dt_impl(void* stream, const void* A, const void* B, float* C, 
     return check_launch("matmul_generic");
 }
 
+}  // namespace gh
+
 extern "C" int gorch_hip_matmul_dt(void* stream, const void* A, const void* B, float* C, uint32_t M,
                                    uint32_t N, uint32_t K, int transA, int transB, int aBF16, int bBF16) {
-    return matmul_dt_impl(stream, A, B, C, M, N, K, 1, transA, transB, aBF16, bBF16);
+    if (aBF16 || bBF16) GH_TRY(bf16_gate(stream_of(stream)));
+    return finish(stream, matmul_dt_raw(stream_of(stream), A, B, C, M, N, K, 1, transA, transB, aBF16, bBF16));
 }
 
 extern "C" int gorch_hip_batched_matmul_dt(void* stream, const void* A, const void* B, float* C, uint32_t M,
                                            uint32_t N, uint32_t K, uint32_t batch, int transA, int transB,
                                            int aBF16, int bBF16) {
-    return matmul_dt_impl(stream, A, B, C, M, N, K, batch, transA, transB, aBF16, bBF16);
+    if (aBF16 || bBF16) GH_TRY(bf16_gate(stream_of(stream)));
+    return finish(stream,
+                  matmul_dt_raw(stream_of(stream), A, B, C, M, N, K, batch, transA, transB, aBF16, bBF16));
 }

@@ -550,6 +550,7 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
     GH_REQUIRE(d % 8 == 0 && F % 8 == 0, "gorch_hip_moe_forward: dim and ffn must be multiples of 8");
     GH_REQUIRE(w->wgate && w->wup && w->wdown, "gorch_hip_moe_forward: null expert weights");
     GH_REQUIRE(logits || w->wr, "gorch_hip_moe_forward: need router weights or injected logits");
+    GH_TRY(bf16_gate(stream_of(stream)));
     const size_t need = moe_layout(M, d, F, E, K, nullptr, nullptr);
     GH_REQUIRE(workspace && workspace_bytes >= need, "gorch_hip_moe_forward: workspace too small");
     MoeWs ws;
@@ -620,5 +621,5 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
                        cslice, w->bdown, ws.perm_w);
     GH_TRY(check_launch("moe_combine"));
     count(CNT_MOE);
-    return GORCH_HIP_OK;
+    return finish(stream, GORCH_HIP_OK);
 }

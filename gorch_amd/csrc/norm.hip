@@ -291,7 +291,7 @@ extern "C" int gorch_hip_layernorm(void* stream, const float* x, const float* ga
     GH_REQUIRE(M >= 0 && N > 0, "gorch_hip_layernorm: bad shape");
     if (M == 0) return GORCH_HIP_OK;
     GH_REQUIRE(x && gamma && beta && y, "gorch_hip_layernorm: null pointer");
-    return launch_layernorm(stream_of(stream), x, gamma, beta, y, M, N, eps, N);
+    return finish(stream, launch_layernorm(stream_of(stream), x, gamma, beta, y, M, N, eps, N));
 }
 
 extern "C" int gorch_hip_add_rmsnorm(void* stream, const float* x, const float* b, const float* gamma, float* sum,
@@ -310,7 +310,7 @@ extern "C" int gorch_hip_add_rmsnorm(void* stream, const float* x, const float* 
     else if (N <= 1024) hipLaunchKernelGGL(k_rmsnorm_rows<4>, grid, dim3(256), 0, s, x, gamma, y, M, N, eps, b, sum);
     else hipLaunchKernelGGL(k_rmsnorm_rows<8>, grid, dim3(256), 0, s, x, gamma, y, M, N, eps, b, sum);
     count(CNT_NORM);
-    return check_launch("add_rmsnorm");
+    return finish(stream, check_launch("add_rmsnorm"));
 }
 
 extern "C" int gorch_hip_rmsnorm(void* stream, const float* x, const float* gamma, float* y, int M, int N,
@@ -318,5 +318,5 @@ extern "C" int gorch_hip_rmsnorm(void* stream, const float* x, const float* gamm
     GH_REQUIRE(M >= 0 && N > 0, "gorch_hip_rmsnorm: bad shape");
     if (M == 0) return GORCH_HIP_OK;
     GH_REQUIRE(x && gamma && y, "gorch_hip_rmsnorm: null pointer");
-    return launch_rmsnorm(stream_of(stream), x, gamma, y, M, N, eps);
+    return finish(stream, launch_rmsnorm(stream_of(stream), x, gamma, y, M, N, eps));
 }

@@ -159,7 +159,7 @@ extern "C" int gorch_hip_rope_tables(void* stream, int head_dim, int max_seq, fl
     hipLaunchKernelGGL(k_rope_tables, dim3(grid_for(n)), dim3(256), 0, stream_of(stream), head_dim, max_seq, base,
                        cos_t, sin_t);
     count(CNT_ELEMENTWISE);
-    return check_launch("rope_tables");
+    return finish(stream, check_launch("rope_tables"));
 }
 
 extern "C" int gorch_hip_rope_apply(void* stream, const float* x, float* y, int outer, int seq_len, int head_dim,
@@ -174,5 +174,5 @@ extern "C" int gorch_hip_rope_apply(void* stream, const float* x, float* y, int 
     hipLaunchKernelGGL(k_rope_apply, dim3(grid_for(n)), dim3(256), 0, stream_of(stream), x, y,
                        (int64_t)outer * seq_len, seq_len, head_dim / 2, start_pos, cos_t, sin_t, neox, sign);
     count(CNT_ELEMENTWISE);
-    return check_launch("rope_apply");
+    return finish(stream, check_launch("rope_apply"));
 }

@@ -45,6 +45,16 @@ SIGNATURES = {
     "gorch_hip_upload": (i32, [vp, vp, vp, C.c_size_t]),
     "gorch_hip_download": (i32, [vp, vp, vp, C.c_size_t]),
     "gorch_hip_sync": (i32, [vp]),
+    "gorch_hip_live_bytes": (C.c_longlong, []),
+    "gorch_hip_buf_new": (vp, [C.c_size_t, i32]),
+    "gorch_hip_buf_release": (None, [vp]),
+    "gorch_hip_buf_len": (C.c_size_t, [vp]),
+    "gorch_hip_buf_device": (vp, [vp, vp, i32]),
+    "gorch_hip_buf_host": (vp, [vp, vp, i32]),
+    "gorch_hip_set_async": (i32, [i32]),
+    "gorch_hip_async_enabled": (i32, []),
+    "gorch_hip_bf16_matmul_supported": (i32, []),
+    "gorch_hip_bf16_probe": (i32, []),
     "gorch_hip_read_dispatch_counts": (i32, [C.POINTER(C.c_uint64), i32]),
     "gorch_hip_reset_dispatch_counts": (None, []),
     "gorch_hip_bf16_to_f32": (i32, [vp, vp, vp, i64]),
@@ -93,6 +103,7 @@ SIGNATURES = {
     "gorch_hip_kvcache_read": (i32, [vp, i32, i32, vp, vp]),
     "gorch_hip_gpt_forward_cached": (i32, [vp, vp, vp, vp, i32, vp]),
     "gorch_hip_generate_cached": (i32, [vp, vp, vp, i32, i32, i32, vp, vp, vp, vp, i32]),
+    "gorch_hip_generate": (i32, [vp, vp, vp, i32, i32, vp, vp, vp, vp, vp]),
 }
 
 
@@ -154,6 +165,65 @@ def dispatch_counts() -> dict:
 
 def reset_dispatch_counts() -> None:
     lib().gorch_hip_reset_dispatch_counts()
+
+
+def set_async(on: bool) -> None:
+    """SetMetalAsync (metal_async.go:30-34): off makes every compute call wait."""
+    _ok(lib().gorch_hip_set_async(int(on)))
+
+
+def async_enabled() -> bool:
+    return bool(lib().gorch_hip_async_enabled())
+
+
+def bf16_matmul_supported() -> bool:
+    """MetalBF16MatMulSupported (bf16_matmul.go:52-59) for the current device."""
+    return bool(lib().gorch_hip_bf16_matmul_supported())
+
+
+def bf16_probe() -> bool:
+    """Runs the bf16 matmul probe again; returns its verdict."""
+    return bool(lib().gorch_hip_bf16_probe())
+
+
+BUF_HOST_MIRROR = 1
+
+
+class Buffer:
+    """A device buffer handle (metal.Buffer, metal/metal.go:240-422):
+    ``bytes`` of zero-filled HBM, optionally with a pinned host mirror.
+    ``release()`` is idempotent; the handle is also released when collected
+    (the reference's finaliser)."""
+
+    def __init__(self, nbytes: int, host_mirror: bool = False):
+        self.h = lib().gorch_hip_buf_new(nbytes, BUF_HOST_MIRROR if host_mirror else 0)
+        if not self.h:
+            raise HipError(4, last_error())
+
+    def __len__(self):
+        return lib().gorch_hip_buf_len(self.h)
+
+    def device(self, will_write: bool = False, stream=None) -> int:
+        p = lib().gorch_hip_buf_device(stream, self.h, int(will_write))
+        if not p:
+            raise HipError(2, last_error())
+        return p
+
+    def host(self, will_write: bool = False, stream=None) -> int:
+        """Data(): waits for ``stream`` and returns the current host mirror."""
+        p = lib().gorch_hip_buf_host(stream, self.h, int(will_write))
+        if not p:
+            raise HipError(2, last_error())
+        return p
+
+    def release(self) -> None:
+        lib().gorch_hip_buf_release(self.h)
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
 
 
 # ------------------------------------------------------------------ codec
@@ -334,6 +404,12 @@ class SafeTensors:
             pass
 
 
+class GenerateConfig(C.Structure):
+    """gorch_hip_generate_config: GenerateConfig (model/generate.go:13-20)."""
+    _fields_ = [("max_new_tokens", C.c_int), ("temperature", C.c_float), ("top_k", C.c_int),
+                ("top_p", C.c_float), ("stop_token", C.c_int), ("use_kv_cache", C.c_int), ("flags", C.c_int)]
+
+
 class GPT:
     """gorch's nn.GPT on the GPU (nn/gpt.go:12-121). ``weights`` is a dict
     of numpy arrays in the layout gorch_amd.synthetic produces (Linear
@@ -408,6 +484,26 @@ class GPT:
                                             timing, int(use_graph)))
         L = out_len.value
         ids = out.reshape(-1)[: B * L].reshape(B, L).copy()
+        return ids, logits, {"prefill_ms": timing[0], "decode_ms": timing[1], "decode_forwards": int(timing[2])}
+
+    def generate(self, prompts, max_new: int, stop_token: int = -1, want_logits=False, use_graph=True):
+        """GenerateWithConfig(GreedyConfig(max_new) + StopToken, UseKVCache)
+        (model/generate.go:52-131) for [batch, n_prompt] prompts. Returns (a
+        list of per-sequence id arrays, step logits or None, timing dict)."""
+        import numpy as np
+
+        prompts = np.ascontiguousarray(np.atleast_2d(prompts), np.int32)
+        B, n = prompts.shape
+        width = min(n, self.cfg["max_seq"]) + max_new
+        out = np.zeros((B, width), np.int32)
+        lens = np.zeros(B, np.int32)
+        cfg = GenerateConfig(max_new, 0.0, 0, 0.0, stop_token, 1, int(use_graph))
+        V = self.cfg["vocab"]
+        logits = np.empty((max_new, B, V), np.float32) if want_logits else None
+        timing = (C.c_float * 3)()
+        _ok(lib().gorch_hip_generate(None, self.h, prompts.ctypes.data, B, n, C.byref(cfg), out.ctypes.data,
+                                     lens.ctypes.data, None if logits is None else logits.ctypes.data, timing))
+        ids = [out[b, :lens[b]].copy() for b in range(B)]
         return ids, logits, {"prefill_ms": timing[0], "decode_ms": timing[1], "decode_forwards": int(timing[2])}
 
     def close(self):

@@ -50,15 +50,62 @@ int gorch_hip_device_count(void);
  * pattern, metal/shim.m:1018). Never NULL. */
 const char* gorch_hip_last_error(void);
 /* Device allocation (metal_new_buffer, metal/shim.h:38-41). NULL on
- * failure. Release is idempotent for NULL (metal_release_buffer). */
+ * failure. gorch_hip_release (metal_release_buffer) ignores NULL and any
+ * pointer that is not a live allocation of this library, so a repeated
+ * release of the same pointer is harmless until the address is handed out
+ * again; it waits for queued work first. Callers that can release from
+ * several threads (an explicit Release racing a finaliser) use the buffer
+ * handles below, whose release is exactly-once. */
 void* gorch_hip_alloc(size_t bytes);
 void gorch_hip_release(void* ptr);
+/* Bytes held by live allocations and buffers (liveBufferBytes,
+ * metal/metal.go:363-368). */
+long long gorch_hip_live_bytes(void);
+
+/* Buffer handles (metal.Buffer, metal/metal.go:240-422; Tensor.ToMetal /
+ * Data, tensor.go:318-406). Device memory of exactly `bytes`, zero-filled;
+ * with GORCH_HIP_BUF_HOST_MIRROR also a pinned host copy, the discrete-GPU
+ * stand-in for Metal's unified memory: gorch_hip_buf_host is the Data()
+ * read barrier (waits for `stream`, copies the device contents down if a
+ * kernel may have written them since), gorch_hip_buf_device brings the
+ * device copy up to date after host writes through the mirror. Pass
+ * will_write = 1 when the caller (host) or the kernel it is about to queue
+ * (device) writes the buffer, so the other copy is refreshed before its next
+ * use. Handles are never reused: gorch_hip_buf_release is idempotent and
+ * thread-safe (Buffer.Release's CompareAndSwap, metal/metal.go:405-422),
+ * and the memory is freed once no call is using it. */
+typedef struct gorch_hip_buf gorch_hip_buf;
+#define GORCH_HIP_BUF_HOST_MIRROR 1
+gorch_hip_buf* gorch_hip_buf_new(size_t bytes, int flags);
+void gorch_hip_buf_release(gorch_hip_buf* buf);
+size_t gorch_hip_buf_len(gorch_hip_buf* buf);
+void* gorch_hip_buf_device(void* stream, gorch_hip_buf* buf, int will_write);
+void* gorch_hip_buf_host(void* stream, gorch_hip_buf* buf, int will_write);
 /* Host<->device copies, ordered on `stream`; they return after the copy
  * completes (the Data() read barrier, tensor.go:318-323). */
 int gorch_hip_upload(void* stream, void* dst_device, const void* src_host, size_t bytes);
 int gorch_hip_download(void* stream, void* dst_host, const void* src_device, size_t bytes);
 /* Waits for all work on `stream` (metal_finish / metal_sync_queue). */
 int gorch_hip_sync(void* stream);
+/* Dispatch mode (SetMetalAsync / MetalAsyncEnabled, metal_async.go:30-38):
+ * on (the default here), compute entry points return once their work is
+ * queued on the stream, and the caller synchronises at read barriers
+ * (gorch_hip_sync, gorch_hip_download, gorch_hip_buf_host). Off, every
+ * compute entry point waits for its stream before returning (the Metal
+ * shim's per-op wait). Turning it off first drains the device. */
+int gorch_hip_set_async(int on);
+int gorch_hip_async_enabled(void);
+/* The bf16 matmul self-probe (MetalBF16MatMulSupported / runBF16MatMulProbe,
+ * bf16_matmul.go:52-112): a 16x16x16 bf16 x bf16 and bf16 x f32 product
+ * through the matmul path against a host f32 product, every element within
+ * 1e-3. It runs once per device in gorch_hip_init (or at the first bf16 call
+ * on a device that was not initialised). While it has failed, every entry
+ * point with bf16 weights returns GORCH_HIP_EUNSUPPORTED, the signal to take
+ * the CPU path (bf16MatMulEligible, :116-119). _supported returns 1 when the
+ * probe passed on the current device; gorch_hip_bf16_probe runs it again
+ * and returns the new verdict. */
+int gorch_hip_bf16_matmul_supported(void);
+int gorch_hip_bf16_probe(void);
 /* Dispatch counters (ReadMetalDispatchCounts / Reset, ops.go:49-78):
  * fills up to `n` slots in the order gemv, gemm, generic_matmul, attention,
  * norm, elementwise, moe, argmax, codec; returns the number of slots. */
@@ -341,6 +388,32 @@ int gorch_hip_gpt_forward_cached(void* stream, gorch_hip_gpt* gpt, gorch_hip_kvc
 int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* gpt, const int* prompts, int batch, int n_prompt,
                               int max_new, int* out_ids, int* out_len, float* step_logits, float* timing_ms,
                               int flags);
+
+/* GenerateConfig (model/generate.go:13-42). Only greedy decoding with the
+ * KV cache runs on this path: temperature must be 0 and use_kv_cache 1
+ * (else GORCH_HIP_EUNSUPPORTED: sampling stays on the caller's CPU path);
+ * top_k / top_p are ignored as in greedy mode. stop_token -1 disables the
+ * stop. flags bit 0: replay the decode step from a HIP graph. */
+typedef struct {
+    int max_new_tokens;
+    float temperature;
+    int top_k;
+    float top_p;
+    int stop_token;
+    int use_kv_cache;
+    int flags;
+} gorch_hip_generate_config;
+/* GenerateWithConfig with UseKVCache (generateCached, model/generate.go:94-131)
+ * for `batch` prompts: each sequence stops on its own at stop_token (which
+ * is not kept), after max_new_tokens, or once its cache holds MaxSeq tokens.
+ * out_ids (host int32 [batch, min(n_prompt, MaxSeq) + max_new_tokens])
+ * receives each sequence's (truncated) prompt and new tokens, row b valid up
+ * to out_lens[b]. step_logits and timing_ms as gorch_hip_generate_cached
+ * (timing_ms[2] counts the decode forwards run: generation ends once every
+ * sequence has stopped, checked every 8 steps). Synchronous. */
+int gorch_hip_generate(void* stream, gorch_hip_gpt* gpt, const int* prompts, int batch, int n_prompt,
+                       const gorch_hip_generate_config* cfg, int* out_ids, int* out_lens, float* step_logits,
+                       float* timing_ms);
 
 #ifdef __cplusplus
 }

@@ -69,7 +69,7 @@ def _load() -> C.CDLL:
         "orc_kvcache_values": (C.POINTER(C.c_float), [vp, C.c_int]),
         "orc_gpt_forward_cached": (C.c_int, [vp, vp, i32p, C.c_int, f32p]),
         "orc_gpt_forward": (C.c_int, [vp, i32p, C.c_int, f32p]),
-        "orc_generate_cached": (C.c_int, [vp, i32p, C.c_int, C.c_int, i32p, vp, vp]),
+        "orc_generate_cached": (C.c_int, [vp, i32p, C.c_int, C.c_int, C.c_int, i32p, vp, vp]),
         "orc_moe_forward": (C.c_int, [vp, f32p, C.c_int, vp, f32p, vp, vp]),
         "orc_gqa_forward_cached": (C.c_int, [vp, f32p, f32p, C.c_int, f32p, C.c_int, f32p]),
     }
@@ -331,13 +331,13 @@ class GPT:
             raise ValueError("gorch: sequence length exceeds MaxSeq")
         return out
 
-    def generate_cached(self, prompt, max_new, want_logits=False):
+    def generate_cached(self, prompt, max_new, want_logits=False, stop_token=-1):
         prompt = np.ascontiguousarray(prompt, np.int32)
         out = np.empty(prompt.size + max_new, np.int32)
         V = self.cfg["vocab"]
         logits = np.empty((max_new, V), np.float32) if want_logits else None
         gaps = np.empty(max_new, np.float32)
-        n = lib.orc_generate_cached(self.ref, prompt, prompt.size, max_new, out,
+        n = lib.orc_generate_cached(self.ref, prompt, prompt.size, max_new, stop_token, out,
                                     _ptr(logits), _ptr(gaps))
         return out[:n].copy(), logits, gaps
 

@@ -607,7 +607,7 @@ static float top2_gap(const float* row, int n) {
 
 /* model/generate.go:94-131 with Temperature 0 and no stop token. */
 int orc_generate_cached(const orc_gpt_weights* w, const int* prompt, int n_prompt,
-                        int max_new, int* out_ids, float* step_logits, float* gaps) {
+                        int max_new, int stop_token, int* out_ids, float* step_logits, float* gaps) {
     int V = w->vocab;
     orc_kvcache* cache = orc_kvcache_new(w->layers, w->dim, w->max_seq);
     const int* p = prompt;
@@ -624,6 +624,8 @@ int orc_generate_cached(const orc_gpt_weights* w, const int* prompt, int n_promp
         int next = orc_argmax(last, V);
         if (step_logits) memcpy(step_logits + (int64_t)i * V, last, (size_t)V * sizeof(float));
         if (gaps) gaps[i] = top2_gap(last, V);
+        /* StopToken (:116-118): the stop token is not kept */
+        if (stop_token >= 0 && next == stop_token) break;
         out_ids[n_out++] = next;
         if (orc_kvcache_len(cache) >= w->max_seq) break;
         orc_gpt_forward_cached(w, cache, &next, 1, last);

@@ -119,9 +119,10 @@ int orc_gpt_forward(const orc_gpt_weights* w, const int* ids, int n, float* logi
  * (prompt + new tokens) to out_ids (capacity n_prompt + max_new) and returns
  * its length. If step_logits is non-null, row i receives the logits that
  * chose new token i ([max_new, vocab]). If gaps is non-null, gaps[i] is the
- * top-1 minus top-2 logit of that row. */
+ * top-1 minus top-2 logit of that row. stop_token >= 0 ends generation
+ * when it is chosen (it is not appended). */
 int orc_generate_cached(const orc_gpt_weights* w, const int* prompt, int n_prompt,
-                        int max_new, int* out_ids, float* step_logits, float* gaps);
+                        int max_new, int stop_token, int* out_ids, float* step_logits, float* gaps);
 
 /* ---- GQA with KV cache (nn/gqa.go:213-363) ----
  * Linear weights [out, in] (bf16 when linear_bf16, else f32), biases

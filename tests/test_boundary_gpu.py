@@ -127,3 +127,92 @@ def test_codec_on_raw_pointers(lib):
     assert np.array_equal(dn.get(np.uint16, f.shape), orc.f32_to_bf16(f))
     for t in (dh, df, dff, dn):
         t.free()
+
+
+def test_bf16_probe_gates_the_matmul_path(gpu, lib, monkeypatch):
+    """MetalBF16MatMulSupported / bf16MatMulEligible (bf16_matmul.go:52-119):
+    the probe passes on a healthy device; when its host-side check rejects
+    the result (the comparison tolerance forced negative), every bf16 matmul
+    entry point returns GORCH_HIP_EUNSUPPORTED, the caller's cue to take its
+    CPU path, while f32 x f32 still runs; a passing probe re-enables them."""
+    assert gpu.bf16_matmul_supported()
+    M, N, K = 4, 64, 64
+    x, W, b = syn.gemv_inputs(M, K, N, seed=5)
+    dx, dW, dy = up(lib, x), up(lib, W), Dev(lib, M * N * 4)
+    Wf = up(lib, orc.bf16_to_f32(W))
+    try:
+        monkeypatch.setenv("GORCH_HIP_BF16_PROBE_TOL", "-1")
+        assert not gpu.bf16_probe()
+        assert not gpu.bf16_matmul_supported()
+        assert lib.gorch_hip_linear_bf16(None, dx.p, dW.p, None, None, dy.p, M, N, K, 0) == 1
+        assert lib.gorch_hip_matmul_dt(None, dx.p, dW.p, dy.p, M, N, K, 0, 1, 0, 1) == 1
+        assert "probe" in lib.gorch_hip_last_error().decode()
+        # no bf16 operand: not gated
+        assert lib.gorch_hip_matmul_dt(None, dx.p, Wf.p, dy.p, M, N, K, 0, 1, 0, 0) == 0
+    finally:
+        monkeypatch.delenv("GORCH_HIP_BF16_PROBE_TOL")
+        assert gpu.bf16_probe()
+    assert lib.gorch_hip_linear_bf16(None, dx.p, dW.p, None, None, dy.p, M, N, K, 0) == 0
+    assert rel_err(dy.get(np.float32, (M, N)), orc.linear(x, W)) <= 1e-3
+    for t in (dx, dW, dy, Wf):
+        t.free()
+
+
+def test_buffer_handles_host_mirror(gpu, lib):
+    """Buffer handles as gorch's Tensor would hold them (ToMetal, Data(),
+    Release; tensor.go:318-406, metal/metal.go:405-422): zero-filled on
+    creation, host writes reach the device before its next use, kernel
+    writes reach the host at the Data() barrier, release is exactly-once."""
+    M, N, K = 3, 96, 128
+    x, W, b = syn.gemv_inputs(M, K, N, seed=9)
+    live0 = lib.gorch_hip_live_bytes()
+    bx = gpu.Buffer(x.nbytes, host_mirror=True)
+    bw = gpu.Buffer(W.nbytes, host_mirror=True)
+    by = gpu.Buffer(M * N * 4, host_mirror=True)
+    assert len(bx) == x.nbytes
+    assert lib.gorch_hip_live_bytes() - live0 == x.nbytes + W.nbytes + M * N * 4
+    # fresh buffers read back as zeros
+    z = np.ctypeslib.as_array(C.cast(by.host(), C.POINTER(C.c_float)), shape=(M * N,))
+    assert not z.any()
+    # the caller fills the mirrors (Data() with intent to write) ...
+    C.memmove(bx.host(will_write=True), x.ctypes.data, x.nbytes)
+    C.memmove(bw.host(will_write=True), W.ctypes.data, W.nbytes)
+    # ... and the kernel reads the device copies, which are brought up to date
+    rc = lib.gorch_hip_linear_bf16(None, bx.device(), bw.device(), None, None, by.device(will_write=True),
+                                   M, N, K, 0)
+    assert rc == 0
+    got = np.ctypeslib.as_array(C.cast(by.host(), C.POINTER(C.c_float)), shape=(M, N)).copy()
+    assert rel_err(got, orc.linear(x, W)) <= 1e-3
+    # a buffer without a mirror has no host view
+    plain = gpu.Buffer(64)
+    with pytest.raises(gpu.HipError):
+        plain.host()
+    for buf in (bx, bw, by, plain):
+        buf.release()
+        buf.release()                      # exactly-once: the second is a no-op
+    assert lib.gorch_hip_live_bytes() == live0
+    with pytest.raises(gpu.HipError):
+        bx.device()                        # released handles are unknown
+    lib.gorch_hip_buf_release(None)
+
+
+def test_sync_dispatch_mode(gpu, lib):
+    """SetMetalAsync(false) (metal_async.go:30-38): every compute call waits
+    for its stream before returning; results are the same in both modes."""
+    M, N, K = 2, 512, 256
+    x, W, b = syn.gemv_inputs(M, K, N, seed=11)
+    dx, dW, db, dy = up(lib, x), up(lib, W), up(lib, b), Dev(lib, M * N * 4)
+    assert gpu.async_enabled()
+    try:
+        gpu.set_async(False)
+        assert not gpu.async_enabled()
+        assert lib.gorch_hip_linear_bf16(None, dx.p, dW.p, db.p, None, dy.p, M, N, K, 0) == 0
+        # no gorch_hip_sync: the call itself waited
+        host = np.empty((M, N), np.float32)
+        assert lib.gorch_hip_download(None, host.ctypes.data, dy.p, host.nbytes) == 0
+        assert rel_err(host, orc.linear(x, W, b)) <= 1e-3
+    finally:
+        gpu.set_async(True)
+    assert gpu.async_enabled()
+    for t in (dx, dW, db, dy):
+        t.free()

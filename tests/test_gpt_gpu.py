@@ -239,3 +239,30 @@ def test_generate_gpt2_xl_width_batch16(gpu):
     assert np.array_equal(ids_graph, ids)
     assert t["decode_forwards"] == steps
     g.close()
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_generate_stop_token(tiny, use_graph):
+    """GenerateConfig.StopToken (model/generate.go:116-118) per sequence: each
+    sequence ends before the first occurrence of the stop token, which it
+    does not keep; sequences that never produce it run to max_new. The
+    token is chosen from the oracle's own unstopped runs so that it occurs
+    in some sequences and not in others."""
+    w, g, o = tiny
+    prompts = np.stack([syn.prompt_ids(5, TINY["vocab"], seed=90 + b) for b in range(4)])
+    runs = [o.generate_cached(prompts[b], 20)[0][5:] for b in range(4)]
+    counts = np.zeros(TINY["vocab"], int)
+    for r in runs:
+        counts[np.unique(r)] += 1
+    cand = [t for t in range(TINY["vocab"]) if 0 < counts[t] < 4]
+    stop = cand[0] if cand else int(runs[0][3])
+    ids, _, t = g.generate(prompts, 20, stop_token=stop, use_graph=use_graph)
+    for b in range(4):
+        ref, _, _ = o.generate_cached(prompts[b], 20, stop_token=stop)
+        assert list(ids[b]) == list(ref), b
+    if all(stop in r for r in runs):
+        assert t["decode_forwards"] < 20
+    # no stop token: the same as generate_cached
+    ids2, _, _ = g.generate(prompts, 20, use_graph=use_graph)
+    full, _, _ = g.generate_cached(prompts, 20, use_graph=use_graph)
+    assert all(np.array_equal(ids2[b], full[b]) for b in range(4))

@@ -334,6 +334,27 @@ def test_gpt_generate_stops_at_max_seq(tiny):
     assert len(toks) == TINY["max_seq"] + 1
 
 
+def test_gpt_generate_stop_token(tiny):
+    # model/generate.go:116-118 against the uncached greedy sequence built by
+    # argmax over full forwards: generation ends at the first occurrence of
+    # the stop token, which is not kept; a token never chosen changes nothing
+    w, g = tiny
+    prompt = syn.prompt_ids(5, TINY["vocab"], seed=17)
+    seq = list(prompt)
+    for _ in range(12):
+        seq.append(int(np.argmax(g.forward(np.array(seq, np.int32))[-1])))
+    new = seq[len(prompt):]
+    stop = new[4]
+    first = new.index(stop)
+    toks, _, _ = g.generate_cached(prompt, 12, stop_token=stop)
+    assert list(toks) == seq[:len(prompt) + first]
+    unused = next(t for t in range(TINY["vocab"]) if t not in new)
+    toks, _, _ = g.generate_cached(prompt, 12, stop_token=unused)
+    assert list(toks) == seq
+    toks, _, _ = g.generate_cached(prompt, 12, stop_token=new[0])
+    assert list(toks) == list(prompt)
+
+
 def test_gpt_max_seq_error(tiny):
     w, g = tiny
     with pytest.raises(ValueError):
