@@ -44,6 +44,10 @@ struct LinearExtras {
     int ksplit = 1;
     int kslice = 0;    // K per slice (set by the launcher)
     int split_nt = 0;  // 16-row tiles per block in split mode (0: 4)
+    // caller-provided device scratch for the narrow-weight K split (null:
+    // the stream's scratch); a split that needs more fails with EINVAL
+    float* scratch = nullptr;
+    size_t scratch_bytes = 0;
 };
 // Number of K slices a K-split Linear actually uses for a requested count
 // (slices are multiples of 32 wide).
@@ -81,12 +85,18 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
                           const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
                           const LinearExtras& ex);
 
+// Per-device address of the no-allocation entry point's scratch array,
+// looked up once per device (gorch_hip_init or that entry point's first
+// call on the device).
+int noalloc_setup(int device);
+
 // End of a compute entry point: in sync mode (gorch_hip_set_async(0)) waits
 // for the stream when rc is 0 and the stream is not being captured.
 int finish(void* stream, int rc);
 // GORCH_HIP_EUNSUPPORTED unless the bf16 matmul probe passed on the current
-// device (runs it first if gorch_hip_init has not).
-int bf16_gate(hipStream_t s);
+// device (runs it first if gorch_hip_init has not and may_probe is set; the
+// probe allocates).
+int bf16_gate(hipStream_t s, bool may_probe = true);
 
 // Dispatch counters (the gorch ReadMetalDispatchCounts analogue).
 enum Counter {

@@ -1359,7 +1359,16 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
         const int nt = ntiles_all >= 128 ? split_nt_wide : 2;
         const int blocks_per_slice = (ntiles_all + nt - 1) / nt;
         const int S = ksplit_slices(K, std::min(kEpiSlices, std::max(2, split_blocks / blocks_per_slice)));
-        void* part = S >= 2 ? stream_scratch(s, (size_t)S * M * N * sizeof(float)) : nullptr;
+        void* part = nullptr;
+        if (S >= 2) {
+            const size_t need = (size_t)S * M * N * sizeof(float);
+            if (ex.scratch && need > ex.scratch_bytes) {
+                set_error("linear_bf16: the K split needs " + std::to_string(need) + " bytes of scratch, above the " +
+                          std::to_string(ex.scratch_bytes) + "-byte maximum");
+                return GORCH_HIP_EINVAL;
+            }
+            part = ex.scratch ? ex.scratch : stream_scratch(s, need);
+        }
         if (part) {
             LinearExtras sx = ex;
             sx.part = static_cast<float*>(part);

@@ -174,11 +174,15 @@ static int run_bf16_probe(int dev) {
     return verdict;
 }
 
-int bf16_gate(hipStream_t s) {
+int bf16_gate(hipStream_t s, bool may_probe) {
     int dev = 0;
     GH_TRY(check(hipGetDevice(&dev), "hipGetDevice"));
     if (dev < 0 || dev >= kMaxDevices) return GORCH_HIP_OK;
     int v = g_probe[dev].load(std::memory_order_acquire);
+    if (v == 0 && !may_probe) {
+        set_error("bf16 matmul probe has not run on this device: call gorch_hip_init first");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
     if (v == 0) {
         // not probed yet (gorch_hip_init runs the probe): probe now unless
         // the caller's stream is being captured into a graph
@@ -294,7 +298,7 @@ int gorch_hip_init(int device) {
         std::lock_guard<std::mutex> lock(g_probe_mu);
         if (g_probe[device].load(std::memory_order_acquire) == 0) (void)run_bf16_probe(device);
     }
-    return GORCH_HIP_OK;
+    return noalloc_setup(device);
 }
 
 const char* gorch_hip_last_error(void) { return t_error.c_str(); }

@@ -66,6 +66,7 @@ SIGNATURES = {
     "gorch_hip_packed_bf16_bytes": (C.c_size_t, [i32, i32]),
     "gorch_hip_pack_bf16": (i32, [vp, vp, vp, i32, i32]),
     "gorch_hip_linear_bf16_packed": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "gorch_hip_linear_bf16_noalloc": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32]),
     "gorch_hip_layernorm": (i32, [vp, vp, vp, vp, vp, i32, i32, f32]),
     "gorch_hip_rmsnorm": (i32, [vp, vp, vp, vp, i32, i32, f32]),
     "gorch_hip_add_rmsnorm": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, f32]),

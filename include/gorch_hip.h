@@ -172,6 +172,20 @@ int gorch_hip_pack_bf16(void* stream, const uint16_t* W, uint16_t* Wp, int N, in
 int gorch_hip_linear_bf16_packed(void* stream, const float* x, const uint16_t* Wp, const float* bias,
                                  const float* residual, float* y, int M, int N, int K, int epilogue);
 
+/* gorch_hip_linear_bf16 that allocates nothing. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results as gorch_hip_linear_bf16; the K-split
+ * partials of a narrow weight over a long K come from a fixed 1 MiB device
+ * array per GPU instead of a per-stream buffer the library allocates. A call
+ * whose split would need more returns GORCH_HIP_EINVAL (the routing never
+ * asks for more than 8 slices x 16 rows x 2032 columns). Calls that overlap
+ * on one GPU (unordered streams or threads) race on the array; calls ordered
+ * on one stream do not. Needs gorch_hip_init on the device first (it looks up
+ * the array's address and runs the bf16 probe, which allocates). */
+int gorch_hip_linear_bf16_noalloc(void* stream, const float* x, const uint16_t* W, const float* bias,
+                                  const float* residual, float* y, int M, int N, int K, int epilogue);
+
 /* ------------------------------------------------------------------------
  * Decode-step ops (the forward halves of gorch's op layer on this path).
  * ---------------------------------------------------------------------- */
