@@ -49,9 +49,10 @@ def parse():
                     help="restrict to one shape 'M,K,N' (for profiling one kernel)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the GPT decode legs")
-    ap.add_argument("--only", choices=("decode", "gemm", "decode-xl", "moe", "decode-qwen"), default=None,
+    ap.add_argument("--only", choices=("decode", "gemm", "decode-xl", "moe", "decode-qwen", "cpu-decode"),
+                    default=None,
                     help="run only one secondary leg and print its JSON (for profiling)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=9.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (PMC byte-counter calibration)")
     return ap.parse_args()
@@ -342,9 +343,47 @@ def qwen_leg(ctxs=(128, 512), steps=100):
         e1.synchronize()
         ms = e0.elapsed_time(e1) / steps
         out.append({"model": "qwen3-0.6b-shaped", "batch": 1, "ctx": ctx, "tok_s": round(1e3 / ms, 1),
-                    "ms_per_token": round(ms, 4), "weights": "bf16 N(0,0.02) random init on the device"})
+                    "ms_per_token": round(ms, 4), "weights": "bf16 N(0,0.02) random init on the device",
+                    "roofline": roofline_block(qwen_step_bytes(cfg, ctx), ms / 1e3,
+                                               "bf16 weights + tied head + gains once, K/V rows read "
+                                               "and written, logits; per token")})
         del g, cache
     return out
+
+
+def gpt_step_bytes(cfg, batch, ctx_mean):
+    """Algorithmic HBM bytes of one GPT decode step (every sequence forwards
+    one token): the bf16 Linear weights (fused QKV, Wo, FFN1, FFN2 per layer
+    and the LM head) and the f32 biases / LayerNorm parameters once each,
+    the embedding rows, the K and V cache rows read by attention (ctx_mean
+    keys per sequence and layer) and written for the new token, and the
+    logits written. Activations between kernels (a few KB per row) are left
+    out."""
+    d, V, L = cfg["dim"], cfg["vocab"], cfg["layers"]
+    weights = L * 2 * 12 * d * d + 2 * V * d
+    params = L * 4 * (3 * d + d + 4 * d + d + 4 * d) + 4 * 2 * d + 4 * V
+    emb = batch * 2 * d * 4
+    kv = batch * L * 2 * d * 4 * (ctx_mean + 1)
+    logits = batch * V * 4
+    return weights + params + emb + kv + logits
+
+
+def qwen_step_bytes(cfg, ctx):
+    """Algorithmic HBM bytes of one Qwen3-shaped decode token: the bf16
+    projection weights of every layer (Q, K, V, O, gate, up, down) and the
+    tied bf16 head once each, the f32 norm gains, the K/V cache rows read
+    (ctx + 1 keys per layer) and written, and the logits written."""
+    d, q, kv, inter, V, L = cfg.hidden, cfg.num_q * cfg.head_dim, cfg.kv_dim, cfg.inter, cfg.vocab, cfg.layers
+    weights = L * 2 * (q * d + 2 * kv * d + d * q + 3 * inter * d) + 2 * V * d
+    params = L * 4 * (2 * d + 2 * cfg.head_dim) + 4 * d
+    kvb = L * 2 * kv * 4 * (ctx + 2)
+    return weights + params + kvb + 4 * V
+
+
+def roofline_block(nbytes, seconds, what):
+    gbs = nbytes / seconds / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_step": int(nbytes), "bytes": what}
 
 
 def decode_leg(cfg_name, batch, n_prompt, max_new, reps=3):
@@ -367,36 +406,109 @@ def decode_leg(cfg_name, batch, n_prompt, max_new, reps=3):
     runs.sort(key=lambda t: t["decode_ms"])
     t = runs[len(runs) // 2]
     fwd = t["decode_forwards"]
+    step_s = t["decode_ms"] / 1e3 / fwd
+    # step i forwards the token at position n_prompt + i over n_prompt + i + 1 keys
+    nbytes = gpt_step_bytes(cfg, batch, n_prompt + (fwd - 1) / 2.0)
     return {"model": cfg_name, "batch": batch, "prompt": n_prompt, "new_tokens": max_new,
             "tok_s": round(batch * fwd / (t["decode_ms"] / 1e3), 1),
             "ms_per_step": round(t["decode_ms"] / fwd, 4), "prefill_ms": round(t["prefill_ms"], 3),
-            "weights": "bf16 N(0,0.02) random init, synthetic prompts"}
+            "weights": "bf16 N(0,0.02) random init, synthetic prompts",
+            "roofline": roofline_block(nbytes, step_s, "bf16 weights + f32 params once, K/V rows read at the "
+                                                        "mean context and written, embeddings, logits; per step")}
 
 
-def cpu_leg(shapes, seconds):
+def host_info():
+    """The CPU the baseline ran on: model name, logical CPUs, the CPUs this
+    process may use, and the thread count the box grants (OMP_NUM_THREADS)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or avail
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity": avail, "threads_granted": share}
+
+
+def cpu_leg(shapes, seconds, host):
     """The oracle (gorch CPU semantics: widen the bf16 weight per call, f32
-    sgemm, bias add) over the same 9 shapes, repeated for ~`seconds`."""
+    sgemm, bias add) over the same 9 shapes, repeated for ~`seconds` on the
+    threads the box grants this job, then for a third of that on one thread."""
     import oracle as orc
     from gorch_amd import synthetic as syn
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    threads = host["threads_granted"]
     inputs = [syn.gemv_inputs(M, K, N, seed=M * 131 + K + N) for (M, K, N) in shapes]
     step_bytes = sum(algo_bytes(M, K, N) for (M, K, N) in shapes)
     orc.set_widen_per_call(True)
-    for (x, W, b) in inputs:  # warm
-        orc.linear(x, W, b)
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        for (x, W, b) in inputs:
+
+    def sweep(nthreads, budget):
+        orc.set_threads(nthreads)
+        for (x, W, b) in inputs:  # warm
             orc.linear(x, W, b)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            for (x, W, b) in inputs:
+                orc.linear(x, W, b)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return n, el
+
+    n, el = sweep(threads, seconds)
+    n1, el1 = sweep(1, seconds / 3)
+    orc.set_threads(threads)
     return dict(value=round(step_bytes * n / el / 1e9, 3), unit="GB/s", cores=threads, kind="port",
-                sample=f"{n} steps of the {len(shapes)}-shape sweep in {el:.1f} s; oracle widens the "
-                       f"bf16 weight on every call (bf16_matmul.go:166) then runs an f32 sgemm")
+                sample=f"{n} steps of the {len(shapes)}-shape sweep in {el:.1f} s on {threads} threads; oracle "
+                       f"widens the bf16 weight on every call (bf16_matmul.go:166) then runs an f32 sgemm",
+                single_thread=dict(value=round(step_bytes * n1 / el1 / 1e9, 3), unit="GB/s",
+                                   sample=f"{n1} steps in {el1:.1f} s"),
+                **host)
+
+
+def cpu_decode_leg(seconds, host, n_prompt=32):
+    """gorch's CPU greedy decode of GPT-2 small at batch 1 (generateCached,
+    model/generate.go:94-131: ForwardCached of one token, then argmax) on the
+    oracle, after a 32-token prefill. Faithful: the bf16 weights are widened
+    on every Linear call (bf16_matmul.go:147-166); pre-widened: widened once.
+    Each mode on the granted threads and on one thread, ~`seconds` each.
+    tok/s = decode steps / their wall time (prefill not timed)."""
+    import oracle as orc
+    from gorch_amd import synthetic as syn
+
+    cfg = syn.GPT2_SMALL
+    w = syn.gpt2_weights(cfg, seed=0)
+    o = orc.GPT(w)
+    prompt = syn.prompt_ids(n_prompt, cfg["vocab"], seed=0)
+    out = []
+    for widen in (True, False):
+        for threads in (host["threads_granted"], 1):
+            orc.set_threads(threads)
+            orc.set_widen_per_call(widen)
+            cache = o.new_cache()
+            tok = orc.argmax(o.forward_cached(prompt, cache)[-1])
+            n = 0
+            t0 = time.perf_counter()
+            while True:
+                tok = orc.argmax(o.forward_cached(np.array([tok], np.int32), cache)[-1])
+                n += 1
+                el = time.perf_counter() - t0
+                if el >= seconds or len(cache) >= cfg["max_seq"]:
+                    break
+            out.append({"mode": "faithful (widen per call)" if widen else "pre-widened",
+                        "threads": threads, "tok_s": round(n / el, 2), "steps": n, "seconds": round(el, 2)})
+    orc.set_widen_per_call(True)
+    orc.set_threads(host["threads_granted"])
+    return {"model": "gpt2-small", "batch": 1, "prompt": n_prompt, "kind": "port", "unit": "tok/s",
+            "runs": out, **host}
 
 
 def main():
@@ -419,6 +531,8 @@ def main():
             print(json.dumps(moe_leg()))
         elif args.only == "decode-qwen":
             print(json.dumps(qwen_leg()))
+        elif args.only == "cpu-decode":
+            print(json.dumps(cpu_decode_leg(3.0, host_info())))
         else:
             print(json.dumps(gemm_leg()))
         return
@@ -440,7 +554,9 @@ def main():
     gemm = [] if args.shape else gemm_leg()
     moe = None if args.shape else moe_leg()
     qwen = [] if (args.shape or args.no_decode) else qwen_leg()
-    cpu = None if args.no_cpu else cpu_leg(shapes, args.cpu_seconds)
+    host = host_info()
+    cpu = None if args.no_cpu else cpu_leg(shapes, args.cpu_seconds, host)
+    cpu_decode = None if (args.no_cpu or args.shape or args.no_decode) else cpu_decode_leg(3.0, host)
     dom_bytes = algo_bytes(dom["M"], dom["K"], dom["N"])
     dom_kernel = gemv_kernel(dom["M"], dom["K"], dom["N"])
     out = {
@@ -479,6 +595,7 @@ def main():
         "cpu_baseline": cpu,
         "per_shape": per_shape,
         "decode": decode,
+        "cpu_decode": cpu_decode,
         "prefill_gemm": gemm,
         "moe_layer": moe,
         "decode_qwen": qwen,

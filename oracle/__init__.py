@@ -43,6 +43,7 @@ def _load() -> C.CDLL:
         "orc_batched_matmul_dt": (C.c_int, [vp, vp, f32p] + [C.c_int] * 8),
         "orc_linear": (None, [f32p, C.c_int, C.c_int, vp, C.c_int, vp, C.c_int, f32p]),
         "orc_set_widen_per_call": (None, [C.c_int]),
+        "orc_set_threads": (C.c_int, [C.c_int]),
         "orc_clear_widen_cache": (None, []),
         "orc_add": (None, [f32p, f32p, f32p, C.c_int64]),
         "orc_gelu": (None, [f32p, f32p, C.c_int64]),
@@ -138,6 +139,12 @@ def linear(x, W, bias=None):
     b = None if bias is None else np.ascontiguousarray(bias, np.float32)
     lib.orc_linear(x, M, K, _ptr(W), int(W.dtype == np.uint16), _ptr(b), N, y)
     return y
+
+
+def set_threads(n: int) -> int:
+    """OpenMP threads of the oracle (n <= 0 keeps the current count); returns
+    the count in effect."""
+    return int(lib.orc_set_threads(n))
 
 
 def set_widen_per_call(on: bool) -> None:

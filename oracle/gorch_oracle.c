@@ -63,6 +63,14 @@ static int g_wcache_len = 0, g_wcache_cap = 0;
 
 void orc_set_widen_per_call(int on) { g_widen_per_call = on; }
 
+/* OpenMP threads for the parallel loops (the CPU baseline's core count;
+ * Accelerate picks its own, accelerate/shim.c:8-32). Returns the count now
+ * in effect. */
+int orc_set_threads(int n) {
+    if (n > 0) omp_set_num_threads(n);
+    return omp_get_max_threads();
+}
+
 void orc_clear_widen_cache(void) {
     for (int i = 0; i < g_wcache_len; i++) free(g_wcache[i].f32);
     free(g_wcache);

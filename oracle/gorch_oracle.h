@@ -50,6 +50,9 @@ void orc_linear(const float* x, int M, int K, const void* W, int wBF16,
  * matMulDTGrad's fallback does; zero keeps one widened copy per weight
  * pointer (the "pre-widened" CPU comparator). */
 void orc_set_widen_per_call(int on);
+/* OpenMP thread count for the oracle's parallel loops (n <= 0 keeps it);
+ * returns the count in effect. */
+int orc_set_threads(int n);
 void orc_clear_widen_cache(void);
 
 /* ---- elementwise / row ops ---- */
