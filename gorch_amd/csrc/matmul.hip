@@ -5,9 +5,10 @@
 //   - f32 A [M,K] x bf16 B stored [N,K] (transB; the nn.Linear layout,
 //     ops.go:788-807 -> bf16_matmul.go:159-173): the MFMA weight-streaming
 //     kernel in gemv.hip;
-//   - every other transpose/dtype combination: a simple tiled kernel that
-//     reads each operand through its own layout and dtype (correct for all
-//     shapes; not a hot path of the decode step).
+//   - every other transpose/dtype combination, and every batch of more than
+//     one entry: k_matmul_mfma, one launch over the batch, each operand
+//     gathered through its own layout and dtype into bf16 matrix-core terms
+//     (not a hot path of the decode step).
 #include <algorithm>
 
 #include "common.h"
@@ -18,44 +19,101 @@ int launch_gemm_bf16w(hipStream_t s, const float* A, const uint16_t* W, const fl
                       const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
                       bool act_bf16);
 
-__device__ __forceinline__ float load_op(const void* p, size_t i, int bf16) {
-    return bf16 ? __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16)
-                : reinterpret_cast<const float*>(p)[i];
+// One element of an operand as bf16 terms: bf16 storage is one exact term;
+// f32 is hi (the value truncated to bf16, exact in f32) + lo (the remainder
+// rounded to bf16), x = hi + lo to ~2^-16 relative.
+__device__ __forceinline__ void op_terms(const void* p, size_t i, bool bf16, uint16_t& hi, uint16_t& lo) {
+    if (bf16) {
+        hi = reinterpret_cast<const uint16_t*>(p)[i];
+        lo = 0;
+        return;
+    }
+    const float v = reinterpret_cast<const float*>(p)[i];
+    const uint32_t u = __float_as_uint(v) & 0xffff0000u;
+    hi = (uint16_t)(u >> 16);
+    lo = __builtin_bit_cast(uint16_t, (__bf16)(v - __uint_as_float(u)));
 }
 
-// C[b] = opA(A[b]) @ opB(B[b]); 16x16 output tile per block, K staged
-// through LDS in 16-wide slabs. Each output sums k in increasing order.
-__global__ __launch_bounds__(256) void k_matmul_generic(const void* __restrict__ A,
-                                                        const void* __restrict__ B,
-                                                        float* __restrict__ C, int M, int N, int K,
-                                                        int transA, int transB, int aBF16, int bBF16) {
-    __shared__ float As[16][17];
-    __shared__ float Bs[16][17];
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int m = blockIdx.y * 16 + ty, n = blockIdx.x * 16 + tx;
+// C[b] = opA(A[b]) @ opB(B[b]) on the matrix cores for every transpose /
+// dtype combination of metal_mps_matmul_dt (one launch for the whole batch,
+// blockIdx.z = batch entry). Block tile 64 x 64, K stepped by 32; each
+// operand tile is gathered through its own layout into LDS as bf16 terms
+// in [row][k] order (NTA / NTB terms: 1 for a bf16 operand, hi + lo for an
+// f32 one), then 4 waves (2 x 2, 32 x 32 each) run v_mfma_f32_16x16x32_bf16
+// over the term products that matter (lo x lo, below f32 rounding, is left
+// out), accumulating in f32. Not a hot path of the decode step: the gather
+// is per element with bounds checks.
+constexpr int kMmBK = 32, kMmLD = kMmBK + 8;  // LDS row: 40 bf16 (80 bytes)
+
+template <int NTA, int NTB>
+__global__ __launch_bounds__(256) void k_matmul_mfma(const void* __restrict__ A, const void* __restrict__ B,
+                                                     float* __restrict__ C, int M, int N, int K, int transA,
+                                                     int transB) {
+    __shared__ __align__(16) uint16_t As[NTA][64][kMmLD];
+    __shared__ __align__(16) uint16_t Bs[NTB][64][kMmLD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, r = lane & 15, g = lane >> 4;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
     const size_t bA = (size_t)blockIdx.z * M * K, bB = (size_t)blockIdx.z * K * N;
-    float acc = 0.f;
-    for (int k0 = 0; k0 < K; k0 += 16) {
-        {   // As[ty][tx] = opA(A)[blockIdx.y*16 + ty][k0 + tx]
-            int am = blockIdx.y * 16 + ty, ak = k0 + tx;
-            float v = 0.f;
-            if (am < M && ak < K)
-                v = load_op(A, bA + (transA ? (size_t)ak * M + am : (size_t)am * K + ak), aBF16);
-            As[ty][tx] = v;
-        }
-        {   // Bs[ty][tx] = opB(B)[k0 + ty][blockIdx.x*16 + tx]
-            int bk = k0 + ty, bn = blockIdx.x * 16 + tx;
-            float v = 0.f;
-            if (bk < K && bn < N)
-                v = load_op(B, bB + (transB ? (size_t)bn * K + bk : (size_t)bk * N + bn), bBF16);
-            Bs[ty][tx] = v;
+    floatx4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < K; k0 += kMmBK) {
+        // 64 x 32 elements per operand, 8 per thread: thread t takes row
+        // t / 4 (of the tile) and k 8 * (t % 4) .. +8, each element read
+        // through the operand's stored layout
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int row = tid >> 2, kk = 8 * (tid & 3) + e, k = k0 + kk;
+            uint16_t h = 0, l = 0;
+            const int m = m0 + row;
+            if (m < M && k < K) op_terms(A, bA + (transA ? (size_t)k * M + m : (size_t)m * K + k), NTA == 1, h, l);
+            As[0][row][kk] = h;
+            if (NTA == 2) As[NTA - 1][row][kk] = l;
+            const int n = n0 + row;
+            h = l = 0;
+            if (n < N && k < K) op_terms(B, bB + (transB ? (size_t)n * K + k : (size_t)k * N + n), NTB == 1, h, l);
+            Bs[0][row][kk] = h;
+            if (NTB == 2) Bs[NTB - 1][row][kk] = l;
         }
         __syncthreads();
+        bf16x8 af[2][NTA], bfr[2][NTB];
 #pragma unroll
-        for (int kk = 0; kk < 16; kk++) acc += As[ty][kk] * Bs[kk][tx];
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int t = 0; t < NTA; t++)
+                af[i][t] = *reinterpret_cast<const bf16x8*>(&As[t][wm * 32 + i * 16 + r][8 * g]);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int t = 0; t < NTB; t++)
+                bfr[j][t] = *reinterpret_cast<const bf16x8*>(&Bs[t][wn * 32 + j * 16 + r][8 * g]);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int ta = 0; ta < NTA; ta++)
+#pragma unroll
+                    for (int tb = 0; tb < NTB; tb++)
+                        if (ta + tb < 2) acc[i][j] = mfma16x16x32(af[i][ta], bfr[j][tb], acc[i][j]);
         __syncthreads();
     }
-    if (m < M && n < N) C[(size_t)blockIdx.z * M * N + (size_t)m * N + n] = acc;
+    // lane holds rows 4g..4g+3 of column r in each 16 x 16 fragment
+    float* Cb = C + (size_t)blockIdx.z * M * N;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn * 32 + j * 16 + r;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int m = m0 + wm * 32 + i * 16 + 4 * g + v;
+                if (m < M && n < N) Cb[(size_t)m * N + n] = acc[i][j][v];
+            }
+        }
 }
 
 static bool linear_fast_ok(const void* x, const void* W, int K) {
@@ -150,7 +208,7 @@ int matmul_dt_raw(hipStream_t s, const void* A, const void* B, float* C, uint32_
         count(CNT_ELEMENTWISE);
         return check_launch("fill_zero");
     }
-    if (!transA && transB && !aBF16 && bBF16 && linear_fast_ok(A, B, (int)K)) {
+    if (batch == 1 && !transA && transB && !aBF16 && bBF16 && linear_fast_ok(A, B, (int)K)) {
         for (uint32_t b = 0; b < batch; b++) {
             const float* a = reinterpret_cast<const float*>(A) + (size_t)b * M * K;
             const uint16_t* w = reinterpret_cast<const uint16_t*>(B) + (size_t)b * N * K;
@@ -160,11 +218,14 @@ int matmul_dt_raw(hipStream_t s, const void* A, const void* B, float* C, uint32_
             if (b + 1 == batch) return GORCH_HIP_OK;
         }
     }
-    dim3 grid((N + 15) / 16, (M + 15) / 16, batch);
-    hipLaunchKernelGGL(k_matmul_generic, grid, dim3(256), 0, s, A, B, C, (int)M, (int)N, (int)K, transA,
-                       transB, aBF16, bBF16);
+    const dim3 grid((N + 63) / 64, (M + 63) / 64, batch);
+    const int tA = transA ? 1 : 0, tB = transB ? 1 : 0, m = (int)M, n = (int)N, k = (int)K;
+    if (aBF16 && bBF16) hipLaunchKernelGGL((k_matmul_mfma<1, 1>), grid, dim3(256), 0, s, A, B, C, m, n, k, tA, tB);
+    else if (aBF16) hipLaunchKernelGGL((k_matmul_mfma<1, 2>), grid, dim3(256), 0, s, A, B, C, m, n, k, tA, tB);
+    else if (bBF16) hipLaunchKernelGGL((k_matmul_mfma<2, 1>), grid, dim3(256), 0, s, A, B, C, m, n, k, tA, tB);
+    else hipLaunchKernelGGL((k_matmul_mfma<2, 2>), grid, dim3(256), 0, s, A, B, C, m, n, k, tA, tB);
     count(CNT_GENERIC_MATMUL);
-    return check_launch("matmul_generic");
+    return check_launch("matmul_mfma");
 }
 
 }  // namespace gh

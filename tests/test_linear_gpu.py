@@ -136,6 +136,31 @@ def test_matmul_dt_all_layouts(gpu, transA, transB, aBF16, bBF16):
     assert rel_err(host(C), orc.matmul_dt(A, B, M, N, K, transA, transB)) <= 1e-3
 
 
+@pytest.mark.parametrize("transA,transB", [(0, 0), (1, 0), (0, 1)])
+@pytest.mark.parametrize("aBF16,bBF16", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_batched_matmul_dt_all_layouts(gpu, transA, transB, aBF16, bBF16):
+    """Every layout and dtype pair of batchedMatMulDTGrad / batchedMatMulBF16
+    (bf16_matmul.go:185-212, :257-304) in one launch, with edges in every
+    dimension (M, N not multiples of the 64-wide tile, K not of the 32-wide
+    step), against the oracle's per-batch f32 sgemm."""
+    rng = np.random.default_rng(25 + 4 * transA + 2 * transB + aBF16)
+    B_, M, N, K = 3, 70, 130, 100
+    a = rng.standard_normal((B_,) + ((K, M) if transA else (M, K))).astype(np.float32)
+    b = rng.standard_normal((B_,) + ((N, K) if transB else (K, N))).astype(np.float32)
+    A = orc.f32_to_bf16(a) if aBF16 else a
+    Bm = orc.f32_to_bf16(b) if bBF16 else b
+    C = torch.empty((B_, M, N), dtype=torch.float32, device="cuda")
+    gpu.reset_dispatch_counts()
+    gpu.batched_matmul_dt(dev(A), dev(Bm), C, M, N, K, B_, transA, transB, aBF16, bBF16)
+    assert gpu.dispatch_counts()["generic_matmul"] == 1
+    ref = orc.batched_matmul_dt(A, Bm, B_, M, N, K, bool(transA), bool(transB))
+    assert rel_err(host(C), ref) <= 1e-3
+    # f32 operands as two bf16 terms each: ~2^-15 per product, far inside
+    # what one bf16 rounding of an operand would give (~2^-9)
+    if not (aBF16 or bBF16):
+        assert rel_err(host(C), ref) <= 2e-4
+
+
 def test_matmul_dt_double_transpose_unsupported(gpu):
     A = torch.zeros((4, 4), device="cuda")
     with pytest.raises(gpu.HipError) as e:
