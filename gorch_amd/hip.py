@@ -660,7 +660,11 @@ class GQA:
         self.w = w
         self.t = {n: up(w.get(n)) for n in ("wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo", "q_norm", "k_norm")}
         if w.get("rope"):
-            self.t["rope_cos"], self.t["rope_sin"] = rope_tables(w["head_dim"], w["rope_max_seq"], w["rope_base"])
+            if isinstance(w.get("rope_cos"), torch.Tensor):  # tables shared with other layers
+                self.t["rope_cos"], self.t["rope_sin"] = w["rope_cos"], w["rope_sin"]
+            else:
+                self.t["rope_cos"], self.t["rope_sin"] = rope_tables(w["head_dim"], w["rope_max_seq"],
+                                                                     w["rope_base"])
         s = _GQAW()
         for n in ("dim", "num_q", "num_kv", "head_dim"):
             setattr(s, n, w[n])

@@ -24,7 +24,10 @@ from . import hip
 
 @dataclass(frozen=True)
 class QwenConfig:
-    """model/qwen/config.go:13-27 (the fields this decoder uses)."""
+    """model/qwen/config.go:13-28. attn_bias: q/k/v projection biases
+    (Qwen2.5); use_qk_norm: per-head q/k RMSNorm (Qwen3); tied_embeddings:
+    the LM head is the embedding table (the reference's Model always ties it,
+    qwen.go:84); eos_tokens: generation stop ids."""
     hidden: int
     layers: int
     num_q: int
@@ -35,14 +38,23 @@ class QwenConfig:
     rope_theta: float = 1_000_000.0
     eps: float = 1e-6
     max_seq: int = 4096
+    attn_bias: bool = False
+    use_qk_norm: bool = True
+    tied_embeddings: bool = True
+    eos_tokens: tuple = ()
 
     @property
     def kv_dim(self) -> int:
         return self.num_kv * self.head_dim
 
 
-# model/qwen/config.go:40-55 (Qwen3-0.6B)
-QWEN3_0_6B = QwenConfig(hidden=1024, layers=28, num_q=16, num_kv=8, head_dim=128, inter=3072, vocab=151936)
+# model/qwen/config.go:40-56 (Qwen3-0.6B) and :61-78 (Qwen2.5-0.5B-Instruct)
+QWEN3_0_6B = QwenConfig(hidden=1024, layers=28, num_q=16, num_kv=8, head_dim=128, inter=3072, vocab=151936,
+                        max_seq=40960, attn_bias=False, use_qk_norm=True, tied_embeddings=True,
+                        eos_tokens=(151645, 151643))
+QWEN2_5_0_5B = QwenConfig(hidden=896, layers=24, num_q=14, num_kv=2, head_dim=64, inter=4864, vocab=151936,
+                          max_seq=32768, attn_bias=True, use_qk_norm=False, tied_embeddings=True,
+                          eos_tokens=(151645, 151643))
 
 
 class Qwen:
@@ -55,17 +67,33 @@ class Qwen:
             a = np.ascontiguousarray(a)
             return torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).cuda()
 
+        if not cfg.tied_embeddings:
+            raise ValueError("qwen: only the tied LM head is supported (the reference Model ties it)")
         self.cfg = cfg
         self.embed_bf16 = w["embed"] if isinstance(w["embed"], torch.Tensor) else up(w["embed"])
         self.embed = torch.empty((cfg.vocab, cfg.hidden), dtype=torch.float32, device="cuda")
         hip.bf16_to_f32(self.embed_bf16, self.embed)
         self.norm = w["norm"] if isinstance(w["norm"], torch.Tensor) else up(w["norm"])
+        # one RoPE table shared by every layer (New, qwen.go:31-36)
+        self.rope_cos, self.rope_sin = hip.rope_tables(cfg.head_dim, cfg.max_seq, cfg.rope_theta)
         self.layers = []
         for lw in w["layers"]:
+            has_bias = all(lw.get(n) is not None for n in ("bq", "bk", "bv"))
+            if cfg.attn_bias != has_bias:
+                raise ValueError("qwen: attn_bias says %s but the layer weights %s q/k/v biases"
+                                 % (cfg.attn_bias, "carry" if has_bias else "lack"))
+            has_norm = lw.get("q_norm") is not None and lw.get("k_norm") is not None
+            if cfg.use_qk_norm != has_norm:
+                raise ValueError("qwen: use_qk_norm says %s but the layer weights %s q/k norm gains"
+                                 % (cfg.use_qk_norm, "carry" if has_norm else "lack"))
             gw = {"dim": cfg.hidden, "num_q": cfg.num_q, "num_kv": cfg.num_kv, "head_dim": cfg.head_dim,
                   "causal": True, "norm_eps": cfg.eps, "wq": lw["wq"], "wk": lw["wk"], "wv": lw["wv"],
-                  "wo": lw["wo"], "q_norm": lw["q_norm"], "k_norm": lw["k_norm"], "rope": True,
-                  "rope_base": cfg.rope_theta, "rope_max_seq": cfg.max_seq}
+                  "wo": lw["wo"], "rope": True, "rope_base": cfg.rope_theta, "rope_max_seq": cfg.max_seq,
+                  "rope_cos": self.rope_cos, "rope_sin": self.rope_sin}
+            if cfg.use_qk_norm:
+                gw["q_norm"], gw["k_norm"] = lw["q_norm"], lw["k_norm"]
+            if cfg.attn_bias:
+                gw["bq"], gw["bk"], gw["bv"] = lw["bq"], lw["bk"], lw["bv"]
             layer = {"attn": hip.GQA(gw)}
             for n in ("norm_attn", "norm_ffn", "wgate", "wup", "wdown"):
                 layer[n] = lw[n] if isinstance(lw[n], torch.Tensor) else up(lw[n])

@@ -134,10 +134,14 @@ def qwen_weights(cfg, seed: int = 0) -> dict:
 
     layers = []
     for _ in range(cfg.layers):
-        layers.append({"wq": bf16_normal(rng, (q, d)), "wk": bf16_normal(rng, (kv, d)),
-                       "wv": bf16_normal(rng, (kv, d)), "wo": bf16_normal(rng, (d, q)),
-                       "q_norm": gain(cfg.head_dim), "k_norm": gain(cfg.head_dim),
-                       "norm_attn": gain(d), "norm_ffn": gain(d),
-                       "wgate": bf16_normal(rng, (cfg.inter, d)), "wup": bf16_normal(rng, (cfg.inter, d)),
-                       "wdown": bf16_normal(rng, (d, cfg.inter))})
+        L = {"wq": bf16_normal(rng, (q, d)), "wk": bf16_normal(rng, (kv, d)),
+             "wv": bf16_normal(rng, (kv, d)), "wo": bf16_normal(rng, (d, q)),
+             "norm_attn": gain(d), "norm_ffn": gain(d),
+             "wgate": bf16_normal(rng, (cfg.inter, d)), "wup": bf16_normal(rng, (cfg.inter, d)),
+             "wdown": bf16_normal(rng, (d, cfg.inter))}
+        if getattr(cfg, "use_qk_norm", True):
+            L["q_norm"], L["k_norm"] = gain(cfg.head_dim), gain(cfg.head_dim)
+        if getattr(cfg, "attn_bias", False):
+            L["bq"], L["bk"], L["bv"] = normal(rng, (q,), 0.05), normal(rng, (kv,), 0.05), normal(rng, (kv,), 0.05)
+        layers.append(L)
     return {"embed": bf16_normal(rng, (cfg.vocab, d)), "norm": gain(d), "layers": layers}

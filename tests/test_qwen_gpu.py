@@ -33,11 +33,14 @@ class OracleQwen:
         self.gqa = []
         for lw, layer in zip(w["layers"], model.layers):
             t = layer["attn"].t
-            self.gqa.append({"dim": cfg.hidden, "num_q": cfg.num_q, "num_kv": cfg.num_kv,
-                             "head_dim": cfg.head_dim, "causal": True, "norm_eps": cfg.eps,
-                             "wq": lw["wq"], "wk": lw["wk"], "wv": lw["wv"], "wo": lw["wo"],
-                             "q_norm": lw["q_norm"], "k_norm": lw["k_norm"],
-                             "rope_cos": host(t["rope_cos"]), "rope_sin": host(t["rope_sin"])})
+            gw = {"dim": cfg.hidden, "num_q": cfg.num_q, "num_kv": cfg.num_kv,
+                  "head_dim": cfg.head_dim, "causal": True, "norm_eps": cfg.eps,
+                  "wq": lw["wq"], "wk": lw["wk"], "wv": lw["wv"], "wo": lw["wo"],
+                  "rope_cos": host(t["rope_cos"]), "rope_sin": host(t["rope_sin"])}
+            for n in ("q_norm", "k_norm", "bq", "bk", "bv"):
+                if lw.get(n) is not None:
+                    gw[n] = lw[n]
+            self.gqa.append(gw)
         cap = cfg.max_seq
         self.cache = [(np.zeros((cap, cfg.kv_dim), np.float32), np.zeros((cap, cfg.kv_dim), np.float32))
                       for _ in w["layers"]]
@@ -114,3 +117,30 @@ def test_qwen_greedy_long_cache(gpu):
     for (kd, vd), (kc, vc) in zip(cache, ref.cache):
         assert rel_err(host(kd)[:pos], kc[:pos]) <= 1e-4
         assert rel_err(host(vd)[:pos], vc[:pos]) <= 1e-4
+
+
+def test_qwen25_style_bias_no_qk_norm(gpu):
+    """The Qwen2.5 configuration switches (config.go:61-78): q/k/v projection
+    biases on, per-head q/k RMSNorm off; greedy tokens and logits against the
+    oracle composition, and a config that disagrees with the weights is
+    refused rather than silently ignoring them."""
+    import dataclasses
+    cfg = dataclasses.replace(TINY, attn_bias=True, use_qk_norm=False)
+    w = syn.qwen_weights(cfg, seed=7)
+    m = Qwen(cfg, w)
+    ref = OracleQwen(cfg, w, m)
+    cache = m.new_cache(cfg.max_seq)
+    ids = np.random.default_rng(12).integers(0, cfg.vocab, 9).astype(np.int32)
+    pos = 0
+    for step in range(4):
+        got = host(m.forward_cached(torch.from_numpy(ids).cuda(), cache, pos))
+        want = ref.forward_cached(ids, pos)
+        assert rel_err(got, want) <= 1e-3, step
+        nxt = int(np.argmax(got[0]))
+        assert nxt == orc.argmax(want), step
+        pos += ids.size
+        ids = np.array([nxt], np.int32)
+    with pytest.raises(ValueError):
+        Qwen(TINY, w)                      # weights carry biases, config says none
+    with pytest.raises(ValueError):
+        Qwen(dataclasses.replace(cfg, tied_embeddings=False), w)
