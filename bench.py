@@ -49,7 +49,8 @@ def parse():
                     help="restrict to one shape 'M,K,N' (for profiling one kernel)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the GPT decode legs")
-    ap.add_argument("--only", choices=("decode", "gemm", "decode-xl", "moe", "decode-qwen", "cpu-decode"),
+    ap.add_argument("--only", choices=("decode", "gemm", "decode-xl", "moe", "decode-qwen", "cpu-decode",
+                                       "attn-xl"),
                     default=None,
                     help="run only one secondary leg and print its JSON (for profiling)")
     ap.add_argument("--cpu-seconds", type=float, default=9.0)
@@ -386,6 +387,46 @@ def roofline_block(nbytes, seconds, what):
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_step": int(nbytes), "bytes": what}
 
 
+def attn_leg(batch=16, heads=25, hd=64, ctx=640, capacity=768, reps=200):
+    """The GPT-2 XL batch-16 step's cached attention alone (MHA.ForwardCached's
+    core, nn/attention.go:355-397): one new row per sequence at position
+    ctx - 1 over a [batch][capacity][heads*hd] f32 cache (the engine's
+    layout), the mean context of configs[4]'s 256 steps. Algorithmic bytes =
+    the K and V rows read (2 * batch * ctx * heads * hd * 4) plus q and out."""
+    import torch
+
+    from gorch_amd import hip
+
+    d = heads * hd
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+    q = torch.randn((batch, d), device="cuda", generator=gen)
+    kc = torch.randn((batch, capacity, d), device="cuda", generator=gen)
+    vc = torch.randn((batch, capacity, d), device="cuda", generator=gen)
+    out = torch.empty((batch, d), device="cuda")
+    stream = torch.cuda.current_stream()
+    hip.attention_cached(q, kc, vc, out, batch, 1, ctx - 1, heads, hd, capacity)
+    torch.cuda.synchronize()
+    L = 20
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(L):
+            hip.attention_cached(q, kc, vc, out, batch, 1, ctx - 1, heads, hd, capacity)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps // L):
+        g.replay()
+    e1.record(stream)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps // L * L)
+    nbytes = 2 * batch * ctx * d * 4 + 2 * batch * d * 4
+    return {"batch": batch, "heads": heads, "head_dim": hd, "ctx": ctx, "capacity": capacity, "us": round(us, 2),
+            "algorithmic_bytes": nbytes, "GBs": round(nbytes / us / 1e3, 1),
+            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
 def decode_leg(cfg_name, batch, n_prompt, max_new, reps=3):
     """Greedy KV-cache decode through the engine (graph-replayed step).
     tok/s = batch * decode forwards / decode wall time (prefill timed apart)."""
@@ -531,6 +572,8 @@ def main():
             print(json.dumps(moe_leg()))
         elif args.only == "decode-qwen":
             print(json.dumps(qwen_leg()))
+        elif args.only == "attn-xl":
+            print(json.dumps(attn_leg()))
         elif args.only == "cpu-decode":
             print(json.dumps(cpu_decode_leg(3.0, host_info())))
         else:
