@@ -48,6 +48,11 @@ struct LinearExtras {
     // the stream's scratch); a split that needs more fails with EINVAL
     float* scratch = nullptr;
     size_t scratch_bytes = 0;
+    // one-row register GEMV only: ln_g is an RMSNorm gain (no beta, no mean)
+    bool ln_rms = false;
+    // one-row register GEMV only: the activation row is [gate | up] of 2K
+    // values and the GEMV reads silu(gate) * up
+    bool swiglu = false;
 };
 // Number of K slices a K-split Linear actually uses for a requested count
 // (slices are multiples of 32 wide).
@@ -257,6 +262,19 @@ struct AttnArgs {
 // key: 16384 keys); longer caches go to the online-softmax kernel.
 constexpr size_t kAttnMaxLdsBytes = 65536;
 int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows);
+
+// GQA.forwardCached for one sequence (gqa.hip); pre_gain: an RMSNorm of x
+// applied first (the decoder block's), resid: added to the output. ws holds
+// gqa_ws(...) bytes.
+size_t gqa_ws(int new_seq, int num_q, int num_kv, int hd, int dim);
+int gqa_check(const gorch_hip_gqa_weights* w, int S, int pos_offset, int max_seq);
+int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int S, float* k_cache, float* v_cache,
+             int pos_offset, int max_seq, float* out, char* ws, const float* pre_gain, float pre_eps,
+             const float* resid);
+int launch_rmsnorm(hipStream_t s, const float* x, const float* g, float* y, int M, int N, float eps);
+// The one-row register GEMV takes K (RMSNorm / SwiGLU prologues need it).
+bool gemv_m1_prologue_ok(int K);
+int launch_swiglu(hipStream_t s, const float* g, const float* v, float* y, int64_t n);
 
 // A tensor entry of a safetensors header (safetensors.hip): dtype
 // GORCH_HIP_ST_*, shape, byte range relative to the data section.

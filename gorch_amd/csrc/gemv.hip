@@ -333,10 +333,14 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const float* __restrict__ x, 
 // row statistics itself with wave reductions — no LDS staging and no block
 // barrier before the weight stream starts. The next row group's weight
 // loads are issued before the current group is reduced.
-template <int T, int C, bool LN>
+// PRO selects what is applied to the activation row as it is loaded: 0
+// nothing, 1 LayerNorm (gamma, beta), 2 RMSNorm (gamma), 3 SwiGLU of a
+// [gate | up] row of 2K values (silu(gate) * up, silu.go:121-136).
+template <int T, int C, int PRO>
 __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, const uint16_t* __restrict__ W,
                                                  const float* __restrict__ bias, const float* residual, OutDesc od,
                                                  int N, int K, int epilogue, LinearExtras ex) {
+    constexpr bool LN = PRO == 1 || PRO == 2;
     __shared__ unsigned long long s_key;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -367,7 +371,7 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
         gr.r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, rloc * 4, 0, 0));
     };
     // the activation row (K = 8*T*C exactly), LayerNorm gamma/beta with it
-    float xr[C][8], gg[LN ? C : 1][8], bb[LN ? C : 1][8];
+    float xr[C][8], gg[LN ? C : 1][8], bb[PRO == 1 ? C : 1][8];
 #pragma unroll
     for (int c = 0; c < C; c++) {
         const int k = 8 * (sub + T * c);
@@ -378,12 +382,25 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
         if constexpr (LN) {
             const float4 g0 = *reinterpret_cast<const float4*>(ex.ln_g + k);
             const float4 g1 = *reinterpret_cast<const float4*>(ex.ln_g + k + 4);
-            const float4 b0 = *reinterpret_cast<const float4*>(ex.ln_b + k);
-            const float4 b1 = *reinterpret_cast<const float4*>(ex.ln_b + k + 4);
             gg[c][0] = g0.x; gg[c][1] = g0.y; gg[c][2] = g0.z; gg[c][3] = g0.w;
             gg[c][4] = g1.x; gg[c][5] = g1.y; gg[c][6] = g1.z; gg[c][7] = g1.w;
+        }
+        if constexpr (PRO == 1) {
+            const float4 b0 = *reinterpret_cast<const float4*>(ex.ln_b + k);
+            const float4 b1 = *reinterpret_cast<const float4*>(ex.ln_b + k + 4);
             bb[c][0] = b0.x; bb[c][1] = b0.y; bb[c][2] = b0.z; bb[c][3] = b0.w;
             bb[c][4] = b1.x; bb[c][5] = b1.y; bb[c][6] = b1.z; bb[c][7] = b1.w;
+        }
+        if constexpr (PRO == 3) {
+            // the up half sits K values after the gate half
+            const float4 u0 = *reinterpret_cast<const float4*>(x + K + k);
+            const float4 u1 = *reinterpret_cast<const float4*>(x + K + k + 4);
+            const float up[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float gv = xr[c][i];
+                xr[c][i] = gv * sigmoidf_ref(gv) * up[i];
+            }
         }
     }
     // then two row groups of the weight stream: the activation loads above
@@ -397,7 +414,23 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
         if (tid == 0) s_key = 0ull;
         __syncthreads();
     }
-    if constexpr (LN) {
+    if constexpr (PRO == 2) {
+        // RMSNorm (nn/rmsnorm.go:39-81): y = x * f32(1/sqrt(sum(x^2)/K + eps)) * gamma,
+        // the sum in f64 over the first T lanes (the row is held RPI times)
+        double s1 = 0.0, s2 = 0.0;
+        if (rloc == 0)
+#pragma unroll
+            for (int c = 0; c < C; c++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) s2 += (double)xr[c][i] * (double)xr[c][i];
+        wave_sum2_d(s1, s2);
+        const float inv = (float)(1.0 / sqrt(s2 / (double)K + (double)ex.ln_eps));
+#pragma unroll
+        for (int c = 0; c < C; c++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) xr[c][i] = xr[c][i] * inv * gg[c][i];
+    }
+    if constexpr (PRO == 1) {
         float fm, inv;
         if (ex.ln_stats) {
             fm = ex.ln_stats[0].x;
@@ -1037,6 +1070,13 @@ static void m1_shape(int K, int* T, int* C) {
         }
 }
 
+bool gemv_m1_prologue_ok(int K) {
+    int T1, C1;
+    m1_shape(K, &T1, &C1);
+    return T1 != 0 && env_int("GORCH_HIP_GEMV_M1", 1) && env_int("GORCH_HIP_GEMV_VALU_MAX_M", 1) >= 1 &&
+           K % 8 == 0;
+}
+
 static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const float* bias, const float* residual,
                      const OutDesc& od, int N, int K, int epilogue, const LinearExtras& ex, int T, int C) {
     const int rpi = 64 / T;
@@ -1051,14 +1091,16 @@ static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const flo
     int blocks = ex.ln_g ? (ngroups + 7) / 8 : (ngroups + 3) / 4;
     if (blocks > max_blocks) blocks = max_blocks;
     if (ex.argmax_key && blocks > max_blocks_argmax) blocks = max_blocks_argmax;
+    const int pro = ex.swiglu ? 3 : (ex.ln_g ? (ex.ln_rms ? 2 : 1) : 0);
+#define GH_M1_L(TT, CC, PV)                                                                                 \
+    hipLaunchKernelGGL((k_gemv_m1<TT, CC, PV>), dim3(blocks), dim3(256), 0, s, x, W, bias, residual, od, N, K, \
+                       epilogue, ex)
 #define GH_M1(TT, CC)                                                                                        \
     if (T == TT && C == CC) {                                                                                \
-        if (ex.ln_g)                                                                                         \
-            hipLaunchKernelGGL((k_gemv_m1<TT, CC, true>), dim3(blocks), dim3(256), 0, s, x, W, bias, residual, \
-                               od, N, K, epilogue, ex);                                                      \
-        else                                                                                                 \
-            hipLaunchKernelGGL((k_gemv_m1<TT, CC, false>), dim3(blocks), dim3(256), 0, s, x, W, bias,         \
-                               residual, od, N, K, epilogue, ex);                                            \
+        if (pro == 1) GH_M1_L(TT, CC, 1);                                                                    \
+        else if (pro == 2) GH_M1_L(TT, CC, 2);                                                               \
+        else if (pro == 3) GH_M1_L(TT, CC, 3);                                                               \
+        else GH_M1_L(TT, CC, 0);                                                                             \
         count(CNT_GEMV);                                                                                     \
         return check_launch("gemv_m1");                                                                      \
     }
@@ -1067,6 +1109,7 @@ static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const flo
     GH_M1(16, 1) GH_M1(16, 3) GH_M1(16, 5) GH_M1(16, 7)
     GH_M1(8, 1) GH_M1(8, 3) GH_M1(8, 5) GH_M1(8, 7)
 #undef GH_M1
+#undef GH_M1_L
     return -1;  // not instantiated: caller falls through
 }
 
@@ -1390,6 +1433,10 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
             int rc = launch_m1(s, x, W, bias, residual, od, N, K, epilogue, ex, T1, C1);
             if (rc >= 0) return rc;
         }
+    }
+    if (ex.ln_rms || ex.swiglu) {
+        set_error("linear_bf16: the RMSNorm / SwiGLU prologues need one row with K/8 = T*C (T in 8..64, C <= 8)");
+        return GORCH_HIP_EUNSUPPORTED;
     }
     static const int tiles_on = env_int("GORCH_HIP_GEMV_TILES", 0);
     if (tiles_on && M >= 2 && !ex.ln_g && (N + 15) / 16 >= 128) {

@@ -72,14 +72,26 @@ __global__ void k_rope_rows(const float* x, float* y, int64_t rows, int heads, i
 // operations, the Llama partner element fetched from lane l +- hd / 8. Row r
 // is token r / heads. In place is fine: a lane writes only its own elements,
 // after every value it needs is in registers.
+// A second segment of rows (x2, y2, heads2, g2) follows the first rows
+// rows: the q and k heads of one projection in one launch.
 __global__ __launch_bounds__(256) void k_norm_rope_rows(const float* x, float* y, int rows, int heads, int hd,
                                                         const float* __restrict__ g, float eps, int start_pos,
                                                         const float* __restrict__ cosT,
-                                                        const float* __restrict__ sinT, int neox) {
+                                                        const float* __restrict__ sinT, int neox,
+                                                        const float* x2 = nullptr, float* y2 = nullptr,
+                                                        int rows2 = 0, int heads2 = 1,
+                                                        const float* __restrict__ g2 = nullptr) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (r >= rows) return;
+    int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    if (r >= rows + rows2) return;
+    if (r >= rows) {  // wave-uniform: a wave is one row
+        r -= rows;
+        x = x2;
+        y = y2;
+        heads = heads2;
+        g = g2;
+    }
     const int half = hd / 2, nl = hd / 4;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (size_t)r * hd, (long long)hd * 4);
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(g, g ? (long long)hd * 4 : 0);
@@ -136,6 +148,16 @@ int launch_norm_rope_rows(hipStream_t s, const float* x, float* y, int rows, int
 static int grid_for(int64_t n) {
     int64_t g = (n + 255) / 256;
     return (int)(g < 1 ? 1 : (g > 16384 ? 16384 : g));
+}
+
+int launch_norm_rope_rows2(hipStream_t s, const float* xq, float* yq, int rows_q, int heads_q, const float* gq,
+                           const float* xk, float* yk, int rows_k, int heads_k, const float* gk, int hd, float eps,
+                           int start_pos, const float* cosT, const float* sinT, int neox) {
+    if (rows_q + rows_k == 0) return GORCH_HIP_OK;
+    hipLaunchKernelGGL(k_norm_rope_rows, dim3((rows_q + rows_k + 3) / 4), dim3(256), 0, s, xq, yq, rows_q, heads_q,
+                       hd, gq, eps, start_pos, cosT, sinT, neox, xk, yk, rows_k, heads_k, gk);
+    count(CNT_ELEMENTWISE);
+    return check_launch("norm_rope_rows2");
 }
 
 int launch_rope_rows(hipStream_t s, const float* x, float* y, int rows, int heads, int hd, int start_pos,

@@ -85,6 +85,8 @@ SIGNATURES = {
     "gorch_hip_gqa_attention_cached": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32]),
     "gorch_hip_gqa_workspace_size": (C.c_size_t, [vp, i32]),
     "gorch_hip_gqa_forward_cached": (i32, [vp, vp, vp, i32, vp, vp, i32, i32, vp, vp, C.c_size_t]),
+    "gorch_hip_qwen_block_workspace_size": (C.c_size_t, [vp, i32]),
+    "gorch_hip_qwen_block_forward_cached": (i32, [vp, vp, vp, i32, vp, vp, i32, i32, vp, C.c_size_t]),
     "gorch_hip_moe_workspace_size": (C.c_size_t, [i32, i32, i32, i32, i32]),
     "gorch_hip_moe_forward": (i32, [vp, vp, vp, i32, vp, vp, vp, vp, vp, C.c_size_t]),
     "gorch_hip_gpt_create": (vp, [vp]),
@@ -690,3 +692,38 @@ class GQA:
                                                pos_offset, k_cache.shape[0], _p(out), self.ws.data_ptr(),
                                                self.ws.numel()))
         return out
+
+
+class _QwenBlockW(C.Structure):
+    _fields_ = [("attn", _GQAW), ("norm_attn", vp), ("norm_ffn", vp), ("wgate_up", vp), ("wdown", vp),
+                ("inter", C.c_int), ("eps", C.c_float)]
+
+
+class QwenBlock:
+    """model/qwen Block.ForwardCached (block.go:71-79) as one C-ABI call.
+    ``attn`` is the block's GQA (its weights and RoPE tables stay owned by
+    it); norm gains, the [2 * inter, dim] gate/up weight and the down weight
+    are device tensors."""
+
+    def __init__(self, attn: GQA, norm_attn, norm_ffn, wgate_up, wdown, inter: int, eps: float):
+        self.attn = attn
+        self.t = {"norm_attn": norm_attn, "norm_ffn": norm_ffn, "wgate_up": wgate_up, "wdown": wdown}
+        s = _QwenBlockW()
+        s.attn = attn.s
+        for n, t in self.t.items():
+            setattr(s, n, t.data_ptr())
+        s.inter, s.eps = inter, eps
+        self.s = s
+        self.ws = None
+
+    def forward_cached(self, x, k_cache, v_cache, pos_offset):
+        """x [new_seq, dim] device f32, updated in place."""
+        import torch
+
+        S = x.shape[0]
+        n = lib().gorch_hip_qwen_block_workspace_size(C.byref(self.s), S)
+        if self.ws is None or self.ws.numel() < n:
+            self.ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+        _ok(lib().gorch_hip_qwen_block_forward_cached(_stream(), C.byref(self.s), _p(x), S, _p(k_cache),
+                                                      _p(v_cache), pos_offset, k_cache.shape[0],
+                                                      self.ws.data_ptr(), self.ws.numel()))

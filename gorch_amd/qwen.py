@@ -1,12 +1,13 @@
 """Qwen3-style decoder on the GPU: gorch's model/qwen (qwen.go:12-98,
 block.go:27-79) — tokens -> embedding -> L x [x1 = x + GQA(RMSNorm(x)); x =
 x1 + SwiGLU-MLP(RMSNorm(x1))] -> RMSNorm -> tied LM head — composed from the
-library's kernels through its C-ABI (gorch_amd.hip): the GQA layer
-(gorch_hip_gqa_forward_cached: Q/K/V Linears, per-head q/k RMSNorm, RoPE at
-absolute positions into the cache, grouped-query cached attention, Wo), RMSNorm,
-the bf16-weight Linears (M = 1 decode GEMV, M > 16 MFMA GEMM), SwiGLU, the
-embedding gather and the residual adds. Every launch goes on torch's current
-stream, so a decode step can be captured in a CUDA graph and replayed.
+library's kernels through its C-ABI (gorch_amd.hip): the embedding gather,
+one gorch_hip_qwen_block_forward_cached call per block (RMSNorm, Q/K/V as one
+weight stream, per-head q/k RMSNorm + RoPE into the cache, grouped-query
+cached attention, Wo + residual, RMSNorm, gate/up as one weight, SwiGLU, down
++ residual: six launches for a one-token step), the final RMSNorm and the tied
+head. Every launch goes on torch's current stream, so a decode step can be
+captured in a CUDA graph and replayed.
 
 Weights are host arrays as gorch_amd.synthetic.qwen_weights builds them, or
 device tensors of the same layout (bf16 as int16): bf16 Linear weights [out,
@@ -86,21 +87,27 @@ class Qwen:
             if cfg.use_qk_norm != has_norm:
                 raise ValueError("qwen: use_qk_norm says %s but the layer weights %s q/k norm gains"
                                  % (cfg.use_qk_norm, "carry" if has_norm else "lack"))
+            # Q, K, V rows as consecutive ranges of one weight (and one bias)
+            # so that a step streams them as one projection
+            q, kv = cfg.num_q * cfg.head_dim, cfg.kv_dim
+            wqkv = torch.cat([lw[n] if isinstance(lw[n], torch.Tensor) else up(lw[n]) for n in ("wq", "wk", "wv")])
             gw = {"dim": cfg.hidden, "num_q": cfg.num_q, "num_kv": cfg.num_kv, "head_dim": cfg.head_dim,
-                  "causal": True, "norm_eps": cfg.eps, "wq": lw["wq"], "wk": lw["wk"], "wv": lw["wv"],
+                  "causal": True, "norm_eps": cfg.eps, "wq": wqkv[:q], "wk": wqkv[q:q + kv], "wv": wqkv[q + kv:],
                   "wo": lw["wo"], "rope": True, "rope_base": cfg.rope_theta, "rope_max_seq": cfg.max_seq,
                   "rope_cos": self.rope_cos, "rope_sin": self.rope_sin}
             if cfg.use_qk_norm:
                 gw["q_norm"], gw["k_norm"] = lw["q_norm"], lw["k_norm"]
             if cfg.attn_bias:
-                gw["bq"], gw["bk"], gw["bv"] = lw["bq"], lw["bk"], lw["bv"]
+                bqkv = torch.cat([lw[n] if isinstance(lw[n], torch.Tensor) else up(lw[n]) for n in ("bq", "bk", "bv")])
+                gw["bq"], gw["bk"], gw["bv"] = bqkv[:q], bqkv[q:q + kv], bqkv[q + kv:]
             layer = {"attn": hip.GQA(gw)}
             for n in ("norm_attn", "norm_ffn", "wgate", "wup", "wdown"):
                 layer[n] = lw[n] if isinstance(lw[n], torch.Tensor) else up(lw[n])
-            # gate and up rows in one weight: a one-row step reads both in
-            # one GEMV launch (its output row is [gate | up]); longer inputs
-            # use the two halves, which are contiguous row ranges of it
+            # gate and up rows in one [2 * inter, d] weight: one GEMV (or one
+            # GEMM with two output segments) produces [gate | up]
             layer["wgu"] = torch.cat([layer.pop("wgate"), layer.pop("wup")], 0)
+            layer["block"] = hip.QwenBlock(layer["attn"], layer["norm_attn"], layer["norm_ffn"], layer["wgu"],
+                                           layer["wdown"], cfg.inter, cfg.eps)
             self.layers.append(layer)
 
     def new_cache(self, capacity: int):
@@ -126,28 +133,8 @@ class Qwen:
         d = cfg.hidden
         x = torch.empty((S, d), device="cuda")
         hip.embedding(self.embed, ids, x)
-        h = torch.empty((S, d), device="cuda")
-        x1 = torch.empty((S, d), device="cuda")
-        F = cfg.inter
-        gu = torch.empty((S, 2 * F), device="cuda")
-        gate, upv = (gu[0, :F], gu[0, F:]) if S == 1 else (torch.empty((S, F), device="cuda"),
-                                                             torch.empty((S, F), device="cuda"))
         for layer, (kc, vc) in zip(self.layers, cache):
-            hip.rmsnorm(x, layer["norm_attn"], h, cfg.eps)
-            a = layer["attn"].forward_cached(h, kc, vc, pos)
-            if d % 4 == 0 and d <= 2048:
-                hip.add_rmsnorm(x, a, layer["norm_ffn"], x1, h, cfg.eps)
-            else:
-                hip.add(x, a, x1)
-                hip.rmsnorm(x1, layer["norm_ffn"], h, cfg.eps)
-            wgu = layer["wgu"]
-            if S == 1:
-                hip.linear_bf16(h, wgu, None, gu)
-            else:
-                hip.linear_bf16(h, wgu[:F], None, gate)
-                hip.linear_bf16(h, wgu[F:], None, upv)
-            hip.swiglu(gate, upv, gate)
-            hip.linear_bf16(gate.view(S, F), layer["wdown"], None, x, residual=x1)
+            layer["block"].forward_cached(x, kc, vc, pos)
         last = torch.empty((1, d), device="cuda")
         hip.rmsnorm(x[S - 1:S], self.norm, last, cfg.eps)
         logits = torch.empty((1, cfg.vocab), device="cuda")

@@ -275,6 +275,33 @@ int gorch_hip_gqa_forward_cached(void* stream, const gorch_hip_gqa_weights* w, c
                                  float* k_cache, float* v_cache, int pos_offset, int max_seq, float* out,
                                  void* workspace, size_t workspace_bytes);
 
+/* One Qwen decoder block (model/qwen Block, block.go:27-79; Config,
+ * config.go:13-28): attn is the block's GQA (q/k/v biases for AttnBias,
+ * q_norm/k_norm for UseQKNorm, the model's shared RoPE tables); norm_attn /
+ * norm_ffn: RMSNorm gains [dim] (eps = RMSNormEps); wgate_up: the gate rows
+ * then the up rows, one bf16 [2*inter, dim] weight; wdown [dim, inter]. The
+ * one-row step fuses Q/K/V into one weight stream when wq, wk, wv (and bq,
+ * bk, bv) are consecutive row ranges of one buffer. */
+typedef struct {
+    gorch_hip_gqa_weights attn;
+    const float* norm_attn;
+    const float* norm_ffn;
+    const uint16_t* wgate_up;
+    const uint16_t* wdown;
+    int inter;
+    float eps;
+} gorch_hip_qwen_block;
+size_t gorch_hip_qwen_block_workspace_size(const gorch_hip_qwen_block* b, int new_seq);
+/* Block.ForwardCached (block.go:71-79) for one sequence, in place on x
+ * [new_seq, dim]: x1 = x + GQA(RMSNorm(x)) (the new K/V rows appended at
+ * pos_offset of the caches [max_seq, num_kv*head_dim]), x = x1 +
+ * down(SwiGLU(gate(h), up(h))) with h = RMSNorm(x1). One-row calls run six
+ * launches (norms and SwiGLU fused into the GEMVs' loads, residual adds into
+ * their stores). Caller workspace, no allocation. */
+int gorch_hip_qwen_block_forward_cached(void* stream, const gorch_hip_qwen_block* b, float* x, int new_seq,
+                                        float* k_cache, float* v_cache, int pos_offset, int max_seq,
+                                        void* workspace, size_t workspace_bytes);
+
 /* ------------------------------------------------------------------------
  * MoE FFN layer (nn.MoE.Forward, nn/moe.go:130-182).
  * ---------------------------------------------------------------------- */

@@ -144,3 +144,35 @@ def test_qwen25_style_bias_no_qk_norm(gpu):
         Qwen(TINY, w)                      # weights carry biases, config says none
     with pytest.raises(ValueError):
         Qwen(dataclasses.replace(cfg, tied_embeddings=False), w)
+
+
+@pytest.mark.parametrize("cfg_kw", [
+    # inter 256: the one-row MLP path (RMSNorm in the gate/up GEMV's loads,
+    # SwiGLU in the down GEMV's loads)
+    dict(hidden=128, layers=2, num_q=4, num_kv=2, head_dim=32, inter=256, vocab=500, max_seq=48),
+    # Qwen3-0.6B width (d 1024, 16 / 8 heads of 128, SwiGLU 3072), two of its
+    # 28 layers and a small vocabulary: the shapes the decode bench times
+    dict(hidden=1024, layers=2, num_q=16, num_kv=8, head_dim=128, inter=3072, vocab=1000, max_seq=48)])
+def test_qwen_fused_block_steps(gpu, cfg_kw):
+    """The six-launch one-token block (gorch_hip_qwen_block_forward_cached)
+    against the oracle composition of model/qwen's block: a 7-token prefill
+    (the separate-kernel path), then one-token steps (the fused path); greedy
+    tokens identical, logits within 1e-3, cache rows within 1e-4."""
+    cfg = QwenConfig(**cfg_kw)
+    w = syn.qwen_weights(cfg, seed=21)
+    m = Qwen(cfg, w)
+    ref = OracleQwen(cfg, w, m)
+    cache = m.new_cache(cfg.max_seq)
+    ids = np.random.default_rng(22).integers(0, cfg.vocab, 7).astype(np.int32)
+    pos = 0
+    for step in range(6):
+        got = host(m.forward_cached(torch.from_numpy(ids).cuda(), cache, pos))
+        want = ref.forward_cached(ids, pos)
+        assert rel_err(got, want) <= 1e-3, step
+        nxt = int(np.argmax(got[0]))
+        assert nxt == orc.argmax(want), step
+        pos += ids.size
+        ids = np.array([nxt], np.int32)
+    for (kd, vd), (kc, vc) in zip(cache, ref.cache):
+        assert rel_err(host(kd)[:pos], kc[:pos]) <= 1e-4
+        assert rel_err(host(vd)[:pos], vc[:pos]) <= 1e-4
