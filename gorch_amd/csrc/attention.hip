@@ -62,7 +62,45 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_cached(AttnArgs a) {
     const float* K = a.kc + base;
     const float* V = a.vc + base;
 
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = a.q[(size_t)row * a.q_stride + h * hd + d];
+    if (a.qkv_part) {
+        // q, k, v of this head from the split QKV Linear's partials: slices
+        // added in order, then the bias (k_splitk_epilogue's order); k and v
+        // go to cache row pos (i = 0), which the score and P.V loops below
+        // read back after the barrier. Buffer loads past the slice count
+        // read zeros, so all of a lane's loads go out together.
+        const int D = a.dim, S = a.qkv_slices;
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.qkv_part, (long long)S * a.qkv_slice_stride * 4);
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.qkv_bias, a.qkv_bias ? (long long)3 * D * 4 : 0);
+        for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+            const int c = h * hd + d;
+            float p[3][kMaxPartSlices];
+#pragma unroll
+            for (int s = 0; s < kMaxPartSlices; s++)
+#pragma unroll
+                for (int t = 0; t < 3; t++) {
+                    const long long e = s * a.qkv_slice_stride + (long long)row * 3 * D + t * D + c;
+                    p[t][s] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rp, s < S ? (int)(e * 4) : kOutOfRange, 0, 0));
+                }
+            float o[3];
+#pragma unroll
+            for (int t = 0; t < 3; t++) {
+                float v = p[t][0];
+#pragma unroll
+                for (int s = 1; s < kMaxPartSlices; s++)
+                    if (s < S) v = v + p[t][s];
+                const float bv =
+                    __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, (t * D + c) * 4, 0, 0));
+                o[t] = a.qkv_bias ? v + bv : v;
+            }
+            qs[d] = o[0];
+            const size_t at = (size_t)pos * kvd + d;
+            const_cast<float*>(K)[at] = o[1];
+            const_cast<float*>(V)[at] = o[2];
+        }
+    } else {
+        for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = a.q[(size_t)row * a.q_stride + h * hd + d];
+    }
     __syncthreads();
 
     // scores: 4 lanes per key, each taking every 4th float4 of the head (so
@@ -145,7 +183,14 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_cached(AttnArgs a) {
 // and are issued before the cache length (written by the previous kernel)
 // has arrived; keys at or past it are masked in the arithmetic (selects, so
 // whatever the unused rows hold never reaches the result).
-template <int HD4, int UNR, bool FULL, int NW = 4>
+//
+// WO (FULL, one row): the output projection in the same kernel. blockIdx.y
+// is a group of WR rows of Wo; every block of head h computes that head's
+// attention output o_h (the same values in each), then adds
+// Wo[n][h*hd .. h*hd+hd) . o_h (+ the bias, from head 0) into a.wo_out[n]
+// for its rows with float atomics. The Wo loads go out with the K/V loads.
+constexpr int kWoRows = 48;  // Wo rows per block of the fused projection
+template <int HD4, int UNR, bool FULL, int NW = 4, bool WO = false>
 __global__ __launch_bounds__(NW * 64) void k_attn_rows(AttnArgs a) {
     extern __shared__ float sc[];  // [visible keys]
     __shared__ float red[16];
@@ -157,7 +202,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_rows(AttnArgs a) {
     const int c = lane % HD4, slot = wave * KPI + lane / HD4;
 
     const int h = blockIdx.x;
-    const int row = blockIdx.y;
+    const int row = WO ? 0 : blockIdx.y;
     const int b = row / a.new_seq;
     const int i = row - b * a.new_seq;
     const int kvh = a.kv_heads ? h / ((int)gridDim.x / a.kv_heads) : h;
@@ -198,6 +243,24 @@ __global__ __launch_bounds__(NW * 64) void k_attn_rows(AttnArgs a) {
     for (int u = 0; u < UNR; u++) kv[u] = ld4(rk, kv_off(KB * u + slot));
 #pragma unroll
     for (int u = 0; u < UNR; u++) vpre[u] = ld4(rv, kv_off(KB * u + slot));
+    // fused projection: thread (row rr, 16-byte chunk cc) of the block's Wo
+    // rows; rows past the block's group or past dim read zeros
+    constexpr int WCH = HD4 / 2;                  // 16-byte chunks of a head's Wo row slice
+    constexpr int WRP = NW * 64 / WCH;            // Wo rows per pass
+    constexpr int WPASS = (kWoRows + WRP - 1) / WRP;
+    const int cc = threadIdx.x % WCH, rr = threadIdx.x / WCH;
+    u32x4 wov[WO ? WPASS : 1];
+    if constexpr (WO) {
+        const int n0 = blockIdx.y * kWoRows;
+        const int nrows = max(0, min(kWoRows, a.dim - n0));
+        const __amdgpu_buffer_rsrc_t rw =
+            make_rsrc(a.wo + (size_t)n0 * a.dim + h * (4 * HD4), nrows > 0 ? ((long long)(nrows - 1) * a.dim + 4 * HD4) * 2 : 0);
+#pragma unroll
+        for (int q = 0; q < WPASS; q++) {
+            const int rl = rr + q * WRP;
+            wov[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, rl < nrows ? (rl * a.dim + 8 * cc) * 2 : kOutOfRange, 0, 0);
+        }
+    }
     if constexpr (FULL) {
         const int pos = load_pos();
         T = a.causal ? pos + i + 1 : pos + a.new_seq;
@@ -251,7 +314,27 @@ __global__ __launch_bounds__(NW * 64) void k_attn_rows(AttnArgs a) {
             } else {
                 t = make_float4(t.x / L, t.y / L, t.z / L, t.w / L);
             }
-            *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + h * (4 * HD4) + 4 * c) = t;
+            if constexpr (WO) po[0][c] = t;
+            else *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + h * (4 * HD4) + 4 * c) = t;
+        }
+        if constexpr (WO) {
+            __syncthreads();
+            // this thread's 8 head dims (16-byte Wo chunk cc) of o_h
+            const float4 t0 = po[0][2 * cc], t1 = po[0][2 * cc + 1];
+            const float o8[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+            const int n0 = blockIdx.y * kWoRows;
+#pragma unroll
+            for (int q = 0; q < WPASS; q++) {
+                float v = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) v += bf16_lo(e & 1 ? wov[q][e >> 1] >> 16 : wov[q][e >> 1] & 0xffffu) * o8[e];
+                v = seg_sum<WCH>(v);
+                const int rl = rr + q * WRP, n = n0 + rl;
+                if (cc == 0 && rl < kWoRows && n < a.dim) {
+                    if (h == 0 && a.wo_bias) v = v + a.wo_bias[n];
+                    __hip_atomic_fetch_add(a.wo_out + n, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
         }
         return;
     }
@@ -600,83 +683,132 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
 // 4 waves per (head, row) block when there are enough blocks to fill the
 // GPU; 16 waves when the visible context is long and blocks are few, so each
 // block keeps more of the KV stream in flight.
-int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
+enum AttnRoute { kRouteFlash, kRouteRows, kRouteLong, kRouteCached16, kRouteCached4, kRouteNone };
+
+// The kernel for a: the matrix-core prefill kernel for many new rows per
+// sequence, the (key, chunk)-lane kernel for short caches, the online-softmax
+// kernel for few (head, row) blocks over a long cache, else the two-pass
+// cached kernel (16 waves when blocks are few and the cache long).
+static AttnRoute attn_route(const AttnArgs& a, int heads, int rows) {
     // the score-staging kernels hold one f32 per visible key in LDS: at most
     // the cache capacity when the cache length is read on the device, else
     // the known length
     const long long visible = a.pos_dev ? (long long)a.max_seq : (long long)a.pos_host + a.new_seq;
-    size_t lds = (size_t)visible * sizeof(float);
-    const bool lds_ok = lds <= kAttnMaxLdsBytes;
+    const bool lds_ok = (size_t)visible * sizeof(float) <= kAttnMaxLdsBytes;
     const int blocks = heads * rows;
     static const int rows_kernel = [] {
         const char* e = getenv("GORCH_HIP_ATTN_ROWS");
         return e ? atoi(e) : 1;
     }();
-    const bool aligned = (a.q_stride % 4 == 0) && (a.dim % 4 == 0) && ((a.kv_dim ? a.kv_dim : a.dim) % 4 == 0) &&
-                         ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.kc) |
-                           reinterpret_cast<uintptr_t>(a.vc) | reinterpret_cast<uintptr_t>(a.out)) % 16 == 0);
-    // many new rows per sequence (prefill): the matrix-core kernel, 128
-    // query rows per block sharing each staged K/V tile
     static const int flash_min = [] {
         const char* e = getenv("GORCH_HIP_ATTN_FLASH_MIN_ROWS");
         return e ? atoi(e) : 32;
     }();
-    if (flash_min > 0 && aligned && a.new_seq >= flash_min && (a.hd == 64 || a.hd == 128) &&
-        (a.q_stride % 4) == 0) {
-        const int batch = rows / a.new_seq;
-        const dim3 grid((a.new_seq + 127) / 128, heads, batch);
-        if (a.hd == 64) hipLaunchKernelGGL((k_attn_flash<64, 8>), grid, dim3(512), 0, s, a);
-        else hipLaunchKernelGGL((k_attn_flash<128, 8>), grid, dim3(512), 0, s, a);
-        count(CNT_ATTENTION);
-        return check_launch("attn_flash");
-    }
-    // short caches: the (key, chunk)-lane kernel; long ones stream better
-    // through the per-dim kernel below
-    if (rows_kernel && aligned && a.max_seq <= 256 && (a.hd == 64 || a.hd == 128 || a.hd == 32 || a.hd == 16)) {
-        const dim3 grid(heads, rows);
-        // one chunk of KB * UNR keys (KB = 64 NW / HD4) covers the cache: FULL
-        // (head dim 128 past 128 rows: 8 waves, 256 keys)
-        const int ms = a.max_seq;
-        switch (a.hd) {
-            case 128:
-                if (ms <= 128) hipLaunchKernelGGL((k_attn_rows<32, 16, true>), grid, dim3(256), lds, s, a);
-                else hipLaunchKernelGGL((k_attn_rows<32, 16, true, 8>), grid, dim3(512), lds, s, a);
-                break;
-            case 64:
-                if (ms <= 128) hipLaunchKernelGGL((k_attn_rows<16, 8, true>), grid, dim3(256), lds, s, a);
-                else hipLaunchKernelGGL((k_attn_rows<16, 16, true>), grid, dim3(256), lds, s, a);
-                break;
-            case 32: hipLaunchKernelGGL((k_attn_rows<8, 8, true>), grid, dim3(256), lds, s, a); break;
-            default: hipLaunchKernelGGL((k_attn_rows<4, 4, true>), grid, dim3(256), lds, s, a); break;
-        }
-        count(CNT_ATTENTION);
-        return check_launch("attn_rows");
-    }
-    // few (head, row) blocks over a long cache (a batch-1 step): the
-    // online-softmax kernel keeps two 256-key chunks in flight per block;
-    // with hundreds of blocks the two-pass kernel below streams better
-    // (measured: XL batch 16, 400 blocks, 29.4 vs 25 us per layer)
     static const int long_kernel = [] {
         const char* e = getenv("GORCH_HIP_ATTN_LONG");
         return e ? atoi(e) : 1;
     }();
-    if (long_kernel && aligned && (blocks < 128 || !lds_ok) && (a.hd == 64 || a.hd == 128)) {
-        const dim3 grid(heads, rows);
-        if (a.hd == 64) hipLaunchKernelGGL((k_attn_long<16, 16, 4>), grid, dim3(1024), 0, s, a);
-        else hipLaunchKernelGGL((k_attn_long<32, 16, 4>), grid, dim3(1024), 0, s, a);
-        count(CNT_ATTENTION);
-        return check_launch("attn_long");
-    }
-    if (!lds_ok) {
-        set_error("attention: a cache longer than 16384 visible rows needs head_dim 64 or 128 and 16-byte aligned rows");
+    const bool aligned = (a.q_stride % 4 == 0) && (a.dim % 4 == 0) && ((a.kv_dim ? a.kv_dim : a.dim) % 4 == 0) &&
+                         ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.kc) |
+                           reinterpret_cast<uintptr_t>(a.vc) | reinterpret_cast<uintptr_t>(a.out)) % 16 == 0);
+    const auto cached = [&] {
+        if (!lds_ok) return kRouteNone;
+        return (blocks < 1024 && a.max_seq >= 128) ? kRouteCached16 : kRouteCached4;
+    };
+    // split QKV partials: only the two-pass kernel adds them
+    if (a.qkv_part) return cached();
+    if (flash_min > 0 && aligned && a.new_seq >= flash_min && (a.hd == 64 || a.hd == 128)) return kRouteFlash;
+    if (rows_kernel && aligned && a.max_seq <= 256 && (a.hd == 64 || a.hd == 128 || a.hd == 32 || a.hd == 16))
+        return kRouteRows;
+    // (measured: XL batch 16, 400 blocks, two-pass 25 vs online-softmax
+    // 29.4 us per layer)
+    if (long_kernel && aligned && (blocks < 128 || !lds_ok) && (a.hd == 64 || a.hd == 128)) return kRouteLong;
+    return cached();
+}
+
+bool attn_rows_wo_ok(const AttnArgs& a, int heads, int rows) {
+    AttnArgs b = a;
+    b.wo = nullptr;
+    return rows == 1 && a.new_seq == 1 && a.kv_heads == 0 && a.hd == 64 && a.max_seq <= 256 &&
+           a.dim % 8 == 0 && heads * a.hd == a.dim && attn_route(b, heads, rows) == kRouteRows;
+}
+
+int launch_attn_rows_wo(hipStream_t s, const AttnArgs& a, int heads) {
+    if (!attn_rows_wo_ok(a, heads, 1) || !a.wo || !a.wo_out || (reinterpret_cast<uintptr_t>(a.wo) % 16) != 0) {
+        set_error("attention: the fused output projection needs one new row, head_dim 64, a cache of <= 256 rows");
         return GORCH_HIP_EUNSUPPORTED;
     }
-    if (blocks < 1024 && a.max_seq >= 128)
-        hipLaunchKernelGGL(k_attn_cached<16>, dim3(heads, rows), dim3(1024), lds, s, a);
-    else
-        hipLaunchKernelGGL(k_attn_cached<4>, dim3(heads, rows), dim3(256), lds, s, a);
+    const size_t lds = (size_t)a.max_seq * sizeof(float);
+    const dim3 grid(heads, (a.dim + kWoRows - 1) / kWoRows);
+    if (a.max_seq <= 128) hipLaunchKernelGGL((k_attn_rows<16, 8, true, 4, true>), grid, dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((k_attn_rows<16, 16, true, 4, true>), grid, dim3(256), lds, s, a);
     count(CNT_ATTENTION);
-    return check_launch("attn_cached");
+    return check_launch("attn_rows_wo");
+}
+
+bool attn_takes_qkv_part(const AttnArgs& a, int heads, int rows) {
+    if (a.new_seq != 1 || a.kv_heads != 0) return false;
+    const AttnRoute r = attn_route(a, heads, rows);
+    return r == kRouteCached16 || r == kRouteCached4;
+}
+
+int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
+    const long long visible = a.pos_dev ? (long long)a.max_seq : (long long)a.pos_host + a.new_seq;
+    const size_t lds = (size_t)visible * sizeof(float);
+    if (a.qkv_part && (a.new_seq != 1 || a.kv_heads != 0 || a.qkv_slices < 1 || a.qkv_slices > kMaxPartSlices)) {
+        set_error("attention: split QKV partials need one new row per sequence, no grouped KV heads, 1..8 slices");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
+    const dim3 grid(heads, rows);
+    switch (attn_route(a, heads, rows)) {
+        case kRouteFlash: {
+            // many new rows per sequence (prefill): the matrix-core kernel,
+            // 128 query rows per block sharing each staged K/V tile
+            const int batch = rows / a.new_seq;
+            const dim3 fg((a.new_seq + 127) / 128, heads, batch);
+            if (a.hd == 64) hipLaunchKernelGGL((k_attn_flash<64, 8>), fg, dim3(512), 0, s, a);
+            else hipLaunchKernelGGL((k_attn_flash<128, 8>), fg, dim3(512), 0, s, a);
+            count(CNT_ATTENTION);
+            return check_launch("attn_flash");
+        }
+        case kRouteRows: {
+            // one chunk of KB * UNR keys (KB = 64 NW / HD4) covers the cache:
+            // FULL (head dim 128 past 128 rows: 8 waves, 256 keys)
+            const int ms = a.max_seq;
+            switch (a.hd) {
+                case 128:
+                    if (ms <= 128) hipLaunchKernelGGL((k_attn_rows<32, 16, true>), grid, dim3(256), lds, s, a);
+                    else hipLaunchKernelGGL((k_attn_rows<32, 16, true, 8>), grid, dim3(512), lds, s, a);
+                    break;
+                case 64:
+                    if (ms <= 128) hipLaunchKernelGGL((k_attn_rows<16, 8, true>), grid, dim3(256), lds, s, a);
+                    else hipLaunchKernelGGL((k_attn_rows<16, 16, true>), grid, dim3(256), lds, s, a);
+                    break;
+                case 32: hipLaunchKernelGGL((k_attn_rows<8, 8, true>), grid, dim3(256), lds, s, a); break;
+                default: hipLaunchKernelGGL((k_attn_rows<4, 4, true>), grid, dim3(256), lds, s, a); break;
+            }
+            count(CNT_ATTENTION);
+            return check_launch("attn_rows");
+        }
+        case kRouteLong:
+            // few (head, row) blocks over a long cache (a batch-1 step): two
+            // 256-key chunks in flight per block
+            if (a.hd == 64) hipLaunchKernelGGL((k_attn_long<16, 16, 4>), grid, dim3(1024), 0, s, a);
+            else hipLaunchKernelGGL((k_attn_long<32, 16, 4>), grid, dim3(1024), 0, s, a);
+            count(CNT_ATTENTION);
+            return check_launch("attn_long");
+        case kRouteCached16:
+            hipLaunchKernelGGL(k_attn_cached<16>, grid, dim3(1024), lds, s, a);
+            count(CNT_ATTENTION);
+            return check_launch("attn_cached");
+        case kRouteCached4:
+            hipLaunchKernelGGL(k_attn_cached<4>, grid, dim3(256), lds, s, a);
+            count(CNT_ATTENTION);
+            return check_launch("attn_cached");
+        default:
+            set_error("attention: a cache longer than 16384 visible rows needs head_dim 64 or 128 and 16-byte aligned rows");
+            return GORCH_HIP_EUNSUPPORTED;
+    }
 }
 
 // softmax_metal.go:111-141

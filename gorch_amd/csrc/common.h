@@ -54,6 +54,9 @@ struct LinearExtras {
     // values and the GEMV reads silu(gate) * up
     bool swiglu = false;
 };
+// Most K slices a K-split partial buffer holds (k_splitk_epilogue, the
+// row reducer, the split QKV input of the cached attention).
+constexpr int kMaxPartSlices = 8;
 // Number of K slices a K-split Linear actually uses for a requested count
 // (slices are multiples of 32 wide).
 inline int ksplit_slices(int K, int S) {
@@ -257,7 +260,33 @@ struct AttnArgs {
     int kv_heads;  // grouped-query attention: KV heads (0 = one per query head)
     int kv_dim;    // cache row stride in floats (0 = dim)
     int recip;     // normalise by multiplying with 1/sum (GQA) instead of dividing
+    // One new row per sequence (new_seq == 1, no grouped KV heads) whose
+    // fused QKV Linear ran split over K: q, k and v of the row are qkv_bias
+    // + the qkv_slices partial sums at qkv_part ([slice][row][3 * dim],
+    // slices qkv_slice_stride floats apart, added in slice order). The
+    // kernel writes k and v into the cache at row pos itself (its block is
+    // the only reader of that head's slice in this step); q is not stored.
+    const float* qkv_part = nullptr;
+    const float* qkv_bias = nullptr;
+    int qkv_slices = 0;
+    long long qkv_slice_stride = 0;
+    // The output projection fused into the one-row attention kernel
+    // (launch_attn_rows_wo): wo_out[n] += sum_c wo[n][h*hd + c] * o_h[c]
+    // for every head h (+ wo_bias[n] once), wo bf16 [dim][dim] row-major
+    const uint16_t* wo = nullptr;
+    const float* wo_bias = nullptr;
+    float* wo_out = nullptr;
 };
+// The kernel launch_attn_cached picks for a; true when it is the two-pass
+// cached kernel, the one that takes split QKV partials.
+bool attn_takes_qkv_part(const AttnArgs& a, int heads, int rows);
+// One new row of one sequence with the output projection fused (a.wo,
+// a.wo_bias, a.wo_out set): launch_attn_rows_wo adds Wo . attention + bias
+// into a.wo_out with float atomics (so the order of the per-head additions
+// varies between runs). attn_rows_wo_ok: the shapes it takes (the one-pass
+// short-cache kernel's).
+bool attn_rows_wo_ok(const AttnArgs& a, int heads, int rows);
+int launch_attn_rows_wo(hipStream_t s, const AttnArgs& a, int heads);
 // LDS the score-staging attention kernels may take (one f32 per visible
 // key: 16384 keys); longer caches go to the online-softmax kernel.
 constexpr size_t kAttnMaxLdsBytes = 65536;

@@ -1012,7 +1012,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
 // Epilogue of a K-split Linear: y[m, n] = epi(sum_s part[s][m][n] + bias[n])
 // (+ residual), slices added in order, written through the output
 // descriptor. All slice loads of an element are issued before the adds.
-constexpr int kEpiSlices = 8;
+constexpr int kEpiSlices = kMaxPartSlices;
 __global__ __launch_bounds__(256) void k_splitk_epilogue(const float* __restrict__ part, int S, int M, int N,
                                                          const float* __restrict__ bias, const float* residual,
                                                          OutDesc od, int epilogue) {

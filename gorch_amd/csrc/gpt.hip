@@ -64,6 +64,9 @@ struct gorch_hip_gpt {
     // and the LayerNorm row statistics they leave for the next GEMV
     float* part = nullptr;
     float2* stats = nullptr;
+    // batched one-token steps: K-split partials of the fused QKV Linear,
+    // summed by the cached attention kernel
+    float* wpart = nullptr;
     int* ids = nullptr;
     size_t ids_cap = 0;
     hipStream_t stream = nullptr;  // engine stream (default priority), used for graph capture
@@ -116,6 +119,7 @@ static int ensure_acts(gorch_hip_gpt* g, size_t rows, size_t logit_rows) {
         if (!g->part) {
             GH_TRY(check(hipMalloc(&g->part, (size_t)kMaxSplit * 16 * d * 4), "hipMalloc part"));
             GH_TRY(check(hipMalloc(&g->stats, 16 * sizeof(float2)), "hipMalloc stats"));
+            GH_TRY(check(hipMalloc(&g->wpart, (size_t)kMaxPartSlices * 16 * 3 * d * 4), "hipMalloc wpart"));
         }
     }
     if (logit_rows > g->logit_rows_cap) {
@@ -162,6 +166,29 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         const char* e = getenv("GORCH_HIP_SPLIT_NT");
         return e ? atoi(e) : 4;
     }();
+    // Batched steps over tile-packed weights split the Linears over K: every
+    // block of a K slice loads that slice of the activations, so activation
+    // traffic is (blocks per slice) x (activation bytes): at 16 rows, d 1600,
+    // 1.7x the weight bytes for an unsplit fused QKV and 2.6x for Wo in 2
+    // slices. 8 slices (GORCH_HIP_QKV_SPLIT, GORCH_HIP_RES_SPLIT) keep it
+    // near a fifth; the partials of the fused QKV are added by the attention
+    // kernel, those of Wo and FFN2 by the row reducer.
+    static const int qkv_split_req = [] {
+        const char* e = getenv("GORCH_HIP_QKV_SPLIT");
+        return std::min(kMaxPartSlices, e ? atoi(e) : 1);
+    }();
+    static const int res_split_req = [] {
+        const char* e = getenv("GORCH_HIP_RES_SPLIT");
+        return std::min(kMaxSplit, e ? atoi(e) : 0);
+    }();
+    // GORCH_HIP_WO_FUSE=0 keeps the one-row output projection a GEMV of its own
+    static const bool wo_fuse = [] {
+        const char* e = getenv("GORCH_HIP_WO_FUSE");
+        return e ? atoi(e) != 0 : true;
+    }();
+    auto res_split = [&](int K) {
+        return res_split_req > 0 ? ksplit_slices(K, res_split_req) : packed_split_slices(K, d);
+    };
     auto split_for = [&](int K) {
         const int tiles = ((d + 15) / 16 + split_nt - 1) / split_nt;
         int S = std::min(kMaxSplit, std::max(1, split_blocks / tiles));
@@ -191,8 +218,25 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             od.row_stride[sgi] = d;
             od.use_pos[sgi] = 1;
         }
+        AttnArgs a{g->q, kc_layer(c, l), vc_layer(c, l), g->att, pos, 0, n, d, hd, c->capacity, d, 1,
+                   1.0f / (float)sqrt((double)hd)};
+        // one token per sequence over tile-packed weights: the fused QKV
+        // Linear split over K into raw partials; the attention kernel adds
+        // the slices and the bias and writes the K/V cache rows
+        const bool qkv_split = batched && w.wqkv_p && n == 1 && qkv_split_req > 1 &&
+                               attn_takes_qkv_part(a, g->heads, rows);
         LinearExtras ln1, ln2;
-        if (batched && w.wqkv_p) {
+        if (qkv_split) {
+            LinearExtras sp;
+            sp.part = g->wpart;
+            sp.ksplit = qkv_split_req;
+            GH_TRY(launch_linear_packed_od(s, g->h, w.wqkv_p, nullptr, nullptr, OutDesc::plain(nullptr, 3 * d), rows,
+                                           3 * d, d, GORCH_HIP_EPI_NONE, sp));
+            a.qkv_part = g->wpart;
+            a.qkv_bias = w.bqkv;
+            a.qkv_slices = ksplit_slices(d, qkv_split_req);
+            a.qkv_slice_stride = (long long)rows * 3 * d;
+        } else if (batched && w.wqkv_p) {
             GH_TRY(launch_linear_packed_od(s, g->h, w.wqkv_p, w.bqkv, nullptr, od, rows, 3 * d, d,
                                            GORCH_HIP_EPI_NONE, LinearExtras{}));
         } else if (batched) {
@@ -211,13 +255,21 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             GH_TRY(launch_linear_bf16_od(s, g->h, w.wqkv, w.bqkv, nullptr, od, rows, 3 * d, d, GORCH_HIP_EPI_NONE,
                                          LinearExtras{}));
         }
-        AttnArgs a{g->q, kc_layer(c, l), vc_layer(c, l), g->att, pos, 0, n, d, hd, c->capacity, d, 1,
-                   1.0f / (float)sqrt((double)hd)};
-        GH_TRY(launch_attn_cached(s, a, g->heads, rows));
-        if (batched) {
+        // one row (batch 1, one token): the output projection runs inside
+        // the attention kernel, which adds Wo . attention + bias into x
+        const bool wo_fused = !batched && rows == 1 && wo_fuse && attn_rows_wo_ok(a, g->heads, rows);
+        if (wo_fused) {
+            a.wo = w.wo;
+            a.wo_bias = w.bo;
+            a.wo_out = g->x;
+            GH_TRY(launch_attn_rows_wo(s, a, g->heads));
+        } else {
+            GH_TRY(launch_attn_cached(s, a, g->heads, rows));
+        }
+        if (!wo_fused && batched) {
             LinearExtras sp;
             sp.part = g->part;
-            sp.ksplit = w.wo_p ? packed_split_slices(d, d) : split_for(d);
+            sp.ksplit = w.wo_p ? res_split(d) : split_for(d);
             if (w.wo_p)
                 GH_TRY(launch_linear_packed_od(s, g->att, w.wo_p, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d,
                                                d, GORCH_HIP_EPI_NONE, sp));
@@ -226,7 +278,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
                                              GORCH_HIP_EPI_NONE, sp));
             GH_TRY(launch_reduce_rows(s, g->part, sp.ksplit, w.bo, g->x, rows, d, eps, g->stats, w.ln2_g, w.ln2_b,
                                       g->h));
-        } else {
+        } else if (!wo_fused) {
             GH_TRY(launch_linear_bf16(s, g->att, w.wo, w.bo, g->x, g->x, rows, d, d, GORCH_HIP_EPI_NONE));
         }
         if (batched && w.w1_p) {
@@ -244,7 +296,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         if (batched) {
             LinearExtras sp;
             sp.part = g->part;
-            sp.ksplit = w.w2_p ? packed_split_slices(4 * d, d) : split_for(4 * d);
+            sp.ksplit = w.w2_p ? res_split(4 * d) : split_for(4 * d);
             if (w.w2_p)
                 GH_TRY(launch_linear_packed_od(s, g->ff, w.w2_p, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d,
                                                4 * d, GORCH_HIP_EPI_NONE, sp));
@@ -630,6 +682,7 @@ void gorch_hip_gpt_free(gorch_hip_gpt* g) {
     (void)hipFree(g->logits);
     (void)hipFree(g->part);
     (void)hipFree(g->stats);
+    (void)hipFree(g->wpart);
     (void)hipFree(g->ids);
     delete g;
 }
