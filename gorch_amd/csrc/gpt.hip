@@ -144,9 +144,10 @@ static int ensure_acts(gorch_hip_gpt* g, size_t rows, size_t logit_rows) {
 // [batch*n, V]); otherwise only on the last row of each sequence
 // (logits [batch, V]). With at most 16 rows the LayerNorms run inside the
 // following GEMV; argmax_key (last-row mode, batch <= 16) receives the
-// packed greedy choice per sequence. Does not advance pos.
+// packed greedy choice per sequence. x_ready: x already holds the input
+// rows (k_finalize_embed wrote them). Does not advance pos.
 static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows, hipStream_t s,
-                   unsigned long long* argmax_key) {
+                   unsigned long long* argmax_key, bool x_ready = false) {
     const int d = g->dim, B = c->batch, rows = B * n, hd = d / g->heads;
     const float eps = 1e-5f;
     const int* pos = c->state;
@@ -194,7 +195,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         int S = std::min(kMaxSplit, std::max(1, split_blocks / tiles));
         return ksplit_slices(K, S);
     };
-    GH_TRY(launch_embed_pos(s, g->wte, g->wpe, g->ids, pos, g->x, d, n, rows));
+    if (!x_ready) GH_TRY(launch_embed_pos(s, g->wte, g->wpe, g->ids, pos, g->x, d, n, rows));
     if (batched)
         GH_TRY(launch_reduce_rows(s, nullptr, 0, nullptr, g->x, rows, d, eps, g->stats, g->L[0].ln1_g,
                                   g->L[0].ln1_b, g->h));
@@ -387,7 +388,47 @@ __global__ void k_finalize_step(unsigned long long* key, int B, int* ids, int* h
     }
 }
 
-static int choose_tokens(gorch_hip_gpt* g, gorch_hip_kvcache* c, int inc, hipStream_t s) {
+// k_finalize_step and the next step's embedding in one launch (up to 16
+// sequences): the chosen tokens' wte rows plus the wpe row of the advanced
+// position become the next step's input x (k_embed_pos's sum). After the
+// last step the position can reach max_seq; that x is never used and reads
+// wpe's last row.
+__global__ __launch_bounds__(1024) void k_finalize_embed(unsigned long long* key, int B, int* ids, int* hist,
+                                                         int* state, int inc, const float* __restrict__ wte,
+                                                         const float* __restrict__ wpe, float* __restrict__ x,
+                                                         int dim, int max_seq) {
+    __shared__ int tok[16];
+    const int step = state[1];
+    const int pos = state[0] + inc;
+    if ((int)threadIdx.x < B) {
+        const int t = argmax_unpack(key[threadIdx.x]);
+        tok[threadIdx.x] = t;
+        ids[threadIdx.x] = t;
+        hist[(size_t)step * B + threadIdx.x] = t;
+        key[threadIdx.x] = 0ull;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        state[0] = pos;
+        state[1] = step + 1;
+    }
+    const float* pe = wpe + (size_t)min(pos, max_seq - 1) * dim;
+    for (int i = threadIdx.x; i < B * dim; i += blockDim.x) {
+        const int b = i / dim, col = i - b * dim;
+        x[i] = wte[(size_t)tok[b] * dim + col] + pe[col];
+    }
+}
+
+// Decodes the chosen tokens (see k_finalize_step); with embed_next (batches
+// of up to 16) it also writes the next step's input rows, and the next
+// forward then skips its embedding.
+static int choose_tokens(gorch_hip_gpt* g, gorch_hip_kvcache* c, int inc, hipStream_t s, bool embed_next = false) {
+    if (c->batch <= 16 && embed_next) {
+        hipLaunchKernelGGL(k_finalize_embed, dim3(1), dim3(c->batch * g->dim >= 4096 ? 1024 : 256), 0, s, c->key,
+                           c->batch, g->ids, c->hist, c->state, inc, g->wte, g->wpe, g->x, g->dim, g->max_seq);
+        count(CNT_ARGMAX);
+        return check_launch("finalize_embed");
+    }
     if (c->batch <= 16) {
         hipLaunchKernelGGL(k_finalize_step, dim3(1), dim3(64), 0, s, c->key, c->batch, g->ids, c->hist, c->state,
                            inc);
@@ -834,7 +875,9 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
         }
         (void)hipEventRecord(ev[0], s);
         // prefill: logits of the last prompt row per sequence -> token 0
-        if (forward(g, c, np, false, s, c->key) || choose_tokens(g, c, np, s)) {
+        // batches of up to 16: each choice also embeds the next step's input
+        const bool fin_embed = batch <= 16;
+        if (forward(g, c, np, false, s, c->key) || choose_tokens(g, c, np, s, fin_embed)) {
             fail(GORCH_HIP_ERUNTIME);
             break;
         }
@@ -845,8 +888,8 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
         }
         // one decode step: forward the latest token of each sequence, choose the next
         auto step = [&]() -> int {
-            GH_TRY(forward(g, c, 1, false, s, c->key));
-            return choose_tokens(g, c, 1, s);
+            GH_TRY(forward(g, c, 1, false, s, c->key, fin_embed));
+            return choose_tokens(g, c, 1, s, fin_embed);
         };
         if (use_graph && forwards > 0) {
             // capture the step once (or again when a buffer it points at moved)
