@@ -29,7 +29,7 @@
 
 namespace gh {
 
-template <int BM, int BNW, int NB, bool SPLIT, int BK = 64>
+template <int BM, int BNW, int NB, bool SPLIT, int BK = 64, bool IL = false>
 struct WideGemm {
     static constexpr int kThreads = 512;  // 8 waves: 2 (rows) x 4 (columns)
     static constexpr int CH = BK / 8;     // 16-byte chunks per row and stage
@@ -147,6 +147,77 @@ struct WideGemm {
             }
         };
 
+        // IL: one stage as an interleaved schedule. The fragments of both
+        // 32-wide halves of the stage are read up front; the second half's
+        // reads are spread between the first half's MFMAs, and the next
+        // stage's LDS writes and global loads between the second half's, so
+        // the matrix cores wait less on LDS round trips (measured: the MoE
+        // gate/up GEMM 191 -> 183 us, down 119 -> 110 us).
+        struct Frag {
+            bf16x8 b[NB][TN];
+            bf16x8 a[TM][NA];
+        };
+        auto read_frags = [&](int buf, int kk, Frag& f) {
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    f.b[b][j] = *reinterpret_cast<const bf16x8*>(
+                        &sm.w[buf][b][wn * WNW + j * 16 + r][8 * swz(r, 4 * kk + g)]);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int p = 0; p < NA; p++)
+                    f.a[i][p] = *reinterpret_cast<const bf16x8*>(
+                        &sm.a[buf][p][wm * WM + i * 16 + r][8 * swz(r, 4 * kk + g)]);
+        };
+        auto mfmas = [&](const Frag& f) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int p = 0; p < NA; p++)
+#pragma unroll
+                    for (int b = 0; b < NB; b++)
+#pragma unroll
+                        for (int j = 0; j < TN; j++) acc[b][i][j] = mfma16x16x32(f.a[i][p], f.b[b][j], acc[b][i][j]);
+        };
+        constexpr int NFR = NB * TN + TM * NA;   // fragment reads per half
+        constexpr int NMF = TM * NA * NB * TN;   // MFMAs per half
+        constexpr int NLD = A_U4 + W_U4;         // LDS writes (and global loads) per stage
+        static_assert(!IL || (BK == 64 && NMF >= NFR && NMF >= 2 * NLD), "interleave shape");
+        auto stage_il = [&](int buf, u32x4 (&ar)[A_U4], u32x4 (&wr)[W_U4], int next) {
+            Frag f0, f1;
+            read_frags(buf, 0, f0);
+            read_frags(buf, 1, f1);
+            mfmas(f0);
+            sstore(buf ^ 1, ar, wr);
+            gload(next, ar, wr);
+            mfmas(f1);
+            // scheduling groups (mask 0x100 LDS reads, 0x008 MFMAs, 0x200
+            // LDS writes, 0x020 global loads): f0's reads; f1's reads spread
+            // between f0's MFMAs; the next stage's writes and loads between
+            // f1's MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x100, NFR, 0);
+#pragma unroll
+            for (int q = 0; q < NFR; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, NMF / NFR, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NMF - NFR * (NMF / NFR), 0);
+#pragma unroll
+            for (int q = 0; q < NLD; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+            }
+#pragma unroll
+            for (int q = 0; q < NLD; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NMF - 2 * NLD, 0);
+            __syncthreads();
+        };
+
         // stage s lives in register set s % 2 until it is stored to LDS
         // buffer s % 2; stage s + 3 is requested once stage s + 1 has left
         // its registers. The body is unconditional (stages past K load
@@ -159,14 +230,19 @@ struct WideGemm {
         gload(2, ra[0], rw[0]);
         __syncthreads();
         for (int it = 0; it < nk2; it += 2) {
-            compute(0);
-            sstore(1, ra[1], rw[1]);
-            gload(it + 3, ra[1], rw[1]);
-            __syncthreads();
-            compute(1);
-            sstore(0, ra[0], rw[0]);
-            gload(it + 4, ra[0], rw[0]);
-            __syncthreads();
+            if constexpr (IL) {
+                stage_il(0, ra[1], rw[1], it + 3);
+                stage_il(1, ra[0], rw[0], it + 4);
+            } else {
+                compute(0);
+                sstore(1, ra[1], rw[1]);
+                gload(it + 3, ra[1], rw[1]);
+                __syncthreads();
+                compute(1);
+                sstore(0, ra[0], rw[0]);
+                gload(it + 4, ra[0], rw[0]);
+                __syncthreads();
+            }
         }
 
         // lane holds rows 4g..4g+3 of column r in each 16x16 fragment

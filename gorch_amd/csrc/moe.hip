@@ -462,14 +462,14 @@ __global__ void k_moe_gather_split(const float* __restrict__ x, const int* __res
 // A: planes (hi, lo) of [rows, Kd]. DUAL: gate and up side by side, H =
 // SwiGLU(gate, up) written as planes (Chi, Clo); else C = (acc + b) * w(row)
 // in f32.
-template <bool DUAL, int BNW>
+template <bool DUAL, int BNW, bool IL = false>
 __global__ __launch_bounds__(512) void k_moe_wide(const uint16_t* __restrict__ Ahi, const uint16_t* __restrict__ Alo,
                                                   const uint16_t* __restrict__ W1, const uint16_t* __restrict__ W2,
                                                   const float* __restrict__ b1, const float* __restrict__ b2,
                                                   float* __restrict__ C, uint16_t* __restrict__ Chi,
                                                   uint16_t* __restrict__ Clo, int N, int Kd, long long cslice,
                                                   MoeWs ws) {
-    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true>;
+    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true, 64, IL>;
     extern __shared__ __align__(16) uint4 moe_smem[];
     if ((int)blockIdx.y >= *ws.ntiles) return;
     const int e = ws.tile_e[blockIdx.y], r0 = ws.tile_r0[blockIdx.y], nrows = ws.tile_n[blockIdx.y];
@@ -514,21 +514,35 @@ __global__ __launch_bounds__(512) void k_moe_wide(const uint16_t* __restrict__ A
            store);
 }
 
-template <bool DUAL, int BNW>
-static int launch_moe_wide(hipStream_t s, dim3 grid, const uint16_t* Ahi, const uint16_t* Alo, const uint16_t* W1,
-                           const uint16_t* W2, const float* b1, const float* b2, float* C, uint16_t* Chi,
-                           uint16_t* Clo, int N, int Kd, long long cslice, const MoeWs& ws) {
-    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true>;
+template <bool DUAL, int BNW, bool IL>
+static int launch_moe_wide_t(hipStream_t s, dim3 grid, const uint16_t* Ahi, const uint16_t* Alo, const uint16_t* W1,
+                             const uint16_t* W2, const float* b1, const float* b2, float* C, uint16_t* Chi,
+                             uint16_t* Clo, int N, int Kd, long long cslice, const MoeWs& ws) {
+    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true, 64, IL>;
     static bool attr_set = false;
     if (!attr_set) {
-        GH_TRY(check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_moe_wide<DUAL, BNW>),
+        GH_TRY(check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_moe_wide<DUAL, BNW, IL>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(typename G::Smem)),
                      "moe_wide attribute"));
         attr_set = true;
     }
-    hipLaunchKernelGGL((k_moe_wide<DUAL, BNW>), grid, dim3(G::kThreads), sizeof(typename G::Smem), s, Ahi, Alo, W1,
-                       W2, b1, b2, C, Chi, Clo, N, Kd, cslice, ws);
+    hipLaunchKernelGGL((k_moe_wide<DUAL, BNW, IL>), grid, dim3(G::kThreads), sizeof(typename G::Smem), s, Ahi, Alo,
+                       W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice, ws);
     return check_launch(DUAL ? "moe_wide_gate_up" : "moe_wide_down");
+}
+
+// GORCH_HIP_MOE_IL=0 keeps the compiler's own schedule of the main loop
+template <bool DUAL, int BNW>
+static int launch_moe_wide(hipStream_t s, dim3 grid, const uint16_t* Ahi, const uint16_t* Alo, const uint16_t* W1,
+                           const uint16_t* W2, const float* b1, const float* b2, float* C, uint16_t* Chi,
+                           uint16_t* Clo, int N, int Kd, long long cslice, const MoeWs& ws) {
+    static const bool il = [] {
+        const char* e = getenv("GORCH_HIP_MOE_IL");
+        return !e || atoi(e) != 0;
+    }();
+    if (il)
+        return launch_moe_wide_t<DUAL, BNW, true>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice, ws);
+    return launch_moe_wide_t<DUAL, BNW, false>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice, ws);
 }
 
 }  // namespace gh
