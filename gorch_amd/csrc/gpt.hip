@@ -413,6 +413,28 @@ __global__ __launch_bounds__(1024) void k_finalize_embed(unsigned long long* key
         state[1] = step + 1;
     }
     const float* pe = wpe + (size_t)min(pos, max_seq - 1) * dim;
+    constexpr int kV = 8;
+    if (dim % 4 == 0 && B * (dim / 4) <= kV * (int)blockDim.x) {
+        // at most 8 float4 per thread (16 rows of 2048 floats with 1024
+        // threads), all loads issued before the adds and stores
+        const int d4 = dim / 4, n4 = B * d4;
+        float4 e[kV], p[kV];
+#pragma unroll
+        for (int u = 0; u < kV; u++) {
+            const int i = min((int)threadIdx.x + u * (int)blockDim.x, n4 - 1);
+            const int b = i / d4, c4 = i - b * d4;
+            e[u] = reinterpret_cast<const float4*>(wte + (size_t)tok[b] * dim)[c4];
+            p[u] = reinterpret_cast<const float4*>(pe)[c4];
+        }
+#pragma unroll
+        for (int u = 0; u < kV; u++) {
+            const int i = (int)threadIdx.x + u * (int)blockDim.x;
+            if (i < n4)
+                reinterpret_cast<float4*>(x)[i] =
+                    make_float4(e[u].x + p[u].x, e[u].y + p[u].y, e[u].z + p[u].z, e[u].w + p[u].w);
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < B * dim; i += blockDim.x) {
         const int b = i / dim, col = i - b * dim;
         x[i] = wte[(size_t)tok[b] * dim + col] + pe[col];
@@ -424,7 +446,8 @@ __global__ __launch_bounds__(1024) void k_finalize_embed(unsigned long long* key
 // forward then skips its embedding.
 static int choose_tokens(gorch_hip_gpt* g, gorch_hip_kvcache* c, int inc, hipStream_t s, bool embed_next = false) {
     if (c->batch <= 16 && embed_next) {
-        hipLaunchKernelGGL(k_finalize_embed, dim3(1), dim3(c->batch * g->dim >= 4096 ? 1024 : 256), 0, s, c->key,
+        // 1024 threads cover 16 rows of 2048 floats with 8 float4 each
+        hipLaunchKernelGGL(k_finalize_embed, dim3(1), dim3(c->batch * g->dim > 8 * 4 * 256 ? 1024 : 256), 0, s, c->key,
                            c->batch, g->ids, c->hist, c->state, inc, g->wte, g->wpe, g->x, g->dim, g->max_seq);
         count(CNT_ARGMAX);
         return check_launch("finalize_embed");
