@@ -14,6 +14,8 @@
 // iteration, 2-step shuffle reduce); block max / sum by LDS reduction; then
 // P.V with lanes across the head's dims (coalesced 256-byte rows) and waves
 // across keys, the 4 wave partials summed in wave order.
+#include <algorithm>
+
 #include "common.h"
 
 namespace gh {
@@ -547,7 +549,12 @@ __global__ __launch_bounds__(NW * 64) void k_attn_flash(AttnArgs a) {
 // branch-free) are in flight while one is used. At the end every slot is
 // rescaled to the block's max and the slots are summed through LDS: out =
 // sum o / sum l.
-template <int HD4, int NW, int UNR>
+// SPLIT (one new row of one sequence): blockIdx.y is a chunk of the keys
+// (gridDim.y chunks of a multiple of KC keys each); the block writes its
+// chunk's max, weight sum and unnormalised weighted values to a.split_ws
+// for k_attn_combine instead of the output. Each head's cache then streams
+// through gridDim.y CUs instead of one.
+template <int HD4, int NW, int UNR, bool SPLIT = false>
 __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
     constexpr int KPI = 64 / HD4;  // keys per wavefront instruction
     constexpr int KB = NW * KPI;   // keys per block instruction
@@ -560,7 +567,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane % HD4, slot = wave * KPI + lane / HD4;
     const int h = blockIdx.x;
-    const int row = blockIdx.y;
+    const int row = SPLIT ? 0 : blockIdx.y;
     const int b = row / a.new_seq;
     const int i = row - b * a.new_seq;
     const int kvh = a.kv_heads ? h / ((int)gridDim.x / a.kv_heads) : h;
@@ -568,6 +575,14 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
     const size_t base = ((size_t)b * a.max_seq) * kvd + (size_t)kvh * (4 * HD4);
     const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
     const int T = a.causal ? pos + i + 1 : pos + a.new_seq;
+    // keys [jb, je) of this block
+    int jb = 0, je = T;
+    if constexpr (SPLIT) {
+        const int nc = gridDim.y;
+        const int L = ((T + nc - 1) / nc + KC - 1) / KC * KC;
+        jb = min(T, (int)blockIdx.y * L);
+        je = min(T, jb + L);
+    }
     const long long span = T > 0 ? ((long long)(T - 1) * kvd + 4 * HD4) * 4 : 0;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.kc + base, span);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.vc + base, span);
@@ -595,7 +610,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
         for (int u = 0; u < UNR; u++) {
             const float d = q.x * kk[u].x + q.y * kk[u].y + q.z * kk[u].z + q.w * kk[u].w;
             sj[u] = seg_sum<HD4>(d) * a.scale;
-            if (j0 + KB * u + slot < T) cm = fmaxf(cm, sj[u]);
+            if (j0 + KB * u + slot < je) cm = fmaxf(cm, sj[u]);
         }
         if (cm > -INFINITY) {
             const float mn = fmaxf(m, cm);
@@ -604,7 +619,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
             o = make_float4(o.x * al, o.y * al, o.z * al, o.w * al);
 #pragma unroll
             for (int u = 0; u < UNR; u++) {
-                if (j0 + KB * u + slot < T) {
+                if (j0 + KB * u + slot < je) {
                     const float p = expf(sj[u] - mn);
                     l += p;
                     o.x += p * vv[u].x;
@@ -617,15 +632,15 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
         }
     };
     float4 ka[UNR], va[UNR], kb[UNR], vb[UNR];
-    load(0, ka, va);
+    load(jb, ka, va);
     __builtin_amdgcn_sched_barrier(0);
-    load(KC, kb, vb);
+    load(jb + KC, kb, vb);
     __builtin_amdgcn_sched_barrier(0);
-    for (int j0 = 0; j0 < T; j0 += 2 * KC) {
+    for (int j0 = jb; j0 < je; j0 += 2 * KC) {
         step(j0, ka, va);
         load(j0 + 2 * KC, ka, va);
         __builtin_amdgcn_sched_barrier(0);
-        if (j0 + KC < T) step(j0 + KC, kb, vb);
+        if (j0 + KC < je) step(j0 + KC, kb, vb);
         load(j0 + 3 * KC, kb, vb);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -670,6 +685,19 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
             t.w += pv.w;
             L += psl[w];
         }
+        if constexpr (SPLIT) {
+            // record (h, chunk): [max, weight sum, 4 * HD4 weighted values]
+            float* rec = a.split_ws + ((size_t)h * gridDim.y + blockIdx.y) * (4 * HD4 + 2);
+            if (c == 0) {
+                rec[0] = M;
+                rec[1] = L;
+            }
+            rec[2 + 4 * c] = t.x;
+            rec[3 + 4 * c] = t.y;
+            rec[4 + 4 * c] = t.z;
+            rec[5 + 4 * c] = t.w;
+            return;
+        }
         if (a.recip) {
             const float rs = 1.0f / L;
             t = make_float4(t.x * rs, t.y * rs, t.z * rs, t.w * rs);
@@ -680,10 +708,83 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
     }
 }
 
+// The key-split long-cache attention's second half: per head, the chunks'
+// records merged in chunk order, each weighted by exp(its max - the max of
+// all), and the weighted values divided by the weighted sum (or multiplied
+// by its reciprocal, a.recip). One new row of one sequence. Thread (ch, c)
+// loads chunk ch's max, sum and values c at once (one round trip for the
+// whole record set), the weighted terms meet in LDS and threads c < HD4 add
+// them in chunk order.
+template <int HD4>
+__global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a, int nc) {
+    constexpr int CPP = 256 / HD4;  // chunks per pass
+    __shared__ float4 st[kAttnSplitMax][HD4];
+    __shared__ float sm[kAttnSplitMax], sl[kAttnSplitMax];
+    const int h = blockIdx.x, c = threadIdx.x % HD4, ch0 = threadIdx.x / HD4;
+    const float* rec = a.split_ws + (size_t)h * nc * (4 * HD4 + 2);
+    constexpr int NP = (kAttnSplitMax + CPP - 1) / CPP;
+    float mc[NP], lc[NP];
+    float4 tc[NP];
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int ch = ch0 + p * CPP;
+        if (ch < nc) {
+            const float* r = rec + (size_t)ch * (4 * HD4 + 2);
+            mc[p] = r[0];
+            lc[p] = r[1];
+            tc[p] = make_float4(r[2 + 4 * c], r[3 + 4 * c], r[4 + 4 * c], r[5 + 4 * c]);
+            if (c == 0) sm[ch] = mc[p];
+        }
+    }
+    __syncthreads();
+    float M = -INFINITY;
+    for (int ch = 0; ch < nc; ch++) M = fmaxf(M, sm[ch]);
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int ch = ch0 + p * CPP;
+        if (ch < nc) {
+            const float w = mc[p] > -INFINITY ? expf(mc[p] - M) : 0.f;
+            st[ch][c] = make_float4(w * tc[p].x, w * tc[p].y, w * tc[p].z, w * tc[p].w);
+            if (c == 0) sl[ch] = w * lc[p];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x >= HD4) return;
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+    float L = 0.f;
+    for (int ch = 0; ch < nc; ch++) {
+        const float4 v = st[ch][c];
+        L += sl[ch];
+        t.x += v.x;
+        t.y += v.y;
+        t.z += v.z;
+        t.w += v.w;
+    }
+    if (a.recip) {
+        const float rs = 1.0f / L;
+        t = make_float4(t.x * rs, t.y * rs, t.z * rs, t.w * rs);
+    } else {
+        t = make_float4(t.x / L, t.y / L, t.z / L, t.w / L);
+    }
+    *reinterpret_cast<float4*>(a.out + h * (4 * HD4) + 4 * c) = t;
+}
+
 // 4 waves per (head, row) block when there are enough blocks to fill the
 // GPU; 16 waves when the visible context is long and blocks are few, so each
 // block keeps more of the KV stream in flight.
-enum AttnRoute { kRouteFlash, kRouteRows, kRouteLong, kRouteCached16, kRouteCached4, kRouteNone };
+enum AttnRoute { kRouteFlash, kRouteSplit, kRouteRows, kRouteLong, kRouteCached16, kRouteCached4, kRouteNone };
+
+// Key chunks of the key-split long-cache attention for a: up to 256 blocks
+// in all, at least one load round of keys per chunk; 0 when a cannot split
+// (no scratch, more than one new row, scratch too small, one chunk).
+static int attn_split_chunks(const AttnArgs& a, int heads, int rows) {
+    if (!a.split_ws || rows != 1 || a.new_seq != 1 || (a.hd != 64 && a.hd != 128)) return 0;
+    const int kc = a.hd == 64 ? 64 : 32;  // keys per 4-wave load round
+    const long long keys = a.pos_dev ? (long long)a.max_seq : (long long)a.pos_host + a.new_seq;
+    const int nc = (int)std::min<long long>(std::min(kAttnSplitMax, std::max(1, 256 / heads)), (keys + kc - 1) / kc);
+    if (nc < 2 || a.split_ws_floats < (long long)heads * nc * (a.hd + 2)) return 0;
+    return nc;
+}
 
 // The kernel for a: the matrix-core prefill kernel for many new rows per
 // sequence, the (key, chunk)-lane kernel for short caches, the online-softmax
@@ -718,6 +819,8 @@ static AttnRoute attn_route(const AttnArgs& a, int heads, int rows) {
     // split QKV partials: only the two-pass kernel adds them
     if (a.qkv_part) return cached();
     if (flash_min > 0 && aligned && a.new_seq >= flash_min && (a.hd == 64 || a.hd == 128)) return kRouteFlash;
+    // one row over few heads: each head's keys over several CUs
+    if (long_kernel && aligned && blocks < 128 && attn_split_chunks(a, heads, rows)) return kRouteSplit;
     if (rows_kernel && aligned && a.max_seq <= 256 && (a.hd == 64 || a.hd == 128 || a.hd == 32 || a.hd == 16))
         return kRouteRows;
     // (measured: XL batch 16, 400 blocks, two-pass 25 vs online-softmax
@@ -729,6 +832,7 @@ static AttnRoute attn_route(const AttnArgs& a, int heads, int rows) {
 bool attn_rows_wo_ok(const AttnArgs& a, int heads, int rows) {
     AttnArgs b = a;
     b.wo = nullptr;
+    b.split_ws = nullptr;
     return rows == 1 && a.new_seq == 1 && a.kv_heads == 0 && a.hd == 64 && a.max_seq <= 256 &&
            a.dim % 8 == 0 && heads * a.hd == a.dim && attn_route(b, heads, rows) == kRouteRows;
 }
@@ -790,9 +894,25 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
             count(CNT_ATTENTION);
             return check_launch("attn_rows");
         }
+        case kRouteSplit: {
+            // one row over few heads: each head's keys split over chunks of
+            // 4-wave blocks, the chunks' records merged by k_attn_combine
+            const int nc = attn_split_chunks(a, heads, rows);
+            const dim3 sg(heads, nc);
+            if (a.hd == 64) {
+                hipLaunchKernelGGL((k_attn_long<16, 4, 4, true>), sg, dim3(256), 0, s, a);
+                hipLaunchKernelGGL((k_attn_combine<16>), dim3(heads), dim3(256), 0, s, a, nc);
+            } else {
+                hipLaunchKernelGGL((k_attn_long<32, 4, 4, true>), sg, dim3(256), 0, s, a);
+                hipLaunchKernelGGL((k_attn_combine<32>), dim3(heads), dim3(256), 0, s, a, nc);
+            }
+            count(CNT_ATTENTION);
+            return check_launch("attn_long_split");
+        }
         case kRouteLong:
-            // few (head, row) blocks over a long cache (a batch-1 step): two
-            // 256-key chunks in flight per block
+            // few (head, row) blocks over a long cache without scratch (or
+            // several rows): one 16-wave block per (head, row), two 256-key
+            // chunks in flight
             if (a.hd == 64) hipLaunchKernelGGL((k_attn_long<16, 16, 4>), grid, dim3(1024), 0, s, a);
             else hipLaunchKernelGGL((k_attn_long<32, 16, 4>), grid, dim3(1024), 0, s, a);
             count(CNT_ATTENTION);

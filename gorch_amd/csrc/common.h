@@ -276,7 +276,14 @@ struct AttnArgs {
     const uint16_t* wo = nullptr;
     const float* wo_bias = nullptr;
     float* wo_out = nullptr;
+    // Scratch for the key-split long-cache path (one new row, fewer than
+    // 128 heads): per (head, key chunk) the chunk's max, weight sum and
+    // unnormalised weighted values, hd + 2 floats. Null: one block per head.
+    float* split_ws = nullptr;
+    long long split_ws_floats = 0;
 };
+// Key chunks per head of the key-split long-cache attention, at most.
+constexpr int kAttnSplitMax = 16;
 // The kernel launch_attn_cached picks for a; true when it is the two-pass
 // cached kernel, the one that takes split QKV partials.
 bool attn_takes_qkv_part(const AttnArgs& a, int heads, int rows);

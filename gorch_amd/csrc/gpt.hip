@@ -221,6 +221,10 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         }
         AttnArgs a{g->q, kc_layer(c, l), vc_layer(c, l), g->att, pos, 0, n, d, hd, c->capacity, d, 1,
                    1.0f / (float)sqrt((double)hd)};
+        // chunk records of the key-split long-cache attention (one-row
+        // steps): the residual Linears' partial buffer, idle until Wo
+        a.split_ws = g->part;
+        a.split_ws_floats = (long long)kMaxSplit * 16 * d;
         // one token per sequence over tile-packed weights: the fused QKV
         // Linear split over K into raw partials; the attention kernel adds
         // the slices and the bias and writes the K/V cache rows

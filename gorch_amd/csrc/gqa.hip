@@ -24,11 +24,12 @@ using namespace gh;
 
 namespace gh {
 // q, the attention output (both [S, q heads * hd]), k before RoPE [S, kv
-// heads * hd], and room for a normalised input [S, dim] (the block path).
+// heads * hd], room for a normalised input [S, dim] (the block path), and
+// for one-row steps the key-split attention's chunk records.
 size_t gqa_ws(int new_seq, int num_q, int num_kv, int hd, int dim) {
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
     return al((size_t)new_seq * num_q * hd * 4) * 2 + al((size_t)new_seq * num_kv * hd * 4) +
-           al((size_t)new_seq * dim * 4);
+           al((size_t)new_seq * dim * 4) + (new_seq == 1 ? al((size_t)num_q * kAttnSplitMax * (hd + 2) * 4) : 0);
 }
 }  // namespace gh
 
@@ -53,6 +54,7 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
     float* att = (float*)(ws + al((size_t)S * qdim * 4));
     float* kt = (float*)(ws + 2 * al((size_t)S * qdim * 4));
     float* h = (float*)(ws + 2 * al((size_t)S * qdim * 4) + al((size_t)S * kvdim * 4));
+    float* split = S == 1 ? (float*)((char*)h + al((size_t)S * d * 4)) : nullptr;
     float* krow = k_cache + (size_t)pos_offset * kvdim;
     float* vrow = v_cache + (size_t)pos_offset * kvdim;
 
@@ -118,6 +120,8 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
     }
     AttnArgs a{q, k_cache, v_cache, att, nullptr, pos_offset, S, qdim, hd, max_seq, qdim, w->causal ? 1 : 0,
                (float)(1.0 / sqrt((double)hd)), nkv, kvdim, 1};
+    a.split_ws = split;
+    a.split_ws_floats = split ? (long long)nq * kAttnSplitMax * (hd + 2) : 0;
     GH_TRY(launch_attn_cached(s, a, nq, S));
     return launch_linear_bf16(s, att, w->wo, w->bo, resid, out, S, d, qdim, GORCH_HIP_EPI_NONE);
 }

@@ -206,6 +206,23 @@ def test_generate_long_cache(gpu):
     g.close()
 
 
+@pytest.mark.parametrize("prompt", [270, 40])
+def test_generate_long_cache_batch1(gpu, prompt):
+    """One sequence over a cache of 300 positions: the key-split long-cache
+    attention (each head's keys over several blocks, their records merged by
+    the combine kernel). A 40-token prompt leaves most key chunks empty.
+    Greedy tokens identical to the oracle, first-step logits within 1e-3."""
+    cfg = dict(vocab=64, dim=128, heads=2, layers=2, max_seq=300)
+    w = syn.gpt2_weights(cfg, seed=45, random_affine=True)
+    g, o = gpu.GPT(w), orc.GPT(w)
+    prompts = syn.prompt_ids(prompt, cfg["vocab"], seed=81)[None, :]
+    ids, logits, _ = g.generate_cached(prompts, 12, want_logits=True)
+    ref, ref_logits, _ = o.generate_cached(prompts[0], 12, want_logits=True)
+    assert list(ids[0]) == list(ref)
+    assert rel_err(logits[0][0], ref_logits[0]) <= 1e-3
+    g.close()
+
+
 XL2 = dict(vocab=8192, dim=1600, heads=25, layers=2, max_seq=544)
 
 

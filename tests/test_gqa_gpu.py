@@ -146,3 +146,20 @@ def test_gqa_qwen3_shaped_decode(gpu):
     rng = np.random.default_rng(8)
     chunks = [rng.standard_normal((n, 1024)).astype(np.float32) for n in (32, 1, 1)]
     _run(gpu, w, chunks, cap=40)
+
+
+@pytest.mark.parametrize("kw,prefill", [
+    # Qwen3-0.6B attention (16 query / 8 KV heads of 128) over a 290-row
+    # prefill, then one-row steps: 10 key chunks of 32 per head
+    (dict(dim=1024, num_q=16, num_kv=8, head_dim=128, base=1000000.0), 290),
+    # heads of 64 over 600 rows: 10 chunks of 64 keys per head
+    (dict(dim=256, num_q=4, num_kv=2, head_dim=64, base=10000.0), 600)])
+def test_gqa_module_key_split_steps(gpu, kw, prefill):
+    """One-row steps over a cache longer than 256 rows with few heads: the
+    key-split long-cache attention (per-chunk max, weight sum and weighted
+    values, merged per head by the combine kernel) inside the module; outputs
+    within 1e-3 of the oracle, cache rows within 1e-4."""
+    w = syn.gqa_weights(max_seq=prefill + 8, seed=14, bias=False, qk_norm=True, rope=True, **kw)
+    rng = np.random.default_rng(15)
+    chunks = [rng.standard_normal((n, w["dim"])).astype(np.float32) for n in (prefill, 1, 1, 1)]
+    _run(gpu, w, chunks, cap=prefill + 4)
