@@ -233,7 +233,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_rows(AttnArgs a) {
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.vc + base, span);
     auto kv_off = [&](int j) { return j * kvd * 4 + 16 * c; };
     auto ld4 = [](__amdgpu_buffer_rsrc_t rs, int off) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kStreamPolicy);
         return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
                            __uint_as_float(v[3]));
     };
@@ -260,7 +260,8 @@ __global__ __launch_bounds__(NW * 64) void k_attn_rows(AttnArgs a) {
 #pragma unroll
         for (int q = 0; q < WPASS; q++) {
             const int rl = rr + q * WRP;
-            wov[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, rl < nrows ? (rl * a.dim + 8 * cc) * 2 : kOutOfRange, 0, 0);
+            wov[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, rl < nrows ? (rl * a.dim + 8 * cc) * 2 : kOutOfRange, 0,
+                                                         kStreamPolicy);
         }
     }
     if constexpr (FULL) {

@@ -373,6 +373,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, long 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, n, 0x00020000);
 }
 constexpr int kOutOfRange = 0x7fff0000;  // an offset past any resource (+ small immediates)
+// Cache policy (the buffer loads' aux bits) for data a launch reads once and
+// the next launches do not reuse: GEMV weights, K/V cache rows. 2 is the nt
+// (non-temporal) bit; measured faster than the default policy for every
+// GEMV shape of the decode path.
+#ifndef GH_STREAM_POLICY
+#define GH_STREAM_POLICY 2
+#endif
+constexpr int kStreamPolicy = GH_STREAM_POLICY;
 
 __device__ __forceinline__ floatx4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const floatx4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

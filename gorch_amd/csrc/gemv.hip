@@ -364,7 +364,7 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
 #pragma unroll
         for (int c = 0; c < C; c++)
             gr.w[c] = __builtin_bit_cast(
-                uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (rloc * K + 8 * (sub + T * c)) * 2, 0, 0));
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (rloc * K + 8 * (sub + T * c)) * 2, 0, kStreamPolicy));
         const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias + (size_t)g * RPI, bias ? (long long)rows * 4 : 0);
         const __amdgpu_buffer_rsrc_t rr = make_rsrc(residual + (size_t)g * RPI, residual ? (long long)rows * 4 : 0);
         gr.b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, rloc * 4, 0, 0));
@@ -714,7 +714,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
             for (int jj = 0; jj < 4; jj++) {
                 const int k = 128 * st + 32 * jj + 8 * g;
                 const int off = k < K ? (r * K + k) * 2 : kOutOfRange;
-                v[q][jj] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+                v[q][jj] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kStreamPolicy));
             }
         }
         const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias + (size_t)t * 16, bias ? (long long)rows * 4 : 0);
@@ -869,7 +869,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
         for (int u = 0; u < KS; u++) {
             const int kc = kb + 32 * u + 8 * g;
             const int off = PACKED ? (kb + 32 * u) * 32 + 16 * lane : (r * K + kc) * 2;
-            tl.w[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, kc < ke ? off : kOutOfRange, 0, 0);
+            tl.w[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, kc < ke ? off : kOutOfRange, 0, kStreamPolicy);
         }
         // this lane's output column's bias and residual
         const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias + (size_t)t * 16, bias ? (long long)rows * 4 : 0);
