@@ -540,6 +540,57 @@ __global__ __launch_bounds__(NW * 64) void k_attn_flash(AttnArgs a) {
     }
 }
 
+// The q/k epilogue of a one-row projection (nn/gqa.go:300-330: per-head
+// RMSNorm, then RoPE at the row's position) for one head held by segments
+// of HD4 lanes, lane c of a segment holding elements 4c .. 4c + 3 (every
+// segment of the wave holds the same row). k_norm_rope_rows' operations in
+// its order: the f64 sum of squares over the head (the wave's 64 / HD4
+// copies summed, then divided back out, which is exact), y = x * inv * g,
+// then each pair rotated without contraction, the Llama partner element
+// taken from lane c +- HD4 / 2 of the same segment.
+template <int HD4>
+__device__ __forceinline__ float4 head_norm_rope(float4 v, const float* gain, int p, const AttnArgs& a, int c) {
+#pragma clang fp contract(off)
+    constexpr int hd = 4 * HD4, half = hd / 2;
+    if (gain) {
+        const float4 gv = *reinterpret_cast<const float4*>(gain + 4 * c);
+        double s = ((double)v.x * (double)v.x + (double)v.y * (double)v.y) +
+                   ((double)v.z * (double)v.z + (double)v.w * (double)v.w);
+        s = wave_sum_d(s) / (double)(64 / HD4);
+        const float inv = (float)(1.0 / sqrt(s / (double)hd + (double)a.qk_eps));
+        v = make_float4(v.x * inv * gv.x, v.y * inv * gv.y, v.z * inv * gv.z, v.w * inv * gv.w);
+    }
+    if (!a.rope_cos) return v;
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    float o[4];
+    if (a.rope_neox) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int i = 2 * c + q;
+            const int cs = p * half + min(i, half - 1);
+            const float co = a.rope_cos[cs], si = a.rope_sin[cs];
+            o[2 * q] = e[2 * q] * co - e[2 * q + 1] * si;
+            o[2 * q + 1] = e[2 * q] * si + e[2 * q + 1] * co;
+        }
+    } else {
+        const int lane = threadIdx.x & 63;
+        const bool lo = c < HD4 / 2;
+        const int src = lo ? lane + HD4 / 2 : lane - HD4 / 2;
+        float pe[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) pe[q] = __shfl(e[q], src);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int k = 4 * c + q;
+            const int i = lo ? k : k - half;
+            const int cs = p * half + min(max(i, 0), half - 1);
+            const float co = a.rope_cos[cs], si = a.rope_sin[cs];
+            o[q] = lo ? e[q] * co - pe[q] * si : pe[q] * si + e[q] * co;
+        }
+    }
+    return make_float4(o[0], o[1], o[2], o[3]);
+}
+
 // k_attn_long: caches longer than one chunk of keys when (head, row) blocks
 // are few (a batch-1 step). Lanes over (key, 16-byte chunk of the head) as in
 // k_attn_rows; NW waves take KB = NW * KPI keys per instruction and UNR
@@ -555,7 +606,11 @@ __global__ __launch_bounds__(NW * 64) void k_attn_flash(AttnArgs a) {
 // chunk's max, weight sum and unnormalised weighted values to a.split_ws
 // for k_attn_combine instead of the output. Each head's cache then streams
 // through gridDim.y CUs instead of one.
-template <int HD4, int NW, int UNR, bool SPLIT = false>
+// QK (with SPLIT): q and the new row's k finished here (AttnArgs::k_raw):
+// head_norm_rope on both, the finished k written to its cache row by one
+// block per KV head and used from registers for that key by every block
+// whose chunk holds it.
+template <int HD4, int NW, int UNR, bool SPLIT = false, bool QK = false>
 __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
     constexpr int KPI = 64 / HD4;  // keys per wavefront instruction
     constexpr int KB = NW * KPI;   // keys per block instruction
@@ -592,7 +647,16 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
         return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
                            __uint_as_float(v[3]));
     };
-    const float4 q = *reinterpret_cast<const float4*>(a.q + (size_t)row * a.q_stride + h * (4 * HD4) + 4 * c);
+    float4 q = *reinterpret_cast<const float4*>(a.q + (size_t)row * a.q_stride + h * (4 * HD4) + 4 * c);
+    float4 knew = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (QK) {
+        q = head_norm_rope<HD4>(q, a.q_gain, pos + i, a, c);
+        const float4 kr = *reinterpret_cast<const float4*>(a.k_raw + (size_t)kvh * (4 * HD4) + 4 * c);
+        knew = head_norm_rope<HD4>(kr, a.k_gain, pos + i, a, c);
+        const int group = a.kv_heads ? (int)gridDim.x / a.kv_heads : 1;
+        if (h % group == 0 && jb <= T - 1 && T - 1 < je && threadIdx.x < HD4)
+            *reinterpret_cast<float4*>(const_cast<float*>(a.kc) + base + (size_t)(T - 1) * kvd + 4 * c) = knew;
+    }
     // keys past T lie outside the resources and read as zeros
     auto load = [&](int j0, float4 (&kk)[UNR], float4 (&vv)[UNR]) {
 #pragma unroll
@@ -609,7 +673,12 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
         float cm = -INFINITY;
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
-            const float d = q.x * kk[u].x + q.y * kk[u].y + q.z * kk[u].z + q.w * kk[u].w;
+            float4 kx = kk[u];
+            if constexpr (QK) {
+                // the new key from registers (its cache row is being written)
+                if (j0 + KB * u + slot == T - 1) kx = knew;
+            }
+            const float d = q.x * kx.x + q.y * kx.y + q.z * kx.z + q.w * kx.w;
             sj[u] = seg_sum<HD4>(d) * a.scale;
             if (j0 + KB * u + slot < je) cm = fmaxf(cm, sj[u]);
         }
@@ -851,6 +920,12 @@ int launch_attn_rows_wo(hipStream_t s, const AttnArgs& a, int heads) {
     return check_launch("attn_rows_wo");
 }
 
+bool attn_split_takes_qk(const AttnArgs& a, int heads, int rows) {
+    AttnArgs b = a;
+    b.k_raw = nullptr;
+    return attn_route(b, heads, rows) == kRouteSplit;
+}
+
 bool attn_takes_qkv_part(const AttnArgs& a, int heads, int rows) {
     if (a.new_seq != 1 || a.kv_heads != 0) return false;
     const AttnRoute r = attn_route(a, heads, rows);
@@ -865,7 +940,12 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
         return GORCH_HIP_EUNSUPPORTED;
     }
     const dim3 grid(heads, rows);
-    switch (attn_route(a, heads, rows)) {
+    const AttnRoute route = attn_route(a, heads, rows);
+    if (a.k_raw && route != kRouteSplit) {
+        set_error("attention: the fused q/k epilogue needs the key-split path (one new row, few heads)");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
+    switch (route) {
         case kRouteFlash: {
             // many new rows per sequence (prefill): the matrix-core kernel,
             // 128 query rows per block sharing each staged K/V tile
@@ -901,10 +981,12 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
             const int nc = attn_split_chunks(a, heads, rows);
             const dim3 sg(heads, nc);
             if (a.hd == 64) {
-                hipLaunchKernelGGL((k_attn_long<16, 4, 4, true>), sg, dim3(256), 0, s, a);
+                if (a.k_raw) hipLaunchKernelGGL((k_attn_long<16, 4, 4, true, true>), sg, dim3(256), 0, s, a);
+                else hipLaunchKernelGGL((k_attn_long<16, 4, 4, true>), sg, dim3(256), 0, s, a);
                 hipLaunchKernelGGL((k_attn_combine<16>), dim3(heads), dim3(256), 0, s, a, nc);
             } else {
-                hipLaunchKernelGGL((k_attn_long<32, 4, 4, true>), sg, dim3(256), 0, s, a);
+                if (a.k_raw) hipLaunchKernelGGL((k_attn_long<32, 4, 4, true, true>), sg, dim3(256), 0, s, a);
+                else hipLaunchKernelGGL((k_attn_long<32, 4, 4, true>), sg, dim3(256), 0, s, a);
                 hipLaunchKernelGGL((k_attn_combine<32>), dim3(heads), dim3(256), 0, s, a, nc);
             }
             count(CNT_ATTENTION);

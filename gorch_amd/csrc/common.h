@@ -281,9 +281,25 @@ struct AttnArgs {
     // unnormalised weighted values, hd + 2 floats. Null: one block per head.
     float* split_ws = nullptr;
     long long split_ws_floats = 0;
+    // Key-split path only (attn_split_takes_qk): the projection's q/k
+    // epilogue in the attention kernel — per-head RMSNorm (q_gain, k_gain,
+    // qk_eps; null gain: none), then RoPE at the row's position (rope_cos /
+    // rope_sin tables, rope_neox pairing; null: none). a.q holds q before
+    // it; k_raw the new row's K before it ([kv heads * hd]): the kernel
+    // writes the finished row into the K cache and uses it for that key.
+    const float* k_raw = nullptr;
+    const float* q_gain = nullptr;
+    const float* k_gain = nullptr;
+    float qk_eps = 0.f;
+    const float* rope_cos = nullptr;
+    const float* rope_sin = nullptr;
+    int rope_neox = 0;
 };
 // Key chunks per head of the key-split long-cache attention, at most.
 constexpr int kAttnSplitMax = 16;
+// True when launch_attn_cached takes the key-split path for a (so it can
+// also finish q and k: AttnArgs::k_raw).
+bool attn_split_takes_qk(const AttnArgs& a, int heads, int rows);
 // The kernel launch_attn_cached picks for a; true when it is the two-pass
 // cached kernel, the one that takes split QKV partials.
 bool attn_takes_qkv_part(const AttnArgs& a, int heads, int rows);

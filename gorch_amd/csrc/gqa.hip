@@ -98,12 +98,32 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
         GH_TRY(launch_linear_bf16(s, x, w->wk, w->bk, nullptr, kt, S, kvdim, d, GORCH_HIP_EPI_NONE));
         GH_TRY(launch_linear_bf16(s, x, w->wv, w->bv, nullptr, vrow, S, kvdim, d, GORCH_HIP_EPI_NONE));
     }
-    // per-head RMSNorm and RoPE of q and k in one launch when the head fits
-    // one wave (hd % 8 == 0, hd <= 256, 16-byte rows)
+    AttnArgs a{q, k_cache, v_cache, att, nullptr, pos_offset, S, qdim, hd, max_seq, qdim, w->causal ? 1 : 0,
+               (float)(1.0 / sqrt((double)hd)), nkv, kvdim, 1};
+    a.split_ws = split;
+    a.split_ws_floats = split ? (long long)nq * kAttnSplitMax * (hd + 2) : 0;
+    // per-head RMSNorm and RoPE of q and k: inside the key-split attention
+    // kernel for one-row steps that take it; else in one launch when the
+    // head fits one wave (hd % 8 == 0, hd <= 256, 16-byte rows)
+    const bool aligned16 = ((reinterpret_cast<uintptr_t>(krow) | reinterpret_cast<uintptr_t>(q) |
+                             reinterpret_cast<uintptr_t>(kt) | reinterpret_cast<uintptr_t>(w->q_norm) |
+                             reinterpret_cast<uintptr_t>(w->k_norm)) % 16) == 0;
+    static const bool qk_in_attn = [] {
+        const char* e = getenv("GORCH_HIP_QK_IN_ATTN");
+        return e ? atoi(e) != 0 : true;
+    }();
     const bool fused = w->rope_cos && hd % 8 == 0 && hd <= 256 &&
                        ((reinterpret_cast<uintptr_t>(krow) | reinterpret_cast<uintptr_t>(q) |
                          reinterpret_cast<uintptr_t>(kt)) % 16) == 0;
-    if (fused) {
+    if (qk_in_attn && aligned16 && attn_split_takes_qk(a, nq, S)) {
+        a.k_raw = kt;
+        a.q_gain = w->q_norm;
+        a.k_gain = w->k_norm;
+        a.qk_eps = w->norm_eps;
+        a.rope_cos = w->rope_cos;
+        a.rope_sin = w->rope_sin;
+        a.rope_neox = w->rope_neox;
+    } else if (fused) {
         GH_TRY(launch_norm_rope_rows2(s, q, q, S * nq, nq, w->q_norm, kt, krow, S * nkv, nkv, w->k_norm, hd,
                                       w->norm_eps, pos_offset, w->rope_cos, w->rope_sin, w->rope_neox));
     } else {
@@ -118,10 +138,6 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
                          "gqa k copy"));
         }
     }
-    AttnArgs a{q, k_cache, v_cache, att, nullptr, pos_offset, S, qdim, hd, max_seq, qdim, w->causal ? 1 : 0,
-               (float)(1.0 / sqrt((double)hd)), nkv, kvdim, 1};
-    a.split_ws = split;
-    a.split_ws_floats = split ? (long long)nq * kAttnSplitMax * (hd + 2) : 0;
     GH_TRY(launch_attn_cached(s, a, nq, S));
     return launch_linear_bf16(s, att, w->wo, w->bo, resid, out, S, d, qdim, GORCH_HIP_EPI_NONE);
 }

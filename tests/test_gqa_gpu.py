@@ -148,18 +148,23 @@ def test_gqa_qwen3_shaped_decode(gpu):
     _run(gpu, w, chunks, cap=40)
 
 
-@pytest.mark.parametrize("kw,prefill", [
+@pytest.mark.parametrize("kw,prefill,qk_norm,neox", [
     # Qwen3-0.6B attention (16 query / 8 KV heads of 128) over a 290-row
     # prefill, then one-row steps: 10 key chunks of 32 per head
-    (dict(dim=1024, num_q=16, num_kv=8, head_dim=128, base=1000000.0), 290),
+    (dict(dim=1024, num_q=16, num_kv=8, head_dim=128, base=1000000.0), 290, True, 0),
     # heads of 64 over 600 rows: 10 chunks of 64 keys per head
-    (dict(dim=256, num_q=4, num_kv=2, head_dim=64, base=10000.0), 600)])
-def test_gqa_module_key_split_steps(gpu, kw, prefill):
-    """One-row steps over a cache longer than 256 rows with few heads: the
-    key-split long-cache attention (per-chunk max, weight sum and weighted
-    values, merged per head by the combine kernel) inside the module; outputs
-    within 1e-3 of the oracle, cache rows within 1e-4."""
-    w = syn.gqa_weights(max_seq=prefill + 8, seed=14, bias=False, qk_norm=True, rope=True, **kw)
+    (dict(dim=256, num_q=4, num_kv=2, head_dim=64, base=10000.0), 600, True, 0),
+    # interleaved (NeoX) pairs, and RoPE without the per-head norm
+    (dict(dim=512, num_q=4, num_kv=2, head_dim=128, base=10000.0), 70, True, 1),
+    (dict(dim=256, num_q=4, num_kv=4, head_dim=64, base=10000.0), 130, False, 0)])
+def test_gqa_module_key_split_steps(gpu, kw, prefill, qk_norm, neox):
+    """One-row steps over few heads and a cache longer than one key chunk:
+    the key-split attention (per-chunk max, weight sum and weighted values,
+    merged per head by the combine kernel) with the q/k RMSNorm and RoPE
+    applied inside it (the new K row written to the cache by the kernel);
+    outputs within 1e-3 of the oracle, cache rows within 1e-4."""
+    w = syn.gqa_weights(max_seq=prefill + 8, seed=14, bias=False, qk_norm=qk_norm, rope=True, **kw)
+    w["rope_neox"] = neox
     rng = np.random.default_rng(15)
     chunks = [rng.standard_normal((n, w["dim"])).astype(np.float32) for n in (prefill, 1, 1, 1)]
     _run(gpu, w, chunks, cap=prefill + 4)

@@ -152,18 +152,24 @@ def test_qwen25_style_bias_no_qk_norm(gpu):
     dict(hidden=128, layers=2, num_q=4, num_kv=2, head_dim=32, inter=256, vocab=500, max_seq=48),
     # Qwen3-0.6B width (d 1024, 16 / 8 heads of 128, SwiGLU 3072), two of its
     # 28 layers and a small vocabulary: the shapes the decode bench times
-    dict(hidden=1024, layers=2, num_q=16, num_kv=8, head_dim=128, inter=3072, vocab=1000, max_seq=48)])
+    dict(hidden=1024, layers=2, num_q=16, num_kv=8, head_dim=128, inter=3072, vocab=1000, max_seq=48),
+    # the same width past one 32-key chunk: one-token steps through the
+    # key-split attention with q/k norm and RoPE inside it
+    dict(hidden=1024, layers=2, num_q=16, num_kv=8, head_dim=128, inter=3072, vocab=1000, max_seq=80,
+         prefill=40)])
 def test_qwen_fused_block_steps(gpu, cfg_kw):
-    """The six-launch one-token block (gorch_hip_qwen_block_forward_cached)
-    against the oracle composition of model/qwen's block: a 7-token prefill
+    """The one-token block (gorch_hip_qwen_block_forward_cached) against the
+    oracle composition of model/qwen's block: a 7-token (or longer) prefill
     (the separate-kernel path), then one-token steps (the fused path); greedy
     tokens identical, logits within 1e-3, cache rows within 1e-4."""
+    cfg_kw = dict(cfg_kw)
+    prefill = cfg_kw.pop("prefill", 7)
     cfg = QwenConfig(**cfg_kw)
     w = syn.qwen_weights(cfg, seed=21)
     m = Qwen(cfg, w)
     ref = OracleQwen(cfg, w, m)
     cache = m.new_cache(cfg.max_seq)
-    ids = np.random.default_rng(22).integers(0, cfg.vocab, 7).astype(np.int32)
+    ids = np.random.default_rng(22).integers(0, cfg.vocab, prefill).astype(np.int32)
     pos = 0
     for step in range(6):
         got = host(m.forward_cached(torch.from_numpy(ids).cuda(), cache, pos))
