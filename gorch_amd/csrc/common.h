@@ -53,6 +53,10 @@ struct LinearExtras {
     // one-row register GEMV only: the activation row is [gate | up] of 2K
     // values and the GEMV reads silu(gate) * up
     bool swiglu = false;
+    // one-row register GEMV only: W is [gate | up] of 2 * pair_swiglu rows
+    // (N = 2 * pair_swiglu); output j = silu(gate_j) * up_j, rows j and
+    // pair_swiglu + j computed by one wave (no bias, residual or GELU)
+    int pair_swiglu = 0;
 };
 // Most K slices a K-split partial buffer holds (k_splitk_epilogue, the
 // row reducer, the split QKV input of the cached attention).
@@ -326,6 +330,9 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
 int launch_rmsnorm(hipStream_t s, const float* x, const float* g, float* y, int M, int N, float eps);
 // The one-row register GEMV takes K (RMSNorm / SwiGLU prologues need it).
 bool gemv_m1_prologue_ok(int K);
+// The one-row GEMV can pair the gate and up rows of a [2F, K] weight
+// (LinearExtras::pair_swiglu = F).
+bool gemv_pair_swiglu_ok(int F, int K);
 int launch_swiglu(hipStream_t s, const float* g, const float* v, float* y, int64_t n);
 
 // A tensor entry of a safetensors header (safetensors.hip): dtype

@@ -346,7 +346,9 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sub = lane % T, rloc = lane / T;
     constexpr int RPI = 64 / T;
-    const int ngroups = (N + RPI - 1) / RPI;
+    // paired SwiGLU rows (RPI == 2): group g is gate row g and up row F + g
+    const int F = ex.pair_swiglu;
+    const int ngroups = F ? F : (N + RPI - 1) / RPI;
     const int stride = gridDim.x * 4;
     int rg = blockIdx.x * 4 + wave;
 
@@ -360,11 +362,15 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
     };
     auto load = [&](int g, Group& gr) {
         const int rows = max(0, min(RPI, N - g * RPI));
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(W + (size_t)g * RPI * K, (long long)rows * K * 2);
+        // paired rows: one resource from gate row g through up row F + g
+        const __amdgpu_buffer_rsrc_t rs =
+            F ? make_rsrc(W + (size_t)g * K, g < F ? ((long long)F * K + K) * 2 : 0)
+              : make_rsrc(W + (size_t)g * RPI * K, (long long)rows * K * 2);
+        const int roff = F ? (rloc ? F * K : 0) : rloc * K;
 #pragma unroll
         for (int c = 0; c < C; c++)
             gr.w[c] = __builtin_bit_cast(
-                uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (rloc * K + 8 * (sub + T * c)) * 2, 0, kStreamPolicy));
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (roff + 8 * (sub + T * c)) * 2, 0, kStreamPolicy));
         const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias + (size_t)g * RPI, bias ? (long long)rows * 4 : 0);
         const __amdgpu_buffer_rsrc_t rr = make_rsrc(residual + (size_t)g * RPI, residual ? (long long)rows * 4 : 0);
         gr.b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, rloc * 4, 0, 0));
@@ -482,6 +488,12 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
                    xr[c][6] * bf16_lo(cw.w) + xr[c][7] * bf16_hi(cw.w);
         }
         acc = seg_sum<T>(acc);
+        if (F) {
+            // lane 0 holds gate_g, lane 32 up_g (silu.go:121-136 order)
+            const float up = readlane_f(acc, 32);
+            if (lane == 0 && g < F) *od.at_p(0, g, posv) = acc * sigmoidf_ref(acc) * up;
+            return;
+        }
         const int row = g * RPI + rloc;
         if (sub == 0 && row < N) {
             float v = acc;
@@ -1070,6 +1082,11 @@ static void m1_shape(int K, int* T, int* C) {
         }
 }
 
+bool gemv_pair_swiglu_ok(int F, int K) {
+    return F > 0 && K % 256 == 0 && K / 256 >= 1 && K / 256 <= 8 && (long long)2 * F * K * 2 < (1ll << 31) &&
+           env_int("GORCH_HIP_PAIR_SWIGLU", 1);
+}
+
 bool gemv_m1_prologue_ok(int K) {
     int T1, C1;
     m1_shape(K, &T1, &C1);
@@ -1106,6 +1123,9 @@ static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const flo
     }
     GH_M1(64, 1) GH_M1(64, 2) GH_M1(64, 3) GH_M1(64, 4) GH_M1(64, 5) GH_M1(64, 6) GH_M1(64, 7) GH_M1(64, 8)
     GH_M1(32, 1) GH_M1(32, 3) GH_M1(32, 5) GH_M1(32, 7)
+    if (ex.pair_swiglu) {
+        GH_M1(32, 2) GH_M1(32, 4) GH_M1(32, 6) GH_M1(32, 8)
+    }
     GH_M1(16, 1) GH_M1(16, 3) GH_M1(16, 5) GH_M1(16, 7)
     GH_M1(8, 1) GH_M1(8, 3) GH_M1(8, 5) GH_M1(8, 7)
 #undef GH_M1
@@ -1426,6 +1446,15 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
     static const int m1_on = env_int("GORCH_HIP_GEMV_M1", 1);
     // M = 1: the register-activation kernel whenever K fits its shape table
     // (K/8 = T*C with C <= 8), else the LDS-staged VALU kernel.
+    if (ex.pair_swiglu) {
+        // paired [gate | up] rows: two rows per wave (32 lanes each)
+        if (M != 1 || !gemv_pair_swiglu_ok(ex.pair_swiglu, K) || N != 2 * ex.pair_swiglu || bias || residual ||
+            epilogue != GORCH_HIP_EPI_NONE || ex.argmax_key || ex.swiglu) {
+            set_error("linear_bf16: paired SwiGLU rows need one row, K a multiple of 256 up to 2048, no epilogue");
+            return GORCH_HIP_EUNSUPPORTED;
+        }
+        return launch_m1(s, x, W, nullptr, nullptr, od, N, K, GORCH_HIP_EPI_NONE, ex, 32, K / 256);
+    }
     if (M == 1 && valu_max_m >= 1 && m1_on) {
         int T1, C1;
         m1_shape(K, &T1, &C1);

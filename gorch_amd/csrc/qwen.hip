@@ -6,11 +6,14 @@
 // the reference does as separate ops:
 //   1. RMSNorm_attn applied as the QKV GEMV loads x, Q/K/V as one weight
 //      stream (V written straight into its cache row);
-//   2. per-head q/k RMSNorm + RoPE of q and k together;
-//   3. grouped-query attention over the cache;
+//   2-3. grouped-query attention over the cache: with few heads the
+//      key-split kernel, which applies the per-head q/k RMSNorm + RoPE
+//      itself and writes the K row, plus its combine kernel; else one
+//      launch for the q/k norm + RoPE and one for the attention;
 //   4. Wo GEMV with the residual add (x1 = x + ...);
-//   5. RMSNorm_ffn applied as the gate/up GEMV loads x1 (one [2F, d] weight);
-//   6. down GEMV reading silu(gate) * up as it loads, with the residual add.
+//   5. RMSNorm_ffn applied as the gate/up GEMV loads x1 (one [2F, d] weight),
+//      gate row j and up row F + j in one wave so it writes silu(gate) * up;
+//   6. down GEMV with the residual add.
 // Longer inputs (prefill) take the same steps with the norms and SwiGLU as
 // launches of their own and the matrix-core GEMM for the Linears.
 #include "common.h"
@@ -62,6 +65,15 @@ extern "C" int gorch_hip_qwen_block_forward_cached(void* stream, const gorch_hip
         pre.ln_g = b->norm_ffn;
         pre.ln_rms = true;
         pre.ln_eps = b->eps;
+        if (gemv_pair_swiglu_ok(F, d)) {
+            // gate row j and up row F + j in one wave: h = silu(gate) * up
+            // straight from the GEMV, then x = x1 + W_down . h
+            pre.pair_swiglu = F;
+            GH_TRY(launch_linear_bf16_od(s, x1, b->wgate_up, nullptr, nullptr, OutDesc::plain(gu, F), 1, 2 * F, d,
+                                         GORCH_HIP_EPI_NONE, pre));
+            return finish(stream, launch_linear_bf16_od(s, gu, b->wdown, nullptr, x1, OutDesc::plain(x, d), 1, d, F,
+                                                        GORCH_HIP_EPI_NONE, LinearExtras{}));
+        }
         GH_TRY(launch_linear_bf16_od(s, x1, b->wgate_up, nullptr, nullptr, OutDesc::plain(gu, 2 * F), 1, 2 * F, d,
                                      GORCH_HIP_EPI_NONE, pre));
         LinearExtras sw;
