@@ -1222,11 +1222,23 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
         count(CNT_GEMV);
         return check_launch("gemv_tiles_ln");
     }
+    // one or two tiles per block: no more blocks (over all K slices) than
+    // CUs, since a second block on a CU streams beside the first and
+    // doubles that CU's time (XL batch 16: FFN2's 7 K slices on 36 instead
+    // of 73 blocks each, 5,059 -> 5,146 tok/s)
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+            n = 256;
+        return n;
+    }();
 #define GH_TILES(NWV, KSV)                                                                                \
     if (nw == NWV && ks <= KSV) {                                                                         \
         static const int blocks_p = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, true, false, false>), NWV * 64); \
         static const int blocks_r = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, false, false, false>), NWV * 64); \
-        const int blocks = std::min(std::max(1, (packed ? blocks_p : blocks_r) / S), ntiles);             \
+        int blocks = std::min(std::max(1, (packed ? blocks_p : blocks_r) / S), ntiles);                   \
+        if (ntiles <= 2 * blocks) blocks = std::min(blocks, std::max(1, cus / S));                        \
         const bool early = ntiles <= 2 * blocks;                                                          \
         if (packed && early) GH_TILES_L(NWV, KSV, true, true);                                            \
         else if (packed) GH_TILES_L(NWV, KSV, true, false);                                               \
