@@ -601,11 +601,12 @@ __device__ __forceinline__ float4 head_norm_rope(float4 v, const float* gain, in
 // branch-free) are in flight while one is used. At the end every slot is
 // rescaled to the block's max and the slots are summed through LDS: out =
 // sum o / sum l.
-// SPLIT (one new row of one sequence): blockIdx.y is a chunk of the keys
-// (gridDim.y chunks of a multiple of KC keys each); the block writes its
-// chunk's max, weight sum and unnormalised weighted values to a.split_ws
-// for k_attn_combine instead of the output. Each head's cache then streams
-// through gridDim.y CUs instead of one.
+// SPLIT (one new row per sequence): blockIdx.z is the row, blockIdx.y a
+// chunk of its keys (gridDim.y chunks of a multiple of KC keys each); the
+// block writes its chunk's max, weight sum and unnormalised weighted values
+// to a.split_ws (record (row, head, chunk)) for k_attn_combine instead of
+// the output. Each head's cache then streams through gridDim.y CUs instead
+// of one.
 // QK (with SPLIT): q and the new row's k finished here (AttnArgs::k_raw):
 // head_norm_rope on both, the finished k written to its cache row by one
 // block per KV head and used from registers for that key by every block
@@ -623,7 +624,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane % HD4, slot = wave * KPI + lane / HD4;
     const int h = blockIdx.x;
-    const int row = SPLIT ? 0 : blockIdx.y;
+    const int row = SPLIT ? blockIdx.z : blockIdx.y;
     const int b = row / a.new_seq;
     const int i = row - b * a.new_seq;
     const int kvh = a.kv_heads ? h / ((int)gridDim.x / a.kv_heads) : h;
@@ -757,7 +758,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
         }
         if constexpr (SPLIT) {
             // record (h, chunk): [max, weight sum, 4 * HD4 weighted values]
-            float* rec = a.split_ws + ((size_t)h * gridDim.y + blockIdx.y) * (4 * HD4 + 2);
+            float* rec = a.split_ws + (((size_t)row * gridDim.x + h) * gridDim.y + blockIdx.y) * (4 * HD4 + 2);
             if (c == 0) {
                 rec[0] = M;
                 rec[1] = L;
@@ -781,7 +782,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
 // The key-split long-cache attention's second half: per head, the chunks'
 // records merged in chunk order, each weighted by exp(its max - the max of
 // all), and the weighted values divided by the weighted sum (or multiplied
-// by its reciprocal, a.recip). One new row of one sequence. Thread (ch, c)
+// by its reciprocal, a.recip). Grid (heads, rows). Thread (ch, c)
 // loads chunk ch's max, sum and values c at once (one round trip for the
 // whole record set), the weighted terms meet in LDS and threads c < HD4 add
 // them in chunk order.
@@ -790,8 +791,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a, int nc) {
     constexpr int CPP = 256 / HD4;  // chunks per pass
     __shared__ float4 st[kAttnSplitMax][HD4];
     __shared__ float sm[kAttnSplitMax], sl[kAttnSplitMax];
-    const int h = blockIdx.x, c = threadIdx.x % HD4, ch0 = threadIdx.x / HD4;
-    const float* rec = a.split_ws + (size_t)h * nc * (4 * HD4 + 2);
+    const int h = blockIdx.x, row = blockIdx.y, c = threadIdx.x % HD4, ch0 = threadIdx.x / HD4;
+    const float* rec = a.split_ws + ((size_t)row * gridDim.x + h) * nc * (4 * HD4 + 2);
     constexpr int NP = (kAttnSplitMax + CPP - 1) / CPP;
     float mc[NP], lc[NP];
     float4 tc[NP];
@@ -836,7 +837,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a, int nc) {
     } else {
         t = make_float4(t.x / L, t.y / L, t.z / L, t.w / L);
     }
-    *reinterpret_cast<float4*>(a.out + h * (4 * HD4) + 4 * c) = t;
+    *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + h * (4 * HD4) + 4 * c) = t;
 }
 
 // 4 waves per (head, row) block when there are enough blocks to fill the
@@ -848,11 +849,19 @@ enum AttnRoute { kRouteFlash, kRouteSplit, kRouteRows, kRouteLong, kRouteCached1
 // in all, at least one load round of keys per chunk; 0 when a cannot split
 // (no scratch, more than one new row, scratch too small, one chunk).
 static int attn_split_chunks(const AttnArgs& a, int heads, int rows) {
-    if (!a.split_ws || rows != 1 || a.new_seq != 1 || (a.hd != 64 && a.hd != 128)) return 0;
+    // one new row per sequence; several sequences only with
+    // GORCH_HIP_ATTN_SPLIT_BATCH = the target number of 4-wave blocks per CU
+    static const int batch_target = [] {
+        const char* e = getenv("GORCH_HIP_ATTN_SPLIT_BATCH");
+        return e ? atoi(e) : 0;
+    }();
+    if (!a.split_ws || a.new_seq != 1 || (a.hd != 64 && a.hd != 128)) return 0;
+    if (rows != 1 && batch_target <= 0) return 0;
     const int kc = a.hd == 64 ? 64 : 32;  // keys per 4-wave load round
     const long long keys = a.pos_dev ? (long long)a.max_seq : (long long)a.pos_host + a.new_seq;
-    const int nc = (int)std::min<long long>(std::min(kAttnSplitMax, std::max(1, 256 / heads)), (keys + kc - 1) / kc);
-    if (nc < 2 || a.split_ws_floats < (long long)heads * nc * (a.hd + 2)) return 0;
+    const int want = rows == 1 ? std::max(1, 256 / heads) : (batch_target * 256 + heads * rows - 1) / (heads * rows);
+    const int nc = (int)std::min<long long>(std::min(kAttnSplitMax, want), (keys + kc - 1) / kc);
+    if (nc < 2 || a.split_ws_floats < (long long)rows * heads * nc * (a.hd + 2)) return 0;
     return nc;
 }
 
@@ -890,7 +899,7 @@ static AttnRoute attn_route(const AttnArgs& a, int heads, int rows) {
     if (a.qkv_part) return cached();
     if (flash_min > 0 && aligned && a.new_seq >= flash_min && (a.hd == 64 || a.hd == 128)) return kRouteFlash;
     // one row over few heads: each head's keys over several CUs
-    if (long_kernel && aligned && blocks < 128 && attn_split_chunks(a, heads, rows)) return kRouteSplit;
+    if (long_kernel && aligned && (blocks < 128 || rows > 1) && attn_split_chunks(a, heads, rows)) return kRouteSplit;
     if (rows_kernel && aligned && a.max_seq <= 256 && (a.hd == 64 || a.hd == 128 || a.hd == 32 || a.hd == 16))
         return kRouteRows;
     // (measured: XL batch 16, 400 blocks, two-pass 25 vs online-softmax
@@ -923,7 +932,7 @@ int launch_attn_rows_wo(hipStream_t s, const AttnArgs& a, int heads) {
 bool attn_split_takes_qk(const AttnArgs& a, int heads, int rows) {
     AttnArgs b = a;
     b.k_raw = nullptr;
-    return attn_route(b, heads, rows) == kRouteSplit;
+    return rows == 1 && attn_route(b, heads, rows) == kRouteSplit;
 }
 
 bool attn_takes_qkv_part(const AttnArgs& a, int heads, int rows) {
@@ -941,7 +950,7 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
     }
     const dim3 grid(heads, rows);
     const AttnRoute route = attn_route(a, heads, rows);
-    if (a.k_raw && route != kRouteSplit) {
+    if (a.k_raw && (route != kRouteSplit || rows != 1)) {
         set_error("attention: the fused q/k epilogue needs the key-split path (one new row, few heads)");
         return GORCH_HIP_EUNSUPPORTED;
     }
@@ -976,18 +985,19 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
             return check_launch("attn_rows");
         }
         case kRouteSplit: {
-            // one row over few heads: each head's keys split over chunks of
-            // 4-wave blocks, the chunks' records merged by k_attn_combine
+            // one new row per sequence: each (head, row)'s keys split over
+            // chunks of 4-wave blocks, the chunks' records merged by
+            // k_attn_combine
             const int nc = attn_split_chunks(a, heads, rows);
-            const dim3 sg(heads, nc);
+            const dim3 sg(heads, nc, rows), cg(heads, rows);
             if (a.hd == 64) {
                 if (a.k_raw) hipLaunchKernelGGL((k_attn_long<16, 4, 4, true, true>), sg, dim3(256), 0, s, a);
                 else hipLaunchKernelGGL((k_attn_long<16, 4, 4, true>), sg, dim3(256), 0, s, a);
-                hipLaunchKernelGGL((k_attn_combine<16>), dim3(heads), dim3(256), 0, s, a, nc);
+                hipLaunchKernelGGL((k_attn_combine<16>), cg, dim3(256), 0, s, a, nc);
             } else {
                 if (a.k_raw) hipLaunchKernelGGL((k_attn_long<32, 4, 4, true, true>), sg, dim3(256), 0, s, a);
                 else hipLaunchKernelGGL((k_attn_long<32, 4, 4, true>), sg, dim3(256), 0, s, a);
-                hipLaunchKernelGGL((k_attn_combine<32>), dim3(heads), dim3(256), 0, s, a, nc);
+                hipLaunchKernelGGL((k_attn_combine<32>), cg, dim3(256), 0, s, a, nc);
             }
             count(CNT_ATTENTION);
             return check_launch("attn_long_split");
