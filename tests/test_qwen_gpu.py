@@ -189,19 +189,20 @@ def test_qwen_full_size_greedy(gpu, preset):
     """The presets at full size (Qwen3-0.6B: 28 layers, d 1024, 16 / 8 heads
     of 128, SwiGLU 3072, vocab 151936, tied head, q/k norm; Qwen2.5-0.5B: 24
     layers, d 896, 14 / 2 heads of 64, SwiGLU 4864, q/k/v biases) with random
-    weights, a 12-token prefill and 4 one-token steps through the serving
-    path the decode bench times, against the oracle composition: greedy
-    tokens identical, logits within 1e-3, cache rows within 1e-4."""
+    weights, a 70-token prefill (matrix-core GEMMs, flash attention) and 4
+    one-token steps through the serving path the decode bench times (past one
+    key chunk: the key-split attention), against the oracle composition:
+    greedy tokens identical, logits within 1e-3, cache rows within 1e-4."""
     import dataclasses
 
     from gorch_amd.qwen import QWEN2_5_0_5B, QWEN3_0_6B
     base = QWEN3_0_6B if preset == "qwen3_0_6b" else QWEN2_5_0_5B
-    cfg = dataclasses.replace(base, max_seq=48)
+    cfg = dataclasses.replace(base, max_seq=96)
     w = syn.qwen_weights(cfg, seed=31)
     m = Qwen(cfg, w)
     ref = OracleQwen(cfg, w, m)
     cache = m.new_cache(cfg.max_seq)
-    ids = np.random.default_rng(32).integers(0, cfg.vocab, 12).astype(np.int32)
+    ids = np.random.default_rng(32).integers(0, cfg.vocab, 70).astype(np.int32)
     pos = 0
     for step in range(5):
         got = host(m.forward_cached(torch.from_numpy(ids).cuda(), cache, pos))
