@@ -1214,12 +1214,19 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
         static const int blocks_ln =
             blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<8, 4, true, false, true>), 512);
         const int blocks = std::min(blocks_ln, ntiles);
-        if (ntiles <= 2 * blocks)
-            hipLaunchKernelGGL((k_gemv_tiles<8, 4, true, true, true>), dim3(blocks), dim3(512), 0, s, x, W, bias,
-                               residual, od, M, N, K, ks, epilogue, ex);
-        else
-            hipLaunchKernelGGL((k_gemv_tiles<8, 4, true, false, true>), dim3(blocks), dim3(512), 0, s, x, W, bias,
-                               residual, od, M, N, K, ks, epilogue, ex);
+#define GH_TILES_LN(KSV)                                                                                    \
+    if (ntiles <= 2 * blocks)                                                                               \
+        hipLaunchKernelGGL((k_gemv_tiles<8, KSV, true, true, true>), dim3(blocks), dim3(512), 0, s, x, W, bias, \
+                           residual, od, M, N, K, ks, epilogue, ex);                                        \
+    else                                                                                                    \
+        hipLaunchKernelGGL((k_gemv_tiles<8, KSV, true, false, true>), dim3(blocks), dim3(512), 0, s, x, W, bias, \
+                           residual, od, M, N, K, ks, epilogue, ex);
+        if (ks <= 3) {
+            GH_TILES_LN(3)
+        } else {
+            GH_TILES_LN(4)
+        }
+#undef GH_TILES_LN
         count(CNT_GEMV);
         return check_launch("gemv_tiles_ln");
     }
@@ -1248,7 +1255,12 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
         count(CNT_GEMV);                                                                                  \
         return check_launch("gemv_tiles");                                                                \
     }
-    GH_TILES(4, 4) GH_TILES(4, 8) GH_TILES(8, 4) GH_TILES(8, 8) GH_TILES(8, 12) GH_TILES(16, 4)
+    // exact k-step counts where they occur (K = 768: 3 per wave, K = 1600: 7):
+    // a padding slot still costs its instructions and registers (measured:
+    // 8 waves x 3 against x 4 at K = 768, 9-shape GEMV sweep 3,362 -> 3,435
+    // GB/s)
+    GH_TILES(4, 4) GH_TILES(4, 8) GH_TILES(8, 3) GH_TILES(8, 4) GH_TILES(8, 7) GH_TILES(8, 8) GH_TILES(8, 12)
+    GH_TILES(16, 4)
 #undef GH_TILES
 #undef GH_TILES_L
     return -1;
