@@ -1109,6 +1109,17 @@ static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const flo
     int blocks = ex.ln_g ? (ngroups + 7) / 8 : (ngroups + 3) / 4;
     if (blocks > max_blocks) blocks = max_blocks;
     if (ex.argmax_key && blocks > max_blocks_argmax) blocks = max_blocks_argmax;
+    // between one and two blocks per CU: one per CU, each taking more row
+    // groups (a second block on a CU doubles that CU's time)
+    static const int cap = env_int("GORCH_HIP_M1_CAP", 1);
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+            n = 256;
+        return n;
+    }();
+    if (cap && blocks > cus && blocks < 2 * cus) blocks = cus;
     const int pro = ex.swiglu ? 3 : (ex.ln_g ? (ex.ln_rms ? 2 : 1) : 0);
 #define GH_M1_L(TT, CC, PV)                                                                                 \
     hipLaunchKernelGGL((k_gemv_m1<TT, CC, PV>), dim3(blocks), dim3(256), 0, s, x, W, bias, residual, od, N, K, \
