@@ -117,6 +117,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* x, const floa
 // beta) before adding, so the row costs one memory round trip. N % 4 == 0.
 constexpr int kRedVec = kReduceRowsMaxCols / 4 / 256, kRedSlices = 8;
 
+template <int RS>
 __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ part, int S,
                                                      const float* __restrict__ bias, float* __restrict__ x, int M,
                                                      int N, float eps, float2* __restrict__ stats,
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(ln_g, h ? (long long)N * 4 : 0);
     const __amdgpu_buffer_rsrc_t rbe = make_rsrc(ln_b, h ? (long long)N * 4 : 0);
     float4 v[kRedVec], bv[kRedVec], gv[kRedVec], be[kRedVec];
-    float4 p[kRedVec][kRedSlices];
+    float4 p[kRedVec][RS];
     auto ld = [](__amdgpu_buffer_rsrc_t r, int off) {
         return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
     };
@@ -144,9 +145,9 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
     // bias and slices), the same for every thread
     const float x0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, 0, 0, 0));
     const float b0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, 0, 0, 0));
-    float p0[kRedSlices];
+    float p0[RS];
 #pragma unroll
-    for (int q = 0; q < kRedSlices; q++)
+    for (int q = 0; q < RS; q++)
         p0[q] = __uint_as_float(
             __builtin_amdgcn_raw_buffer_load_b32(rp, q < S ? (int)((size_t)q * M * N * 4) : kOutOfRange, 0, 0));
 #pragma unroll
@@ -158,14 +159,14 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
         gv[c] = ld(rg, off);
         be[c] = ld(rbe, off);
 #pragma unroll
-        for (int q = 0; q < kRedSlices; q++)
+        for (int q = 0; q < RS; q++)
             p[c][q] = ld(rp, (j < N && q < S) ? (int)(((size_t)q * M * N + j) * 4) : kOutOfRange);
     }
     float shift = x0;
     if (S > 0) {
         float acc = p0[0];
 #pragma unroll
-        for (int q = 1; q < kRedSlices; q++)
+        for (int q = 1; q < RS; q++)
             if (q < S) acc += p0[q];
         if (bias) acc = acc + b0;
         shift = x0 + acc;
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
             for (int e = 0; e < 4; e++) {
                 float acc = reinterpret_cast<const float*>(&p[c][0])[e];
 #pragma unroll
-                for (int q = 1; q < kRedSlices; q++)
+                for (int q = 1; q < RS; q++)
                     if (q < S) acc += reinterpret_cast<const float*>(&p[c][q])[e];
                 if (bias) acc = acc + reinterpret_cast<const float*>(&bv[c])[e];
                 vc[e] = vc[e] + acc;
@@ -250,7 +251,15 @@ int launch_reduce_rows(hipStream_t s, const float* part, int S, const float* bia
         set_error("reduce_rows: the normalised output needs gamma and beta");
         return GORCH_HIP_EINVAL;
     }
-    hipLaunchKernelGGL(k_reduce_rows, dim3(M), dim3(256), 0, s, part, S, bias, x, M, N, eps, stats, ln_g, ln_b, h);
+    // slice registers sized to S (loads of absent slices still cost their
+    // instructions)
+    if (S <= 2)
+        hipLaunchKernelGGL(k_reduce_rows<2>, dim3(M), dim3(256), 0, s, part, S, bias, x, M, N, eps, stats, ln_g, ln_b, h);
+    else if (S <= 4)
+        hipLaunchKernelGGL(k_reduce_rows<4>, dim3(M), dim3(256), 0, s, part, S, bias, x, M, N, eps, stats, ln_g, ln_b, h);
+    else
+        hipLaunchKernelGGL(k_reduce_rows<kRedSlices>, dim3(M), dim3(256), 0, s, part, S, bias, x, M, N, eps, stats,
+                           ln_g, ln_b, h);
     count(CNT_NORM);
     return check_launch("reduce_rows");
 }
