@@ -1025,6 +1025,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
 // (+ residual), slices added in order, written through the output
 // descriptor. All slice loads of an element are issued before the adds.
 constexpr int kEpiSlices = kMaxPartSlices;
+template <int ES>
 __global__ __launch_bounds__(256) void k_splitk_epilogue(const float* __restrict__ part, int S, int M, int N,
                                                          const float* __restrict__ bias, const float* residual,
                                                          OutDesc od, int epilogue) {
@@ -1037,9 +1038,9 @@ __global__ __launch_bounds__(256) void k_splitk_epilogue(const float* __restrict
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, (long long)S * total * 4);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias, bias ? (long long)N * 4 : 0);
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(residual, residual ? total * 4 : 0);
-    float p[kEpiSlices];
+    float p[ES];
 #pragma unroll
-    for (int q = 0; q < kEpiSlices; q++) {
+    for (int q = 0; q < ES; q++) {
         const int off = q < S ? (int)(((int64_t)q * total + i) * 4) : kOutOfRange;
         p[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, off, 0, 0));
     }
@@ -1047,7 +1048,7 @@ __global__ __launch_bounds__(256) void k_splitk_epilogue(const float* __restrict
     const float rv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, (int)(i * 4), 0, 0));
     float sum = p[0];
 #pragma unroll
-    for (int q = 1; q < kEpiSlices; q++)
+    for (int q = 1; q < ES; q++)
         if (q < S) sum += p[q];
     if (bias) sum = sum + bv;
     if (epilogue == GORCH_HIP_EPI_GELU) sum = gelu_tanh(sum);
@@ -1063,8 +1064,14 @@ int launch_splitk_epilogue(hipStream_t s, const float* part, int S, int M, int N
     }
     const int64_t total = (int64_t)M * N;
     if (total == 0) return GORCH_HIP_OK;
-    hipLaunchKernelGGL(k_splitk_epilogue, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, S, M, N,
-                       bias, residual, od, epilogue);
+    // slice registers sized to S (loads of absent slices still cost their
+    // instructions)
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (S <= 4)
+        hipLaunchKernelGGL(k_splitk_epilogue<4>, grid, dim3(256), 0, s, part, S, M, N, bias, residual, od, epilogue);
+    else
+        hipLaunchKernelGGL(k_splitk_epilogue<kEpiSlices>, grid, dim3(256), 0, s, part, S, M, N, bias, residual, od,
+                           epilogue);
     count(CNT_GEMV);
     return check_launch("splitk_epilogue");
 }
