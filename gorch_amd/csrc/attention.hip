@@ -651,6 +651,17 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
     // keys [jb, je) of this block
     int jb = 0, je = T;
     if constexpr (SPLIT) {
+        // with the fused output projection: the residual into the output
+        // rows (chunk 0 of each head copies its share) before the combine
+        // kernel adds to them
+        if (a.wo && blockIdx.y == 0) {
+            const int rows_out = a.wo_rows ? a.wo_rows : a.dim;
+            const int seg = (rows_out + (int)gridDim.x - 1) / (int)gridDim.x;
+            for (int e = threadIdx.x; e < seg; e += blockDim.x) {
+                const int n = h * seg + e;
+                if (n < rows_out) a.wo_out[(size_t)row * rows_out + n] = a.wo_resid ? a.wo_resid[(size_t)row * rows_out + n] : 0.f;
+            }
+        }
         const int nc = gridDim.y;
         const int L = ((T + nc - 1) / nc + KC - 1) / KC * KC;
         jb = min(T, (int)blockIdx.y * L);
@@ -856,6 +867,101 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a, int nc) {
     *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + h * (4 * HD4) + 4 * c) = t;
 }
 
+// k_attn_combine with the output projection: grid (heads, row groups of
+// kCombineWoRows Wo rows), one new row. Each block merges head h's chunk
+// records into o_h (k_attn_combine's order, in LDS), then adds
+// Wo[n][h*hd .. h*hd+hd) . o_h (+ the bias, from head 0) into a.wo_out[n]
+// for its rows with float atomics (the order of the per-head additions
+// varies between runs). Its Wo loads go out before the records'.
+constexpr int kCombineWoRows = 64;
+template <int HD4>
+__global__ __launch_bounds__(256) void k_attn_combine_wo(AttnArgs a, int nc) {
+    constexpr int CPP = 256 / HD4;
+    constexpr int WCH = HD4 / 2;          // 16-byte chunks of a head's Wo row slice
+    constexpr int WRP = 256 / WCH;        // Wo rows per pass
+    constexpr int WPASS = kCombineWoRows / WRP;
+    __shared__ float4 st[kAttnSplitMax][HD4];
+    __shared__ float sm[kAttnSplitMax], sl[kAttnSplitMax];
+    __shared__ float4 oh[HD4];
+    const int h = blockIdx.x, c = threadIdx.x % HD4, ch0 = threadIdx.x / HD4;
+    const int rows_out = a.wo_rows ? a.wo_rows : a.dim;
+    const int cc = threadIdx.x % WCH, rr = threadIdx.x / WCH;
+    const int n0 = blockIdx.y * kCombineWoRows;
+    const int nrows = max(0, min(kCombineWoRows, rows_out - n0));
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.wo + (size_t)n0 * a.dim + h * (4 * HD4),
+                                                nrows > 0 ? ((long long)(nrows - 1) * a.dim + 4 * HD4) * 2 : 0);
+    u32x4 wov[WPASS];
+#pragma unroll
+    for (int q = 0; q < WPASS; q++) {
+        const int rl = rr + q * WRP;
+        wov[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, rl < nrows ? (rl * a.dim + 8 * cc) * 2 : kOutOfRange, 0,
+                                                     kStreamPolicy);
+    }
+    const float* rec = a.split_ws + (size_t)h * nc * (4 * HD4 + 2);
+    constexpr int NP = (kAttnSplitMax + CPP - 1) / CPP;
+    float mc[NP], lc[NP];
+    float4 tc[NP];
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int ch = ch0 + p * CPP;
+        if (ch < nc) {
+            const float* r = rec + (size_t)ch * (4 * HD4 + 2);
+            mc[p] = r[0];
+            lc[p] = r[1];
+            tc[p] = make_float4(r[2 + 4 * c], r[3 + 4 * c], r[4 + 4 * c], r[5 + 4 * c]);
+            if (c == 0) sm[ch] = mc[p];
+        }
+    }
+    __syncthreads();
+    float M = -INFINITY;
+    for (int ch = 0; ch < nc; ch++) M = fmaxf(M, sm[ch]);
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int ch = ch0 + p * CPP;
+        if (ch < nc) {
+            const float w = mc[p] > -INFINITY ? expf(mc[p] - M) : 0.f;
+            st[ch][c] = make_float4(w * tc[p].x, w * tc[p].y, w * tc[p].z, w * tc[p].w);
+            if (c == 0) sl[ch] = w * lc[p];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < HD4) {
+        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+        float L = 0.f;
+        for (int ch = 0; ch < nc; ch++) {
+            const float4 v = st[ch][c];
+            L += sl[ch];
+            t.x += v.x;
+            t.y += v.y;
+            t.z += v.z;
+            t.w += v.w;
+        }
+        if (a.recip) {
+            const float rs = 1.0f / L;
+            t = make_float4(t.x * rs, t.y * rs, t.z * rs, t.w * rs);
+        } else {
+            t = make_float4(t.x / L, t.y / L, t.z / L, t.w / L);
+        }
+        oh[c] = t;
+    }
+    __syncthreads();
+    // this thread's 8 head dims (16-byte Wo chunk cc) of o_h
+    const float4 t0 = oh[2 * cc], t1 = oh[2 * cc + 1];
+    const float o8[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+#pragma unroll
+    for (int q = 0; q < WPASS; q++) {
+        float v = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) v += bf16_lo(e & 1 ? wov[q][e >> 1] >> 16 : wov[q][e >> 1] & 0xffffu) * o8[e];
+        v = seg_sum<WCH>(v);
+        const int rl = rr + q * WRP, n = n0 + rl;
+        if (cc == 0 && rl < nrows) {
+            if (h == 0 && a.wo_bias) v = v + a.wo_bias[n];
+            __hip_atomic_fetch_add(a.wo_out + n, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 // 4 waves per (head, row) block when there are enough blocks to fill the
 // GPU; 16 waves when the visible context is long and blocks are few, so each
 // block keeps more of the KV stream in flight.
@@ -966,6 +1072,10 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
     }
     const dim3 grid(heads, rows);
     const AttnRoute route = attn_route(a, heads, rows);
+    if (a.wo && route != kRouteSplit) {
+        set_error("attention: the fused output projection here needs the key-split path");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
     if (a.k_raw && (route != kRouteSplit || rows != 1)) {
         set_error("attention: the fused q/k epilogue needs the key-split path (one new row, few heads)");
         return GORCH_HIP_EUNSUPPORTED;
@@ -1006,6 +1116,27 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
             // k_attn_combine
             const int nc = attn_split_chunks(a, heads, rows);
             const dim3 sg(heads, nc, rows), cg(heads, rows);
+            if (a.wo) {
+                // the output projection fused into the combine (one row)
+                const int rows_out = a.wo_rows ? a.wo_rows : a.dim;
+                if (rows != 1 || !a.wo_out || a.dim % 8 != 0 || (reinterpret_cast<uintptr_t>(a.wo) % 16) != 0 ||
+                    a.dim != heads * a.hd) {
+                    set_error("attention: the fused output projection needs one row and 16-byte Wo rows");
+                    return GORCH_HIP_EUNSUPPORTED;
+                }
+                const dim3 wg(heads, (rows_out + kCombineWoRows - 1) / kCombineWoRows);
+                if (a.hd == 64) {
+                    if (a.k_raw) hipLaunchKernelGGL((k_attn_long<16, 4, 4, true, true>), sg, dim3(256), 0, s, a);
+                    else hipLaunchKernelGGL((k_attn_long<16, 4, 4, true>), sg, dim3(256), 0, s, a);
+                    hipLaunchKernelGGL((k_attn_combine_wo<16>), wg, dim3(256), 0, s, a, nc);
+                } else {
+                    if (a.k_raw) hipLaunchKernelGGL((k_attn_long<32, 4, 4, true, true>), sg, dim3(256), 0, s, a);
+                    else hipLaunchKernelGGL((k_attn_long<32, 4, 4, true>), sg, dim3(256), 0, s, a);
+                    hipLaunchKernelGGL((k_attn_combine_wo<32>), wg, dim3(256), 0, s, a, nc);
+                }
+                count(CNT_ATTENTION);
+                return check_launch("attn_long_split_wo");
+            }
             if (a.hd == 64) {
                 if (a.k_raw) hipLaunchKernelGGL((k_attn_long<16, 4, 4, true, true>), sg, dim3(256), 0, s, a);
                 else hipLaunchKernelGGL((k_attn_long<16, 4, 4, true>), sg, dim3(256), 0, s, a);

@@ -280,6 +280,12 @@ struct AttnArgs {
     const uint16_t* wo = nullptr;
     const float* wo_bias = nullptr;
     float* wo_out = nullptr;
+    // key-split path with the output projection (a.wo set): Wo has wo_rows
+    // rows (0: dim) of row stride dim; wo_out is first set to wo_resid (or
+    // zeros) by the split kernel, then k_attn_combine_wo adds every head's
+    // Wo . o_h (+ wo_bias from head 0) with float atomics
+    int wo_rows = 0;
+    const float* wo_resid = nullptr;
     // Scratch for the key-split long-cache path (one new row, fewer than
     // 128 heads): per (head, key chunk) the chunk's max, weight sum and
     // unnormalised weighted values, hd + 2 floats. Null: one block per head.

@@ -138,6 +138,22 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
                          "gqa k copy"));
         }
     }
+    // one-row steps on the key-split path: Wo (+ bias and the residual) in
+    // the kernel that merges the key chunks, added into out with float
+    // atomics per head
+    static const bool wo_in_attn = [] {
+        const char* e = getenv("GORCH_HIP_GQA_WO_FUSE");
+        return e ? atoi(e) != 0 : true;
+    }();
+    if (wo_in_attn && S == 1 && qdim % 8 == 0 && (reinterpret_cast<uintptr_t>(w->wo) % 16) == 0 &&
+        attn_split_takes_qk(a, nq, S)) {
+        a.wo = w->wo;
+        a.wo_bias = w->bo;
+        a.wo_out = out;
+        a.wo_rows = d;
+        a.wo_resid = resid;
+        return launch_attn_cached(s, a, nq, S);
+    }
     GH_TRY(launch_attn_cached(s, a, nq, S));
     return launch_linear_bf16(s, att, w->wo, w->bo, resid, out, S, d, qdim, GORCH_HIP_EPI_NONE);
 }

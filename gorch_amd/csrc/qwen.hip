@@ -2,18 +2,19 @@
 // Block.ForwardCached, block.go:71-79) as one C-ABI call:
 //   x1 = x + GQA(RMSNorm_attn(x));  x = x1 + down(SwiGLU(gate(h), up(h))), h = RMSNorm_ffn(x1)
 //
-// One-row decode (the serving step) runs in six launches, each fusing what
+// One-row decode (the serving step) runs in five launches, each fusing what
 // the reference does as separate ops:
 //   1. RMSNorm_attn applied as the QKV GEMV loads x, Q/K/V as one weight
 //      stream (V written straight into its cache row);
-//   2-3. grouped-query attention over the cache: with few heads the
+//   2-3. grouped-query attention over the cache and Wo: with few heads the
 //      key-split kernel, which applies the per-head q/k RMSNorm + RoPE
-//      itself and writes the K row, plus its combine kernel; else one
-//      launch for the q/k norm + RoPE and one for the attention;
-//   4. Wo GEMV with the residual add (x1 = x + ...);
-//   5. RMSNorm_ffn applied as the gate/up GEMV loads x1 (one [2F, d] weight),
+//      itself, writes the K row and sets x1 = x, then the kernel that
+//      merges its key chunks and adds each head's Wo . o_h (+ bias) into
+//      x1; else a q/k norm + RoPE launch, the attention and a Wo GEMV with
+//      the residual add (x1 = x + ...);
+//   4. RMSNorm_ffn applied as the gate/up GEMV loads x1 (one [2F, d] weight),
 //      gate row j and up row F + j in one wave so it writes silu(gate) * up;
-//   6. down GEMV with the residual add.
+//   5. down GEMV with the residual add.
 // Longer inputs (prefill) take the same steps with the norms and SwiGLU as
 // launches of their own and the matrix-core GEMM for the Linears.
 #include "common.h"
