@@ -156,14 +156,19 @@ def test_gqa_qwen3_shaped_decode(gpu):
     (dict(dim=256, num_q=4, num_kv=2, head_dim=64, base=10000.0), 600, True, 0),
     # interleaved (NeoX) pairs, and RoPE without the per-head norm
     (dict(dim=512, num_q=4, num_kv=2, head_dim=128, base=10000.0), 70, True, 1),
-    (dict(dim=256, num_q=4, num_kv=4, head_dim=64, base=10000.0), 130, False, 0)])
+    (dict(dim=256, num_q=4, num_kv=4, head_dim=64, base=10000.0), 130, False, 0),
+    # q/k/v and output biases, and query width (8 x 64) above the model width
+    (dict(dim=256, num_q=8, num_kv=2, head_dim=64, base=10000.0, bias=True), 100, True, 0)])
 def test_gqa_module_key_split_steps(gpu, kw, prefill, qk_norm, neox):
     """One-row steps over few heads and a cache longer than one key chunk:
     the key-split attention (per-chunk max, weight sum and weighted values,
-    merged per head by the combine kernel) with the q/k RMSNorm and RoPE
+    merged per head by the kernel that also adds the output projection and
+    its bias) with the q/k RMSNorm and RoPE
     applied inside it (the new K row written to the cache by the kernel);
     outputs within 1e-3 of the oracle, cache rows within 1e-4."""
-    w = syn.gqa_weights(max_seq=prefill + 8, seed=14, bias=False, qk_norm=qk_norm, rope=True, **kw)
+    kw = dict(kw)
+    bias = kw.pop("bias", False)
+    w = syn.gqa_weights(max_seq=prefill + 8, seed=14, bias=bias, qk_norm=qk_norm, rope=True, **kw)
     w["rope_neox"] = neox
     rng = np.random.default_rng(15)
     chunks = [rng.standard_normal((n, w["dim"])).astype(np.float32) for n in (prefill, 1, 1, 1)]
