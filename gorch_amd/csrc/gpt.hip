@@ -171,12 +171,14 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
     // block of a K slice loads that slice of the activations, so activation
     // traffic is (blocks per slice) x (activation bytes): at 16 rows, d 1600,
     // 1.7x the weight bytes for an unsplit fused QKV and 2.6x for Wo in 2
-    // slices. 8 slices (GORCH_HIP_QKV_SPLIT, GORCH_HIP_RES_SPLIT) keep it
-    // near a fifth; the partials of the fused QKV are added by the attention
-    // kernel, those of Wo and FFN2 by the row reducer.
+    // slices. More slices (GORCH_HIP_QKV_SPLIT, GORCH_HIP_RES_SPLIT) cut it;
+    // the partials of the fused QKV are added by the two-pass attention
+    // kernel, those of Wo and FFN2 by the row reducer. The fused QKV takes 3
+    // slices by default (XL batch 16, exact-k-step tiles, CU-capped grid:
+    // 1 / 2 / 3 / 4 slices 5,249 / 5,330 / 5,335 / 5,240 tok/s).
     static const int qkv_split_req = [] {
         const char* e = getenv("GORCH_HIP_QKV_SPLIT");
-        return std::min(kMaxPartSlices, e ? atoi(e) : 1);
+        return std::min(kMaxPartSlices, e ? atoi(e) : 3);
     }();
     static const int res_split_req = [] {
         const char* e = getenv("GORCH_HIP_RES_SPLIT");
