@@ -189,6 +189,13 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         const char* e = getenv("GORCH_HIP_WO_FUSE");
         return e ? atoi(e) != 0 : true;
     }();
+    // Wo's slices (0: the packed-split rule); measured at XL batch 16 (with
+    // the 3-slice QKV): 2 / 3 / 4 / 5 / 6 / 8 slices 5,335 / 5,336 / 5,359 /
+    // 5,332 / 5,258 / 5,254 tok/s
+    static const int wo_split_req = [] {
+        const char* e = getenv("GORCH_HIP_WO_SPLIT");
+        return std::min(kMaxSplit, e ? atoi(e) : 4);
+    }();
     auto res_split = [&](int K) {
         return res_split_req > 0 ? ksplit_slices(K, res_split_req) : packed_split_slices(K, d);
     };
@@ -276,7 +283,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         if (!wo_fused && batched) {
             LinearExtras sp;
             sp.part = g->part;
-            sp.ksplit = w.wo_p ? res_split(d) : split_for(d);
+            sp.ksplit = w.wo_p ? (wo_split_req > 0 ? ksplit_slices(d, wo_split_req) : res_split(d)) : split_for(d);
             if (w.wo_p)
                 GH_TRY(launch_linear_packed_od(s, g->att, w.wo_p, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d,
                                                d, GORCH_HIP_EPI_NONE, sp));
