@@ -652,9 +652,9 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
     int jb = 0, je = T;
     if constexpr (SPLIT) {
         // with the fused output projection: the residual into the output
-        // rows (chunk 0 of each head copies its share) before the combine
-        // kernel adds to them
-        if (a.wo && blockIdx.y == 0) {
+        // rows (chunk 0 of each head copies its share; nothing when they
+        // are one buffer) before the combine kernel adds to them
+        if (a.wo && blockIdx.y == 0 && a.wo_out != a.wo_resid) {
             const int rows_out = a.wo_rows ? a.wo_rows : a.dim;
             const int seg = (rows_out + (int)gridDim.x - 1) / (int)gridDim.x;
             for (int e = threadIdx.x; e < seg; e += blockDim.x) {

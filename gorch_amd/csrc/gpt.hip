@@ -272,11 +272,22 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         // one row (batch 1, one token): the output projection runs inside
         // the attention kernel, which adds Wo . attention + bias into x
         const bool wo_fused = !batched && rows == 1 && wo_fuse && attn_rows_wo_ok(a, g->heads, rows);
+        // a longer cache on the key-split path: Wo in its chunk merge, added
+        // into x in place
+        const bool wo_split = !batched && rows == 1 && wo_fuse && !wo_fused && d % 8 == 0 &&
+                              (reinterpret_cast<uintptr_t>(w.wo) % 16) == 0 && attn_split_takes_qk(a, g->heads, rows);
         if (wo_fused) {
             a.wo = w.wo;
             a.wo_bias = w.bo;
             a.wo_out = g->x;
             GH_TRY(launch_attn_rows_wo(s, a, g->heads));
+        } else if (wo_split) {
+            a.wo = w.wo;
+            a.wo_bias = w.bo;
+            a.wo_out = g->x;
+            a.wo_rows = d;
+            a.wo_resid = g->x;
+            GH_TRY(launch_attn_cached(s, a, g->heads, rows));
         } else {
             GH_TRY(launch_attn_cached(s, a, g->heads, rows));
         }
@@ -292,7 +303,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
                                              GORCH_HIP_EPI_NONE, sp));
             GH_TRY(launch_reduce_rows(s, g->part, sp.ksplit, w.bo, g->x, rows, d, eps, g->stats, w.ln2_g, w.ln2_b,
                                       g->h));
-        } else if (!wo_fused) {
+        } else if (!wo_fused && !wo_split) {
             GH_TRY(launch_linear_bf16(s, g->att, w.wo, w.bo, g->x, g->x, rows, d, d, GORCH_HIP_EPI_NONE));
         }
         if (batched && w.w1_p) {
