@@ -979,9 +979,21 @@ static int attn_split_chunks(const AttnArgs& a, int heads, int rows) {
     }();
     if (!a.split_ws || a.new_seq != 1 || (a.hd != 64 && a.hd != 128)) return 0;
     if (rows != 1 && batch_target <= 0) return 0;
-    const int kc = a.hd == 64 ? 64 : 32;  // keys per 4-wave load round
+    static const int min_keys = [] {
+        const char* e = getenv("GORCH_HIP_SPLIT_MIN_KEYS");
+        return e ? atoi(e) : 0;
+    }();
+    const int kc = std::max(min_keys, a.hd == 64 ? 64 : 32);  // keys per 4-wave load round (at least)
     const long long keys = a.pos_dev ? (long long)a.max_seq : (long long)a.pos_host + a.new_seq;
-    const int want = rows == 1 ? std::max(1, 256 / heads) : (batch_target * 256 + heads * rows - 1) / (heads * rows);
+    // at most 8 chunks per head by default (Qwen3-shaped step at context
+    // 512: 16 / 12 / 10 / 8 / 6 chunks 1,245 / 1,249 / 1,257 / 1,256 / 1,249
+    // tok/s; GPT-2 small batch 1 at a 512-token prompt 3,572 -> 3,591 with 8)
+    static const int max_chunks = [] {
+        const char* e = getenv("GORCH_HIP_SPLIT_MAX_CHUNKS");
+        return std::max(2, std::min(kAttnSplitMax, e ? atoi(e) : 8));
+    }();
+    const int want = rows == 1 ? std::min(max_chunks, std::max(1, 256 / heads))
+                               : (batch_target * 256 + heads * rows - 1) / (heads * rows);
     const int nc = (int)std::min<long long>(std::min(kAttnSplitMax, want), (keys + kc - 1) / kc);
     if (nc < 2 || a.split_ws_floats < (long long)rows * heads * nc * (a.hd + 2)) return 0;
     return nc;
