@@ -1205,12 +1205,29 @@ static int launch_mt(hipStream_t s, const float* x, const uint16_t* W, const flo
 static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const float* bias, const float* residual,
                         const OutDesc& od, int M, int N, int K, int epilogue, const LinearExtras& ex, bool packed) {
     static const int nw_env = env_int("GORCH_HIP_TILES_NW", 0);
+    static const int auto_nw4 = env_int("GORCH_HIP_TILES_NW4", 1);
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+            n = 256;
+        return env_int("GORCH_HIP_TILES_CAP", n);
+    }();
     static const int blocks_env = env_int("GORCH_HIP_TILES_BLOCKS", 0);
     const int ntiles = (N + 15) / 16;
     // with ex.part the grid's y dimension is ex.ksplit K slices of ex.kslice
     const int S = ex.part ? ex.ksplit : 1;
     const int ksteps = ex.part ? ex.kslice / 32 : (K + 31) / 32;
-    const int nw = nw_env ? nw_env : 8;
+    // 8 waves per block; 4 when the blocks hold one or two tiles each (the
+    // weight is short in tiles for the grid) and a 4-wave instantiation
+    // takes the k-steps (measured: 9-shape GEMV sweep, 768x3072 at M = 4 /
+    // 16 3.43 / 3.95 -> 3.21 / 3.74 us; the LM head keeps 8)
+    int nw = nw_env ? nw_env : 8;
+    if (!nw_env && !ex.ln_g && auto_nw4) {
+        const int ks4 = (ksteps + 3) / 4;
+        const bool fits4 = ks4 <= 8 && ks4 != 5 && ks4 != 7;
+        if (fits4 && ntiles * S <= 2 * cus) nw = 4;
+    }
     const int ks = (ksteps + nw - 1) / nw;
     // one round of resident blocks: a block beyond what the CUs hold at once
     // would run as a second, mostly idle round (measured 10 vs 7 us)
@@ -1252,13 +1269,6 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
     // CUs, since a second block on a CU streams beside the first and
     // doubles that CU's time (XL batch 16: FFN2's 7 K slices on 36 instead
     // of 73 blocks each, 5,059 -> 5,146 tok/s)
-    static const int cus = [] {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
-            n = 256;
-        return env_int("GORCH_HIP_TILES_CAP", n);
-    }();
 #define GH_TILES(NWV, KSV)                                                                                \
     if (nw == NWV && ks <= KSV) {                                                                         \
         static const int blocks_p = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, true, false, false>), NWV * 64); \
@@ -1277,7 +1287,8 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
     // a padding slot still costs its instructions and registers (measured:
     // 8 waves x 3 against x 4 at K = 768, 9-shape GEMV sweep 3,362 -> 3,435
     // GB/s)
-    GH_TILES(4, 4) GH_TILES(4, 8) GH_TILES(8, 3) GH_TILES(8, 4) GH_TILES(8, 7) GH_TILES(8, 8) GH_TILES(8, 12)
+    GH_TILES(4, 3) GH_TILES(4, 4) GH_TILES(4, 6) GH_TILES(4, 8) GH_TILES(8, 2) GH_TILES(8, 3) GH_TILES(8, 4) GH_TILES(8, 7)
+    GH_TILES(8, 8) GH_TILES(8, 12)
     GH_TILES(16, 4)
 #undef GH_TILES
 #undef GH_TILES_L
@@ -1565,8 +1576,11 @@ int launch_pack_bf16(hipStream_t s, const uint16_t* W, uint16_t* Wp, int N, int 
 // K = 1600 / 3072 / 6400 over 1600 / 768 / 1600 rows: 7.2 / 7.1 / 10.9 us at
 // 16 rows against 7.7 / 7.2 / 15.6 us for the row-major split).
 int packed_split_slices(int K, int N) {
+    // blocks a K split aims at (3072x768 at M = 4 / 16 with 4-wave blocks:
+    // 192 -> 384 took 5.16 / 5.77 to 5.05 / 5.50 us)
+    static const int split_target = env_int("GORCH_HIP_SPLIT_TARGET", 384);
     const int ksteps = (K + 31) / 32, ntiles = (N + 15) / 16;
-    int S = std::max((ksteps + 31) / 32, (192 + ntiles - 1) / ntiles);
+    int S = std::max((ksteps + 31) / 32, (split_target + ntiles - 1) / ntiles);
     S = std::min(std::min(S, kEpiSlices), std::max(1, ksteps / 3));
     return ksplit_slices(K, S);
 }
