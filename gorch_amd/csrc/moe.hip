@@ -146,6 +146,7 @@ __global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ logi
 // are parked in inv; once every expert's size is known the bases, the GEMM
 // tile table (one thread per expert) and the packed-row maps follow.
 constexpr int kRouteThreads = 1024, kRouteWaves = kRouteThreads / 64;
+template <int KT>
 __global__ __launch_bounds__(kRouteThreads) void k_moe_route(int M, int E, int K, int tile_rows, MoeWs ws) {
     __shared__ int wtot[kRouteWaves][kMaxExperts];
     __shared__ int run[kMaxExperts];
@@ -155,36 +156,57 @@ __global__ __launch_bounds__(kRouteThreads) void k_moe_route(int M, int E, int K
     const unsigned long long lt_mask = (1ull << lane) - 1ull;
     if (t < E) run[t] = 0;
     __syncthreads();
-    for (int r0 = 0; r0 < M; r0 += kRouteThreads) {
+    // up to RR rounds keep their slots' experts, ranks and weights in
+    // registers for the final scatter (no second read of the tables); fewer
+    // rounds with more slots, within the 128 registers of a 1024-thread block
+    constexpr int RR = KT <= 2 ? 4 : 1;
+    const bool regs = M <= RR * kRouteThreads;
+    int ridx[RR][KT], rrank[RR][KT];
+    float rw[RR][KT];
+    int round = 0;
+    for (int r0 = 0; r0 < M; r0 += kRouteThreads, round++) {
         const int tok = r0 + t;
         const bool live = tok < M;
-        int idx[kMaxTopK];
+        int idx[KT];
 #pragma unroll
-        for (int s = 0; s < kMaxTopK; s++) idx[s] = (live && s < K) ? ws.topi[(size_t)tok * K + s] : -1;
+        for (int s = 0; s < KT; s++) idx[s] = (live && s < K) ? ws.topi[(size_t)tok * K + s] : -1;
+        float wv[KT];
+#pragma unroll
+        for (int s = 0; s < KT; s++) wv[s] = (regs && live && s < K) ? ws.topw[(size_t)tok * K + s] : 0.f;
         // this round's per-wave counts and lane prefixes, expert by expert
-        int pre[kMaxTopK];
+        int pre[KT];
 #pragma unroll
-        for (int s = 0; s < kMaxTopK; s++) pre[s] = 0;
+        for (int s = 0; s < KT; s++) pre[s] = 0;
         for (int e = 0; e < E; e++) {
             bool mine = false;
 #pragma unroll
-            for (int s = 0; s < kMaxTopK; s++) mine |= (idx[s] == e);
+            for (int s = 0; s < KT; s++) mine |= (idx[s] == e);
             const unsigned long long bits = __ballot(mine);
             if (lane == 0) wtot[wave][e] = __popcll(bits);
             const int lp = __popcll(bits & lt_mask);
 #pragma unroll
-            for (int s = 0; s < kMaxTopK; s++)
+            for (int s = 0; s < KT; s++)
                 if (idx[s] == e) pre[s] = lp;
         }
         __syncthreads();
         if (live)
 #pragma unroll
-            for (int s = 0; s < kMaxTopK; s++) {
+            for (int s = 0; s < KT; s++) {
                 if (s >= K) break;
                 const int e = idx[s];
                 int rank = run[e] + pre[s];
                 for (int w = 0; w < wave; w++) rank += wtot[w][e];
-                ws.inv[(size_t)tok * K + s] = rank;  // rank inside expert e for now
+                if (regs) {
+#pragma unroll
+                    for (int q = 0; q < RR; q++)
+                        if (q == round) {
+                            ridx[q][s] = e;
+                            rrank[q][s] = rank;
+                            rw[q][s] = wv[s];
+                        }
+                } else {
+                    ws.inv[(size_t)tok * K + s] = rank;  // rank inside expert e for now
+                }
             }
         __syncthreads();
         if (t < E)
@@ -211,6 +233,23 @@ __global__ __launch_bounds__(kRouteThreads) void k_moe_route(int M, int E, int K
             ws.tile_r0[i] = base[t] + r;
             ws.tile_n[i] = min(tile_rows, n - r);
         }
+    }
+    if (regs) {
+#pragma unroll
+        for (int q = 0; q < RR; q++) {
+            const int tok = t + q * kRouteThreads;
+            if (tok >= M) break;
+#pragma unroll
+            for (int s = 0; s < KT; s++) {
+                if (s >= K) break;
+                const size_t a = (size_t)tok * K + s;
+                const int p = base[ridx[q][s]] + rrank[q][s];
+                ws.perm_tok[p] = tok;
+                ws.perm_w[p] = rw[q][s];
+                ws.inv[a] = p;
+            }
+        }
+        return;
     }
     for (int tok = t; tok < M; tok += kRouteThreads)
         for (int s = 0; s < K; s++) {
@@ -583,7 +622,9 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
         return !e || atoi(e) != 0;
     }();
     const int tile_rows = wide ? kWideBM : kMoeBM;
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(kRouteThreads), 0, s, M, E, K, tile_rows, ws);
+    // top-K slots sized to K (every absent slot still costs its compares)
+    if (K <= 2) hipLaunchKernelGGL(k_moe_route<2>, dim3(1), dim3(kRouteThreads), 0, s, M, E, K, tile_rows, ws);
+    else hipLaunchKernelGGL(k_moe_route<kMaxTopK>, dim3(1), dim3(kRouteThreads), 0, s, M, E, K, tile_rows, ws);
     GH_TRY(check_launch("moe_route"));
     const int MK = M * K;
     const int max_tiles = MK / tile_rows + E + 1;
