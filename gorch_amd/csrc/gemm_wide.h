@@ -7,13 +7,18 @@
 // moves bytes: every global load and LDS store is 16 bytes. W is bf16 in the
 // nn.Linear [out, in] layout.
 //
-// What bounds these GEMMs on MI355X is the L2 -> CU path, ~16 B/clock per CU
-// (~9.6 TB/s over the chip, measured), not the matrix cores: the time is the
-// L2 traffic — A re-read once per column tile, W once per row tile. Wide
-// tiles (128 rows x up to 256 weight columns, 8 waves in a 2 x 4 grid, each
-// a region of 16x16 v_mfma_f32_16x16x32_bf16 accumulators) cut that traffic,
-// and 64-wide K stages read whole 128-byte cache lines (a 32-wide stage
-// reads half a line per row and fetches every line twice).
+// Measured on MI355X (MoE gate/up GEMM, 2048 tokens x top-2, d 1024, ffn
+// 4096): the matrix cores and LDS together take most of the time — with the
+// global loads switched off 163 of 180 us, with the MFMAs switched off 127
+// us (global -> LDS alone, ~16 B/clock per CU, 73% L2 hits) — and the MFMAs
+// run at ~42% of their measured 2.05 PFLOP/s peak. Wide tiles (128 rows x up
+// to 256 weight columns on WGM x WGN waves, each a region of 16x16
+// v_mfma_f32_16x16x32_bf16 accumulators) bound the L2 traffic (A re-read
+// once per column tile, W once per row tile) and the LDS fragment reads per
+// MFMA; 16 waves (4 x 4) measured faster than 8 (2 x 4): four waves per SIMD
+// cover one another's LDS round trips. 64-wide K stages read whole 128-byte
+// cache lines (a 32-wide stage reads half a line per row and fetches every
+// line twice).
 //
 // Pipeline: LDS is double-buffered and registers hold two stages, so stage
 // i+3's loads are issued while stage i runs on the matrix cores; one barrier
@@ -29,12 +34,12 @@
 
 namespace gh {
 
-template <int BM, int BNW, int NB, bool SPLIT, int BK = 64, bool IL = false>
+template <int BM, int BNW, int NB, bool SPLIT, int BK = 64, bool IL = false, int WGM = 2, int WGN = 4>
 struct WideGemm {
-    static constexpr int kThreads = 512;  // 8 waves: 2 (rows) x 4 (columns)
-    static constexpr int CH = BK / 8;     // 16-byte chunks per row and stage
+    static constexpr int kThreads = 64 * WGM * WGN;  // WGM (rows) x WGN (columns) waves
+    static constexpr int CH = BK / 8;                // 16-byte chunks per row and stage
     static constexpr int NA = SPLIT ? 2 : 1;
-    static constexpr int WM = BM / 2, WNW = BNW / 4;
+    static constexpr int WM = BM / WGM, WNW = BNW / WGN;
     static constexpr int TM = WM / 16, TN = WNW / 16;
     static constexpr int A_U4 = NA * BM * CH / kThreads;  // 16-byte loads per thread per stage
     static constexpr int W_U4 = NB * BNW * CH / kThreads;
@@ -68,7 +73,7 @@ struct WideGemm {
                                const uint16_t* const* w, int ncols, int K, int kb, int ke, Xform& xform,
                                Store& store) {
         const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-        const int wm = wave >> 2, wn = wave & 3;
+        const int wm = wave / WGN, wn = wave % WGN;
         const int r = lane & 15, g = lane >> 4;
         const int nk = (ke - kb + BK - 1) / BK;
 

@@ -501,18 +501,34 @@ __global__ void k_moe_gather_split(const float* __restrict__ x, const int* __res
 // A: planes (hi, lo) of [rows, Kd]. DUAL: gate and up side by side, H =
 // SwiGLU(gate, up) written as planes (Chi, Clo); else C = (acc + b) * w(row)
 // in f32.
-template <bool DUAL, int BNW, bool IL = false>
-__global__ __launch_bounds__(512) void k_moe_wide(const uint16_t* __restrict__ Ahi, const uint16_t* __restrict__ Alo,
+template <bool DUAL, int BNW, bool IL = false, int WGM = 2>
+__global__ __launch_bounds__(WGM * 256) void k_moe_wide(const uint16_t* __restrict__ Ahi, const uint16_t* __restrict__ Alo,
                                                   const uint16_t* __restrict__ W1, const uint16_t* __restrict__ W2,
                                                   const float* __restrict__ b1, const float* __restrict__ b2,
                                                   float* __restrict__ C, uint16_t* __restrict__ Chi,
                                                   uint16_t* __restrict__ Clo, int N, int Kd, long long cslice,
-                                                  MoeWs ws) {
-    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true, 64, IL>;
+                                                  int xcd_map, MoeWs ws) {
+    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true, 64, IL, WGM, 4>;
     extern __shared__ __align__(16) uint4 moe_smem[];
-    if ((int)blockIdx.y >= *ws.ntiles) return;
-    const int e = ws.tile_e[blockIdx.y], r0 = ws.tile_r0[blockIdx.y], nrows = ws.tile_n[blockIdx.y];
-    const int n0 = blockIdx.x * BNW;
+    int tx = blockIdx.x, ty = blockIdx.y;
+    if (xcd_map) {
+        // Blocks are dealt to the 8 XCDs round-robin by linear index; here
+        // XCD k takes the k-th contiguous run of the live (row tile, column
+        // tile) items, row-tile major, so the column tiles of one row tile
+        // share that XCD's L2 for their A reads. The host pads the grid to
+        // at least 8 * ceil(items / 8) blocks per K slice.
+        const int L = blockIdx.y * gridDim.x + blockIdx.x;
+        const int items = *ws.ntiles * (int)gridDim.x;
+        const int per = (items + 7) >> 3;
+        const int item = (L & 7) * per + (L >> 3);
+        if ((L >> 3) >= per || item >= items) return;
+        tx = item % gridDim.x;
+        ty = item / gridDim.x;
+    } else if (ty >= *ws.ntiles) {
+        return;
+    }
+    const int e = ws.tile_e[ty], r0 = ws.tile_r0[ty], nrows = ws.tile_n[ty];
+    const int n0 = tx * BNW;
     const uint16_t* a[2] = {Ahi + (size_t)r0 * Kd, Alo + (size_t)r0 * Kd};
     const uint16_t* w[2] = {W1 + ((size_t)e * N + n0) * Kd, DUAL ? W2 + ((size_t)e * N + n0) * Kd : nullptr};
     const float* bg = b1 ? b1 + (size_t)e * N + n0 : nullptr;
@@ -553,20 +569,20 @@ __global__ __launch_bounds__(512) void k_moe_wide(const uint16_t* __restrict__ A
            store);
 }
 
-template <bool DUAL, int BNW, bool IL>
+template <bool DUAL, int BNW, bool IL, int WGM>
 static int launch_moe_wide_t(hipStream_t s, dim3 grid, const uint16_t* Ahi, const uint16_t* Alo, const uint16_t* W1,
                              const uint16_t* W2, const float* b1, const float* b2, float* C, uint16_t* Chi,
-                             uint16_t* Clo, int N, int Kd, long long cslice, const MoeWs& ws) {
-    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true, 64, IL>;
+                             uint16_t* Clo, int N, int Kd, long long cslice, int xcd_map, const MoeWs& ws) {
+    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true, 64, IL, WGM, 4>;
     static bool attr_set = false;
     if (!attr_set) {
-        GH_TRY(check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_moe_wide<DUAL, BNW, IL>),
+        GH_TRY(check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_moe_wide<DUAL, BNW, IL, WGM>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(typename G::Smem)),
                      "moe_wide attribute"));
         attr_set = true;
     }
-    hipLaunchKernelGGL((k_moe_wide<DUAL, BNW, IL>), grid, dim3(G::kThreads), sizeof(typename G::Smem), s, Ahi, Alo,
-                       W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice, ws);
+    hipLaunchKernelGGL((k_moe_wide<DUAL, BNW, IL, WGM>), grid, dim3(G::kThreads), sizeof(typename G::Smem), s, Ahi, Alo,
+                       W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice, xcd_map, ws);
     return check_launch(DUAL ? "moe_wide_gate_up" : "moe_wide_down");
 }
 
@@ -579,9 +595,37 @@ static int launch_moe_wide(hipStream_t s, dim3 grid, const uint16_t* Ahi, const 
         const char* e = getenv("GORCH_HIP_MOE_IL");
         return !e || atoi(e) != 0;
     }();
+    // GORCH_HIP_MOE_XCD: bit 0 the down GEMM, bit 1 the gate/up GEMM take
+    // the XCD-contiguous block order
+    static const int xcd_bits = [] {
+        const char* e = getenv("GORCH_HIP_MOE_XCD");
+        return e ? atoi(e) : 1;
+    }();
+    const int xcd_map = (xcd_bits >> (DUAL ? 1 : 0)) & 1;
+    if (xcd_map) {
+        // at least 8 * ceil(items / 8) blocks per slice, a multiple of 8
+        const long long need = ((long long)grid.x * grid.y + 7) / 8 * 8;
+        grid.y = (unsigned)((need + grid.x - 1) / grid.x);
+        while (((long long)grid.x * grid.y) % 8) grid.y++;
+    }
+    // GORCH_HIP_MOE_W16: bit 0 the down GEMM, bit 1 the gate/up GEMM run
+    // 16 waves (4 x 4) per block instead of 8 (2 x 4): four waves per SIMD
+    // hide the LDS round trips of one another (measured: gate/up 180 -> 170
+    // us, down 108 -> 102 us). They take the compiler's schedule: the
+    // interleaved one holds both halves' fragments and spills at 128
+    // registers.
+    static const int w16_bits = [] {
+        const char* e = getenv("GORCH_HIP_MOE_W16");
+        return e ? atoi(e) : 3;
+    }();
+    if ((w16_bits >> (DUAL ? 1 : 0)) & 1)
+        return launch_moe_wide_t<DUAL, BNW, false, 4>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice,
+                                                      xcd_map, ws);
     if (il)
-        return launch_moe_wide_t<DUAL, BNW, true>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice, ws);
-    return launch_moe_wide_t<DUAL, BNW, false>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice, ws);
+        return launch_moe_wide_t<DUAL, BNW, true, 2>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice,
+                                                     xcd_map, ws);
+    return launch_moe_wide_t<DUAL, BNW, false, 2>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice,
+                                                  xcd_map, ws);
 }
 
 }  // namespace gh
