@@ -34,7 +34,7 @@
 
 namespace gh {
 
-template <int BM, int BNW, int NB, bool SPLIT, int BK = 64, bool IL = false, int WGM = 2, int WGN = 4>
+template <int BM, int BNW, int NB, bool SPLIT, int BK = 64, bool IL = false, int WGM = 2, int WGN = 4, int PD = 2>
 struct WideGemm {
     static constexpr int kThreads = 64 * WGM * WGN;  // WGM (rows) x WGN (columns) waves
     static constexpr int CH = BK / 8;                // 16-byte chunks per row and stage
@@ -84,7 +84,7 @@ struct WideGemm {
 #pragma unroll
         for (int b = 0; b < NB; b++) rsw[b] = make_rsrc(w[b], (long long)ncols * K * 2);
 
-        u32x4 ra[2][A_U4], rw[2][W_U4];
+        u32x4 ra[PD][A_U4], rw[PD][W_U4];
         auto gload = [&](int st, u32x4 (&ar)[A_U4], u32x4 (&wr)[W_U4]) {
             const int k0 = kb + st * BK;
 #pragma unroll
@@ -229,6 +229,29 @@ struct WideGemm {
         // zeros; an odd stage count runs one all-zero stage) so the compiler
         // can keep the newer stage's loads in flight across the wait.
         const int nk2 = (nk + 1) & ~1;
+        if constexpr (PD == 1) {
+            // one register set: stage s + 2 is requested as stage s + 1
+            // leaves it (one stage of load latency covered)
+            gload(0, ra[0], rw[0]);
+            sstore(0, ra[0], rw[0]);
+            gload(1, ra[0], rw[0]);
+            __syncthreads();
+            for (int it = 0; it < nk2; it += 2) {
+                if constexpr (IL) {
+                    stage_il(0, ra[0], rw[0], it + 2);
+                    stage_il(1, ra[0], rw[0], it + 3);
+                } else {
+                    compute(0);
+                    sstore(1, ra[0], rw[0]);
+                    gload(it + 2, ra[0], rw[0]);
+                    __syncthreads();
+                    compute(1);
+                    sstore(0, ra[0], rw[0]);
+                    gload(it + 3, ra[0], rw[0]);
+                    __syncthreads();
+                }
+            }
+        } else {
         gload(0, ra[0], rw[0]);
         gload(1, ra[1], rw[1]);
         sstore(0, ra[0], rw[0]);
@@ -248,6 +271,7 @@ struct WideGemm {
                 gload(it + 4, ra[0], rw[0]);
                 __syncthreads();
             }
+        }
         }
 
         // lane holds rows 4g..4g+3 of column r in each 16x16 fragment

@@ -501,14 +501,14 @@ __global__ void k_moe_gather_split(const float* __restrict__ x, const int* __res
 // A: planes (hi, lo) of [rows, Kd]. DUAL: gate and up side by side, H =
 // SwiGLU(gate, up) written as planes (Chi, Clo); else C = (acc + b) * w(row)
 // in f32.
-template <bool DUAL, int BNW, bool IL = false, int WGM = 2>
+template <bool DUAL, int BNW, bool IL = false, int WGM = 2, int PD = 2>
 __global__ __launch_bounds__(WGM * 256) void k_moe_wide(const uint16_t* __restrict__ Ahi, const uint16_t* __restrict__ Alo,
                                                   const uint16_t* __restrict__ W1, const uint16_t* __restrict__ W2,
                                                   const float* __restrict__ b1, const float* __restrict__ b2,
                                                   float* __restrict__ C, uint16_t* __restrict__ Chi,
                                                   uint16_t* __restrict__ Clo, int N, int Kd, long long cslice,
                                                   int xcd_map, MoeWs ws) {
-    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true, 64, IL, WGM, 4>;
+    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true, 64, IL, WGM, 4, PD>;
     extern __shared__ __align__(16) uint4 moe_smem[];
     int tx = blockIdx.x, ty = blockIdx.y;
     if (xcd_map) {
@@ -569,19 +569,19 @@ __global__ __launch_bounds__(WGM * 256) void k_moe_wide(const uint16_t* __restri
            store);
 }
 
-template <bool DUAL, int BNW, bool IL, int WGM>
+template <bool DUAL, int BNW, bool IL, int WGM, int PD = 2>
 static int launch_moe_wide_t(hipStream_t s, dim3 grid, const uint16_t* Ahi, const uint16_t* Alo, const uint16_t* W1,
                              const uint16_t* W2, const float* b1, const float* b2, float* C, uint16_t* Chi,
                              uint16_t* Clo, int N, int Kd, long long cslice, int xcd_map, const MoeWs& ws) {
-    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true, 64, IL, WGM, 4>;
+    using G = WideGemm<kWideBM, BNW, DUAL ? 2 : 1, true, 64, IL, WGM, 4, PD>;
     static bool attr_set = false;
     if (!attr_set) {
-        GH_TRY(check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_moe_wide<DUAL, BNW, IL, WGM>),
+        GH_TRY(check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_moe_wide<DUAL, BNW, IL, WGM, PD>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(typename G::Smem)),
                      "moe_wide attribute"));
         attr_set = true;
     }
-    hipLaunchKernelGGL((k_moe_wide<DUAL, BNW, IL, WGM>), grid, dim3(G::kThreads), sizeof(typename G::Smem), s, Ahi, Alo,
+    hipLaunchKernelGGL((k_moe_wide<DUAL, BNW, IL, WGM, PD>), grid, dim3(G::kThreads), sizeof(typename G::Smem), s, Ahi, Alo,
                        W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice, xcd_map, ws);
     return check_launch(DUAL ? "moe_wide_gate_up" : "moe_wide_down");
 }
@@ -611,13 +611,24 @@ static int launch_moe_wide(hipStream_t s, dim3 grid, const uint16_t* Ahi, const 
     // GORCH_HIP_MOE_W16: bit 0 the down GEMM, bit 1 the gate/up GEMM run
     // 16 waves (4 x 4) per block instead of 8 (2 x 4): four waves per SIMD
     // hide the LDS round trips of one another (measured: gate/up 180 -> 170
-    // us, down 108 -> 102 us). They take the compiler's schedule: the
-    // interleaved one holds both halves' fragments and spills at 128
-    // registers.
+    // us, down 108 -> 102 us). GORCH_HIP_MOE_W16IL: 1 (default) the
+    // interleaved schedule with one register set for the global loads (both
+    // halves' fragments fit the 128 registers then; gate/up 169 -> 159 us,
+    // down 102 -> 96 us), 2 the compiler's schedule with one set, 0 with two.
     static const int w16_bits = [] {
         const char* e = getenv("GORCH_HIP_MOE_W16");
         return e ? atoi(e) : 3;
     }();
+    static const int w16il = [] {
+        const char* e = getenv("GORCH_HIP_MOE_W16IL");
+        return e ? atoi(e) : 1;
+    }();
+    if (((w16_bits >> (DUAL ? 1 : 0)) & 1) && w16il == 1)
+        return launch_moe_wide_t<DUAL, BNW, true, 4, 1>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice,
+                                                        xcd_map, ws);
+    if (((w16_bits >> (DUAL ? 1 : 0)) & 1) && w16il == 2)
+        return launch_moe_wide_t<DUAL, BNW, false, 4, 1>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd,
+                                                         cslice, xcd_map, ws);
     if ((w16_bits >> (DUAL ? 1 : 0)) & 1)
         return launch_moe_wide_t<DUAL, BNW, false, 4>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice,
                                                       xcd_map, ws);
