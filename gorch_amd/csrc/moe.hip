@@ -85,15 +85,22 @@ static size_t moe_layout(int M, int dim, int ffn, int E, int K, char* base, MoeW
 // the reference's > compare) and the routing weights, softmaxRows over the
 // K values: max, exp in f64 rounded to f32, f32 sum, divide. Written to the
 // workspace and, when given, to the caller's arrays.
+template <int EV>
 __global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ logits, int M, int E, int K,
                                                   int* __restrict__ topi, float* __restrict__ topw,
                                                   int* __restrict__ topi_out, float* __restrict__ topw_out) {
     const int tok = blockIdx.x * blockDim.x + threadIdx.x;
     if (tok >= M) return;
-    const float* row = logits + (size_t)tok * E;
-    float lv[kMaxExperts];  // the token's logits in registers, all loads in flight
+    // the token's EV >= E logits in registers, every load in flight at once:
+    // raw buffer loads through one resource over the whole [M, E] table
+    // (slots past E read the next row or, past the table, zeros, and are
+    // never selected; a load under a branch would be waited on before the
+    // next one, one round trip per expert). M * E < 2^29 (host check).
+    const __amdgpu_buffer_rsrc_t rl = make_rsrc(logits, (long long)M * E * 4);
+    float lv[EV];
 #pragma unroll
-    for (int j = 0; j < kMaxExperts; j++) lv[j] = j < E ? row[j] : 0.f;
+    for (int j = 0; j < EV; j++)
+        lv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rl, (tok * E + j) * 4, 0, 0));
     int idx[kMaxTopK];
     float val[kMaxTopK];
     unsigned long long taken = 0ull;
@@ -103,7 +110,7 @@ __global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ logi
         int best = -1;
         float bv = 0.f;
 #pragma unroll
-        for (int j = 0; j < kMaxExperts; j++) {
+        for (int j = 0; j < EV; j++) {
             if (j >= E || ((taken >> j) & 1ull)) continue;
             if (best < 0 || lv[j] > bv) {
                 best = j;
@@ -655,6 +662,7 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
     const int E = w->experts, K = w->top_k, d = w->dim, F = w->ffn;
     GH_REQUIRE(K >= 1 && K <= E, "gorch/nn: MoE numExpertsPerToken out of range");
     GH_REQUIRE(E <= kMaxExperts && K <= kMaxTopK, "gorch_hip_moe_forward: at most 64 experts and top-8");
+    GH_REQUIRE((long long)M * E < (1ll << 29), "gorch_hip_moe_forward: M * experts must be below 2^29");
     GH_REQUIRE(d % 8 == 0 && F % 8 == 0, "gorch_hip_moe_forward: dim and ffn must be multiples of 8");
     GH_REQUIRE(w->wgate && w->wup && w->wdown, "gorch_hip_moe_forward: null expert weights");
     GH_REQUIRE(logits || w->wr, "gorch_hip_moe_forward: need router weights or injected logits");
@@ -669,8 +677,14 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
         GH_TRY(launch_linear_bf16(s, x, w->wr, w->br, nullptr, ws.logits, M, E, d, GORCH_HIP_EPI_NONE));
         lg = ws.logits;
     }
-    hipLaunchKernelGGL(k_moe_topk, dim3((M + 255) / 256), dim3(256), 0, s, lg, M, E, K, ws.topi, ws.topw, topk_idx,
-                       topk_w);
+    const dim3 tgrid((M + 255) / 256);
+    if (E <= 8)
+        hipLaunchKernelGGL(k_moe_topk<8>, tgrid, dim3(256), 0, s, lg, M, E, K, ws.topi, ws.topw, topk_idx, topk_w);
+    else if (E <= 16)
+        hipLaunchKernelGGL(k_moe_topk<16>, tgrid, dim3(256), 0, s, lg, M, E, K, ws.topi, ws.topw, topk_idx, topk_w);
+    else
+        hipLaunchKernelGGL(k_moe_topk<kMaxExperts>, tgrid, dim3(256), 0, s, lg, M, E, K, ws.topi, ws.topw, topk_idx,
+                           topk_w);
     GH_TRY(check_launch("moe_topk"));
     static const bool wide = [] {
         const char* e = getenv("GORCH_HIP_MOE_WIDE");
