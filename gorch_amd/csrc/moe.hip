@@ -282,53 +282,85 @@ __global__ void k_moe_gather(const float* __restrict__ x, const int* __restrict_
 // (the reference adds each expert's ScatterAdd contribution in order). One
 // thread per (token, 4 columns); dim % 4 == 0. nsl > 1: the down GEMM left
 // raw K-slice partials, and a row's value is ((sum of slices) + bias) * w.
+// out[t] = the token's K expert rows summed in ascending expert order
+// (nn/moe.go:155-180). KT >= K slots: the token's expert indices and packed
+// rows are loaded together, sorted in registers, then every row's chunk is
+// loaded at once (raw buffer loads, unused slots out of range), so a chunk
+// costs two dependent round trips. With nsl > 1 K slices of the down GEMM
+// the slices, bias and routing weight are added here.
+template <int KT>
 __global__ void k_moe_combine(const float* __restrict__ yg, const int* __restrict__ inv,
                               const int* __restrict__ topi, float* out, int M, int K, int dim, int nsl,
                               long long cslice, const float* __restrict__ bdown,
                               const float* __restrict__ perm_w) {
     const int d4 = dim / 4;
+    const long long MK = (long long)M * K;
+    const __amdgpu_buffer_rsrc_t rt = make_rsrc(topi, MK * 4);
+    const __amdgpu_buffer_rsrc_t ri = make_rsrc(inv, MK * 4);
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(yg, MK * dim * 4);
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)M * d4;
          i += (int64_t)gridDim.x * blockDim.x) {
         const int t = (int)(i / d4), c = (int)(i - (int64_t)t * d4);
-        int order[kMaxTopK];
-        for (int s = 0; s < K; s++) order[s] = s;
-        for (int a = 1; a < K; a++)  // insertion sort of slots by expert index
-            for (int b = a; b > 0 && topi[(size_t)t * K + order[b]] < topi[(size_t)t * K + order[b - 1]]; b--) {
-                int tmp = order[b];
-                order[b] = order[b - 1];
-                order[b - 1] = tmp;
+        int e[KT], p[KT], order[KT];
+#pragma unroll
+        for (int s = 0; s < KT; s++) {
+            const int off = s < K ? (t * K + s) * 4 : kOutOfRange;
+            e[s] = (int)__builtin_amdgcn_raw_buffer_load_b32(rt, off, 0, 0);
+            p[s] = (int)__builtin_amdgcn_raw_buffer_load_b32(ri, off, 0, 0);
+            order[s] = s;
+        }
+#pragma unroll
+        for (int a = 1; a < KT; a++)  // insertion sort of the slots by expert index
+#pragma unroll
+            for (int b = a; b > 0; b--) {
+                const bool sw = b < K && e[order[b]] < e[order[b - 1]];
+                const int lo = sw ? order[b] : order[b - 1], hi = sw ? order[b - 1] : order[b];
+                order[b - 1] = lo;
+                order[b] = hi;
             }
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int s = 0; s < K; s++) {
-            const int p = inv[(size_t)t * K + order[s]];
-            float4 v = reinterpret_cast<const float4*>(yg + (size_t)p * dim)[c];
-            if (nsl > 1) {
+        float4 v[KT];
+#pragma unroll
+        for (int s = 0; s < KT; s++) {
+            const int q = order[s];
+            int pq = p[0];
+#pragma unroll
+            for (int u = 1; u < KT; u++) pq = q == u ? p[u] : pq;
+            const int off = s < K ? (pq * dim + 4 * c) * 4 : kOutOfRange;
+            v[s] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ry, off, 0, 0));
+            if (nsl > 1 && s < K) {
+                int eq = e[0];
+#pragma unroll
+                for (int u = 1; u < KT; u++) eq = q == u ? e[u] : eq;
                 for (int z = 1; z < nsl; z++) {
-                    const float4 u = reinterpret_cast<const float4*>(yg + z * cslice + (size_t)p * dim)[c];
-                    v.x = v.x + u.x;
-                    v.y = v.y + u.y;
-                    v.z = v.z + u.z;
-                    v.w = v.w + u.w;
+                    const float4 w = reinterpret_cast<const float4*>(yg + z * cslice + (size_t)pq * dim)[c];
+                    v[s].x = v[s].x + w.x;
+                    v[s].y = v[s].y + w.y;
+                    v[s].z = v[s].z + w.z;
+                    v[s].w = v[s].w + w.w;
                 }
                 if (bdown) {
-                    const float4 b =
-                        reinterpret_cast<const float4*>(bdown + (size_t)topi[(size_t)t * K + order[s]] * dim)[c];
-                    v.x = v.x + b.x;
-                    v.y = v.y + b.y;
-                    v.z = v.z + b.z;
-                    v.w = v.w + b.w;
+                    const float4 b = reinterpret_cast<const float4*>(bdown + (size_t)eq * dim)[c];
+                    v[s].x = v[s].x + b.x;
+                    v[s].y = v[s].y + b.y;
+                    v[s].z = v[s].z + b.z;
+                    v[s].w = v[s].w + b.w;
                 }
-                const float wgt = perm_w[p];  // weighted = exOut * w
-                v.x = v.x * wgt;
-                v.y = v.y * wgt;
-                v.z = v.z * wgt;
-                v.w = v.w * wgt;
+                const float wgt = perm_w[pq];  // weighted = exOut * w
+                v[s].x = v[s].x * wgt;
+                v[s].y = v[s].y * wgt;
+                v[s].z = v[s].z * wgt;
+                v[s].w = v[s].w * wgt;
             }
-            acc.x = acc.x + v.x;
-            acc.y = acc.y + v.y;
-            acc.z = acc.z + v.z;
-            acc.w = acc.w + v.w;
         }
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int s = 0; s < KT; s++)
+            if (s < K) {
+                acc.x = acc.x + v[s].x;
+                acc.y = acc.y + v[s].y;
+                acc.z = acc.z + v[s].z;
+                acc.w = acc.w + v[s].w;
+            }
         reinterpret_cast<float4*>(out)[i] = acc;
     }
 }
@@ -662,7 +694,8 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
     const int E = w->experts, K = w->top_k, d = w->dim, F = w->ffn;
     GH_REQUIRE(K >= 1 && K <= E, "gorch/nn: MoE numExpertsPerToken out of range");
     GH_REQUIRE(E <= kMaxExperts && K <= kMaxTopK, "gorch_hip_moe_forward: at most 64 experts and top-8");
-    GH_REQUIRE((long long)M * E < (1ll << 29), "gorch_hip_moe_forward: M * experts must be below 2^29");
+    GH_REQUIRE((long long)M * E < (1ll << 29) && (long long)M * K * d < (1ll << 29),
+               "gorch_hip_moe_forward: M * experts and M * top_k * dim must be below 2^29");
     GH_REQUIRE(d % 8 == 0 && F % 8 == 0, "gorch_hip_moe_forward: dim and ffn must be multiples of 8");
     GH_REQUIRE(w->wgate && w->wup && w->wdown, "gorch_hip_moe_forward: null expert weights");
     GH_REQUIRE(logits || w->wr, "gorch_hip_moe_forward: need router weights or injected logits");
@@ -741,8 +774,12 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
         GH_TRY(check_launch("moe_gemm_down"));
     }
     const int cblocks = (int)std::min<int64_t>(8192, ((int64_t)M * d / 4 + 255) / 256);
-    hipLaunchKernelGGL(k_moe_combine, dim3(cblocks), dim3(256), 0, s, ws.yg, ws.inv, ws.topi, out, M, K, d, nsl,
-                       cslice, w->bdown, ws.perm_w);
+if (K <= 2)
+        hipLaunchKernelGGL(k_moe_combine<2>, dim3(cblocks), dim3(256), 0, s, ws.yg, ws.inv, ws.topi, out, M, K, d, nsl,
+                           cslice, w->bdown, ws.perm_w);
+    else
+        hipLaunchKernelGGL(k_moe_combine<kMaxTopK>, dim3(cblocks), dim3(256), 0, s, ws.yg, ws.inv, ws.topi, out, M, K, d, nsl,
+                           cslice, w->bdown, ws.perm_w);
     GH_TRY(check_launch("moe_combine"));
     count(CNT_MOE);
     return finish(stream, GORCH_HIP_OK);

@@ -325,7 +325,8 @@ size_t gorch_hip_moe_workspace_size(int M, int dim, int ffn, int experts, int to
  * nullable) receive the chosen experts [M, top_k] (descending logit, ties
  * to the lower index) and their softmax weights. The workspace is the
  * caller's (no allocation inside; the call is graph-capturable). Top-k is
- * limited to 8 and experts to 64. */
+ * limited to 8, experts to 64, and M * experts and M * top_k * dim to
+ * below 2^29 (32-bit buffer offsets). */
 int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* w, const float* x, int M,
                           const float* logits, float* out, int* topk_idx, float* topk_w,
                           void* workspace, size_t workspace_bytes);
