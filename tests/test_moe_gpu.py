@@ -43,7 +43,8 @@ def with_biases(w, seed):
 
 @pytest.mark.parametrize("M,dim,ffn,E,K", [(40, 32, 64, 4, 2), (300, 64, 128, 8, 2), (97, 128, 96, 6, 3),
                                            (5, 32, 32, 8, 8), (2500, 32, 64, 64, 8), (1025, 32, 32, 3, 1),
-                                           (4200, 32, 32, 4, 2)])
+                                           (4200, 32, 32, 4, 2), (300, 32, 64, 12, 3), (200, 32, 64, 16, 2),
+                                           (150, 32, 32, 33, 5)])
 def test_moe_vs_oracle(gpu, M, dim, ffn, E, K):
     x, logits, w = syn.moe_inputs(M=M, dim=dim, ffn=ffn, experts=E, top_k=K, seed=M + E)
     w = with_biases(w, M)
