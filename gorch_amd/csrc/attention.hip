@@ -268,16 +268,19 @@ __global__ __launch_bounds__(NW * 64) void k_attn_rows(AttnArgs a) {
     constexpr int WPASS = (kWoRows + WRP - 1) / WRP;
     const int cc = threadIdx.x % WCH, rr = threadIdx.x / WCH;
     u32x4 wov[WO ? WPASS : 1];
+    float wob[WO ? WPASS : 1];  // head 0's bias values, loaded with Wo (no load in the epilogue)
     if constexpr (WO) {
         const int n0 = blockIdx.y * kWoRows;
         const int nrows = max(0, min(kWoRows, a.dim - n0));
         const __amdgpu_buffer_rsrc_t rw =
             make_rsrc(a.wo + (size_t)n0 * a.dim + h * (4 * HD4), nrows > 0 ? ((long long)(nrows - 1) * a.dim + 4 * HD4) * 2 : 0);
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.wo_bias + n0, (h == 0 && a.wo_bias) ? (long long)nrows * 4 : 0);
 #pragma unroll
         for (int q = 0; q < WPASS; q++) {
             const int rl = rr + q * WRP;
             wov[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, rl < nrows ? (rl * a.dim + 8 * cc) * 2 : kOutOfRange, 0,
                                                          kStreamPolicy);
+            wob[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, rl * 4, 0, 0));
         }
     }
     if constexpr (FULL) {
@@ -350,7 +353,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_rows(AttnArgs a) {
                 v = seg_sum<WCH>(v);
                 const int rl = rr + q * WRP, n = n0 + rl;
                 if (cc == 0 && rl < kWoRows && n < a.dim) {
-                    if (h == 0 && a.wo_bias) v = v + a.wo_bias[n];
+                    if (h == 0 && a.wo_bias) v = v + wob[q];
                     __hip_atomic_fetch_add(a.wo_out + n, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
@@ -890,12 +893,15 @@ __global__ __launch_bounds__(256) void k_attn_combine_wo(AttnArgs a, int nc) {
     const int nrows = max(0, min(kCombineWoRows, rows_out - n0));
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.wo + (size_t)n0 * a.dim + h * (4 * HD4),
                                                 nrows > 0 ? ((long long)(nrows - 1) * a.dim + 4 * HD4) * 2 : 0);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.wo_bias + n0, (h == 0 && a.wo_bias) ? (long long)nrows * 4 : 0);
     u32x4 wov[WPASS];
+    float wob[WPASS];  // head 0's bias values, loaded with Wo (no load in the epilogue)
 #pragma unroll
     for (int q = 0; q < WPASS; q++) {
         const int rl = rr + q * WRP;
         wov[q] = __builtin_amdgcn_raw_buffer_load_b128(rw, rl < nrows ? (rl * a.dim + 8 * cc) * 2 : kOutOfRange, 0,
                                                      kStreamPolicy);
+        wob[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, rl * 4, 0, 0));
     }
     const float* rec = a.split_ws + (size_t)h * nc * (4 * HD4 + 2);
     constexpr int NP = (kAttnSplitMax + CPP - 1) / CPP;
@@ -956,7 +962,7 @@ __global__ __launch_bounds__(256) void k_attn_combine_wo(AttnArgs a, int nc) {
         v = seg_sum<WCH>(v);
         const int rl = rr + q * WRP, n = n0 + rl;
         if (cc == 0 && rl < nrows) {
-            if (h == 0 && a.wo_bias) v = v + a.wo_bias[n];
+            if (h == 0 && a.wo_bias) v = v + wob[q];
             __hip_atomic_fetch_add(a.wo_out + n, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
