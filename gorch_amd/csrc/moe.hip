@@ -85,28 +85,25 @@ static size_t moe_layout(int M, int dim, int ffn, int E, int K, char* base, MoeW
 // the reference's > compare) and the routing weights, softmaxRows over the
 // K values: max, exp in f64 rounded to f32, f32 sum, divide. Written to the
 // workspace and, when given, to the caller's arrays.
-template <int EV>
-__global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ logits, int M, int E, int K,
-                                                  int* __restrict__ topi, float* __restrict__ topw,
-                                                  int* __restrict__ topi_out, float* __restrict__ topw_out) {
-    const int tok = blockIdx.x * blockDim.x + threadIdx.x;
-    if (tok >= M) return;
-    // the token's EV >= E logits in registers, every load in flight at once:
-    // raw buffer loads through one resource over the whole [M, E] table
-    // (slots past E read the next row or, past the table, zeros, and are
-    // never selected; a load under a branch would be waited on before the
-    // next one, one round trip per expert). M * E < 2^29 (host check).
-    const __amdgpu_buffer_rsrc_t rl = make_rsrc(logits, (long long)M * E * 4);
+// The top-K of one token (EV >= E logits, KT >= K slots): the logits come
+// through raw buffer loads over the whole [M, E] table, all in flight at
+// once (slots past E read the next row or, past the table, zeros, and are
+// never selected; a load under a branch would be waited on before the
+// next one, one round trip per expert). M * E < 2^29 (host check).
+template <int EV, int KT>
+__device__ __forceinline__ void moe_topk_token(__amdgpu_buffer_rsrc_t rl, int tok, int E, int K, int (&idx)[KT],
+                                               float (&wgt)[KT]) {
     float lv[EV];
 #pragma unroll
     for (int j = 0; j < EV; j++)
         lv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rl, (tok * E + j) * 4, 0, 0));
-    int idx[kMaxTopK];
-    float val[kMaxTopK];
+    float val[KT];
     unsigned long long taken = 0ull;
 #pragma unroll
-    for (int s = 0; s < kMaxTopK; s++) {
-        if (s >= K) break;
+    for (int s = 0; s < KT; s++) {
+        idx[s] = -1;
+        val[s] = 0.f;
+        if (s >= K) continue;
         int best = -1;
         float bv = 0.f;
 #pragma unroll
@@ -123,25 +120,39 @@ __global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ logi
     }
     float mx = val[0];
 #pragma unroll
-    for (int s = 1; s < kMaxTopK; s++)
+    for (int s = 1; s < KT; s++)
         if (s < K) mx = val[s] > mx ? val[s] : mx;
-    float e_[kMaxTopK];
+    float e_[KT];
     float sum = 0.f;
 #pragma unroll
-    for (int s = 0; s < kMaxTopK; s++)
+    for (int s = 0; s < KT; s++) {
+        e_[s] = 0.f;
         if (s < K) {
             e_[s] = (float)exp((double)(val[s] - mx));
             sum += e_[s];
         }
+    }
+#pragma unroll
+    for (int s = 0; s < KT; s++) wgt[s] = s < K ? e_[s] / sum : 0.f;
+}
+
+template <int EV>
+__global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ logits, int M, int E, int K,
+                                                  int* __restrict__ topi, float* __restrict__ topw,
+                                                  int* __restrict__ topi_out, float* __restrict__ topw_out) {
+    const int tok = blockIdx.x * blockDim.x + threadIdx.x;
+    if (tok >= M) return;
+    int idx[kMaxTopK];
+    float wgt[kMaxTopK];
+    moe_topk_token<EV, kMaxTopK>(make_rsrc(logits, (long long)M * E * 4), tok, E, K, idx, wgt);
 #pragma unroll
     for (int s = 0; s < kMaxTopK; s++)
         if (s < K) {
             const size_t a = (size_t)tok * K + s;
-            const float wgt = e_[s] / sum;
             topi[a] = idx[s];
-            topw[a] = wgt;
+            topw[a] = wgt[s];
             if (topi_out) topi_out[a] = idx[s];
-            if (topw_out) topw_out[a] = wgt;
+            if (topw_out) topw_out[a] = wgt[s];
         }
 }
 
@@ -153,8 +164,12 @@ __global__ __launch_bounds__(256) void k_moe_topk(const float* __restrict__ logi
 // are parked in inv; once every expert's size is known the bases, the GEMM
 // tile table (one thread per expert) and the packed-row maps follow.
 constexpr int kRouteThreads = 1024, kRouteWaves = kRouteThreads / 64;
-template <int KT>
-__global__ __launch_bounds__(kRouteThreads) void k_moe_route(int M, int E, int K, int tile_rows, MoeWs ws) {
+// EV > 0: the block takes each token's top-K itself (moe_topk_token, E <=
+// EV) and writes the tables and the caller's arrays as k_moe_topk does.
+template <int KT, int EV = 0>
+__global__ __launch_bounds__(kRouteThreads) void k_moe_route(int M, int E, int K, int tile_rows, MoeWs ws,
+                                                             const float* __restrict__ logits, int* topi_out,
+                                                             float* topw_out) {
     __shared__ int wtot[kRouteWaves][kMaxExperts];
     __shared__ int run[kMaxExperts];
     __shared__ int base[kMaxExperts + 1];
@@ -175,11 +190,26 @@ __global__ __launch_bounds__(kRouteThreads) void k_moe_route(int M, int E, int K
         const int tok = r0 + t;
         const bool live = tok < M;
         int idx[KT];
-#pragma unroll
-        for (int s = 0; s < KT; s++) idx[s] = (live && s < K) ? ws.topi[(size_t)tok * K + s] : -1;
         float wv[KT];
+        if constexpr (EV > 0) {
+            moe_topk_token<EV, KT>(make_rsrc(logits, (long long)M * E * 4), live ? tok : 0, E, K, idx, wv);
 #pragma unroll
-        for (int s = 0; s < KT; s++) wv[s] = (regs && live && s < K) ? ws.topw[(size_t)tok * K + s] : 0.f;
+            for (int s = 0; s < KT; s++) {
+                if (!live) idx[s] = -1;
+                if (live && s < K) {
+                    const size_t a = (size_t)tok * K + s;
+                    ws.topi[a] = idx[s];
+                    ws.topw[a] = wv[s];
+                    if (topi_out) topi_out[a] = idx[s];
+                    if (topw_out) topw_out[a] = wv[s];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < KT; s++) idx[s] = (live && s < K) ? ws.topi[(size_t)tok * K + s] : -1;
+#pragma unroll
+            for (int s = 0; s < KT; s++) wv[s] = (regs && live && s < K) ? ws.topw[(size_t)tok * K + s] : 0.f;
+        }
         // this round's per-wave counts and lane prefixes, expert by expert
         int pre[KT];
 #pragma unroll
@@ -710,23 +740,40 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
         GH_TRY(launch_linear_bf16(s, x, w->wr, w->br, nullptr, ws.logits, M, E, d, GORCH_HIP_EPI_NONE));
         lg = ws.logits;
     }
-    const dim3 tgrid((M + 255) / 256);
-    if (E <= 8)
-        hipLaunchKernelGGL(k_moe_topk<8>, tgrid, dim3(256), 0, s, lg, M, E, K, ws.topi, ws.topw, topk_idx, topk_w);
-    else if (E <= 16)
-        hipLaunchKernelGGL(k_moe_topk<16>, tgrid, dim3(256), 0, s, lg, M, E, K, ws.topi, ws.topw, topk_idx, topk_w);
-    else
-        hipLaunchKernelGGL(k_moe_topk<kMaxExperts>, tgrid, dim3(256), 0, s, lg, M, E, K, ws.topi, ws.topw, topk_idx,
-                           topk_w);
-    GH_TRY(check_launch("moe_topk"));
     static const bool wide = [] {
         const char* e = getenv("GORCH_HIP_MOE_WIDE");
         return !e || atoi(e) != 0;
     }();
     const int tile_rows = wide ? kWideBM : kMoeBM;
-    // top-K slots sized to K (every absent slot still costs its compares)
-    if (K <= 2) hipLaunchKernelGGL(k_moe_route<2>, dim3(1), dim3(kRouteThreads), 0, s, M, E, K, tile_rows, ws);
-    else hipLaunchKernelGGL(k_moe_route<kMaxTopK>, dim3(1), dim3(kRouteThreads), 0, s, M, E, K, tile_rows, ws);
+    // top-K slots sized to K (every absent slot still costs its compares).
+    // Up to two slots, 8 experts and 4096 tokens: the routing block takes
+    // the top-K itself (one launch fewer; GORCH_HIP_MOE_FUSE_TOPK=0 keeps
+    // k_moe_topk)
+    static const bool fuse_topk = [] {
+        const char* e = getenv("GORCH_HIP_MOE_FUSE_TOPK");
+        return !e || atoi(e) != 0;
+    }();
+    if (fuse_topk && K <= 2 && E <= 8 && M <= 4 * kRouteThreads) {
+        hipLaunchKernelGGL((k_moe_route<2, 8>), dim3(1), dim3(kRouteThreads), 0, s, M, E, K, tile_rows, ws, lg,
+                           topk_idx, topk_w);
+    } else {
+        const dim3 tgrid((M + 255) / 256);
+        if (E <= 8)
+            hipLaunchKernelGGL(k_moe_topk<8>, tgrid, dim3(256), 0, s, lg, M, E, K, ws.topi, ws.topw, topk_idx, topk_w);
+        else if (E <= 16)
+            hipLaunchKernelGGL(k_moe_topk<16>, tgrid, dim3(256), 0, s, lg, M, E, K, ws.topi, ws.topw, topk_idx,
+                               topk_w);
+        else
+            hipLaunchKernelGGL(k_moe_topk<kMaxExperts>, tgrid, dim3(256), 0, s, lg, M, E, K, ws.topi, ws.topw,
+                               topk_idx, topk_w);
+        GH_TRY(check_launch("moe_topk"));
+        if (K <= 2)
+            hipLaunchKernelGGL((k_moe_route<2>), dim3(1), dim3(kRouteThreads), 0, s, M, E, K, tile_rows, ws, nullptr,
+                               nullptr, nullptr);
+        else
+            hipLaunchKernelGGL((k_moe_route<kMaxTopK>), dim3(1), dim3(kRouteThreads), 0, s, M, E, K, tile_rows, ws,
+                               nullptr, nullptr, nullptr);
+    }
     GH_TRY(check_launch("moe_route"));
     const int MK = M * K;
     const int max_tiles = MK / tile_rows + E + 1;
