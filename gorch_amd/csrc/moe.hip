@@ -171,6 +171,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_moe_route(int M, int E, int K
                                                              const float* __restrict__ logits, int* topi_out,
                                                              float* topw_out) {
     __shared__ int wtot[kRouteWaves][kMaxExperts];
+    __shared__ int wpre[kRouteWaves][kMaxExperts];
     __shared__ int run[kMaxExperts];
     __shared__ int base[kMaxExperts + 1];
     __shared__ int tbase[kMaxExperts + 1];
@@ -226,13 +227,23 @@ __global__ __launch_bounds__(kRouteThreads) void k_moe_route(int M, int E, int K
                 if (idx[s] == e) pre[s] = lp;
         }
         __syncthreads();
+        // per expert: the ranks lower waves of this round take (after the
+        // earlier rounds' run), and the run advanced past this round
+        if (t < E) {
+            int acc = run[t];
+            for (int w = 0; w < kRouteWaves; w++) {
+                wpre[w][t] = acc;
+                acc += wtot[w][t];
+            }
+            run[t] = acc;
+        }
+        __syncthreads();
         if (live)
 #pragma unroll
             for (int s = 0; s < KT; s++) {
                 if (s >= K) break;
                 const int e = idx[s];
-                int rank = run[e] + pre[s];
-                for (int w = 0; w < wave; w++) rank += wtot[w][e];
+                const int rank = wpre[wave][e] + pre[s];
                 if (regs) {
 #pragma unroll
                     for (int q = 0; q < RR; q++)
@@ -245,11 +256,8 @@ __global__ __launch_bounds__(kRouteThreads) void k_moe_route(int M, int E, int K
                     ws.inv[(size_t)tok * K + s] = rank;  // rank inside expert e for now
                 }
             }
-        __syncthreads();
-        if (t < E)
-            for (int w = 0; w < kRouteWaves; w++) run[t] += wtot[w][t];
-        __syncthreads();
     }
+    __syncthreads();
     if (t == 0) {
         int b = 0, nt = 0;
         for (int e = 0; e < E; e++) {
