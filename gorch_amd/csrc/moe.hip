@@ -584,8 +584,10 @@ __global__ void k_moe_gather_split(const float* __restrict__ x, const int* __res
 // straight from the accumulators.
 template <bool DUAL, int BNW>
 struct MoeStage {
-    static constexpr int LDH = BNW + 8, LDC = BNW + 4;  // padded rows: conflict-free element writes
-    static constexpr size_t kBytes = DUAL ? (size_t)2 * kWideBM * LDH * 2 : (size_t)kWideBM * LDC * 4;
+    // padded rows: conflict-free element writes. DUAL: one u32 per element,
+    // hi in the high half and lo in the low half
+    static constexpr int LDH = BNW + 4, LDC = BNW + 4;
+    static constexpr size_t kBytes = DUAL ? (size_t)kWideBM * LDH * 4 : (size_t)kWideBM * LDC * 4;
 };
 
 template <bool DUAL, int BNW, bool IL = false, int WGM = 2, int PD = 2, bool STG = false>
@@ -643,15 +645,14 @@ __global__ __launch_bounds__(WGM * 256) void k_moe_wide(const uint16_t* __restri
         }
     };
     using ST = MoeStage<DUAL, BNW>;
-    uint16_t* hs = reinterpret_cast<uint16_t*>(moe_smem);  // STG, DUAL: [2][kWideBM][LDH] hi, lo
+    uint32_t* hs = reinterpret_cast<uint32_t*>(moe_smem);  // STG, DUAL: [kWideBM][LDH] (hi << 16 | lo)
     float* cs = reinterpret_cast<float*>(moe_smem);        // STG, else: [kWideBM][LDC]
     auto store = [&](int row, int col, const float* v) {
         if constexpr (STG) {
             if constexpr (DUAL) {
                 const uint32_t hb = __float_as_uint(v[0]) & 0xffff0000u;
-                hs[row * ST::LDH + col] = (uint16_t)(hb >> 16);
-                hs[(kWideBM + row) * ST::LDH + col] =
-                    __builtin_bit_cast(uint16_t, (__bf16)(v[0] - __uint_as_float(hb)));
+                hs[row * ST::LDH + col] =
+                    hb | __builtin_bit_cast(uint16_t, (__bf16)(v[0] - __uint_as_float(hb)));
             } else {
                 cs[row * ST::LDC + col] = v[0];
             }
@@ -672,12 +673,26 @@ __global__ __launch_bounds__(WGM * 256) void k_moe_wide(const uint16_t* __restri
         __syncthreads();
         // N % 8 == 0 and n0 % BNW == 0: every chunk is whole and 16-byte aligned
         if constexpr (DUAL) {
-            constexpr int CPR = BNW / 8, CHUNKS = 2 * kWideBM * CPR;
+            // 8 columns per chunk: 32 bytes of (hi, lo) pairs -> 16 bytes of each plane
+            constexpr int CPR = BNW / 8, CHUNKS = kWideBM * CPR;
             for (int c = threadIdx.x; c < CHUNKS; c += G::kThreads) {
-                const int p = c / (kWideBM * CPR), rem = c % (kWideBM * CPR), row = rem / CPR, ch = rem % CPR;
-                if (row < nrows && 8 * ch < ncols)
-                    *reinterpret_cast<uint4*>((p ? Clo : Chi) + (size_t)(r0 + row) * N + n0 + 8 * ch) =
-                        *reinterpret_cast<const uint4*>(hs + (p * kWideBM + row) * ST::LDH + 8 * ch);
+                const int row = c / CPR, ch = c % CPR;
+                if (row < nrows && 8 * ch < ncols) {
+                    const uint4 u0 = *reinterpret_cast<const uint4*>(hs + row * ST::LDH + 8 * ch);
+                    const uint4 u1 = *reinterpret_cast<const uint4*>(hs + row * ST::LDH + 8 * ch + 4);
+                    const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+                    uint4 hv, lv;
+                    uint32_t* hp = reinterpret_cast<uint32_t*>(&hv);
+                    uint32_t* lp = reinterpret_cast<uint32_t*>(&lv);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        hp[q] = (w[2 * q] >> 16) | (w[2 * q + 1] & 0xffff0000u);
+                        lp[q] = (w[2 * q] & 0xffffu) | (w[2 * q + 1] << 16);
+                    }
+                    const size_t o = (size_t)(r0 + row) * N + n0 + 8 * ch;
+                    *reinterpret_cast<uint4*>(Chi + o) = hv;
+                    *reinterpret_cast<uint4*>(Clo + o) = lv;
+                }
             }
         } else {
             constexpr int CPR = BNW / 4, CHUNKS = kWideBM * CPR;
