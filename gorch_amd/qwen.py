@@ -5,7 +5,7 @@ library's kernels through its C-ABI (gorch_amd.hip): the embedding gather,
 one gorch_hip_qwen_block_forward_cached call per block (RMSNorm, Q/K/V as one
 weight stream, per-head q/k RMSNorm + RoPE into the cache, grouped-query
 cached attention, Wo + residual, RMSNorm, gate/up as one weight, SwiGLU, down
-+ residual: six launches for a one-token step), the final RMSNorm and the tied
++ residual: five launches for a one-token step), the final RMSNorm and the tied
 head. Every launch goes on torch's current stream, so a decode step can be
 captured in a CUDA graph and replayed.
 
