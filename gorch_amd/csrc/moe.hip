@@ -558,19 +558,32 @@ __global__ __launch_bounds__(256) void k_moe_gemm(const float* __restrict__ A, c
 // from beyond L2, not by the number of busy CUs.
 constexpr int kWideBM = 128, kWideBNDual = 128, kWideBNDown = 256;
 
-__global__ void k_moe_gather_split(const float* __restrict__ x, const int* __restrict__ perm_tok, uint16_t* hi,
-                                   uint16_t* lo, int rows, int dim) {
+// Token-major: item (t, chunk c) loads x's chunk and the token's K packed
+// rows (inv) together — no load waits on another — splits once and stores
+// the planes at each of the K rows.
+template <int KT>
+__global__ void k_moe_gather_split(const float* __restrict__ x, const int* __restrict__ inv, uint16_t* hi,
+                                   uint16_t* lo, int M, int K, int dim) {
     const int d8 = dim / 8;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)rows * d8;
+    const __amdgpu_buffer_rsrc_t ri = make_rsrc(inv, (long long)M * K * 4);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)M * d8;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int p = (int)(i / d8), c = (int)(i - (int64_t)p * d8);
-        const float4* src = reinterpret_cast<const float4*>(x + (size_t)perm_tok[p] * dim + 8 * c);
+        const int t = (int)(i / d8), c = (int)(i - (int64_t)t * d8);
+        int p[KT];
+#pragma unroll
+        for (int s = 0; s < KT; s++)
+            p[s] = (int)__builtin_amdgcn_raw_buffer_load_b32(ri, s < K ? (t * K + s) * 4 : kOutOfRange, 0, 0);
+        const float4* src = reinterpret_cast<const float4*>(x + (size_t)t * dim + 8 * c);
         const float4 u = src[0], v = src[1];
         const float f[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
         bf16x8 h, l;
         split_hi_lo(f, h, l);
-        *reinterpret_cast<bf16x8*>(hi + (size_t)p * dim + 8 * c) = h;
-        *reinterpret_cast<bf16x8*>(lo + (size_t)p * dim + 8 * c) = l;
+#pragma unroll
+        for (int s = 0; s < KT; s++)
+            if (s < K) {
+                *reinterpret_cast<bf16x8*>(hi + (size_t)p[s] * dim + 8 * c) = h;
+                *reinterpret_cast<bf16x8*>(lo + (size_t)p[s] * dim + 8 * c) = l;
+            }
     }
 }
 
@@ -867,8 +880,12 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
         uint16_t* xlo = xhi + (size_t)MK * d;
         uint16_t* hhi = reinterpret_cast<uint16_t*>(ws.h);
         uint16_t* hlo = hhi + (size_t)MK * F;
-        const int gblocks = (int)std::min<int64_t>(8192, ((int64_t)MK * d / 8 + 255) / 256);
-        hipLaunchKernelGGL(k_moe_gather_split, dim3(gblocks), dim3(256), 0, s, x, ws.perm_tok, xhi, xlo, MK, d);
+        const int gblocks = (int)std::min<int64_t>(8192, ((int64_t)M * d / 8 + 255) / 256);
+        if (K <= 2)
+            hipLaunchKernelGGL(k_moe_gather_split<2>, dim3(gblocks), dim3(256), 0, s, x, ws.inv, xhi, xlo, M, K, d);
+        else
+            hipLaunchKernelGGL(k_moe_gather_split<kMaxTopK>, dim3(gblocks), dim3(256), 0, s, x, ws.inv, xhi, xlo, M,
+                               K, d);
         GH_TRY(check_launch("moe_gather"));
         GH_TRY((launch_moe_wide<true, kWideBNDual>(s, dim3((F + kWideBNDual - 1) / kWideBNDual, max_tiles), xhi,
                                                   xlo, w->wgate, w->wup, w->bgate, w->bup, nullptr, hhi, hlo, F, d,
