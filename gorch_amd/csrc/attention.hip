@@ -567,12 +567,51 @@ __global__ __launch_bounds__(NW * 64) void k_attn_flash(AttnArgs a) {
 // copies summed, then divided back out, which is exact), y = x * inv * g,
 // then each pair rotated without contraction, the Llama partner element
 // taken from lane c +- HD4 / 2 of the same segment.
+// The values head_norm_rope reads besides the row: the gain's 4 elements
+// and the RoPE cos / sin of this lane's pairs, loaded together through raw
+// buffer resources (absent gain or tables read zeros, unused) so that no
+// load waits on another — q and k share the tables.
 template <int HD4>
-__device__ __forceinline__ float4 head_norm_rope(float4 v, const float* gain, int p, const AttnArgs& a, int c) {
-#pragma clang fp contract(off)
+struct HeadNormRopeIn {
+    float4 gq, gk;
+    float co[4], si[4];
+};
+template <int HD4>
+__device__ __forceinline__ HeadNormRopeIn<HD4> head_norm_rope_load(int p, const AttnArgs& a, int c) {
     constexpr int hd = 4 * HD4, half = hd / 2;
-    if (gain) {
-        const float4 gv = *reinterpret_cast<const float4*>(gain + 4 * c);
+    HeadNormRopeIn<HD4> in;
+    auto ld4 = [](__amdgpu_buffer_rsrc_t r, int off) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                           __uint_as_float(v[3]));
+    };
+    in.gq = ld4(make_rsrc(a.q_gain, a.q_gain ? (long long)hd * 4 : 0), 16 * c);
+    in.gk = ld4(make_rsrc(a.k_gain, a.k_gain ? (long long)hd * 4 : 0), 16 * c);
+    const long long tb = a.rope_cos ? (long long)(p + 1) * half * 4 : 0;
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.rope_cos, tb), rs = make_rsrc(a.rope_sin, tb);
+    const bool lo = c < HD4 / 2;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int cs;
+        if (a.rope_neox) {
+            cs = p * half + min(2 * c + q / 2, half - 1);  // pair q / 2 of the lane
+        } else {
+            const int k = 4 * c + q;
+            const int i = lo ? k : k - half;
+            cs = p * half + min(max(i, 0), half - 1);
+        }
+        in.co[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rc, cs * 4, 0, 0));
+        in.si[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, cs * 4, 0, 0));
+    }
+    return in;
+}
+
+template <int HD4>
+__device__ __forceinline__ float4 head_norm_rope(float4 v, bool norm, float4 gv, const HeadNormRopeIn<HD4>& in,
+                                                 const AttnArgs& a, int c) {
+#pragma clang fp contract(off)
+    constexpr int hd = 4 * HD4;
+    if (norm) {
         double s = ((double)v.x * (double)v.x + (double)v.y * (double)v.y) +
                    ((double)v.z * (double)v.z + (double)v.w * (double)v.w);
         s = wave_sum_d(s) / (double)(64 / HD4);
@@ -585,9 +624,7 @@ __device__ __forceinline__ float4 head_norm_rope(float4 v, const float* gain, in
     if (a.rope_neox) {
 #pragma unroll
         for (int q = 0; q < 2; q++) {
-            const int i = 2 * c + q;
-            const int cs = p * half + min(i, half - 1);
-            const float co = a.rope_cos[cs], si = a.rope_sin[cs];
+            const float co = in.co[2 * q], si = in.si[2 * q];
             o[2 * q] = e[2 * q] * co - e[2 * q + 1] * si;
             o[2 * q + 1] = e[2 * q] * si + e[2 * q + 1] * co;
         }
@@ -600,10 +637,7 @@ __device__ __forceinline__ float4 head_norm_rope(float4 v, const float* gain, in
         for (int q = 0; q < 4; q++) pe[q] = __shfl(e[q], src);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int k = 4 * c + q;
-            const int i = lo ? k : k - half;
-            const int cs = p * half + min(max(i, 0), half - 1);
-            const float co = a.rope_cos[cs], si = a.rope_sin[cs];
+            const float co = in.co[q], si = in.si[q];
             o[q] = lo ? e[q] * co - pe[q] * si : pe[q] * si + e[q] * co;
         }
     }
@@ -681,9 +715,10 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
     float4 q = *reinterpret_cast<const float4*>(a.q + (size_t)row * a.q_stride + h * (4 * HD4) + 4 * c);
     float4 knew = make_float4(0.f, 0.f, 0.f, 0.f);
     if constexpr (QK) {
-        q = head_norm_rope<HD4>(q, a.q_gain, pos + i, a, c);
         const float4 kr = *reinterpret_cast<const float4*>(a.k_raw + (size_t)kvh * (4 * HD4) + 4 * c);
-        knew = head_norm_rope<HD4>(kr, a.k_gain, pos + i, a, c);
+        const HeadNormRopeIn<HD4> in = head_norm_rope_load<HD4>(pos + i, a, c);
+        q = head_norm_rope<HD4>(q, a.q_gain != nullptr, in.gq, in, a, c);
+        knew = head_norm_rope<HD4>(kr, a.k_gain != nullptr, in.gk, in, a, c);
         const int group = a.kv_heads ? (int)gridDim.x / a.kv_heads : 1;
         if (h % group == 0 && jb <= T - 1 && T - 1 < je && threadIdx.x < HD4)
             *reinterpret_cast<float4*>(const_cast<float*>(a.kc) + base + (size_t)(T - 1) * kvd + 4 * c) = knew;
