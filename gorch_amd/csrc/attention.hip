@@ -714,15 +714,6 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
     };
     float4 q = *reinterpret_cast<const float4*>(a.q + (size_t)row * a.q_stride + h * (4 * HD4) + 4 * c);
     float4 knew = make_float4(0.f, 0.f, 0.f, 0.f);
-    if constexpr (QK) {
-        const float4 kr = *reinterpret_cast<const float4*>(a.k_raw + (size_t)kvh * (4 * HD4) + 4 * c);
-        const HeadNormRopeIn<HD4> in = head_norm_rope_load<HD4>(pos + i, a, c);
-        q = head_norm_rope<HD4>(q, a.q_gain != nullptr, in.gq, in, a, c);
-        knew = head_norm_rope<HD4>(kr, a.k_gain != nullptr, in.gk, in, a, c);
-        const int group = a.kv_heads ? (int)gridDim.x / a.kv_heads : 1;
-        if (h % group == 0 && jb <= T - 1 && T - 1 < je && threadIdx.x < HD4)
-            *reinterpret_cast<float4*>(const_cast<float*>(a.kc) + base + (size_t)(T - 1) * kvd + 4 * c) = knew;
-    }
     // keys past T lie outside the resources and read as zeros
     auto load = [&](int j0, float4 (&kk)[UNR], float4 (&vv)[UNR]) {
 #pragma unroll
@@ -732,6 +723,23 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
             vv[u] = ld4(rv, off);
         }
     };
+    float4 ka[UNR], va[UNR], kb[UNR], vb[UNR];
+    if constexpr (QK) {
+        const float4 kr = *reinterpret_cast<const float4*>(a.k_raw + (size_t)kvh * (4 * HD4) + 4 * c);
+        const HeadNormRopeIn<HD4> in = head_norm_rope_load<HD4>(pos + i, a, c);
+        // the first two chunks' keys and values go out behind the epilogue's
+        // loads and arrive while it computes (the new key's stale cache row
+        // is replaced by knew in step; its value row is already written)
+        load(jb, ka, va);
+        __builtin_amdgcn_sched_barrier(0);
+        load(jb + KC, kb, vb);
+        __builtin_amdgcn_sched_barrier(0);
+        q = head_norm_rope<HD4>(q, a.q_gain != nullptr, in.gq, in, a, c);
+        knew = head_norm_rope<HD4>(kr, a.k_gain != nullptr, in.gk, in, a, c);
+        const int group = a.kv_heads ? (int)gridDim.x / a.kv_heads : 1;
+        if (h % group == 0 && jb <= T - 1 && T - 1 < je && threadIdx.x < HD4)
+            *reinterpret_cast<float4*>(const_cast<float*>(a.kc) + base + (size_t)(T - 1) * kvd + 4 * c) = knew;
+    }
     float m = -INFINITY, l = 0.f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     auto step = [&](int j0, const float4 (&kk)[UNR], const float4 (&vv)[UNR]) {
@@ -767,11 +775,12 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
             m = mn;
         }
     };
-    float4 ka[UNR], va[UNR], kb[UNR], vb[UNR];
-    load(jb, ka, va);
-    __builtin_amdgcn_sched_barrier(0);
-    load(jb + KC, kb, vb);
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!QK) {
+        load(jb, ka, va);
+        __builtin_amdgcn_sched_barrier(0);
+        load(jb + KC, kb, vb);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     for (int j0 = jb; j0 < je; j0 += 2 * KC) {
         step(j0, ka, va);
         load(j0 + 2 * KC, ka, va);
