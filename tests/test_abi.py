@@ -43,3 +43,27 @@ def test_error_string_without_gpu():
         rc = hip.lib().gorch_hip_init(0)
         assert rc != 0
         assert hip.last_error()
+
+
+def test_moe_rejects_bad_shapes_without_gpu():
+    # Argument checks come before any device work (nn/moe.go:130-140's
+    # panics become rc 2): top-k above 8, dim not a multiple of 8, and the
+    # 32-bit buffer-offset bound M * top_k * dim < 2^29.
+    import ctypes as C
+
+    ws = hip._MoEWeights()
+    fake = C.c_void_p(0x1000)
+    ws.wgate = ws.wup = ws.wdown = fake
+    ws.wr = fake
+    x = out = C.c_void_p(0x2000)
+    L = hip.lib()
+
+    def call(dim, ffn, experts, top_k, M):
+        ws.dim, ws.ffn, ws.experts, ws.top_k = dim, ffn, experts, top_k
+        return L.gorch_hip_moe_forward(None, C.byref(ws), x, M, None, out, None, None, fake, 1 << 40)
+
+    assert call(64, 64, 16, 9, 8) == 2
+    assert call(60, 64, 8, 2, 8) == 2
+    assert call(1024, 64, 8, 2, 1 << 18) == 2
+    assert "2^29" in hip.last_error()
+    assert hip.lib().gorch_hip_moe_workspace_size(8, 64, 64, 8, 0) == 0
