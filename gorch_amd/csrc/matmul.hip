@@ -19,21 +19,6 @@ int launch_gemm_bf16w(hipStream_t s, const float* A, const uint16_t* W, const fl
                       const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
                       bool act_bf16);
 
-// One element of an operand as bf16 terms: bf16 storage is one exact term;
-// f32 is hi (the value truncated to bf16, exact in f32) + lo (the remainder
-// rounded to bf16), x = hi + lo to ~2^-16 relative.
-__device__ __forceinline__ void op_terms(const void* p, size_t i, bool bf16, uint16_t& hi, uint16_t& lo) {
-    if (bf16) {
-        hi = reinterpret_cast<const uint16_t*>(p)[i];
-        lo = 0;
-        return;
-    }
-    const float v = reinterpret_cast<const float*>(p)[i];
-    const uint32_t u = __float_as_uint(v) & 0xffff0000u;
-    hi = (uint16_t)(u >> 16);
-    lo = __builtin_bit_cast(uint16_t, (__bf16)(v - __uint_as_float(u)));
-}
-
 // C[b] = opA(A[b]) @ opB(B[b]) on the matrix cores for every transpose /
 // dtype combination of metal_mps_matmul_dt (one launch for the whole batch,
 // blockIdx.z = batch entry). Block tile 64 x 64, K stepped by 32; each
@@ -42,7 +27,9 @@ __device__ __forceinline__ void op_terms(const void* p, size_t i, bool bf16, uin
 // f32 one), then 4 waves (2 x 2, 32 x 32 each) run v_mfma_f32_16x16x32_bf16
 // over the term products that matter (lo x lo, below f32 rounding, is left
 // out), accumulating in f32. Not a hot path of the decode step: the gather
-// is per element with bounds checks.
+// is per element (bf16 storage is one exact term; f32 is hi, the value
+// truncated to bf16, plus lo, the remainder rounded to bf16: x = hi + lo to
+// ~2^-16 relative).
 constexpr int kMmBK = 32, kMmLD = kMmBK + 8;  // LDS row: 40 bf16 (80 bytes)
 
 template <int NTA, int NTB>
@@ -60,21 +47,50 @@ __global__ __launch_bounds__(256) void k_matmul_mfma(const void* __restrict__ A,
     for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // one raw buffer resource per operand over this batch entry (< 2 GiB,
+    // host check): elements outside the matrix get an out-of-range offset and
+    // read as zero, so all 16 of a thread's element loads go out together (a
+    // load under a bounds branch waits for the one before it)
+    constexpr int EA = NTA == 1 ? 2 : 4, EB = NTB == 1 ? 2 : 4;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(reinterpret_cast<const char*>(A) + bA * EA, (long long)M * K * EA);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(reinterpret_cast<const char*>(B) + bB * EB, (long long)K * N * EB);
+    auto ld = [](__amdgpu_buffer_rsrc_t rs, int off, bool half) -> uint32_t {
+        return half ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0)
+                    : __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+    };
+    auto terms = [](uint32_t bits, bool half, uint16_t& h, uint16_t& l) {
+        if (half) {
+            h = (uint16_t)bits;
+            l = 0;
+            return;
+        }
+        const float v = __uint_as_float(bits);
+        const uint32_t u = bits & 0xffff0000u;
+        h = (uint16_t)(u >> 16);
+        l = __builtin_bit_cast(uint16_t, (__bf16)(v - __uint_as_float(u)));
+    };
     for (int k0 = 0; k0 < K; k0 += kMmBK) {
         // 64 x 32 elements per operand, 8 per thread: thread t takes row
         // t / 4 (of the tile) and k 8 * (t % 4) .. +8, each element read
         // through the operand's stored layout
+        const int row = tid >> 2, m = m0 + row, n = n0 + row;
+        uint32_t av[8], bv[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const int row = tid >> 2, kk = 8 * (tid & 3) + e, k = k0 + kk;
-            uint16_t h = 0, l = 0;
-            const int m = m0 + row;
-            if (m < M && k < K) op_terms(A, bA + (transA ? (size_t)k * M + m : (size_t)m * K + k), NTA == 1, h, l);
+            const int k = k0 + 8 * (tid & 3) + e;
+            const int oa = (m < M && k < K) ? (transA ? k * M + m : m * K + k) * EA : kOutOfRange;
+            const int ob = (n < N && k < K) ? (transB ? n * K + k : k * N + n) * EB : kOutOfRange;
+            av[e] = ld(ra, oa, NTA == 1);
+            bv[e] = ld(rb, ob, NTB == 1);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int kk = 8 * (tid & 3) + e;
+            uint16_t h, l;
+            terms(av[e], NTA == 1, h, l);
             As[0][row][kk] = h;
             if (NTA == 2) As[NTA - 1][row][kk] = l;
-            const int n = n0 + row;
-            h = l = 0;
-            if (n < N && k < K) op_terms(B, bB + (transB ? (size_t)n * K + k : (size_t)k * N + n), NTB == 1, h, l);
+            terms(bv[e], NTB == 1, h, l);
             Bs[0][row][kk] = h;
             if (NTB == 2) Bs[NTB - 1][row][kk] = l;
         }
@@ -217,6 +233,12 @@ int matmul_dt_raw(hipStream_t s, const void* A, const void* B, float* C, uint32_
                                       GORCH_HIP_EPI_NONE));
             if (b + 1 == batch) return GORCH_HIP_OK;
         }
+    }
+    // the kernel's 32-bit buffer offsets: each batch entry below 2 GiB
+    if ((unsigned long long)M * K * (aBF16 ? 2 : 4) >= (1ull << 31) ||
+        (unsigned long long)K * N * (bBF16 ? 2 : 4) >= (1ull << 31)) {
+        set_error("gorch_hip_matmul_dt: an operand of one batch entry is 2 GiB or more");
+        return GORCH_HIP_EUNSUPPORTED;
     }
     const dim3 grid((N + 63) / 64, (M + 63) / 64, batch);
     const int tA = transA ? 1 : 0, tB = transB ? 1 : 0, m = (int)M, n = (int)N, k = (int)K;
