@@ -98,6 +98,27 @@ __global__ __launch_bounds__(256) void k_norm_rope_rows(const float* x, float* y
     float4 v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, 16 * lane, 0, 0));
     const float4 gv = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, 16 * lane, 0, 0));
     const int p = start_pos + r / heads;
+    // this lane's cos / sin, requested with the row (before the norm's
+    // reduction): raw buffer loads, so no load waits on another
+    const bool lo = lane < nl / 2;
+    float co[4], sn[4];
+    {
+        const long long tb = (long long)(p + 1) * half * 4;
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(cosT, tb), rs = make_rsrc(sinT, tb);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            int cs;
+            if (neox) {
+                cs = p * half + min(2 * lane + q / 2, half - 1);  // pair q / 2 of the lane
+            } else {
+                const int k = 4 * lane + q;
+                const int i = lo ? k : k - half;
+                cs = p * half + min(max(i, 0), half - 1);
+            }
+            co[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rc, cs * 4, 0, 0));
+            sn[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, cs * 4, 0, 0));
+        }
+    }
     if (g) {
         double s = ((double)v.x * (double)v.x + (double)v.y * (double)v.y) +
                    ((double)v.z * (double)v.z + (double)v.w * (double)v.w);
@@ -111,25 +132,19 @@ __global__ __launch_bounds__(256) void k_norm_rope_rows(const float* x, float* y
         // pairs (2i, 2i + 1) inside the lane's four elements, i = 2l, 2l + 1
 #pragma unroll
         for (int q = 0; q < 2; q++) {
-            const int i = 2 * lane + q;
-            const int cs = p * half + min(i, half - 1);
-            const float c = cosT[cs], si = sinT[cs];
+            const float c = co[2 * q], si = sn[2 * q];
             o[2 * q] = e[2 * q] * c - e[2 * q + 1] * si;
             o[2 * q + 1] = e[2 * q] * si + e[2 * q + 1] * c;
         }
     } else {
         // Llama pairs (i, i + half): the partner sits hd / 8 lanes away
-        const bool lo = lane < nl / 2;
         const int src = lo ? lane + nl / 2 : lane - nl / 2;
         float pe[4];
 #pragma unroll
         for (int q = 0; q < 4; q++) pe[q] = __shfl(e[q], src);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int k = 4 * lane + q;
-            const int i = lo ? k : k - half;
-            const int cs = p * half + min(max(i, 0), half - 1);
-            const float c = cosT[cs], si = sinT[cs];
+            const float c = co[q], si = sn[q];
             o[q] = lo ? e[q] * c - pe[q] * si : pe[q] * si + e[q] * c;
         }
     }
