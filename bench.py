@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps-per-graph", type=int, default=32,
+                    help="timed GEMV steps captured per graph replay (1 = one replay per step)")
     ap.add_argument("--shape", default=None,
                     help="restrict to one shape 'M,K,N' (for profiling one kernel)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -138,24 +140,42 @@ def gpu_leg(args, shapes):
                               frac=round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)))
         del g
 
-    # step graphs: step s launches every shape once, on copy s
+    # step graphs: step s launches every shape once, on copy s. The timed
+    # steps replay G of them per graph (a serving loop's capture), so the
+    # per-replay submission cost is paid once per G steps; a remainder of
+    # fewer than G steps replays one-step graphs.
     n_graphs = max(len(buf["W"]) for buf in bufs)
-    graphs = []
-    for s in range(n_graphs):
+    G = max(1, min(args.steps_per_graph, args.steps))
+
+    def capture(first, count):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
-            for buf in bufs:
-                launch(buf, s)
-        graphs.append(g)
+            for s in range(first, first + count):
+                for buf in bufs:
+                    launch(buf, s % n_graphs)
+        return g
 
-    def run(nsteps, start):
-        for s in range(nsteps):
+    graphs = [capture(s, 1) for s in range(n_graphs)]
+    groups = {}
+    for j in range(args.steps // G):
+        c = (args.warmup + j * G) % n_graphs
+        if c not in groups:
+            groups[c] = capture(c, G)
+
+    def run(nsteps, start, grouped):
+        s = 0
+        while grouped and nsteps - s >= G and G > 1:
+            groups[(start + s) % n_graphs].replay()
+            s += G
+        for s in range(s, nsteps):
             graphs[(start + s) % n_graphs].replay()
 
-    run(args.warmup, 0)
+    run(args.warmup, 0, False)
+    for g in groups.values():  # first replay of each grouped graph, untimed
+        g.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    run(args.steps, args.warmup)
+    run(args.steps, args.warmup, True)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     step_bytes = sum(algo_bytes(b_["M"], b_["K"], b_["N"]) for b_ in bufs)
@@ -618,6 +638,7 @@ def main():
         "config": {
             "workload": "bf16-weight Linear GEMV microbench (BASELINE configs[1]): x f32 N(0,1) [M,K], "
                         "W bf16 N(0,0.02) [N,K], f32 out; one step = one launch per shape",
+            "steps_per_graph_replay": max(1, min(args.steps_per_graph, args.steps)),
             "shapes": [f"M={s[0]},K={s[1]},N={s[2]}" for s in shapes],
             "weights_rotated_over_bytes": ROTATE_BYTES,
             "weight_layout": "each shape on the decode path's resident format (per_shape.layout): "
