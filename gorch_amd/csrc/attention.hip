@@ -1287,6 +1287,8 @@ extern "C" int gorch_hip_attention_cached(void* stream, const float* q, const fl
     GH_REQUIRE(head_dim % 4 == 0 && head_dim <= 256, "gorch_hip_attention_cached: head_dim must be a multiple of 4, <= 256");
     GH_REQUIRE(pos_offset >= 0 && pos_offset + new_seq <= max_seq,
                "gorch_hip_attention_cached: cached sequence length exceeds max_seq");
+    GH_SUPPORTED(kv_span_ok(max_seq, (long long)heads * head_dim),
+               "gorch_hip_attention_cached: a sequence's cache span (max_seq x dim x 4 bytes) must be below 2 GiB");
     GH_REQUIRE(q && k_cache && v_cache && out, "gorch_hip_attention_cached: null pointer");
     const int dim = heads * head_dim;
     GH_REQUIRE(((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0, "gorch_hip_attention_cached: cache must be 16-byte aligned");
@@ -1325,6 +1327,8 @@ extern "C" int gorch_hip_gqa_attention_cached(void* stream, const float* q, cons
                "gorch_hip_gqa_attention_cached: head_dim must be a multiple of 4, <= 256");
     GH_REQUIRE(pos_offset >= 0 && pos_offset + new_seq <= max_seq,
                "gorch_hip_gqa_attention_cached: cached sequence length exceeds max_seq");
+    GH_SUPPORTED(kv_span_ok(max_seq, (long long)num_kv * head_dim),
+               "gorch_hip_gqa_attention_cached: a sequence's cache span (max_seq x kv_dim x 4 bytes) must be below 2 GiB");
     GH_REQUIRE(q && k_cache && v_cache && out, "gorch_hip_gqa_attention_cached: null pointer");
     GH_REQUIRE(((uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0,
                "gorch_hip_gqa_attention_cached: cache must be 16-byte aligned");

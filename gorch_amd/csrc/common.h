@@ -101,6 +101,8 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
 // looked up once per device (gorch_hip_init or that entry point's first
 // call on the device).
 int noalloc_setup(int device);
+// Device bytes held by the per-stream scratch buffers (stream_scratch).
+long long scratch_bytes_held();
 
 // End of a compute entry point: in sync mode (gorch_hip_set_async(0)) waits
 // for the stream when rc is 0 and the stream is not being captured.
@@ -141,6 +143,16 @@ int check_launch(const char* what);
         if (!(cond)) {                        \
             ::gh::set_error(msg);             \
             return GORCH_HIP_EINVAL;          \
+        }                                     \
+    } while (0)
+
+// A configuration the kernels do not handle (the caller's cue for its CPU
+// path), as opposed to a bad argument.
+#define GH_SUPPORTED(cond, msg)               \
+    do {                                      \
+        if (!(cond)) {                        \
+            ::gh::set_error(msg);             \
+            return GORCH_HIP_EUNSUPPORTED;    \
         }                                     \
     } while (0)
 
@@ -324,6 +336,11 @@ int launch_attn_rows_wo(hipStream_t s, const AttnArgs& a, int heads);
 // key: 16384 keys); longer caches go to the online-softmax kernel.
 constexpr size_t kAttnMaxLdsBytes = 65536;
 int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows);
+// The attention kernels address one sequence's K (or V) rows through a
+// buffer resource whose byte span and offsets are 32-bit: a sequence's cache
+// of max_seq rows of kv_dim floats must stay below the out-of-range offset
+// (0x7fff0000 bytes, just under 2 GiB). Longer caches are refused.
+inline bool kv_span_ok(long long max_seq, long long kv_dim) { return max_seq * kv_dim * 4 < 0x7fff0000LL; }
 
 // GQA.forwardCached for one sequence (gqa.hip); pre_gain: an RMSNorm of x
 // applied first (the decoder block's), resid: added to the output. ws holds

@@ -504,6 +504,10 @@ static bool gpt_config_ok(int vocab, int dim, int heads, int layers, int max_seq
         set_error(std::string(who) + ": needs dim % 8 == 0 and head_dim a multiple of 4, <= 256");
         return false;
     }
+    if (!kv_span_ok(max_seq, dim)) {
+        set_error(std::string(who) + ": a sequence's cache span (max_seq x dim x 4 bytes) must be below 2 GiB");
+        return false;
+    }
     if (max_seq > (int)(kAttnMaxLdsBytes / sizeof(float)) && hd != 64 && hd != 128) {
         set_error(std::string(who) + ": max_seq above 16384 needs head_dim 64 or 128");
         return false;

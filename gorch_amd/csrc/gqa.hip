@@ -163,6 +163,8 @@ int gqa_check(const gorch_hip_gqa_weights* w, int S, int pos_offset, int max_seq
     GH_REQUIRE(nq > 0 && nkv > 0 && hd > 0 && d > 0, "gorch/nn: GQAConfig fields must be positive");
     GH_REQUIRE(nq % nkv == 0, "gorch/nn: GQA NumQ must be divisible by NumKV");
     GH_REQUIRE(pos_offset >= 0 && pos_offset + S <= max_seq, "gorch_hip_gqa_forward_cached: cache overflow");
+    GH_SUPPORTED(kv_span_ok(max_seq, (long long)nkv * hd),
+               "gorch_hip_gqa_forward_cached: a sequence's cache span (max_seq x kv_dim x 4 bytes) must be below 2 GiB");
     GH_REQUIRE(w->wq && w->wk && w->wv && w->wo, "gorch_hip_gqa_forward_cached: null projection weight");
     GH_REQUIRE(!w->rope_cos == !w->rope_sin, "gorch_hip_gqa_forward_cached: need both RoPE tables");
     GH_REQUIRE(!w->rope_cos || pos_offset + S <= w->rope_max_seq, "gorch/nn: RoPE startPos+seqLen exceeds MaxSeq");

@@ -46,7 +46,10 @@ struct StreamScratch {
 };
 std::mutex g_scratch_mu;
 std::vector<StreamScratch> g_scratch;
+std::atomic<long long> g_scratch_bytes{0};
 }  // namespace
+
+long long scratch_bytes_held() { return g_scratch_bytes.load(); }
 
 void* stream_scratch(hipStream_t s, size_t bytes) {
     int dev = 0;
@@ -67,7 +70,9 @@ void* stream_scratch(hipStream_t s, size_t bytes) {
         (void)hipGetLastError();
         return nullptr;
     }
+    g_scratch_bytes += (long long)want;
     if (e) {
+        // the smaller buffer stays allocated: a captured graph may point at it
         e->ptr = p;
         e->bytes = want;
     } else {
@@ -298,7 +303,11 @@ int gorch_hip_init(int device) {
         std::lock_guard<std::mutex> lock(g_probe_mu);
         if (g_probe[device].load(std::memory_order_acquire) == 0) (void)run_bf16_probe(device);
     }
-    return noalloc_setup(device);
+    // The no-allocation entry point's scratch lookup is optional here: a
+    // failure leaves that one entry point to retry (and report) on its own
+    // first call, and does not fail the library's set-up.
+    if (noalloc_setup(device) != GORCH_HIP_OK) clear_error();
+    return GORCH_HIP_OK;
 }
 
 const char* gorch_hip_last_error(void) { return t_error.c_str(); }
@@ -408,6 +417,8 @@ void* gorch_hip_buf_host(void* stream, gorch_hip_buf* h, int will_write) {
 }
 
 long long gorch_hip_live_bytes(void) { return g_live_bytes.load(); }
+
+long long gorch_hip_scratch_bytes(void) { return scratch_bytes_held(); }
 
 int gorch_hip_upload(void* stream, void* dst, const void* src, size_t bytes) {
     GH_REQUIRE(dst && src, "gorch_hip_upload: null pointer");

@@ -46,6 +46,7 @@ SIGNATURES = {
     "gorch_hip_download": (i32, [vp, vp, vp, C.c_size_t]),
     "gorch_hip_sync": (i32, [vp]),
     "gorch_hip_live_bytes": (C.c_longlong, []),
+    "gorch_hip_scratch_bytes": (C.c_longlong, []),
     "gorch_hip_buf_new": (vp, [C.c_size_t, i32]),
     "gorch_hip_buf_release": (None, [vp]),
     "gorch_hip_buf_len": (C.c_size_t, [vp]),

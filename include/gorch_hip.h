@@ -61,6 +61,13 @@ void gorch_hip_release(void* ptr);
 /* Bytes held by live allocations and buffers (liveBufferBytes,
  * metal/metal.go:363-368). */
 long long gorch_hip_live_bytes(void);
+/* Device bytes the library holds for its own scratch: the per-stream
+ * K-split partial buffers of gorch_hip_linear_bf16 and the engines, each
+ * allocated on a stream's first split launch outside capture and kept until
+ * the process ends (a captured graph may point at it). No counterpart in the
+ * reference (Metal's MPSGraph keeps its own scratch); it lets a caller check
+ * that a call allocated nothing. */
+long long gorch_hip_scratch_bytes(void);
 
 /* Buffer handles (metal.Buffer, metal/metal.go:240-422; Tensor.ToMetal /
  * Data, tensor.go:318-406). Device memory of exactly `bytes`, zero-filled;

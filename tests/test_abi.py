@@ -67,3 +67,27 @@ def test_moe_rejects_bad_shapes_without_gpu():
     assert call(1024, 64, 8, 2, 1 << 18) == 2
     assert "2^29" in hip.last_error()
     assert hip.lib().gorch_hip_moe_workspace_size(8, 64, 64, 8, 0) == 0
+
+
+def test_attention_rejects_cache_span_of_2gib_without_gpu():
+    # The attention kernels address one sequence's K/V rows with 32-bit
+    # buffer offsets: a span of max_seq * kv_dim * 4 bytes at or above
+    # 0x7fff0000 is refused with rc 1 (use the CPU path) before any device
+    # work, for MHA and GQA alike. Just below the bound the same call gets
+    # past the check (and then fails for want of a GPU, not for the span).
+    import ctypes as C
+
+    L = hip.lib()
+    q = kc = vc = out = C.c_void_p(0x10000)
+    # 64 heads x 128 dims = 8192 floats per row: 65,535 rows is under 2 GiB,
+    # 65,536 rows is 2 GiB
+    rc = L.gorch_hip_attention_cached(None, q, kc, vc, out, 1, 1, 0, 64, 128, 65536, 1)
+    assert rc == 1 and "2 GiB" in hip.last_error()
+    rc = L.gorch_hip_gqa_attention_cached(None, q, kc, vc, out, 1, 1, 0, 64, 64, 128, 65536, 1)
+    assert rc == 1 and "2 GiB" in hip.last_error()
+    # GQA: the span counts KV heads only; 8 KV heads x 128 fit at 65,536 rows
+    if hip.device_count() == 0:
+        rc = L.gorch_hip_gqa_attention_cached(None, q, kc, vc, out, 1, 1, 0, 64, 8, 128, 65536, 1)
+        assert rc != 1 or "2 GiB" not in hip.last_error()
+    rc = L.gorch_hip_attention_cached(None, q, kc, vc, out, 1, 1, 0, 64, 128, 1 << 22, 1)
+    assert rc == 1

@@ -61,10 +61,15 @@ def _pair(lib, M, N, K, epi, seed, residual=False, stream=None, check_mem=True):
     want = y0.get((M, N))
     assert lib.gorch_hip_sync(None) == 0
     free0 = _mem_free()
+    held0, live0 = lib.gorch_hip_scratch_bytes(), lib.gorch_hip_live_bytes()
     assert lib.gorch_hip_linear_bf16_noalloc(stream, dx.p, dW.p, db.p, rp, y1.p, M, N, K, epi) == 0, \
         lib.gorch_hip_last_error()
     assert lib.gorch_hip_sync(stream) == 0
-    # a fresh stream has no partials buffer: an allocating call would take one
+    # a fresh stream has no partials buffer: an allocating call would take
+    # one, which the library's own counters show (the device-wide free bytes
+    # are a second signal, exposed to other tenants of the GPU)
+    assert lib.gorch_hip_scratch_bytes() == held0
+    assert lib.gorch_hip_live_bytes() == live0
     if check_mem:
         assert _mem_free() == free0
     got = y1.get((M, N))
@@ -97,6 +102,18 @@ def test_noalloc_two_calls_second_smaller(lib):
     assert np.array_equal(got, want)
     got, want = _pair(lib, 40, 256, 512, 0, seed=5, stream=s.cuda_stream)
     assert np.array_equal(got, want)
+    # the counter the checks above rely on does see an allocation: the
+    # allocating entry point takes a partials buffer for a new stream's
+    # first K split
+    s2 = torch.cuda.Stream()
+    x, W, b = syn.gemv_inputs(16, 3072, 768, seed=6)
+    dx, dW, db, dy = Dev(lib, x), Dev(lib, W), Dev(lib, b), Dev(lib, nbytes=16 * 768 * 4)
+    held = lib.gorch_hip_scratch_bytes()
+    assert lib.gorch_hip_linear_bf16(s2.cuda_stream, dx.p, dW.p, db.p, None, dy.p, 16, 768, 3072, 0) == 0
+    assert lib.gorch_hip_sync(s2.cuda_stream) == 0
+    assert lib.gorch_hip_scratch_bytes() > held
+    for t in (dx, dW, db, dy):
+        t.free()
 
 
 def test_noalloc_rejects_bad_arguments(lib):
