@@ -104,6 +104,9 @@ int noalloc_setup(int device);
 // Device bytes held by the per-stream scratch buffers (stream_scratch).
 long long scratch_bytes_held();
 
+// gorch_hip_set_deterministic's setting: no float-atomic sums when true.
+bool deterministic();
+
 // End of a compute entry point: in sync mode (gorch_hip_set_async(0)) waits
 // for the stream when rc is 0 and the stream is not being captured.
 int finish(void* stream, int rc);
@@ -347,9 +350,13 @@ inline bool kv_span_ok(long long max_seq, long long kv_dim) { return max_seq * k
 // gqa_ws(...) bytes.
 size_t gqa_ws(int new_seq, int num_q, int num_kv, int hd, int dim);
 int gqa_check(const gorch_hip_gqa_weights* w, int S, int pos_offset, int max_seq);
+// pos_dev (one-row steps only): the position is read on the device (a
+// graph-replayed decode step); pos_offset is then ignored, and shapes whose
+// step does not take the key-split attention with the q/k norm and RoPE
+// inside return GORCH_HIP_EUNSUPPORTED.
 int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int S, float* k_cache, float* v_cache,
              int pos_offset, int max_seq, float* out, char* ws, const float* pre_gain, float pre_eps,
-             const float* resid);
+             const float* resid, const int* pos_dev = nullptr);
 int launch_rmsnorm(hipStream_t s, const float* x, const float* g, float* y, int M, int N, float eps);
 // The one-row register GEMV takes K (RMSNorm / SwiGLU prologues need it).
 bool gemv_m1_prologue_ok(int K);

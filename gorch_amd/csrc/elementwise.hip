@@ -77,6 +77,13 @@ int launch_embed_pos(hipStream_t s, const float* wte, const float* wpe, const in
     return check_launch("embed_pos");
 }
 
+int launch_embedding(hipStream_t s, const float* w, const int* ids, float* out, int dim, int rows) {
+    const int64_t total = (int64_t)rows * dim;
+    hipLaunchKernelGGL(k_embedding, dim3(grid_1d(total)), dim3(256), 0, s, w, ids, out, dim, total);
+    count(CNT_ELEMENTWISE);
+    return check_launch("embedding");
+}
+
 int launch_swiglu(hipStream_t s, const float* g, const float* v, float* y, int64_t n) {
     if (n == 0) return GORCH_HIP_OK;
     hipLaunchKernelGGL(k_swiglu, dim3(grid_1d(n)), dim3(256), 0, s, g, v, y, n);

@@ -184,11 +184,9 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         const char* e = getenv("GORCH_HIP_RES_SPLIT");
         return std::min(kMaxSplit, e ? atoi(e) : 0);
     }();
-    // GORCH_HIP_WO_FUSE=0 keeps the one-row output projection a GEMV of its own
-    static const bool wo_fuse = [] {
-        const char* e = getenv("GORCH_HIP_WO_FUSE");
-        return e ? atoi(e) != 0 : true;
-    }();
+    // deterministic mode keeps the one-row output projection a GEMV of its
+    // own (the fused forms add per-head products with float atomics)
+    const bool wo_fuse = !deterministic();
     // Wo's slices (0: the packed-split rule); measured at XL batch 16 (with
     // the 3-slice QKV): 2 / 3 / 4 / 5 / 6 / 8 slices 5,335 / 5,336 / 5,359 /
     // 5,332 / 5,258 / 5,254 tok/s
@@ -946,7 +944,9 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
             // capture the step once (or again when a buffer it points at moved)
             const std::vector<const void*> sig = {g->x,    g->h,    g->q,    g->att,      g->ff,
                                                   g->logits, g->ids, g->part, g->stats, c->k,
-                                                  c->v,    c->state, c->hist, c->key};
+                                                  c->v,    c->state, c->hist, c->key,
+                                                  // the kernels differ by the deterministic setting
+                                                  reinterpret_cast<const void*>(deterministic() ? 1 : 0)};
             if (!g->gen_exec || g->gen_sig != sig) {
                 if (g->gen_exec) (void)hipGraphExecDestroy(g->gen_exec);
                 if (g->gen_graph) (void)hipGraphDestroy(g->gen_graph);

@@ -15,9 +15,12 @@ int launch_rope_rows(hipStream_t s, const float* x, float* y, int rows, int head
 int launch_rmsnorm(hipStream_t s, const float* x, const float* g, float* y, int M, int N, float eps);
 int launch_norm_rope_rows(hipStream_t s, const float* x, float* y, int rows, int heads, int hd, const float* g,
                           float eps, int start_pos, const float* cosT, const float* sinT, int neox);
+// pos_dev (nullable): start position read on the device; yk then starts at
+// yk + *pos_dev * yk_pos_stride
 int launch_norm_rope_rows2(hipStream_t s, const float* xq, float* yq, int rows_q, int heads_q, const float* gq,
                            const float* xk, float* yk, int rows_k, int heads_k, const float* gk, int hd, float eps,
-                           int start_pos, const float* cosT, const float* sinT, int neox);
+                           int start_pos, const float* cosT, const float* sinT, int neox,
+                           const int* pos_dev = nullptr, long long yk_pos_stride = 0);
 }  // namespace gh
 
 using namespace gh;
@@ -46,7 +49,7 @@ namespace gh {
 // (nullable): added to the Wo output (the block's residual add).
 int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int S, float* k_cache, float* v_cache,
              int pos_offset, int max_seq, float* out, char* ws, const float* pre_gain, float pre_eps,
-             const float* resid) {
+             const float* resid, const int* pos_dev) {
     const int nq = w->num_q, nkv = w->num_kv, hd = w->head_dim, d = w->dim;
     const int qdim = nq * hd, kvdim = nkv * hd;
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
@@ -55,6 +58,11 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
     float* kt = (float*)(ws + 2 * al((size_t)S * qdim * 4));
     float* h = (float*)(ws + 2 * al((size_t)S * qdim * 4) + al((size_t)S * kvdim * 4));
     float* split = S == 1 ? (float*)((char*)h + al((size_t)S * d * 4)) : nullptr;
+    if (pos_dev && S != 1) {
+        set_error("gqa: a device-side position needs one new row");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
+    if (pos_dev) pos_offset = 0;
     float* krow = k_cache + (size_t)pos_offset * kvdim;
     float* vrow = v_cache + (size_t)pos_offset * kvdim;
 
@@ -74,7 +82,7 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
         OutDesc od{};
         od.nseg = 3;
         od.rows_per_seq = 1 << 30;
-        od.pos_dev = nullptr;
+        od.pos_dev = pos_dev;
         float* dst[3] = {q, kt, vrow};
         const int ends[3] = {qdim, qdim + kvdim, qdim + 2 * kvdim};
         const int widths[3] = {qdim, kvdim, kvdim};
@@ -83,7 +91,8 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
             od.n_end[i] = ends[i];
             od.seq_stride[i] = 0;
             od.row_stride[i] = widths[i];
-            od.use_pos[i] = 0;
+            // the V row at the device position (vrow is the cache base then)
+            od.use_pos[i] = pos_dev && i == 2 ? 1 : 0;
         }
         LinearExtras ex;
         if (pre_gain) {
@@ -94,11 +103,15 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
         GH_TRY(launch_linear_bf16_od(s, x, w->wq, w->bq, nullptr, od, S, qdim + 2 * kvdim, d, GORCH_HIP_EPI_NONE,
                                      ex));
     } else {
+        if (pos_dev) {
+            set_error("gqa: a device-side position needs Q, K and V rows of one weight");
+            return GORCH_HIP_EUNSUPPORTED;
+        }
         GH_TRY(launch_linear_bf16(s, x, w->wq, w->bq, nullptr, q, S, qdim, d, GORCH_HIP_EPI_NONE));
         GH_TRY(launch_linear_bf16(s, x, w->wk, w->bk, nullptr, kt, S, kvdim, d, GORCH_HIP_EPI_NONE));
         GH_TRY(launch_linear_bf16(s, x, w->wv, w->bv, nullptr, vrow, S, kvdim, d, GORCH_HIP_EPI_NONE));
     }
-    AttnArgs a{q, k_cache, v_cache, att, nullptr, pos_offset, S, qdim, hd, max_seq, qdim, w->causal ? 1 : 0,
+    AttnArgs a{q, k_cache, v_cache, att, pos_dev, pos_offset, S, qdim, hd, max_seq, qdim, w->causal ? 1 : 0,
                (float)(1.0 / sqrt((double)hd)), nkv, kvdim, 1};
     a.split_ws = split;
     a.split_ws_floats = split ? (long long)nq * kAttnSplitMax * (hd + 2) : 0;
@@ -108,14 +121,10 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
     const bool aligned16 = ((reinterpret_cast<uintptr_t>(krow) | reinterpret_cast<uintptr_t>(q) |
                              reinterpret_cast<uintptr_t>(kt) | reinterpret_cast<uintptr_t>(w->q_norm) |
                              reinterpret_cast<uintptr_t>(w->k_norm)) % 16) == 0;
-    static const bool qk_in_attn = [] {
-        const char* e = getenv("GORCH_HIP_QK_IN_ATTN");
-        return e ? atoi(e) != 0 : true;
-    }();
     const bool fused = w->rope_cos && hd % 8 == 0 && hd <= 256 &&
                        ((reinterpret_cast<uintptr_t>(krow) | reinterpret_cast<uintptr_t>(q) |
                          reinterpret_cast<uintptr_t>(kt)) % 16) == 0;
-    if (qk_in_attn && aligned16 && attn_split_takes_qk(a, nq, S)) {
+    if (aligned16 && attn_split_takes_qk(a, nq, S)) {
         a.k_raw = kt;
         a.q_gain = w->q_norm;
         a.k_gain = w->k_norm;
@@ -124,8 +133,13 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
         a.rope_sin = w->rope_sin;
         a.rope_neox = w->rope_neox;
     } else if (fused) {
+        // (with pos_dev krow is the cache base and the kernel offsets it)
         GH_TRY(launch_norm_rope_rows2(s, q, q, S * nq, nq, w->q_norm, kt, krow, S * nkv, nkv, w->k_norm, hd,
-                                      w->norm_eps, pos_offset, w->rope_cos, w->rope_sin, w->rope_neox));
+                                      w->norm_eps, pos_offset, w->rope_cos, w->rope_sin, w->rope_neox, pos_dev,
+                                      kvdim));
+    } else if (pos_dev) {
+        set_error("gqa: a device-side position needs RoPE and head_dim % 8 == 0, <= 256");
+        return GORCH_HIP_EUNSUPPORTED;
     } else {
         if (w->q_norm) GH_TRY(launch_rmsnorm(s, q, w->q_norm, q, S * nq, hd, w->norm_eps));
         if (w->k_norm) GH_TRY(launch_rmsnorm(s, kt, w->k_norm, kt, S * nkv, hd, w->norm_eps));
@@ -140,11 +154,8 @@ int gqa_core(hipStream_t s, const gorch_hip_gqa_weights* w, const float* x, int 
     }
     // one-row steps on the key-split path: Wo (+ bias and the residual) in
     // the kernel that merges the key chunks, added into out with float
-    // atomics per head
-    static const bool wo_in_attn = [] {
-        const char* e = getenv("GORCH_HIP_GQA_WO_FUSE");
-        return e ? atoi(e) != 0 : true;
-    }();
+    // atomics per head (not in deterministic mode)
+    const bool wo_in_attn = !deterministic();
     if (wo_in_attn && S == 1 && qdim % 8 == 0 && (reinterpret_cast<uintptr_t>(w->wo) % 16) == 0 &&
         attn_split_takes_qk(a, nq, S)) {
         a.wo = w->wo;

@@ -80,15 +80,21 @@ __global__ __launch_bounds__(256) void k_norm_rope_rows(const float* x, float* y
                                                         const float* __restrict__ sinT, int neox,
                                                         const float* x2 = nullptr, float* y2 = nullptr,
                                                         int rows2 = 0, int heads2 = 1,
-                                                        const float* __restrict__ g2 = nullptr) {
+                                                        const float* __restrict__ g2 = nullptr,
+                                                        const int* __restrict__ pos_dev = nullptr,
+                                                        long long y2_pos_stride = 0) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     int r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     if (r >= rows + rows2) return;
+    // pos_dev: the start position read on the device (a captured decode
+    // step); the second segment's output (the K cache rows) then starts at
+    // y2 + start_pos * y2_pos_stride
+    if (pos_dev) start_pos = *pos_dev;
     if (r >= rows) {  // wave-uniform: a wave is one row
         r -= rows;
         x = x2;
-        y = y2;
+        y = y2 + (pos_dev ? (long long)start_pos * y2_pos_stride : 0);
         heads = heads2;
         g = g2;
     }
@@ -167,10 +173,11 @@ static int grid_for(int64_t n) {
 
 int launch_norm_rope_rows2(hipStream_t s, const float* xq, float* yq, int rows_q, int heads_q, const float* gq,
                            const float* xk, float* yk, int rows_k, int heads_k, const float* gk, int hd, float eps,
-                           int start_pos, const float* cosT, const float* sinT, int neox) {
+                           int start_pos, const float* cosT, const float* sinT, int neox, const int* pos_dev,
+                           long long yk_pos_stride) {
     if (rows_q + rows_k == 0) return GORCH_HIP_OK;
     hipLaunchKernelGGL(k_norm_rope_rows, dim3((rows_q + rows_k + 3) / 4), dim3(256), 0, s, xq, yq, rows_q, heads_q,
-                       hd, gq, eps, start_pos, cosT, sinT, neox, xk, yk, rows_k, heads_k, gk);
+                       hd, gq, eps, start_pos, cosT, sinT, neox, xk, yk, rows_k, heads_k, gk, pos_dev, yk_pos_stride);
     count(CNT_ELEMENTWISE);
     return check_launch("norm_rope_rows2");
 }

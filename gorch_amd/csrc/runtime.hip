@@ -86,6 +86,10 @@ void* stream_scratch(hipStream_t s, size_t bytes) {
 // point waits for its stream before returning (the Metal shim's per-op
 // waitUntilCompleted, metal/shim.m:216-227).
 static std::atomic<int> g_async{1};
+// gorch_hip_set_deterministic: fixed-order sums only (no float atomics)
+static std::atomic<int> g_deterministic{0};
+
+bool deterministic() { return g_deterministic.load(std::memory_order_relaxed) != 0; }
 
 int finish(void* stream, int rc) {
     if (rc != GORCH_HIP_OK || g_async.load(std::memory_order_relaxed)) return rc;
@@ -255,6 +259,10 @@ int gorch_hip_set_async(int on) {
 }
 
 int gorch_hip_async_enabled(void) { return g_async.load(); }
+
+int gorch_hip_set_deterministic(int on) { return g_deterministic.exchange(on ? 1 : 0); }
+
+int gorch_hip_deterministic_enabled(void) { return g_deterministic.load(); }
 
 int gorch_hip_bf16_matmul_supported(void) {
     int dev = 0;

@@ -47,6 +47,13 @@ SIGNATURES = {
     "gorch_hip_sync": (i32, [vp]),
     "gorch_hip_live_bytes": (C.c_longlong, []),
     "gorch_hip_scratch_bytes": (C.c_longlong, []),
+    "gorch_hip_qwen_create": (C.c_void_p, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_float,
+                                           C.c_int, C.c_int]),
+    "gorch_hip_qwen_destroy": (None, [C.c_void_p]),
+    "gorch_hip_qwen_generate": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
+                                          C.c_void_p, C.POINTER(C.c_int), C.c_void_p, C.c_void_p, C.c_int]),
+    "gorch_hip_set_deterministic": (C.c_int, [C.c_int]),
+    "gorch_hip_deterministic_enabled": (C.c_int, []),
     "gorch_hip_buf_new": (vp, [C.c_size_t, i32]),
     "gorch_hip_buf_release": (None, [vp]),
     "gorch_hip_buf_len": (C.c_size_t, [vp]),
@@ -178,6 +185,16 @@ def set_async(on: bool) -> None:
 
 def async_enabled() -> bool:
     return bool(lib().gorch_hip_async_enabled())
+
+
+def set_deterministic(on: bool) -> bool:
+    """Fixed-order sums only (no float atomics in the one-row decode steps);
+    returns the previous setting."""
+    return bool(lib().gorch_hip_set_deterministic(int(on)))
+
+
+def deterministic_enabled() -> bool:
+    return bool(lib().gorch_hip_deterministic_enabled())
 
 
 def bf16_matmul_supported() -> bool:

@@ -71,6 +71,7 @@ class Qwen:
         if not cfg.tied_embeddings:
             raise ValueError("qwen: only the tied LM head is supported (the reference Model ties it)")
         self.cfg = cfg
+        self._engine = None
         self.embed_bf16 = w["embed"] if isinstance(w["embed"], torch.Tensor) else up(w["embed"])
         self.embed = torch.empty((cfg.vocab, cfg.hidden), dtype=torch.float32, device="cuda")
         hip.bf16_to_f32(self.embed_bf16, self.embed)
@@ -109,6 +110,53 @@ class Qwen:
             layer["block"] = hip.QwenBlock(layer["attn"], layer["norm_attn"], layer["norm_ffn"], layer["wgu"],
                                            layer["wdown"], cfg.inter, cfg.eps)
             self.layers.append(layer)
+
+    def generate(self, prompt, max_new: int, stop_tokens=None, want_logits=False, use_graph=True):
+        """Generate with a greedy config (model/qwen/generate.go:35-66) on the
+        device: prefill, then one token per step with the argmax fused into
+        the tied head, each step replayed from a HIP graph that reads the
+        position on the device. stop_tokens (default cfg.eos_tokens, the
+        reference's Greedy list) end generation and are not kept. Returns
+        (ids: prompt + new tokens, step logits [n_new, vocab] or None,
+        timing dict)."""
+        import ctypes as C
+
+        cfg = self.cfg
+        if self._engine is None:
+            blocks = (hip._QwenBlockW * len(self.layers))(*[layer["block"].s for layer in self.layers])
+            h = hip.lib().gorch_hip_qwen_create(blocks, len(self.layers), self.embed_bf16.data_ptr(),
+                                                self.embed.data_ptr(), self.norm.data_ptr(), cfg.eps, cfg.vocab,
+                                                cfg.max_seq)
+            if not h:
+                raise hip.HipError(2, hip.last_error())
+            self._engine = h
+        prompt = np.ascontiguousarray(np.asarray(prompt, np.int32).reshape(-1))
+        stops = np.ascontiguousarray(np.asarray(cfg.eos_tokens if stop_tokens is None else stop_tokens, np.int32))
+        out = np.zeros(prompt.size + max(max_new, 0), np.int32)
+        n = C.c_int(0)
+        logits = np.zeros((max(max_new, 1), cfg.vocab), np.float32) if want_logits else None
+        timing = (C.c_float * 4)()
+        hip._ok(hip.lib().gorch_hip_qwen_generate(hip._stream(), self._engine, prompt.ctypes.data, prompt.size,
+                                                  max_new, stops.ctypes.data if stops.size else None, stops.size,
+                                                  out.ctypes.data, C.byref(n), None if logits is None else
+                                                  logits.ctypes.data, timing, int(use_graph)))
+        ids = out[: n.value].copy()
+        if logits is not None:
+            logits = logits[: n.value - prompt.size]
+        return ids, logits, {"prefill_ms": timing[0], "decode_ms": timing[1], "decode_forwards": int(timing[2]),
+                             "graph": bool(timing[3])}
+
+    def close(self):
+        """Releases the generation engine (its cache and buffers)."""
+        if getattr(self, "_engine", None):
+            hip.lib().gorch_hip_qwen_destroy(self._engine)
+            self._engine = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def new_cache(self, capacity: int):
         """Per-layer K and V rows [capacity, kv_dim] f32 (nn/kvcache.go:14-60)."""

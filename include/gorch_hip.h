@@ -102,6 +102,19 @@ int gorch_hip_sync(void* stream);
  * shim's per-op wait). Turning it off first drains the device. */
 int gorch_hip_set_async(int on);
 int gorch_hip_async_enabled(void);
+/* Run-to-run bit reproducibility. Off (the default), the one-row decode
+ * steps of the GPT engine and of the GQA/Qwen block add the output
+ * projection into the residual inside the attention kernel with float
+ * atomics, one per head, whose order varies between runs (the last bits of
+ * the logits can differ; greedy tokens are identical unless two logits tie
+ * to that precision). On, those steps run the projection as a GEMV of its
+ * own and every sum has a fixed order, as gorch's greedy loop
+ * (model/generate.go:134-144). Takes effect at the next launch; a caller's
+ * own captured graphs keep the kernels they captured. Returns the previous
+ * setting. No counterpart in the reference, whose CPU and Metal paths have
+ * no cross-block atomics. */
+int gorch_hip_set_deterministic(int on);
+int gorch_hip_deterministic_enabled(void);
 /* The bf16 matmul self-probe (MetalBF16MatMulSupported / runBF16MatMulProbe,
  * bf16_matmul.go:52-112): a 16x16x16 bf16 x bf16 and bf16 x f32 product
  * through the matmul path against a host f32 product, every element within
@@ -308,6 +321,36 @@ size_t gorch_hip_qwen_block_workspace_size(const gorch_hip_qwen_block* b, int ne
 int gorch_hip_qwen_block_forward_cached(void* stream, const gorch_hip_qwen_block* b, float* x, int new_seq,
                                         float* k_cache, float* v_cache, int pos_offset, int max_seq,
                                         void* workspace, size_t workspace_bytes);
+
+/* model/qwen Model (qwen.go:12-98) for greedy generation: blocks[0 ..
+ * layers) as above (copied; their device weights stay the caller's and
+ * must outlive the model; every block needs RoPE tables covering max_seq),
+ * embed_bf16 the tied [vocab, dim] bf16 embedding (the LM head, qwen.go:84),
+ * embed_f32 its f32 widening (the lookup), norm the final RMSNorm gain.
+ * The model owns its KV cache (MaxSeq rows at most, grown as needed),
+ * activations and decode state. NULL on failure (gorch_hip_last_error). */
+typedef struct gorch_hip_qwen gorch_hip_qwen;
+gorch_hip_qwen* gorch_hip_qwen_create(const gorch_hip_qwen_block* blocks, int layers, const uint16_t* embed_bf16,
+                                      const float* embed_f32, const float* norm, float eps, int vocab, int max_seq);
+void gorch_hip_qwen_destroy(gorch_hip_qwen* m);
+/* Generate with a greedy config (model/qwen/generate.go:35-66, Greedy
+ * :24-29): a prefill over the host prompt, then one token per step; a token
+ * in stop_tokens[0 .. n_stop) ends generation and is not kept; generation
+ * also ends after max_new tokens, or once the cache holds max_seq rows (the
+ * token chosen then is kept). out_ids (host, n_prompt + max_new ints)
+ * receives the prompt and the new tokens, *out_len their count. The argmax
+ * is fused into the tied head; flags bit 0 replays each step from a HIP
+ * graph that reads the position from device memory (shapes whose
+ * attention step cannot, and runs with step_logits, launch each step
+ * directly). step_logits (nullable, host [max_new, vocab]): each chosen
+ * token's logits. timing_ms (nullable, 4 floats): prefill ms, decode ms,
+ * decode forwards run, 1 when the steps were graph-replayed (else 0). Stop
+ * tokens are read back every 8 steps. Returns
+ * EINVAL for an empty prompt ("qwen: empty prompt", the reference's panic)
+ * or one longer than max_seq. Synchronous. */
+int gorch_hip_qwen_generate(void* stream, gorch_hip_qwen* m, const int* prompt, int n_prompt, int max_new,
+                            const int* stop_tokens, int n_stop, int* out_ids, int* out_len, float* step_logits,
+                            float* timing_ms, int flags);
 
 /* ------------------------------------------------------------------------
  * MoE FFN layer (nn.MoE.Forward, nn/moe.go:130-182).

@@ -215,3 +215,132 @@ def test_qwen_full_size_greedy(gpu, preset):
     for (kd, vd), (kc, vc) in zip(cache, ref.cache):
         assert rel_err(host(kd)[:pos], kc[:pos]) <= 1e-4
         assert rel_err(host(vd)[:pos], vc[:pos]) <= 1e-4
+
+
+def test_qwen_deterministic_steps(gpu):
+    """gorch_hip_set_deterministic(1) on the Qwen block's one-row steps (the
+    key-split attention without Wo in its merge; Wo as a GEMV with the
+    residual): the same logits bit for bit on a second run, and the oracle
+    composition's tokens and 1e-3 logits."""
+    from gorch_amd import hip
+
+    cfg = QwenConfig(hidden=64, layers=2, num_q=4, num_kv=2, head_dim=64, inter=96, vocab=300, max_seq=320)
+    w = syn.qwen_weights(cfg, seed=6)
+    m = Qwen(cfg, w)
+    ref = OracleQwen(cfg, w, m)
+    prompt = np.random.default_rng(12).integers(0, cfg.vocab, 200).astype(np.int32)
+    prev = hip.set_deterministic(True)
+    try:
+        runs = []
+        for run in range(2):
+            cache = m.new_cache(cfg.max_seq)
+            ids, pos, out = prompt, 0, []
+            for step in range(5):
+                got = host(m.forward_cached(torch.from_numpy(ids).cuda(), cache, pos))
+                if run == 0:
+                    want = ref.forward_cached(ids, pos)
+                    assert rel_err(got, want) <= 1e-3, step
+                    assert int(np.argmax(got[0])) == orc.argmax(want), step
+                out.append(got)
+                pos += ids.size
+                ids = np.array([int(np.argmax(got[0]))], np.int32)
+            runs.append(np.concatenate(out))
+        assert np.array_equal(runs[0], runs[1])
+    finally:
+        hip.set_deterministic(prev)
+
+
+def oracle_generate(ref, prompt, max_new, stops, max_seq):
+    """model/qwen/generate.go:35-66 with a greedy config over the oracle
+    composition: token i from the latest logits; a stop token ends the loop
+    and is not kept; the loop also ends once the cache holds MaxSeq rows
+    (after keeping that token)."""
+    result = [int(t) for t in prompt]
+    logits = ref.forward_cached(np.asarray(prompt, np.int32), 0)
+    pos, steps = len(prompt), []
+    for _ in range(max_new):
+        nxt = orc.argmax(logits)
+        steps.append(logits[0])
+        if nxt in stops:
+            break
+        result.append(nxt)
+        if pos >= max_seq:
+            break
+        logits = ref.forward_cached(np.array([nxt], np.int32), pos)
+        pos += 1
+    return result, np.stack(steps)
+
+
+GEN = QwenConfig(hidden=128, layers=2, num_q=4, num_kv=2, head_dim=64, inter=192, vocab=500, max_seq=96)
+
+
+@pytest.mark.parametrize("cfg", [GEN, TINY], ids=["hd64", "hd32"])
+def test_qwen_generate_matches_oracle(gpu, cfg):
+    """The device generation loop (gorch_hip_qwen_generate): tokens identical
+    to the oracle loop, each step's logits within 1e-3 and the run within
+    2e-2; the graph-replayed steps (position read on the device) give the
+    same tokens as the directly launched ones (head_dim 64 and 32: the
+    one-pass short-cache attention after a q/k norm + RoPE launch, both at
+    the device position)."""
+    w = syn.qwen_weights(cfg, seed=21)
+    m = Qwen(cfg, w)
+    ref = OracleQwen(cfg, w, m)
+    prompt = np.random.default_rng(22).integers(0, cfg.vocab, 10).astype(np.int32)
+    want, want_logits = oracle_generate(ref, prompt, 20, (), cfg.max_seq)
+    ids, logits, t = m.generate(prompt, 20, stop_tokens=(), want_logits=True)
+    assert list(ids) == want
+    assert rel_err(logits[0], want_logits[0]) <= 1e-3
+    assert rel_err(logits, want_logits) <= 2e-2
+    ids_g, _, t = m.generate(prompt, 20, stop_tokens=())
+    assert list(ids_g) == want
+    assert t["decode_forwards"] == 19
+    assert t["graph"]
+    # a second run reuses the engine (cache, captured step)
+    ids_g2, _, _ = m.generate(prompt, 20, stop_tokens=())
+    assert np.array_equal(ids_g2, ids_g)
+    m.close()
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_qwen_generate_stops_on_stop_token(gpu, use_graph):
+    """A stop token ends generation and is not kept (generate.go:50-53):
+    the oracle's 6th new token as the stop id (one of two, as Greedy's
+    ChatML pair) cuts the output before its first occurrence; the steps run
+    stop within the 8-step read-back window."""
+    w = syn.qwen_weights(GEN, seed=23)
+    m = Qwen(GEN, w)
+    ref = OracleQwen(GEN, w, m)
+    prompt = np.random.default_rng(24).integers(0, GEN.vocab, 12).astype(np.int32)
+    full, _ = oracle_generate(ref, prompt, 40, (), GEN.max_seq)
+    stop = full[len(prompt) + 5]
+    stops = (GEN.vocab - 1 if stop != GEN.vocab - 1 else 0, stop)
+    ref2 = OracleQwen(GEN, w, m)
+    want, _ = oracle_generate(ref2, prompt, 40, stops, GEN.max_seq)
+    assert len(want) <= len(prompt) + 5
+    ids, _, t = m.generate(prompt, 40, stop_tokens=stops, use_graph=use_graph)
+    assert list(ids) == want
+    assert t["decode_forwards"] < 39
+    m.close()
+
+
+def test_qwen_generate_max_seq_and_errors(gpu):
+    """Generation ends once the cache holds MaxSeq rows, keeping the token
+    chosen then (generate.go:55-57): a 90-row prompt at MaxSeq 96 yields 7
+    new tokens, not 20. An empty prompt is an error ("qwen: empty prompt"),
+    as is one longer than MaxSeq; max_new 0 returns the prompt."""
+    w = syn.qwen_weights(GEN, seed=25)
+    m = Qwen(GEN, w)
+    ref = OracleQwen(GEN, w, m)
+    prompt = np.random.default_rng(26).integers(0, GEN.vocab, 90).astype(np.int32)
+    want, _ = oracle_generate(ref, prompt, 20, (), GEN.max_seq)
+    assert len(want) == GEN.max_seq + 1
+    ids, _, _ = m.generate(prompt, 20, stop_tokens=())
+    assert list(ids) == want
+    ids0, _, _ = m.generate(prompt, 0, stop_tokens=())
+    assert list(ids0) == list(prompt)
+    from gorch_amd import hip
+    with pytest.raises(hip.HipError, match="empty prompt"):
+        m.generate(np.zeros(0, np.int32), 4)
+    with pytest.raises(hip.HipError):
+        m.generate(np.zeros(GEN.max_seq + 1, np.int32), 4)
+    m.close()
