@@ -307,13 +307,14 @@ def moe_leg():
             "TFLOPs": round(flops / us / 1e6, 1), "frac_mfma_peak": round(flops / us / 1e6 / MFMA_PEAK_TFLOPS, 4)}
 
 
-def qwen_leg(ctxs=(128, 512), steps=100):
+def qwen_leg(ctxs=(128, 512), steps=100, gen_tokens=65):
     """Qwen3-0.6B-shaped cached decode (the reference's BenchmarkQwenDecode,
     model/qwen/bench_test.go:21-43): 28 layers, d 1024, 16 query / 8 KV heads
     of 128, SwiGLU 3072, vocab 151936 tied head; random bf16 weights N(0,0.02)
     generated on the device. The cache is prefilled to ctx tokens, then one
     graph-captured single-token step at position ctx is replayed (it rewrites
-    the same cache row, as the reference trims the cache back each step)."""
+    the same cache row, as the reference trims the cache back each step).
+    "generate" times the device generation loop from the same prompt."""
     import dataclasses
 
     import torch
@@ -321,7 +322,7 @@ def qwen_leg(ctxs=(128, 512), steps=100):
     from gorch_amd import hip
     from gorch_amd.qwen import QWEN3_0_6B, Qwen
 
-    cfg = dataclasses.replace(QWEN3_0_6B, max_seq=max(ctxs) + 8)
+    cfg = dataclasses.replace(QWEN3_0_6B, max_seq=max(ctxs) + gen_tokens + 8)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0)
 
@@ -363,12 +364,23 @@ def qwen_leg(ctxs=(128, 512), steps=100):
         e1.record(stream)
         e1.synchronize()
         ms = e0.elapsed_time(e1) / steps
+        del g, cache
+        # the greedy generation loop on the device (model/qwen/generate.go:
+        # 35-66): prefill of the ctx prompt, then new_tokens - 1 graph-replayed
+        # steps with the argmax fused into the tied head; decode time only
+        prompt = ids.cpu().numpy()
+        m.generate(prompt, gen_tokens, stop_tokens=())
+        _, _, t = m.generate(prompt, gen_tokens, stop_tokens=())
+        gen_ms = t["decode_ms"] / max(t["decode_forwards"], 1)
         out.append({"model": "qwen3-0.6b-shaped", "batch": 1, "ctx": ctx, "tok_s": round(1e3 / ms, 1),
                     "ms_per_token": round(ms, 4), "weights": "bf16 N(0,0.02) random init on the device",
                     "roofline": roofline_block(qwen_step_bytes(cfg, ctx), ms / 1e3,
                                                "bf16 weights + tied head + gains once, K/V rows read "
-                                               "and written, logits; per token")})
-        del g, cache
+                                               "and written, logits; per token"),
+                    "generate": {"new_tokens": gen_tokens, "decode_forwards": t["decode_forwards"],
+                                 "graph": t["graph"], "tok_s": round(1e3 / gen_ms, 1),
+                                 "ms_per_token": round(gen_ms, 4), "prefill_ms": round(t["prefill_ms"], 3)}})
+    m.close()
     return out
 
 

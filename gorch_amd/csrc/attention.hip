@@ -1021,31 +1021,19 @@ enum AttnRoute { kRouteFlash, kRouteSplit, kRouteRows, kRouteLong, kRouteCached1
 // in all, at least one load round of keys per chunk; 0 when a cannot split
 // (no scratch, more than one new row, scratch too small, one chunk).
 static int attn_split_chunks(const AttnArgs& a, int heads, int rows) {
-    // one new row per sequence; several sequences only with
-    // GORCH_HIP_ATTN_SPLIT_BATCH = the target number of 4-wave blocks per CU
-    static const int batch_target = [] {
-        const char* e = getenv("GORCH_HIP_ATTN_SPLIT_BATCH");
-        return e ? atoi(e) : 0;
-    }();
-    if (!a.split_ws || a.new_seq != 1 || (a.hd != 64 && a.hd != 128)) return 0;
-    if (rows != 1 && batch_target <= 0) return 0;
-    static const int min_keys = [] {
-        const char* e = getenv("GORCH_HIP_SPLIT_MIN_KEYS");
-        return e ? atoi(e) : 0;
-    }();
-    const int kc = std::max(min_keys, a.hd == 64 ? 64 : 32);  // keys per 4-wave load round (at least)
+    // one new row of one sequence (for many sequences the one-block-per-
+    // (head, row) kernels were faster: XL batch 16 with 2 / 3 / 6 chunks per
+    // (head, row) 4,498 / 4,564 / 4,273 tok/s against 5,149)
+    if (!a.split_ws || a.new_seq != 1 || rows != 1 || (a.hd != 64 && a.hd != 128)) return 0;
+    const int kc = a.hd == 64 ? 64 : 32;  // keys per 4-wave load round
     const long long keys = a.pos_dev ? (long long)a.max_seq : (long long)a.pos_host + a.new_seq;
-    // at most 8 chunks per head by default (Qwen3-shaped step at context
-    // 512: 16 / 12 / 10 / 8 / 6 chunks 1,245 / 1,249 / 1,257 / 1,256 / 1,249
-    // tok/s; GPT-2 small batch 1 at a 512-token prompt 3,572 -> 3,591 with 8)
-    static const int max_chunks = [] {
-        const char* e = getenv("GORCH_HIP_SPLIT_MAX_CHUNKS");
-        return std::max(2, std::min(kAttnSplitMax, e ? atoi(e) : 8));
-    }();
-    const int want = rows == 1 ? std::min(max_chunks, std::max(1, 256 / heads))
-                               : (batch_target * 256 + heads * rows - 1) / (heads * rows);
+    // at most 8 chunks per head (Qwen3-shaped step at context 512: 16 / 12 /
+    // 10 / 8 / 6 chunks 1,245 / 1,249 / 1,257 / 1,256 / 1,249 tok/s; GPT-2
+    // small batch 1 at a 512-token prompt 3,572 -> 3,591 with 8)
+    constexpr int max_chunks = 8;
+    const int want = std::min(max_chunks, std::max(1, 256 / heads));
     const int nc = (int)std::min<long long>(std::min(kAttnSplitMax, want), (keys + kc - 1) / kc);
-    if (nc < 2 || a.split_ws_floats < (long long)rows * heads * nc * (a.hd + 2)) return 0;
+    if (nc < 2 || a.split_ws_floats < (long long)heads * nc * (a.hd + 2)) return 0;
     return nc;
 }
 
@@ -1060,18 +1048,8 @@ static AttnRoute attn_route(const AttnArgs& a, int heads, int rows) {
     const long long visible = a.pos_dev ? (long long)a.max_seq : (long long)a.pos_host + a.new_seq;
     const bool lds_ok = (size_t)visible * sizeof(float) <= kAttnMaxLdsBytes;
     const int blocks = heads * rows;
-    static const int rows_kernel = [] {
-        const char* e = getenv("GORCH_HIP_ATTN_ROWS");
-        return e ? atoi(e) : 1;
-    }();
-    static const int flash_min = [] {
-        const char* e = getenv("GORCH_HIP_ATTN_FLASH_MIN_ROWS");
-        return e ? atoi(e) : 32;
-    }();
-    static const int long_kernel = [] {
-        const char* e = getenv("GORCH_HIP_ATTN_LONG");
-        return e ? atoi(e) : 1;
-    }();
+    // new rows per sequence from which the matrix-core prefill kernel runs
+    constexpr int flash_min = 32;
     const bool aligned = (a.q_stride % 4 == 0) && (a.dim % 4 == 0) && ((a.kv_dim ? a.kv_dim : a.dim) % 4 == 0) &&
                          ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.kc) |
                            reinterpret_cast<uintptr_t>(a.vc) | reinterpret_cast<uintptr_t>(a.out)) % 16 == 0);
@@ -1081,14 +1059,14 @@ static AttnRoute attn_route(const AttnArgs& a, int heads, int rows) {
     };
     // split QKV partials: only the two-pass kernel adds them
     if (a.qkv_part) return cached();
-    if (flash_min > 0 && aligned && a.new_seq >= flash_min && (a.hd == 64 || a.hd == 128)) return kRouteFlash;
+    if (aligned && a.new_seq >= flash_min && (a.hd == 64 || a.hd == 128)) return kRouteFlash;
     // one row over few heads: each head's keys over several CUs
-    if (long_kernel && aligned && (blocks < 128 || rows > 1) && attn_split_chunks(a, heads, rows)) return kRouteSplit;
-    if (rows_kernel && aligned && a.max_seq <= 256 && (a.hd == 64 || a.hd == 128 || a.hd == 32 || a.hd == 16))
+    if (aligned && blocks < 128 && attn_split_chunks(a, heads, rows)) return kRouteSplit;
+    if (aligned && a.max_seq <= 256 && (a.hd == 64 || a.hd == 128 || a.hd == 32 || a.hd == 16))
         return kRouteRows;
     // (measured: XL batch 16, 400 blocks, two-pass 25 vs online-softmax
     // 29.4 us per layer)
-    if (long_kernel && aligned && (blocks < 128 || !lds_ok) && (a.hd == 64 || a.hd == 128)) return kRouteLong;
+    if (aligned && (blocks < 128 || !lds_ok) && (a.hd == 64 || a.hd == 128)) return kRouteLong;
     return cached();
 }
 

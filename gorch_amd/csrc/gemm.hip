@@ -496,48 +496,26 @@ static void launch_db(hipStream_t s, const float* A, const uint16_t* W, const fl
 template <int BM, int BN, bool SPLIT>
 static void launch_gemm_t(hipStream_t s, const float* A, const uint16_t* W, const float* bias,
                           const float* residual, const OutDesc& od, int M, int N, int K, int epilogue) {
-    static const int pf_env = [] {
-        const char* e = getenv("GORCH_HIP_GEMM_PF");
-        return e ? atoi(e) : 0;
-    }();
     dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-    // measured: one register stage for 128 x 128 tiles (more stages cost
-    // occupancy: 4096^3 247 vs 301 us), two for the smaller tiles
-    const int pf = pf_env ? pf_env : (BM * BN >= 128 * 128 ? 1 : 2);
-    // no K tail and a step count the stages divide: loads with no bound on k
-    // (a select on every offset compiles to branches around the loads)
-    const int nk = (K + kBK - 1) / kBK;
-    const bool kt = K % kBK != 0 || nk % pf != 0;
-#define GH_GEMM_L(PFV, KTV)                                                                                    \
-    hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT, PFV, KTV>), grid, dim3(256), 0, s, A, W, bias, residual, od, M, \
-                       N, K, epilogue)
-    if (pf == 1) {
-        if (kt) GH_GEMM_L(1, true);
-        else GH_GEMM_L(1, false);
-    } else if (pf == 2) {
-        if (kt) GH_GEMM_L(2, true);
-        else GH_GEMM_L(2, false);
-    } else {
-        if (kt) GH_GEMM_L(3, true);
-        else GH_GEMM_L(3, false);
-    }
-#undef GH_GEMM_L
+    // one register stage for 128 x 128 tiles (more stages cost occupancy:
+    // 4096^3 247 vs 301 us); no K tail: loads with no bound on k (a select
+    // on every offset compiles to branches around the loads)
+    constexpr int pf = 1;
+    if (K % kBK != 0)
+        hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT, pf, true>), grid, dim3(256), 0, s, A, W, bias, residual, od, M,
+                           N, K, epilogue);
+    else
+        hipLaunchKernelGGL((k_gemm_bf16w<BM, BN, SPLIT, pf, false>), grid, dim3(256), 0, s, A, W, bias, residual, od,
+                           M, N, K, epilogue);
 }
 
 // Tile choice: 128 x 128 tiles (k_gemm_bf16w) when they give every CU a
 // block, else the double-buffered 64-row kernel (k_gemm_db).
-// GORCH_HIP_GEMM_TILE = 2 / 3 forces one of them.
 int launch_gemm_bf16w(hipStream_t s, const float* A, const uint16_t* W, const float* bias,
                       const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
                       bool act_bf16) {
     const long long big = (long long)((M + 127) / 128) * ((N + 127) / 128);
-    int tile = big >= 256 ? 2 : 3;
-    static const int tile_env = [] {
-        const char* e = getenv("GORCH_HIP_GEMM_TILE");
-        return e ? atoi(e) : -1;
-    }();
-    if (tile_env == 2 || tile_env == 3) tile = tile_env;
-    if (tile == 3) {
+    if (big < 256) {
         if (act_bf16) launch_db<false>(s, A, W, bias, residual, od, M, N, K, epilogue);
         else launch_db<true>(s, A, W, bias, residual, od, M, N, K, epilogue);
     } else if (act_bf16) {

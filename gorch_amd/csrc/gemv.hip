@@ -208,10 +208,6 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
     }
 }
 
-static int env_int(const char* name, int dflt) {
-    const char* s = getenv(name);
-    return s ? atoi(s) : dflt;
-}
 
 // ---------------------------------------------------------------------------
 // VALU GEMV for M <= 4 (decode batch 1..4): the weight stream uses the
@@ -797,7 +793,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
 }
 
 // ---------------------------------------------------------------------------
-// Persistent multi-row GEMV for 2 <= M <= 16 over 128+ weight tiles.
+// Persistent multi-row GEMV for 1 <= M <= 16 over tile-packed weights.
 //
 // A block is NW waves; wave w owns k-steps [w*ks, (w+1)*ks) of every 16-row
 // weight tile. It loads the activation A fragments of that K range once, as
@@ -810,7 +806,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
 // residual, output, argmax keys). Every load is a raw buffer load with no
 // branch around it: k past the wave's range, rows past M or N and tiles
 // past the last read as zeros.
-template <int NW, int KS, bool PACKED, bool EARLY, bool LN>
+template <int NW, int KS, bool EARLY, bool LN>
 __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict__ x, const uint16_t* __restrict__ W,
                                                         const float* __restrict__ bias, const float* residual,
                                                         OutDesc od, int M, int N, int K, int ks, int epilogue,
@@ -868,19 +864,18 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
         u32x4 w[KS];
         float b, res;
     };
-    // packed: tile t is 16 * K32 bf16 from W + t * 16 * K32 (K32 = K rounded
-    // up to 32), fragment (t, k-step j) the 1 KB at byte 1024 * j, lane l's
-    // 16 bytes at 16 * l; row-major: row n at W + n * K
+    // tile t is 16 * K32 bf16 from W + t * 16 * K32 (K32 = K rounded up to
+    // 32), fragment (t, k-step j) the 1 KB at byte 1024 * j, lane l's 16
+    // bytes at 16 * l
     const int K32 = (K + 31) & ~31;
     auto load = [&](int t, Tile& tl) {
         const int rows = max(0, min(16, N - 16 * t));
         const __amdgpu_buffer_rsrc_t rs =
-            PACKED ? make_rsrc(W + (size_t)t * 16 * K32, t < ntiles ? (long long)16 * K32 * 2 : 0)
-                   : make_rsrc(W + (size_t)t * 16 * K, (long long)rows * K * 2);
+            make_rsrc(W + (size_t)t * 16 * K32, t < ntiles ? (long long)16 * K32 * 2 : 0);
 #pragma unroll
         for (int u = 0; u < KS; u++) {
             const int kc = kb + 32 * u + 8 * g;
-            const int off = PACKED ? (kb + 32 * u) * 32 + 16 * lane : (r * K + kc) * 2;
+            const int off = (kb + 32 * u) * 32 + 16 * lane;
             tl.w[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, kc < ke ? off : kOutOfRange, 0, kStreamPolicy);
         }
         // this lane's output column's bias and residual
@@ -1090,26 +1085,24 @@ static void m1_shape(int K, int* T, int* C) {
 }
 
 bool gemv_pair_swiglu_ok(int F, int K) {
-    return F > 0 && K % 256 == 0 && K / 256 >= 1 && K / 256 <= 8 && (long long)2 * F * K * 2 < (1ll << 31) &&
-           env_int("GORCH_HIP_PAIR_SWIGLU", 1);
+    return F > 0 && K % 256 == 0 && K / 256 >= 1 && K / 256 <= 8 && (long long)2 * F * K * 2 < (1ll << 31);
 }
 
 bool gemv_m1_prologue_ok(int K) {
     int T1, C1;
     m1_shape(K, &T1, &C1);
-    return T1 != 0 && env_int("GORCH_HIP_GEMV_M1", 1) && env_int("GORCH_HIP_GEMV_VALU_MAX_M", 1) >= 1 &&
-           K % 8 == 0;
+    return T1 != 0 && K % 8 == 0;
 }
 
 static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const float* bias, const float* residual,
                      const OutDesc& od, int N, int K, int epilogue, const LinearExtras& ex, int T, int C) {
     const int rpi = 64 / T;
     const int ngroups = (N + rpi - 1) / rpi;
-    static const int max_blocks = env_int("GORCH_HIP_GEMV_M1_BLOCKS", 768);
+    constexpr int max_blocks = 768;
     // with the argmax fusion every block ends in one 64-bit atomicMax on the
     // same global word, and those serialise at one L2 channel (4096 of them
     // cost ~40 us): fewer, longer-running blocks
-    static const int max_blocks_argmax = env_int("GORCH_HIP_GEMV_M1_ARGMAX_BLOCKS", 512);
+    constexpr int max_blocks_argmax = 512;
     // one row group per wave; two with a fused LayerNorm, whose activation,
     // gamma and beta rows every wave loads whole (GPT-2 small batch-1 decode
     // with 1, 3 or 4 groups per wave: 4,135 / 4,168 / 4,023 tok/s, 2: 4,450)
@@ -1118,7 +1111,6 @@ static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const flo
     if (ex.argmax_key && blocks > max_blocks_argmax) blocks = max_blocks_argmax;
     // between one and two blocks per CU: one per CU, each taking more row
     // groups (a second block on a CU doubles that CU's time)
-    static const int cap = env_int("GORCH_HIP_M1_CAP", 1);
     static const int cus = [] {
         int dev = 0, n = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -1126,7 +1118,7 @@ static int launch_m1(hipStream_t s, const float* x, const uint16_t* W, const flo
             n = 256;
         return n;
     }();
-    if (cap && blocks > cus && blocks < 2 * cus) blocks = cus;
+    if (blocks > cus && blocks < 2 * cus) blocks = cus;
     const int pro = ex.swiglu ? 3 : (ex.ln_g ? (ex.ln_rms ? 2 : 1) : 0);
 #define GH_M1_L(TT, CC, PV)                                                                                 \
     hipLaunchKernelGGL((k_gemv_m1<TT, CC, PV>), dim3(blocks), dim3(256), 0, s, x, W, bias, residual, od, N, K, \
@@ -1173,19 +1165,14 @@ constexpr size_t kMtLds = 128 * 1024;
 
 // Multi-row GEMV launch; returns -1 when the activations do not fit LDS
 // (the caller then uses the in-block-split MFMA kernel).
-// GORCH_HIP_MT_{NW,ST,BPS} override the plan.
 static int launch_mt(hipStream_t s, const float* x, const uint16_t* W, const float* bias, const float* residual,
                      const OutDesc& od, int M, int N, int K, int epilogue, const LinearExtras& ex) {
-    static const int nw_env = env_int("GORCH_HIP_MT_NW", 0);
-    static const int st_env = env_int("GORCH_HIP_MT_ST", 0);
-    static const int bps_env = env_int("GORCH_HIP_MT_BPS", 0);
     const int ntiles = (N + 15) / 16;
     const int mr = M <= 4 ? 4 : (M <= 8 ? 8 : 16);
     const size_t lds = (size_t)((K + 127) / 128) * 16 * mr * 16 * 2;
     if (lds > kMtLds || residual) return -1;  // the kernel has no residual add
-    const int nw = nw_env ? nw_env : 16;
-    const int st = st_env ? st_env : 2;
-    const int bps = bps_env ? bps_env : std::min(256, ntiles);
+    const int nw = 16, st = 2;
+    const int bps = std::min(256, ntiles);
     int rc = -1;
 #define GH_MT(NWV, STV, MRV)                                                                                 \
     if (nw == NWV && st == STV && mr == MRV)                                                                 \
@@ -1201,19 +1188,16 @@ static int launch_mt(hipStream_t s, const float* x, const uint16_t* W, const flo
 }
 
 // Persistent multi-row GEMV launch; -1 when K exceeds 8 x 12 k-steps.
-// GORCH_HIP_TILES_{NW,BLOCKS} override the plan.
 static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const float* bias, const float* residual,
-                        const OutDesc& od, int M, int N, int K, int epilogue, const LinearExtras& ex, bool packed) {
-    static const int nw_env = env_int("GORCH_HIP_TILES_NW", 0);
-    static const int auto_nw4 = env_int("GORCH_HIP_TILES_NW4", 1);
+                        const OutDesc& od, int M, int N, int K, int epilogue, const LinearExtras& ex) {
+
     static const int cus = [] {
         int dev = 0, n = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
             n = 256;
-        return env_int("GORCH_HIP_TILES_CAP", n);
+        return n;
     }();
-    static const int blocks_env = env_int("GORCH_HIP_TILES_BLOCKS", 0);
     const int ntiles = (N + 15) / 16;
     // with ex.part the grid's y dimension is ex.ksplit K slices of ex.kslice
     const int S = ex.part ? ex.ksplit : 1;
@@ -1222,8 +1206,8 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
     // weight is short in tiles for the grid) and a 4-wave instantiation
     // takes the k-steps (measured: 9-shape GEMV sweep, 768x3072 at M = 4 /
     // 16 3.43 / 3.95 -> 3.21 / 3.74 us; the LM head keeps 8)
-    int nw = nw_env ? nw_env : 8;
-    if (!nw_env && !ex.ln_g && auto_nw4) {
+    int nw = 8;
+    if (!ex.ln_g) {
         const int ks4 = (ksteps + 3) / 4;
         const bool fits4 = ks4 <= 8 && ks4 != 5 && ks4 != 7;
         if (fits4 && ntiles * S <= 2 * cus) nw = 4;
@@ -1237,24 +1221,24 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0) != hipSuccess || per_cu < 1)
             per_cu = 1, cus = cus > 0 ? cus : 256;
-        return blocks_env ? blocks_env : per_cu * cus;
+        return per_cu * cus;
     };
-#define GH_TILES_L(NWV, KSV, PK, EA)                                                                    \
-    hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, PK, EA, false>), dim3(blocks, S), dim3(NWV * 64), 0, s, x, W, \
-                       bias, residual, od, M, N, K, ks, epilogue, ex)
+#define GH_TILES_L(NWV, KSV, EA)                                                                        \
+    hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, EA, false>), dim3(blocks, S), dim3(NWV * 64), 0, s, x, W, bias, \
+                       residual, od, M, N, K, ks, epilogue, ex)
     // fused LayerNorm: packed weights, 8 waves, K <= 1024 (the LM head of a
     // one-row decode step)
     if (ex.ln_g) {
-        if (!packed || nw != 8 || ks > 4 || S != 1) return -1;
+        if (nw != 8 || ks > 4 || S != 1) return -1;
         static const int blocks_ln =
-            blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<8, 4, true, false, true>), 512);
+            blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<8, 4, false, true>), 512);
         const int blocks = std::min(blocks_ln, ntiles);
 #define GH_TILES_LN(KSV)                                                                                    \
     if (ntiles <= 2 * blocks)                                                                               \
-        hipLaunchKernelGGL((k_gemv_tiles<8, KSV, true, true, true>), dim3(blocks), dim3(512), 0, s, x, W, bias, \
+        hipLaunchKernelGGL((k_gemv_tiles<8, KSV, true, true>), dim3(blocks), dim3(512), 0, s, x, W, bias, \
                            residual, od, M, N, K, ks, epilogue, ex);                                        \
     else                                                                                                    \
-        hipLaunchKernelGGL((k_gemv_tiles<8, KSV, true, false, true>), dim3(blocks), dim3(512), 0, s, x, W, bias, \
+        hipLaunchKernelGGL((k_gemv_tiles<8, KSV, false, true>), dim3(blocks), dim3(512), 0, s, x, W, bias, \
                            residual, od, M, N, K, ks, epilogue, ex);
         if (ks <= 3) {
             GH_TILES_LN(3)
@@ -1271,15 +1255,11 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
     // of 73 blocks each, 5,059 -> 5,146 tok/s)
 #define GH_TILES(NWV, KSV)                                                                                \
     if (nw == NWV && ks <= KSV) {                                                                         \
-        static const int blocks_p = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, true, false, false>), NWV * 64); \
-        static const int blocks_r = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, false, false, false>), NWV * 64); \
-        int blocks = std::min(std::max(1, (packed ? blocks_p : blocks_r) / S), ntiles);                   \
+        static const int blocks_p = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, false, false>), NWV * 64); \
+        int blocks = std::min(std::max(1, blocks_p / S), ntiles);                                         \
         if (ntiles <= 2 * blocks) blocks = std::min(blocks, std::max(1, cus / S));                        \
-        const bool early = ntiles <= 2 * blocks;                                                          \
-        if (packed && early) GH_TILES_L(NWV, KSV, true, true);                                            \
-        else if (packed) GH_TILES_L(NWV, KSV, true, false);                                               \
-        else if (early) GH_TILES_L(NWV, KSV, false, true);                                                \
-        else GH_TILES_L(NWV, KSV, false, false);                                                          \
+        if (ntiles <= 2 * blocks) GH_TILES_L(NWV, KSV, true);                                             \
+        else GH_TILES_L(NWV, KSV, false);                                                                 \
         count(CNT_GEMV);                                                                                  \
         return check_launch("gemv_tiles");                                                                \
     }
@@ -1300,7 +1280,7 @@ static int launch_valu_mt(hipStream_t s, const float* x, const uint16_t* W, cons
                           const OutDesc& od, int M, int N, int K, int epilogue, const LinearExtras& ex, int T) {
     const int rpi = 64 / T;
     const int ngroups = (N + rpi - 1) / rpi;
-    static const int max_blocks = env_int("GORCH_HIP_GEMV_VALU_BLOCKS", 2048);
+    constexpr int max_blocks = 2048;
     int blocks = (ngroups + 3) / 4;
     if (blocks > max_blocks) blocks = max_blocks;
     const size_t lds = (size_t)MT * K * sizeof(float);
@@ -1333,15 +1313,12 @@ static int valu_lanes_per_row(int K) {
 
 // Launch plan: NT weight tiles and NW K-splitting waves per block, chosen
 // from a sweep of the decode shapes (GPT-2 small and XL, M = 1..16) on
-// MI355X. GORCH_HIP_GEMV_NT / GORCH_HIP_GEMV_NW override them.
+// MI355X.
 struct GemvPlan {
     int nt, nw, u;
 };
 
 static GemvPlan plan_gemv(int M, int N, int K) {
-    static const int nt_env = env_int("GORCH_HIP_GEMV_NT", 0);
-    static const int nw_env = env_int("GORCH_HIP_GEMV_NW", 0);
-    static const int u_env = env_int("GORCH_HIP_GEMV_U", 0);
     const int ntiles = (N + 15) / 16;
     GemvPlan p;
     if (ntiles >= 2048) {          // LM-head class: many tiles
@@ -1368,9 +1345,6 @@ static GemvPlan plan_gemv(int M, int N, int K) {
     }
     // keep at least one 32-wide k-step per wave
     while (p.nw > 1 && (K + p.nw - 1) / p.nw < 32) p.nw /= 2;
-    if (nt_env) p.nt = nt_env;
-    if (nw_env) p.nw = nw_env;
-    if (u_env) p.u = u_env;
     return p;
 }
 
@@ -1407,8 +1381,7 @@ static int launch_mfma_gemv(hipStream_t s, const float* x, const uint16_t* W, co
     if (ex.part) {
         // more tiles per block: each block's activation slice then feeds
         // more weight rows
-        static const int split_nt_env = env_int("GORCH_HIP_SPLIT_NT", 0);
-        const int split_nt = split_nt_env ? split_nt_env : (ex.split_nt ? ex.split_nt : 4);
+        const int split_nt = ex.split_nt ? ex.split_nt : 4;
         if ((N + 15) / 16 >= 4 * split_nt) p.nt = split_nt;
         ex.kslice = ((K + ex.ksplit - 1) / ex.ksplit + 31) / 32 * 32;
         span = ex.kslice;
@@ -1467,12 +1440,11 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
     // cannot pull the weight at full rate). Wider weights stay unsplit:
     // 8-tile K-slice blocks measured slower at 16 rows (12.5 vs 9.4 us at
     // K 1600, N 4800) once the epilogue kernel is counted.
-    static const int auto_split = env_int("GORCH_HIP_GEMV_SPLIT", 1);
-    static const int split_blocks = env_int("GORCH_HIP_GEMV_SPLIT_BLOCKS", 300);
-    static const int split_max_tiles = env_int("GORCH_HIP_GEMV_SPLIT_MAX_TILES", 128);
-    static const int split_nt_wide = env_int("GORCH_HIP_GEMV_SPLIT_NT_WIDE", 2);
+    constexpr int split_blocks = 300;
+    constexpr int split_max_tiles = 128;
+    constexpr int split_nt_wide = 2;
     const int ntiles_all = (N + 15) / 16;
-    if (auto_split && M >= 2 && !ex.argmax_key && ntiles_all < split_max_tiles && K >= 1024) {
+    if (M >= 2 && !ex.argmax_key && ntiles_all < split_max_tiles && K >= 1024) {
         const int nt = ntiles_all >= 128 ? split_nt_wide : 2;
         const int blocks_per_slice = (ntiles_all + nt - 1) / nt;
         const int S = ksplit_slices(K, std::min(kEpiSlices, std::max(2, split_blocks / blocks_per_slice)));
@@ -1496,8 +1468,6 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
             return launch_splitk_epilogue(s, sx.part, S, M, N, bias, residual, od, epilogue);
         }
     }
-    static const int valu_max_m = env_int("GORCH_HIP_GEMV_VALU_MAX_M", 1);
-    static const int m1_on = env_int("GORCH_HIP_GEMV_M1", 1);
     // M = 1: the register-activation kernel whenever K fits its shape table
     // (K/8 = T*C with C <= 8), else the LDS-staged VALU kernel.
     if (ex.pair_swiglu) {
@@ -1509,7 +1479,7 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
         }
         return launch_m1(s, x, W, nullptr, nullptr, od, N, K, GORCH_HIP_EPI_NONE, ex, 32, K / 256);
     }
-    if (M == 1 && valu_max_m >= 1 && m1_on) {
+    if (M == 1) {
         int T1, C1;
         m1_shape(K, &T1, &C1);
         if (T1) {
@@ -1521,22 +1491,15 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
         set_error("linear_bf16: the RMSNorm / SwiGLU prologues need one row with K/8 = T*C (T in 8..64, C <= 8)");
         return GORCH_HIP_EUNSUPPORTED;
     }
-    static const int tiles_on = env_int("GORCH_HIP_GEMV_TILES", 0);
-    if (tiles_on && M >= 2 && !ex.ln_g && (N + 15) / 16 >= 128) {
-        int rc = launch_tiles(s, x, W, bias, residual, od, M, N, K, epilogue, ex, false);
-        if (rc >= 0) return rc;
-    }
-    static const int mt_on = env_int("GORCH_HIP_MT", 1);
-    if (M >= 2 && mt_on && (N + 15) / 16 >= 1024) {
+    if (M >= 2 && (N + 15) / 16 >= 1024) {
         int rc = launch_mt(s, x, W, bias, residual, od, M, N, K, epilogue, ex);
         if (rc >= 0) return rc;
     }
     const int T = valu_lanes_per_row(K);
-    if (M <= valu_max_m && T && (size_t)4 * K * sizeof(float) <= 64 * 1024) {
-        if (M == 1) return launch_valu_mt<1>(s, x, W, bias, residual, od, M, N, K, epilogue, ex, T);
-        if (M == 2) return launch_valu_mt<2>(s, x, W, bias, residual, od, M, N, K, epilogue, ex, T);
-        return launch_valu_mt<4>(s, x, W, bias, residual, od, M, N, K, epilogue, ex, T);
-    }
+    // one row whose K the register kernel's shape table does not take: the
+    // LDS-staged VALU kernel (2..16 rows run on the matrix cores)
+    if (M == 1 && T && (size_t)4 * K * sizeof(float) <= 64 * 1024)
+        return launch_valu_mt<1>(s, x, W, bias, residual, od, M, N, K, epilogue, ex, T);
     return launch_mfma_gemv(s, x, W, bias, residual, od, M, N, K, epilogue, ex);
 }
 
@@ -1578,7 +1541,7 @@ int launch_pack_bf16(hipStream_t s, const uint16_t* W, uint16_t* Wp, int N, int 
 int packed_split_slices(int K, int N) {
     // blocks a K split aims at (3072x768 at M = 4 / 16 with 4-wave blocks:
     // 192 -> 384 took 5.16 / 5.77 to 5.05 / 5.50 us)
-    static const int split_target = env_int("GORCH_HIP_SPLIT_TARGET", 384);
+    constexpr int split_target = 384;
     const int ksteps = (K + 31) / 32, ntiles = (N + 15) / 16;
     int S = std::max((ksteps + 31) / 32, (split_target + ntiles - 1) / ntiles);
     S = std::min(std::min(S, kEpiSlices), std::max(1, ksteps / 3));
@@ -1599,7 +1562,7 @@ int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, c
         sx.kslice = ((K + ex.ksplit - 1) / ex.ksplit + 31) / 32 * 32;
         sx.ksplit = (K + sx.kslice - 1) / sx.kslice;
         const int rc = launch_tiles(s, x, Wp, nullptr, nullptr, OutDesc::plain(nullptr, N), M, N, K,
-                                    GORCH_HIP_EPI_NONE, sx, true);
+                                    GORCH_HIP_EPI_NONE, sx);
         if (rc < 0) set_error("linear_bf16_packed: K slice above 3072 is not supported");
         return rc < 0 ? GORCH_HIP_EUNSUPPORTED : rc;
     }
@@ -1616,14 +1579,14 @@ int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, c
             sx.kslice = ((K + S - 1) / S + 31) / 32 * 32;
             sx.ksplit = (K + sx.kslice - 1) / sx.kslice;
             const int rc = launch_tiles(s, x, Wp, nullptr, nullptr, OutDesc::plain(nullptr, N), M, N, K,
-                                        GORCH_HIP_EPI_NONE, sx, true);
+                                        GORCH_HIP_EPI_NONE, sx);
             if (rc >= 0) {
                 GH_TRY(rc);
                 return launch_splitk_epilogue(s, sx.part, sx.ksplit, M, N, bias, residual, od, epilogue);
             }
         }
     }
-    const int rc = launch_tiles(s, x, Wp, bias, residual, od, M, N, K, epilogue, ex, true);
+    const int rc = launch_tiles(s, x, Wp, bias, residual, od, M, N, K, epilogue, ex);
     if (rc < 0) {
         set_error(ex.ln_g ? "linear_bf16_packed: a fused LayerNorm needs K <= 1024"
                           : "linear_bf16_packed: K above 3072 is not supported");

@@ -159,44 +159,27 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
     // as a plain operand (a LayerNorm fused into the GEMV's loads costs
     // ~3.5 us per call at 16 rows, d 1600, for its gamma/beta loads).
     const bool batched = fused && rows >= 2 && d <= kReduceRowsMaxCols;
-    static const int split_blocks = [] {
-        const char* e = getenv("GORCH_HIP_SPLIT_BLOCKS");
-        return e ? atoi(e) : 300;
-    }();
-    static const int split_nt = [] {
-        const char* e = getenv("GORCH_HIP_SPLIT_NT");
-        return e ? atoi(e) : 4;
-    }();
+    // row-major weights (no packed copy, dim above 3072): the K split aims
+    // at ~300 blocks of 4 tiles
+    constexpr int split_blocks = 300, split_nt = 4;
     // Batched steps over tile-packed weights split the Linears over K: every
     // block of a K slice loads that slice of the activations, so activation
     // traffic is (blocks per slice) x (activation bytes): at 16 rows, d 1600,
     // 1.7x the weight bytes for an unsplit fused QKV and 2.6x for Wo in 2
-    // slices. More slices (GORCH_HIP_QKV_SPLIT, GORCH_HIP_RES_SPLIT) cut it;
+    // slices. More slices cut it;
     // the partials of the fused QKV are added by the two-pass attention
     // kernel, those of Wo and FFN2 by the row reducer. The fused QKV takes 3
     // slices by default (XL batch 16, exact-k-step tiles, CU-capped grid:
     // 1 / 2 / 3 / 4 slices 5,249 / 5,330 / 5,335 / 5,240 tok/s).
-    static const int qkv_split_req = [] {
-        const char* e = getenv("GORCH_HIP_QKV_SPLIT");
-        return std::min(kMaxPartSlices, e ? atoi(e) : 3);
-    }();
-    static const int res_split_req = [] {
-        const char* e = getenv("GORCH_HIP_RES_SPLIT");
-        return std::min(kMaxSplit, e ? atoi(e) : 0);
-    }();
+    constexpr int qkv_split_req = 3;
     // deterministic mode keeps the one-row output projection a GEMV of its
     // own (the fused forms add per-head products with float atomics)
     const bool wo_fuse = !deterministic();
-    // Wo's slices (0: the packed-split rule); measured at XL batch 16 (with
-    // the 3-slice QKV): 2 / 3 / 4 / 5 / 6 / 8 slices 5,335 / 5,336 / 5,359 /
-    // 5,332 / 5,258 / 5,254 tok/s
-    static const int wo_split_req = [] {
-        const char* e = getenv("GORCH_HIP_WO_SPLIT");
-        return std::min(kMaxSplit, e ? atoi(e) : 4);
-    }();
-    auto res_split = [&](int K) {
-        return res_split_req > 0 ? ksplit_slices(K, res_split_req) : packed_split_slices(K, d);
-    };
+    // Wo's slices, measured at XL batch 16 (with the 3-slice QKV): 2 / 3 / 4
+    // / 5 / 6 / 8 slices 5,335 / 5,336 / 5,359 / 5,332 / 5,258 / 5,254 tok/s
+    constexpr int wo_split_req = 4;
+    // FFN2's slices: packed_split_slices' rule (7 at XL's 6400 x 1600)
+    auto res_split = [&](int K) { return packed_split_slices(K, d); };
     auto split_for = [&](int K) {
         const int tiles = ((d + 15) / 16 + split_nt - 1) / split_nt;
         int S = std::min(kMaxSplit, std::max(1, split_blocks / tiles));
@@ -235,7 +218,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         // one token per sequence over tile-packed weights: the fused QKV
         // Linear split over K into raw partials; the attention kernel adds
         // the slices and the bias and writes the K/V cache rows
-        const bool qkv_split = batched && w.wqkv_p && n == 1 && qkv_split_req > 1 &&
+        const bool qkv_split = batched && w.wqkv_p && n == 1 &&
                                attn_takes_qkv_part(a, g->heads, rows);
         LinearExtras ln1, ln2;
         if (qkv_split) {
@@ -292,7 +275,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         if (!wo_fused && batched) {
             LinearExtras sp;
             sp.part = g->part;
-            sp.ksplit = w.wo_p ? (wo_split_req > 0 ? ksplit_slices(d, wo_split_req) : res_split(d)) : split_for(d);
+            sp.ksplit = w.wo_p ? ksplit_slices(d, wo_split_req) : split_for(d);
             if (w.wo_p)
                 GH_TRY(launch_linear_packed_od(s, g->att, w.wo_p, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d,
                                                d, GORCH_HIP_EPI_NONE, sp));
@@ -357,11 +340,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         lf.ln_eps = eps;
         lf.x_stride = head_stride;
         lf.argmax_key = all_rows ? nullptr : argmax_key;
-        static const bool head_tiles = [] {
-            const char* e = getenv("GORCH_HIP_HEAD_TILES");
-            return e ? atoi(e) != 0 : true;
-        }();
-        if (g->wlm_p && head_tiles && d <= 1024) {
+        if (g->wlm_p && d <= 1024) {
             // tile-packed head with LayerNorm_f fused: each block normalises
             // the rows it holds in registers, so no separate LayerNorm launch
             GH_TRY(launch_linear_packed_od(s, head_in, g->wlm_p, g->blm, nullptr,
@@ -590,11 +569,7 @@ static gorch_hip_gpt* gpt_finish(gorch_hip_gpt* g) {
         gorch_hip_gpt_free(g);
         return nullptr;
     }
-    static const int packed_on = [] {
-        const char* e = getenv("GORCH_HIP_PACKED");
-        return e ? atoi(e) : 1;
-    }();
-    if (packed_on && g->dim <= 3072) {
+    if (g->dim <= 3072) {
         const int D = g->dim;
         const size_t pq = align256(packed_bf16_elems(3 * D, D) * 2), p1 = align256(packed_bf16_elems(4 * D, D) * 2);
         const size_t po = align256(packed_bf16_elems(D, D) * 2), p2 = align256(packed_bf16_elems(D, 4 * D) * 2);

@@ -10,7 +10,7 @@
 //   k_moe_route      one block: stable counting sort of the (token, slot)
 //                    assignments by expert, the inverse map, and the tile
 //                    table of the grouped GEMMs;
-//   k_moe_gather     packs each expert's rows contiguously (Xg), as bf16
+//   k_moe_gather_split packs each expert's rows contiguously (Xg), as bf16
 //                    hi/lo planes for the wide-tile GEMMs (gemm_wide.h);
 //   grouped GEMM 1   H = SwiGLU(Xg We_gate^T + bg, Xg We_up^T + bu): gate and
 //                    up tiles accumulate side by side, SwiGLU in the epilogue;
@@ -25,12 +25,9 @@
 
 namespace gh {
 
-// Grouped-GEMM tiles: kMoeBM packed rows (the routing tile table's unit) x
-// BN output columns, K stepped by kMoeBK. 64 x 64 measured faster than
-// 128-row tiles here (more resident blocks per CU), although the larger
-// tile halves the weight re-reads through L2.
-constexpr int kMoeBM = 64, kMoeBK = 64, kMoeLD = kMoeBK + 16;
-constexpr int kMoeBNDual = 64, kMoeBNDown = 64;
+// The tile table's row unit for sizing: at most M*K / kMoeBM + E + 1 row
+// tiles (the grouped GEMMs take 128-row tiles, kWideBM, so fewer are used).
+constexpr int kMoeBM = 64;
 constexpr int kMaxExperts = 64;
 constexpr int kDownSlices = 2;  // K slices of the wide down GEMM at most
 constexpr int kMaxTopK = 8;
@@ -306,16 +303,6 @@ __global__ __launch_bounds__(kRouteThreads) void k_moe_route(int M, int E, int K
         }
 }
 
-__global__ void k_moe_gather(const float* __restrict__ x, const int* __restrict__ perm_tok, float* xg, int rows,
-                             int dim) {
-    const int d4 = dim / 4;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)rows * d4;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int p = (int)(i / d4), c = (int)(i - (int64_t)p * d4);
-        reinterpret_cast<float4*>(xg)[i] = reinterpret_cast<const float4*>(x + (size_t)perm_tok[p] * dim)[c];
-    }
-}
-
 // out[t] = sum over the token's K packed rows in ascending expert order
 // (the reference adds each expert's ScatterAdd contribution in order). One
 // thread per (token, 4 columns); dim % 4 == 0. nsl > 1: the down GEMM left
@@ -403,159 +390,17 @@ __global__ void k_moe_combine(const float* __restrict__ yg, const int* __restric
     }
 }
 
-// Grouped GEMM over the tile table: blockIdx.y = m-tile (expert, packed rows),
-// blockIdx.x = 64-wide n tile. A rows are f32 (split into bf16 hi + lo), the
-// expert's weights bf16 [N, Kd]. DUAL: a second weight (up) accumulates
-// beside the first (gate) and the epilogue writes SwiGLU(gate, up). Else the
-// epilogue multiplies by the packed row's routing weight.
-template <bool DUAL, int BN>
-__global__ __launch_bounds__(256) void k_moe_gemm(const float* __restrict__ A, const uint16_t* __restrict__ W1,
-                                                  const uint16_t* __restrict__ W2, const float* __restrict__ b1,
-                                                  const float* __restrict__ b2, float* __restrict__ C, int N,
-                                                  int Kd, MoeWs ws) {
-    constexpr int NB = DUAL ? 2 : 1;
-    constexpr int BM = kMoeBM;
-    constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;  // 2x2 waves
-    constexpr int A_F4 = BM * kMoeBK / 4 / 256, W_U4 = BN * kMoeBK / 8 / 256;
-    __shared__ __align__(16) uint16_t As[2][BM][kMoeLD];
-    __shared__ __align__(16) uint16_t Ws[NB][BN][kMoeLD];
-    if ((int)blockIdx.y >= *ws.ntiles) return;
-    const int e = ws.tile_e[blockIdx.y], r0 = ws.tile_r0[blockIdx.y], nrows = ws.tile_n[blockIdx.y];
-    const int n0 = blockIdx.x * BN;
-    const uint16_t* Wb[2] = {W1 + (size_t)e * N * Kd, DUAL ? W2 + (size_t)e * N * Kd : nullptr};
-    const float* bb[2] = {b1 ? b1 + (size_t)e * N : nullptr, (DUAL && b2) ? b2 + (size_t)e * N : nullptr};
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int r = lane & 15, g = lane >> 4;
-    float4 ra[A_F4];
-    uint4 rw[NB][W_U4];
-    auto gload = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < A_F4; i++) {
-            const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
-            const int k = k0 + 4 * c4;
-            ra[i] = (row < nrows && k < Kd) ? *reinterpret_cast<const float4*>(A + (size_t)(r0 + row) * Kd + k)
-                                            : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int b = 0; b < NB; b++)
-#pragma unroll
-            for (int i = 0; i < W_U4; i++) {
-                const int idx = tid + 256 * i, row = idx >> 3, c8 = idx & 7;
-                const int n = n0 + row, k = k0 + 8 * c8;
-                rw[b][i] = (n < N && k < Kd) ? *reinterpret_cast<const uint4*>(Wb[b] + (size_t)n * Kd + k)
-                                             : make_uint4(0, 0, 0, 0);
-            }
-    };
-    auto sstore = [&]() {
-#pragma unroll
-        for (int i = 0; i < A_F4; i++) {
-            const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
-            const float f[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
-            uint16_t hi[4], lo[4];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                uint32_t u = __float_as_uint(f[q]) & 0xffff0000u;
-                hi[q] = (uint16_t)(u >> 16);
-                lo[q] = __builtin_bit_cast(uint16_t, (__bf16)(f[q] - __uint_as_float(u)));
-            }
-            *reinterpret_cast<uint2*>(&As[0][row][4 * c4]) =
-                make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
-            *reinterpret_cast<uint2*>(&As[1][row][4 * c4]) =
-                make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
-        }
-#pragma unroll
-        for (int b = 0; b < NB; b++)
-#pragma unroll
-            for (int i = 0; i < W_U4; i++) {
-                const int idx = tid + 256 * i, row = idx >> 3, c8 = idx & 7;
-                *reinterpret_cast<uint4*>(&Ws[b][row][8 * c8]) = rw[b][i];
-            }
-    };
-
-    floatx4 acc[NB][TM][TN];
-#pragma unroll
-    for (int b = 0; b < NB; b++)
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int j = 0; j < TN; j++) acc[b][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    gload(0);
-    for (int k0 = 0; k0 < Kd; k0 += kMoeBK) {
-        __syncthreads();
-        sstore();
-        __syncthreads();
-        if (k0 + kMoeBK < Kd) gload(k0 + kMoeBK);
-#pragma unroll
-        for (int kk = 0; kk < kMoeBK; kk += 32) {
-            bf16x8 wf[NB][TN];
-#pragma unroll
-            for (int b = 0; b < NB; b++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    wf[b][j] = *reinterpret_cast<const bf16x8*>(&Ws[b][wn * WN + j * 16 + r][kk + 8 * g]);
-#pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const bf16x8 ahi = *reinterpret_cast<const bf16x8*>(&As[0][wm * WM + i * 16 + r][kk + 8 * g]);
-                const bf16x8 alo = *reinterpret_cast<const bf16x8*>(&As[1][wm * WM + i * 16 + r][kk + 8 * g]);
-#pragma unroll
-                for (int b = 0; b < NB; b++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++) {
-                        acc[b][i][j] = mfma16x16x32(ahi, wf[b][j], acc[b][i][j]);
-                        acc[b][i][j] = mfma16x16x32(alo, wf[b][j], acc[b][i][j]);
-                    }
-            }
-        }
-    }
-
-    float bn[NB][TN];
-#pragma unroll
-    for (int b = 0; b < NB; b++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int n = n0 + wn * WN + j * 16 + r;
-            bn[b][j] = (bb[b] && n < N) ? bb[b][n] : 0.f;
-        }
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int n = n0 + wn * WN + j * 16 + r;
-            if (n >= N) continue;
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int row = wm * WM + i * 16 + 4 * g + v;
-                if (row >= nrows) continue;
-                const int p = r0 + row;
-                float s = acc[0][i][j][v];
-                if (bb[0]) s = s + bn[0][j];
-                if (DUAL) {
-                    float u = acc[NB - 1][i][j][v];
-                    if (bb[1]) u = u + bn[NB - 1][j];
-                    s = s * sigmoidf_ref(s) * u;  // SwiGLU: gate * sigma(gate) * up
-                } else {
-                    s = s * ws.perm_w[p];          // weighted = exOut * w
-                }
-                C[(size_t)p * N + n] = s;
-            }
-        }
-}
-
 // Wide-tile path. The gather writes Xg as two bf16 planes (hi, lo: x = hi +
 // lo to ~2^-16 relative, the split the MFMA kernels use) in the space of the
 // f32 Xg, and GEMM 1's epilogue writes H the same way, so both GEMMs load
 // 16-byte bf16 words only. Rows are grouped in 128-row tiles. The down GEMM
 // keeps 256-wide tiles although at d = 1024 that leaves half the CUs idle:
 // 128-wide tiles on every CU measured slower (148 vs 121 us, 2048 tokens).
-// GORCH_HIP_MOE_WIDE=0 selects the 64 x 64 f32-activation kernels;
-// GORCH_HIP_MOE_DOWN_BN=128 the narrower down tile; GORCH_HIP_MOE_DOWN_SPLIT=2
-// splits the down GEMM's K over twice the blocks (raw partials, summed with
-// bias and routing weight by the combine), which measured within noise of
-// the unsplit kernel (118 vs 121 us): these GEMMs are bound by the traffic
-// from beyond L2, not by the number of busy CUs.
+// Splitting the down GEMM's K over twice the blocks (raw partials, summed
+// with bias and routing weight by the combine) measured within noise of the
+// unsplit kernel (118 vs 121 us): these GEMMs are bound by the traffic from
+// beyond L2, not by the number of busy CUs. (64 x 64 tiles over f32
+// activations were slower than these 128-row bf16 hi/lo tiles.)
 constexpr int kWideBM = 128, kWideBNDual = 128, kWideBNDown = 256;
 
 // Token-major: item (t, chunk c) loads x's chunk and the token's K packed
@@ -739,68 +584,25 @@ static int launch_moe_wide_t(hipStream_t s, dim3 grid, const uint16_t* Ahi, cons
     return check_launch(DUAL ? "moe_wide_gate_up" : "moe_wide_down");
 }
 
-// GORCH_HIP_MOE_IL=0 keeps the compiler's own schedule of the main loop
+// The expert GEMMs run 16 waves (4 x 4) per block, with the interleaved
+// stage schedule and one register set for the global loads (measured,
+// against 8-wave blocks and the compiler's own schedule: gate/up 180 -> 159
+// us, down 108 -> 96 us at the MoE layer config). The down GEMM stages its
+// finished tile in LDS for 16-byte stores (100.6 -> 97.3 us; gate/up 164.7 ->
+// 165.9, so only down) and takes the XCD-contiguous block order.
 template <bool DUAL, int BNW>
 static int launch_moe_wide(hipStream_t s, dim3 grid, const uint16_t* Ahi, const uint16_t* Alo, const uint16_t* W1,
                            const uint16_t* W2, const float* b1, const float* b2, float* C, uint16_t* Chi,
                            uint16_t* Clo, int N, int Kd, long long cslice, const MoeWs& ws) {
-    static const bool il = [] {
-        const char* e = getenv("GORCH_HIP_MOE_IL");
-        return !e || atoi(e) != 0;
-    }();
-    // GORCH_HIP_MOE_XCD: bit 0 the down GEMM, bit 1 the gate/up GEMM take
-    // the XCD-contiguous block order
-    static const int xcd_bits = [] {
-        const char* e = getenv("GORCH_HIP_MOE_XCD");
-        return e ? atoi(e) : 1;
-    }();
-    const int xcd_map = (xcd_bits >> (DUAL ? 1 : 0)) & 1;
+    constexpr int xcd_map = DUAL ? 0 : 1;
     if (xcd_map) {
         // at least 8 * ceil(items / 8) blocks per slice, a multiple of 8
         const long long need = ((long long)grid.x * grid.y + 7) / 8 * 8;
         grid.y = (unsigned)((need + grid.x - 1) / grid.x);
         while (((long long)grid.x * grid.y) % 8) grid.y++;
     }
-    // GORCH_HIP_MOE_W16: bit 0 the down GEMM, bit 1 the gate/up GEMM run
-    // 16 waves (4 x 4) per block instead of 8 (2 x 4): four waves per SIMD
-    // hide the LDS round trips of one another (measured: gate/up 180 -> 170
-    // us, down 108 -> 102 us). GORCH_HIP_MOE_W16IL: 1 (default) the
-    // interleaved schedule with one register set for the global loads (both
-    // halves' fragments fit the 128 registers then; gate/up 169 -> 159 us,
-    // down 102 -> 96 us), 2 the compiler's schedule with one set, 0 with two.
-    static const int w16_bits = [] {
-        const char* e = getenv("GORCH_HIP_MOE_W16");
-        return e ? atoi(e) : 3;
-    }();
-    static const int w16il = [] {
-        const char* e = getenv("GORCH_HIP_MOE_W16IL");
-        return e ? atoi(e) : 1;
-    }();
-    // GORCH_HIP_MOE_STG: bit 0 down, bit 1 gate/up stage the finished tile
-    // in LDS for 16-byte stores (measured: down 100.6 -> 97.3 us; gate/up
-    // 164.7 -> 165.9, so down only by default)
-    static const int stg_bits = [] {
-        const char* e = getenv("GORCH_HIP_MOE_STG");
-        return e ? atoi(e) : 1;
-    }();
-    const bool stg = (stg_bits >> (DUAL ? 1 : 0)) & 1;
-    if (((w16_bits >> (DUAL ? 1 : 0)) & 1) && w16il == 1 && stg)
-        return launch_moe_wide_t<DUAL, BNW, true, 4, 1, true>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd,
-                                                              cslice, xcd_map, ws);
-    if (((w16_bits >> (DUAL ? 1 : 0)) & 1) && w16il == 1)
-        return launch_moe_wide_t<DUAL, BNW, true, 4, 1>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice,
-                                                        xcd_map, ws);
-    if (((w16_bits >> (DUAL ? 1 : 0)) & 1) && w16il == 2)
-        return launch_moe_wide_t<DUAL, BNW, false, 4, 1>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd,
-                                                         cslice, xcd_map, ws);
-    if ((w16_bits >> (DUAL ? 1 : 0)) & 1)
-        return launch_moe_wide_t<DUAL, BNW, false, 4>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice,
-                                                      xcd_map, ws);
-    if (il)
-        return launch_moe_wide_t<DUAL, BNW, true, 2>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice,
-                                                     xcd_map, ws);
-    return launch_moe_wide_t<DUAL, BNW, false, 2>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd, cslice,
-                                                  xcd_map, ws);
+    return launch_moe_wide_t<DUAL, BNW, true, 4, 1, !DUAL>(s, grid, Ahi, Alo, W1, W2, b1, b2, C, Chi, Clo, N, Kd,
+                                                           cslice, xcd_map, ws);
 }
 
 }  // namespace gh
@@ -835,20 +637,11 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
         GH_TRY(launch_linear_bf16(s, x, w->wr, w->br, nullptr, ws.logits, M, E, d, GORCH_HIP_EPI_NONE));
         lg = ws.logits;
     }
-    static const bool wide = [] {
-        const char* e = getenv("GORCH_HIP_MOE_WIDE");
-        return !e || atoi(e) != 0;
-    }();
-    const int tile_rows = wide ? kWideBM : kMoeBM;
+    const int tile_rows = kWideBM;
     // top-K slots sized to K (every absent slot still costs its compares).
     // Up to two slots, 8 experts and 4096 tokens: the routing block takes
-    // the top-K itself (one launch fewer; GORCH_HIP_MOE_FUSE_TOPK=0 keeps
-    // k_moe_topk)
-    static const bool fuse_topk = [] {
-        const char* e = getenv("GORCH_HIP_MOE_FUSE_TOPK");
-        return !e || atoi(e) != 0;
-    }();
-    if (fuse_topk && K <= 2 && E <= 8 && M <= 4 * kRouteThreads) {
+    // the top-K itself (one launch fewer)
+    if (K <= 2 && E <= 8 && M <= 4 * kRouteThreads) {
         hipLaunchKernelGGL((k_moe_route<2, 8>), dim3(1), dim3(kRouteThreads), 0, s, M, E, K, tile_rows, ws, lg,
                            topk_idx, topk_w);
     } else {
@@ -872,55 +665,28 @@ extern "C" int gorch_hip_moe_forward(void* stream, const gorch_hip_moe_weights* 
     GH_TRY(check_launch("moe_route"));
     const int MK = M * K;
     const int max_tiles = MK / tile_rows + E + 1;
-    int nsl = 1;            // K slices of the down GEMM's partials in yg
-    long long cslice = 0;   // their stride in floats
-    if (wide) {
-        // Xg and H hold (hi, lo) bf16 planes in the space of their f32 form
-        uint16_t* xhi = reinterpret_cast<uint16_t*>(ws.xg);
-        uint16_t* xlo = xhi + (size_t)MK * d;
-        uint16_t* hhi = reinterpret_cast<uint16_t*>(ws.h);
-        uint16_t* hlo = hhi + (size_t)MK * F;
-        const int gblocks = (int)std::min<int64_t>(8192, ((int64_t)M * d / 8 + 255) / 256);
-        if (K <= 2)
-            hipLaunchKernelGGL(k_moe_gather_split<2>, dim3(gblocks), dim3(256), 0, s, x, ws.inv, xhi, xlo, M, K, d);
-        else
-            hipLaunchKernelGGL(k_moe_gather_split<kMaxTopK>, dim3(gblocks), dim3(256), 0, s, x, ws.inv, xhi, xlo, M,
-                               K, d);
-        GH_TRY(check_launch("moe_gather"));
-        GH_TRY((launch_moe_wide<true, kWideBNDual>(s, dim3((F + kWideBNDual - 1) / kWideBNDual, max_tiles), xhi,
-                                                  xlo, w->wgate, w->wup, w->bgate, w->bup, nullptr, hhi, hlo, F, d,
-                                                  0, ws)));
-        static const int down_bn = [] {
-            const char* e = getenv("GORCH_HIP_MOE_DOWN_BN");
-            return e ? atoi(e) : kWideBNDown;
-        }();
-        static const int down_split = [] {
-            const char* e = getenv("GORCH_HIP_MOE_DOWN_SPLIT");
-            return e ? std::max(1, std::min(kDownSlices, atoi(e))) : 1;
-        }();
-        nsl = F >= 64 * down_split ? down_split : 1;
-        cslice = (long long)MK * d;
-        if (down_bn == 256)
-            GH_TRY((launch_moe_wide<false, 256>(s, dim3((d + 255) / 256, max_tiles, nsl), hhi, hlo, w->wdown,
-                                                nullptr, w->bdown, nullptr, ws.yg, nullptr, nullptr, d, F, cslice,
-                                                ws)));
-        else
-            GH_TRY((launch_moe_wide<false, 128>(s, dim3((d + 127) / 128, max_tiles, nsl), hhi, hlo, w->wdown,
-                                                nullptr, w->bdown, nullptr, ws.yg, nullptr, nullptr, d, F, cslice,
-                                                ws)));
-    } else {
-        const int gblocks = (int)std::min<int64_t>(8192, ((int64_t)MK * d / 4 + 255) / 256);
-        hipLaunchKernelGGL(k_moe_gather, dim3(gblocks), dim3(256), 0, s, x, ws.perm_tok, ws.xg, MK, d);
-        GH_TRY(check_launch("moe_gather"));
-        hipLaunchKernelGGL((k_moe_gemm<true, kMoeBNDual>), dim3((F + kMoeBNDual - 1) / kMoeBNDual, max_tiles),
-                           dim3(256), 0, s, ws.xg, w->wgate, w->wup, w->bgate, w->bup, ws.h, F, d, ws);
-        GH_TRY(check_launch("moe_gemm_gate_up"));
-        hipLaunchKernelGGL((k_moe_gemm<false, kMoeBNDown>), dim3((d + kMoeBNDown - 1) / kMoeBNDown, max_tiles),
-                           dim3(256), 0, s, ws.h, w->wdown, nullptr, w->bdown, nullptr, ws.yg, d, F, ws);
-        GH_TRY(check_launch("moe_gemm_down"));
-    }
+    // Xg and H hold (hi, lo) bf16 planes in the space of their f32 form
+    uint16_t* xhi = reinterpret_cast<uint16_t*>(ws.xg);
+    uint16_t* xlo = xhi + (size_t)MK * d;
+    uint16_t* hhi = reinterpret_cast<uint16_t*>(ws.h);
+    uint16_t* hlo = hhi + (size_t)MK * F;
+    const int gblocks = (int)std::min<int64_t>(8192, ((int64_t)M * d / 8 + 255) / 256);
+    if (K <= 2)
+        hipLaunchKernelGGL(k_moe_gather_split<2>, dim3(gblocks), dim3(256), 0, s, x, ws.inv, xhi, xlo, M, K, d);
+    else
+        hipLaunchKernelGGL(k_moe_gather_split<kMaxTopK>, dim3(gblocks), dim3(256), 0, s, x, ws.inv, xhi, xlo, M, K,
+                           d);
+    GH_TRY(check_launch("moe_gather"));
+    GH_TRY((launch_moe_wide<true, kWideBNDual>(s, dim3((F + kWideBNDual - 1) / kWideBNDual, max_tiles), xhi, xlo,
+                                              w->wgate, w->wup, w->bgate, w->bup, nullptr, hhi, hlo, F, d, 0, ws)));
+    // the down GEMM unsplit over K (one slice of partials in yg)
+    const int nsl = 1;
+    const long long cslice = (long long)MK * d;
+    GH_TRY((launch_moe_wide<false, kWideBNDown>(s, dim3((d + kWideBNDown - 1) / kWideBNDown, max_tiles, nsl), hhi,
+                                                hlo, w->wdown, nullptr, w->bdown, nullptr, ws.yg, nullptr, nullptr, d,
+                                                F, cslice, ws)));
     const int cblocks = (int)std::min<int64_t>(8192, ((int64_t)M * d / 4 + 255) / 256);
-if (K <= 2)
+    if (K <= 2)
         hipLaunchKernelGGL(k_moe_combine<2>, dim3(cblocks), dim3(256), 0, s, ws.yg, ws.inv, ws.topi, out, M, K, d, nsl,
                            cslice, w->bdown, ws.perm_w);
     else
