@@ -103,6 +103,10 @@ int launch_linear_bf16_od(hipStream_t s, const float* x, const uint16_t* W, cons
 int noalloc_setup(int device);
 // Device bytes held by the per-stream scratch buffers (stream_scratch).
 long long scratch_bytes_held();
+// Frees the scratch of a stream about to be destroyed (its work finished,
+// no graph left that points at it): the library's engines call it for their
+// own streams, so a later stream at the same address starts without one.
+void release_stream_scratch(hipStream_t s);
 
 // gorch_hip_set_deterministic's setting: no float-atomic sums when true.
 bool deterministic();

@@ -730,12 +730,13 @@ gorch_hip_gpt* gorch_hip_gpt_load_gpt2(const char* path, int vocab, int dim, int
 
 void gorch_hip_gpt_free(gorch_hip_gpt* g) {
     if (!g) return;
-    if (g->stream) {
-        (void)hipStreamSynchronize(g->stream);
-        (void)hipStreamDestroy(g->stream);
-    }
+    if (g->stream) (void)hipStreamSynchronize(g->stream);
     if (g->gen_exec) (void)hipGraphExecDestroy(g->gen_exec);
     if (g->gen_graph) (void)hipGraphDestroy(g->gen_graph);
+    if (g->stream) {
+        release_stream_scratch(g->stream);
+        (void)hipStreamDestroy(g->stream);
+    }
     gorch_hip_kvcache_free(g->gen_cache);
     (void)hipFree(g->blob);
     (void)hipFree(g->pblob);

@@ -309,6 +309,7 @@ void gorch_hip_qwen_destroy(gorch_hip_qwen* m) {
     for (void* p : {(void*)m->kv, (void*)m->ws, (void*)m->x, (void*)m->h, (void*)m->logits, (void*)m->ids,
                     (void*)m->state, (void*)m->hist, (void*)m->key})
         (void)hipFree(p);
+    release_stream_scratch(m->stream);
     (void)hipStreamDestroy(m->stream);
     delete m;
 }

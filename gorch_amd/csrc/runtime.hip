@@ -51,6 +51,19 @@ std::atomic<long long> g_scratch_bytes{0};
 
 long long scratch_bytes_held() { return g_scratch_bytes.load(); }
 
+void release_stream_scratch(hipStream_t s) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    for (size_t i = 0; i < g_scratch.size();) {
+        if (g_scratch[i].stream == s) {
+            (void)hipFree(g_scratch[i].ptr);
+            g_scratch_bytes -= (long long)g_scratch[i].bytes;
+            g_scratch.erase(g_scratch.begin() + (long)i);
+        } else {
+            i++;
+        }
+    }
+}
+
 void* stream_scratch(hipStream_t s, size_t bytes) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
@@ -178,7 +191,10 @@ static int run_bf16_probe(int dev) {
     } while (false);
     (void)hipGetLastError();
     if (buf) (void)hipFree(buf);
-    if (s) (void)hipStreamDestroy(s);
+    if (s) {
+        release_stream_scratch(s);
+        (void)hipStreamDestroy(s);
+    }
     g_probe[dev].store(verdict, std::memory_order_release);
     return verdict;
 }

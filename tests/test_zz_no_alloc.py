@@ -104,16 +104,20 @@ def test_noalloc_two_calls_second_smaller(lib):
     assert np.array_equal(got, want)
     # the counter the checks above rely on does see an allocation: the
     # allocating entry point takes a partials buffer for a new stream's
-    # first K split
-    s2 = torch.cuda.Stream()
+    # first K split (a stream made here: torch hands out streams from a
+    # pool, which earlier calls may have used)
+    hip_rt = C.CDLL("libamdhip64.so")
+    s2 = C.c_void_p()
+    assert hip_rt.hipStreamCreate(C.byref(s2)) == 0
     x, W, b = syn.gemv_inputs(16, 3072, 768, seed=6)
     dx, dW, db, dy = Dev(lib, x), Dev(lib, W), Dev(lib, b), Dev(lib, nbytes=16 * 768 * 4)
     held = lib.gorch_hip_scratch_bytes()
-    assert lib.gorch_hip_linear_bf16(s2.cuda_stream, dx.p, dW.p, db.p, None, dy.p, 16, 768, 3072, 0) == 0
-    assert lib.gorch_hip_sync(s2.cuda_stream) == 0
+    assert lib.gorch_hip_linear_bf16(s2, dx.p, dW.p, db.p, None, dy.p, 16, 768, 3072, 0) == 0
+    assert lib.gorch_hip_sync(s2) == 0
     assert lib.gorch_hip_scratch_bytes() > held
     for t in (dx, dW, db, dy):
         t.free()
+    # (the stream stays: the library keeps its partials buffer for it)
 
 
 def test_noalloc_rejects_bad_arguments(lib):
