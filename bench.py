@@ -51,7 +51,7 @@ def parse():
                     help="restrict to one shape 'M,K,N' (for profiling one kernel)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the GPT decode legs")
-    ap.add_argument("--only", choices=("decode", "gemm", "decode-xl", "moe", "decode-qwen", "cpu-decode",
+    ap.add_argument("--only", choices=("decode", "gemm", "decode-xl", "moe", "decode-qwen", "cpu-decode", "cpu-configs",
                                        "attn-xl"),
                     default=None,
                     help="run only one secondary leg and print its JSON (for profiling)")
@@ -264,11 +264,19 @@ def gemm_leg(M=512, K=768, Ns=(2304, 3072)):
             e1.synchronize()
             us = e0.elapsed_time(e1) * 1e3 / (3 * L)
             flops = 2.0 * M * K * N
+            # algorithmic bytes: f32 A, bf16 W, f32 C once each; the roofline
+            # ceiling min(MFMA peak, AI x HBM peak) is the HBM side here
+            # (AI 184 / 192 FLOP/B: 58-61% of the MFMA peak)
+            nbytes = 4 * M * K + 2 * K * N + 4 * M * N
+            ceiling = min(MFMA_PEAK_TFLOPS, flops / nbytes * HBM_PEAK_GBS / 1e3)
             # the f32-accurate mode issues two MFMAs per fragment: report the
             # algorithmic rate (2MKN / time) for both
             out.append({"M": M, "K": K, "N": N, "activations": "bf16" if act_bf16 else "f32 (hi+lo split)",
                         "us": round(us, 3), "TFLOPs": round(flops / us / 1e6, 1),
-                        "frac_mfma_peak": round(flops / us / 1e6 / MFMA_PEAK_TFLOPS, 4)})
+                        "frac_mfma_peak": round(flops / us / 1e6 / MFMA_PEAK_TFLOPS, 4),
+                        "algorithmic_bytes": nbytes, "roofline_ceiling_TFLOPs": round(ceiling, 1),
+                        "frac_roofline_ceiling": round(flops / us / 1e6 / ceiling, 4),
+                        "frac_hbm_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
             del g
     return out
 
@@ -459,16 +467,15 @@ def attn_leg(batch=16, heads=25, hd=64, ctx=640, capacity=768, reps=200):
             "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
-def decode_leg(cfg_name, batch, n_prompt, max_new, reps=3):
+def decode_leg(cfg_name, batch, n_prompt, max_new, reps=3, w=None):
     """Greedy KV-cache decode through the engine (graph-replayed step).
-    tok/s = batch * decode forwards / decode wall time (prefill timed apart)."""
+    tok/s = batch * decode forwards / decode wall time (prefill timed apart).
+    w: the host weights when the caller made them already."""
     from gorch_amd import hip
     from gorch_amd import synthetic as syn
 
     cfg = dict(syn.GPT2_SMALL if cfg_name == "gpt2-small" else syn.GPT2_XL)
-    w = syn.gpt2_weights(cfg, seed=0)
-    g = hip.GPT(w)
-    del w
+    g = hip.GPT(w if w is not None else syn.gpt2_weights(cfg, seed=0))
     prompts = np.stack([syn.prompt_ids(n_prompt, cfg["vocab"], seed=b) for b in range(batch)])
     g.generate_cached(prompts, max_new, use_graph=True)   # warm-up (graph build, caches)
     runs = []
@@ -584,10 +591,97 @@ def cpu_decode_leg(seconds, host, n_prompt=32):
             "runs": out, **host}
 
 
+def cpu_configs_leg(host, gemm, moe, xl, xl_w, seconds=2.0):
+    """The oracle beside the GPU for the other configs, on the granted
+    threads and on one thread (bounded samples):
+    P: the prefill GEMM 512 x 768 x N (bf16-rounded activations, the weight
+       widened per call as bf16_matmul.go:166), repeated ~seconds;
+    E: the MoE layer (configs[3], 2048 tokens): one forward on the granted
+       threads, a 256-token slice of the same input on one thread;
+    X: the GPT-2 XL-shaped model (configs[4] weights): an 8-token prompt
+       (not timed), then decode steps of one sequence, faithful (widen per
+       call) and pre-widened; the per-token cost is the weights' (at context
+       9 rather than 512-767: attention is ~6% of a step's FLOPs there).
+    GPU/CPU speed-ups against the GPU legs of the same run."""
+    import oracle as orc
+    from gorch_amd import synthetic as syn
+
+    threads = host["threads_granted"]
+
+    def timed(fn, budget, min_n=1):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget and n >= min_n:
+                return el / n, n
+
+    out = {"kind": "port", "cores": threads, **host}
+    orc.set_widen_per_call(True)
+    p = []
+    for N in (2304, 3072):
+        x, W, b = syn.gemv_inputs(512, 768, N, seed=N)
+        xb = orc.bf16_to_f32(orc.f32_to_bf16(x))
+        gpu_us = next((g["us"] for g in gemm if g["N"] == N and g["activations"] == "bf16"), None)
+        for th in (threads, 1):
+            orc.set_threads(th)
+            sec, n = timed(lambda: orc.linear(xb, W, b), seconds if th == threads else seconds / 2)
+            p.append({"N": N, "threads": th, "us": round(sec * 1e6, 1), "calls": n,
+                      "TFLOPs": round(2.0 * 512 * 768 * N / sec / 1e12, 4),
+                      "gpu_speedup": round(sec * 1e6 / gpu_us, 1) if gpu_us else None})
+    out["prefill_gemm"] = p
+    x, logits, w = syn.moe_inputs(seed=0)
+    e = []
+    for th, rows in ((threads, x.shape[0]), (1, 256)):
+        orc.set_threads(th)
+        t0 = time.perf_counter()
+        orc.moe_forward(w, x[:rows], logits[:rows])
+        sec = (time.perf_counter() - t0) * x.shape[0] / rows
+        e.append({"threads": th, "tokens_timed": rows, "us_per_layer": round(sec * 1e6, 1),
+                  "gpu_speedup": round(sec * 1e6 / moe["us"], 1) if moe else None})
+    out["moe_layer"] = e
+    del x, logits, w
+    if xl_w is not None:
+        o = orc.GPT(xl_w)
+        prompt = syn.prompt_ids(8, syn.GPT2_XL["vocab"], seed=0)
+        runs = []
+        gpu_tok_s = xl["tok_s"] if xl else None
+        for widen in (True, False):
+            orc.set_widen_per_call(widen)
+            for th in (threads, 1):
+                orc.set_threads(th)
+                cache = o.new_cache()
+                tok = orc.argmax(o.forward_cached(prompt, cache)[-1])
+                if not widen:   # the one-time widening happens on the first call
+                    tok = orc.argmax(o.forward_cached(np.array([tok], np.int32), cache)[-1])
+                steps = 2 if th == threads else 1
+                t0 = time.perf_counter()
+                for _ in range(steps):
+                    tok = orc.argmax(o.forward_cached(np.array([tok], np.int32), cache)[-1])
+                el = time.perf_counter() - t0
+                runs.append({"mode": "faithful (widen per call)" if widen else "pre-widened", "threads": th,
+                             "steps": steps, "tok_s": round(steps / el, 3),
+                             "gpu_speedup": round(gpu_tok_s / (steps / el), 1) if gpu_tok_s else None})
+        out["decode_xl"] = {"model": "gpt2-xl", "prompt": 8, "runs": runs,
+                            "gpu": "batch 16 tok/s of the decode leg (16 sequences at once)"}
+        del o
+    orc.set_widen_per_call(True)
+    orc.set_threads(threads)
+    return out
+
+
 def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.only == "cpu-configs":
+        # the oracle legs alone (no GPU); the XL model's weights are made here
+        from gorch_amd import synthetic as syn
+        print(json.dumps(cpu_configs_leg(host_info(), [], None, None,
+                                         syn.gpt2_weights(dict(syn.GPT2_XL), seed=0))))
         return
     if args.only:
         import torch
@@ -624,14 +718,19 @@ def main():
     value, wall, per_shape, dom = gpu_leg(args, shapes)
     # the metric's two decode rates: GPT-2 small at batch 1 (configs[0]'s
     # workload) and the GPT-2 XL shape at batch 16
+    from gorch_amd import synthetic as syn
+    xl_w = None if (args.shape or args.no_decode) else syn.gpt2_weights(dict(syn.GPT2_XL), seed=0)
     decode = [] if (args.shape or args.no_decode) else [decode_leg("gpt2-small", 1, 32, 64),
-                                                         decode_leg("gpt2-xl", 16, 512, 256, reps=1)]
+                                                         decode_leg("gpt2-xl", 16, 512, 256, reps=1, w=xl_w)]
     gemm = [] if args.shape else gemm_leg()
     moe = None if args.shape else moe_leg()
     qwen = [] if (args.shape or args.no_decode) else qwen_leg()
     host = host_info()
     cpu = None if args.no_cpu else cpu_leg(shapes, args.cpu_seconds, host)
     cpu_decode = None if (args.no_cpu or args.shape or args.no_decode) else cpu_decode_leg(3.0, host)
+    cpu_configs = None if (args.no_cpu or args.shape) else cpu_configs_leg(
+        host, gemm, moe, decode[1] if len(decode) > 1 else None, xl_w if not args.no_cpu else None)
+    del xl_w
     dom_bytes = algo_bytes(dom["M"], dom["K"], dom["N"])
     dom_kernel = gemv_kernel(dom["M"], dom["K"], dom["N"])
     out = {
@@ -672,6 +771,7 @@ def main():
         "per_shape": per_shape,
         "decode": decode,
         "cpu_decode": cpu_decode,
+        "cpu_configs": cpu_configs,
         "prefill_gemm": gemm,
         "moe_layer": moe,
         "decode_qwen": qwen,
