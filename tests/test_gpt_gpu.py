@@ -223,23 +223,27 @@ def test_generate_long_cache_batch1(gpu, prompt):
     g.close()
 
 
-XL2 = dict(vocab=8192, dim=1600, heads=25, layers=2, max_seq=544)
+XL2 = dict(vocab=50257, dim=1600, heads=25, layers=2, max_seq=768)
 
 
 def test_generate_gpt2_xl_width_batch16(gpu):
-    """BASELINE configs[4] at its per-step shape with 2 of its 48 layers:
-    d 1600, 25 heads of 64, batch 16, 512-token prompts (the matrix-core
-    prefill GEMMs, flash attention over 512 rows, K/V rows written into the
-    cache segments by the fused QKV GEMM), then 16 greedy steps through the
-    batched decode path (tile-packed GEMVs, K-split Wo/FFN2 with the row
-    reducer, and the 16-wave two-pass attention kernel at 400 (head, row)
-    blocks over a 528-row cache). Tokens identical to the oracle for every
-    sequence, first-step logits within 1e-3, graph replay identical."""
+    """BASELINE configs[4] at its full per-step shape with 2 of its 48 layers:
+    d 1600, 25 heads of 64, vocab 50257, batch 16, 512-token prompts (the
+    matrix-core prefill GEMMs, flash attention over 512 rows, K/V rows
+    written into the cache segments by the fused QKV GEMM), then 256 greedy
+    steps through the batched decode path (tile-packed GEMVs, the fused QKV
+    split over K with the attention adding its slices, K-split Wo/FFN2 with
+    the row reducer, the 16-wave two-pass attention kernel at 400 (head,
+    row) blocks, the LM head with the argmax fused) out to a 768-row cache.
+    Every sequence against the oracle's generateCached: tokens identical
+    over all 256 steps, first-step logits within 1e-3 and the run's within
+    2e-2; the graph-replayed run gives the same tokens."""
     w = syn.gpt2_weights(XL2, seed=90, random_affine=True)
     g, o = gpu.GPT(w), orc.GPT(w)
-    B, P, steps = 16, 512, 16
+    B, P, steps = 16, 512, 256
     prompts = np.stack([syn.prompt_ids(P, XL2["vocab"], seed=200 + b) for b in range(B)])
     ids, logits, _ = g.generate_cached(prompts, steps, want_logits=True)
+    assert ids.shape == (B, P + steps)
     orc.set_widen_per_call(False)
     try:
         gaps = []
@@ -252,6 +256,7 @@ def test_generate_gpt2_xl_width_batch16(gpu):
     finally:
         orc.set_widen_per_call(True)
     print(f"min top-1/top-2 logit gap: {min(gaps):.3e}")
+    del logits
     ids_graph, _, t = g.generate_cached(prompts, steps, use_graph=True)
     assert np.array_equal(ids_graph, ids)
     assert t["decode_forwards"] == steps
