@@ -23,13 +23,14 @@ int launch_gemm_bf16w(hipStream_t s, const float* A, const uint16_t* W, const fl
 // dtype combination of metal_mps_matmul_dt (one launch for the whole batch,
 // blockIdx.z = batch entry). Block tile 64 x 64, K stepped by 32; each
 // operand tile is gathered through its own layout into LDS as bf16 terms
-// in [row][k] order (NTA / NTB terms: 1 for a bf16 operand, hi + lo for an
-// f32 one), then 4 waves (2 x 2, 32 x 32 each) run v_mfma_f32_16x16x32_bf16
-// over the term products that matter (lo x lo, below f32 rounding, is left
-// out), accumulating in f32. Not a hot path of the decode step: the gather
-// is per element (bf16 storage is one exact term; f32 is hi, the value
-// truncated to bf16, plus lo, the remainder rounded to bf16: x = hi + lo to
-// ~2^-16 relative).
+// in [row][k] order (NTA / NTB terms: 1 for a bf16 operand, 3 for an f32
+// one), then 4 waves (2 x 2, 32 x 32 each) run v_mfma_f32_16x16x32_bf16
+// over the term products whose term indices sum to at most 2 (the rest lie
+// below f32 rounding), accumulating in f32. Not a hot path of the decode
+// step: the gather is per element (bf16 storage is one exact term; f32 is
+// hi, the value truncated to bf16, mid, the remainder truncated to bf16, and
+// lo, what is left rounded to bf16: x = hi + mid + lo to ~2^-25 relative, so
+// f32 x f32 products carry f32-level error).
 constexpr int kMmBK = 32, kMmLD = kMmBK + 8;  // LDS row: 40 bf16 (80 bytes)
 
 template <int NTA, int NTB>
@@ -52,22 +53,29 @@ __global__ __launch_bounds__(256) void k_matmul_mfma(const void* __restrict__ A,
     // read as zero, so all 16 of a thread's element loads go out together (a
     // load under a bounds branch waits for the one before it)
     constexpr int EA = NTA == 1 ? 2 : 4, EB = NTB == 1 ? 2 : 4;
+    static_assert(NTA == 1 || NTA == 3, "bf16: one term, f32: three");
+    static_assert(NTB == 1 || NTB == 3, "bf16: one term, f32: three");
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(reinterpret_cast<const char*>(A) + bA * EA, (long long)M * K * EA);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(reinterpret_cast<const char*>(B) + bB * EB, (long long)K * N * EB);
     auto ld = [](__amdgpu_buffer_rsrc_t rs, int off, bool half) -> uint32_t {
         return half ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0)
                     : __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
     };
-    auto terms = [](uint32_t bits, bool half, uint16_t& h, uint16_t& l) {
+    // the operand's terms: bf16 storage is exact; f32 v = hi + mid + lo (hi
+    // and mid truncations, each remainder exact in f32, lo rounded)
+    auto terms = [](uint32_t bits, bool half, uint16_t (&t)[3]) {
         if (half) {
-            h = (uint16_t)bits;
-            l = 0;
+            t[0] = (uint16_t)bits;
+            t[1] = t[2] = 0;
             return;
         }
         const float v = __uint_as_float(bits);
         const uint32_t u = bits & 0xffff0000u;
-        h = (uint16_t)(u >> 16);
-        l = __builtin_bit_cast(uint16_t, (__bf16)(v - __uint_as_float(u)));
+        const float r1 = v - __uint_as_float(u);
+        const uint32_t u1 = __float_as_uint(r1) & 0xffff0000u;
+        t[0] = (uint16_t)(u >> 16);
+        t[1] = (uint16_t)(u1 >> 16);
+        t[2] = __builtin_bit_cast(uint16_t, (__bf16)(r1 - __uint_as_float(u1)));
     };
     for (int k0 = 0; k0 < K; k0 += kMmBK) {
         // 64 x 32 elements per operand, 8 per thread: thread t takes row
@@ -86,13 +94,13 @@ __global__ __launch_bounds__(256) void k_matmul_mfma(const void* __restrict__ A,
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const int kk = 8 * (tid & 3) + e;
-            uint16_t h, l;
-            terms(av[e], NTA == 1, h, l);
-            As[0][row][kk] = h;
-            if (NTA == 2) As[NTA - 1][row][kk] = l;
-            terms(bv[e], NTB == 1, h, l);
-            Bs[0][row][kk] = h;
-            if (NTB == 2) Bs[NTB - 1][row][kk] = l;
+            uint16_t t[3];
+            terms(av[e], NTA == 1, t);
+#pragma unroll
+            for (int q = 0; q < NTA; q++) As[q][row][kk] = t[q];
+            terms(bv[e], NTB == 1, t);
+#pragma unroll
+            for (int q = 0; q < NTB; q++) Bs[q][row][kk] = t[q];
         }
         __syncthreads();
         bf16x8 af[2][NTA], bfr[2][NTB];
@@ -114,7 +122,7 @@ __global__ __launch_bounds__(256) void k_matmul_mfma(const void* __restrict__ A,
                 for (int ta = 0; ta < NTA; ta++)
 #pragma unroll
                     for (int tb = 0; tb < NTB; tb++)
-                        if (ta + tb < 2) acc[i][j] = mfma16x16x32(af[i][ta], bfr[j][tb], acc[i][j]);
+                        if (ta + tb <= 2) acc[i][j] = mfma16x16x32(af[i][ta], bfr[j][tb], acc[i][j]);
         __syncthreads();
     }
     // lane holds rows 4g..4g+3 of column r in each 16 x 16 fragment
@@ -243,9 +251,9 @@ int matmul_dt_raw(hipStream_t s, const void* A, const void* B, float* C, uint32_
     const dim3 grid((N + 63) / 64, (M + 63) / 64, batch);
     const int tA = transA ? 1 : 0, tB = transB ? 1 : 0, m = (int)M, n = (int)N, k = (int)K;
     if (aBF16 && bBF16) hipLaunchKernelGGL((k_matmul_mfma<1, 1>), grid, dim3(256), 0, s, A, B, C, m, n, k, tA, tB);
-    else if (aBF16) hipLaunchKernelGGL((k_matmul_mfma<1, 2>), grid, dim3(256), 0, s, A, B, C, m, n, k, tA, tB);
-    else if (bBF16) hipLaunchKernelGGL((k_matmul_mfma<2, 1>), grid, dim3(256), 0, s, A, B, C, m, n, k, tA, tB);
-    else hipLaunchKernelGGL((k_matmul_mfma<2, 2>), grid, dim3(256), 0, s, A, B, C, m, n, k, tA, tB);
+    else if (aBF16) hipLaunchKernelGGL((k_matmul_mfma<1, 3>), grid, dim3(256), 0, s, A, B, C, m, n, k, tA, tB);
+    else if (bBF16) hipLaunchKernelGGL((k_matmul_mfma<3, 1>), grid, dim3(256), 0, s, A, B, C, m, n, k, tA, tB);
+    else hipLaunchKernelGGL((k_matmul_mfma<3, 3>), grid, dim3(256), 0, s, A, B, C, m, n, k, tA, tB);
     count(CNT_GENERIC_MATMUL);
     return check_launch("matmul_mfma");
 }

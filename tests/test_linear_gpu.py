@@ -134,6 +134,16 @@ def test_matmul_dt_all_layouts(gpu, transA, transB, aBF16, bBF16):
     C = torch.empty((M, N), dtype=torch.float32, device="cuda")
     gpu.matmul_dt(dev(A), dev(B), C, M, N, K, transA, transB, aBF16, bBF16)
     assert rel_err(host(C), orc.matmul_dt(A, B, M, N, K, transA, transB)) <= 1e-3
+    # against float64 over the operands' stored values: the Linear layout
+    # (f32 A, bf16 B stored [N, K]) takes the weight-streaming kernels, whose
+    # activations are two bf16 terms (x = hi + lo to ~2^-16: <= 1e-4); every
+    # other route splits an f32 operand into three (x = hi + mid + lo to
+    # ~2^-25), f32-level error (a two-term split measures ~1e-5 here)
+    a64 = (orc.bf16_to_f32(A) if aBF16 else a).astype(np.float64)
+    b64 = (orc.bf16_to_f32(B) if bBF16 else b).astype(np.float64)
+    ref64 = (a64.T if transA else a64) @ (b64.T if transB else b64)
+    linear_route = not transA and transB and not aBF16 and bBF16
+    assert rel_err(host(C), ref64) <= (1e-4 if linear_route else 2e-6)
 
 
 @pytest.mark.parametrize("transA,transB", [(0, 0), (1, 0), (0, 1)])
