@@ -180,8 +180,17 @@ def gpu_leg(args, shapes):
     wall = time.perf_counter() - t0
     step_bytes = sum(algo_bytes(b_["M"], b_["K"], b_["N"]) for b_ in bufs)
     value = step_bytes * args.steps / wall / 1e9
+    # the same steps with one graph replay each (the submission cost paid
+    # per step), reported beside the grouped figure
+    value_one = None
+    if G > 1:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        run(args.steps, args.warmup, False)
+        torch.cuda.synchronize()
+        value_one = step_bytes * args.steps / (time.perf_counter() - t0) / 1e9
     dom = max(per_shape, key=lambda r: r["us"])
-    return value, wall, per_shape, dom
+    return value, wall, per_shape, dom, value_one
 
 
 MFMA_PEAK_TFLOPS = 2516.6  # dense bf16: 256 CU x 2.4 GHz x 4096 FLOP/clk
@@ -715,7 +724,7 @@ def main():
     else:
         shapes = [(M, K, N) for (K, N) in KN for M in MS]
 
-    value, wall, per_shape, dom = gpu_leg(args, shapes)
+    value, wall, per_shape, dom, value_one = gpu_leg(args, shapes)
     # the metric's two decode rates: GPT-2 small at batch 1 (configs[0]'s
     # workload) and the GPT-2 XL shape at batch 16
     from gorch_amd import synthetic as syn
@@ -750,6 +759,7 @@ def main():
             "workload": "bf16-weight Linear GEMV microbench (BASELINE configs[1]): x f32 N(0,1) [M,K], "
                         "W bf16 N(0,0.02) [N,K], f32 out; one step = one launch per shape",
             "steps_per_graph_replay": max(1, min(args.steps_per_graph, args.steps)),
+            "value_one_replay_per_step": None if value_one is None else round(value_one, 1),
             "shapes": [f"M={s[0]},K={s[1]},N={s[2]}" for s in shapes],
             "weights_rotated_over_bytes": ROTATE_BYTES,
             "weight_layout": "each shape on the decode path's resident format (per_shape.layout): "

@@ -324,11 +324,12 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const float* __restrict__ x, 
 }
 
 // M = 1 variant with the activation row held in registers: lane `sub`
-// always needs the same C chunks of x (k = 8*(sub + T*c)), so each wave
-// loads (and, with a fused LayerNorm, normalises) them once, computing the
-// row statistics itself with wave reductions — no LDS staging and no block
-// barrier before the weight stream starts. The next row group's weight
-// loads are issued before the current group is reduced.
+// always needs the same C chunks of x (k = 8*(sub + T*c)). The block stages
+// the row once in LDS (with a fused norm, its moments too) behind one
+// barrier, while the first two row groups' weight loads are already in
+// flight; each lane then keeps its chunks (normalised) in registers. The
+// next row group's weight loads are issued before the current group is
+// reduced.
 // PRO selects what is applied to the activation row as it is loaded: 0
 // nothing, 1 LayerNorm (gamma, beta), 2 RMSNorm (gamma), 3 SwiGLU of a
 // [gate | up] row of 2K values (silu(gate) * up, silu.go:121-136).
@@ -372,39 +373,38 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
         gr.b = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, rloc * 4, 0, 0));
         gr.r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, rloc * 4, 0, 0));
     };
-    // the activation row (K = 8*T*C exactly), LayerNorm gamma/beta with it
-    float xr[C][8], gg[LN ? C : 1][8], bb[PRO == 1 ? C : 1][8];
+    // The activation row (K = 8*T*C exactly) is loaded once per block, not
+    // once per wave: thread t takes float4 t, t + 256, ... of x (and of
+    // gamma/beta, or of the up half), computes its share of the row moments
+    // and parks the values in LDS; after one barrier every lane reads the
+    // chunks it needs (k = 8*(sub + T*c)). A CU's vector-memory requests are
+    // what bounds this kernel, so four waves each fetching the whole row (and
+    // gamma/beta) cost as much as a large part of the weight slice.
+    constexpr int KX = 8 * T * C, NV = KX / 4, PER = (NV + 255) / 256;
+    __shared__ float4 s_x[NV];
+    __shared__ float4 s_g[LN ? NV : 1];
+    __shared__ float4 s_b[PRO == 1 ? NV : 1];
+    __shared__ double2 s_mom[4];
+    auto ld4 = [](__amdgpu_buffer_rsrc_t r, int off) {
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    };
+    // raw buffer loads with no branch around them: float4s past the row read
+    // zeros and are neither counted nor stored
+    const __amdgpu_buffer_rsrc_t rxs = make_rsrc(x, (long long)(PRO == 3 ? 2 : 1) * KX * 4);
+    const __amdgpu_buffer_rsrc_t rgs = make_rsrc(ex.ln_g, LN ? (long long)KX * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rbs = make_rsrc(ex.ln_b, PRO == 1 ? (long long)KX * 4 : 0);
+    float4 vx[PER], vg[LN ? PER : 1], vb[PRO == 1 ? PER : 1], vu[PRO == 3 ? PER : 1];
 #pragma unroll
-    for (int c = 0; c < C; c++) {
-        const int k = 8 * (sub + T * c);
-        const float4 a0 = *reinterpret_cast<const float4*>(x + k);
-        const float4 a1 = *reinterpret_cast<const float4*>(x + k + 4);
-        xr[c][0] = a0.x; xr[c][1] = a0.y; xr[c][2] = a0.z; xr[c][3] = a0.w;
-        xr[c][4] = a1.x; xr[c][5] = a1.y; xr[c][6] = a1.z; xr[c][7] = a1.w;
-        if constexpr (LN) {
-            const float4 g0 = *reinterpret_cast<const float4*>(ex.ln_g + k);
-            const float4 g1 = *reinterpret_cast<const float4*>(ex.ln_g + k + 4);
-            gg[c][0] = g0.x; gg[c][1] = g0.y; gg[c][2] = g0.z; gg[c][3] = g0.w;
-            gg[c][4] = g1.x; gg[c][5] = g1.y; gg[c][6] = g1.z; gg[c][7] = g1.w;
-        }
-        if constexpr (PRO == 1) {
-            const float4 b0 = *reinterpret_cast<const float4*>(ex.ln_b + k);
-            const float4 b1 = *reinterpret_cast<const float4*>(ex.ln_b + k + 4);
-            bb[c][0] = b0.x; bb[c][1] = b0.y; bb[c][2] = b0.z; bb[c][3] = b0.w;
-            bb[c][4] = b1.x; bb[c][5] = b1.y; bb[c][6] = b1.z; bb[c][7] = b1.w;
-        }
-        if constexpr (PRO == 3) {
-            // the up half sits K values after the gate half
-            const float4 u0 = *reinterpret_cast<const float4*>(x + K + k);
-            const float4 u1 = *reinterpret_cast<const float4*>(x + K + k + 4);
-            const float up[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float gv = xr[c][i];
-                xr[c][i] = gv * sigmoidf_ref(gv) * up[i];
-            }
-        }
+    for (int p = 0; p < PER; p++) {
+        const int i = tid + 256 * p;
+        const int off = i < NV ? 16 * i : kOutOfRange;
+        vx[p] = ld4(rxs, off);
+        if constexpr (LN) vg[p] = ld4(rgs, off);
+        if constexpr (PRO == 1) vb[p] = ld4(rbs, off);
+        if constexpr (PRO == 3) vu[p] = ld4(rxs, i < NV ? 16 * (NV + i) : kOutOfRange);
     }
+    // LayerNorm's moment shift: the row's first value, the same for every thread
+    const float x0 = PRO == 1 ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rxs, 0, 0, 0)) : 0.f;
     // then two row groups of the weight stream: the activation loads above
     // come from L2 and were issued first, so using them waits for them
     // alone, not for the weights (a wave's loads complete in issue order)
@@ -412,28 +412,50 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
     load(rg, ga);
     load(rg + stride, gb);
     const int posv = od.pos_dev ? *od.pos_dev : 0;
-    if (ex.argmax_key) {
-        if (tid == 0) s_key = 0ull;
-        __syncthreads();
+    const bool own_stats = LN && !(PRO == 1 && ex.ln_stats);
+    double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+    for (int p = 0; p < PER; p++) {
+        const int i = tid + 256 * p;
+        if constexpr (PRO == 3) {
+            // silu(gate) * up (silu.go:121-136), the up half K values later
+            const float gv[4] = {vx[p].x, vx[p].y, vx[p].z, vx[p].w};
+            const float up[4] = {vu[p].x, vu[p].y, vu[p].z, vu[p].w};
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = gv[e] * sigmoidf_ref(gv[e]) * up[e];
+            vx[p] = make_float4(o[0], o[1], o[2], o[3]);
+        }
+        if (i < NV) {
+            if (own_stats) {
+                const float e4[4] = {vx[p].x, vx[p].y, vx[p].z, vx[p].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    // RMSNorm: sum(x^2); LayerNorm: shifted moments
+                    const double dd = (double)e4[e] - (double)x0;
+                    if constexpr (PRO == 1) s1 += dd;
+                    s2 += dd * dd;
+                }
+            }
+            s_x[i] = vx[p];
+            if constexpr (LN) s_g[i] = vg[p];
+            if constexpr (PRO == 1) s_b[i] = vb[p];
+        }
     }
-    if constexpr (PRO == 2) {
-        // RMSNorm (nn/rmsnorm.go:39-81): y = x * f32(1/sqrt(sum(x^2)/K + eps)) * gamma,
-        // the sum in f64 over the first T lanes (the row is held RPI times)
-        double s1 = 0.0, s2 = 0.0;
-        if (rloc == 0)
-#pragma unroll
-            for (int c = 0; c < C; c++)
-#pragma unroll
-                for (int i = 0; i < 8; i++) s2 += (double)xr[c][i] * (double)xr[c][i];
+    if (own_stats) {
         wave_sum2_d(s1, s2);
-        const float inv = (float)(1.0 / sqrt(s2 / (double)K + (double)ex.ln_eps));
-#pragma unroll
-        for (int c = 0; c < C; c++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) xr[c][i] = xr[c][i] * inv * gg[c][i];
+        if (lane == 0) s_mom[wave] = make_double2(s1, s2);
+    }
+    if (ex.argmax_key && tid == 0) s_key = 0ull;
+    __syncthreads();
+    float fm = 0.f, inv = 1.f;
+    if constexpr (PRO == 2) {
+        // RMSNorm (nn/rmsnorm.go:39-81): y = x * f32(1/sqrt(sum(x^2)/K + eps))
+        // * gamma, the sum in f64
+        const double t2 = (s_mom[0].y + s_mom[1].y) + (s_mom[2].y + s_mom[3].y);
+        inv = (float)(1.0 / sqrt(t2 / (double)K + (double)ex.ln_eps));
     }
     if constexpr (PRO == 1) {
-        float fm, inv;
         if (ex.ln_stats) {
             fm = ex.ln_stats[0].x;
             inv = ex.ln_stats[0].y;
@@ -442,35 +464,42 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
             // shifted moments in one pass: with c = x[0], s1 = sum(x - c)
             // and s2 = sum((x - c)^2), mean = c + s1/K and var = s2/K -
             // (s1/K)^2 — the reference's two-pass values to f64 rounding
-            // (the shift keeps the subtraction well conditioned), with one
-            // joint wave reduction instead of two dependent ones. The
-            // wave's lanes hold the row RPI times over (one copy per rloc):
-            // sum over the first T lanes only.
-            const double cs = (double)readlane_f(xr[0][0], 0);
-            double s1 = 0.0, s2 = 0.0;
-            if (rloc == 0)
-#pragma unroll
-                for (int c = 0; c < C; c++)
-#pragma unroll
-                    for (int i = 0; i < 8; i++) {
-                        const double dd = (double)xr[c][i] - cs;
-                        s1 += dd;
-                        s2 += dd * dd;
-                    }
-            wave_sum2_d(s1, s2);
-            const double ms = s1 / (double)K;
-            const double mean = cs + ms;
-            const double var = fmax(s2 / (double)K - ms * ms, 0.0);
+            // (the shift keeps the subtraction well conditioned)
+            const double t1 = (s_mom[0].x + s_mom[1].x) + (s_mom[2].x + s_mom[3].x);
+            const double t2 = (s_mom[0].y + s_mom[1].y) + (s_mom[2].y + s_mom[3].y);
+            const double ms = t1 / (double)K;
+            const double var = fmax(t2 / (double)K - ms * ms, 0.0);
             inv = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
-            fm = (float)mean;
+            fm = (float)((double)x0 + ms);
         }
+    }
+    // this lane's chunks of the (normalised) row
+    float xr[C][8];
 #pragma unroll
-        for (int c = 0; c < C; c++)
+    for (int c = 0; c < C; c++) {
+        const int v4 = 2 * (sub + T * c);
+        const float4 a0 = s_x[v4], a1 = s_x[v4 + 1];
+        xr[c][0] = a0.x; xr[c][1] = a0.y; xr[c][2] = a0.z; xr[c][3] = a0.w;
+        xr[c][4] = a1.x; xr[c][5] = a1.y; xr[c][6] = a1.z; xr[c][7] = a1.w;
+        if constexpr (LN) {
+            const float4 g0 = s_g[v4], g1 = s_g[v4 + 1];
+            const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+            float bb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if constexpr (PRO == 1) {
+                const float4 b0 = s_b[v4], b1 = s_b[v4 + 1];
+                bb[0] = b0.x; bb[1] = b0.y; bb[2] = b0.z; bb[3] = b0.w;
+                bb[4] = b1.x; bb[5] = b1.y; bb[6] = b1.z; bb[7] = b1.w;
+            }
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const float normalized = (xr[c][i] - fm) * inv;
-                xr[c][i] = normalized * gg[c][i] + bb[c][i];
+                if constexpr (PRO == 2) {
+                    xr[c][i] = xr[c][i] * inv * gg[i];
+                } else {
+                    const float normalized = (xr[c][i] - fm) * inv;
+                    xr[c][i] = normalized * gg[i] + bb[i];
+                }
             }
+        }
     }
 
     unsigned long long best = 0ull;
@@ -1075,6 +1104,7 @@ int launch_splitk_epilogue(hipStream_t s, const float* part, int S, int M, int N
 // per lane, C <= 8; {0, 0} when K does not fit.
 static void m1_shape(int K, int* T, int* C) {
     *T = *C = 0;
+    if (K % 8 != 0) return;  // the kernel reads K = 8*T*C values exactly
     const int chunks = K / 8;
     for (int t = 64; t >= 8; t >>= 1)
         if (chunks % t == 0 && chunks / t <= 8) {

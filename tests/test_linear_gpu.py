@@ -75,7 +75,8 @@ def test_gemv_microbench_shapes(gpu, M, K, N):
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 8), (3, 7, 40), (16, 65, 128), (5, 16, 3072), (2, 33, 6400),
                                    (16, 6400, 1600), (16, 1600, 6400), (13, 4800, 1600), (17, 100, 96),
-                                   (33, 65, 128), (64, 300, 256), (7, 200, 4104), (16, 1000, 1032)])
+                                   (33, 65, 128), (64, 300, 256), (7, 200, 4104), (16, 1000, 1032),
+                                   (1, 300, 776), (1, 100, 1280), (1, 50, 4096), (1, 2304, 768), (1, 768, 3072)])
 def test_linear_ragged_shapes(gpu, M, N, K):
     rng = np.random.default_rng(M * 1000 + N + K)
     x = rng.standard_normal((M, K)).astype(np.float32)
