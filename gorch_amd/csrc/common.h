@@ -28,7 +28,8 @@ struct OutDesc;
 // Optional fusions of the weight-streaming GEMV (M <= 16):
 //   ln_g/ln_b: LayerNorm of each activation row applied as it is loaded;
 //   argmax_key: per-row packed (value, index) maximum of the outputs,
-//     combined with 64-bit atomicMax into argmax_key[m] (must start at 0).
+//     combined with 64-bit atomicMax into the block's slot of a
+//     kArgmaxKeys-entry key array (argmax_slot; all zero before the call).
 struct LinearExtras {
     const float* ln_g = nullptr;
     const float* ln_b = nullptr;
@@ -456,6 +457,28 @@ __device__ __forceinline__ unsigned long long argmax_pack(float v, int idx) {
 }
 __device__ __forceinline__ int argmax_unpack(unsigned long long key) {
     return (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+}
+// Fused-argmax key arrays hold kArgmaxSlots slots of kArgmaxStride keys
+// (key[slot * kArgmaxStride + row], rows < 16, all zero between uses): a
+// GEMV block combines its rows' maxima into slot blockIdx.x % kArgmaxSlots,
+// so the end-of-kernel atomics of hundreds of blocks spread over addresses
+// 256 bytes apart instead of queueing on one; the consumer takes the
+// maximum over the slots and clears them (argmax_take).
+constexpr int kArgmaxSlots = 16, kArgmaxStride = 32, kArgmaxKeys = kArgmaxSlots * kArgmaxStride;
+__device__ __forceinline__ unsigned long long* argmax_slot(unsigned long long* key) {
+    return key + (blockIdx.x % kArgmaxSlots) * kArgmaxStride;
+}
+__device__ __forceinline__ unsigned long long argmax_take(unsigned long long* key, int row) {
+    unsigned long long v[kArgmaxSlots];
+#pragma unroll
+    for (int q = 0; q < kArgmaxSlots; q++) v[q] = key[q * kArgmaxStride + row];
+    unsigned long long best = 0ull;
+#pragma unroll
+    for (int q = 0; q < kArgmaxSlots; q++) {
+        best = v[q] > best ? v[q] : best;
+        key[q * kArgmaxStride + row] = 0ull;
+    }
+    return best;
 }
 
 // tanh-form GELU as gorch computes it (ops.go:417-443), f32 throughout.

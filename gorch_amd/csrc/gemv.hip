@@ -204,7 +204,7 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
     if (ex.argmax_key) {
         __syncthreads();
         if (threadIdx.x < 16 && m0 + (int)threadIdx.x < M)
-            atomicMax(&ex.argmax_key[m0 + threadIdx.x], s_key[threadIdx.x]);
+            atomicMax(argmax_slot(ex.argmax_key) + m0 + threadIdx.x, s_key[threadIdx.x]);
     }
 }
 
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const float* __restrict__ x, 
     }
     if (ex.argmax_key) {
         __syncthreads();
-        if (tid < MT && tid < M) atomicMax(&ex.argmax_key[tid], s_key[tid]);
+        if (tid < MT && tid < M) atomicMax(argmax_slot(ex.argmax_key) + tid, s_key[tid]);
     }
 }
 
@@ -545,7 +545,7 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
         best = wave_max_u64(best);
         if (lane == 0) atomicMax(&s_key, best);
         __syncthreads();
-        if (tid == 0) atomicMax(ex.argmax_key, s_key);
+        if (tid == 0) atomicMax(argmax_slot(ex.argmax_key), s_key);
     }
 }
 
@@ -817,7 +817,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
     }
     if (ex.argmax_key) {
         __syncthreads();
-        if (threadIdx.x < 16 && (int)threadIdx.x < M) atomicMax(&ex.argmax_key[threadIdx.x], s_key[threadIdx.x]);
+        if (threadIdx.x < 16 && (int)threadIdx.x < M) atomicMax(argmax_slot(ex.argmax_key) + threadIdx.x, s_key[threadIdx.x]);
     }
 }
 
@@ -1041,7 +1041,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
         best = row16_max_u64(best);
         if (out_lane && oc == 0 && om < M) atomicMax(&s_key[om], best);
         __syncthreads();
-        if (threadIdx.x < 16 && (int)threadIdx.x < M) atomicMax(&ex.argmax_key[threadIdx.x], s_key[threadIdx.x]);
+        if (threadIdx.x < 16 && (int)threadIdx.x < M) atomicMax(argmax_slot(ex.argmax_key) + threadIdx.x, s_key[threadIdx.x]);
     }
 }
 

@@ -340,7 +340,13 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         lf.ln_eps = eps;
         lf.x_stride = head_stride;
         lf.argmax_key = all_rows ? nullptr : argmax_key;
-        if (g->wlm_p && d <= 1024) {
+        if (head_rows == 1 && gemv_m1_prologue_ok(d)) {
+            // one row: the register GEMV over the row-major head, LayerNorm_f
+            // staged once per block in its prologue (GPT-2 small batch 1:
+            // 17.1 us on the tile-packed head)
+            GH_TRY(launch_linear_bf16_od(s, head_in, g->wlm, g->blm, nullptr, OutDesc::plain(g->logits, g->vocab), 1,
+                                         g->vocab, d, GORCH_HIP_EPI_NONE, lf));
+        } else if (g->wlm_p && d <= 1024) {
             // tile-packed head with LayerNorm_f fused: each block normalises
             // the rows it holds in registers, so no separate LayerNorm launch
             GH_TRY(launch_linear_packed_od(s, head_in, g->wlm_p, g->blm, nullptr,
@@ -377,10 +383,9 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
 __global__ void k_finalize_step(unsigned long long* key, int B, int* ids, int* hist, int* state, int inc) {
     const int step = state[1];
     for (int b = threadIdx.x; b < B; b += blockDim.x) {
-        const int tok = argmax_unpack(key[b]);
+        const int tok = argmax_unpack(argmax_take(key, b));
         ids[b] = tok;
         hist[(size_t)step * B + b] = tok;
-        key[b] = 0ull;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -402,11 +407,10 @@ __global__ __launch_bounds__(1024) void k_finalize_embed(unsigned long long* key
     const int step = state[1];
     const int pos = state[0] + inc;
     if ((int)threadIdx.x < B) {
-        const int t = argmax_unpack(key[threadIdx.x]);
+        const int t = argmax_unpack(argmax_take(key, threadIdx.x));
         tok[threadIdx.x] = t;
         ids[threadIdx.x] = t;
         hist[(size_t)step * B + threadIdx.x] = t;
-        key[threadIdx.x] = 0ull;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -766,8 +770,8 @@ gorch_hip_kvcache* gorch_hip_kvcache_create(gorch_hip_gpt* g, int batch, int cap
     if (check(hipMalloc(&c->k, elems * 4), "hipMalloc kv") || check(hipMalloc(&c->v, elems * 4), "hipMalloc kv") ||
         check(hipMalloc(&c->state, 2 * sizeof(int)), "hipMalloc state") ||
         check(hipMalloc(&c->hist, ((size_t)capacity + 1) * batch * sizeof(int)), "hipMalloc hist") ||
-        check(hipMalloc(&c->key, (size_t)batch * sizeof(unsigned long long)), "hipMalloc key") ||
-        check(hipMemset(c->key, 0, (size_t)batch * sizeof(unsigned long long)), "hipMemset key") ||
+        check(hipMalloc(&c->key, (size_t)kArgmaxKeys * sizeof(unsigned long long)), "hipMalloc key") ||
+        check(hipMemset(c->key, 0, (size_t)kArgmaxKeys * sizeof(unsigned long long)), "hipMemset key") ||
         check(hipMemset(c->state, 0, 2 * sizeof(int)), "hipMemset state")) {
         gorch_hip_kvcache_free(c);
         return nullptr;
@@ -869,7 +873,7 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
         // reuse: empty cache, zero keys (the graph reads both from device memory)
         c->len = 0;
         GH_TRY(check(hipMemsetAsync(c->state, 0, 2 * sizeof(int), s), "reset state"));
-        GH_TRY(check(hipMemsetAsync(c->key, 0, (size_t)batch * sizeof(unsigned long long), s), "reset keys"));
+        GH_TRY(check(hipMemsetAsync(c->key, 0, (size_t)kArgmaxKeys * sizeof(unsigned long long), s), "reset keys"));
     } else {
         if (g->gen_exec) (void)hipGraphExecDestroy(g->gen_exec);
         if (g->gen_graph) (void)hipGraphDestroy(g->gen_graph);

@@ -166,11 +166,10 @@ __global__ __launch_bounds__(256) void k_qwen_finalize(unsigned long long* key, 
                                                        int dim) {
     __shared__ int tok;
     if (threadIdx.x == 0) {
-        const int t = argmax_unpack(key[0]);
+        const int t = argmax_unpack(argmax_take(key, 0));
         const int step = state[1];
         tok = t;
         hist[step] = t;
-        key[0] = 0ull;
         state[0] += inc;
         state[1] = step + 1;
     }
@@ -231,7 +230,7 @@ static int qwen_ensure(gorch_hip_qwen* m, int n, int cap, int hist) {
         GH_TRY(check(hipMalloc(&m->h, (size_t)m->dim * sizeof(float)), "qwen hipMalloc"));
         GH_TRY(check(hipMalloc(&m->logits, (size_t)m->vocab * sizeof(float)), "qwen hipMalloc"));
         GH_TRY(check(hipMalloc(&m->state, 2 * sizeof(int)), "qwen hipMalloc"));
-        GH_TRY(check(hipMalloc(&m->key, sizeof(unsigned long long)), "qwen hipMalloc"));
+        GH_TRY(check(hipMalloc(&m->key, kArgmaxKeys * sizeof(unsigned long long)), "qwen hipMalloc"));
     }
     return GORCH_HIP_OK;
 }
@@ -337,7 +336,7 @@ int gorch_hip_qwen_generate(void* stream, gorch_hip_qwen* m, const int* prompt, 
     GH_TRY(check(hipStreamSynchronize(stream_of(stream)), "caller stream sync"));
     hipStream_t s = m->stream;
     GH_TRY(check(hipMemsetAsync(m->state, 0, 2 * sizeof(int), s), "reset state"));
-    GH_TRY(check(hipMemsetAsync(m->key, 0, sizeof(unsigned long long), s), "reset key"));
+    GH_TRY(check(hipMemsetAsync(m->key, 0, kArgmaxKeys * sizeof(unsigned long long), s), "reset key"));
     GH_TRY(check(hipMemcpyAsync(m->ids, prompt, (size_t)n_prompt * sizeof(int), hipMemcpyHostToDevice, s), "ids"));
     const auto t0 = std::chrono::steady_clock::now();
     GH_TRY(qwen_forward(m, s, n_prompt, true, 0, nullptr));
