@@ -55,6 +55,8 @@ def parse():
                                        "attn-xl"),
                     default=None,
                     help="run only one secondary leg and print its JSON (for profiling)")
+    ap.add_argument("--decode-steps", type=int, default=0, metavar="N",
+                    help="with --only decode-xl: N new tokens instead of 256 (short runs for PMC counters)")
     ap.add_argument("--cpu-seconds", type=float, default=9.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (PMC byte-counter calibration)")
@@ -702,7 +704,7 @@ def main():
         if args.only == "decode":
             print(json.dumps(decode_leg("gpt2-small", 1, 32, 64)))
         elif args.only == "decode-xl":
-            print(json.dumps(decode_leg("gpt2-xl", 16, 512, 256, reps=1)))
+            print(json.dumps(decode_leg("gpt2-xl", 16, 512, args.decode_steps or 256, reps=1)))
         elif args.only == "moe":
             print(json.dumps(moe_leg()))
         elif args.only == "decode-qwen":
