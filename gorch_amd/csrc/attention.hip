@@ -615,7 +615,7 @@ __device__ __forceinline__ float4 head_norm_rope(float4 v, bool norm, float4 gv,
         double s = ((double)v.x * (double)v.x + (double)v.y * (double)v.y) +
                    ((double)v.z * (double)v.z + (double)v.w * (double)v.w);
         s = wave_sum_d(s) / (double)(64 / HD4);
-        const float inv = (float)(1.0 / sqrt(s / (double)hd + (double)a.qk_eps));
+        const float inv = (float)rsqrt_f64(div_rcp(s, (double)hd, 1.0 / hd) + (double)a.qk_eps);
         v = make_float4(v.x * inv * gv.x, v.y * inv * gv.y, v.z * inv * gv.z, v.w * inv * gv.w);
     }
     if (!a.rope_cos) return v;

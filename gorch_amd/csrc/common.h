@@ -516,6 +516,21 @@ __device__ __forceinline__ double dpp_d(double v) {
 __device__ __forceinline__ float readlane_f(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
+// Row statistics in f64 (LayerNorm / RMSNorm): a / b with rb = 1/b as one
+// product and one FMA correction, and 1/sqrt(v) (v > 0) as the hardware
+// reciprocal square root refined by one Newton step. Both are accurate to
+// f64 rounding (the quotient's correction is Markstein's), where the
+// library's correctly rounded division and square root are dependent
+// sequences of ~12 f64 instructions each on the critical path of every
+// fused norm; the callers round the result to f32.
+__device__ __forceinline__ double div_rcp(double a, double b, double rb) {
+    const double q = a * rb;
+    return fma(fma(-q, b, a), rb, q);
+}
+__device__ __forceinline__ double rsqrt_f64(double v) {
+    const double y = __builtin_amdgcn_rsq(v);
+    return y * fma(-0.5 * v * y, y, 1.5);
+}
 __device__ __forceinline__ double readlane_d(double v, int l) {
     const unsigned long long b = (unsigned long long)__double_as_longlong(v);
     const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);

@@ -85,7 +85,7 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
                 float4 v = *reinterpret_cast<const float4*>(row + k);
                 s1 += (double)v.x + (double)v.y + (double)v.z + (double)v.w;
             }
-            const double mean = wave_sum_d(s1) / (double)K;
+            const double mean = div_rcp(wave_sum_d(s1), (double)K, 1.0 / K);
             double s2 = 0.0;
             for (int k = 4 * lane; k < K; k += 256) {
                 float4 v = *reinterpret_cast<const float4*>(row + k);
@@ -93,10 +93,10 @@ __global__ __launch_bounds__(NW * 64) void k_linear_bf16_mfma(
                        d3 = (double)v.w - mean;
                 s2 += d0 * d0 + d1 * d1 + d2 * d2 + d3 * d3;
             }
-            const double var = wave_sum_d(s2) / (double)K;
+            const double var = div_rcp(wave_sum_d(s2), (double)K, 1.0 / K);
             if (lane == 0) {
                 s_mean[rr] = (float)mean;
-                s_inv[rr] = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
+                s_inv[rr] = (float)rsqrt_f64(var + (double)ex.ln_eps);
             }
         }
         __syncthreads();
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const float* __restrict__ x, 
         s1 = wave_sum_d(s1);
         if (lane == 0) red[wave] = s1;
         __syncthreads();
-        const double mean = (red[0] + red[1] + red[2] + red[3]) / (double)K;
+        const double mean = div_rcp(red[0] + red[1] + red[2] + red[3], (double)K, 1.0 / K);
         __syncthreads();
         double s2 = 0.0;
         for (int k = tid; k < K; k += 256) {
@@ -258,9 +258,9 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const float* __restrict__ x, 
         s2 = wave_sum_d(s2);
         if (lane == 0) red[wave] = s2;
         __syncthreads();
-        const double var = (red[0] + red[1] + red[2] + red[3]) / (double)K;
+        const double var = div_rcp(red[0] + red[1] + red[2] + red[3], (double)K, 1.0 / K);
         __syncthreads();
-        const float inv = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
+        const float inv = (float)rsqrt_f64(var + (double)ex.ln_eps);
         const float fm = (float)mean;
         for (int k = tid; k < K; k += 256) {
             float normalized = (row[k] - fm) * inv;
@@ -448,12 +448,32 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
     }
     if (ex.argmax_key && tid == 0) s_key = 0ull;
     __syncthreads();
+    // this lane's chunks of the row (and of gamma / beta) from LDS first, so
+    // their reads overlap the statistics' f64 arithmetic
+    float xr[C][8], gr8[LN ? C : 1][8], br8[PRO == 1 ? C : 1][8];
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        const int v4 = 2 * (sub + T * c);
+        const float4 a0 = s_x[v4], a1 = s_x[v4 + 1];
+        xr[c][0] = a0.x; xr[c][1] = a0.y; xr[c][2] = a0.z; xr[c][3] = a0.w;
+        xr[c][4] = a1.x; xr[c][5] = a1.y; xr[c][6] = a1.z; xr[c][7] = a1.w;
+        if constexpr (LN) {
+            const float4 g0 = s_g[v4], g1 = s_g[v4 + 1];
+            gr8[c][0] = g0.x; gr8[c][1] = g0.y; gr8[c][2] = g0.z; gr8[c][3] = g0.w;
+            gr8[c][4] = g1.x; gr8[c][5] = g1.y; gr8[c][6] = g1.z; gr8[c][7] = g1.w;
+        }
+        if constexpr (PRO == 1) {
+            const float4 b0 = s_b[v4], b1 = s_b[v4 + 1];
+            br8[c][0] = b0.x; br8[c][1] = b0.y; br8[c][2] = b0.z; br8[c][3] = b0.w;
+            br8[c][4] = b1.x; br8[c][5] = b1.y; br8[c][6] = b1.z; br8[c][7] = b1.w;
+        }
+    }
     float fm = 0.f, inv = 1.f;
     if constexpr (PRO == 2) {
         // RMSNorm (nn/rmsnorm.go:39-81): y = x * f32(1/sqrt(sum(x^2)/K + eps))
         // * gamma, the sum in f64
         const double t2 = (s_mom[0].y + s_mom[1].y) + (s_mom[2].y + s_mom[3].y);
-        inv = (float)(1.0 / sqrt(t2 / (double)K + (double)ex.ln_eps));
+        inv = (float)rsqrt_f64(div_rcp(t2, (double)KX, 1.0 / KX) + (double)ex.ln_eps);
     }
     if constexpr (PRO == 1) {
         if (ex.ln_stats) {
@@ -467,39 +487,24 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
             // (the shift keeps the subtraction well conditioned)
             const double t1 = (s_mom[0].x + s_mom[1].x) + (s_mom[2].x + s_mom[3].x);
             const double t2 = (s_mom[0].y + s_mom[1].y) + (s_mom[2].y + s_mom[3].y);
-            const double ms = t1 / (double)K;
-            const double var = fmax(t2 / (double)K - ms * ms, 0.0);
-            inv = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
+            const double ms = div_rcp(t1, (double)KX, 1.0 / KX);
+            const double var = fmax(div_rcp(t2, (double)KX, 1.0 / KX) - ms * ms, 0.0);
+            inv = (float)rsqrt_f64(var + (double)ex.ln_eps);
             fm = (float)((double)x0 + ms);
         }
     }
-    // this lane's chunks of the (normalised) row
-    float xr[C][8];
+    if constexpr (LN) {
 #pragma unroll
-    for (int c = 0; c < C; c++) {
-        const int v4 = 2 * (sub + T * c);
-        const float4 a0 = s_x[v4], a1 = s_x[v4 + 1];
-        xr[c][0] = a0.x; xr[c][1] = a0.y; xr[c][2] = a0.z; xr[c][3] = a0.w;
-        xr[c][4] = a1.x; xr[c][5] = a1.y; xr[c][6] = a1.z; xr[c][7] = a1.w;
-        if constexpr (LN) {
-            const float4 g0 = s_g[v4], g1 = s_g[v4 + 1];
-            const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-            float bb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if constexpr (PRO == 1) {
-                const float4 b0 = s_b[v4], b1 = s_b[v4 + 1];
-                bb[0] = b0.x; bb[1] = b0.y; bb[2] = b0.z; bb[3] = b0.w;
-                bb[4] = b1.x; bb[5] = b1.y; bb[6] = b1.z; bb[7] = b1.w;
-            }
+        for (int c = 0; c < C; c++)
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 if constexpr (PRO == 2) {
-                    xr[c][i] = xr[c][i] * inv * gg[i];
+                    xr[c][i] = xr[c][i] * inv * gr8[c][i];
                 } else {
                     const float normalized = (xr[c][i] - fm) * inv;
-                    xr[c][i] = normalized * gg[i] + bb[i];
+                    xr[c][i] = normalized * gr8[c][i] + br8[c][i];
                 }
             }
-        }
     }
 
     unsigned long long best = 0ull;
@@ -577,17 +582,17 @@ __device__ void mt_ln_stats(const float* x, long long xs, int M, int K, float ep
             float4 a = *reinterpret_cast<const float4*>(row + k);
             s1 += (double)a.x + (double)a.y + (double)a.z + (double)a.w;
         }
-        const double mean = wave_sum_d(s1) / (double)K;
+        const double mean = div_rcp(wave_sum_d(s1), (double)K, 1.0 / K);
         double s2 = 0.0;
         for (int k = 4 * lane; k < K; k += 256) {
             float4 a = *reinterpret_cast<const float4*>(row + k);
             double d0 = (double)a.x - mean, d1 = (double)a.y - mean, d2 = (double)a.z - mean, d3 = (double)a.w - mean;
             s2 += d0 * d0 + d1 * d1 + d2 * d2 + d3 * d3;
         }
-        const double var = wave_sum_d(s2) / (double)K;
+        const double var = div_rcp(wave_sum_d(s2), (double)K, 1.0 / K);
         if (lane == 0) {
             s_mean[rr] = (float)mean;
-            s_inv[rr] = (float)(1.0 / sqrt(var + (double)eps));
+            s_inv[rr] = (float)rsqrt_f64(var + (double)eps);
         }
     }
 }
@@ -948,10 +953,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
                     t1 += q.x;
                     t2 += q.y;
                 }
-            const double mean = t1 / (double)K;
-            const double var = fmax(t2 / (double)K - mean * mean, 0.0);
+            const double rk = 1.0 / K;
+            const double mean = div_rcp(t1, (double)K, rk);
+            const double var = fmax(div_rcp(t2, (double)K, rk) - mean * mean, 0.0);
             s_stat[threadIdx.x][0] = (float)mean;
-            s_stat[threadIdx.x][1] = (float)(1.0 / sqrt(var + (double)ex.ln_eps));
+            s_stat[threadIdx.x][1] = (float)rsqrt_f64(var + (double)ex.ln_eps);
         }
         __syncthreads();
         ln_mean = s_stat[r][0];

@@ -30,14 +30,15 @@ __global__ __launch_bounds__(256) void k_layernorm(const float* __restrict__ x, 
     float* out = y + (size_t)blockIdx.x * N;
     double s = 0.0;
     for (int j = threadIdx.x; j < N; j += blockDim.x) s += (double)row[j];
-    const double mean = block_sum_d(s, sh) / (double)N;
+    const double rn = 1.0 / N;
+    const double mean = div_rcp(block_sum_d(s, sh), (double)N, rn);
     double v = 0.0;
     for (int j = threadIdx.x; j < N; j += blockDim.x) {
         double d = (double)row[j] - mean;
         v += d * d;
     }
-    const double var = block_sum_d(v, sh) / (double)N;
-    const float inv = (float)(1.0 / sqrt(var + (double)eps));
+    const double var = div_rcp(block_sum_d(v, sh), (double)N, rn);
+    const float inv = (float)rsqrt_f64(var + (double)eps);
     const float fm = (float)mean;
     for (int j = threadIdx.x; j < N; j += blockDim.x) {
         float normalized = (row[j] - fm) * inv;
@@ -55,7 +56,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* __
     double s = 0.0;
     for (int j = threadIdx.x; j < N; j += blockDim.x) s += (double)row[j] * (double)row[j];
     const double ss = block_sum_d(s, sh);
-    const float inv = (float)(1.0 / sqrt(ss / (double)N + (double)eps));
+    const float inv = (float)rsqrt_f64(div_rcp(ss, (double)N, 1.0 / N) + (double)eps);
     for (int j = threadIdx.x; j < N; j += blockDim.x) out[j] = row[j] * inv * g[j];
 }
 
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* x, const floa
         s += ((double)v[c].x * (double)v[c].x + (double)v[c].y * (double)v[c].y) +
              ((double)v[c].z * (double)v[c].z + (double)v[c].w * (double)v[c].w);
     s = wave_sum_d(s);
-    const float inv = (float)(1.0 / sqrt(s / (double)N + (double)eps));
+    const float inv = (float)rsqrt_f64(div_rcp(s, (double)N, 1.0 / N) + (double)eps);
     float* out = y + (size_t)m * N;
 #pragma unroll
     for (int c = 0; c < R; c++) {
@@ -215,10 +216,11 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
         }
     }
     if (!stats && !h) return;
-    const double d1 = s1 / (double)N;
+    const double rn = 1.0 / N;
+    const double d1 = div_rcp(s1, (double)N, rn);
     const double mean = (double)shift + d1;
-    const double var = fmax(s2 / (double)N - d1 * d1, 0.0);
-    const float fm = (float)mean, inv = (float)(1.0 / sqrt(var + (double)eps));
+    const double var = fmax(div_rcp(s2, (double)N, rn) - d1 * d1, 0.0);
+    const float fm = (float)mean, inv = (float)rsqrt_f64(var + (double)eps);
     if (stats && threadIdx.x == 0) stats[m] = make_float2(fm, inv);
     if (!h) return;
     // the same f32 operations as a LayerNorm fused into a GEMV's operand load

@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void k_norm_rope_rows(const float* x, float* y
         double s = ((double)v.x * (double)v.x + (double)v.y * (double)v.y) +
                    ((double)v.z * (double)v.z + (double)v.w * (double)v.w);
         s = wave_sum_d(s);
-        const float inv = (float)(1.0 / sqrt(s / (double)hd + (double)eps));
+        const float inv = (float)rsqrt_f64(div_rcp(s, (double)hd, 1.0 / hd) + (double)eps);
         v = make_float4(v.x * inv * gv.x, v.y * inv * gv.y, v.z * inv * gv.z, v.w * inv * gv.w);
     }
     float o[4];
