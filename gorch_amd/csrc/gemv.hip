@@ -448,26 +448,6 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
     }
     if (ex.argmax_key && tid == 0) s_key = 0ull;
     __syncthreads();
-    // this lane's chunks of the row (and of gamma / beta) from LDS first, so
-    // their reads overlap the statistics' f64 arithmetic
-    float xr[C][8], gr8[LN ? C : 1][8], br8[PRO == 1 ? C : 1][8];
-#pragma unroll
-    for (int c = 0; c < C; c++) {
-        const int v4 = 2 * (sub + T * c);
-        const float4 a0 = s_x[v4], a1 = s_x[v4 + 1];
-        xr[c][0] = a0.x; xr[c][1] = a0.y; xr[c][2] = a0.z; xr[c][3] = a0.w;
-        xr[c][4] = a1.x; xr[c][5] = a1.y; xr[c][6] = a1.z; xr[c][7] = a1.w;
-        if constexpr (LN) {
-            const float4 g0 = s_g[v4], g1 = s_g[v4 + 1];
-            gr8[c][0] = g0.x; gr8[c][1] = g0.y; gr8[c][2] = g0.z; gr8[c][3] = g0.w;
-            gr8[c][4] = g1.x; gr8[c][5] = g1.y; gr8[c][6] = g1.z; gr8[c][7] = g1.w;
-        }
-        if constexpr (PRO == 1) {
-            const float4 b0 = s_b[v4], b1 = s_b[v4 + 1];
-            br8[c][0] = b0.x; br8[c][1] = b0.y; br8[c][2] = b0.z; br8[c][3] = b0.w;
-            br8[c][4] = b1.x; br8[c][5] = b1.y; br8[c][6] = b1.z; br8[c][7] = b1.w;
-        }
-    }
     float fm = 0.f, inv = 1.f;
     if constexpr (PRO == 2) {
         // RMSNorm (nn/rmsnorm.go:39-81): y = x * f32(1/sqrt(sum(x^2)/K + eps))
@@ -493,18 +473,33 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const float* __restrict__ x, co
             fm = (float)((double)x0 + ms);
         }
     }
-    if constexpr (LN) {
+    // this lane's chunks of the (normalised) row
+    float xr[C][8];
 #pragma unroll
-        for (int c = 0; c < C; c++)
+    for (int c = 0; c < C; c++) {
+        const int v4 = 2 * (sub + T * c);
+        const float4 a0 = s_x[v4], a1 = s_x[v4 + 1];
+        xr[c][0] = a0.x; xr[c][1] = a0.y; xr[c][2] = a0.z; xr[c][3] = a0.w;
+        xr[c][4] = a1.x; xr[c][5] = a1.y; xr[c][6] = a1.z; xr[c][7] = a1.w;
+        if constexpr (LN) {
+            const float4 g0 = s_g[v4], g1 = s_g[v4 + 1];
+            const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+            float bb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if constexpr (PRO == 1) {
+                const float4 b0 = s_b[v4], b1 = s_b[v4 + 1];
+                bb[0] = b0.x; bb[1] = b0.y; bb[2] = b0.z; bb[3] = b0.w;
+                bb[4] = b1.x; bb[5] = b1.y; bb[6] = b1.z; bb[7] = b1.w;
+            }
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 if constexpr (PRO == 2) {
-                    xr[c][i] = xr[c][i] * inv * gr8[c][i];
+                    xr[c][i] = xr[c][i] * inv * gg[i];
                 } else {
                     const float normalized = (xr[c][i] - fm) * inv;
-                    xr[c][i] = normalized * gr8[c][i] + br8[c][i];
+                    xr[c][i] = normalized * gg[i] + bb[i];
                 }
             }
+        }
     }
 
     unsigned long long best = 0ull;
