@@ -88,6 +88,7 @@ SIGNATURES = {
     "gorch_hip_causal_softmax": (i32, [vp, vp, vp, i32, i32, i32, f32]),
     "gorch_hip_softmax_rows": (i32, [vp, vp, i32, i32]),
     "gorch_hip_argmax": (i32, [vp, vp, i32, i32, vp]),
+    "gorch_hip_sample": (i32, [vp, vp, i32, i32, C.c_float, i32, C.c_float, vp, vp, vp]),
     "gorch_hip_rope_tables": (i32, [vp, i32, i32, f32, vp, vp]),
     "gorch_hip_rope_apply": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, i32, i32, f32]),
     "gorch_hip_gqa_attention_cached": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32]),
@@ -337,6 +338,15 @@ def argmax(logits, out) -> None:
     """out: int32 device tensor [rows]."""
     rows, n = logits.shape
     _ok(lib().gorch_hip_argmax(_stream(), _p(logits), rows, n, _p(out)))
+
+
+def sample(logits, temperature, top_k, top_p, u, out, probs=None) -> None:
+    """sample() (model/generate.go:147-243) per row: logits f32 [rows, n],
+    u f64 draws [rows], out int32 [rows], probs f64 [rows, n] or None (all
+    device tensors)."""
+    rows, n = logits.shape
+    _ok(lib().gorch_hip_sample(_stream(), _p(logits), rows, n, float(temperature), int(top_k), float(top_p), _p(u),
+                               _p(out), _p(probs)))
 
 
 def linear_bf16(x, W, bias, y, residual=None, epilogue=EPI_NONE, act_bf16=False) -> None:

@@ -251,6 +251,20 @@ int gorch_hip_softmax_rows(void* stream, float* x, int rows, int cols);
 /* Row argmax, first maximum wins (argmax, model/generate.go:134-144);
  * out: device int32 [rows]. */
 int gorch_hip_argmax(void* stream, const float* logits, int rows, int n, int* out);
+/* sample() (model/generate.go:147-243, kthLargest :247-262) for each of
+ * `rows` rows of logits [rows, n] (device): scaled = logits / temperature;
+ * with 0 < top_k < n the values below the top_k-th largest become -inf;
+ * softmax in f64; with 0 < top_p < 1 the smallest positive probabilities go
+ * (lowest index first among equals) until the rest sum to at most
+ * 1.5 * top_p, then renormalised; the token is the first index whose
+ * running sum exceeds the draw u[row] (device f64 in [0, 1); the reference
+ * draws rand.Float64()), n - 1 if none. out (device int32 [rows]); probs
+ * (device f64 [rows, n], may be NULL) receives the final distribution.
+ * EINVAL for temperature <= 0 (the greedy argmax is gorch_hip_argmax) or
+ * top_k < 0; EUNSUPPORTED for n > 262144, or top_p in (0, 1) without
+ * 1 <= top_k <= 4096 (those candidates are sorted on the device). */
+int gorch_hip_sample(void* stream, const float* logits, int rows, int n, float temperature, int top_k, float top_p,
+                     const double* u, int* out, double* probs);
 
 /* Rotary tables (NewRoPE, nn/rope.go:71-96): cos/sin [max_seq, head_dim/2]
  * device f32, invFreq = f32(base^(-2i/hd)), theta = f64(f32(pos)*invFreq). */

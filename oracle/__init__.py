@@ -60,6 +60,12 @@ def _load() -> C.CDLL:
                                   C.c_int, C.c_float]),
         "orc_topk": (None, [f32p, C.c_int, C.c_int, C.c_int, f32p, i32p]),
         "orc_argmax": (C.c_int, [f32p, C.c_int]),
+        "orc_kth_largest": (C.c_float, [f32p, C.c_int, C.c_int]),
+        "orc_sample": (C.c_int, [f32p, C.c_int, C.c_float, C.c_int, C.c_float, C.c_double, vp]),
+        "orc_philox_uniform": (C.c_double, [C.c_uint64, C.c_uint32, C.c_uint32]),
+        "orc_philox4x32_10": (None, [vp, vp, vp]),
+        "orc_generate_sampled": (C.c_int, [vp, i32p, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, C.c_float,
+                                           C.c_uint64, C.c_int, i32p]),
         "orc_attention_cached": (None, [f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int,
                                         C.c_int]),
         "orc_kvcache_new": (vp, [C.c_int, C.c_int, C.c_int]),
@@ -275,6 +281,34 @@ def argmax(logits):
     return int(lib.orc_argmax(logits, logits.size))
 
 
+def kth_largest(data, k):
+    """model/generate.go:247-262."""
+    data = np.ascontiguousarray(data, np.float32)
+    return float(lib.orc_kth_largest(data, data.size, k))
+
+
+def sample(logits, temperature, top_k, top_p, r):
+    """model/generate.go:147-243 with the uniform draw r given. Returns
+    (token, final distribution as float64)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    probs = np.empty(logits.size, np.float64)
+    tok = lib.orc_sample(logits, logits.size, temperature, top_k, top_p, r, _ptr(probs))
+    return int(tok), probs
+
+
+def philox4x32_10(ctr, key):
+    c = np.ascontiguousarray(ctr, np.uint32)
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.empty(4, np.uint32)
+    lib.orc_philox4x32_10(_ptr(c), _ptr(k), _ptr(out))
+    return [int(v) for v in out]
+
+
+def philox_uniform(seed, step, row):
+    """The device sampler's draw for (seed, step, row)."""
+    return float(lib.orc_philox_uniform(seed, step, row))
+
+
 # ---------------------------------------------------------------- GPT
 
 class _GPTWeights(C.Structure):
@@ -347,6 +381,13 @@ class GPT:
         n = lib.orc_generate_cached(self.ref, prompt, prompt.size, max_new, stop_token, out,
                                     _ptr(logits), _ptr(gaps))
         return out[:n].copy(), logits, gaps
+
+    def generate_sampled(self, prompt, max_new, temperature, top_k, top_p, seed, row=0, stop_token=-1):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(prompt.size + max_new, np.int32)
+        n = lib.orc_generate_sampled(self.ref, prompt, prompt.size, max_new, stop_token, temperature, top_k,
+                                     top_p, seed, row, out)
+        return out[:n].copy()
 
 
 class KVCache:

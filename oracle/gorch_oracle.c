@@ -392,6 +392,113 @@ int orc_argmax(const float* logits, int n) {
     return maxIdx;
 }
 
+/* model/generate.go:247-262 kthLargest: k passes of a selection sort
+ * (strict >, first maximum) over a copy; the k-th pass's value. */
+float orc_kth_largest(const float* data, int n, int k) {
+    float* s = (float*)malloc((size_t)n * sizeof(float));
+    memcpy(s, data, (size_t)n * sizeof(float));
+    for (int i = 0; i < k; i++) {
+        int maxIdx = i;
+        for (int j = i + 1; j < n; j++)
+            if (s[j] > s[maxIdx]) maxIdx = j;
+        float t = s[i];
+        s[i] = s[maxIdx];
+        s[maxIdx] = t;
+    }
+    float r = s[k - 1];
+    free(s);
+    return r;
+}
+
+/* model/generate.go:147-243 sample() with the uniform draw r passed in (the
+ * reference draws rand.Float64()): scaled = logits / temperature (f32);
+ * with 0 < top_k < n every scaled value below kthLargest(scaled, top_k)
+ * becomes -inf (:155-163); softmax in f64 of the f32 differences to the
+ * maximum (:165-180); with 0 < top_p < 1 the smallest positive probability
+ * (first index among equals) is zeroed until the positive ones sum to at most
+ * float64(top_p) * 1.5, then all are divided by their sum (:182-229); the
+ * token is the first index whose running f64 sum exceeds r, else n - 1
+ * (:231-240). probs (may be NULL) receives the final distribution. */
+int orc_sample(const float* logits, int n, float temperature, int top_k, float top_p, double r, double* probs_out) {
+    if (n <= 0) return -1;
+    float* scaled = (float*)malloc((size_t)n * sizeof(float));
+    double* probs = (double*)malloc((size_t)n * sizeof(double));
+    for (int i = 0; i < n; i++) scaled[i] = logits[i] / temperature;
+    if (top_k > 0 && top_k < n) {
+        float threshold = orc_kth_largest(scaled, n, top_k);
+        for (int i = 0; i < n; i++)
+            if (scaled[i] < threshold) scaled[i] = -INFINITY;
+    }
+    float maxVal = scaled[0];
+    for (int i = 1; i < n; i++)
+        if (scaled[i] > maxVal) maxVal = scaled[i];
+    double sum = 0.0;
+    for (int i = 0; i < n; i++) {
+        probs[i] = exp((double)(scaled[i] - maxVal));
+        sum += probs[i];
+    }
+    for (int i = 0; i < n; i++) probs[i] /= sum;
+    if (top_p > 0.0f && top_p < 1.0f) {
+        const double limit = (double)top_p * 1.5;
+        for (;;) {
+            double cum = 0.0;
+            for (int i = 0; i < n; i++)
+                if (probs[i] > 0) cum += probs[i];
+            if (cum <= limit) break;
+            double minP = 1.7976931348623157e308;
+            int minI = -1;
+            for (int i = 0; i < n; i++)
+                if (probs[i] > 0 && probs[i] < minP) { minP = probs[i]; minI = i; }
+            if (minI < 0) break;
+            probs[minI] = 0.0;
+        }
+        double resum = 0.0;
+        for (int i = 0; i < n; i++) resum += probs[i];
+        for (int i = 0; i < n; i++) probs[i] /= resum;
+    }
+    int tok = n - 1;
+    double cumulative = 0.0;
+    for (int i = 0; i < n; i++) {
+        cumulative += probs[i];
+        if (r < cumulative) { tok = i; break; }
+    }
+    if (probs_out) memcpy(probs_out, probs, (size_t)n * sizeof(double));
+    free(scaled);
+    free(probs);
+    return tok;
+}
+
+/* The device sampler's uniform draws, restated for the tests (this build's
+ * own definition; the reference uses math/rand): Philox4x32-10 (Salmon,
+ * Moraes, Dror and Shaw, SC 2011) on counter (row, step, 0, 0) with key
+ * (seed low, seed high); u = ((x0 >> 5) * 2^26 + (x1 >> 6)) / 2^53. */
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+    uint32_t k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; r++) {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+        const uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+        c0 = hi1 ^ c1 ^ k0;
+        c1 = lo1;
+        c2 = hi0 ^ c3 ^ k1;
+        c3 = lo0;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = c0;
+    out[1] = c1;
+    out[2] = c2;
+    out[3] = c3;
+}
+
+double orc_philox_uniform(uint64_t seed, uint32_t step, uint32_t row) {
+    const uint32_t ctr[4] = {row, step, 0u, 0u}, key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t x[4];
+    orc_philox4x32_10(ctr, key, x);
+    return ((double)(x[0] >> 5) * 67108864.0 + (double)(x[1] >> 6)) / 9007199254740992.0;
+}
+
 /* ------------------------------------------------------------------ */
 /* KV cache (nn/kvcache.go:14-60)                                      */
 /* ------------------------------------------------------------------ */
@@ -633,6 +740,36 @@ int orc_generate_cached(const orc_gpt_weights* w, const int* prompt, int n_promp
         if (step_logits) memcpy(step_logits + (int64_t)i * V, last, (size_t)V * sizeof(float));
         if (gaps) gaps[i] = top2_gap(last, V);
         /* StopToken (:116-118): the stop token is not kept */
+        if (stop_token >= 0 && next == stop_token) break;
+        out_ids[n_out++] = next;
+        if (orc_kvcache_len(cache) >= w->max_seq) break;
+        orc_gpt_forward_cached(w, cache, &next, 1, last);
+    }
+    free(last);
+    orc_kvcache_free(cache);
+    return n_out;
+}
+
+/* model/generate.go:94-131 with Temperature > 0: each new token from
+ * sample() (:105-110), the draw for new token i of sequence `row` being
+ * orc_philox_uniform(seed, i, row). Returns the result length. */
+int orc_generate_sampled(const orc_gpt_weights* w, const int* prompt, int n_prompt, int max_new, int stop_token,
+                         float temperature, int top_k, float top_p, uint64_t seed, int row, int* out_ids) {
+    int V = w->vocab;
+    orc_kvcache* cache = orc_kvcache_new(w->layers, w->dim, w->max_seq);
+    const int* p = prompt;
+    int np = n_prompt;
+    if (np > w->max_seq) { p = prompt + (np - w->max_seq); np = w->max_seq; }
+    memcpy(out_ids, p, (size_t)np * sizeof(int));
+    int n_out = np;
+    float* logits = (float*)malloc((size_t)np * V * sizeof(float));
+    orc_gpt_forward_cached(w, cache, p, np, logits);
+    float* last = (float*)malloc((size_t)V * sizeof(float));
+    memcpy(last, logits + (int64_t)(np - 1) * V, (size_t)V * sizeof(float));
+    free(logits);
+    for (int i = 0; i < max_new; i++) {
+        int next = orc_sample(last, V, temperature, top_k, top_p, orc_philox_uniform(seed, (uint32_t)i, (uint32_t)row),
+                              NULL);
         if (stop_token >= 0 && next == stop_token) break;
         out_ids[n_out++] = next;
         if (orc_kvcache_len(cache) >= w->max_seq) break;

@@ -76,6 +76,12 @@ void orc_rope_apply(const float* x, float* y, int outer, int seqLen, int headDim
                     float sign);                                      /* nn/rope.go:172-223 */
 void orc_topk(const float* x, int B, int V, int k, float* vals, int* idx); /* index_ops.go:153-186 */
 int orc_argmax(const float* logits, int n);                          /* model/generate.go:134-144 */
+float orc_kth_largest(const float* data, int n, int k);             /* model/generate.go:247-262 */
+/* model/generate.go:147-243 with the uniform draw r given; probs may be NULL */
+int orc_sample(const float* logits, int n, float temperature, int top_k, float top_p, double r, double* probs);
+/* Philox4x32-10 uniform in [0, 1) for (seed, step, row): the device sampler's draw */
+double orc_philox_uniform(uint64_t seed, uint32_t step, uint32_t row);
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 
 /* MHA.ForwardCached's attention loops (nn/attention.go:348-397) for one
  * sequence: q [newSeq, dim], K/V [posOffset + newSeq, dim]; out [newSeq, dim]. */
@@ -126,6 +132,11 @@ int orc_gpt_forward(const orc_gpt_weights* w, const int* ids, int n, float* logi
  * when it is chosen (it is not appended). */
 int orc_generate_cached(const orc_gpt_weights* w, const int* prompt, int n_prompt,
                         int max_new, int stop_token, int* out_ids, float* step_logits, float* gaps);
+/* generateCached with Temperature > 0 (model/generate.go:94-131, sample at
+ * :105-110): new token i of sequence `row` drawn with
+ * orc_philox_uniform(seed, i, row). Returns the result length. */
+int orc_generate_sampled(const orc_gpt_weights* w, const int* prompt, int n_prompt, int max_new, int stop_token,
+                         float temperature, int top_k, float top_p, uint64_t seed, int row, int* out_ids);
 
 /* ---- GQA with KV cache (nn/gqa.go:213-363) ----
  * Linear weights [out, in] (bf16 when linear_bf16, else f32), biases
