@@ -78,6 +78,7 @@ struct gorch_hip_gpt {
     hipGraph_t gen_graph = nullptr;
     hipGraphExec_t gen_exec = nullptr;
     std::vector<const void*> gen_sig;
+    int* sample_err = nullptr;  // sampled generation: top-p support overflow flag
 };
 
 struct gorch_hip_kvcache {
@@ -754,6 +755,7 @@ void gorch_hip_gpt_free(gorch_hip_gpt* g) {
     (void)hipFree(g->stats);
     (void)hipFree(g->wpart);
     (void)hipFree(g->ids);
+    (void)hipFree(g->sample_err);
     delete g;
 }
 
@@ -840,9 +842,20 @@ namespace gh {
 // or once the cache holds MaxSeq tokens. Every sequence's row of out_ids is
 // np + max_new wide; its length goes to out_lens[b] (nullable) and the
 // longest to *out_len (nullable).
+// Sampled choice (generateCached with Temperature > 0, model/generate.go:
+// 105-110): the step's LM head writes logits instead of argmax keys and
+// k_sample draws each sequence's token into its key slot, which the
+// finalize kernel decodes as it does the argmax's.
+struct GenSample {
+    float temperature;
+    int top_k;
+    float top_p;
+    unsigned long long seed;
+};
+
 static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int batch, int n_prompt, int max_new,
                          int stop_token, int* out_ids, int* out_lens, int* out_len, float* step_logits,
-                         float* timing_ms, int flags) {
+                         float* timing_ms, int flags, const GenSample* smp = nullptr) {
     GH_REQUIRE(g && prompts && out_ids && batch > 0 && n_prompt > 0 && max_new >= 0,
                "gorch_hip_generate_cached: bad arguments");
     GH_TRY(bf16_gate(stream_of(stream)));
@@ -886,9 +899,21 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
         if (!c) return GORCH_HIP_ENOMEM;
         g->gen_cache = c;
     }
+    if (smp) {
+        if (!g->sample_err && check(hipMalloc(&g->sample_err, sizeof(int)), "hipMalloc sample flag"))
+            return GORCH_HIP_ENOMEM;
+        GH_TRY(check(hipMemsetAsync(g->sample_err, 0, sizeof(int), s), "reset sample flag"));
+    }
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     int rc = GORCH_HIP_OK;
     const bool use_graph = (flags & 1) && !step_logits;
+    // the step's choice: the fused argmax, or the sampler over the logits
+    unsigned long long* head_key = smp ? nullptr : c->key;
+    auto sample_tokens = [&]() -> int {
+        if (!smp) return GORCH_HIP_OK;
+        return launch_sample(s, g->logits, batch, g->vocab, smp->temperature, smp->top_k, smp->top_p, nullptr,
+                             smp->seed, c->state + 1, nullptr, nullptr, c->key, g->sample_err);
+    };
     auto fail = [&](int r) {
         rc = r;
         return r;
@@ -906,7 +931,7 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
         // prefill: logits of the last prompt row per sequence -> token 0
         // batches of up to 16: each choice also embeds the next step's input
         const bool fin_embed = batch <= 16;
-        if (forward(g, c, np, false, s, c->key) || choose_tokens(g, c, np, s, fin_embed)) {
+        if (forward(g, c, np, false, s, head_key) || sample_tokens() || choose_tokens(g, c, np, s, fin_embed)) {
             fail(GORCH_HIP_ERUNTIME);
             break;
         }
@@ -917,7 +942,8 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
         }
         // one decode step: forward the latest token of each sequence, choose the next
         auto step = [&]() -> int {
-            GH_TRY(forward(g, c, 1, false, s, c->key, fin_embed));
+            GH_TRY(forward(g, c, 1, false, s, head_key, fin_embed));
+            GH_TRY(sample_tokens());
             return choose_tokens(g, c, 1, s, fin_embed);
         };
         if (use_graph && forwards > 0) {
@@ -926,7 +952,15 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
                                                   g->logits, g->ids, g->part, g->stats, c->k,
                                                   c->v,    c->state, c->hist, c->key,
                                                   // the kernels differ by the deterministic setting
-                                                  reinterpret_cast<const void*>(deterministic() ? 1 : 0)};
+                                                  reinterpret_cast<const void*>(deterministic() ? 1 : 0),
+                                                  // and by the sampling parameters (kernel arguments)
+                                                  reinterpret_cast<const void*>(smp ? 1 : 0), g->sample_err,
+                                                  reinterpret_cast<const void*>(
+                                                      smp ? (uintptr_t)__builtin_bit_cast(uint32_t, smp->temperature) : 0),
+                                                  reinterpret_cast<const void*>(smp ? (uintptr_t)smp->top_k : 0),
+                                                  reinterpret_cast<const void*>(
+                                                      smp ? (uintptr_t)__builtin_bit_cast(uint32_t, smp->top_p) : 0),
+                                                  reinterpret_cast<const void*>(smp ? (uintptr_t)smp->seed : 0)};
             if (!g->gen_exec || g->gen_sig != sig) {
                 if (g->gen_exec) (void)hipGraphExecDestroy(g->gen_exec);
                 if (g->gen_graph) (void)hipGraphDestroy(g->gen_graph);
@@ -1006,6 +1040,18 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
             break;
         }
         if (check(hipStreamSynchronize(s), "generate sync")) { fail(GORCH_HIP_ERUNTIME); break; }
+        if (smp) {
+            int flag = 0;
+            if (check(hipMemcpy(&flag, g->sample_err, sizeof(int), hipMemcpyDeviceToHost), "sample flag")) {
+                fail(GORCH_HIP_ERUNTIME);
+                break;
+            }
+            if (flag) {
+                set_error("gorch_hip_generate: more than 4096 top-p candidates (ties at the top-k threshold)");
+                fail(GORCH_HIP_EUNSUPPORTED);
+                break;
+            }
+        }
         // result = (truncated) prompt followed by the generated tokens, each
         // sequence cut before its first stop token
         const int width = np + max_new;
@@ -1060,12 +1106,23 @@ int gorch_hip_generate(void* stream, gorch_hip_gpt* g, const int* prompts, int b
                        const gorch_hip_generate_config* cfg, int* out_ids, int* out_lens, float* step_logits,
                        float* timing_ms) {
     GH_REQUIRE(cfg && out_lens, "gorch_hip_generate: null config or out_lens");
-    if (!cfg->use_kv_cache || cfg->temperature != 0.0f) {
-        set_error("gorch_hip_generate: only greedy decoding with the KV cache runs here (Temperature 0, UseKVCache)");
+    if (!cfg->use_kv_cache) {
+        set_error("gorch_hip_generate: only decoding with the KV cache runs here (UseKVCache)");
         return GORCH_HIP_EUNSUPPORTED;
     }
+    if (cfg->temperature == 0.0f)
+        return generate_impl(stream, g, prompts, batch, n_prompt, cfg->max_new_tokens, cfg->stop_token, out_ids,
+                             out_lens, nullptr, step_logits, timing_ms, cfg->flags);
+    // sampled: up to 16 sequences (the finalize kernel's key path)
+    GH_REQUIRE(g && batch >= 1, "gorch_hip_generate: bad arguments");
+    if (batch > 16) {
+        set_error("gorch_hip_generate: sampled generation runs for up to 16 sequences");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
+    GH_TRY(sample_check(batch, g->vocab, cfg->temperature, cfg->top_k, cfg->top_p));
+    const GenSample smp{cfg->temperature, cfg->top_k, cfg->top_p, cfg->seed};
     return generate_impl(stream, g, prompts, batch, n_prompt, cfg->max_new_tokens, cfg->stop_token, out_ids,
-                         out_lens, nullptr, step_logits, timing_ms, cfg->flags);
+                         out_lens, nullptr, step_logits, timing_ms, cfg->flags, &smp);
 }
 
 }  // extern "C"

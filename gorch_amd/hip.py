@@ -438,7 +438,8 @@ class SafeTensors:
 class GenerateConfig(C.Structure):
     """gorch_hip_generate_config: GenerateConfig (model/generate.go:13-20)."""
     _fields_ = [("max_new_tokens", C.c_int), ("temperature", C.c_float), ("top_k", C.c_int),
-                ("top_p", C.c_float), ("stop_token", C.c_int), ("use_kv_cache", C.c_int), ("flags", C.c_int)]
+                ("top_p", C.c_float), ("stop_token", C.c_int), ("use_kv_cache", C.c_int), ("flags", C.c_int),
+                ("seed", C.c_uint64)]
 
 
 class GPT:
@@ -517,10 +518,13 @@ class GPT:
         ids = out.reshape(-1)[: B * L].reshape(B, L).copy()
         return ids, logits, {"prefill_ms": timing[0], "decode_ms": timing[1], "decode_forwards": int(timing[2])}
 
-    def generate(self, prompts, max_new: int, stop_token: int = -1, want_logits=False, use_graph=True):
-        """GenerateWithConfig(GreedyConfig(max_new) + StopToken, UseKVCache)
-        (model/generate.go:52-131) for [batch, n_prompt] prompts. Returns (a
-        list of per-sequence id arrays, step logits or None, timing dict)."""
+    def generate(self, prompts, max_new: int, stop_token: int = -1, want_logits=False, use_graph=True,
+                 temperature: float = 0.0, top_k: int = 0, top_p: float = 0.0, seed: int = 0):
+        """GenerateWithConfig(cfg, UseKVCache) (model/generate.go:52-131)
+        for [batch, n_prompt] prompts: greedy with temperature 0, else
+        sample() with top_k / top_p and Philox draws from ``seed``. Returns
+        (a list of per-sequence id arrays, step logits or None, timing
+        dict)."""
         import numpy as np
 
         prompts = np.ascontiguousarray(np.atleast_2d(prompts), np.int32)
@@ -528,7 +532,8 @@ class GPT:
         width = min(n, self.cfg["max_seq"]) + max_new
         out = np.zeros((B, width), np.int32)
         lens = np.zeros(B, np.int32)
-        cfg = GenerateConfig(max_new, 0.0, 0, 0.0, stop_token, 1, int(use_graph))
+        cfg = GenerateConfig(max_new, float(temperature), int(top_k), float(top_p), stop_token, 1, int(use_graph),
+                             int(seed))
         V = self.cfg["vocab"]
         logits = np.empty((max_new, B, V), np.float32) if want_logits else None
         timing = (C.c_float * 3)()

@@ -495,11 +495,15 @@ int gorch_hip_generate_cached(void* stream, gorch_hip_gpt* gpt, const int* promp
                               int max_new, int* out_ids, int* out_len, float* step_logits, float* timing_ms,
                               int flags);
 
-/* GenerateConfig (model/generate.go:13-42). Only greedy decoding with the
- * KV cache runs on this path: temperature must be 0 and use_kv_cache 1
- * (else GORCH_HIP_EUNSUPPORTED: sampling stays on the caller's CPU path);
- * top_k / top_p are ignored as in greedy mode. stop_token -1 disables the
- * stop. flags bit 0: replay the decode step from a HIP graph. */
+/* GenerateConfig (model/generate.go:13-42) with UseKVCache (use_kv_cache 1,
+ * else GORCH_HIP_EUNSUPPORTED). temperature 0: greedy (top_k / top_p
+ * ignored, as the reference). temperature > 0: each new token from sample()
+ * (model/generate.go:105-110, 147-243; gorch_hip_sample) over the step's
+ * logits, for up to 16 sequences; the uniform draw for new token i of
+ * sequence b is Philox4x32-10 of counter (b, i, 0, 0) under key (seed low,
+ * seed high), u = ((x0 >> 5) * 2^26 + (x1 >> 6)) / 2^53 (the reference
+ * draws math/rand's stream instead). stop_token -1 disables the stop.
+ * flags bit 0: replay the decode step from a HIP graph. */
 typedef struct {
     int max_new_tokens;
     float temperature;
@@ -508,6 +512,7 @@ typedef struct {
     int stop_token;
     int use_kv_cache;
     int flags;
+    unsigned long long seed;
 } gorch_hip_generate_config;
 /* GenerateWithConfig with UseKVCache (generateCached, model/generate.go:94-131)
  * for `batch` prompts: each sequence stops on its own at stop_token (which

@@ -326,3 +326,65 @@ def test_deterministic_mode_bit_identical(gpu, cfg, prompt):
     assert list(ids[0]) == list(ref)
     assert rel_err(logits[0][0], ref_logits[0]) <= 1e-3
     g.close()
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+@pytest.mark.parametrize("T,K,P", [(1.0, 0, 0.0), (0.8, 10, 0.9), (1.5, 5, 0.4)])
+def test_generate_sampled_matches_oracle(tiny, use_graph, T, K, P):
+    """GenerateWithConfig with Temperature > 0 and the KV cache
+    (model/generate.go:94-131, sample() at :147-243): every new token drawn
+    from the step's logits with the Philox draw (seed, token index,
+    sequence); token-identical to the oracle's generateCached + sample()
+    given the same draws, for 4 sequences and 20 tokens."""
+    w, g, o = tiny
+    prompts = np.stack([syn.prompt_ids(6, TINY["vocab"], seed=120 + b) for b in range(4)])
+    ids, _, _ = g.generate(prompts, 20, use_graph=use_graph, temperature=T, top_k=K, top_p=P, seed=2024)
+    for b in range(4):
+        ref = o.generate_sampled(prompts[b], 20, T, K, P, 2024, row=b)
+        assert list(ids[b]) == list(ref), b
+
+
+def test_generate_sampled_seed_and_stop(tiny):
+    w, g, o = tiny
+    prompts = np.stack([syn.prompt_ids(6, TINY["vocab"], seed=130 + b) for b in range(2)])
+    a, _, _ = g.generate(prompts, 16, temperature=1.0, seed=5)
+    b_, _, _ = g.generate(prompts, 16, temperature=1.0, seed=5)
+    c, _, _ = g.generate(prompts, 16, temperature=1.0, seed=6)
+    assert all(np.array_equal(a[i], b_[i]) for i in range(2))
+    assert any(not np.array_equal(a[i], c[i]) for i in range(2))
+    # top_k = 1 keeps only the maximum: the greedy tokens
+    s1, _, _ = g.generate(prompts, 16, temperature=0.7, top_k=1, seed=9)
+    gr, _, _ = g.generate(prompts, 16)
+    assert all(np.array_equal(s1[i], gr[i]) for i in range(2))
+    # a stop token drawn in the sampled run ends that sequence without it
+    stop = int(a[0][8])
+    st, _, _ = g.generate(prompts, 16, stop_token=stop, temperature=1.0, seed=5)
+    for i in range(2):
+        ref = o.generate_sampled(prompts[i], 16, 1.0, 0, 0.0, 5, row=i, stop_token=stop)
+        assert list(st[i]) == list(ref), i
+
+
+def test_generate_sampled_gpt2_vocab(gpu):
+    """The sampler at GPT-2's vocabulary (50,257 logits per row, top-k 40,
+    temperature 0.8: the reference's DefaultGenerateConfig) over a small
+    model, 2 sequences, graph-replayed steps."""
+    cfg = dict(vocab=50257, dim=64, heads=4, layers=2, max_seq=48)
+    w = syn.gpt2_weights(cfg, seed=47, random_affine=True)
+    g, o = gpu.GPT(w), orc.GPT(w)
+    prompts = np.stack([syn.prompt_ids(8, cfg["vocab"], seed=140 + b) for b in range(2)])
+    ids, _, _ = g.generate(prompts, 12, temperature=0.8, top_k=40, seed=77)
+    for b in range(2):
+        ref = o.generate_sampled(prompts[b], 12, 0.8, 40, 0.0, 77, row=b)
+        assert list(ids[b]) == list(ref), b
+    g.close()
+
+
+def test_generate_sampled_argument_errors(tiny, gpu):
+    w, g, o = tiny
+    prompts = np.stack([syn.prompt_ids(4, TINY["vocab"], seed=150 + b) for b in range(17)])
+    with pytest.raises(gpu.HipError) as e:   # sampled generation: up to 16 sequences
+        g.generate(prompts, 4, temperature=1.0)
+    assert e.value.rc == 1
+    with pytest.raises(gpu.HipError) as e:   # top-p needs 1 <= top_k <= 4096
+        g.generate(prompts[:2], 4, temperature=1.0, top_p=0.5)
+    assert e.value.rc == 1
