@@ -106,7 +106,14 @@ def test_add_rmsnorm(gpu, M, N):
                                                         # than 256 rows: the 16-wave two-pass kernel that
                                                         # the GPT-2 XL batch-16 step runs (25 heads x 16)
                                                         (16, 1, 511, 25, 64), (16, 1, 767, 25, 64),
-                                                        (8, 1, 600, 16, 128), (4, 1, 300, 8, 80)])
+                                                        (8, 1, 600, 16, 128), (4, 1, 300, 8, 80),
+                                                        # a short cache in a longer capacity, causal new
+                                                        # rows, 900 rows
+                                                        (12, 1, 255, 25, 64), (2, 5, 600, 25, 64),
+                                                        (16, 1, 900, 25, 64),
+                                                        # past 16384 visible rows (no LDS score row):
+                                                        # the online-softmax long-cache kernel
+                                                        (1, 1, 16400, 2, 64), (2, 1, 17000, 4, 128)])
 def test_attention_cached(gpu, batch, new_seq, pos, heads, hd):
     rng = np.random.default_rng(pos + heads)
     d = heads * hd
