@@ -71,10 +71,11 @@ inline int ksplit_slices(int K, int S) {
 // sample() (model/generate.go:147-243) per row (sample.hip): the draw is
 // u[row], or Philox4x32-10 of (seed, *step, row) when u is null; key (may be
 // null) receives a fused-argmax key decoding to the token, err (may be null)
-// is set when the top-p candidates exceed the sort's capacity.
+// is set when the top-p candidates exceed the sort's capacity. nucleus: top-p
+// as the Qwen loop's sampleLogits (model/qwen/generate.go:121-152).
 int launch_sample(hipStream_t s, const float* logits, int rows, int n, float temperature, int top_k, float top_p,
                   const double* u, unsigned long long seed, const int* step, int* out, double* probs,
-                  unsigned long long* key, int* err);
+                  unsigned long long* key, int* err, bool nucleus = false);
 int sample_check(int rows, int n, float temperature, int top_k, float top_p);
 // Per-(device, stream) scratch for K-split partials; nullptr when it would
 // have to grow during stream capture or the allocation fails.

@@ -19,6 +19,8 @@
 // launches of their own and the matrix-core GEMM for the Linears.
 #include <algorithm>
 #include <chrono>
+#include <cmath>
+#include <cstring>
 #include <vector>
 
 #include "common.h"
@@ -123,12 +125,14 @@ extern "C" int gorch_hip_qwen_block_forward_cached(void* stream, const gorch_hip
 // ---------------------------------------------------------------- the model
 
 // model/qwen Model (qwen.go:12-98) over caller-owned weights, with its own KV
-// cache, activations and decode state, for greedy generation (Generate,
+// cache, activations and decode state, for generation (Generate,
 // generate.go:35-66). Per token, one captured HIP graph: the blocks' one-row
 // steps reading the position from device memory, the final RMSNorm, the tied
-// head with the argmax fused into it, and a kernel that turns the argmax key
-// into the next token, appends it to the history, advances the position and
-// writes the next input row (the token's embedding).
+// head with the argmax fused into it (greedy) or followed by the sampler
+// (sampleLogits, generate.go:94-181, which leaves its token in the argmax
+// key), and a kernel that turns the key into the next token, appends it to
+// the history, advances the position and writes the next input row (the
+// token's embedding).
 struct gorch_hip_qwen {
     std::vector<gorch_hip_qwen_block> blocks;
     const uint16_t* embed_bf16 = nullptr;
@@ -150,6 +154,11 @@ struct gorch_hip_qwen {
     int* hist = nullptr;     // chosen tokens [hist_cap]
     int hist_cap = 0;
     unsigned long long* key = nullptr;  // fused-argmax key, zero between steps
+    int* sample_err = nullptr;          // set by the sampler: top-p candidates past its sort
+    // the running generation's sampling config (temperature 0: greedy)
+    float smp_t = 0.f, smp_p = 0.f;
+    int smp_k = 0;
+    unsigned long long smp_seed = 0;
     hipStream_t stream = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -231,6 +240,7 @@ static int qwen_ensure(gorch_hip_qwen* m, int n, int cap, int hist) {
         GH_TRY(check(hipMalloc(&m->logits, (size_t)m->vocab * sizeof(float)), "qwen hipMalloc"));
         GH_TRY(check(hipMalloc(&m->state, 2 * sizeof(int)), "qwen hipMalloc"));
         GH_TRY(check(hipMalloc(&m->key, kArgmaxKeys * sizeof(unsigned long long)), "qwen hipMalloc"));
+        GH_TRY(check(hipMalloc(&m->sample_err, sizeof(int)), "qwen hipMalloc"));
     }
     return GORCH_HIP_OK;
 }
@@ -249,12 +259,17 @@ static int qwen_forward(gorch_hip_qwen* m, hipStream_t s, int n, bool prefill, i
         GH_TRY(qwen_block_core(s, &m->blocks[l], m->x, n, kc, vc, pos, m->cap, m->ws, pos_dev));
     }
     // final RMSNorm of the last row, then the tied head (MatMulTransB with
-    // the bf16 embedding, qwen.go:84) with the greedy choice fused in
+    // the bf16 embedding, qwen.go:84) with the greedy choice fused in, or
+    // the logits sampled (the draw of token i is Philox(seed, i, 0), the
+    // step read from state[1])
     GH_TRY(launch_rmsnorm(s, m->x + (size_t)(n - 1) * d, m->norm, m->h, 1, d, m->eps));
     LinearExtras ex;
-    ex.argmax_key = m->key;
+    if (m->smp_t <= 0.f) ex.argmax_key = m->key;
     GH_TRY(launch_linear_bf16_od(s, m->h, m->embed_bf16, nullptr, nullptr, OutDesc::plain(m->logits, m->vocab), 1,
                                  m->vocab, d, GORCH_HIP_EPI_NONE, ex));
+    if (m->smp_t > 0.f)
+        GH_TRY(launch_sample(s, m->logits, 1, m->vocab, m->smp_t, m->smp_k, m->smp_p, nullptr, m->smp_seed,
+                             m->state + 1, nullptr, nullptr, m->key, m->sample_err, true));
     hipLaunchKernelGGL(k_qwen_finalize, dim3(1), dim3(256), 0, s, m->key, m->hist, m->state, n, m->embed_f32, m->x,
                        d);
     count(CNT_ARGMAX);
@@ -306,16 +321,22 @@ void gorch_hip_qwen_destroy(gorch_hip_qwen* m) {
     (void)hipStreamSynchronize(m->stream);
     qwen_drop_graph(m);
     for (void* p : {(void*)m->kv, (void*)m->ws, (void*)m->x, (void*)m->h, (void*)m->logits, (void*)m->ids,
-                    (void*)m->state, (void*)m->hist, (void*)m->key})
+                    (void*)m->state, (void*)m->hist, (void*)m->key, (void*)m->sample_err})
         (void)hipFree(p);
     release_stream_scratch(m->stream);
     (void)hipStreamDestroy(m->stream);
     delete m;
 }
 
-int gorch_hip_qwen_generate(void* stream, gorch_hip_qwen* m, const int* prompt, int n_prompt, int max_new,
-                            const int* stop_tokens, int n_stop, int* out_ids, int* out_len, float* step_logits,
-                            float* timing_ms, int flags) {
+}  // extern "C"
+
+namespace gh {
+
+// Generate (model/qwen/generate.go:35-66) with temperature t (0: greedy) and
+// the sampling config of sampleLogits otherwise.
+static int qwen_generate(void* stream, gorch_hip_qwen* m, const int* prompt, int n_prompt, int max_new,
+                         const int* stop_tokens, int n_stop, int* out_ids, int* out_len, float* step_logits,
+                         float* timing_ms, int flags, float t, int top_k, float top_p, unsigned long long seed) {
     GH_REQUIRE(m && prompt && out_ids && out_len && max_new >= 0 && n_stop >= 0 && (n_stop == 0 || stop_tokens),
                "gorch_hip_qwen_generate: bad arguments");
     GH_REQUIRE(n_prompt > 0, "qwen: empty prompt");
@@ -337,6 +358,11 @@ int gorch_hip_qwen_generate(void* stream, gorch_hip_qwen* m, const int* prompt, 
     hipStream_t s = m->stream;
     GH_TRY(check(hipMemsetAsync(m->state, 0, 2 * sizeof(int), s), "reset state"));
     GH_TRY(check(hipMemsetAsync(m->key, 0, kArgmaxKeys * sizeof(unsigned long long), s), "reset key"));
+    GH_TRY(check(hipMemsetAsync(m->sample_err, 0, sizeof(int), s), "reset sample flag"));
+    m->smp_t = t;
+    m->smp_k = top_k;
+    m->smp_p = top_p;
+    m->smp_seed = seed;
     GH_TRY(check(hipMemcpyAsync(m->ids, prompt, (size_t)n_prompt * sizeof(int), hipMemcpyHostToDevice, s), "ids"));
     const auto t0 = std::chrono::steady_clock::now();
     GH_TRY(qwen_forward(m, s, n_prompt, true, 0, nullptr));
@@ -354,8 +380,15 @@ int gorch_hip_qwen_generate(void* stream, gorch_hip_qwen* m, const int* prompt, 
     // each step is launched directly with the host's position
     bool graph = (flags & 1) && !step_logits && k > 0;
     if (graph) {
-        const std::vector<const void*> sig = {m->kv, m->ws, m->x, m->hist, reinterpret_cast<const void*>(
-                                                                              deterministic() ? 1 : 0)};
+        uint32_t tb, pb;
+        memcpy(&tb, &t, 4);
+        memcpy(&pb, &top_p, 4);
+        const std::vector<const void*> sig = {m->kv, m->ws, m->x, m->hist,
+                                              reinterpret_cast<const void*>(deterministic() ? 1 : 0),
+                                              reinterpret_cast<const void*>((uintptr_t)tb),
+                                              reinterpret_cast<const void*>((uintptr_t)pb),
+                                              reinterpret_cast<const void*>((uintptr_t)(unsigned)top_k),
+                                              reinterpret_cast<const void*>((uintptr_t)seed)};
         if (!m->exec || m->sig != sig) {
             qwen_drop_graph(m);
             GH_TRY(check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture"));
@@ -413,6 +446,14 @@ int gorch_hip_qwen_generate(void* stream, gorch_hip_qwen* m, const int* prompt, 
     int keep = chosen;
     const int cut = first_stop(chosen);
     if (cut >= 0) keep = cut;
+    if (t > 0.f) {
+        int err = 0;
+        GH_TRY(check(hipMemcpy(&err, m->sample_err, sizeof(int), hipMemcpyDeviceToHost), "sample flag"));
+        if (err) {
+            set_error("qwen generate: more than 4096 top-p candidates (values tied at the top-k threshold)");
+            return GORCH_HIP_EUNSUPPORTED;
+        }
+    }
     for (int i = 0; i < keep; i++) out_ids[n_prompt + i] = hist[i];
     *out_len = n_prompt + keep;
     if (timing_ms) {
@@ -422,6 +463,29 @@ int gorch_hip_qwen_generate(void* stream, gorch_hip_qwen* m, const int* prompt, 
         timing_ms[3] = graph ? 1.f : 0.f;
     }
     return GORCH_HIP_OK;
+}
+
+}  // namespace gh
+
+extern "C" {
+
+int gorch_hip_qwen_generate(void* stream, gorch_hip_qwen* m, const int* prompt, int n_prompt, int max_new,
+                            const int* stop_tokens, int n_stop, int* out_ids, int* out_len, float* step_logits,
+                            float* timing_ms, int flags) {
+    return qwen_generate(stream, m, prompt, n_prompt, max_new, stop_tokens, n_stop, out_ids, out_len, step_logits,
+                         timing_ms, flags, 0.f, 0, 0.f, 0ull);
+}
+
+int gorch_hip_qwen_generate_sampled(void* stream, gorch_hip_qwen* m, const int* prompt, int n_prompt, int max_new,
+                                    const int* stop_tokens, int n_stop, float temperature, int top_k, float top_p,
+                                    unsigned long long seed, int* out_ids, int* out_len, float* step_logits,
+                                    float* timing_ms, int flags) {
+    GH_REQUIRE(m, "gorch_hip_qwen_generate_sampled: null model");
+    GH_REQUIRE(temperature >= 0.f && std::isfinite(temperature),
+               "gorch_hip_qwen_generate_sampled: temperature must be finite and >= 0");
+    if (temperature > 0.f) GH_TRY(sample_check(1, m->vocab, temperature, top_k, top_p));
+    return qwen_generate(stream, m, prompt, n_prompt, max_new, stop_tokens, n_stop, out_ids, out_len, step_logits,
+                         timing_ms, flags, temperature, top_k, top_p, seed);
 }
 
 }  // extern "C"

@@ -1,6 +1,7 @@
 // sample.hip — the sampled next-token choice of generateCached with
 // Temperature > 0 (model/generate.go:105-110; sample() at :147-243,
-// kthLargest at :247-262), one 1024-thread block per row of logits.
+// kthLargest at :247-262) and of the Qwen Generate loop (sampleLogits,
+// model/qwen/generate.go:94-181), one 1024-thread block per row of logits.
 //
 //   scaled = logits / temperature (f32)
 //   0 < top_k < n: values below the top_k-th largest scaled value -> -inf
@@ -16,6 +17,11 @@
 //     candidates through ties at the top-k threshold set the error flag) are
 //     sorted in LDS by that order (bitonic), prefix-summed, and the prefix
 //     kept.
+//   nucleus (the Qwen loop's top-p, 0 < top_p < 1): the shortest prefix, in
+//     order of (p descending, index ascending), whose running sum reaches
+//     f64(top_p) is kept and divided by its sum, every other probability set
+//     to 0 (sort.Slice leaves the order of equal probabilities open; this
+//     one takes the lower index first). Same candidate limits and sort.
 //   token = the first index whose running sum of the final probabilities
 //     exceeds the uniform draw r (n - 1 if none).
 //
@@ -135,6 +141,7 @@ struct SampleArgs {
     double* probs;             // final distribution [rows, n] (may be null)
     unsigned long long* key;   // fused-argmax key slot 0 of row b gets the token (may be null)
     int* err;                  // set to 1 when the top-p candidates exceed kSampleCap
+    int nucleus;               // top-p as sampleLogits' nucleus cut, else as sample()
 };
 
 __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
@@ -241,7 +248,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
                     const bool desc = (i & size) == 0;
                     const double pi = s_p[i], pj = s_p[j];
                     const int ii = s_idx[i], ij = s_idx[j];
-                    const bool j_first = pj > pi || (pj == pi && ij > ii);
+                    const bool j_first = pj > pi || (pj == pi && (a.nucleus ? ij < ii : ij > ii));
                     if (j_first == desc) {
                         s_p[i] = pj;
                         s_p[j] = pi;
@@ -253,9 +260,10 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
             }
         }
         // kept: the longest sorted prefix whose sum is at most the limit
-        // (the prefix sums increase with its length)
+        // (the prefix sums increase with its length); nucleus: every entry
+        // whose preceding sum is still below top_p
         constexpr int PER = kSampleCap / kSampleThreads;
-        const double limit = (double)a.top_p * 1.5;
+        const double limit = a.nucleus ? (double)a.top_p : (double)a.top_p * 1.5;
         double loc = 0.0;
 #pragma unroll
         for (int q = 0; q < PER; q++) {
@@ -270,8 +278,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
         for (int q = 0; q < PER; q++) {
             const int j = tid * PER + q;
             if (j < cnt) {
+                const bool kept = a.nucleus ? run < limit : run + s_p[j] <= limit;
                 run += s_p[j];
-                if (run <= limit) {
+                if (kept) {
                     keep++;
                     kept_sum += s_p[j];
                 }
@@ -292,7 +301,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     auto final_p = [&](int i) {
         const double p = expo(i) / sum;
         if (!use_p) return p;
-        return (((s_keep[i >> 5] >> (i & 31)) & 1u) ? p : 0.0) / resum;
+        const bool kept = (s_keep[i >> 5] >> (i & 31)) & 1u;
+        if (a.nucleus) return kept ? p / resum : 0.0;
+        return (kept ? p : 0.0) / resum;
     };
 
     // the draw and the inverse CDF in index order (:231-240): each thread a
@@ -322,8 +333,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
 
 int launch_sample(hipStream_t s, const float* logits, int rows, int n, float temperature, int top_k, float top_p,
                   const double* u, unsigned long long seed, const int* step, int* out, double* probs,
-                  unsigned long long* key, int* err) {
-    SampleArgs a{logits, n, temperature, top_k, top_p, u, seed, step, out, probs, key, err};
+                  unsigned long long* key, int* err, bool nucleus) {
+    SampleArgs a{logits, n, temperature, top_k, top_p, u, seed, step, out, probs, key, err, nucleus ? 1 : 0};
     hipLaunchKernelGGL(k_sample, dim3(rows), dim3(kSampleThreads), 0, s, a);
     count(CNT_ARGMAX);
     return check_launch("sample");
@@ -362,5 +373,13 @@ extern "C" int gorch_hip_sample(void* stream, const float* logits, int rows, int
     GH_REQUIRE(logits && u && out, "gorch_hip_sample: null logits, draws or output");
     GH_TRY(sample_check(rows, n, temperature, top_k, top_p));
     return launch_sample(stream_of(stream), logits, rows, n, temperature, top_k, top_p, u, 0ull, nullptr, out, probs,
-                         nullptr, nullptr);
+                         nullptr, nullptr, false);
+}
+
+extern "C" int gorch_hip_sample_nucleus(void* stream, const float* logits, int rows, int n, float temperature,
+                                        int top_k, float top_p, const double* u, int* out, double* probs) {
+    GH_REQUIRE(logits && u && out, "gorch_hip_sample_nucleus: null logits, draws or output");
+    GH_TRY(sample_check(rows, n, temperature, top_k, top_p));
+    return launch_sample(stream_of(stream), logits, rows, n, temperature, top_k, top_p, u, 0ull, nullptr, out, probs,
+                         nullptr, nullptr, true);
 }

@@ -52,6 +52,9 @@ SIGNATURES = {
     "gorch_hip_qwen_destroy": (None, [C.c_void_p]),
     "gorch_hip_qwen_generate": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int,
                                           C.c_void_p, C.POINTER(C.c_int), C.c_void_p, C.c_void_p, C.c_int]),
+    "gorch_hip_qwen_generate_sampled": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                                  C.c_int, C.c_float, C.c_int, C.c_float, C.c_uint64, C.c_void_p,
+                                                  C.POINTER(C.c_int), C.c_void_p, C.c_void_p, C.c_int]),
     "gorch_hip_set_deterministic": (C.c_int, [C.c_int]),
     "gorch_hip_deterministic_enabled": (C.c_int, []),
     "gorch_hip_buf_new": (vp, [C.c_size_t, i32]),
@@ -89,6 +92,7 @@ SIGNATURES = {
     "gorch_hip_softmax_rows": (i32, [vp, vp, i32, i32]),
     "gorch_hip_argmax": (i32, [vp, vp, i32, i32, vp]),
     "gorch_hip_sample": (i32, [vp, vp, i32, i32, C.c_float, i32, C.c_float, vp, vp, vp]),
+    "gorch_hip_sample_nucleus": (i32, [vp, vp, i32, i32, C.c_float, i32, C.c_float, vp, vp, vp]),
     "gorch_hip_rope_tables": (i32, [vp, i32, i32, f32, vp, vp]),
     "gorch_hip_rope_apply": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, i32, i32, f32]),
     "gorch_hip_gqa_attention_cached": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32]),
@@ -347,6 +351,14 @@ def sample(logits, temperature, top_k, top_p, u, out, probs=None) -> None:
     rows, n = logits.shape
     _ok(lib().gorch_hip_sample(_stream(), _p(logits), rows, n, float(temperature), int(top_k), float(top_p), _p(u),
                                _p(out), _p(probs)))
+
+
+def sample_nucleus(logits, temperature, top_k, top_p, u, out, probs=None) -> None:
+    """sampleLogits (model/qwen/generate.go:94-181) per row: the arguments of
+    sample(), top-p as the Qwen loop's nucleus cut."""
+    rows, n = logits.shape
+    _ok(lib().gorch_hip_sample_nucleus(_stream(), _p(logits), rows, n, float(temperature), int(top_k), float(top_p),
+                                       _p(u), _p(out), _p(probs)))
 
 
 def linear_bf16(x, W, bias, y, residual=None, epilogue=EPI_NONE, act_bf16=False) -> None:

@@ -111,11 +111,14 @@ class Qwen:
                                            layer["wdown"], cfg.inter, cfg.eps)
             self.layers.append(layer)
 
-    def generate(self, prompt, max_new: int, stop_tokens=None, want_logits=False, use_graph=True):
-        """Generate with a greedy config (model/qwen/generate.go:35-66) on the
-        device: prefill, then one token per step with the argmax fused into
-        the tied head, each step replayed from a HIP graph that reads the
-        position on the device. stop_tokens (default cfg.eos_tokens, the
+    def generate(self, prompt, max_new: int, stop_tokens=None, want_logits=False, use_graph=True,
+                 temperature=0.0, top_k=0, top_p=0.0, seed=0):
+        """Generate (model/qwen/generate.go:35-66) on the device: prefill,
+        then one token per step, each step replayed from a HIP graph that
+        reads the position on the device. temperature 0 (the Greedy config):
+        the argmax fused into the tied head; temperature > 0: sampleLogits
+        (:94-181) on the device with top_k / top_p, new token i drawn from
+        Philox(seed, i, 0). stop_tokens (default cfg.eos_tokens, the
         reference's Greedy list) end generation and are not kept. Returns
         (ids: prompt + new tokens, step logits [n_new, vocab] or None,
         timing dict)."""
@@ -136,10 +139,11 @@ class Qwen:
         n = C.c_int(0)
         logits = np.zeros((max(max_new, 1), cfg.vocab), np.float32) if want_logits else None
         timing = (C.c_float * 4)()
-        hip._ok(hip.lib().gorch_hip_qwen_generate(hip._stream(), self._engine, prompt.ctypes.data, prompt.size,
-                                                  max_new, stops.ctypes.data if stops.size else None, stops.size,
-                                                  out.ctypes.data, C.byref(n), None if logits is None else
-                                                  logits.ctypes.data, timing, int(use_graph)))
+        hip._ok(hip.lib().gorch_hip_qwen_generate_sampled(
+            hip._stream(), self._engine, prompt.ctypes.data, prompt.size, max_new,
+            stops.ctypes.data if stops.size else None, stops.size, float(temperature), int(top_k), float(top_p),
+            int(seed), out.ctypes.data, C.byref(n), None if logits is None else logits.ctypes.data, timing,
+            int(use_graph)))
         ids = out[: n.value].copy()
         if logits is not None:
             logits = logits[: n.value - prompt.size]

@@ -265,6 +265,14 @@ int gorch_hip_argmax(void* stream, const float* logits, int rows, int n, int* ou
  * 1 <= top_k <= 4096 (those candidates are sorted on the device). */
 int gorch_hip_sample(void* stream, const float* logits, int rows, int n, float temperature, int top_k, float top_p,
                      const double* u, int* out, double* probs);
+/* sampleLogits (model/qwen/generate.go:94-181): gorch_hip_sample with the
+ * Qwen loop's nucleus top-p: with 0 < top_p < 1 the probabilities in
+ * descending order (equal ones by ascending index: the reference's
+ * sort.Slice leaves their order open), the shortest prefix whose running sum
+ * reaches top_p kept and divided by its sum, every other probability 0. Same
+ * arguments, draws, outputs and return codes as gorch_hip_sample. */
+int gorch_hip_sample_nucleus(void* stream, const float* logits, int rows, int n, float temperature, int top_k,
+                             float top_p, const double* u, int* out, double* probs);
 
 /* Rotary tables (NewRoPE, nn/rope.go:71-96): cos/sin [max_seq, head_dim/2]
  * device f32, invFreq = f32(base^(-2i/hd)), theta = f64(f32(pos)*invFreq). */
@@ -365,6 +373,21 @@ void gorch_hip_qwen_destroy(gorch_hip_qwen* m);
 int gorch_hip_qwen_generate(void* stream, gorch_hip_qwen* m, const int* prompt, int n_prompt, int max_new,
                             const int* stop_tokens, int n_stop, int* out_ids, int* out_len, float* step_logits,
                             float* timing_ms, int flags);
+/* Generate with a sampling config (GenerateConfig, model/qwen/generate.go:
+ * 12-20, 35-66): temperature 0 is gorch_hip_qwen_generate (top_k, top_p and
+ * seed ignored); temperature > 0 chooses each token with sampleLogits
+ * (:94-181; gorch_hip_sample_nucleus) over the step's logits on the device,
+ * the draw of new token i being the Philox4x32-10 uniform of counter (0, i)
+ * under key seed (the reference seeds math/rand; its stream is not
+ * reproduced, so runs agree with it given the same draws). Other arguments
+ * and outputs as gorch_hip_qwen_generate. EINVAL for a negative or
+ * non-finite temperature or top_k < 0; EUNSUPPORTED for top_p in (0, 1)
+ * without 1 <= top_k <= 4096, or when values tied at the top-k threshold
+ * put more than 4096 candidates in the top-p sort. Synchronous. */
+int gorch_hip_qwen_generate_sampled(void* stream, gorch_hip_qwen* m, const int* prompt, int n_prompt, int max_new,
+                                    const int* stop_tokens, int n_stop, float temperature, int top_k, float top_p,
+                                    unsigned long long seed, int* out_ids, int* out_len, float* step_logits,
+                                    float* timing_ms, int flags);
 
 /* ------------------------------------------------------------------------
  * MoE FFN layer (nn.MoE.Forward, nn/moe.go:130-182).

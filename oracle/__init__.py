@@ -62,6 +62,7 @@ def _load() -> C.CDLL:
         "orc_argmax": (C.c_int, [f32p, C.c_int]),
         "orc_kth_largest": (C.c_float, [f32p, C.c_int, C.c_int]),
         "orc_sample": (C.c_int, [f32p, C.c_int, C.c_float, C.c_int, C.c_float, C.c_double, vp]),
+        "orc_sample_nucleus": (C.c_int, [f32p, C.c_int, C.c_float, C.c_int, C.c_float, C.c_double, vp]),
         "orc_philox_uniform": (C.c_double, [C.c_uint64, C.c_uint32, C.c_uint32]),
         "orc_philox4x32_10": (None, [vp, vp, vp]),
         "orc_generate_sampled": (C.c_int, [vp, i32p, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, C.c_float,
@@ -293,6 +294,16 @@ def sample(logits, temperature, top_k, top_p, r):
     logits = np.ascontiguousarray(logits, np.float32)
     probs = np.empty(logits.size, np.float64)
     tok = lib.orc_sample(logits, logits.size, temperature, top_k, top_p, r, _ptr(probs))
+    return int(tok), probs
+
+
+def sample_nucleus(logits, temperature, top_k, top_p, r):
+    """model/qwen/generate.go:94-163 (sampleLogits) with the uniform draw r
+    given; equal probabilities in the nucleus sort by ascending index.
+    Returns (token, final distribution as float64)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    probs = np.empty(logits.size, np.float64)
+    tok = lib.orc_sample_nucleus(logits, logits.size, temperature, top_k, top_p, r, _ptr(probs))
     return int(tok), probs
 
 

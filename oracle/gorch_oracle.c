@@ -468,6 +468,87 @@ int orc_sample(const float* logits, int n, float temperature, int top_k, float t
     return tok;
 }
 
+/* model/qwen/generate.go:94-163 (sampleLogits) with the draw r given: the
+ * same scaling, top-k threshold (kthLargestF32 :165-181 is kthLargest's
+ * selection, ties counted) and f64 softmax as sample(), then a standard
+ * nucleus cut (:121-152): the probabilities in descending order, the shortest
+ * prefix whose running sum reaches f64(top_p) kept and divided by its sum,
+ * every other probability set to 0; the inverse CDF in index order (:154-162).
+ * sort.Slice (:126) is not a stable sort, so the reference leaves the order
+ * of equal probabilities open; this restatement orders them by ascending
+ * index (the device sampler's order). */
+typedef struct {
+    double p;
+    int i;
+} orc_pi;
+static int orc_pi_desc(const void* a, const void* b) {
+    const orc_pi* x = (const orc_pi*)a;
+    const orc_pi* y = (const orc_pi*)b;
+    if (x->p > y->p) return -1;
+    if (x->p < y->p) return 1;
+    return (x->i > y->i) - (x->i < y->i);
+}
+int orc_sample_nucleus(const float* logits, int n, float temperature, int top_k, float top_p, double r,
+                       double* probs_out) {
+    if (n <= 0) return -1;
+    float* scaled = (float*)malloc((size_t)n * sizeof(float));
+    double* probs = (double*)malloc((size_t)n * sizeof(double));
+    for (int i = 0; i < n; i++) scaled[i] = logits[i] / temperature;
+    if (top_k > 0 && top_k < n) {
+        float threshold = orc_kth_largest(scaled, n, top_k);
+        for (int i = 0; i < n; i++)
+            if (scaled[i] < threshold) scaled[i] = -INFINITY;
+    }
+    float maxVal = scaled[0];
+    for (int i = 1; i < n; i++)
+        if (scaled[i] > maxVal) maxVal = scaled[i];
+    double sum = 0.0;
+    for (int i = 0; i < n; i++) {
+        probs[i] = exp((double)(scaled[i] - maxVal));
+        sum += probs[i];
+    }
+    for (int i = 0; i < n; i++) probs[i] /= sum;
+    if (top_p > 0.0f && top_p < 1.0f) {
+        orc_pi* idx = (orc_pi*)malloc((size_t)n * sizeof(orc_pi));
+        for (int i = 0; i < n; i++) {
+            idx[i].p = probs[i];
+            idx[i].i = i;
+        }
+        qsort(idx, (size_t)n, sizeof(orc_pi), orc_pi_desc);
+        double cum = 0.0;
+        int cut = n;
+        for (int q = 0; q < n; q++) {
+            cum += idx[q].p;
+            if (cum >= (double)top_p) {
+                cut = q + 1;
+                break;
+            }
+        }
+        double resum = 0.0;
+        unsigned char* kept = (unsigned char*)calloc((size_t)n, 1);
+        for (int q = 0; q < cut; q++) {
+            kept[idx[q].i] = 1;
+            resum += idx[q].p;
+        }
+        for (int i = 0; i < n; i++) probs[i] = kept[i] ? probs[i] / resum : 0.0;
+        free(kept);
+        free(idx);
+    }
+    int tok = n - 1;
+    double cumulative = 0.0;
+    for (int i = 0; i < n; i++) {
+        cumulative += probs[i];
+        if (r < cumulative) {
+            tok = i;
+            break;
+        }
+    }
+    if (probs_out) memcpy(probs_out, probs, (size_t)n * sizeof(double));
+    free(scaled);
+    free(probs);
+    return tok;
+}
+
 /* The device sampler's uniform draws, restated for the tests (this build's
  * own definition; the reference uses math/rand): Philox4x32-10 (Salmon,
  * Moraes, Dror and Shaw, SC 2011) on counter (row, step, 0, 0) with key

@@ -79,6 +79,9 @@ int orc_argmax(const float* logits, int n);                          /* model/ge
 float orc_kth_largest(const float* data, int n, int k);             /* model/generate.go:247-262 */
 /* model/generate.go:147-243 with the uniform draw r given; probs may be NULL */
 int orc_sample(const float* logits, int n, float temperature, int top_k, float top_p, double r, double* probs);
+/* model/qwen/generate.go:94-163 (sampleLogits, nucleus top-p) with the draw r given */
+int orc_sample_nucleus(const float* logits, int n, float temperature, int top_k, float top_p, double r,
+                       double* probs);
 /* Philox4x32-10 uniform in [0, 1) for (seed, step, row): the device sampler's draw */
 double orc_philox_uniform(uint64_t seed, uint32_t step, uint32_t row);
 void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);

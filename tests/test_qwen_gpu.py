@@ -344,3 +344,92 @@ def test_qwen_generate_max_seq_and_errors(gpu):
     with pytest.raises(hip.HipError):
         m.generate(np.zeros(GEN.max_seq + 1, np.int32), 4)
     m.close()
+
+
+def oracle_generate_sampled(ref, prompt, max_new, stops, max_seq, T, K, P, seed):
+    """model/qwen/generate.go:35-66 with a sampling config over the oracle
+    composition: token i = sampleLogits (the oracle's restatement) of the
+    latest logits with the draw Philox(seed, i, 0), the device loop's draw."""
+    result = [int(t) for t in prompt]
+    logits = ref.forward_cached(np.asarray(prompt, np.int32), 0)
+    pos = len(prompt)
+    for i in range(max_new):
+        nxt, _ = orc.sample_nucleus(logits[0], T, K, P, orc.philox_uniform(seed, i, 0))
+        if nxt in stops:
+            break
+        result.append(nxt)
+        if pos >= max_seq:
+            break
+        logits = ref.forward_cached(np.array([nxt], np.int32), pos)
+        pos += 1
+    return result
+
+
+@pytest.mark.parametrize("T,K,P", [(1.0, 0, 0.0), (0.7, 20, 0.8), (1.5, 50, 0.95), (0.9, 5, 0.0)])
+def test_qwen_generate_sampled_matches_oracle(gpu, T, K, P):
+    """Sampled generation (gorch_hip_qwen_generate_sampled): every token the
+    oracle loop's, given the same Philox draws, with the steps launched
+    directly and replayed from the graph; a second seed gives another
+    sequence."""
+    w = syn.qwen_weights(GEN, seed=31)
+    m = Qwen(GEN, w)
+    ref = OracleQwen(GEN, w, m)
+    prompt = np.random.default_rng(32).integers(0, GEN.vocab, 10).astype(np.int32)
+    want = oracle_generate_sampled(ref, prompt, 24, (), GEN.max_seq, T, K, P, seed=77)
+    for use_graph in (False, True):
+        ids, _, t = m.generate(prompt, 24, stop_tokens=(), use_graph=use_graph, temperature=T, top_k=K, top_p=P,
+                               seed=77)
+        assert list(ids) == want
+        assert t["graph"] == use_graph
+    ids2, _, _ = m.generate(prompt, 24, stop_tokens=(), temperature=T, top_k=K, top_p=P, seed=78)
+    assert list(ids2) == oracle_generate_sampled(OracleQwen(GEN, w, m), prompt, 24, (), GEN.max_seq, T, K, P, 78)
+    assert list(ids2) != want
+    # greedy again on the same engine (the sampled graph is not reused)
+    ids_g, _, _ = m.generate(prompt, 24, stop_tokens=())
+    assert list(ids_g) == oracle_generate(OracleQwen(GEN, w, m), prompt, 24, (), GEN.max_seq)[0]
+    m.close()
+
+
+def test_qwen_generate_sampled_stop_and_errors(gpu):
+    """A sampled stop token ends generation and is not kept; a negative
+    temperature or top_k is EINVAL, top-p without 1 <= top_k <= 4096
+    EUNSUPPORTED."""
+    from gorch_amd import hip
+    w = syn.qwen_weights(GEN, seed=33)
+    m = Qwen(GEN, w)
+    ref = OracleQwen(GEN, w, m)
+    prompt = np.random.default_rng(34).integers(0, GEN.vocab, 12).astype(np.int32)
+    full = oracle_generate_sampled(ref, prompt, 30, (), GEN.max_seq, 1.2, 30, 0.9, 5)
+    stop = full[len(prompt) + 4]
+    want = oracle_generate_sampled(OracleQwen(GEN, w, m), prompt, 30, (stop,), GEN.max_seq, 1.2, 30, 0.9, 5)
+    assert len(want) <= len(prompt) + 4
+    ids, _, _ = m.generate(prompt, 30, stop_tokens=(stop,), temperature=1.2, top_k=30, top_p=0.9, seed=5)
+    assert list(ids) == want
+    with pytest.raises(hip.HipError) as e:
+        m.generate(prompt, 4, temperature=-1.0)
+    assert e.value.rc == 2
+    with pytest.raises(hip.HipError) as e:
+        m.generate(prompt, 4, temperature=1.0, top_k=-1)
+    assert e.value.rc == 2
+    with pytest.raises(hip.HipError) as e:
+        m.generate(prompt, 4, temperature=1.0, top_k=0, top_p=0.5)
+    assert e.value.rc == 1
+    m.close()
+
+
+def test_qwen_full_size_sampled(gpu):
+    """Sampled generation at the full Qwen3-0.6B shape (vocab 151,936):
+    tokens identical to the oracle loop for 8 new tokens with Qwen's
+    recommended sampling (temperature 0.7, top-k 20, top-p 0.8)."""
+    import dataclasses
+
+    from gorch_amd.qwen import QWEN3_0_6B
+    cfg = dataclasses.replace(QWEN3_0_6B, max_seq=96)
+    w = syn.qwen_weights(cfg, seed=41)
+    m = Qwen(cfg, w)
+    ref = OracleQwen(cfg, w, m)
+    prompt = np.random.default_rng(42).integers(0, cfg.vocab, 16).astype(np.int32)
+    want = oracle_generate_sampled(ref, prompt, 8, (), cfg.max_seq, 0.7, 20, 0.8, 11)
+    ids, _, _ = m.generate(prompt, 8, stop_tokens=(), temperature=0.7, top_k=20, top_p=0.8, seed=11)
+    assert list(ids) == want
+    m.close()

@@ -74,3 +74,46 @@ def test_sample_argument_errors(gpu):
     with pytest.raises(gpu.HipError) as e:
         gpu.sample(x, 1.0, 0, 0.5, u, out)  # top-p needs 1 <= top_k <= 4096
     assert e.value.rc == 1  # GORCH_HIP_EUNSUPPORTED
+
+
+# ------------------------------------------------------------ sampleLogits (Qwen)
+
+NUCLEUS = [(151936, 0.7, 20, 0.8), (151936, 0.9, 4096, 0.95), (151936, 1.0, 0, 0.0), (1000, 0.7, 100, 0.9),
+           (1000, 1.3, 50, 0.3), (4096, 4.0, 200, 0.4), (500, 0.5, 1, 0.5), (7, 1.0, 3, 0.99)]
+
+
+@pytest.mark.parametrize("n,T,K,P", NUCLEUS)
+def test_sample_nucleus_matches_oracle(gpu, n, T, K, P):
+    """gorch_hip_sample_nucleus against the oracle's sampleLogits
+    (model/qwen/generate.go:94-181) with the same draws: support exact,
+    probabilities within 1e-12, the same token."""
+    rng = np.random.default_rng(2 * n + K + int(P * 100))
+    rows = 3
+    logits = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+    u = rng.random(rows)
+    out = torch.empty(rows, dtype=torch.int32, device="cuda")
+    probs = torch.empty((rows, n), dtype=torch.float64, device="cuda")
+    gpu.sample_nucleus(dev(logits), T, K, P, dev(u), out, probs)
+    got_tok, got_p = host(out), host(probs)
+    for r in range(rows):
+        tok, want = orc.sample_nucleus(logits[r], T, K, P, float(u[r]))
+        assert np.array_equal(got_p[r] > 0, want > 0)
+        np.testing.assert_allclose(got_p[r], want, rtol=0, atol=1e-12)
+        assert got_tok[r] == tok
+
+
+def test_sample_nucleus_ties_by_index(gpu):
+    """Equal probabilities in the nucleus: the lower indices are kept first
+    (integer logits, many ties at the top-k threshold and in the cut)."""
+    rng = np.random.default_rng(5)
+    logits = rng.integers(0, 6, size=(4, 2000)).astype(np.float32)
+    u = rng.random(4)
+    out = torch.empty(4, dtype=torch.int32, device="cuda")
+    probs = torch.empty((4, 2000), dtype=torch.float64, device="cuda")
+    for K, P in ((10, 0.5), (700, 0.3), (700, 0.9)):
+        gpu.sample_nucleus(dev(logits), 1.0, K, P, dev(u), out, probs)
+        got_tok, got_p = host(out), host(probs)
+        for r in range(4):
+            tok, want = orc.sample_nucleus(logits[r], 1.0, K, P, float(u[r]))
+            np.testing.assert_allclose(got_p[r], want, rtol=0, atol=1e-12)
+            assert got_tok[r] == tok
