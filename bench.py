@@ -391,6 +391,12 @@ def qwen_leg(ctxs=(128, 512), steps=100, gen_tokens=65):
         m.generate(prompt, gen_tokens, stop_tokens=())
         _, _, t = m.generate(prompt, gen_tokens, stop_tokens=())
         gen_ms = t["decode_ms"] / max(t["decode_forwards"], 1)
+        # the same loop with Qwen's recommended sampling config (sampleLogits,
+        # :94-181, on the device after the tied head)
+        smp = dict(temperature=0.7, top_k=20, top_p=0.8, seed=1)
+        m.generate(prompt, gen_tokens, stop_tokens=(), **smp)
+        _, _, ts = m.generate(prompt, gen_tokens, stop_tokens=(), **smp)
+        smp_ms = ts["decode_ms"] / max(ts["decode_forwards"], 1)
         out.append({"model": "qwen3-0.6b-shaped", "batch": 1, "ctx": ctx, "tok_s": round(1e3 / ms, 1),
                     "ms_per_token": round(ms, 4), "weights": "bf16 N(0,0.02) random init on the device",
                     "roofline": roofline_block(qwen_step_bytes(cfg, ctx), ms / 1e3,
@@ -398,7 +404,9 @@ def qwen_leg(ctxs=(128, 512), steps=100, gen_tokens=65):
                                                "and written, logits; per token"),
                     "generate": {"new_tokens": gen_tokens, "decode_forwards": t["decode_forwards"],
                                  "graph": t["graph"], "tok_s": round(1e3 / gen_ms, 1),
-                                 "ms_per_token": round(gen_ms, 4), "prefill_ms": round(t["prefill_ms"], 3)}})
+                                 "ms_per_token": round(gen_ms, 4), "prefill_ms": round(t["prefill_ms"], 3)},
+                    "generate_sampled": {**smp, "decode_forwards": ts["decode_forwards"], "graph": ts["graph"],
+                                         "tok_s": round(1e3 / smp_ms, 1), "ms_per_token": round(smp_ms, 4)}})
     m.close()
     return out
 
@@ -493,6 +501,12 @@ def decode_leg(cfg_name, batch, n_prompt, max_new, reps=3, w=None):
     for _ in range(reps):
         _, _, t = g.generate_cached(prompts, max_new, use_graph=True)
         runs.append(t)
+    # the same steps with sampled choices (GenerateConfig Temperature 0.8,
+    # TopK 40, TopP 0.95: sample() on the device after the LM head)
+    smp = dict(temperature=0.8, top_k=40, top_p=0.95, seed=1)
+    g.generate(prompts, max_new, **smp)
+    sruns = sorted((g.generate(prompts, max_new, **smp)[2] for _ in range(reps)), key=lambda t: t["decode_ms"])
+    ts = sruns[len(sruns) // 2]
     g.close()
     runs.sort(key=lambda t: t["decode_ms"])
     t = runs[len(runs) // 2]
@@ -505,7 +519,10 @@ def decode_leg(cfg_name, batch, n_prompt, max_new, reps=3, w=None):
             "ms_per_step": round(t["decode_ms"] / fwd, 4), "prefill_ms": round(t["prefill_ms"], 3),
             "weights": "bf16 N(0,0.02) random init, synthetic prompts",
             "roofline": roofline_block(nbytes, step_s, "bf16 weights + f32 params once, K/V rows read at the "
-                                                        "mean context and written, embeddings, logits; per step")}
+                                                        "mean context and written, embeddings, logits; per step"),
+            "sampled": {**smp, "decode_forwards": ts["decode_forwards"],
+                        "tok_s": round(batch * ts["decode_forwards"] / (ts["decode_ms"] / 1e3), 1),
+                        "ms_per_step": round(ts["decode_ms"] / max(ts["decode_forwards"], 1), 4)}}
 
 
 def host_info():

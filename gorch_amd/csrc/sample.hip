@@ -23,7 +23,8 @@
 //     to 0 (sort.Slice leaves the order of equal probabilities open; this
 //     one takes the lower index first). Same candidate limits and sort.
 //   token = the first index whose running sum of the final probabilities
-//     exceeds the uniform draw r (n - 1 if none).
+//     exceeds the uniform draw r (n - 1 if none), found over 16 contiguous
+//     wave ranges read 64 entries at a time.
 //
 // The draw r is u[row] when u is given, else Philox4x32-10 (Salmon, Moraes,
 // Dror and Shaw, SC 2011) of counter (row, step, 0, 0) under key (seed low,
@@ -306,21 +307,43 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
         return (kept ? p : 0.0) / resum;
     };
 
-    // the draw and the inverse CDF in index order (:231-240): each thread a
-    // contiguous segment, segment sums scanned across the block
+    // the draw and the inverse CDF in index order (:231-240): wave w owns
+    // the contiguous range [w * seg, (w + 1) * seg) of the row (seg a
+    // multiple of 64) and reads it 64 consecutive entries at a time; the
+    // range sums are added in wave order, and only the wave whose range
+    // holds the crossing (or every wave, when the distribution is written
+    // out) scans its range again, 64 entries per step
     const double r = a.u ? a.u[row] : philox_uniform(a.seed, (uint32_t)*a.step, (uint32_t)row);
-    const int seg = (n + kSampleThreads - 1) / kSampleThreads;
-    const int i0 = min(n, tid * seg), i1 = min(n, i0 + seg);
-    double segsum = 0.0;
-    for (int i = i0; i < i1; i++) segsum += final_p(i);
-    double total;
-    double cum = block_exclusive_scan_f64(segsum, s_scan, &total);
+    const int lane = tid & 63, wave = tid >> 6;
+    const int seg = ((n + kSampleThreads / 64 - 1) / (kSampleThreads / 64) + 63) & ~63;
+    const int w0 = min(n, wave * seg), w1 = min(n, w0 + seg);
+    double rsum = 0.0;
+    for (int i = w0 + lane; i < w1; i += 64) rsum += final_p(i);
+    rsum = wave_sum_d(rsum);
+    if (lane == 0) s_scan[wave] = rsum;
+    __syncthreads();
+    double cum = 0.0;
+    for (int w = 0; w < wave; w++) cum += s_scan[w];
     int cand = INT_MAX;
-    for (int i = i0; i < i1; i++) {
-        const double p = final_p(i);
-        cum += p;
-        if (a.probs) a.probs[(size_t)row * n + i] = p;
-        if (cand == INT_MAX && r < cum) cand = i;
+    if (a.probs || (r >= cum && r < cum + rsum)) {
+        for (int base = w0; base < w1; base += 64) {
+            const int i = base + lane;
+            const double p = i < w1 ? final_p(i) : 0.0;
+            if (a.probs && i < w1) a.probs[(size_t)row * n + i] = p;
+            double inc = p;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const double t = __shfl_up(inc, o);
+                if (lane >= o) inc += t;
+            }
+            const unsigned long long hit = __ballot(i < w1 && r < cum + inc);
+            if (hit && cand == INT_MAX) cand = base + (int)__builtin_ctzll(hit);
+            cum += readlane_d(inc, 63);
+            if (cand != INT_MAX && !a.probs) break;
+        }
+        // within rounding of the range's end the rescan may not cross where
+        // the range sums did: the range's last entry then
+        if (cand == INT_MAX && w1 > w0 && r < cum) cand = w1 - 1;
     }
     int tok = block_min_i32(cand, red_i);
     if (tok == INT_MAX) tok = n - 1;
