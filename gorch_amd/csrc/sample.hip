@@ -43,6 +43,7 @@ namespace gh {
 constexpr int kSampleThreads = 1024;
 constexpr int kSampleCap = 4096;
 constexpr int kSampleMaxN = 1 << 18;  // columns (the top-p bitmap's size)
+constexpr int kRowUnroll = 8;         // row entries per thread in flight in a pass
 
 __device__ __forceinline__ uint32_t f32_order_key(float f) {
     const uint32_t b = __float_as_uint(f);
@@ -111,22 +112,47 @@ __device__ int block_min_i32(int v, int* sh) {
     __syncthreads();
     return t;
 }
-// Exclusive prefix of one f64 per thread in thread order (Hillis-Steele in
-// LDS); returns this thread's exclusive prefix, *total the block's sum.
+// Exclusive prefix of one f64 per thread in thread order: an inclusive
+// scan within each wave (lane shifts), then the waves' totals added in wave
+// order; returns this thread's exclusive prefix, *total the block's sum.
 __device__ double block_exclusive_scan_f64(double v, double* sc, double* total) {
-    const int t = threadIdx.x;
-    sc[t] = v;
-    __syncthreads();
-    for (int o = 1; o < kSampleThreads; o <<= 1) {
-        const double add = t >= o ? sc[t - o] : 0.0;
-        __syncthreads();
-        sc[t] += add;
-        __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    double inc = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double t = __shfl_up(inc, o);
+        if (lane >= o) inc += t;
     }
-    const double incl = sc[t];
-    *total = sc[kSampleThreads - 1];
+    if (lane == 63) sc[wave] = inc;
     __syncthreads();
-    return incl - v;
+    double before = 0.0, tot = 0.0;
+    for (int w = 0; w < kSampleThreads / 64; w++) {
+        const double x = sc[w];
+        if (w < wave) before += x;
+        tot += x;
+    }
+    *total = tot;
+    __syncthreads();
+    return before + (inc - v);
+}
+
+// Bitonic sort of one element per lane across the 64 lanes of a wave
+// (before(a, b): a sorts first; elements must be distinct under it).
+template <typename E, typename Before>
+__device__ __forceinline__ E wave_bitonic_sort(E mine, Before before) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            E other;
+            other.a = __shfl_xor(mine.a, stride);
+            other.b = __shfl_xor(mine.b, stride);
+            const bool lower = (lane & stride) == 0, asc = (lane & size) == 0;
+            if (lower == asc ? before(other, mine) : before(mine, other)) mine = other;
+        }
+    }
+    return mine;
 }
 
 struct SampleArgs {
@@ -150,98 +176,110 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     __shared__ double red_d[kSampleThreads / 64];
     __shared__ float red_f[kSampleThreads / 64];
     __shared__ int red_i[kSampleThreads / 64];
+    __shared__ uint32_t red_u[kSampleThreads / 64];
     __shared__ uint32_t s_prefix;
-    __shared__ int s_k, s_cnt;
+    __shared__ int s_k, s_cnt, s_bin, s_above;
     __shared__ double s_p[kSampleCap];
     __shared__ int s_idx[kSampleCap];
     __shared__ double s_scan[kSampleThreads];
-    __shared__ uint32_t s_keep[kSampleMaxN / 32];  // kept indices (top-p)
+    // kept indices (top-p) as a bitmap over n; the top-k candidate pass's
+    // 4096-bin key histogram before that
+    __shared__ uint32_t s_keep[kSampleMaxN / 32];
+    __shared__ uint32_t c_key[kSampleCap];  // top-k candidates: order keys
+    __shared__ int c_idx[kSampleCap];       // and indices
     const int row = blockIdx.x, tid = threadIdx.x, n = a.n;
     const float* lg = a.logits + (size_t)row * n;
     const float T = a.temperature;
-
-    // top-k threshold (model/generate.go:155-163): the top_k-th largest
-    // scaled value, counting equal values
     const bool use_k = a.top_k > 0 && a.top_k < n;
-    float thr = -INFINITY;
-    if (use_k) {
+    const bool use_p = a.top_p > 0.f && a.top_p < 1.f;
+    const double r = a.u ? a.u[row] : philox_uniform(a.seed, (uint32_t)*a.step, (uint32_t)row);
+    // the row's entries base + u * kSampleThreads + tid (u < kRowUnroll), all
+    // loads in flight together; past n they read 0
+    const __amdgpu_buffer_rsrc_t rrow = make_rsrc(lg, (long long)n * 4);
+    auto load_row = [&](int base, float (&v)[kRowUnroll]) {
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; u++)
+            v[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rrow, (base + u * kSampleThreads + tid) * 4, 0, 0));
+    };
+
+    // The k-th largest of `count` order keys key_at(j), counting equal keys:
+    // a 4-pass radix select, 256-bin LDS histograms.
+    auto radix_kth = [&](auto key_at, int count, int k) -> uint32_t {
         uint32_t prefix = 0u, mask = 0u;
-        int k = a.top_k;
         for (int shift = 24; shift >= 0; shift -= 8) {
             for (int b = tid; b < 256; b += kSampleThreads) hist[b] = 0;
             __syncthreads();
-            for (int i = tid; i < n; i += kSampleThreads) {
-                const uint32_t key = f32_order_key(lg[i] / T);
+            for (int j = tid; j < count; j += kSampleThreads) {
+                const uint32_t key = key_at(j);
                 if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
             }
             __syncthreads();
-            if (tid == 0) {
-                int cum = 0, d = 255;
-                for (; d > 0; d--) {
-                    if (cum + hist[d] >= k) break;
-                    cum += hist[d];
+            // the bin holding the k-th largest, from the top: wave 0, lane l
+            // owning bins 255 - 4l - q (q < 4), an inclusive scan of the
+            // lanes' sums
+            if (tid < 64) {
+                int gs = 0;
+#pragma unroll
+                for (int q = 0; q < 4; q++) gs += hist[255 - 4 * tid - q];
+                int inc = gs;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int t = __shfl_up(inc, o);
+                    if (tid >= o) inc += t;
                 }
-                s_prefix = prefix | ((uint32_t)d << shift);
-                s_k = k - cum;
+                const int above = inc - gs;
+                if (above < k && inc >= k) {
+                    int cum = above, d = 255 - 4 * tid;
+#pragma unroll
+                    for (int q = 0; q < 3; q++) {
+                        if (cum + hist[d] >= k) break;
+                        cum += hist[d];
+                        d--;
+                    }
+                    s_prefix = prefix | ((uint32_t)d << shift);
+                    s_k = k - cum;
+                }
             }
             __syncthreads();
             prefix = s_prefix;
             k = s_k;
             mask |= 255u << shift;
         }
-        thr = f32_from_order_key(prefix);
-    }
-    auto value = [&](int i) {
-        const float v = lg[i] / T;
-        return (use_k && v < thr) ? -INFINITY : v;
+        return prefix;
     };
 
-    // softmax in f64 of the f32 differences to the maximum (:165-180)
-    float mx = -INFINITY;
-    for (int i = tid; i < n; i += kSampleThreads) mx = fmaxf(mx, value(i));
-    mx = block_max_f32(mx, red_f);
-    // (exp of -inf is 0: entries below the top-k threshold skip the f64 exp)
-    auto expo = [&](int i) {
-        const float v = value(i);
-        return v == -INFINITY ? 0.0 : exp((double)(v - mx));
-    };
-    double part = 0.0;
-    for (int i = tid; i < n; i += kSampleThreads) part += expo(i);
-    const double sum = block_sum_f64(part, red_d);
-
-    // top-p (:182-229)
-    const bool use_p = a.top_p > 0.f && a.top_p < 1.f;
-    double resum = 1.0;
-    if (use_p) {
-        if (tid == 0) s_cnt = 0;
-        __syncthreads();
-        for (int i = tid; i < n; i += kSampleThreads) {
-            const double p = expo(i) / sum;
-            if (p > 0.0) {
-                const int slot = atomicAdd(&s_cnt, 1);
-                if (slot < kSampleCap) {
-                    s_p[slot] = p;
-                    s_idx[slot] = i;
-                }
-            }
-        }
-        __syncthreads();
-        const int cnt = s_cnt;
-        if (cnt > kSampleCap) {
-            if (tid == 0) {
-                if (a.err) atomicOr(a.err, 1);
-                if (a.out) a.out[row] = -1;
-            }
-            return;
-        }
+    // Top-p over the probabilities in s_p / s_idx[0, cnt) (cnt <= kSampleCap;
+    // entries of probability 0 change nothing): sorted in LDS, the kept
+    // prefix marked in the s_keep bitmap; returns the kept sum. sample()
+    // keeps the longest prefix, in order of (p descending, index
+    // descending), whose sum is at most 1.5 * top_p; the nucleus keeps, in
+    // order of (p descending, index ascending), every entry whose preceding
+    // sum is still below top_p.
+    auto top_p_keep = [&](int cnt) -> double {
         int P = 1;
         while (P < cnt) P <<= 1;
+        if (P <= 64) {
+            // one wave sorts up to 64
+            struct PI {
+                double a;  // p
+                int b;     // index
+            };
+            if (tid < 64) {
+                PI e = tid < cnt ? PI{s_p[tid], s_idx[tid]} : PI{-1.0, -1};
+                const bool nuc = a.nucleus != 0;
+                e = wave_bitonic_sort(e, [nuc](const PI& x, const PI& y) {
+                    return x.a > y.a || (x.a == y.a && (nuc ? x.b < y.b : x.b > y.b));
+                });
+                s_p[tid] = e.a;
+                s_idx[tid] = e.b;
+            }
+            P = 1;  // (the block sort below then does nothing)
+        }
         for (int i = cnt + tid; i < P; i += kSampleThreads) {
             s_p[i] = -1.0;
             s_idx[i] = -1;
         }
         __syncthreads();
-        // bitonic sort into (p descending, index descending)
         for (int size = 2; size <= P; size <<= 1) {
             for (int stride = size >> 1; stride > 0; stride >>= 1) {
                 for (int t = tid; t < P / 2; t += kSampleThreads) {
@@ -260,9 +298,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
                 __syncthreads();
             }
         }
-        // kept: the longest sorted prefix whose sum is at most the limit
-        // (the prefix sums increase with its length); nucleus: every entry
-        // whose preceding sum is still below top_p
+        // (the prefix sums increase with the prefix's length)
         constexpr int PER = kSampleCap / kSampleThreads;
         const double limit = a.nucleus ? (double)a.top_p : (double)a.top_p * 1.5;
         double loc = 0.0;
@@ -288,24 +324,311 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
             }
         }
         const int L = block_sum_i32(keep, red_i);
-        resum = block_sum_f64(kept_sum, red_d);
-        // kept indices as a bitmap over n
+        const double rs = block_sum_f64(kept_sum, red_d);
         const int words = (n + 31) / 32;
         for (int w = tid; w < words; w += kSampleThreads) s_keep[w] = 0u;
         __syncthreads();
         for (int j = tid; j < L; j += kSampleThreads) atomicOr(&s_keep[s_idx[j] >> 5], 1u << (s_idx[j] & 31));
         __syncthreads();
-    }
+        return rs;
+    };
+    auto is_kept = [&](int i) { return ((s_keep[i >> 5] >> (i & 31)) & 1u) != 0u; };
     // (with top-p every value is divided by the kept sum, as the reference
     // does: 0/0 = NaN everywhere when nothing was kept, and the draw then
     // falls through to n - 1)
-    auto final_p = [&](int i) {
-        const double p = expo(i) / sum;
+    auto finish = [&](double p, bool kept, double resum) -> double {
         if (!use_p) return p;
-        const bool kept = (s_keep[i >> 5] >> (i & 31)) & 1u;
         if (a.nucleus) return kept ? p / resum : 0.0;
         return (kept ? p : 0.0) / resum;
     };
+    auto emit = [&](int tok) {
+        if (tid == 0) {
+            if (a.out) a.out[row] = tok;
+            // a key the fused-argmax consumers decode to tok (slot 0 of row)
+            if (a.key) a.key[row] = (1ull << 32) | (unsigned long long)(0xffffffffu - (uint32_t)tok);
+        }
+    };
+
+    // top-k on candidates. Division by T > 0 is monotone, so the scaled
+    // values' top_k-th largest is the raw logits' top_k-th largest divided by
+    // T: one pass builds a 4096-bin histogram of the raw logits' order keys
+    // (zeros taken as +0, which compares equal), which locates the bin of the
+    // top_k-th largest; a second pass collects every key at or above that
+    // bin. When they fit kSampleCap and no logit is NaN, the threshold,
+    // softmax, top-p and the inverse CDF run on them alone (scaled, in index
+    // order); the rest of the row has probability 0. A logit below the bin
+    // whose scaled value still equals the threshold (rounding) sends the
+    // row to the full path.
+    if (use_k && a.top_k <= kSampleCap) {
+        int* hist12 = reinterpret_cast<int*>(s_keep);
+        for (int b = tid; b < 4096; b += kSampleThreads) hist12[b] = 0;
+        __syncthreads();
+        uint32_t kmax = 0u;
+        int nan = 0;
+        for (int base = 0; base < n; base += kRowUnroll * kSampleThreads) {
+            float v[kRowUnroll];
+            load_row(base, v);
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; u++) {
+                if (base + u * kSampleThreads + tid < n) {
+                    const uint32_t key = f32_order_key(v[u] == 0.f ? 0.f : v[u]);
+                    kmax = max(kmax, key);
+                    nan |= v[u] != v[u];
+                    atomicAdd(&hist12[key >> 20], 1);
+                }
+            }
+        }
+        for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+        if ((tid & 63) == 0) red_u[tid >> 6] = kmax;
+        // (its barriers also publish red_u and the histogram)
+        const bool any_nan = block_sum_i32(nan, red_i) > 0;
+        for (int w = 0; w < kSampleThreads / 64; w++) kmax = max(kmax, red_u[w]);
+        // thread t sums bins 4095 - 4t - q (q < 4): the scan of those sums in
+        // thread order is the count above each group of bins
+        int gs = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) gs += hist12[4095 - 4 * tid - q];
+        double tot;
+        const int above_g = (int)block_exclusive_scan_f64((double)gs, s_scan, &tot);
+        if (above_g < a.top_k && above_g + gs >= a.top_k) {
+            int cum = above_g;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int b = 4095 - 4 * tid - q;
+                if (cum + hist12[b] >= a.top_k) {
+                    s_bin = b;
+                    s_above = cum;
+                    break;
+                }
+                cum += hist12[b];
+            }
+        }
+        __syncthreads();
+        const int dbin = s_bin;
+        const int C = s_above + hist12[dbin];
+        __syncthreads();
+        if (C <= kSampleCap && !any_nan) {
+            if (tid == 0) s_cnt = 0;
+            __syncthreads();
+            for (int base = 0; base < n; base += kRowUnroll * kSampleThreads) {
+                float v[kRowUnroll];
+                load_row(base, v);
+#pragma unroll
+                for (int u = 0; u < kRowUnroll; u++) {
+                    const int i = base + u * kSampleThreads + tid;
+                    const uint32_t key = f32_order_key(v[u] == 0.f ? 0.f : v[u]);
+                    if (i < n && (int)(key >> 20) >= dbin) {
+                        const int slot = atomicAdd(&s_cnt, 1);
+                        c_key[slot] = key;
+                        c_idx[slot] = i;
+                    }
+                }
+            }
+            __syncthreads();
+            // the top_k-th largest key (every key above dbin's floor is a
+            // candidate, so it is the row's): with few candidates the largest
+            // key that at least top_k keys reach, each thread counting for
+            // its own candidates; else the radix select
+            uint32_t tkey;
+            if (C <= 512) {
+                uint32_t best = 0u;
+                for (int j = tid; j < C; j += kSampleThreads) {
+                    const uint32_t kj = c_key[j];
+                    int ge = 0;
+                    for (int i = 0; i < C; i++) ge += c_key[i] >= kj;
+                    if (ge >= a.top_k) best = max(best, kj);
+                }
+                for (int o = 32; o > 0; o >>= 1) best = max(best, (uint32_t)__shfl_xor((int)best, o));
+                if ((tid & 63) == 0) red_u[tid >> 6] = best;
+                __syncthreads();
+                tkey = 0u;
+                for (int w = 0; w < kSampleThreads / 64; w++) tkey = max(tkey, red_u[w]);
+            } else {
+                tkey = radix_kth([&](int j) { return c_key[j]; }, C, a.top_k);
+            }
+            const float thr = f32_from_order_key(tkey) / T;
+            const float mx = f32_from_order_key(kmax) / T;
+            const bool below = dbin > 0 && f32_from_order_key((uint32_t)dbin << 20) / T >= thr;
+            if (!below) {
+                // candidates into index order (bitonic; padding sorts last):
+                // up to 64 in one wave, else across the block
+                int P = 1;
+                while (P < C) P <<= 1;
+                if (P <= 64) {
+                    struct KI {
+                        int a;       // index
+                        uint32_t b;  // key
+                    };
+                    if (tid < 64) {
+                        KI e = tid < C ? KI{c_idx[tid], c_key[tid]} : KI{INT_MAX, 0u};
+                        e = wave_bitonic_sort(e, [](const KI& x, const KI& y) { return x.a < y.a; });
+                        c_idx[tid] = e.a;
+                        c_key[tid] = e.b;
+                    }
+                    P = 1;  // (the block sort below then does nothing)
+                }
+                for (int j = C + tid; j < P; j += kSampleThreads) {
+                    c_idx[j] = INT_MAX;
+                    c_key[j] = 0u;
+                }
+                __syncthreads();
+                for (int size = 2; size <= P; size <<= 1) {
+                    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                        for (int t = tid; t < P / 2; t += kSampleThreads) {
+                            const int i = 2 * stride * (t / stride) + (t % stride), j = i + stride;
+                            const bool up = (i & size) == 0;
+                            const int ii = c_idx[i], ij = c_idx[j];
+                            if ((ij < ii) == up) {
+                                const uint32_t ki = c_key[i];
+                                c_idx[i] = ij;
+                                c_idx[j] = ii;
+                                c_key[i] = c_key[j];
+                                c_key[j] = ki;
+                            }
+                        }
+                        __syncthreads();
+                    }
+                }
+                // softmax over the kept (key >= tkey): the f64 exp of the f32
+                // difference to the maximum, the sum in index order
+                constexpr int PER = kSampleCap / kSampleThreads;
+                double e[PER];
+                double loc = 0.0;
+#pragma unroll
+                for (int q = 0; q < PER; q++) {
+                    const int j = tid * PER + q;
+                    e[q] = 0.0;
+                    if (j < C) {
+                        const float v = f32_from_order_key(c_key[j]) / T;
+                        if (v >= thr) e[q] = exp((double)(v - mx));
+                    }
+                    loc += e[q];
+                }
+                const double sum = block_sum_f64(loc, red_d);
+                double resum = 1.0;
+                if (use_p) {
+#pragma unroll
+                    for (int q = 0; q < PER; q++) {
+                        const int j = tid * PER + q;
+                        if (j < C) {
+                            s_p[j] = e[q] / sum;
+                            s_idx[j] = c_idx[j];
+                        }
+                    }
+                    __syncthreads();
+                    resum = top_p_keep(C);
+                }
+                // the inverse CDF in index order over the candidates
+                double f[PER];
+                double seg = 0.0;
+#pragma unroll
+                for (int q = 0; q < PER; q++) {
+                    const int j = tid * PER + q;
+                    f[q] = j < C ? finish(e[q] / sum, use_p && is_kept(c_idx[j]), resum) : 0.0;
+                    seg += f[q];
+                }
+                double total;
+                double run = block_exclusive_scan_f64(seg, s_scan, &total);
+                int cand = INT_MAX;
+#pragma unroll
+                for (int q = 0; q < PER; q++) {
+                    const int j = tid * PER + q;
+                    if (j < C) {
+                        run += f[q];
+                        if (cand == INT_MAX && r < run) cand = c_idx[j];
+                    }
+                }
+                int tok = block_min_i32(cand, red_i);
+                if (tok == INT_MAX) tok = n - 1;
+                if (a.probs) {
+                    // every other entry: 0, or 0 / resum as the reference divides
+                    const double rest = finish(0.0, false, resum);
+                    for (int i = tid; i < n; i += kSampleThreads) a.probs[(size_t)row * n + i] = rest;
+                    __threadfence_block();
+                    __syncthreads();
+#pragma unroll
+                    for (int q = 0; q < PER; q++) {
+                        const int j = tid * PER + q;
+                        if (j < C) a.probs[(size_t)row * n + c_idx[j]] = f[q];
+                    }
+                }
+                emit(tok);
+                return;
+            }
+        }
+    }
+
+    // top-k threshold (model/generate.go:155-163): the top_k-th largest
+    // scaled value, counting equal values
+    float thr = -INFINITY;
+    if (use_k)
+        thr = f32_from_order_key(radix_kth([&](int i) { return f32_order_key(lg[i] / T); }, n, a.top_k));
+    // (top-k rows reach here with more than kSampleCap candidates, a NaN,
+    // or a scaled tie below the candidates' bin)
+    // the scaled value of a logit x, -inf below the top-k threshold
+    auto value = [&](float x) {
+        const float v = x / T;
+        return (use_k && v < thr) ? -INFINITY : v;
+    };
+
+    // softmax in f64 of the f32 differences to the maximum (:165-180)
+    float mx = -INFINITY;
+    for (int base = 0; base < n; base += kRowUnroll * kSampleThreads) {
+        float v[kRowUnroll];
+        load_row(base, v);
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; u++)
+            if (base + u * kSampleThreads + tid < n) mx = fmaxf(mx, value(v[u]));
+    }
+    mx = block_max_f32(mx, red_f);
+    // (exp of -inf is 0: entries below the top-k threshold skip the f64 exp)
+    auto expo = [&](float x) {
+        const float v = value(x);
+        return v == -INFINITY ? 0.0 : exp((double)(v - mx));
+    };
+    double part = 0.0;
+    for (int base = 0; base < n; base += kRowUnroll * kSampleThreads) {
+        float v[kRowUnroll];
+        load_row(base, v);
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; u++)
+            if (base + u * kSampleThreads + tid < n) part += expo(v[u]);
+    }
+    const double sum = block_sum_f64(part, red_d);
+
+    // top-p (:182-229) over the positive probabilities
+    double resum = 1.0;
+    if (use_p) {
+        if (tid == 0) s_cnt = 0;
+        __syncthreads();
+        for (int base = 0; base < n; base += kRowUnroll * kSampleThreads) {
+            float v[kRowUnroll];
+            load_row(base, v);
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; u++) {
+                const int i = base + u * kSampleThreads + tid;
+                const double p = i < n ? expo(v[u]) / sum : 0.0;
+                if (p > 0.0) {
+                    const int slot = atomicAdd(&s_cnt, 1);
+                    if (slot < kSampleCap) {
+                        s_p[slot] = p;
+                        s_idx[slot] = i;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        const int cnt = s_cnt;
+        if (cnt > kSampleCap) {
+            if (tid == 0) {
+                if (a.err) atomicOr(a.err, 1);
+                if (a.out) a.out[row] = -1;
+            }
+            return;
+        }
+        resum = top_p_keep(cnt);
+    }
+    auto final_p = [&](int i, float x) { return finish(expo(x) / sum, use_p && is_kept(i), resum); };
 
     // the draw and the inverse CDF in index order (:231-240): wave w owns
     // the contiguous range [w * seg, (w + 1) * seg) of the row (seg a
@@ -313,12 +636,25 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     // range sums are added in wave order, and only the wave whose range
     // holds the crossing (or every wave, when the distribution is written
     // out) scans its range again, 64 entries per step
-    const double r = a.u ? a.u[row] : philox_uniform(a.seed, (uint32_t)*a.step, (uint32_t)row);
     const int lane = tid & 63, wave = tid >> 6;
     const int seg = ((n + kSampleThreads / 64 - 1) / (kSampleThreads / 64) + 63) & ~63;
     const int w0 = min(n, wave * seg), w1 = min(n, w0 + seg);
+    // entries base + lane + 64 u (u < kRowUnroll), all loads in flight
+    auto load_range = [&](int base, float (&v)[kRowUnroll]) {
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; u++)
+            v[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rrow, (base + lane + 64 * u) * 4, 0, 0));
+    };
     double rsum = 0.0;
-    for (int i = w0 + lane; i < w1; i += 64) rsum += final_p(i);
+    for (int base = w0; base < w1; base += 64 * kRowUnroll) {
+        float v[kRowUnroll];
+        load_range(base, v);
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; u++) {
+            const int i = base + lane + 64 * u;
+            if (i < w1) rsum += final_p(i, v[u]);
+        }
+    }
     rsum = wave_sum_d(rsum);
     if (lane == 0) s_scan[wave] = rsum;
     __syncthreads();
@@ -328,7 +664,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     if (a.probs || (r >= cum && r < cum + rsum)) {
         for (int base = w0; base < w1; base += 64) {
             const int i = base + lane;
-            const double p = i < w1 ? final_p(i) : 0.0;
+            const double p = i < w1 ? final_p(i, lg[i]) : 0.0;
             if (a.probs && i < w1) a.probs[(size_t)row * n + i] = p;
             double inc = p;
 #pragma unroll
@@ -347,11 +683,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     }
     int tok = block_min_i32(cand, red_i);
     if (tok == INT_MAX) tok = n - 1;
-    if (tid == 0) {
-        if (a.out) a.out[row] = tok;
-        // a key the fused-argmax consumers decode to tok (slot 0 of row)
-        if (a.key) a.key[row] = (1ull << 32) | (unsigned long long)(0xffffffffu - (uint32_t)tok);
-    }
+    emit(tok);
 }
 
 int launch_sample(hipStream_t s, const float* logits, int rows, int n, float temperature, int top_k, float top_p,

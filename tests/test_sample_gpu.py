@@ -117,3 +117,34 @@ def test_sample_nucleus_ties_by_index(gpu):
             tok, want = orc.sample_nucleus(logits[r], 1.0, K, P, float(u[r]))
             np.testing.assert_allclose(got_p[r], want, rtol=0, atol=1e-12)
             assert got_tok[r] == tok
+
+
+@pytest.mark.parametrize("v2,nucleus", [(1.4099166, False), (1.4099166, True), (1.5, False), (1.5, True)])
+def test_sample_scaled_ties_below_raw_threshold(gpu, v2, nucleus):
+    """Two logits one float apart whose values divided by the temperature
+    (0.7) are equal: the top_k-th largest scaled value is reached by both,
+    so both stay (the reference's kthLargest counts the scaled values). With
+    1.4099166 both sit in one histogram bin of the top-k candidate pass;
+    with 1.5 (a bin's lowest value) the lower one sits in the bin below."""
+    v2 = np.float32(v2)
+    v1 = np.nextafter(v2, np.float32(0))
+    T = np.float32(0.7)
+    assert v1 / T == v2 / T and v1 < v2
+    rng = np.random.default_rng(8)
+    n = 3000
+    logits = (rng.standard_normal((2, n)) * 0.3).astype(np.float32)
+    logits[:, 100:105] = [2.5, 2.6, 2.7, 2.8, 2.9]
+    logits[:, 700] = v2
+    logits[:, 1700] = v1
+    K = 6  # v2 is the 6th largest logit, v1 the 7th: both kept
+    u = np.array([0.3, 0.97])
+    out = torch.empty(2, dtype=torch.int32, device="cuda")
+    probs = torch.empty((2, n), dtype=torch.float64, device="cuda")
+    (gpu.sample_nucleus if nucleus else gpu.sample)(dev(logits), float(T), K, 0.0, dev(u), out, probs)
+    got_tok, got_p = host(out), host(probs)
+    for r in range(2):
+        tok, want = (orc.sample_nucleus if nucleus else orc.sample)(logits[r], float(T), K, 0.0, float(u[r]))
+        assert np.count_nonzero(want) == 7
+        assert np.array_equal(got_p[r] > 0, want > 0)
+        np.testing.assert_allclose(got_p[r], want, rtol=0, atol=1e-12)
+        assert got_tok[r] == tok
