@@ -5,8 +5,13 @@
 //
 //   scaled = logits / temperature (f32)
 //   0 < top_k < n: values below the top_k-th largest scaled value -> -inf
-//     (the threshold found by a 4-pass radix select over order-preserving
-//     32-bit keys, 256-bin histograms in LDS: the value kthLargest returns)
+//     (the value kthLargest returns, counting equal values). Up to
+//     kSampleCap candidates: a 4096-bin histogram of the raw logits'
+//     order-preserving 32-bit keys (division by T is monotone) locates the
+//     bin of the top_k-th largest, one more pass collects every key at or
+//     above it, and everything below runs on those candidates in index
+//     order; otherwise a 4-pass radix select (256-bin histograms) over the
+//     row and the passes below over the whole row.
 //   p = exp(f64(scaled - max)) / sum (f64)
 //   0 < top_p < 1: the reference zeroes the smallest positive probability
 //     (lowest index first among equals) until the positive ones sum to at
