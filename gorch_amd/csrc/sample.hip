@@ -342,7 +342,9 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     // does: 0/0 = NaN everywhere when nothing was kept, and the draw then
     // falls through to n - 1)
     auto finish = [&](double p, bool kept, double resum) -> double {
-        if (!use_p) return p;
+        // (a NaN logit makes the sum and every p NaN; the nucleus cut then
+        // never reaches top_p and keeps everything: NaN as well)
+        if (!use_p || p != p) return p;
         if (a.nucleus) return kept ? p / resum : 0.0;
         return (kept ? p : 0.0) / resum;
     };

@@ -148,3 +148,26 @@ def test_sample_scaled_ties_below_raw_threshold(gpu, v2, nucleus):
         assert np.array_equal(got_p[r] > 0, want > 0)
         np.testing.assert_allclose(got_p[r], want, rtol=0, atol=1e-12)
         assert got_tok[r] == tok
+
+
+@pytest.mark.parametrize("nucleus", [False, True])
+def test_sample_nan_logit(gpu, nucleus):
+    """A NaN logit is never below the top-k threshold (the reference's
+    `scaled[i] < threshold` is false for it), so the f64 sum is NaN, every
+    probability NaN and the draw falls through to the last index, on the
+    device as in the oracle."""
+    rng = np.random.default_rng(9)
+    n = 5000
+    logits = (rng.standard_normal((2, n)) * 2).astype(np.float32)
+    logits[0, 17] = np.nan
+    logits[1, 4321] = np.nan
+    u = np.array([0.1, 0.8])
+    out = torch.empty(2, dtype=torch.int32, device="cuda")
+    probs = torch.empty((2, n), dtype=torch.float64, device="cuda")
+    for K, P in ((40, 0.0), (40, 0.9), (0, 0.0)):
+        (gpu.sample_nucleus if nucleus else gpu.sample)(dev(logits), 0.8, K, P, dev(u), out, probs)
+        got_tok, got_p = host(out), host(probs)
+        for r in range(2):
+            tok, want = (orc.sample_nucleus if nucleus else orc.sample)(logits[r], 0.8, K, P, float(u[r]))
+            assert got_tok[r] == tok == n - 1
+            assert np.isnan(want).all() and np.isnan(got_p[r]).all()
