@@ -593,15 +593,32 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
         const float v = value(x);
         return v == -INFINITY ? 0.0 : exp((double)(v - mx));
     };
-    double part = 0.0;
-    for (int base = 0; base < n; base += kRowUnroll * kSampleThreads) {
-        float v[kRowUnroll];
-        load_row(base, v);
+    // the f64 sum over 16 contiguous wave ranges of the row (seg entries,
+    // a multiple of 64, read 64 at a time), added in wave order; the
+    // inverse CDF below walks the same ranges
+    const int lane = tid & 63, wave = tid >> 6;
+    const int seg = ((n + kSampleThreads / 64 - 1) / (kSampleThreads / 64) + 63) & ~63;
+    const int w0 = min(n, wave * seg), w1 = min(n, w0 + seg);
+    // entries base + lane + 64 u (u < kRowUnroll), all loads in flight
+    auto load_range = [&](int base, float (&v)[kRowUnroll]) {
 #pragma unroll
         for (int u = 0; u < kRowUnroll; u++)
-            if (base + u * kSampleThreads + tid < n) part += expo(v[u]);
+            v[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rrow, (base + lane + 64 * u) * 4, 0, 0));
+    };
+    double esum = 0.0;
+    for (int base = w0; base < w1; base += 64 * kRowUnroll) {
+        float v[kRowUnroll];
+        load_range(base, v);
+#pragma unroll
+        for (int u = 0; u < kRowUnroll; u++)
+            if (base + lane + 64 * u < w1) esum += expo(v[u]);
     }
-    const double sum = block_sum_f64(part, red_d);
+    esum = wave_sum_d(esum);
+    if (lane == 0) red_d[wave] = esum;
+    __syncthreads();
+    double sum = 0.0;
+    for (int w = 0; w < kSampleThreads / 64; w++) sum += red_d[w];
+    __syncthreads();
 
     // top-p (:182-229) over the positive probabilities
     double resum = 1.0;
@@ -637,32 +654,27 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     }
     auto final_p = [&](int i, float x) { return finish(expo(x) / sum, use_p && is_kept(i), resum); };
 
-    // the draw and the inverse CDF in index order (:231-240): wave w owns
-    // the contiguous range [w * seg, (w + 1) * seg) of the row (seg a
-    // multiple of 64) and reads it 64 consecutive entries at a time; the
-    // range sums are added in wave order, and only the wave whose range
-    // holds the crossing (or every wave, when the distribution is written
-    // out) scans its range again, 64 entries per step
-    const int lane = tid & 63, wave = tid >> 6;
-    const int seg = ((n + kSampleThreads / 64 - 1) / (kSampleThreads / 64) + 63) & ~63;
-    const int w0 = min(n, wave * seg), w1 = min(n, w0 + seg);
-    // entries base + lane + 64 u (u < kRowUnroll), all loads in flight
-    auto load_range = [&](int base, float (&v)[kRowUnroll]) {
-#pragma unroll
-        for (int u = 0; u < kRowUnroll; u++)
-            v[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rrow, (base + lane + 64 * u) * 4, 0, 0));
-    };
+    // the draw and the inverse CDF in index order (:231-240) over the wave
+    // ranges: each range's share of the final distribution (without top-p
+    // its exp sum over the total; with it a pass of the final values), the
+    // shares added in wave order, and only the wave whose range holds the
+    // crossing (or every wave, when the distribution is written out) scans
+    // its range again, 64 entries per step
     double rsum = 0.0;
-    for (int base = w0; base < w1; base += 64 * kRowUnroll) {
-        float v[kRowUnroll];
-        load_range(base, v);
+    if (use_p) {
+        for (int base = w0; base < w1; base += 64 * kRowUnroll) {
+            float v[kRowUnroll];
+            load_range(base, v);
 #pragma unroll
-        for (int u = 0; u < kRowUnroll; u++) {
-            const int i = base + lane + 64 * u;
-            if (i < w1) rsum += final_p(i, v[u]);
+            for (int u = 0; u < kRowUnroll; u++) {
+                const int i = base + lane + 64 * u;
+                if (i < w1) rsum += final_p(i, v[u]);
+            }
         }
+        rsum = wave_sum_d(rsum);
+    } else {
+        rsum = esum / sum;
     }
-    rsum = wave_sum_d(rsum);
     if (lane == 0) s_scan[wave] = rsum;
     __syncthreads();
     double cum = 0.0;
