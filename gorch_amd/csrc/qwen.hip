@@ -262,10 +262,19 @@ static int qwen_forward(gorch_hip_qwen* m, hipStream_t s, int n, bool prefill, i
     // the bf16 embedding, qwen.go:84) with the greedy choice fused in, or
     // the logits sampled (the draw of token i is Philox(seed, i, 0), the
     // step read from state[1])
-    GH_TRY(launch_rmsnorm(s, m->x + (size_t)(n - 1) * d, m->norm, m->h, 1, d, m->eps));
+    // (RMSNorm in the one-row GEMV's prologue where its shape table takes d)
     LinearExtras ex;
     if (m->smp_t <= 0.f) ex.argmax_key = m->key;
-    GH_TRY(launch_linear_bf16_od(s, m->h, m->embed_bf16, nullptr, nullptr, OutDesc::plain(m->logits, m->vocab), 1,
+    const float* head_in = m->h;
+    if (gemv_m1_prologue_ok(d)) {
+        ex.ln_g = m->norm;
+        ex.ln_rms = true;
+        ex.ln_eps = m->eps;
+        head_in = m->x + (size_t)(n - 1) * d;
+    } else {
+        GH_TRY(launch_rmsnorm(s, m->x + (size_t)(n - 1) * d, m->norm, m->h, 1, d, m->eps));
+    }
+    GH_TRY(launch_linear_bf16_od(s, head_in, m->embed_bf16, nullptr, nullptr, OutDesc::plain(m->logits, m->vocab), 1,
                                  m->vocab, d, GORCH_HIP_EPI_NONE, ex));
     if (m->smp_t > 0.f)
         GH_TRY(launch_sample(s, m->logits, 1, m->vocab, m->smp_t, m->smp_k, m->smp_p, nullptr, m->smp_seed,
