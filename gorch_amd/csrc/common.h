@@ -42,6 +42,11 @@ struct LinearExtras {
     // K split across ksplit blocks: raw partial sums to part[s][m][n]
     // (bias, activation and residual are then applied by the reduction)
     float* part = nullptr;
+    // tile-packed GEMV only: K split across ksplit blocks that add their
+    // partial sums (slice 0 also the bias) into the output with float
+    // atomics; the output holds what they add to (the residual), and the
+    // order of the additions varies between runs
+    bool accumulate = false;
     int ksplit = 1;
     int kslice = 0;    // K per slice (set by the launcher)
     int split_nt = 0;  // 16-row tiles per block in split mode (0: 4)

@@ -844,10 +844,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
     __shared__ unsigned long long s_key[16];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
-    // K-split mode (ex.part): blockIdx.y is the K slice [ex.kslice * y, ..)
-    // and the block writes raw partial sums for a following reduction
-    const int k_off = ex.part ? (int)blockIdx.y * ex.kslice : 0;
-    const int k_end = ex.part ? min(K, k_off + ex.kslice) : K;
+    // K-split mode (ex.part or ex.accumulate): blockIdx.y is the K slice
+    // [ex.kslice * y, ..) and the block writes raw partial sums for a
+    // following reduction, or adds them into the output
+    const bool ksplit = ex.part || ex.accumulate;
+    const int k_off = ksplit ? (int)blockIdx.y * ex.kslice : 0;
+    const int k_end = ksplit ? min(K, k_off + ex.kslice) : K;
     const int kb = k_off + wave * ks * 32, ke = min(k_end, kb + ks * 32);
     const long long xs = ex.x_stride ? ex.x_stride : K;
     const int ntiles = (N + 15) >> 4;
@@ -1011,6 +1013,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
             float val = 0.f;
 #pragma unroll
             for (int w = 0; w < NW; w++) val += redf[((buf * NW + w) * 64 + src) * 4 + comp];
+            if (ex.accumulate) {
+                if (bias && blockIdx.y == 0) val = val + (EARLY ? bv : tl.b);
+                __hip_atomic_fetch_add(od.at_p(om, on, posv), val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return;
+            }
             if (ex.part) {
                 ex.part[((size_t)blockIdx.y * M + om) * N + on] = val;
                 return;
@@ -1234,9 +1241,11 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
         return n;
     }();
     const int ntiles = (N + 15) / 16;
-    // with ex.part the grid's y dimension is ex.ksplit K slices of ex.kslice
-    const int S = ex.part ? ex.ksplit : 1;
-    const int ksteps = ex.part ? ex.kslice / 32 : (K + 31) / 32;
+    // with ex.part or ex.accumulate the grid's y dimension is ex.ksplit K
+    // slices of ex.kslice
+    const bool ksplit = ex.part || ex.accumulate;
+    const int S = ksplit ? ex.ksplit : 1;
+    const int ksteps = ksplit ? ex.kslice / 32 : (K + 31) / 32;
     // 8 waves per block; 4 when the blocks hold one or two tiles each (the
     // weight is short in tiles for the grid) and a 4-wave instantiation
     // takes the k-steps (measured: 9-shape GEMV sweep, 768x3072 at M = 4 /
@@ -1587,17 +1596,21 @@ int packed_split_slices(int K, int N) {
 int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, const float* bias,
                             const float* residual, const OutDesc& od, int M, int N, int K, int epilogue,
                             const LinearExtras& ex) {
-    if (M < 1 || M > 16 || (ex.part && (ex.argmax_key || ex.ln_g)) || (ex.ln_g && ex.ln_stats)) {
+    if (M < 1 || M > 16 || ((ex.part || ex.accumulate) && (ex.argmax_key || ex.ln_g)) || (ex.ln_g && ex.ln_stats) ||
+        (ex.accumulate && (ex.part || residual || epilogue != GORCH_HIP_EPI_NONE))) {
         set_error("linear_bf16_packed: needs 1 <= M <= 16, no argmax or LayerNorm with a K split");
         return GORCH_HIP_EUNSUPPORTED;
     }
-    if (ex.part) {
-        // caller-owned partials (the engine's row reducer sums them)
+    if (ex.part || ex.accumulate) {
+        // caller-owned partials (the engine's row reducer sums them), or
+        // slices added into the output
         LinearExtras sx = ex;
         sx.kslice = ((K + ex.ksplit - 1) / ex.ksplit + 31) / 32 * 32;
         sx.ksplit = (K + sx.kslice - 1) / sx.kslice;
-        const int rc = launch_tiles(s, x, Wp, nullptr, nullptr, OutDesc::plain(nullptr, N), M, N, K,
-                                    GORCH_HIP_EPI_NONE, sx);
+        const int rc = ex.accumulate
+                           ? launch_tiles(s, x, Wp, bias, nullptr, od, M, N, K, GORCH_HIP_EPI_NONE, sx)
+                           : launch_tiles(s, x, Wp, nullptr, nullptr, OutDesc::plain(nullptr, N), M, N, K,
+                                          GORCH_HIP_EPI_NONE, sx);
         if (rc < 0) set_error("linear_bf16_packed: K slice above 3072 is not supported");
         return rc < 0 ? GORCH_HIP_EUNSUPPORTED : rc;
     }

@@ -273,7 +273,16 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         } else {
             GH_TRY(launch_attn_cached(s, a, g->heads, rows));
         }
-        if (!wo_fused && batched) {
+        if (!wo_fused && batched && w.wo_p && wo_fuse) {
+            // K slices add themselves (slice 0 with the bias) into x, which
+            // holds the residual; the reducer then only normalises
+            LinearExtras sp;
+            sp.accumulate = true;
+            sp.ksplit = ksplit_slices(d, wo_split_req);
+            GH_TRY(launch_linear_packed_od(s, g->att, w.wo_p, w.bo, nullptr, OutDesc::plain(g->x, d), rows, d, d,
+                                           GORCH_HIP_EPI_NONE, sp));
+            GH_TRY(launch_reduce_rows(s, nullptr, 0, nullptr, g->x, rows, d, eps, g->stats, w.ln2_g, w.ln2_b, g->h));
+        } else if (!wo_fused && batched) {
             LinearExtras sp;
             sp.part = g->part;
             sp.ksplit = w.wo_p ? ksplit_slices(d, wo_split_req) : split_for(d);
@@ -300,7 +309,17 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             GH_TRY(launch_layernorm(s, g->x, w.ln2_g, w.ln2_b, g->h, rows, d, eps, d));
             GH_TRY(launch_linear_bf16(s, g->h, w.w1, w.b1, nullptr, g->ff, rows, 4 * d, d, GORCH_HIP_EPI_GELU));
         }
-        if (batched) {
+        if (batched && w.w2_p && wo_fuse) {
+            LinearExtras sp;
+            sp.accumulate = true;
+            sp.ksplit = res_split(4 * d);
+            GH_TRY(launch_linear_packed_od(s, g->ff, w.w2_p, w.b2, nullptr, OutDesc::plain(g->x, d), rows, d, 4 * d,
+                                           GORCH_HIP_EPI_NONE, sp));
+            const bool last = l + 1 == g->layers;
+            GH_TRY(launch_reduce_rows(s, nullptr, 0, nullptr, g->x, rows, d, eps, g->stats,
+                                      last ? g->lnf_g : g->L[l + 1].ln1_g, last ? g->lnf_b : g->L[l + 1].ln1_b,
+                                      g->h));
+        } else if (batched) {
             LinearExtras sp;
             sp.part = g->part;
             sp.ksplit = w.w2_p ? res_split(4 * d) : split_for(4 * d);

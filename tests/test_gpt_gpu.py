@@ -290,41 +290,48 @@ def test_generate_stop_token(tiny, use_graph):
     assert all(np.array_equal(ids2[b], full[b]) for b in range(4))
 
 
-@pytest.mark.parametrize("cfg,prompt", [
+@pytest.mark.parametrize("cfg,prompt,batch", [
     # one sequence, short cache: the one-pass attention kernel with Wo fused
     # by float atomics in the default mode
-    (dict(vocab=64, dim=64, heads=4, layers=2, max_seq=64), 20),
+    (dict(vocab=64, dim=64, heads=4, layers=2, max_seq=64), 20, 1),
     # one sequence, 300-row cache: the key-split attention with Wo in its
     # chunk merge in the default mode
-    (dict(vocab=64, dim=128, heads=2, layers=2, max_seq=300), 270),
+    (dict(vocab=64, dim=128, heads=2, layers=2, max_seq=300), 270, 1),
+    # four sequences: the batched step, whose Wo and FFN2 K slices add
+    # themselves into the residual stream with float atomics in the default
+    # mode (K 1024 / 4096: four and seven slices)
+    (dict(vocab=96, dim=1024, heads=8, layers=2, max_seq=64), 24, 4),
 ])
-def test_deterministic_mode_bit_identical(gpu, cfg, prompt):
-    """gorch_hip_set_deterministic(1): the one-row decode step takes the
-    output projection as a GEMV of its own (no float atomics), so two runs
-    give bit-identical logits, tokens identical to the oracle and first-step
+def test_deterministic_mode_bit_identical(gpu, cfg, prompt, batch):
+    """gorch_hip_set_deterministic(1): the decode step takes the output
+    projection as a GEMV of its own and the batched residual Linears' K
+    slices are summed in slice order (no float atomics), so two runs give
+    bit-identical logits, tokens identical to the oracle and first-step
     logits within 1e-3 (model/generate.go:134-144 is a fixed-order loop).
     The default (atomic) mode matches the oracle to the same bar."""
     w = syn.gpt2_weights(cfg, seed=46, random_affine=True)
     g, o = gpu.GPT(w), orc.GPT(w)
-    prompts = syn.prompt_ids(prompt, cfg["vocab"], seed=82)[None, :]
-    ref, ref_logits, _ = o.generate_cached(prompts[0], 10, want_logits=True)
+    prompts = np.stack([syn.prompt_ids(prompt, cfg["vocab"], seed=82 + b) for b in range(batch)])
+    refs = [o.generate_cached(prompts[b], 10, want_logits=True) for b in range(batch)]
     prev = gpu.set_deterministic(True)
     try:
         assert gpu.deterministic_enabled()
         runs = []
         for use_graph in (False, True, True):
             ids, logits, _ = g.generate_cached(prompts, 10, want_logits=True, use_graph=use_graph)
-            assert list(ids[0]) == list(ref)
-            assert rel_err(logits[0][0], ref_logits[0]) <= 1e-3
-            assert rel_err(logits[:, 0], ref_logits) <= 2e-2
+            for b, (ref, ref_logits, _) in enumerate(refs):
+                assert list(ids[b]) == list(ref)
+                assert rel_err(logits[0][b], ref_logits[0]) <= 1e-3
+                assert rel_err(logits[:, b], ref_logits) <= 2e-2
             runs.append(logits)
         assert np.array_equal(runs[0], runs[1]) and np.array_equal(runs[1], runs[2])
     finally:
         gpu.set_deterministic(prev)
     assert not gpu.deterministic_enabled()
     ids, logits, _ = g.generate_cached(prompts, 10, want_logits=True)
-    assert list(ids[0]) == list(ref)
-    assert rel_err(logits[0][0], ref_logits[0]) <= 1e-3
+    for b, (ref, ref_logits, _) in enumerate(refs):
+        assert list(ids[b]) == list(ref)
+        assert rel_err(logits[0][b], ref_logits[0]) <= 1e-3
     g.close()
 
 
