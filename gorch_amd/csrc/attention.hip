@@ -20,6 +20,37 @@
 
 namespace gh {
 
+// Four consecutive output columns of row `row` (col % 4 == 0): f32 to
+// a.out, or hi/lo halves to a.out_frag (8-byte stores: one lane's group of
+// eight columns holds all four)
+__device__ __forceinline__ void attn_out4(const AttnArgs& a, int row, int col, float4 t) {
+    if (a.out_frag) {
+        const float v[4] = {t.x, t.y, t.z, t.w};
+        uint16_t hi[4], lo[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) split_hi_lo1(v[e], hi[e], lo[e]);
+        const size_t i = xfrag_index(row, col);
+        *reinterpret_cast<uint2*>(a.out_frag + i) =
+            make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+        *reinterpret_cast<uint2*>(a.out_frag + i + 512) =
+            make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
+    } else {
+        *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + col) = t;
+    }
+}
+// one output column: f32, or its hi/lo halves
+__device__ __forceinline__ void attn_out1(const AttnArgs& a, int row, int col, float v) {
+    if (a.out_frag) {
+        uint16_t hi, lo;
+        split_hi_lo1(v, hi, lo);
+        const size_t i = xfrag_index(row, col);
+        a.out_frag[i] = hi;
+        a.out_frag[i + 512] = lo;
+    } else {
+        a.out[(size_t)row * a.dim + col] = v;
+    }
+}
+
 __device__ float block_max(float v, float* sh) {
     v = wave_max(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -185,7 +216,7 @@ __global__ __launch_bounds__(NWV * 64) void k_attn_cached(AttnArgs a) {
         float o = pv[0][d];
 #pragma unroll
         for (int w = 1; w < NWV; w++) o = o + pv[w][d];
-        a.out[(size_t)row * a.dim + h * hd + d] = o;
+        attn_out1(a, row, h * hd + d, o);
     }
 }
 
@@ -337,7 +368,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_rows(AttnArgs a) {
                 t = make_float4(t.x / L, t.y / L, t.z / L, t.w / L);
             }
             if constexpr (WO) po[0][c] = t;
-            else *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + h * (4 * HD4) + 4 * c) = t;
+            else attn_out4(a, row, h * (4 * HD4) + 4 * c, t);
         }
         if constexpr (WO) {
             __syncthreads();
@@ -423,7 +454,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_rows(AttnArgs a) {
                 t.z += pv.z;
                 t.w += pv.w;
             }
-        *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + h * (4 * HD4) + 4 * c) = t;
+        attn_out4(a, row, h * (4 * HD4) + 4 * c, t);
     }
 }
 
@@ -550,12 +581,12 @@ __global__ __launch_bounds__(NW * 64) void k_attn_flash(AttnArgs a) {
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
     if (qok) {
-        float* orow = a.out + (size_t)(b * a.new_seq + qi) * a.dim + h * HD;
+        const int orow = b * a.new_seq + qi;
         const float inv = 1.0f / l;
 #pragma unroll
         for (int t = 0; t < QU; t++)
-            *reinterpret_cast<float4*>(orow + 16 * t + 4 * g) =
-                make_float4(o[t][0] * inv, o[t][1] * inv, o[t][2] * inv, o[t][3] * inv);
+            attn_out4(a, orow, h * HD + 16 * t + 4 * g,
+                      make_float4(o[t][0] * inv, o[t][1] * inv, o[t][2] * inv, o[t][3] * inv));
     }
 }
 
@@ -849,7 +880,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_long(AttnArgs a) {
         } else {
             t = make_float4(t.x / L, t.y / L, t.z / L, t.w / L);
         }
-        *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + h * (4 * HD4) + 4 * c) = t;
+        attn_out4(a, row, h * (4 * HD4) + 4 * c, t);
     }
 }
 
@@ -911,7 +942,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a, int nc) {
     } else {
         t = make_float4(t.x / L, t.y / L, t.z / L, t.w / L);
     }
-    *reinterpret_cast<float4*>(a.out + (size_t)row * a.dim + h * (4 * HD4) + 4 * c) = t;
+    attn_out4(a, row, h * (4 * HD4) + 4 * c, t);
 }
 
 // k_attn_combine with the output projection: grid (heads, row groups of
@@ -1108,6 +1139,10 @@ int launch_attn_cached(hipStream_t s, const AttnArgs& a, int heads, int rows) {
     const size_t lds = (size_t)visible * sizeof(float);
     if (a.qkv_part && (a.new_seq != 1 || a.kv_heads != 0 || a.qkv_slices < 1 || a.qkv_slices > kMaxPartSlices)) {
         set_error("attention: split QKV partials need one new row per sequence, no grouped KV heads, 1..8 slices");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
+    if (a.out_frag && (rows > 16 || a.wo)) {
+        set_error("attention: a fragment-layout output takes at most 16 rows and no fused output projection");
         return GORCH_HIP_EUNSUPPORTED;
     }
     const dim3 grid(heads, rows);

@@ -47,6 +47,14 @@ struct LinearExtras {
     // atomics; the output holds what they add to (the residual), and the
     // order of the additions varies between runs
     bool accumulate = false;
+    // tile-packed GEMV only: the activations come pre-split in the fragment
+    // layout (xfrag_index) instead of as f32 rows of x (no fused LayerNorm,
+    // x_stride unused)
+    const uint16_t* x_frag = nullptr;
+    // tile-packed GEMV only: the outputs go to this fragment-layout buffer
+    // (as the next GEMV's pre-split activations) instead of the output
+    // descriptor (no K split, no argmax)
+    uint16_t* out_frag = nullptr;
     int ksplit = 1;
     int kslice = 0;    // K per slice (set by the launcher)
     int split_nt = 0;  // 16-row tiles per block in split mode (0: 4)
@@ -93,10 +101,11 @@ constexpr int kReduceRowsMaxCols = 2048;
 // Row reduction after a K-split Linear: x[m] = x[m] + bias + sum_s part[s][m]
 // (slices added in order; S = 0 leaves x as is), then the LayerNorm
 // statistics of the new row into stats[m] when stats is not null, and with
-// h the normalised row h[m] = LayerNorm(x[m]; ln_g, ln_b) as well.
+// h the normalised row h[m] = LayerNorm(x[m]; ln_g, ln_b) as well; with hf
+// (M <= 16) that row goes to hf in the fragment layout (xfrag_index).
 int launch_reduce_rows(hipStream_t s, const float* part, int S, const float* bias, float* x, int M, int N,
                        float eps, float2* stats, const float* ln_g = nullptr, const float* ln_b = nullptr,
-                       float* h = nullptr);
+                       float* h = nullptr, uint16_t* hf = nullptr);
 int launch_linear_bf16(hipStream_t s, const float* x, const uint16_t* W, const float* bias,
                        const float* residual, float* y, int M, int N, int K, int epilogue);
 // Tile-packed bf16 weights (gemv.hip): element count of the packed copy,
@@ -298,6 +307,9 @@ struct AttnArgs {
     int kv_heads;  // grouped-query attention: KV heads (0 = one per query head)
     int kv_dim;    // cache row stride in floats (0 = dim)
     int recip;     // normalise by multiplying with 1/sum (GQA) instead of dividing
+    // not null (at most 16 rows): the output goes here in the fragment
+    // layout (xfrag_index, K = dim) instead of to out
+    uint16_t* out_frag = nullptr;
     // One new row per sequence (new_seq == 1, no grouped KV heads) whose
     // fused QKV Linear ran split over K: q, k and v of the row are qkv_bias
     // + the qkv_slices partial sums at qkv_part ([slice][row][3 * dim],
@@ -429,6 +441,25 @@ __device__ __forceinline__ void split_hi_lo(const float (&f)[8], bf16x8& hi, bf1
         hi[i] = __builtin_bit_cast(__bf16, (uint16_t)(u >> 16));
         lo[i] = (__bf16)(f[i] - h);
     }
+}
+
+// Fragment layout of up to 16 activation rows of K columns, the tile GEMV's
+// MFMA A operand already split: k-step j (columns 32 j .. 32 j + 31) takes
+// 2 KB, the bf16 hi parts of lanes 0..63 then their lo parts (split_hi_lo),
+// lane 16 g + r holding row r, columns 32 j + 8 g .. 32 j + 8 g + 7. A wave
+// reads one k-step as two contiguous 1 KB loads. Rows and columns nobody
+// writes keep what the buffer held (zero it once at allocation: columns
+// past K must read as zeros; rows past M only feed outputs nobody stores).
+__host__ __device__ inline size_t xfrag_bytes(int K) { return (size_t)((K + 31) / 32) * 2048; }
+// uint16 index of the hi part of (row m, column k); the lo part is 512 on
+__device__ __forceinline__ size_t xfrag_index(int m, int k) {
+    return (size_t)(k >> 5) * 1024 + (size_t)((((k >> 3) & 3) * 16 + m) * 8 + (k & 7));
+}
+// hi/lo bits of one value, as split_hi_lo makes them
+__device__ __forceinline__ void split_hi_lo1(float f, uint16_t& hi, uint16_t& lo) {
+    const uint32_t u = __float_as_uint(f) & 0xffff0000u;
+    hi = (uint16_t)(u >> 16);
+    lo = __builtin_bit_cast(uint16_t, (__bf16)(f - __uint_as_float(u)));
 }
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));

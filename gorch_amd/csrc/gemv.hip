@@ -857,14 +857,28 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
 
     // activations first (they come from L2): converting them waits for
     // them alone, not for the weights issued after them
-    const __amdgpu_buffer_rsrc_t rsx = make_rsrc(x, ((long long)(M - 1) * xs + K) * 4);
+    // (pre-split activations: k-step j's hi and lo fragments, one
+    // contiguous 1 KB each per wave)
+    const bool xf = !LN && ex.x_frag;
     u32x4 xa[KS][2];
+    if (xf) {
+        const __amdgpu_buffer_rsrc_t rsf = make_rsrc(ex.x_frag, (long long)xfrag_bytes(K));
 #pragma unroll
-    for (int u = 0; u < KS; u++) {
-        const int kc = kb + 32 * u + 8 * g;
-        const int off = (r < M && kc < ke) ? (int)((r * xs + kc) * 4) : kOutOfRange;
-        xa[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rsx, off, 0, 0);
-        xa[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rsx, off + 16, 0, 0);
+        for (int u = 0; u < KS; u++) {
+            const int k0 = kb + 32 * u;
+            const int off = k0 < ke ? (k0 >> 5) * 2048 + 16 * lane : kOutOfRange;
+            xa[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rsf, off, 0, 0);
+            xa[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rsf, off + 1024, 0, 0);
+        }
+    } else {
+        const __amdgpu_buffer_rsrc_t rsx = make_rsrc(x, ((long long)(M - 1) * xs + K) * 4);
+#pragma unroll
+        for (int u = 0; u < KS; u++) {
+            const int kc = kb + 32 * u + 8 * g;
+            const int off = (r < M && kc < ke) ? (int)((r * xs + kc) * 4) : kOutOfRange;
+            xa[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rsx, off, 0, 0);
+            xa[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rsx, off + 16, 0, 0);
+        }
     }
     // LayerNorm gamma/beta fragments (nn/layernorm.go:31-91), loaded with the
     // activations
@@ -963,6 +977,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
     bf16x8 ah[KS], al[KS];
 #pragma unroll
     for (int u = 0; u < KS; u++) {
+        if (xf) {
+            ah[u] = __builtin_bit_cast(bf16x8, xa[u][0]);
+            al[u] = __builtin_bit_cast(bf16x8, xa[u][1]);
+            continue;
+        }
         float f[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) f[e] = __uint_as_float(xa[u][e >> 2][e & 3]);
@@ -1025,6 +1044,14 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
             if (bias) val = val + (EARLY ? bv : tl.b);
             if (epilogue == GORCH_HIP_EPI_GELU) val = gelu_tanh(val);
             if (residual) val = (EARLY ? rv : tl.res) + val;
+            if (ex.out_frag) {
+                uint16_t hi, lo;
+                split_hi_lo1(val, hi, lo);
+                const size_t i = xfrag_index(om, on);
+                ex.out_frag[i] = hi;
+                ex.out_frag[i + 512] = lo;
+                return;
+            }
             *od.at_p(om, on, posv) = val;
             if (ex.argmax_key) {
                 const unsigned long long key = argmax_pack(val, on);
@@ -1601,6 +1628,11 @@ int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, c
         set_error("linear_bf16_packed: needs 1 <= M <= 16, no argmax or LayerNorm with a K split");
         return GORCH_HIP_EUNSUPPORTED;
     }
+    if ((ex.x_frag && ex.ln_g) || (ex.out_frag && (ex.part || ex.accumulate || ex.argmax_key))) {
+        set_error("linear_bf16_packed: fragment-layout activations take no fused LayerNorm, and a fragment-layout "
+                  "output no K split or argmax");
+        return GORCH_HIP_EUNSUPPORTED;
+    }
     if (ex.part || ex.accumulate) {
         // caller-owned partials (the engine's row reducer sums them), or
         // slices added into the output
@@ -1618,7 +1650,7 @@ int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, c
     // into the stream's scratch, then the ordered epilogue kernel (a CU
     // streams ~25 GB/s, so 48..127 tiles alone leave most of the chip idle)
     const int ntiles = (N + 15) / 16;
-    if (!ex.argmax_key && !ex.ln_g && ntiles < 128 && K >= 1024) {
+    if (!ex.argmax_key && !ex.ln_g && !ex.out_frag && ntiles < 128 && K >= 1024) {
         const int S = packed_split_slices(K, N);
         void* part = S >= 2 ? stream_scratch(s, (size_t)S * M * N * sizeof(float)) : nullptr;
         if (part) {

@@ -67,6 +67,10 @@ struct gorch_hip_gpt {
     // batched one-token steps: K-split partials of the fused QKV Linear,
     // summed by the cached attention kernel
     float* wpart = nullptr;
+    // batched decode over tile-packed weights: the GEMVs' activations
+    // pre-split in the fragment layout (LayerNorm outputs; FFN1's GELU
+    // output), zeroed at allocation
+    uint16_t *hfrag = nullptr, *ffrag = nullptr, *afrag = nullptr;
     int* ids = nullptr;
     size_t ids_cap = 0;
     hipStream_t stream = nullptr;  // engine stream (default priority), used for graph capture
@@ -121,6 +125,12 @@ static int ensure_acts(gorch_hip_gpt* g, size_t rows, size_t logit_rows) {
             GH_TRY(check(hipMalloc(&g->part, (size_t)kMaxSplit * 16 * d * 4), "hipMalloc part"));
             GH_TRY(check(hipMalloc(&g->stats, 16 * sizeof(float2)), "hipMalloc stats"));
             GH_TRY(check(hipMalloc(&g->wpart, (size_t)kMaxPartSlices * 16 * 3 * d * 4), "hipMalloc wpart"));
+            GH_TRY(check(hipMalloc(&g->hfrag, xfrag_bytes((int)d)), "hipMalloc hfrag"));
+            GH_TRY(check(hipMalloc(&g->ffrag, xfrag_bytes(4 * (int)d)), "hipMalloc ffrag"));
+            GH_TRY(check(hipMemset(g->hfrag, 0, xfrag_bytes((int)d)), "hipMemset hfrag"));
+            GH_TRY(check(hipMemset(g->ffrag, 0, xfrag_bytes(4 * (int)d)), "hipMemset ffrag"));
+            GH_TRY(check(hipMalloc(&g->afrag, xfrag_bytes((int)d)), "hipMalloc afrag"));
+            GH_TRY(check(hipMemset(g->afrag, 0, xfrag_bytes((int)d)), "hipMemset afrag"));
         }
     }
     if (logit_rows > g->logit_rows_cap) {
@@ -160,6 +170,19 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
     // as a plain operand (a LayerNorm fused into the GEMV's loads costs
     // ~3.5 us per call at 16 rows, d 1600, for its gamma/beta loads).
     const bool batched = fused && rows >= 2 && d <= kReduceRowsMaxCols;
+    // batched steps over tile-packed weights: the LayerNorm row passes and
+    // FFN1 write their outputs in the fragment layout the following tile
+    // GEMVs read as their MFMA operand (one contiguous 1 KB per wave and
+    // k-step instead of 16 rows of 32-byte pieces, and no split in the
+    // GEMV); the LM head reads it when it takes every row
+    const bool xfrag = batched && g->wlm_p && g->hfrag;
+    const bool head_frag = xfrag && (n == 1 || all_rows);
+    LinearExtras xin;
+    xin.x_frag = xfrag ? g->hfrag : nullptr;
+    // the LayerNorm output of a row pass: fragment layout, or row-major h
+    // (and the final one for a head that picks rows)
+    auto ln_h = [&](bool last) { return (xfrag && (!last || head_frag)) ? nullptr : g->h; };
+    auto ln_hf = [&](bool last) { return ln_h(last) ? nullptr : g->hfrag; };
     // row-major weights (no packed copy, dim above 3072): the K split aims
     // at ~300 blocks of 4 tiles
     constexpr int split_blocks = 300, split_nt = 4;
@@ -189,7 +212,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
     if (!x_ready) GH_TRY(launch_embed_pos(s, g->wte, g->wpe, g->ids, pos, g->x, d, n, rows));
     if (batched)
         GH_TRY(launch_reduce_rows(s, nullptr, 0, nullptr, g->x, rows, d, eps, g->stats, g->L[0].ln1_g,
-                                  g->L[0].ln1_b, g->h));
+                                  g->L[0].ln1_b, ln_h(false), ln_hf(false)));
     for (int l = 0; l < g->layers; l++) {
         const LayerW& w = g->L[l];
         OutDesc od{};
@@ -223,7 +246,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
                                attn_takes_qkv_part(a, g->heads, rows);
         LinearExtras ln1, ln2;
         if (qkv_split) {
-            LinearExtras sp;
+            LinearExtras sp = xin;
             sp.part = g->wpart;
             sp.ksplit = qkv_split_req;
             GH_TRY(launch_linear_packed_od(s, g->h, w.wqkv_p, nullptr, nullptr, OutDesc::plain(nullptr, 3 * d), rows,
@@ -234,7 +257,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             a.qkv_slice_stride = (long long)rows * 3 * d;
         } else if (batched && w.wqkv_p) {
             GH_TRY(launch_linear_packed_od(s, g->h, w.wqkv_p, w.bqkv, nullptr, od, rows, 3 * d, d,
-                                           GORCH_HIP_EPI_NONE, LinearExtras{}));
+                                           GORCH_HIP_EPI_NONE, xin));
         } else if (batched) {
             GH_TRY(launch_linear_bf16_od(s, g->h, w.wqkv, w.bqkv, nullptr, od, rows, 3 * d, d, GORCH_HIP_EPI_NONE,
                                          LinearExtras{}));
@@ -271,6 +294,8 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             a.wo_resid = g->x;
             GH_TRY(launch_attn_cached(s, a, g->heads, rows));
         } else {
+            // batched: the attention output in the fragment layout for Wo
+            if (xfrag) a.out_frag = g->afrag;
             GH_TRY(launch_attn_cached(s, a, g->heads, rows));
         }
         if (!wo_fused && batched && w.wo_p && wo_fuse) {
@@ -279,13 +304,16 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             LinearExtras sp;
             sp.accumulate = true;
             sp.ksplit = ksplit_slices(d, wo_split_req);
+            sp.x_frag = xfrag ? g->afrag : nullptr;
             GH_TRY(launch_linear_packed_od(s, g->att, w.wo_p, w.bo, nullptr, OutDesc::plain(g->x, d), rows, d, d,
                                            GORCH_HIP_EPI_NONE, sp));
-            GH_TRY(launch_reduce_rows(s, nullptr, 0, nullptr, g->x, rows, d, eps, g->stats, w.ln2_g, w.ln2_b, g->h));
+            GH_TRY(launch_reduce_rows(s, nullptr, 0, nullptr, g->x, rows, d, eps, g->stats, w.ln2_g, w.ln2_b,
+                                      ln_h(false), ln_hf(false)));
         } else if (!wo_fused && batched) {
             LinearExtras sp;
             sp.part = g->part;
             sp.ksplit = w.wo_p ? ksplit_slices(d, wo_split_req) : split_for(d);
+            sp.x_frag = xfrag ? g->afrag : nullptr;
             if (w.wo_p)
                 GH_TRY(launch_linear_packed_od(s, g->att, w.wo_p, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d,
                                                d, GORCH_HIP_EPI_NONE, sp));
@@ -293,13 +321,15 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
                 GH_TRY(launch_linear_bf16_od(s, g->att, w.wo, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d, d,
                                              GORCH_HIP_EPI_NONE, sp));
             GH_TRY(launch_reduce_rows(s, g->part, sp.ksplit, w.bo, g->x, rows, d, eps, g->stats, w.ln2_g, w.ln2_b,
-                                      g->h));
+                                      ln_h(false), ln_hf(false)));
         } else if (!wo_fused && !wo_split) {
             GH_TRY(launch_linear_bf16(s, g->att, w.wo, w.bo, g->x, g->x, rows, d, d, GORCH_HIP_EPI_NONE));
         }
         if (batched && w.w1_p) {
+            LinearExtras f1 = xin;
+            f1.out_frag = xfrag ? g->ffrag : nullptr;
             GH_TRY(launch_linear_packed_od(s, g->h, w.w1_p, w.b1, nullptr, OutDesc::plain(g->ff, 4 * d), rows, 4 * d,
-                                           d, GORCH_HIP_EPI_GELU, LinearExtras{}));
+                                           d, GORCH_HIP_EPI_GELU, f1));
         } else if (batched) {
             GH_TRY(launch_linear_bf16(s, g->h, w.w1, w.b1, nullptr, g->ff, rows, 4 * d, d, GORCH_HIP_EPI_GELU));
         } else if (fused) {
@@ -313,16 +343,18 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             LinearExtras sp;
             sp.accumulate = true;
             sp.ksplit = res_split(4 * d);
+            sp.x_frag = xfrag ? g->ffrag : nullptr;
             GH_TRY(launch_linear_packed_od(s, g->ff, w.w2_p, w.b2, nullptr, OutDesc::plain(g->x, d), rows, d, 4 * d,
                                            GORCH_HIP_EPI_NONE, sp));
             const bool last = l + 1 == g->layers;
             GH_TRY(launch_reduce_rows(s, nullptr, 0, nullptr, g->x, rows, d, eps, g->stats,
                                       last ? g->lnf_g : g->L[l + 1].ln1_g, last ? g->lnf_b : g->L[l + 1].ln1_b,
-                                      g->h));
+                                      ln_h(last), ln_hf(last)));
         } else if (batched) {
             LinearExtras sp;
             sp.part = g->part;
             sp.ksplit = w.w2_p ? res_split(4 * d) : split_for(4 * d);
+            sp.x_frag = xfrag ? g->ffrag : nullptr;
             if (w.w2_p)
                 GH_TRY(launch_linear_packed_od(s, g->ff, w.w2_p, nullptr, nullptr, OutDesc::plain(g->x, d), rows, d,
                                                4 * d, GORCH_HIP_EPI_NONE, sp));
@@ -333,7 +365,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
             const bool last = l + 1 == g->layers;
             GH_TRY(launch_reduce_rows(s, g->part, sp.ksplit, w.b2, g->x, rows, d, eps, g->stats,
                                       last ? g->lnf_g : g->L[l + 1].ln1_g, last ? g->lnf_b : g->L[l + 1].ln1_b,
-                                      g->h));
+                                      ln_h(last), ln_hf(last)));
         } else {
             GH_TRY(launch_linear_bf16(s, g->ff, w.w2, w.b2, g->x, g->x, rows, d, 4 * d, GORCH_HIP_EPI_NONE));
         }
@@ -346,6 +378,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
         LinearExtras lf;
         lf.x_stride = head_stride;
         lf.argmax_key = all_rows ? nullptr : argmax_key;
+        if (head_frag) lf.x_frag = g->hfrag;
         const float* head_h = g->h + (head_in - g->x);
         if (g->wlm_p)
             GH_TRY(launch_linear_packed_od(s, head_h, g->wlm_p, g->blm, nullptr, OutDesc::plain(g->logits, g->vocab),
@@ -773,6 +806,9 @@ void gorch_hip_gpt_free(gorch_hip_gpt* g) {
     (void)hipFree(g->part);
     (void)hipFree(g->stats);
     (void)hipFree(g->wpart);
+    (void)hipFree(g->hfrag);
+    (void)hipFree(g->ffrag);
+    (void)hipFree(g->afrag);
     (void)hipFree(g->ids);
     (void)hipFree(g->sample_err);
     delete g;

@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
                                                      const float* __restrict__ bias, float* __restrict__ x, int M,
                                                      int N, float eps, float2* __restrict__ stats,
                                                      const float* __restrict__ ln_g, const float* __restrict__ ln_b,
-                                                     float* __restrict__ h) {
+                                                     float* __restrict__ h, uint16_t* __restrict__ hf) {
     __shared__ double2 sh2[4];
     const int m = blockIdx.x;
     float* row = x + (size_t)m * N;
@@ -135,8 +135,9 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
     const long long pspan = S > 0 ? ((long long)(S - 1) * M + 1) * N * 4 : 0;
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(part + (S > 0 ? (size_t)m * N : 0), pspan);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias, bias ? (long long)N * 4 : 0);
-    const __amdgpu_buffer_rsrc_t rg = make_rsrc(ln_g, h ? (long long)N * 4 : 0);
-    const __amdgpu_buffer_rsrc_t rbe = make_rsrc(ln_b, h ? (long long)N * 4 : 0);
+    const bool norm = h || hf;
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(ln_g, norm ? (long long)N * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rbe = make_rsrc(ln_b, norm ? (long long)N * 4 : 0);
     float4 v[kRedVec], bv[kRedVec], gv[kRedVec], be[kRedVec];
     float4 p[kRedVec][RS];
     auto ld = [](__amdgpu_buffer_rsrc_t r, int off) {
@@ -199,7 +200,7 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
             s2 += d * d;
         }
     }
-    if (stats || h) {
+    if (stats || norm) {
         wave_sum2_d(s1, s2);
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
         if (lane == 0) sh2[wave] = make_double2(s1, s2);
@@ -215,14 +216,14 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
             if (j < N) *reinterpret_cast<float4*>(row + j) = v[c];
         }
     }
-    if (!stats && !h) return;
+    if (!stats && !norm) return;
     const double rn = 1.0 / N;
     const double d1 = div_rcp(s1, (double)N, rn);
     const double mean = (double)shift + d1;
     const double var = fmax(div_rcp(s2, (double)N, rn) - d1 * d1, 0.0);
     const float fm = (float)mean, inv = (float)rsqrt_f64(var + (double)eps);
     if (stats && threadIdx.x == 0) stats[m] = make_float2(fm, inv);
-    if (!h) return;
+    if (!norm) return;
     // the same f32 operations as a LayerNorm fused into a GEMV's operand load
 #pragma unroll
     for (int c = 0; c < kRedVec; c++) {
@@ -238,30 +239,47 @@ __global__ __launch_bounds__(256) void k_reduce_rows(const float* __restrict__ p
             const float normalized = (vc[e] - fm) * inv;
             oc[e] = normalized * gc[e] + bc[e];
         }
-        *reinterpret_cast<float4*>(h + (size_t)m * N + j) = o;
+        if (hf) {
+            // columns j .. j + 3 share one lane's 8-element group: 8-byte
+            // hi and lo stores
+            uint16_t hi[4], lo[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) split_hi_lo1(oc[e], hi[e], lo[e]);
+            const size_t i = xfrag_index(m, j);
+            *reinterpret_cast<uint2*>(hf + i) =
+                make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+            *reinterpret_cast<uint2*>(hf + i + 512) =
+                make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
+        } else {
+            *reinterpret_cast<float4*>(h + (size_t)m * N + j) = o;
+        }
     }
 }
 
 int launch_reduce_rows(hipStream_t s, const float* part, int S, const float* bias, float* x, int M, int N,
-                       float eps, float2* stats, const float* ln_g, const float* ln_b, float* h) {
+                       float eps, float2* stats, const float* ln_g, const float* ln_b, float* h, uint16_t* hf) {
     if (M == 0) return GORCH_HIP_OK;
+    if (hf && (h || M > 16)) {
+        set_error("reduce_rows: a fragment-layout output takes at most 16 rows and no row-major h");
+        return GORCH_HIP_EINVAL;
+    }
     if (N > 1024 * kRedVec || S > kRedSlices || N % 4) {
         set_error("reduce_rows: at most 2048 columns (a multiple of 4) and 8 slices");
         return GORCH_HIP_EUNSUPPORTED;
     }
-    if (h && (!ln_g || !ln_b)) {
+    if ((h || hf) && (!ln_g || !ln_b)) {
         set_error("reduce_rows: the normalised output needs gamma and beta");
         return GORCH_HIP_EINVAL;
     }
     // slice registers sized to S (loads of absent slices still cost their
     // instructions)
     if (S <= 2)
-        hipLaunchKernelGGL(k_reduce_rows<2>, dim3(M), dim3(256), 0, s, part, S, bias, x, M, N, eps, stats, ln_g, ln_b, h);
+        hipLaunchKernelGGL(k_reduce_rows<2>, dim3(M), dim3(256), 0, s, part, S, bias, x, M, N, eps, stats, ln_g, ln_b, h, hf);
     else if (S <= 4)
-        hipLaunchKernelGGL(k_reduce_rows<4>, dim3(M), dim3(256), 0, s, part, S, bias, x, M, N, eps, stats, ln_g, ln_b, h);
+        hipLaunchKernelGGL(k_reduce_rows<4>, dim3(M), dim3(256), 0, s, part, S, bias, x, M, N, eps, stats, ln_g, ln_b, h, hf);
     else
         hipLaunchKernelGGL(k_reduce_rows<kRedSlices>, dim3(M), dim3(256), 0, s, part, S, bias, x, M, N, eps, stats,
-                           ln_g, ln_b, h);
+                           ln_g, ln_b, h, hf);
     count(CNT_NORM);
     return check_launch("reduce_rows");
 }
