@@ -231,10 +231,12 @@ def test_generate_gpt2_xl_width_batch16(gpu):
     d 1600, 25 heads of 64, vocab 50257, batch 16, 512-token prompts (the
     matrix-core prefill GEMMs, flash attention over 512 rows, K/V rows
     written into the cache segments by the fused QKV GEMM), then 256 greedy
-    steps through the batched decode path (tile-packed GEMVs, the fused QKV
-    split over K with the attention adding its slices, K-split Wo/FFN2 with
-    the row reducer, the 16-wave two-pass attention kernel at 400 (head,
-    row) blocks, the LM head with the argmax fused) out to a 768-row cache.
+    steps through the batched decode path (tile-packed GEMVs reading their
+    activations in the MFMA fragment layout, the fused QKV split over K with
+    the attention adding its slices, Wo/FFN2 K slices added into the
+    residual with float atomics and the LayerNorm row passes, the 16-wave
+    two-pass attention kernel at 400 (head, row) blocks, the LM head with
+    the argmax fused) out to a 768-row cache.
     Every sequence against the oracle's generateCached: tokens identical
     over all 256 steps, first-step logits within 1e-3 and the run's within
     2e-2; the graph-replayed run gives the same tokens."""
