@@ -30,6 +30,7 @@
 // the prefetch each stage. K % 8 == 0. LDS rows are unpadded with
 // XOR-swizzled 16-byte chunks (no bank conflicts).
 #pragma once
+#include <type_traits>
 #include "common.h"
 
 namespace gh {
@@ -223,56 +224,67 @@ struct WideGemm {
             __syncthreads();
         };
 
+        // A wave whose rows all lie past nrows (the tail tile of an expert)
+        // computes nothing that is stored: it still moves its share of the
+        // stage's loads and meets every barrier, but reads no fragments and
+        // issues no MFMAs, leaving its SIMD's matrix core to the live waves.
+        auto stage_idle = [&](int buf, u32x4 (&ar)[A_U4], u32x4 (&wr)[W_U4], int next) {
+            sstore(buf ^ 1, ar, wr);
+            gload(next, ar, wr);
+            __syncthreads();
+        };
+        // wave-uniform by construction (scalar registers), so the choice is
+        // a scalar branch and each wave meets the same barriers in either arm
+        const int wave_s = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const bool live = (wave_s / WGN) * WM < __builtin_amdgcn_readfirstlane(nrows);
+
         // stage s lives in register set s % 2 until it is stored to LDS
         // buffer s % 2; stage s + 3 is requested once stage s + 1 has left
         // its registers. The body is unconditional (stages past K load
         // zeros; an odd stage count runs one all-zero stage) so the compiler
         // can keep the newer stage's loads in flight across the wait.
         const int nk2 = (nk + 1) & ~1;
-        if constexpr (PD == 1) {
-            // one register set: stage s + 2 is requested as stage s + 1
-            // leaves it (one stage of load latency covered)
-            gload(0, ra[0], rw[0]);
-            sstore(0, ra[0], rw[0]);
-            gload(1, ra[0], rw[0]);
-            __syncthreads();
-            for (int it = 0; it < nk2; it += 2) {
-                if constexpr (IL) {
-                    stage_il(0, ra[0], rw[0], it + 2);
-                    stage_il(1, ra[0], rw[0], it + 3);
+        auto main_loop = [&](auto live_tag) {
+            constexpr bool LIVE = decltype(live_tag)::value;
+            auto stage = [&](int buf, u32x4 (&ar)[A_U4], u32x4 (&wr)[W_U4], int next) {
+                if constexpr (!LIVE) {
+                    stage_idle(buf, ar, wr, next);
+                } else if constexpr (IL) {
+                    stage_il(buf, ar, wr, next);
                 } else {
-                    compute(0);
-                    sstore(1, ra[0], rw[0]);
-                    gload(it + 2, ra[0], rw[0]);
-                    __syncthreads();
-                    compute(1);
-                    sstore(0, ra[0], rw[0]);
-                    gload(it + 3, ra[0], rw[0]);
+                    compute(buf);
+                    sstore(buf ^ 1, ar, wr);
+                    gload(next, ar, wr);
                     __syncthreads();
                 }
-            }
-        } else {
-        gload(0, ra[0], rw[0]);
-        gload(1, ra[1], rw[1]);
-        sstore(0, ra[0], rw[0]);
-        gload(2, ra[0], rw[0]);
-        __syncthreads();
-        for (int it = 0; it < nk2; it += 2) {
-            if constexpr (IL) {
-                stage_il(0, ra[1], rw[1], it + 3);
-                stage_il(1, ra[0], rw[0], it + 4);
-            } else {
-                compute(0);
-                sstore(1, ra[1], rw[1]);
-                gload(it + 3, ra[1], rw[1]);
-                __syncthreads();
-                compute(1);
+            };
+            if constexpr (PD == 1) {
+                // one register set: stage s + 2 is requested as stage s + 1
+                // leaves it (one stage of load latency covered)
+                gload(0, ra[0], rw[0]);
                 sstore(0, ra[0], rw[0]);
-                gload(it + 4, ra[0], rw[0]);
+                gload(1, ra[0], rw[0]);
                 __syncthreads();
+                for (int it = 0; it < nk2; it += 2) {
+                    stage(0, ra[0], rw[0], it + 2);
+                    stage(1, ra[0], rw[0], it + 3);
+                }
+            } else {
+                gload(0, ra[0], rw[0]);
+                gload(1, ra[1], rw[1]);
+                sstore(0, ra[0], rw[0]);
+                gload(2, ra[0], rw[0]);
+                __syncthreads();
+                for (int it = 0; it < nk2; it += 2) {
+                    stage(0, ra[1], rw[1], it + 3);
+                    stage(1, ra[0], rw[0], it + 4);
+                }
             }
-        }
-        }
+        };
+        if (live)
+            main_loop(std::true_type{});
+        else
+            main_loop(std::false_type{});
 
         // lane holds rows 4g..4g+3 of column r in each 16x16 fragment
 #pragma unroll
