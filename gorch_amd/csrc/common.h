@@ -53,7 +53,7 @@ struct LinearExtras {
     const uint16_t* x_frag = nullptr;
     // tile-packed GEMV only: the outputs go to this fragment-layout buffer
     // (as the next GEMV's pre-split activations) instead of the output
-    // descriptor (no K split, no argmax)
+    // descriptor (with x_frag; no K split, no argmax)
     uint16_t* out_frag = nullptr;
     int ksplit = 1;
     int kslice = 0;    // K per slice (set by the launcher)

@@ -835,7 +835,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_mt(
 // residual, output, argmax keys). Every load is a raw buffer load with no
 // branch around it: k past the wave's range, rows past M or N and tiles
 // past the last read as zeros.
-template <int NW, int KS, bool EARLY, bool LN>
+// Activation input of k_gemv_tiles: f32 rows, f32 rows with LayerNorm
+// fused, or the fragment layout (a template argument, so the f32 kernels
+// compile as if the other forms did not exist)
+constexpr int kXmRows = 0, kXmLn = 1, kXmFrag = 2;
+template <int NW, int KS, bool EARLY, int XM>
 __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict__ x, const uint16_t* __restrict__ W,
                                                         const float* __restrict__ bias, const float* residual,
                                                         OutDesc od, int M, int N, int K, int ks, int epilogue,
@@ -859,9 +863,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
     // them alone, not for the weights issued after them
     // (pre-split activations: k-step j's hi and lo fragments, one
     // contiguous 1 KB each per wave)
-    const bool xf = !LN && ex.x_frag;
+    constexpr bool LN = XM == kXmLn, XF = XM == kXmFrag;
     u32x4 xa[KS][2];
-    if (xf) {
+    if constexpr (XF) {
         const __amdgpu_buffer_rsrc_t rsf = make_rsrc(ex.x_frag, (long long)xfrag_bytes(K));
 #pragma unroll
         for (int u = 0; u < KS; u++) {
@@ -977,7 +981,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
     bf16x8 ah[KS], al[KS];
 #pragma unroll
     for (int u = 0; u < KS; u++) {
-        if (xf) {
+        if constexpr (XF) {
             ah[u] = __builtin_bit_cast(bf16x8, xa[u][0]);
             al[u] = __builtin_bit_cast(bf16x8, xa[u][1]);
             continue;
@@ -1044,13 +1048,15 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_tiles(const float* __restrict_
             if (bias) val = val + (EARLY ? bv : tl.b);
             if (epilogue == GORCH_HIP_EPI_GELU) val = gelu_tanh(val);
             if (residual) val = (EARLY ? rv : tl.res) + val;
-            if (ex.out_frag) {
-                uint16_t hi, lo;
-                split_hi_lo1(val, hi, lo);
-                const size_t i = xfrag_index(om, on);
-                ex.out_frag[i] = hi;
-                ex.out_frag[i + 512] = lo;
-                return;
+            if constexpr (XF) {
+                if (ex.out_frag) {
+                    uint16_t hi, lo;
+                    split_hi_lo1(val, hi, lo);
+                    const size_t i = xfrag_index(om, on);
+                    ex.out_frag[i] = hi;
+                    ex.out_frag[i + 512] = lo;
+                    return;
+                }
             }
             *od.at_p(om, on, posv) = val;
             if (ex.argmax_key) {
@@ -1295,21 +1301,25 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
         return per_cu * cus;
     };
 #define GH_TILES_L(NWV, KSV, EA)                                                                        \
-    hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, EA, false>), dim3(blocks, S), dim3(NWV * 64), 0, s, x, W, bias, \
-                       residual, od, M, N, K, ks, epilogue, ex)
+    if (ex.x_frag)                                                                                      \
+        hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, EA, kXmFrag>), dim3(blocks, S), dim3(NWV * 64), 0, s, x, W, \
+                           bias, residual, od, M, N, K, ks, epilogue, ex);                              \
+    else                                                                                                \
+        hipLaunchKernelGGL((k_gemv_tiles<NWV, KSV, EA, kXmRows>), dim3(blocks, S), dim3(NWV * 64), 0, s, x, W, \
+                           bias, residual, od, M, N, K, ks, epilogue, ex)
     // fused LayerNorm: packed weights, 8 waves, K <= 1024 (the LM head of a
     // one-row decode step)
     if (ex.ln_g) {
         if (nw != 8 || ks > 4 || S != 1) return -1;
         static const int blocks_ln =
-            blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<8, 4, false, true>), 512);
+            blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<8, 4, false, kXmLn>), 512);
         const int blocks = std::min(blocks_ln, ntiles);
 #define GH_TILES_LN(KSV)                                                                                    \
     if (ntiles <= 2 * blocks)                                                                               \
-        hipLaunchKernelGGL((k_gemv_tiles<8, KSV, true, true>), dim3(blocks), dim3(512), 0, s, x, W, bias, \
+        hipLaunchKernelGGL((k_gemv_tiles<8, KSV, true, kXmLn>), dim3(blocks), dim3(512), 0, s, x, W, bias, \
                            residual, od, M, N, K, ks, epilogue, ex);                                        \
     else                                                                                                    \
-        hipLaunchKernelGGL((k_gemv_tiles<8, KSV, false, true>), dim3(blocks), dim3(512), 0, s, x, W, bias, \
+        hipLaunchKernelGGL((k_gemv_tiles<8, KSV, false, kXmLn>), dim3(blocks), dim3(512), 0, s, x, W, bias, \
                            residual, od, M, N, K, ks, epilogue, ex);
         if (ks <= 3) {
             GH_TILES_LN(3)
@@ -1326,7 +1336,7 @@ static int launch_tiles(hipStream_t s, const float* x, const uint16_t* W, const 
     // of 73 blocks each, 5,059 -> 5,146 tok/s)
 #define GH_TILES(NWV, KSV)                                                                                \
     if (nw == NWV && ks <= KSV) {                                                                         \
-        static const int blocks_p = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, false, false>), NWV * 64); \
+        static const int blocks_p = blocks_for(reinterpret_cast<const void*>(&k_gemv_tiles<NWV, KSV, false, kXmRows>), NWV * 64); \
         int blocks = std::min(std::max(1, blocks_p / S), ntiles);                                         \
         if (ntiles <= 2 * blocks) blocks = std::min(blocks, std::max(1, cus / S));                        \
         if (ntiles <= 2 * blocks) GH_TILES_L(NWV, KSV, true);                                             \
@@ -1628,9 +1638,9 @@ int launch_linear_packed_od(hipStream_t s, const float* x, const uint16_t* Wp, c
         set_error("linear_bf16_packed: needs 1 <= M <= 16, no argmax or LayerNorm with a K split");
         return GORCH_HIP_EUNSUPPORTED;
     }
-    if ((ex.x_frag && ex.ln_g) || (ex.out_frag && (ex.part || ex.accumulate || ex.argmax_key))) {
+    if ((ex.x_frag && ex.ln_g) || (ex.out_frag && (!ex.x_frag || ex.part || ex.accumulate || ex.argmax_key))) {
         set_error("linear_bf16_packed: fragment-layout activations take no fused LayerNorm, and a fragment-layout "
-                  "output no K split or argmax");
+                  "output needs fragment-layout activations, no K split and no argmax");
         return GORCH_HIP_EUNSUPPORTED;
     }
     if (ex.part || ex.accumulate) {
