@@ -88,7 +88,12 @@ inline int ksplit_slices(int K, int S) {
 // as the Qwen loop's sampleLogits (model/qwen/generate.go:121-152).
 int launch_sample(hipStream_t s, const float* logits, int rows, int n, float temperature, int top_k, float top_p,
                   const double* u, unsigned long long seed, const int* step, int* out, double* probs,
-                  unsigned long long* key, int* err, bool nucleus = false);
+                  unsigned long long* key, int* err, bool nucleus = false, int* ws = nullptr);
+// Workspace for launch_sample's ws (zeroed once at allocation; every call
+// leaves it zero): with it, a top-k row's two candidate-search passes run
+// over many blocks per row instead of inside the row's one block. Calls that
+// share a workspace must not overlap.
+size_t sample_ws_bytes(int rows);
 int sample_check(int rows, int n, float temperature, int top_k, float top_p);
 // Per-(device, stream) scratch for K-split partials; nullptr when it would
 // have to grow during stream capture or the allocation fails.

@@ -83,6 +83,10 @@ struct gorch_hip_gpt {
     hipGraphExec_t gen_exec = nullptr;
     std::vector<const void*> gen_sig;
     int* sample_err = nullptr;  // sampled generation: top-p support overflow flag
+    // sampled generation: the sampler's multi-block candidate search for up
+    // to sample_ws_rows rows (zero when idle)
+    int* sample_ws = nullptr;
+    int sample_ws_rows = 0;
 };
 
 struct gorch_hip_kvcache {
@@ -811,6 +815,7 @@ void gorch_hip_gpt_free(gorch_hip_gpt* g) {
     (void)hipFree(g->afrag);
     (void)hipFree(g->ids);
     (void)hipFree(g->sample_err);
+    (void)hipFree(g->sample_ws);
     delete g;
 }
 
@@ -958,6 +963,16 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
         if (!g->sample_err && check(hipMalloc(&g->sample_err, sizeof(int)), "hipMalloc sample flag"))
             return GORCH_HIP_ENOMEM;
         GH_TRY(check(hipMemsetAsync(g->sample_err, 0, sizeof(int), s), "reset sample flag"));
+        if (batch > g->sample_ws_rows) {
+            GH_TRY(check(hipStreamSynchronize(s), "sample workspace"));
+            (void)hipFree(g->sample_ws);
+            g->sample_ws = nullptr;
+            g->sample_ws_rows = 0;
+            if (check(hipMalloc(&g->sample_ws, sample_ws_bytes(batch)), "hipMalloc sample workspace"))
+                return GORCH_HIP_ENOMEM;
+            GH_TRY(check(hipMemset(g->sample_ws, 0, sample_ws_bytes(batch)), "clear sample workspace"));
+            g->sample_ws_rows = batch;
+        }
     }
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     int rc = GORCH_HIP_OK;
@@ -967,7 +982,8 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
     auto sample_tokens = [&]() -> int {
         if (!smp) return GORCH_HIP_OK;
         return launch_sample(s, g->logits, batch, g->vocab, smp->temperature, smp->top_k, smp->top_p, nullptr,
-                             smp->seed, c->state + 1, nullptr, nullptr, c->key, g->sample_err);
+                             smp->seed, c->state + 1, nullptr, nullptr, c->key, g->sample_err, false,
+                             g->sample_ws);
     };
     auto fail = [&](int r) {
         rc = r;
@@ -1010,6 +1026,7 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
                                                   reinterpret_cast<const void*>(deterministic() ? 1 : 0),
                                                   // and by the sampling parameters (kernel arguments)
                                                   reinterpret_cast<const void*>(smp ? 1 : 0), g->sample_err,
+                                                  g->sample_ws,
                                                   reinterpret_cast<const void*>(
                                                       smp ? (uintptr_t)__builtin_bit_cast(uint32_t, smp->temperature) : 0),
                                                   reinterpret_cast<const void*>(smp ? (uintptr_t)smp->top_k : 0),

@@ -155,6 +155,7 @@ struct gorch_hip_qwen {
     int hist_cap = 0;
     unsigned long long* key = nullptr;  // fused-argmax key, zero between steps
     int* sample_err = nullptr;          // set by the sampler: top-p candidates past its sort
+    int* sample_ws = nullptr;           // the sampler's multi-block candidate search (zero when idle)
     // the running generation's sampling config (temperature 0: greedy)
     float smp_t = 0.f, smp_p = 0.f;
     int smp_k = 0;
@@ -241,6 +242,8 @@ static int qwen_ensure(gorch_hip_qwen* m, int n, int cap, int hist) {
         GH_TRY(check(hipMalloc(&m->state, 2 * sizeof(int)), "qwen hipMalloc"));
         GH_TRY(check(hipMalloc(&m->key, kArgmaxKeys * sizeof(unsigned long long)), "qwen hipMalloc"));
         GH_TRY(check(hipMalloc(&m->sample_err, sizeof(int)), "qwen hipMalloc"));
+        GH_TRY(check(hipMalloc(&m->sample_ws, sample_ws_bytes(1)), "qwen hipMalloc"));
+        GH_TRY(check(hipMemset(m->sample_ws, 0, sample_ws_bytes(1)), "qwen hipMemset"));
     }
     return GORCH_HIP_OK;
 }
@@ -278,7 +281,7 @@ static int qwen_forward(gorch_hip_qwen* m, hipStream_t s, int n, bool prefill, i
                                  m->vocab, d, GORCH_HIP_EPI_NONE, ex));
     if (m->smp_t > 0.f)
         GH_TRY(launch_sample(s, m->logits, 1, m->vocab, m->smp_t, m->smp_k, m->smp_p, nullptr, m->smp_seed,
-                             m->state + 1, nullptr, nullptr, m->key, m->sample_err, true));
+                             m->state + 1, nullptr, nullptr, m->key, m->sample_err, true, m->sample_ws));
     hipLaunchKernelGGL(k_qwen_finalize, dim3(1), dim3(256), 0, s, m->key, m->hist, m->state, n, m->embed_f32, m->x,
                        d);
     count(CNT_ARGMAX);
@@ -330,7 +333,7 @@ void gorch_hip_qwen_destroy(gorch_hip_qwen* m) {
     (void)hipStreamSynchronize(m->stream);
     qwen_drop_graph(m);
     for (void* p : {(void*)m->kv, (void*)m->ws, (void*)m->x, (void*)m->h, (void*)m->logits, (void*)m->ids,
-                    (void*)m->state, (void*)m->hist, (void*)m->key, (void*)m->sample_err})
+                    (void*)m->state, (void*)m->hist, (void*)m->key, (void*)m->sample_err, (void*)m->sample_ws})
         (void)hipFree(p);
     release_stream_scratch(m->stream);
     (void)hipStreamDestroy(m->stream);

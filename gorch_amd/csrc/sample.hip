@@ -49,6 +49,11 @@ constexpr int kSampleThreads = 1024;
 constexpr int kSampleCap = 4096;
 constexpr int kSampleMaxN = 1 << 18;  // columns (the top-p bitmap's size)
 constexpr int kRowUnroll = 8;         // row entries per thread in flight in a pass
+// up to this many elements a sort places each one at its rank (one pass of
+// comparisons, one barrier) instead of a bitonic network (a barrier per
+// stage: 36 at 256 elements; across one wave's lanes 21 shuffle stages,
+// ~2.5 us at 40 elements)
+constexpr int kRankSortMax = 256;
 
 __device__ __forceinline__ uint32_t f32_order_key(float f) {
     const uint32_t b = __float_as_uint(f);
@@ -73,6 +78,153 @@ __device__ double philox_uniform(unsigned long long seed, uint32_t step, uint32_
         k1 += 0xBB67AE85u;
     }
     return ((double)(c0 >> 5) * 67108864.0 + (double)(c1 >> 6)) / 9007199254740992.0;
+}
+
+// Sample workspace (launch_sample's ws), per row in ints: the 4096-bin
+// histogram of the raw logits' order keys, the appended-candidate count,
+// the maximum key, the NaN flag, the bin of the top_k-th largest key and the
+// count of keys from that bin up, then kSampleCap candidate keys and
+// kSampleCap indices. Zero while idle: k_sample clears all of it after
+// reading it, so a captured step graph finds it zero again.
+constexpr int kWsCnt = 4096, kWsMax = 4097, kWsNan = 4098, kWsBin = 4099, kWsC = 4100, kWsKey = 4104,
+              kWsIdx = kWsKey + kSampleCap;
+constexpr int kWsRowInts = kWsIdx + kSampleCap;
+// below this row length the one-block passes are as fast
+constexpr int kSampleWsMinN = 8192;
+constexpr int kScanThreads = 256, kScanUnroll = 4;
+
+// Pass one of the top-k candidate search spread over gridDim.x blocks per
+// row (blockIdx.y): each block histograms the order keys of its chunk
+// [chunk * blockIdx.x, ..) in LDS (zeros taken as +0, as in k_sample), then
+// adds its non-empty bins into the row's histogram (one atomic per bin and
+// block), its maximum key and its NaN flag.
+__global__ __launch_bounds__(kScanThreads) void k_sample_scan(const float* __restrict__ logits, int n, int chunk,
+                                                             int* __restrict__ ws) {
+    __shared__ int h[4096];
+    __shared__ uint32_t s_max[kScanThreads / 64];
+    __shared__ int s_nan;
+    const int row = blockIdx.y, tid = threadIdx.x;
+    int* w = ws + (size_t)row * kWsRowInts;
+    for (int b = tid; b < 4096; b += kScanThreads) h[b] = 0;
+    if (tid == 0) s_nan = 0;
+    __syncthreads();
+    const int i0 = blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(logits + (size_t)row * n, (long long)n * 4);
+    uint32_t kmax = 0u;
+    int nan = 0;
+    for (int base = i0; base < i1; base += kScanUnroll * kScanThreads) {
+        float v[kScanUnroll];
+#pragma unroll
+        for (int u = 0; u < kScanUnroll; u++) {
+            const int i = base + u * kScanThreads + tid;
+            v[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rr, i < i1 ? i * 4 : kOutOfRange, 0, 0));
+        }
+#pragma unroll
+        for (int u = 0; u < kScanUnroll; u++) {
+            if (base + u * kScanThreads + tid < i1) {
+                const uint32_t key = f32_order_key(v[u] == 0.f ? 0.f : v[u]);
+                kmax = max(kmax, key);
+                nan |= v[u] != v[u];
+                atomicAdd(&h[key >> 20], 1);
+            }
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+    if ((tid & 63) == 0) s_max[tid >> 6] = kmax;
+    if (nan) s_nan = 1;
+    __syncthreads();
+    for (int b = tid; b < 4096; b += kScanThreads)
+        if (h[b]) atomicAdd(&w[b], h[b]);
+    if (tid == 0) {
+        for (int q = 0; q < kScanThreads / 64; q++) kmax = max(kmax, s_max[q]);
+        atomicMax(reinterpret_cast<unsigned int*>(&w[kWsMax]), kmax);
+        if (s_nan) atomicOr(&w[kWsNan], 1);
+    }
+}
+
+// Pass two: every block locates the bin of the top_k-th largest key from the
+// row's histogram (the same scan as k_sample's) and, when the candidates
+// fit kSampleCap and no logit is NaN, appends its chunk's keys at or above
+// that bin (one slot reservation per block).
+__global__ __launch_bounds__(kScanThreads) void k_sample_gather(const float* __restrict__ logits, int n, int chunk,
+                                                               int top_k, int* __restrict__ ws) {
+    __shared__ int s_scan[kScanThreads / 64];
+    __shared__ int s_bin, s_above, s_cnt, s_base;
+    __shared__ uint32_t l_key[kSampleCap];
+    __shared__ int l_idx[kSampleCap];
+    const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int* w = ws + (size_t)row * kWsRowInts;
+    // thread t sums bins 4095 - 16 t - q (q < 16): a scan of those sums in
+    // thread order is the count above each group of bins
+    constexpr int BPT = 4096 / kScanThreads;
+    int hb[BPT];
+    int gs = 0;
+#pragma unroll
+    for (int q = 0; q < BPT; q++) {
+        hb[q] = w[4095 - BPT * tid - q];
+        gs += hb[q];
+    }
+    int incl = gs;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) s_scan[wave] = incl;
+    if (tid == 0) s_cnt = 0;
+    __syncthreads();
+    int above = incl - gs;
+    for (int q = 0; q < wave; q++) above += s_scan[q];
+    if (above < top_k && above + gs >= top_k) {
+        int cum = above;
+#pragma unroll
+        for (int q = 0; q < BPT; q++) {
+            if (cum + hb[q] >= top_k) {
+                s_bin = 4095 - BPT * tid - q;
+                s_above = cum;
+                break;
+            }
+            cum += hb[q];
+        }
+    }
+    __syncthreads();
+    const int dbin = s_bin;
+    const int C = s_above + w[dbin];
+    if (blockIdx.x == 0 && tid == 0) {
+        w[kWsBin] = dbin;
+        w[kWsC] = C;
+    }
+    if (C > kSampleCap || w[kWsNan] != 0) return;
+    const int i0 = blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(logits + (size_t)row * n, (long long)n * 4);
+    for (int base = i0; base < i1; base += kScanUnroll * kScanThreads) {
+        float v[kScanUnroll];
+#pragma unroll
+        for (int u = 0; u < kScanUnroll; u++) {
+            const int i = base + u * kScanThreads + tid;
+            v[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rr, i < i1 ? i * 4 : kOutOfRange, 0, 0));
+        }
+#pragma unroll
+        for (int u = 0; u < kScanUnroll; u++) {
+            const int i = base + u * kScanThreads + tid;
+            const uint32_t key = f32_order_key(v[u] == 0.f ? 0.f : v[u]);
+            if (i < i1 && (int)(key >> 20) >= dbin) {
+                const int slot = atomicAdd(&s_cnt, 1);
+                l_key[slot] = key;
+                l_idx[slot] = i;
+            }
+        }
+    }
+    __syncthreads();
+    const int cnt = s_cnt;
+    if (cnt == 0) return;
+    if (tid == 0) s_base = atomicAdd(&w[kWsCnt], cnt);
+    __syncthreads();
+    const int b0 = s_base;
+    for (int j = tid; j < cnt; j += kScanThreads)
+        if (b0 + j < kSampleCap) {
+            w[kWsKey + b0 + j] = (int)l_key[j];
+            w[kWsIdx + b0 + j] = l_idx[j];
+        }
 }
 
 // Block reductions over 1024 threads in a fixed order (wave partials in
@@ -174,6 +326,7 @@ struct SampleArgs {
     unsigned long long* key;   // fused-argmax key slot 0 of row b gets the token (may be null)
     int* err;                  // set to 1 when the top-p candidates exceed kSampleCap
     int nucleus;               // top-p as sampleLogits' nucleus cut, else as sample()
+    int* ws = nullptr;         // workspace the two scan kernels filled (top-k rows), or null
 };
 
 __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
@@ -260,10 +413,32 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     // descending), whose sum is at most 1.5 * top_p; the nucleus keeps, in
     // order of (p descending, index ascending), every entry whose preceding
     // sum is still below top_p.
-    auto top_p_keep = [&](int cnt) -> double {
+    // rank_ok: every p is a number (the rank sort needs a strict order; the
+    // bitonic network tolerates NaN)
+    auto top_p_keep = [&](int cnt, bool rank_ok) -> double {
         int P = 1;
         while (P < cnt) P <<= 1;
-        if (P <= 64) {
+        if (rank_ok && cnt <= kRankSortMax) {
+            // (p descending, then index as below): distinct pairs, so the
+            // ranks are a permutation
+            double pm = 0.0;
+            int im = 0, rank = 0;
+            if (tid < cnt) {
+                pm = s_p[tid];
+                im = s_idx[tid];
+                for (int i = 0; i < cnt; i++) {
+                    const double pi = s_p[i];
+                    const int ii = s_idx[i];
+                    rank += pi > pm || (pi == pm && (a.nucleus ? ii < im : ii > im));
+                }
+            }
+            __syncthreads();
+            if (tid < cnt) {
+                s_p[rank] = pm;
+                s_idx[rank] = im;
+            }
+            P = 1;  // (the block sort below then does nothing)
+        } else if (P <= 64) {
             // one wave sorts up to 64
             struct PI {
                 double a;  // p
@@ -368,9 +543,21 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     // row to the full path.
     if (use_k && a.top_k <= kSampleCap) {
         int* hist12 = reinterpret_cast<int*>(s_keep);
+        // with a workspace, k_sample_scan built the histogram, maximum and
+        // NaN flag over many blocks; else the block's own pass
+        int* w = a.ws ? a.ws + (size_t)row * kWsRowInts : nullptr;
+        uint32_t kmax = 0u;
+        bool any_nan = false;
+        int dbin = 0, C = 0;
+        if (w) {
+            // (k_sample_gather located the bin and counted the candidates)
+            kmax = (uint32_t)w[kWsMax];
+            any_nan = w[kWsNan] != 0;
+            dbin = w[kWsBin];
+            C = w[kWsC];
+        } else {
         for (int b = tid; b < 4096; b += kSampleThreads) hist12[b] = 0;
         __syncthreads();
-        uint32_t kmax = 0u;
         int nan = 0;
         for (int base = 0; base < n; base += kRowUnroll * kSampleThreads) {
             float v[kRowUnroll];
@@ -388,8 +575,8 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
         for (int o = 32; o > 0; o >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
         if ((tid & 63) == 0) red_u[tid >> 6] = kmax;
         // (its barriers also publish red_u and the histogram)
-        const bool any_nan = block_sum_i32(nan, red_i) > 0;
-        for (int w = 0; w < kSampleThreads / 64; w++) kmax = max(kmax, red_u[w]);
+        any_nan = block_sum_i32(nan, red_i) > 0;
+        for (int q = 0; q < kSampleThreads / 64; q++) kmax = max(kmax, red_u[q]);
         // thread t sums bins 4095 - 4t - q (q < 4): the scan of those sums in
         // thread order is the count above each group of bins
         int gs = 0;
@@ -411,10 +598,33 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
             }
         }
         __syncthreads();
-        const int dbin = s_bin;
-        const int C = s_above + hist12[dbin];
+        dbin = s_bin;
+        C = s_above + hist12[dbin];
+        }
+        bool cand_ok = C <= kSampleCap && !any_nan;
+        if (w) {
+            // k_sample_gather appended exactly the C candidates (any order);
+            // then the workspace is cleared for the next use
+            const int wcnt = min(w[kWsCnt], kSampleCap);
+            if (cand_ok) {
+                cand_ok = wcnt == C;
+                if (cand_ok)
+                    for (int j = tid; j < C; j += kSampleThreads) {
+                        c_key[j] = (uint32_t)w[kWsKey + j];
+                        c_idx[j] = w[kWsIdx + j];
+                    }
+            }
+            __syncthreads();
+            for (int b = tid; b < 4096; b += kSampleThreads) w[b] = 0;
+            for (int j = tid; j < wcnt; j += kSampleThreads) {
+                w[kWsKey + j] = 0;
+                w[kWsIdx + j] = 0;
+            }
+            if (tid < kWsKey - kWsCnt) w[kWsCnt + tid] = 0;
+        }
         __syncthreads();
-        if (C <= kSampleCap && !any_nan) {
+        if (cand_ok) {
+            if (!w) {
             if (tid == 0) s_cnt = 0;
             __syncthreads();
             for (int base = 0; base < n; base += kRowUnroll * kSampleThreads) {
@@ -432,6 +642,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
                 }
             }
             __syncthreads();
+            }
             // the top_k-th largest key (every key above dbin's floor is a
             // candidate, so it is the row's): with few candidates the largest
             // key that at least top_k keys reach, each thread counting for
@@ -457,24 +668,55 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
             const float mx = f32_from_order_key(kmax) / T;
             const bool below = dbin > 0 && f32_from_order_key((uint32_t)dbin << 20) / T >= thr;
             if (!below) {
-                // candidates into index order (bitonic; padding sorts last):
-                // up to 64 in one wave, else across the block
+                // only the candidates at or above the threshold carry
+                // probability: keep those (top_k plus ties) before the sorts,
+                // the softmax, top-p and the inverse CDF
+                int Ck;
+                {
+                    constexpr int PC = kSampleCap / kSampleThreads;
+                    uint32_t kk[PC];
+                    int ii[PC];
+#pragma unroll
+                    for (int q = 0; q < PC; q++) {
+                        const int j = tid + q * kSampleThreads;
+                        kk[q] = j < C ? c_key[j] : 0u;
+                        ii[q] = j < C ? c_idx[j] : 0;
+                    }
+                    if (tid == 0) s_cnt = 0;
+                    __syncthreads();
+#pragma unroll
+                    for (int q = 0; q < PC; q++) {
+                        const int j = tid + q * kSampleThreads;
+                        if (j < C && f32_from_order_key(kk[q]) / T >= thr) {
+                            const int slot = atomicAdd(&s_cnt, 1);
+                            c_key[slot] = kk[q];
+                            c_idx[slot] = ii[q];
+                        }
+                    }
+                    __syncthreads();
+                    Ck = s_cnt;
+                }
+                // candidates into index order: by rank up to kRankSortMax,
+                // else a bitonic network across the block (padding sorts last)
                 int P = 1;
-                while (P < C) P <<= 1;
-                if (P <= 64) {
-                    struct KI {
-                        int a;       // index
-                        uint32_t b;  // key
-                    };
-                    if (tid < 64) {
-                        KI e = tid < C ? KI{c_idx[tid], c_key[tid]} : KI{INT_MAX, 0u};
-                        e = wave_bitonic_sort(e, [](const KI& x, const KI& y) { return x.a < y.a; });
-                        c_idx[tid] = e.a;
-                        c_key[tid] = e.b;
+                while (P < Ck) P <<= 1;
+                if (Ck <= kRankSortMax) {
+                    // distinct indices: each candidate's rank is its slot
+                    int im = INT_MAX, rank = 0;
+                    uint32_t km = 0u;
+                    if (tid < Ck) {
+                        im = c_idx[tid];
+                        km = c_key[tid];
+                        for (int i = 0; i < Ck; i++) rank += c_idx[i] < im;
+                    }
+                    __syncthreads();
+                    if (tid < Ck) {
+                        c_idx[rank] = im;
+                        c_key[rank] = km;
                     }
                     P = 1;  // (the block sort below then does nothing)
                 }
-                for (int j = C + tid; j < P; j += kSampleThreads) {
+                for (int j = Ck + tid; j < P; j += kSampleThreads) {
                     c_idx[j] = INT_MAX;
                     c_key[j] = 0u;
                 }
@@ -505,7 +747,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
                 for (int q = 0; q < PER; q++) {
                     const int j = tid * PER + q;
                     e[q] = 0.0;
-                    if (j < C) {
+                    if (j < Ck) {
                         const float v = f32_from_order_key(c_key[j]) / T;
                         if (v >= thr) e[q] = exp((double)(v - mx));
                     }
@@ -517,13 +759,13 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
 #pragma unroll
                     for (int q = 0; q < PER; q++) {
                         const int j = tid * PER + q;
-                        if (j < C) {
+                        if (j < Ck) {
                             s_p[j] = e[q] / sum;
                             s_idx[j] = c_idx[j];
                         }
                     }
                     __syncthreads();
-                    resum = top_p_keep(C);
+                    resum = top_p_keep(Ck, std::isfinite(sum));
                 }
                 // the inverse CDF in index order over the candidates
                 double f[PER];
@@ -531,7 +773,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
 #pragma unroll
                 for (int q = 0; q < PER; q++) {
                     const int j = tid * PER + q;
-                    f[q] = j < C ? finish(e[q] / sum, use_p && is_kept(c_idx[j]), resum) : 0.0;
+                    f[q] = j < Ck ? finish(e[q] / sum, use_p && is_kept(c_idx[j]), resum) : 0.0;
                     seg += f[q];
                 }
                 double total;
@@ -540,7 +782,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
 #pragma unroll
                 for (int q = 0; q < PER; q++) {
                     const int j = tid * PER + q;
-                    if (j < C) {
+                    if (j < Ck) {
                         run += f[q];
                         if (cand == INT_MAX && r < run) cand = c_idx[j];
                     }
@@ -556,7 +798,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
 #pragma unroll
                     for (int q = 0; q < PER; q++) {
                         const int j = tid * PER + q;
-                        if (j < C) a.probs[(size_t)row * n + c_idx[j]] = f[q];
+                        if (j < Ck) a.probs[(size_t)row * n + c_idx[j]] = f[q];
                     }
                 }
                 emit(tok);
@@ -650,7 +892,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
             }
             return;
         }
-        resum = top_p_keep(cnt);
+        resum = top_p_keep(cnt, false);
     }
     auto final_p = [&](int i, float x) { return finish(expo(x) / sum, use_p && is_kept(i), resum); };
 
@@ -705,10 +947,24 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
     emit(tok);
 }
 
+size_t sample_ws_bytes(int rows) { return (size_t)rows * kWsRowInts * sizeof(int); }
+
 int launch_sample(hipStream_t s, const float* logits, int rows, int n, float temperature, int top_k, float top_p,
                   const double* u, unsigned long long seed, const int* step, int* out, double* probs,
-                  unsigned long long* key, int* err, bool nucleus) {
+                  unsigned long long* key, int* err, bool nucleus, int* ws) {
     SampleArgs a{logits, n, temperature, top_k, top_p, u, seed, step, out, probs, key, err, nucleus ? 1 : 0};
+    if (ws && top_k > 0 && top_k < n && top_k <= kSampleCap && n >= kSampleWsMinN) {
+        // the candidate search's two row passes over many blocks per row
+        // (about 2048 entries each, at most ~512 blocks in all)
+        const int G = std::max(1, std::min((n + 2047) / 2048, std::max(1, 512 / rows)));
+        const int chunk = ((n + G - 1) / G + kScanThreads - 1) / kScanThreads * kScanThreads;
+        const int g = (n + chunk - 1) / chunk;
+        hipLaunchKernelGGL(k_sample_scan, dim3(g, rows), dim3(kScanThreads), 0, s, logits, n, chunk, ws);
+        GH_TRY(check_launch("sample_scan"));
+        hipLaunchKernelGGL(k_sample_gather, dim3(g, rows), dim3(kScanThreads), 0, s, logits, n, chunk, top_k, ws);
+        GH_TRY(check_launch("sample_gather"));
+        a.ws = ws;
+    }
     hipLaunchKernelGGL(k_sample, dim3(rows), dim3(kSampleThreads), 0, s, a);
     count(CNT_ARGMAX);
     return check_launch("sample");
@@ -756,4 +1012,15 @@ extern "C" int gorch_hip_sample_nucleus(void* stream, const float* logits, int r
     GH_TRY(sample_check(rows, n, temperature, top_k, top_p));
     return launch_sample(stream_of(stream), logits, rows, n, temperature, top_k, top_p, u, 0ull, nullptr, out, probs,
                          nullptr, nullptr, true);
+}
+
+extern "C" size_t gorch_hip_sample_workspace_size(int rows) { return rows > 0 ? sample_ws_bytes(rows) : 0; }
+
+extern "C" int gorch_hip_sample_with_workspace(void* stream, const float* logits, int rows, int n, float temperature,
+                                               int top_k, float top_p, const double* u, int* out, double* probs,
+                                               int nucleus, void* workspace) {
+    GH_REQUIRE(logits && u && out && workspace, "gorch_hip_sample_with_workspace: null logits, draws, output or workspace");
+    GH_TRY(sample_check(rows, n, temperature, top_k, top_p));
+    return launch_sample(stream_of(stream), logits, rows, n, temperature, top_k, top_p, u, 0ull, nullptr, out, probs,
+                         nullptr, nullptr, nucleus != 0, static_cast<int*>(workspace));
 }

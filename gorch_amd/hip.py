@@ -93,6 +93,8 @@ SIGNATURES = {
     "gorch_hip_argmax": (i32, [vp, vp, i32, i32, vp]),
     "gorch_hip_sample": (i32, [vp, vp, i32, i32, C.c_float, i32, C.c_float, vp, vp, vp]),
     "gorch_hip_sample_nucleus": (i32, [vp, vp, i32, i32, C.c_float, i32, C.c_float, vp, vp, vp]),
+    "gorch_hip_sample_workspace_size": (C.c_size_t, [i32]),
+    "gorch_hip_sample_with_workspace": (i32, [vp, vp, i32, i32, C.c_float, i32, C.c_float, vp, vp, vp, i32, vp]),
     "gorch_hip_rope_tables": (i32, [vp, i32, i32, f32, vp, vp]),
     "gorch_hip_rope_apply": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, i32, i32, f32]),
     "gorch_hip_gqa_attention_cached": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32]),
@@ -359,6 +361,23 @@ def sample_nucleus(logits, temperature, top_k, top_p, u, out, probs=None) -> Non
     rows, n = logits.shape
     _ok(lib().gorch_hip_sample_nucleus(_stream(), _p(logits), rows, n, float(temperature), int(top_k), float(top_p),
                                        _p(u), _p(out), _p(probs)))
+
+
+def sample_workspace(rows):
+    """A zeroed device workspace for sample_with_workspace over `rows` rows."""
+    import torch
+
+    n = lib().gorch_hip_sample_workspace_size(rows)
+    return torch.zeros(n, dtype=torch.uint8, device="cuda")
+
+
+def sample_with_workspace(logits, temperature, top_k, top_p, u, out, ws, probs=None, nucleus=False) -> None:
+    """sample() (or with nucleus the Qwen loop's sampleLogits) per row, the
+    top-k candidate search spread over many blocks per row; ws from
+    sample_workspace (left zero by every call)."""
+    rows, n = logits.shape
+    _ok(lib().gorch_hip_sample_with_workspace(_stream(), _p(logits), rows, n, float(temperature), int(top_k),
+                                              float(top_p), _p(u), _p(out), _p(probs), int(bool(nucleus)), _p(ws)))
 
 
 def linear_bf16(x, W, bias, y, residual=None, epilogue=EPI_NONE, act_bf16=False) -> None:

@@ -171,3 +171,52 @@ def test_sample_nan_logit(gpu, nucleus):
             tok, want = (orc.sample_nucleus if nucleus else orc.sample)(logits[r], 0.8, K, P, float(u[r]))
             assert got_tok[r] == tok == n - 1
             assert np.isnan(want).all() and np.isnan(got_p[r]).all()
+
+
+WS_CASES = [(1, 50257, 0.8, 40, 0.0, "normal"), (1, 50257, 0.8, 40, 0.95, "normal"),
+            (3, 151936, 0.7, 20, 0.8, "normal"), (16, 50257, 1.3, 1, 0.0, "normal"),
+            (16, 8192, 1.0, 4096, 0.5, "normal"), (2, 20000, 1.0, 300, 0.0, "ties"),
+            (2, 20000, 1.0, 10, 0.9, "ties"), (2, 9000, 0.8, 40, 0.9, "nan"), (2, 12000, 0.9, 50, 0.0, "zeros"),
+            (2, 8192, 0.7, 6, 0.0, "below")]
+
+
+@pytest.mark.parametrize("nucleus", [False, True])
+@pytest.mark.parametrize("rows,n,T,K,P,kind", WS_CASES)
+def test_sample_workspace_matches_one_block(gpu, rows, n, T, K, P, kind, nucleus):
+    """gorch_hip_sample_with_workspace runs the top-k candidate search's two
+    row passes over many blocks per row: its tokens and final distributions
+    must equal the one-block kernel's bit for bit, including the rows that
+    fall back to the full path (more than 4096 keys tied into the threshold
+    bin, a NaN, a scaled tie below the bin), and every call must leave the
+    workspace zero (three calls in a row on one workspace)."""
+    rng = np.random.default_rng(n + K + rows)
+    if kind == "ties":       # 5,000 copies of each of 0..3: the top bin holds more than 4096 keys
+        logits = rng.integers(0, 4, size=(rows, n)).astype(np.float32)
+    else:
+        logits = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+    if kind == "nan":
+        logits[:, 1234] = np.nan
+    if kind == "zeros":      # +0 and -0 compare equal; the keys must treat them as one value
+        logits[:, ::3] = 0.0
+        logits[:, 1::7] = -0.0
+        logits *= (rng.random((rows, n)) < 0.999)
+    if kind == "below":      # two logits one float apart, equal after division by T = 0.7
+        logits = (rng.standard_normal((rows, n)) * 0.3).astype(np.float32)
+        logits[:, 100:105] = [2.5, 2.6, 2.7, 2.8, 2.9]
+        logits[:, 700] = np.float32(1.5)
+        logits[:, 1700] = np.nextafter(np.float32(1.5), np.float32(0))
+    u = rng.random(rows)
+    lg, ud = dev(logits), dev(u)
+    out0 = torch.empty(rows, dtype=torch.int32, device="cuda")
+    p0 = torch.empty((rows, n), dtype=torch.float64, device="cuda")
+    (gpu.sample_nucleus if nucleus else gpu.sample)(lg, T, K, P, ud, out0, p0)
+    want_tok, want_p = host(out0), host(p0)
+    ws = gpu.sample_workspace(rows)
+    out1 = torch.empty(rows, dtype=torch.int32, device="cuda")
+    p1 = torch.empty((rows, n), dtype=torch.float64, device="cuda")
+    for _ in range(3):
+        out1.fill_(-1)
+        gpu.sample_with_workspace(lg, T, K, P, ud, out1, ws, p1, nucleus=nucleus)
+        assert np.array_equal(host(out1), want_tok)
+        assert np.array_equal(host(p1).view(np.uint64), want_p.view(np.uint64))
+        assert not bool(ws.any())
