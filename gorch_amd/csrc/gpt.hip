@@ -131,10 +131,12 @@ static int ensure_acts(gorch_hip_gpt* g, size_t rows, size_t logit_rows) {
             GH_TRY(check(hipMalloc(&g->wpart, (size_t)kMaxPartSlices * 16 * 3 * d * 4), "hipMalloc wpart"));
             GH_TRY(check(hipMalloc(&g->hfrag, xfrag_bytes((int)d)), "hipMalloc hfrag"));
             GH_TRY(check(hipMalloc(&g->ffrag, xfrag_bytes(4 * (int)d)), "hipMalloc ffrag"));
-            GH_TRY(check(hipMemset(g->hfrag, 0, xfrag_bytes((int)d)), "hipMemset hfrag"));
-            GH_TRY(check(hipMemset(g->ffrag, 0, xfrag_bytes(4 * (int)d)), "hipMemset ffrag"));
+            // (cleared on the engine's stream, which does not wait for the
+            // null stream)
+            GH_TRY(check(hipMemsetAsync(g->hfrag, 0, xfrag_bytes((int)d), g->stream), "clear hfrag"));
+            GH_TRY(check(hipMemsetAsync(g->ffrag, 0, xfrag_bytes(4 * (int)d), g->stream), "clear ffrag"));
             GH_TRY(check(hipMalloc(&g->afrag, xfrag_bytes((int)d)), "hipMalloc afrag"));
-            GH_TRY(check(hipMemset(g->afrag, 0, xfrag_bytes((int)d)), "hipMemset afrag"));
+            GH_TRY(check(hipMemsetAsync(g->afrag, 0, xfrag_bytes((int)d), g->stream), "clear afrag"));
         }
     }
     if (logit_rows > g->logit_rows_cap) {
@@ -970,7 +972,7 @@ static int generate_impl(void* stream, gorch_hip_gpt* g, const int* prompts, int
             g->sample_ws_rows = 0;
             if (check(hipMalloc(&g->sample_ws, sample_ws_bytes(batch)), "hipMalloc sample workspace"))
                 return GORCH_HIP_ENOMEM;
-            GH_TRY(check(hipMemset(g->sample_ws, 0, sample_ws_bytes(batch)), "clear sample workspace"));
+            GH_TRY(check(hipMemsetAsync(g->sample_ws, 0, sample_ws_bytes(batch), s), "clear sample workspace"));
             g->sample_ws_rows = batch;
         }
     }
