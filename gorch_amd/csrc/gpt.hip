@@ -137,6 +137,8 @@ static int ensure_acts(gorch_hip_gpt* g, size_t rows, size_t logit_rows) {
             GH_TRY(check(hipMemsetAsync(g->ffrag, 0, xfrag_bytes(4 * (int)d), g->stream), "clear ffrag"));
             GH_TRY(check(hipMalloc(&g->afrag, xfrag_bytes((int)d)), "hipMalloc afrag"));
             GH_TRY(check(hipMemsetAsync(g->afrag, 0, xfrag_bytes((int)d), g->stream), "clear afrag"));
+            // (forwards may run on a caller's stream: finish the clears here)
+            GH_TRY(check(hipStreamSynchronize(g->stream), "clear fragment buffers"));
         }
     }
     if (logit_rows > g->logit_rows_cap) {

@@ -244,6 +244,7 @@ static int qwen_ensure(gorch_hip_qwen* m, int n, int cap, int hist) {
         GH_TRY(check(hipMalloc(&m->sample_err, sizeof(int)), "qwen hipMalloc"));
         GH_TRY(check(hipMalloc(&m->sample_ws, sample_ws_bytes(1)), "qwen hipMalloc"));
         GH_TRY(check(hipMemsetAsync(m->sample_ws, 0, sample_ws_bytes(1), m->stream), "qwen clear sample workspace"));
+        GH_TRY(check(hipStreamSynchronize(m->stream), "qwen clear sample workspace"));
     }
     return GORCH_HIP_OK;
 }
