@@ -91,3 +91,27 @@ def test_attention_rejects_cache_span_of_2gib_without_gpu():
         assert rc != 1 or "2 GiB" not in hip.last_error()
     rc = L.gorch_hip_attention_cached(None, q, kc, vc, out, 1, 1, 0, 64, 128, 1 << 22, 1)
     assert rc == 1
+
+
+def test_sample_workspace_arguments_without_gpu():
+    # gorch_hip_sample_with_workspace: its size is linear in the rows (0 for
+    # none), and its argument checks come before any device work: a null
+    # workspace, a temperature of 0 and a top_p without 1 <= top_k <= 4096
+    # are refused like gorch_hip_sample's.
+    import ctypes as C
+
+    L = hip.lib()
+    one = L.gorch_hip_sample_workspace_size(1)
+    assert one > 0 and L.gorch_hip_sample_workspace_size(3) == 3 * one
+    assert L.gorch_hip_sample_workspace_size(0) == 0
+    fake = C.c_void_p(0x1000)
+
+    def call(T, K, P, ws):
+        return L.gorch_hip_sample_with_workspace(None, fake, 2, 50257, C.c_float(T), K, C.c_float(P), fake, fake,
+                                                 None, 0, ws)
+
+    assert call(0.8, 40, 0.9, None) == 2
+    assert "workspace" in hip.last_error()
+    assert call(0.0, 40, 0.9, fake) == 2
+    assert call(0.8, 0, 0.9, fake) == 1
+    assert call(0.8, 5000, 0.9, fake) == 1
