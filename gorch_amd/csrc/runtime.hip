@@ -43,6 +43,9 @@ struct StreamScratch {
     hipStream_t stream;
     void* ptr;
     size_t bytes;
+    // buffers this one replaced when it grew (a captured graph may still
+    // point at them): freed with it
+    std::vector<std::pair<void*, size_t>> retired;
 };
 std::mutex g_scratch_mu;
 std::vector<StreamScratch> g_scratch;
@@ -57,6 +60,10 @@ void release_stream_scratch(hipStream_t s) {
         if (g_scratch[i].stream == s) {
             (void)hipFree(g_scratch[i].ptr);
             g_scratch_bytes -= (long long)g_scratch[i].bytes;
+            for (auto& r : g_scratch[i].retired) {
+                (void)hipFree(r.first);
+                g_scratch_bytes -= (long long)r.second;
+            }
             g_scratch.erase(g_scratch.begin() + (long)i);
         } else {
             i++;
@@ -86,10 +93,11 @@ void* stream_scratch(hipStream_t s, size_t bytes) {
     g_scratch_bytes += (long long)want;
     if (e) {
         // the smaller buffer stays allocated: a captured graph may point at it
+        e->retired.emplace_back(e->ptr, e->bytes);
         e->ptr = p;
         e->bytes = want;
     } else {
-        g_scratch.push_back({dev, s, p, want});
+        g_scratch.push_back({dev, s, p, want, {}});
     }
     return p;
 }
@@ -443,6 +451,12 @@ void* gorch_hip_buf_host(void* stream, gorch_hip_buf* h, int will_write) {
 long long gorch_hip_live_bytes(void) { return g_live_bytes.load(); }
 
 long long gorch_hip_scratch_bytes(void) { return scratch_bytes_held(); }
+
+void gorch_hip_release_stream_scratch(void* stream) {
+    hipStream_t s = stream_of(stream);
+    (void)hipStreamSynchronize(s);
+    release_stream_scratch(s);
+}
 
 int gorch_hip_upload(void* stream, void* dst, const void* src, size_t bytes) {
     GH_REQUIRE(dst && src, "gorch_hip_upload: null pointer");

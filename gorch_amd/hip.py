@@ -47,6 +47,7 @@ SIGNATURES = {
     "gorch_hip_sync": (i32, [vp]),
     "gorch_hip_live_bytes": (C.c_longlong, []),
     "gorch_hip_scratch_bytes": (C.c_longlong, []),
+    "gorch_hip_release_stream_scratch": (None, [vp]),
     "gorch_hip_qwen_create": (C.c_void_p, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_float,
                                            C.c_int, C.c_int]),
     "gorch_hip_qwen_destroy": (None, [C.c_void_p]),

@@ -63,11 +63,18 @@ void gorch_hip_release(void* ptr);
 long long gorch_hip_live_bytes(void);
 /* Device bytes the library holds for its own scratch: the per-stream
  * K-split partial buffers of gorch_hip_linear_bf16 and the engines, each
- * allocated on a stream's first split launch outside capture and kept until
- * the process ends (a captured graph may point at it). No counterpart in the
- * reference (Metal's MPSGraph keeps its own scratch); it lets a caller check
- * that a call allocated nothing. */
+ * allocated on a stream's first split launch outside capture and kept (with
+ * any it replaced when it grew: a captured graph may point at them) until
+ * gorch_hip_release_stream_scratch or the process ends. No counterpart in
+ * the reference (Metal's MPSGraph keeps its own scratch); it lets a caller
+ * check that a call allocated nothing. */
 long long gorch_hip_scratch_bytes(void);
+/* No counterpart in the reference: frees the scratch the library holds for
+ * `stream` (NULL = the null stream) after waiting for the stream, for a
+ * caller about to destroy a stream of its own. No graph captured on that
+ * stream may be launched afterwards; the next split launch on it allocates
+ * again. The engines release their own streams' scratch when destroyed. */
+void gorch_hip_release_stream_scratch(void* stream);
 
 /* Buffer handles (metal.Buffer, metal/metal.go:240-422; Tensor.ToMetal /
  * Data, tensor.go:318-406). Device memory of exactly `bytes`, zero-filled;

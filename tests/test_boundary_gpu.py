@@ -216,3 +216,31 @@ def test_sync_dispatch_mode(gpu, lib):
     assert gpu.async_enabled()
     for t in (dx, dW, db, dy):
         t.free()
+
+
+def test_release_stream_scratch(gpu, lib):
+    """gorch_hip_release_stream_scratch: the narrow long-K GEMV's split takes
+    scratch for the stream it runs on; releasing that stream's scratch gives
+    the bytes back, and the next split launch on the stream allocates again
+    and still matches the oracle."""
+    import torch
+
+    s = torch.cuda.Stream()
+    M, K, N = 4, 3072, 768
+    x, W, b = syn.gemv_inputs(M, K, N, seed=5)
+    ref = orc.linear(x, W, b)
+    Wp = gpu.pack_bf16(torch.from_numpy(W.view(np.int16)).cuda())
+    xd, bd = torch.from_numpy(x).cuda(), torch.from_numpy(b).cuda()
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    held0 = lib.gorch_hip_scratch_bytes()
+    for _ in range(2):
+        y.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            gpu.linear_bf16_packed(xd, Wp, N, bd, y)
+        s.synchronize()
+        assert lib.gorch_hip_scratch_bytes() > held0
+        assert rel_err(y.cpu().numpy(), ref) <= 1e-3
+        lib.gorch_hip_release_stream_scratch(C.c_void_p(s.cuda_stream))
+        assert lib.gorch_hip_scratch_bytes() == held0
