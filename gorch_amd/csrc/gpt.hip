@@ -53,6 +53,7 @@ struct gorch_hip_gpt {
     int vocab = 0, dim = 0, heads = 0, layers = 0, max_seq = 0;
     char* blob = nullptr;
     char* pblob = nullptr;  // tile-packed weights
+    size_t pblob_bytes = 0;
     float *wte = nullptr, *wpe = nullptr, *lnf_g = nullptr, *lnf_b = nullptr, *blm = nullptr;
     uint16_t* wlm = nullptr;
     uint16_t* wlm_p = nullptr;
@@ -640,7 +641,8 @@ static gorch_hip_gpt* gpt_finish(gorch_hip_gpt* g) {
         const size_t po = align256(packed_bf16_elems(D, D) * 2), p2 = align256(packed_bf16_elems(D, 4 * D) * 2);
         const size_t plm = align256(packed_bf16_elems(g->vocab, D) * 2);
         const size_t per_layer = pq + p1 + po + p2;
-        if (check(hipMalloc(&g->pblob, plm + (size_t)g->layers * per_layer), "hipMalloc packed weights")) {
+        g->pblob_bytes = plm + (size_t)g->layers * per_layer;
+        if (check(hipMalloc(&g->pblob, g->pblob_bytes), "hipMalloc packed weights")) {
             gorch_hip_gpt_free(g);
             return nullptr;
         }
@@ -791,6 +793,24 @@ gorch_hip_gpt* gorch_hip_gpt_load_gpt2(const char* path, int vocab, int dim, int
         return nullptr;
     }
     return gpt_finish(g);
+}
+
+size_t gorch_hip_gpt_drop_packed(gorch_hip_gpt* g) {
+    if (!g || !g->pblob) return 0;
+    (void)hipStreamSynchronize(g->stream);
+    // the captured generate step points at the packed weights
+    if (g->gen_exec) (void)hipGraphExecDestroy(g->gen_exec);
+    if (g->gen_graph) (void)hipGraphDestroy(g->gen_graph);
+    g->gen_exec = nullptr;
+    g->gen_graph = nullptr;
+    g->gen_sig.clear();
+    (void)hipFree(g->pblob);
+    g->pblob = nullptr;
+    g->wlm_p = nullptr;
+    for (LayerW& L : g->L) L.wqkv_p = L.w1_p = L.wo_p = L.w2_p = nullptr;
+    const size_t freed = g->pblob_bytes;
+    g->pblob_bytes = 0;
+    return freed;
 }
 
 void gorch_hip_gpt_free(gorch_hip_gpt* g) {

@@ -115,6 +115,7 @@ SIGNATURES = {
                                 C.POINTER(i64)]),
     "gorch_hip_st_load": (i32, [vp, vp, C.c_char_p, vp, i32, i32]),
     "gorch_hip_gpt_free": (None, [vp]),
+    "gorch_hip_gpt_drop_packed": (C.c_size_t, [vp]),
     "gorch_hip_kvcache_create": (vp, [vp, i32, i32]),
     "gorch_hip_kvcache_free": (None, [vp]),
     "gorch_hip_kvcache_len": (i32, [vp]),
@@ -573,6 +574,11 @@ class GPT:
                                      lens.ctypes.data, None if logits is None else logits.ctypes.data, timing))
         ids = [out[b, :lens[b]].copy() for b in range(B)]
         return ids, logits, {"prefill_ms": timing[0], "decode_ms": timing[1], "decode_forwards": int(timing[2])}
+
+    def drop_packed(self) -> int:
+        """Frees the engine's tile-packed weight copies (2..16-row steps then
+        run the row-major GEMVs); returns the bytes freed."""
+        return int(lib().gorch_hip_gpt_drop_packed(self.h))
 
     def close(self):
         if getattr(self, "h", None):

@@ -508,6 +508,15 @@ gorch_hip_gpt* gorch_hip_gpt_create(const gorch_hip_gpt_weights* w);
  * configuration fails, as in copyTensor. NULL on failure. */
 gorch_hip_gpt* gorch_hip_gpt_load_gpt2(const char* path, int vocab, int dim, int heads, int layers, int max_seq);
 void gorch_hip_gpt_free(gorch_hip_gpt* gpt);
+/* No counterpart in the reference: frees the engine's tile-packed copies of
+ * its weights (made at creation for the 2..16-row decode GEMVs when
+ * dim <= 3072: about the bf16 weights' bytes again) and its captured
+ * generate step. Steps of 2..16 rows then run the row-major GEMVs (same
+ * results to the tested bars, slower: the GPT-2 XL shape at batch 16 and 128
+ * new tokens 5,966 -> 4,887 tok/s for 3.1 GB freed); graphs a caller
+ * captured before must not be launched afterwards. Returns the bytes freed
+ * (0 if none). */
+size_t gorch_hip_gpt_drop_packed(gorch_hip_gpt* gpt);
 /* KV cache for `batch` independent sequences of up to `capacity` tokens
  * (NewKVCache, nn/kvcache.go:23-36; one reference cache per sequence). */
 gorch_hip_kvcache* gorch_hip_kvcache_create(gorch_hip_gpt* gpt, int batch, int capacity);

@@ -397,3 +397,27 @@ def test_generate_sampled_argument_errors(tiny, gpu):
     with pytest.raises(gpu.HipError) as e:   # top-p needs 1 <= top_k <= 4096
         g.generate(prompts[:2], 4, temperature=1.0, top_p=0.5)
     assert e.value.rc == 1
+
+
+def test_drop_packed_weights(gpu):
+    """gorch_hip_gpt_drop_packed: the engine frees its tile-packed weight
+    copies (the bytes of its bf16 Linear and LM-head weights again) and its
+    captured step; batched decode then runs the row-major GEMVs with the
+    same greedy tokens as the oracle, eager and graph-replayed."""
+    cfg = dict(vocab=4096, dim=1024, heads=16, layers=2, max_seq=48)
+    w = syn.gpt2_weights(cfg, seed=47, random_affine=True)
+    g, o = gpu.GPT(w), orc.GPT(w)
+    prompts = np.stack([syn.prompt_ids(12, cfg["vocab"], seed=120 + b) for b in range(4)])
+    refs = [o.generate_cached(prompts[b], 10, want_logits=True) for b in range(4)]
+    before, _, _ = g.generate_cached(prompts, 10, use_graph=True)
+    d, V, L = cfg["dim"], cfg["vocab"], cfg["layers"]
+    freed = g.drop_packed()
+    assert freed >= 2 * (L * 12 * d * d + V * d)
+    assert g.drop_packed() == 0
+    for use_graph in (False, True):
+        ids, logits, _ = g.generate_cached(prompts, 10, want_logits=True, use_graph=use_graph)
+        assert np.array_equal(ids, before)
+        for b, (ref, ref_logits, _) in enumerate(refs):
+            assert list(ids[b]) == list(ref)
+            assert rel_err(logits[0, b], ref_logits[0]) <= 1e-3
+    g.close()
