@@ -738,6 +738,52 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleArgs a) {
                         __syncthreads();
                     }
                 }
+                if (Ck <= 64 && !a.probs) {
+                    // up to 64 kept candidates and no distribution to write:
+                    // wave 0 alone, candidate j in lane j (index order), the
+                    // f64 sums across the wave, no barrier
+                    if ((tid >> 6) != 0) return;
+                    const int ln = tid & 63;
+                    const bool on = ln < Ck;
+                    const int ij = on ? c_idx[ln] : INT_MAX;
+                    const float vj = on ? f32_from_order_key(c_key[ln]) / T : 0.f;
+                    const double ej = on ? exp((double)(vj - mx)) : 0.0;
+                    double sum = ej, zero = 0.0;
+                    wave_sum2_d(sum, zero);
+                    const double pj = ej / sum;
+                    bool kept = false;
+                    double resum = 1.0;
+                    if (use_p) {
+                        // the probabilities before this one in (p descending,
+                        // then index: ascending for the nucleus cut,
+                        // descending for sample()) order; kept as the block
+                        // path's prefix rule
+                        double before = 0.0;
+                        for (int i = 0; i < Ck; i++) {
+                            const double pi = __shfl(pj, i, 64);
+                            const int ii = __shfl(ij, i, 64);
+                            if (pi > pj || (pi == pj && (a.nucleus ? ii < ij : ii > ij))) before += pi;
+                        }
+                        const double limit = a.nucleus ? (double)a.top_p : (double)a.top_p * 1.5;
+                        kept = on && (a.nucleus ? before < limit : before + pj <= limit);
+                        double ks = kept ? pj : 0.0;
+                        zero = 0.0;
+                        wave_sum2_d(ks, zero);
+                        resum = ks;
+                    }
+                    const double fj = on ? finish(pj, use_p && kept, resum) : 0.0;
+                    // the inverse CDF in index order: the first candidate whose
+                    // running sum exceeds the draw
+                    double incl = fj;
+                    for (int o = 1; o < 64; o <<= 1) {
+                        const double y = __shfl_up(incl, o, 64);
+                        if (ln >= o) incl += y;
+                    }
+                    const unsigned long long hit = __ballot(on && r < incl);
+                    const int tok = hit ? __shfl(ij, __ffsll((long long)hit) - 1, 64) : n - 1;
+                    emit(tok);
+                    return;
+                }
                 // softmax over the kept (key >= tkey): the f64 exp of the f32
                 // difference to the maximum, the sum in index order
                 constexpr int PER = kSampleCap / kSampleThreads;

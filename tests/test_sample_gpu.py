@@ -220,3 +220,30 @@ def test_sample_workspace_matches_one_block(gpu, rows, n, T, K, P, kind, nucleus
         assert np.array_equal(host(out1), want_tok)
         assert np.array_equal(host(p1).view(np.uint64), want_p.view(np.uint64))
         assert not bool(ws.any())
+
+
+@pytest.mark.parametrize("nucleus", [False, True])
+def test_sample_tokens_without_probs(gpu, nucleus):
+    """Without a distribution to write, up to 64 kept candidates finish in
+    one wave (f64 sums across the wave, no barrier): its tokens must be the
+    ones the block path (distribution written) chooses, over 64 rows of
+    draws for top-k 1..64 with and without top-p, and the oracle's."""
+    rng = np.random.default_rng(21)
+    rows, n, T = 64, 20000, 0.9
+    logits = (rng.standard_normal((rows, n)) * 2).astype(np.float32)
+    lg = dev(logits)
+    f = gpu.sample_nucleus if nucleus else gpu.sample
+    ref = orc.sample_nucleus if nucleus else orc.sample
+    probs = torch.empty((rows, n), dtype=torch.float64, device="cuda")
+    for K, P in ((1, 0.0), (20, 0.8), (40, 0.95), (64, 0.5), (64, 0.0)):
+        u = rng.random(rows)
+        ud = dev(u)
+        block = torch.empty(rows, dtype=torch.int32, device="cuda")
+        wave = torch.empty(rows, dtype=torch.int32, device="cuda")
+        f(lg, T, K, P, ud, block, probs)
+        f(lg, T, K, P, ud, wave, None)
+        got = host(wave)
+        assert np.array_equal(host(block), got)
+        for r in range(0, rows, 8):
+            tok, _ = ref(logits[r], T, K, P, float(u[r]))
+            assert got[r] == tok
