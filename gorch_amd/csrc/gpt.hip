@@ -174,10 +174,12 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
     const bool fused = rows <= 16;
     // 2..16 rows: the residual Linears (Wo, FFN2) are split over K across
     // blocks (their N = d alone gives too few blocks to pull HBM at full
-    // rate); one small per-row kernel adds the slices, bias and residual and
-    // writes the next LayerNorm's output h, which the following GEMV reads
-    // as a plain operand (a LayerNorm fused into the GEMV's loads costs
-    // ~3.5 us per call at 16 rows, d 1600, for its gamma/beta loads).
+    // rate); the slices add themselves into x with float atomics (in
+    // deterministic mode one small per-row kernel adds them, the bias and the
+    // residual in slice order), and a per-row kernel writes the next
+    // LayerNorm's output h, which the following GEMV reads as a plain
+    // operand (a LayerNorm fused into the GEMV's loads costs ~3.5 us per
+    // call at 16 rows, d 1600, for its gamma/beta loads).
     const bool batched = fused && rows >= 2 && d <= kReduceRowsMaxCols;
     // batched steps over tile-packed weights: the LayerNorm row passes and
     // FFN1 write their outputs in the fragment layout the following tile
@@ -201,7 +203,7 @@ static int forward(gorch_hip_gpt* g, gorch_hip_kvcache* c, int n, bool all_rows,
     // 1.7x the weight bytes for an unsplit fused QKV and 2.6x for Wo in 2
     // slices. More slices cut it;
     // the partials of the fused QKV are added by the two-pass attention
-    // kernel, those of Wo and FFN2 by the row reducer. The fused QKV takes 3
+    // kernel, those of Wo and FFN2 into x (above). The fused QKV takes 3
     // slices by default (XL batch 16, exact-k-step tiles, CU-capped grid:
     // 1 / 2 / 3 / 4 slices 5,249 / 5,330 / 5,335 / 5,240 tok/s).
     constexpr int qkv_split_req = 3;
